@@ -1,0 +1,291 @@
+"""ctypes bindings for the CPU oracle — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker or the timed CPU baseline.
+The qwn_hip library never calls into it.
+
+``load()`` returns the restatement (liboracle.so, built by oracle/Makefile);
+``load_ref()`` returns the reference's own CPU kernels compiled in place
+(oracle/_ref/libqwn_ref.so) or None when that build is absent.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libqwn_ref.so")
+
+_c_i8p = ctypes.POINTER(ctypes.c_int8)
+_c_u8p = ctypes.POINTER(ctypes.c_uint8)
+_c_u16p = ctypes.POINTER(ctypes.c_uint16)
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def ptr(a: np.ndarray, ctype):
+    assert a.flags["C_CONTIGUOUS"], "oracle buffers must be contiguous"
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+class Oracle:
+    """Typed numpy front end of liboracle.so."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build()
+        lib = ctypes.CDLL(path)
+        self.lib = lib
+        lib.qo_half_to_float.argtypes = [ctypes.c_uint16]
+        lib.qo_half_to_float.restype = ctypes.c_float
+        lib.qo_quantize_tokens.argtypes = [_c_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           _c_i8p, _c_f32p, _c_i32p, ctypes.c_int]
+        lib.qo_gemv_q4_0_q8.argtypes = [_c_u8p, _c_i8p, ctypes.c_float, ctypes.c_int,
+                                        ctypes.c_int, _c_f32p, ctypes.c_int]
+        lib.qo_matmul_q4_0.argtypes = [_c_u8p, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, _c_f32p, ctypes.c_int]
+        lib.qo_q4_0_block_sums.argtypes = [_c_u8p, _c_i8p, ctypes.c_int, ctypes.c_int, _c_i32p]
+        lib.qo_gemv_hvsq2_scalar.argtypes = [_c_u8p, _c_i8p, _c_i32p, ctypes.c_float,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_size_t, _c_f32p]
+        lib.qo_gemv_hvsq2_delayed.argtypes = [_c_u8p, _c_i8p, _c_i32p, ctypes.c_float,
+                                              ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                              _c_f32p, ctypes.c_int]
+        lib.qo_matmul_hvsq2.argtypes = [_c_u8p, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, _c_f32p, ctypes.c_int, ctypes.c_int]
+        lib.qo_hvsq2_octant_sums.argtypes = [_c_u8p, _c_i8p, ctypes.c_int, ctypes.c_int,
+                                             _c_i32p, _c_i32p]
+        lib.qo_hvsq2_best_variant.restype = ctypes.c_int
+        lib.qo_variant_name.argtypes = [ctypes.c_int]
+        lib.qo_variant_name.restype = ctypes.c_char_p
+        lib.qo_matmul_f16.argtypes = [_c_u16p, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, _c_f32p, ctypes.c_int]
+        lib.qo_q8_quantize_vector.argtypes = [_c_f32p, _c_i8p, _c_f32p, ctypes.c_int]
+        lib.qo_q8_attention.argtypes = [_c_f32p, _c_i8p, _c_i8p, _c_f32p, _c_f32p,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_float, _c_f32p, ctypes.c_int]
+
+    # -- scalar helpers -------------------------------------------------
+    def half_to_float(self, h: int) -> float:
+        return self.lib.qo_half_to_float(h)
+
+    def best_variant(self) -> int:
+        return self.lib.qo_hvsq2_best_variant()
+
+    def variant_name(self, v: int) -> str:
+        return self.lib.qo_variant_name(v).decode()
+
+    # -- a1 ---------------------------------------------------------------
+    def quantize(self, x: np.ndarray, padded_k: int | None = None):
+        """Per-token quantization; returns (q8 [M, padded_k], scales [M],
+        sums [M, padded_k/32])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        M, K = x.shape
+        padded = padded_k or (K + 255) // 256 * 256
+        q8 = np.zeros((M, padded), dtype=np.int8)
+        scales = np.zeros(M, dtype=np.float32)
+        sums = np.zeros((M, padded // 32), dtype=np.int32)
+        self.lib.qo_quantize_tokens(ptr(x, ctypes.c_float), M, K, padded, ptr(q8, ctypes.c_int8),
+                                    ptr(scales, ctypes.c_float), ptr(sums, ctypes.c_int32),
+                                    padded // 32)
+        return q8, scales, sums
+
+    # -- Q4_0 ---------------------------------------------------------------
+    def gemv_q4_0_q8(self, w: np.ndarray, q8: np.ndarray, x_scale: float, K: int, N: int,
+                     threads: int = 0) -> np.ndarray:
+        y = np.zeros(N, dtype=np.float32)
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        self.lib.qo_gemv_q4_0_q8(ptr(w, ctypes.c_uint8), ptr(q8, ctypes.c_int8), x_scale, K, N,
+                                 ptr(y, ctypes.c_float), threads)
+        return y
+
+    def matmul_q4_0(self, w: np.ndarray, x: np.ndarray, N: int, threads: int = 0) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        M, K = x.shape
+        y = np.zeros((M, N), dtype=np.float32)
+        rc = self.lib.qo_matmul_q4_0(ptr(w, ctypes.c_uint8), ptr(x, ctypes.c_float), M, K, N,
+                                     ptr(y, ctypes.c_float), threads)
+        assert rc == 0
+        return y
+
+    def q4_0_block_sums(self, w: np.ndarray, q8: np.ndarray, K: int, N: int) -> np.ndarray:
+        raw = np.zeros((N, (K + 31) // 32), dtype=np.int32)
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        self.lib.qo_q4_0_block_sums(ptr(w, ctypes.c_uint8), ptr(q8, ctypes.c_int8), K, N,
+                                    ptr(raw, ctypes.c_int32))
+        return raw
+
+    # -- HyperVSQ-2 ------------------------------------------------------------
+    def gemv_hvsq2(self, w: np.ndarray, q8: np.ndarray, sums, x_scale: float, K: int, N: int,
+                   variant: int = -1) -> np.ndarray:
+        """variant -2 = scalar golden, otherwise the delayed kernel."""
+        y = np.zeros(N, dtype=np.float32)
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        sp = ptr(np.ascontiguousarray(sums, dtype=np.int32), ctypes.c_int32) if sums is not None \
+            else None
+        row_bytes = (K + 255) // 256 * 74
+        if variant == -2:
+            self.lib.qo_gemv_hvsq2_scalar(ptr(w, ctypes.c_uint8), ptr(q8, ctypes.c_int8), sp,
+                                          x_scale, K, N, row_bytes, ptr(y, ctypes.c_float))
+        else:
+            self.lib.qo_gemv_hvsq2_delayed(ptr(w, ctypes.c_uint8), ptr(q8, ctypes.c_int8), sp,
+                                           x_scale, K, N, row_bytes, ptr(y, ctypes.c_float),
+                                           variant)
+        return y
+
+    def matmul_hvsq2(self, w: np.ndarray, x: np.ndarray, N: int, threads: int = 0,
+                     variant: int = -1) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        M, K = x.shape
+        y = np.zeros((M, N), dtype=np.float32)
+        rc = self.lib.qo_matmul_hvsq2(ptr(w, ctypes.c_uint8), ptr(x, ctypes.c_float), M, K, N,
+                                      ptr(y, ctypes.c_float), threads, variant)
+        assert rc == 0
+        return y
+
+    def hvsq2_octant_sums(self, w: np.ndarray, q8: np.ndarray, K: int, N: int):
+        nb = (K + 255) // 256
+        sq = np.zeros((N, nb * 8), dtype=np.int32)
+        sa = np.zeros(nb * 8, dtype=np.int32)
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        self.lib.qo_hvsq2_octant_sums(ptr(w, ctypes.c_uint8), ptr(q8, ctypes.c_int8), K, N,
+                                      ptr(sq, ctypes.c_int32), ptr(sa, ctypes.c_int32))
+        return sq, sa
+
+    # -- F16 -------------------------------------------------------------------
+    def matmul_f16(self, w: np.ndarray, x: np.ndarray, threads: int = 1) -> np.ndarray:
+        w = np.ascontiguousarray(w, dtype=np.float16)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        N, K = w.shape
+        M = x.shape[0]
+        y = np.zeros((M, N), dtype=np.float32)
+        self.lib.qo_matmul_f16(w.view(np.uint16).ctypes.data_as(_c_u16p), ptr(x, ctypes.c_float),
+                               M, K, N, ptr(y, ctypes.c_float), threads)
+        return y
+
+    # -- Q8 KV -----------------------------------------------------------------
+    def q8_quantize(self, v: np.ndarray):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        n = v.shape[-1]
+        groups = (n + 63) // 64
+        flat = v.reshape(-1, n)
+        q = np.zeros(flat.shape, dtype=np.int8)
+        s = np.zeros((flat.shape[0], groups), dtype=np.float32)
+        for t in range(flat.shape[0]):
+            self.lib.qo_q8_quantize_vector(ptr(flat[t], ctypes.c_float), ptr(q[t], ctypes.c_int8),
+                                           ptr(s[t], ctypes.c_float), n)
+        return q.reshape(v.shape), (s[0] if v.ndim == 1 else s.reshape(v.shape[:-1] + (groups,)))
+
+    def q8_attention(self, query, kq, vq, ks, vs, query_heads, kv_heads, head_dim, pos, scale,
+                     threads: int = 0) -> np.ndarray:
+        out = np.zeros(query_heads * head_dim, dtype=np.float32)
+        query = np.ascontiguousarray(query, dtype=np.float32)
+        self.lib.qo_q8_attention(ptr(query, ctypes.c_float), ptr(kq, ctypes.c_int8),
+                                 ptr(vq, ctypes.c_int8), ptr(ks, ctypes.c_float),
+                                 ptr(vs, ctypes.c_float), query_heads, kv_heads, head_dim, pos,
+                                 scale, ptr(out, ctypes.c_float), threads)
+        return out
+
+
+class Reference:
+    """The reference's own CPU kernels (oracle/_ref), for pinning the oracle."""
+
+    def __init__(self, path: str = REF_SO):
+        lib = ctypes.CDLL(path)
+        self.lib = lib
+        for name in ("ref_matmul_q4_0", "ref_matmul_hvsq2", "ref_matmul_f16"):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, _c_f32p, ctypes.c_int, ctypes.c_int,
+                           ctypes.c_int, _c_f32p]
+        lib.ref_quantize_token.argtypes = [_c_f32p, ctypes.c_int, _c_i8p, _c_f32p, _c_i32p]
+        lib.ref_cpu_kernel_name.restype = ctypes.c_char_p
+        lib.ref_q8_attention.argtypes = [_c_f32p, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_float, _c_f32p, _c_i8p, _c_i8p, _c_f32p,
+                                         _c_f32p]
+        lib.qwn_gemv_hypervsq2_scalar.argtypes = [_c_u8p, _c_i8p, _c_i32p, ctypes.c_float,
+                                                  ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                                  _c_f32p]
+        lib.qwn_gemv_hypervsq2_vnni_delayed.argtypes = lib.qwn_gemv_hypervsq2_scalar.argtypes
+
+    def cpu_kernel_name(self) -> str:
+        return self.lib.ref_cpu_kernel_name().decode()
+
+    def _matmul(self, fn, w: np.ndarray, x: np.ndarray, N: int) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        M, K = x.shape
+        y = np.zeros((M, N), dtype=np.float32)
+        rc = fn(w.ctypes.data, w.nbytes, ptr(x, ctypes.c_float), M, K, N, ptr(y, ctypes.c_float))
+        assert rc == 0, "reference matmul rejected its input"
+        return y
+
+    def matmul_q4_0(self, w, x, N):
+        return self._matmul(self.lib.ref_matmul_q4_0, w, x, N)
+
+    def matmul_hvsq2(self, w, x, N):
+        return self._matmul(self.lib.ref_matmul_hvsq2, w, x, N)
+
+    def matmul_f16(self, w, x):
+        w = np.ascontiguousarray(w, dtype=np.float16)
+        return self._matmul(self.lib.ref_matmul_f16, w, x, w.shape[0])
+
+    def quantize_token(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        K = x.shape[0]
+        padded = (K + 255) // 256 * 256
+        q8 = np.zeros(padded, dtype=np.int8)
+        scale = np.zeros(1, dtype=np.float32)
+        sums = np.zeros(padded // 32, dtype=np.int32)
+        rc = self.lib.ref_quantize_token(ptr(x, ctypes.c_float), K, ptr(q8, ctypes.c_int8),
+                                         ptr(scale, ctypes.c_float), ptr(sums, ctypes.c_int32))
+        assert rc == 0
+        return q8, float(scale[0]), sums
+
+    def gemv_hvsq2(self, w, q8, sums, x_scale, K, N, delayed=True):
+        y = np.zeros(N, dtype=np.float32)
+        fn = self.lib.qwn_gemv_hypervsq2_vnni_delayed if delayed else \
+            self.lib.qwn_gemv_hypervsq2_scalar
+        sp = ptr(np.ascontiguousarray(sums, dtype=np.int32), ctypes.c_int32) if sums is not None \
+            else None
+        fn(ptr(w, ctypes.c_uint8), ptr(np.ascontiguousarray(q8, dtype=np.int8), ctypes.c_int8), sp,
+           x_scale, K, N, (K + 255) // 256 * 74, ptr(y, ctypes.c_float))
+        return y
+
+    def q8_attention(self, keys, values, kv_heads, head_dim, query, query_heads, pos, scale):
+        keys = np.ascontiguousarray(keys, dtype=np.float32)
+        values = np.ascontiguousarray(values, dtype=np.float32)
+        query = np.ascontiguousarray(query, dtype=np.float32)
+        tokens = keys.shape[0]
+        channels = kv_heads * head_dim
+        groups = (channels + 63) // 64
+        out = np.zeros(query_heads * head_dim, dtype=np.float32)
+        kq = np.zeros((tokens, channels), dtype=np.int8)
+        vq = np.zeros((tokens, channels), dtype=np.int8)
+        ks = np.zeros((tokens, groups), dtype=np.float32)
+        vs = np.zeros((tokens, groups), dtype=np.float32)
+        rc = self.lib.ref_q8_attention(ptr(keys, ctypes.c_float), ptr(values, ctypes.c_float),
+                                       tokens, kv_heads, head_dim, ptr(query, ctypes.c_float),
+                                       query_heads, pos, scale, ptr(out, ctypes.c_float),
+                                       ptr(kq, ctypes.c_int8), ptr(vq, ctypes.c_int8),
+                                       ptr(ks, ctypes.c_float), ptr(vs, ctypes.c_float))
+        assert rc == 0
+        return out, kq, vq, ks, vs
+
+
+def load() -> Oracle:
+    return Oracle()
+
+
+def load_ref():
+    return Reference() if os.path.exists(REF_SO) else None

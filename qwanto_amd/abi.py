@@ -1,0 +1,411 @@
+"""ctypes binding of the qwn_hip C ABI (include/qwn_cuda_abi.h, qwn_hip_ext.h).
+
+This is the host-side mirror of what qwnrun binds with dlsym
+(c/qwanto_decode.c:267-462): the same struct layouts, the same call
+sequence (query -> enumerate -> context_create -> upload -> gemv), the same
+status codes.  ``Library`` loads the in-tree build and raises if it is
+missing; there is no CPU fallback anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libqwn_hip.so")
+
+ABI_VERSION = 1
+STATUS = {0: "OK", -1: "INVALID_ARGUMENT", -2: "ABI_MISMATCH", -3: "UNAVAILABLE",
+          -4: "OUT_OF_MEMORY", -5: "UNSUPPORTED", -6: "RUNTIME_ERROR"}
+
+CAP_HYPERVSQ2_GEMV = 1 << 0
+CAP_HYPERVSQ2_GEMM = 1 << 1
+CAP_RESIDENT_WEIGHTS = 1 << 2
+CAP_TELEMETRY = 1 << 3
+CAP_DEVICE_ENUMERATION = 1 << 4
+CAP_Q8_KV = 1 << 5
+CAP_Q4_0_GEMV = 1 << 6
+CAP_F16_GEMV = 1 << 7
+CAP_DEVICE_POINTERS = 1 << 8
+
+TENSOR_HYPERVSQ2_74 = 1
+TENSOR_Q4_0_18 = 2
+TENSOR_F16 = 3
+INPUT_Q8 = 1
+INPUT_F32 = 2
+
+DTYPES = {"hvsq2": (TENSOR_HYPERVSQ2_74, 74), "q4_0": (TENSOR_Q4_0_18, 18), "f16": (TENSOR_F16, 2)}
+
+EXPORTS = (
+    "qwn_cuda_abi_query", "qwn_cuda_abi_get_capabilities", "qwn_cuda_abi_enumerate_devices",
+    "qwn_cuda_abi_context_create", "qwn_cuda_abi_context_destroy", "qwn_cuda_abi_upload_tensor",
+    "qwn_cuda_abi_release_tensor", "qwn_cuda_abi_kv_cache_create", "qwn_cuda_abi_kv_cache_destroy",
+    "qwn_cuda_abi_kv_cache_append", "qwn_cuda_abi_kv_cache_attention", "qwn_cuda_abi_kv_cache_reset",
+    "qwn_cuda_abi_hypervsq2_gemv", "qwn_cuda_abi_hypervsq2_gemm", "qwn_cuda_abi_synchronize",
+    "qwn_cuda_abi_get_telemetry", "qwn_cuda_abi_last_error",
+)
+EXT_EXPORTS = (
+    "qwn_hip_ext_tensor_info", "qwn_hip_ext_gemm_device", "qwn_hip_ext_quantize_device",
+    "qwn_hip_ext_kv_append_device", "qwn_hip_ext_attention_workspace_bytes",
+    "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
+)
+
+
+class Header(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("abi_version", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32 * 4)]
+
+
+class _Versioned(ctypes.Structure):
+    """Structs whose first member is a Header, initialised on construction."""
+
+    def __init__(self, **kw):
+        super().__init__(**kw)
+        self.header.struct_size = ctypes.sizeof(self)
+        self.header.abi_version = ABI_VERSION
+
+
+class AbiInfo(_Versioned):
+    _fields_ = [("header", Header), ("capability_bits", ctypes.c_uint64),
+                ("max_devices", ctypes.c_uint32), ("max_resident_tensors", ctypes.c_uint32),
+                ("hypervsq2_block_bytes", ctypes.c_uint32),
+                ("hypervsq2_block_elements", ctypes.c_uint32), ("abi_name", ctypes.c_char * 32)]
+
+
+class DeviceInfo(_Versioned):
+    _fields_ = [("header", Header), ("device_id", ctypes.c_int32), ("compute_major", ctypes.c_int32),
+                ("compute_minor", ctypes.c_int32), ("total_vram_bytes", ctypes.c_uint64),
+                ("free_vram_bytes", ctypes.c_uint64), ("name", ctypes.c_char * 128),
+                ("driver", ctypes.c_char * 64)]
+
+
+class ContextOptions(_Versioned):
+    _fields_ = [("header", Header), ("device_id", ctypes.c_int32), ("flags", ctypes.c_uint32),
+                ("memory_budget_bytes", ctypes.c_uint64), ("context_size", ctypes.c_uint64)]
+
+
+class Handle(_Versioned):
+    _fields_ = [("header", Header), ("opaque", ctypes.c_void_p)]
+
+
+ContextHandle = TensorHandle = KvCacheHandle = Handle
+
+
+class KvCacheOptions(_Versioned):
+    _fields_ = [("header", Header), ("max_tokens", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class KvAppendRequest(_Versioned):
+    _fields_ = [("header", Header), ("cache", Handle), ("host_key", ctypes.c_void_p),
+                ("host_value", ctypes.c_void_p), ("n_channels", ctypes.c_uint32),
+                ("token", ctypes.c_uint32)]
+
+
+class KvAttentionRequest(_Versioned):
+    _fields_ = [("header", Header), ("cache", Handle), ("host_query", ctypes.c_void_p),
+                ("host_output", ctypes.c_void_p), ("query_heads", ctypes.c_uint32),
+                ("kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("position", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+class TensorUpload(_Versioned):
+    _fields_ = [("header", Header), ("host_data", ctypes.c_void_p), ("data_bytes", ctypes.c_uint64),
+                ("dtype", ctypes.c_uint32), ("rows", ctypes.c_uint32), ("cols", ctypes.c_uint32),
+                ("block_bytes", ctypes.c_uint32)]
+
+
+class GemmRequest(_Versioned):
+    _fields_ = [("header", Header), ("tensor", Handle), ("input_q8", ctypes.c_void_p),
+                ("input_scale", ctypes.c_float), ("input_scales", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("batch", ctypes.c_uint32), ("rows", ctypes.c_uint32),
+                ("cols", ctypes.c_uint32), ("input_stride", ctypes.c_uint32),
+                ("output_stride", ctypes.c_uint32), ("input_mode", ctypes.c_uint32)]
+
+
+class Telemetry(_Versioned):
+    _fields_ = [("header", Header), ("gpu_matmul_count", ctypes.c_uint64),
+                ("gpu_kernel_launch_count", ctypes.c_uint64),
+                ("gpu_projection_count", ctypes.c_uint64), ("gpu_upload_count", ctypes.c_uint64),
+                ("gpu_upload_bytes", ctypes.c_uint64), ("gpu_resident_bytes", ctypes.c_uint64),
+                ("cpu_matmul_fallback_count", ctypes.c_uint64),
+                ("unsupported_projection_count", ctypes.c_uint64),
+                ("gpu_kernel_ms", ctypes.c_double), ("gpu_transfer_ms", ctypes.c_double),
+                ("gpu_sync_ms", ctypes.c_double), ("device_id", ctypes.c_int32),
+                ("reserved_device", ctypes.c_uint32), ("device_name", ctypes.c_char * 128),
+                ("kernel_type", ctypes.c_char * 32), ("dll_hash", ctypes.c_char * 65),
+                ("kv_cache_kernel_count", ctypes.c_uint64),
+                ("kv_cache_upload_bytes", ctypes.c_uint64),
+                ("kv_cache_resident_bytes", ctypes.c_uint64),
+                ("kv_cache_kernel_ms", ctypes.c_double), ("kv_cache_transfer_ms", ctypes.c_double),
+                ("kv_cache_kernel_type", ctypes.c_char * 32)]
+
+
+class TensorInfo(_Versioned):
+    _fields_ = [("header", Header), ("dtype", ctypes.c_uint32), ("rows", ctypes.c_uint32),
+                ("cols", ctypes.c_uint32), ("units_per_row", ctypes.c_uint32),
+                ("logical_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
+                ("lanes_per_row", ctypes.c_uint32), ("units_per_lane", ctypes.c_uint32),
+                ("rows_per_wave", ctypes.c_uint32), ("grid", ctypes.c_uint32)]
+
+
+STRUCTS = {
+    "QwnCudaAbiHeader": Header, "QwnCudaAbiInfo": AbiInfo, "QwnCudaDeviceInfo": DeviceInfo,
+    "QwnCudaContextOptions": ContextOptions, "QwnCudaContextHandle": Handle,
+    "QwnCudaTensorHandle": Handle, "QwnCudaKvCacheHandle": Handle,
+    "QwnCudaKvCacheOptions": KvCacheOptions, "QwnCudaKvAppendRequest": KvAppendRequest,
+    "QwnCudaKvAttentionRequest": KvAttentionRequest, "QwnCudaTensorUpload": TensorUpload,
+    "QwnCudaGemmRequest": GemmRequest, "QwnCudaTelemetry": Telemetry,
+}
+
+
+class AbiError(RuntimeError):
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} -> {STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+def _p(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+class Library:
+    """The loaded qwn_hip shared library (no fallback: missing -> error)."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is missing; build it with qwanto_amd.build.build() (the GPU path has no "
+                "CPU fallback)")
+        self.path = path
+        lib = ctypes.CDLL(path)
+        self.lib = lib
+        P = ctypes.POINTER
+        lib.qwn_cuda_abi_query.argtypes = [P(AbiInfo)]
+        lib.qwn_cuda_abi_get_capabilities.argtypes = [P(AbiInfo)]
+        lib.qwn_cuda_abi_enumerate_devices.argtypes = [P(DeviceInfo), ctypes.c_uint32,
+                                                       P(ctypes.c_uint32)]
+        lib.qwn_cuda_abi_context_create.argtypes = [P(ContextOptions), P(Handle)]
+        lib.qwn_cuda_abi_context_destroy.argtypes = [P(Handle)]
+        lib.qwn_cuda_abi_upload_tensor.argtypes = [P(Handle), P(TensorUpload), P(Handle)]
+        lib.qwn_cuda_abi_release_tensor.argtypes = [P(Handle), P(Handle)]
+        lib.qwn_cuda_abi_kv_cache_create.argtypes = [P(Handle), P(KvCacheOptions), P(Handle)]
+        lib.qwn_cuda_abi_kv_cache_destroy.argtypes = [P(Handle), P(Handle)]
+        lib.qwn_cuda_abi_kv_cache_append.argtypes = [P(Handle), P(KvAppendRequest), P(Telemetry)]
+        lib.qwn_cuda_abi_kv_cache_attention.argtypes = [P(Handle), P(KvAttentionRequest),
+                                                        P(Telemetry)]
+        lib.qwn_cuda_abi_kv_cache_reset.argtypes = [P(Handle), P(Handle)]
+        lib.qwn_cuda_abi_hypervsq2_gemv.argtypes = [P(Handle), P(GemmRequest), P(Telemetry)]
+        lib.qwn_cuda_abi_hypervsq2_gemm.argtypes = [P(Handle), P(GemmRequest), P(Telemetry)]
+        lib.qwn_cuda_abi_synchronize.argtypes = [P(Handle)]
+        lib.qwn_cuda_abi_get_telemetry.argtypes = [P(Handle), P(Telemetry)]
+        lib.qwn_cuda_abi_last_error.argtypes = [ctypes.c_char_p, ctypes.c_uint32]
+        lib.qwn_hip_ext_tensor_info.argtypes = [P(Handle), P(TensorInfo)]
+        lib.qwn_hip_ext_gemm_device.argtypes = [P(Handle), P(GemmRequest), ctypes.c_void_p]
+        lib.qwn_hip_ext_quantize_device.argtypes = [P(Handle), ctypes.c_void_p, ctypes.c_uint32,
+                                                    ctypes.c_uint32, ctypes.c_uint32,
+                                                    ctypes.c_void_p, ctypes.c_uint32,
+                                                    ctypes.c_void_p, ctypes.c_void_p]
+        lib.qwn_hip_ext_kv_append_device.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
+                                                     ctypes.c_void_p, ctypes.c_uint32,
+                                                     ctypes.c_void_p]
+        lib.qwn_hip_ext_attention_workspace_bytes.argtypes = [P(Handle), ctypes.c_uint32,
+                                                              ctypes.c_uint32]
+        lib.qwn_hip_ext_attention_workspace_bytes.restype = ctypes.c_uint64
+        lib.qwn_hip_ext_kv_attention_device.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
+                                                        ctypes.c_void_p, ctypes.c_uint32,
+                                                        ctypes.c_uint32, ctypes.c_float,
+                                                        ctypes.c_void_p, ctypes.c_void_p]
+        lib.qwn_hip_ext_debug_int_sums.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
+                                                   ctypes.c_void_p, ctypes.c_uint64]
+
+    def last_error(self) -> str:
+        buf = ctypes.create_string_buffer(512)
+        self.lib.qwn_cuda_abi_last_error(buf, 512)
+        return buf.value.decode(errors="replace")
+
+    def check(self, fn: str, status: int) -> None:
+        if status != 0:
+            raise AbiError(fn, status, self.last_error())
+
+    def call(self, fn: str, *args) -> int:
+        return getattr(self.lib, fn)(*args)
+
+    def query(self) -> AbiInfo:
+        info = AbiInfo()
+        self.check("query", self.lib.qwn_cuda_abi_query(ctypes.byref(info)))
+        return info
+
+    def devices(self) -> list[DeviceInfo]:
+        arr = (DeviceInfo * 16)()
+        for d in arr:
+            d.header.struct_size = ctypes.sizeof(DeviceInfo)
+            d.header.abi_version = ABI_VERSION
+        count = ctypes.c_uint32(0)
+        st = self.lib.qwn_cuda_abi_enumerate_devices(arr, 16, ctypes.byref(count))
+        if st != 0:
+            return []
+        return [arr[i] for i in range(min(count.value, 16))]
+
+
+class Context:
+    """One qwn_hip context: resident tensors, KV caches, telemetry."""
+
+    def __init__(self, lib: Library, device: int = 0, budget: int = 0):
+        self.lib = lib
+        opts = ContextOptions(device_id=device, memory_budget_bytes=budget)
+        self.handle = Handle()
+        lib.check("context_create",
+                  lib.lib.qwn_cuda_abi_context_create(ctypes.byref(opts), ctypes.byref(self.handle)))
+        self._h = ctypes.byref(self.handle)
+
+    def close(self) -> None:
+        if self.handle.opaque:
+            self.lib.check("context_destroy", self.lib.lib.qwn_cuda_abi_context_destroy(self._h))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- tensors --------------------------------------------------------------
+    def upload(self, data: np.ndarray, dtype: str, rows: int, cols: int) -> Handle:
+        code, block = DTYPES[dtype]
+        data = np.ascontiguousarray(data)
+        up = TensorUpload(host_data=_p(data), data_bytes=data.nbytes, dtype=code, rows=rows,
+                          cols=cols, block_bytes=block)
+        h = Handle()
+        self.lib.check("upload_tensor", self.lib.lib.qwn_cuda_abi_upload_tensor(
+            self._h, ctypes.byref(up), ctypes.byref(h)))
+        return h
+
+    def release(self, h: Handle) -> None:
+        self.lib.check("release_tensor",
+                       self.lib.lib.qwn_cuda_abi_release_tensor(self._h, ctypes.byref(h)))
+
+    def tensor_info(self, h: Handle) -> TensorInfo:
+        info = TensorInfo()
+        self.lib.check("tensor_info",
+                       self.lib.lib.qwn_hip_ext_tensor_info(ctypes.byref(h), ctypes.byref(info)))
+        return info
+
+    def gemm(self, h: Handle, x: np.ndarray, rows: int, cols: int, scale=None, scales=None,
+             gemv: bool = False, telemetry: Telemetry | None = None) -> np.ndarray:
+        """y[batch][rows] for int8 x[batch][>=cols] (or fp32 x for F16 tensors)."""
+        x = np.ascontiguousarray(x)
+        if x.ndim == 1:
+            x = x[None, :]
+        batch, stride = x.shape
+        out = np.zeros((batch, rows), dtype=np.float32)
+        sc = None if scales is None else np.ascontiguousarray(scales, dtype=np.float32)
+        req = GemmRequest(tensor=h, input_q8=_p(x), input_scale=float(scale or 0.0),
+                          input_scales=_p(sc), output=_p(out), batch=batch, rows=rows, cols=cols,
+                          input_stride=stride, output_stride=rows,
+                          input_mode=INPUT_F32 if x.dtype == np.float32 else INPUT_Q8)
+        tm = telemetry if telemetry is not None else Telemetry()
+        fn = "qwn_cuda_abi_hypervsq2_gemv" if gemv else "qwn_cuda_abi_hypervsq2_gemm"
+        self.lib.check(fn, getattr(self.lib.lib, fn)(self._h, ctypes.byref(req), ctypes.byref(tm)))
+        return out
+
+    def debug_int_sums(self, h: Handle, q8: np.ndarray, count: int) -> np.ndarray:
+        out = np.zeros(count, dtype=np.int32)
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        self.lib.check("debug_int_sums", self.lib.lib.qwn_hip_ext_debug_int_sums(
+            self._h, ctypes.byref(h), _p(q8), _p(out), count))
+        return out
+
+    def gemm_device(self, h: Handle, x_ptr: int, out_ptr: int, rows: int, cols: int,
+                    batch: int, input_stride: int, scales_ptr: int | None = None,
+                    scale: float = 0.0, f32: bool = False, stream: int | None = None) -> None:
+        req = GemmRequest(tensor=h, input_q8=x_ptr, input_scale=scale, input_scales=scales_ptr,
+                          output=out_ptr, batch=batch, rows=rows, cols=cols,
+                          input_stride=input_stride, output_stride=rows,
+                          input_mode=INPUT_F32 if f32 else INPUT_Q8)
+        self.lib.check("gemm_device", self.lib.lib.qwn_hip_ext_gemm_device(
+            self._h, ctypes.byref(req), stream))
+
+    def quantize_device(self, x_ptr: int, batch: int, cols: int, x_stride: int, q8_ptr: int,
+                        q8_stride: int, scales_ptr: int, stream: int | None = None) -> None:
+        self.lib.check("quantize_device", self.lib.lib.qwn_hip_ext_quantize_device(
+            self._h, x_ptr, batch, cols, x_stride, q8_ptr, q8_stride, scales_ptr, stream))
+
+    # -- KV cache ---------------------------------------------------------------
+    def kv_create(self, max_tokens: int, kv_heads: int, head_dim: int) -> Handle:
+        opts = KvCacheOptions(max_tokens=max_tokens, kv_heads=kv_heads, head_dim=head_dim)
+        h = Handle()
+        self.lib.check("kv_cache_create", self.lib.lib.qwn_cuda_abi_kv_cache_create(
+            self._h, ctypes.byref(opts), ctypes.byref(h)))
+        return h
+
+    def kv_destroy(self, h: Handle) -> None:
+        self.lib.check("kv_cache_destroy",
+                       self.lib.lib.qwn_cuda_abi_kv_cache_destroy(self._h, ctypes.byref(h)))
+
+    def kv_reset(self, h: Handle) -> None:
+        self.lib.check("kv_cache_reset",
+                       self.lib.lib.qwn_cuda_abi_kv_cache_reset(self._h, ctypes.byref(h)))
+
+    def kv_append(self, h: Handle, key: np.ndarray, value: np.ndarray, token: int,
+                  telemetry: Telemetry | None = None) -> None:
+        key = np.ascontiguousarray(key, dtype=np.float32)
+        value = np.ascontiguousarray(value, dtype=np.float32)
+        req = KvAppendRequest(cache=h, host_key=_p(key), host_value=_p(value),
+                              n_channels=key.size, token=token)
+        tm = telemetry if telemetry is not None else Telemetry()
+        self.lib.check("kv_cache_append", self.lib.lib.qwn_cuda_abi_kv_cache_append(
+            self._h, ctypes.byref(req), ctypes.byref(tm)))
+
+    def kv_attention(self, h: Handle, query: np.ndarray, query_heads: int, kv_heads: int,
+                     head_dim: int, position: int, scale: float,
+                     telemetry: Telemetry | None = None) -> np.ndarray:
+        query = np.ascontiguousarray(query, dtype=np.float32)
+        out = np.zeros(query_heads * head_dim, dtype=np.float32)
+        req = KvAttentionRequest(cache=h, host_query=_p(query), host_output=_p(out),
+                                 query_heads=query_heads, kv_heads=kv_heads, head_dim=head_dim,
+                                 position=position, scale=scale)
+        tm = telemetry if telemetry is not None else Telemetry()
+        self.lib.check("kv_cache_attention", self.lib.lib.qwn_cuda_abi_kv_cache_attention(
+            self._h, ctypes.byref(req), ctypes.byref(tm)))
+        return out
+
+    def kv_append_device(self, h: Handle, k_ptr: int, v_ptr: int, count: int,
+                         stream: int | None = None) -> None:
+        self.lib.check("kv_append_device", self.lib.lib.qwn_hip_ext_kv_append_device(
+            self._h, ctypes.byref(h), k_ptr, v_ptr, count, stream))
+
+    def attention_workspace_bytes(self, h: Handle, query_heads: int, position: int) -> int:
+        return int(self.lib.lib.qwn_hip_ext_attention_workspace_bytes(ctypes.byref(h),
+                                                                     query_heads, position))
+
+    def kv_attention_device(self, h: Handle, q_ptr: int, out_ptr: int, query_heads: int,
+                            position: int, scale: float, work_ptr: int,
+                            stream: int | None = None) -> None:
+        self.lib.check("kv_attention_device", self.lib.lib.qwn_hip_ext_kv_attention_device(
+            self._h, ctypes.byref(h), q_ptr, out_ptr, query_heads, position, scale, work_ptr,
+            stream))
+
+    # -- misc -----------------------------------------------------------------
+    def telemetry(self) -> Telemetry:
+        tm = Telemetry()
+        self.lib.check("get_telemetry",
+                       self.lib.lib.qwn_cuda_abi_get_telemetry(self._h, ctypes.byref(tm)))
+        return tm
+
+    def synchronize(self) -> None:
+        self.lib.check("synchronize", self.lib.lib.qwn_cuda_abi_synchronize(self._h))
+
+
+_LIB: Library | None = None
+
+
+def load() -> Library:
+    global _LIB
+    if _LIB is None:
+        _LIB = Library()
+    return _LIB

@@ -1,0 +1,330 @@
+// Q8 KV cache: append (quantize) and split-T decode attention for gfx950.
+//
+// Numerics follow the CPU Q8 cache (c/qwanto_turboquant.c:555-702):
+//   append:    per 64-channel group scale = amax(finite)/127 (1 if 0),
+//              q = rint(clamp(v / scale, -127, 127)), non-finite -> 0
+//   attention: s_t = scale * sum_c q_c * (k_c * ks), softmax over t <= pos,
+//              ctx = sum_t p_t * (v_t * vs)
+// The reference GPU kernel walks tokens serially with every score in
+// shared memory (c/cuda/qwn_hypervsq2_cuda_abi.cu:175-223); here the token
+// range is split across workgroups (flash-decoding), every K/V row is
+// loaded once per KV head and reused by all query heads of its group, and a
+// second pass merges the per-split (max, sum, output) triples.
+//
+// Layout: 16-token pages, K/V int8 [page][kv_head][16][head_dim], scales
+// fp32 [page][16][groups] with groups over the flattened kv_head*head_dim
+// channels (the reference's token-major grouping).
+#include "qwn_internal.h"
+
+#include <algorithm>
+
+namespace qwn {
+namespace {
+
+constexpr int kAttnThreads = 256;
+constexpr int kMaxSplitTokens = 256;
+
+__device__ __forceinline__ size_t kv_offset(const KvCache &c, uint32_t token, uint32_t head) {
+    const uint32_t page = token / kKvPageTokens, slot = token % kKvPageTokens;
+    return ((static_cast<size_t>(page) * c.kv_heads + head) * kKvPageTokens + slot) * c.head_dim;
+}
+
+__device__ __forceinline__ size_t scale_offset(const KvCache &c, uint32_t token) {
+    return static_cast<size_t>(token) * c.groups;  // pages are contiguous: [page][16][groups]
+}
+
+// grid (groups, 2): y = 0 quantizes K, y = 1 quantizes V.  64 threads, one
+// per channel of the group.
+__global__ __launch_bounds__(64) void kv_append_kernel(KvCache c, const float *__restrict__ key,
+                                                       const float *__restrict__ value, uint32_t token) {
+    const uint32_t g = blockIdx.x;
+    const bool is_v = blockIdx.y == 1;
+    const float *src = is_v ? value : key;
+    const uint32_t ch = g * 64 + threadIdx.x;
+    const bool valid = ch < c.channels;
+    const float v = valid ? src[ch] : 0.0f;
+    float amax = (valid && isfinite(v)) ? fabsf(v) : 0.0f;
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    if (threadIdx.x == 0) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, token) + g] = scale;
+    if (valid) {
+        int8_t q = 0;
+        if (isfinite(v)) {
+            const float s = v / scale;  // IEEE division, like the CPU path
+            q = s >= 127.0f ? 127 : (s <= -127.0f ? -127 : static_cast<int8_t>(__builtin_rintf(s)));
+        }
+        const uint32_t head = ch / c.head_dim, dim = ch % c.head_dim;
+        (is_v ? c.values : c.keys)[kv_offset(c, token, head) + dim] = q;
+    }
+}
+
+struct AttnArgs {
+    KvCache c;
+    const float *query;
+    float *partials;  // [query_heads][nsplit][head_dim + 2]
+    uint32_t query_heads;
+    uint32_t group;   // query heads per kv head
+    uint32_t tokens;  // position + 1
+    uint32_t split;   // tokens per split
+    uint32_t nsplit;
+    float scale;
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float i8(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xffu));
+}
+
+// One workgroup = one KV head x one split of <= 256 tokens.
+// FAST: head_dim % 16 == 0 and head_dim <= 256 (16-byte row loads, one
+// scale per 16-channel chunk); otherwise channel-by-channel.
+template <int GMAX, bool FAST>
+__global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    const KvCache &c = a.c;
+    const uint32_t D = c.head_dim;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t split = blockIdx.x;
+    const uint32_t t0 = split * a.split;
+    const uint32_t n = min(a.split, a.tokens - t0);
+    const uint32_t G = a.group;
+    float *q = sm;                              // [GMAX][D]
+    float *p = q + GMAX * D;                    // [split][GMAX]
+    float *wred = p + kMaxSplitTokens * GMAX;   // [4 waves][GMAX]
+    float *pv = wred + 4 * GMAX;                // PV reduction [phases][GMAX][D]
+
+    for (uint32_t i = threadIdx.x; i < GMAX * D; i += blockDim.x) {
+        const uint32_t g = i / D, d = i % D;
+        q[i] = g < G ? a.query[(static_cast<size_t>(kvh) * G + g) * D + d] : 0.0f;
+    }
+    __syncthreads();
+
+    // ---- scores: one thread per token, all query heads of the group ----
+    const uint32_t t = threadIdx.x;
+    float s[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) s[g] = -INFINITY;
+    if (t < n) {
+        const uint32_t tok = t0 + t;
+        const int8_t *krow = c.keys + kv_offset(c, tok, kvh);
+        const float *ks = c.key_scales + scale_offset(c, tok);
+        float dot[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) dot[g] = 0.0f;
+        if (FAST) {
+            for (uint32_t c0 = 0; c0 < D; c0 += 16) {
+                const uint4 kw = *reinterpret_cast<const uint4 *>(krow + c0);
+                const float sc = ks[(kvh * D + c0) / 64];
+                const uint32_t w[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    float kf[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) kf[i] = i8(w[qd], i) * sc;
+#pragma unroll
+                    for (int g = 0; g < GMAX; ++g) {
+                        if (g >= static_cast<int>(G)) break;
+                        const float4 qq = *reinterpret_cast<const float4 *>(q + g * D + c0 + qd * 4);
+                        dot[g] = fmaf(qq.x, kf[0], dot[g]);
+                        dot[g] = fmaf(qq.y, kf[1], dot[g]);
+                        dot[g] = fmaf(qq.z, kf[2], dot[g]);
+                        dot[g] = fmaf(qq.w, kf[3], dot[g]);
+                    }
+                }
+            }
+        } else {
+            for (uint32_t d = 0; d < D; ++d) {
+                const float kf = static_cast<float>(krow[d]) * ks[(kvh * D + d) / 64];
+#pragma unroll
+                for (int g = 0; g < GMAX; ++g)
+                    if (g < static_cast<int>(G)) dot[g] = fmaf(q[g * D + d], kf, dot[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) s[g] = g < static_cast<int>(G) ? dot[g] * a.scale : -INFINITY;
+    }
+
+    // ---- split-local softmax statistics ----
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    float m[GMAX], l[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        const float wm = wave_max(s[g]);
+        if (lane == 0) wred[wave * GMAX + g] = wm;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+        m[g] = fmaxf(fmaxf(wred[g], wred[GMAX + g]), fmaxf(wred[2 * GMAX + g], wred[3 * GMAX + g]));
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        const float e = (t < n && g < static_cast<int>(G)) ? expf(s[g] - m[g]) : 0.0f;
+        if (t < kMaxSplitTokens) p[t * GMAX + g] = e;
+        const float ws = wave_sum(e);
+        if (lane == 0) wred[wave * GMAX + g] = ws;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) l[g] = (wred[g] + wred[GMAX + g]) + (wred[2 * GMAX + g] + wred[3 * GMAX + g]);
+
+    // ---- P.V: thread = (channel quad, token phase), all heads of the group ----
+    const uint32_t quads = (D + 3) / 4;
+    const uint32_t phases = blockDim.x / quads;  // >= 1 since D <= 1024
+    const uint32_t quad = threadIdx.x % quads, phase = threadIdx.x / quads;
+    float acc[GMAX][4];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[g][i] = 0.0f;
+    if (phase < phases) {
+        for (uint32_t tt = phase; tt < n; tt += phases) {
+            const uint32_t tok = t0 + tt;
+            const int8_t *vrow = c.values + kv_offset(c, tok, kvh);
+            const float *vs = c.value_scales + scale_offset(c, tok);
+            float vf[4];
+            if (FAST) {
+                const uint32_t w = *reinterpret_cast<const uint32_t *>(vrow + quad * 4);
+                const float sc = vs[(kvh * D + quad * 4) / 64];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vf[i] = i8(w, i) * sc;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t d = quad * 4 + i;
+                    vf[i] = d < D ? static_cast<float>(vrow[d]) * vs[(kvh * D + d) / 64] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                if (g >= static_cast<int>(G)) break;
+                const float pg = p[tt * GMAX + g];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[g][i] = fmaf(pg, vf[i], acc[g][i]);
+            }
+        }
+    }
+    // reduce the phases through LDS
+    for (uint32_t i = threadIdx.x; i < phases * GMAX * D; i += blockDim.x) pv[i] = 0.0f;
+    __syncthreads();
+    if (phase < phases) {
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t d = quad * 4 + i;
+                if (g < static_cast<int>(G) && d < D) pv[(phase * GMAX + g) * D + d] = acc[g][i];
+            }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < G * D; i += blockDim.x) {
+        const uint32_t g = i / D, d = i % D;
+        float o = 0.0f;
+        for (uint32_t ph = 0; ph < phases; ++ph) o += pv[(ph * GMAX + g) * D + d];
+        const uint32_t head = kvh * G + g;
+        float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
+        dst[2 + d] = o;
+        if (d == 0) {
+            dst[0] = m[g];
+            dst[1] = l[g];
+        }
+    }
+}
+
+// grid (query_heads): merge the split partials of one head.
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float *__restrict__ partials,
+                                                              float *out, uint32_t nsplit, uint32_t D) {
+    const uint32_t head = blockIdx.x;
+    const float *base = partials + static_cast<size_t>(head) * nsplit * (D + 2);
+    float mx = -INFINITY;
+    for (uint32_t sidx = 0; sidx < nsplit; ++sidx) mx = fmaxf(mx, base[sidx * (D + 2)]);
+    float total = 0.0f;
+    for (uint32_t sidx = 0; sidx < nsplit; ++sidx)
+        total += base[sidx * (D + 2) + 1] * expf(base[sidx * (D + 2)] - mx);
+    const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float o = 0.0f;
+        for (uint32_t sidx = 0; sidx < nsplit; ++sidx)
+            o = fmaf(base[sidx * (D + 2) + 2 + d], expf(base[sidx * (D + 2)] - mx), o);
+        out[static_cast<size_t>(head) * D + d] = o * inv;
+    }
+}
+
+uint32_t split_tokens(const KvCache &c, uint32_t tokens) {
+    // aim for >= 1024 workgroups over the KV heads, 16..256 tokens each
+    uint32_t s = (tokens * c.kv_heads + 1023) / 1024;
+    s = (s + 15) / 16 * 16;
+    return std::min<uint32_t>(std::max<uint32_t>(s, 16), kMaxSplitTokens);
+}
+
+template <int GMAX, bool FAST>
+hipError_t launch_split(const AttnArgs &args, hipStream_t stream) {
+    const uint32_t D = args.c.head_dim;
+    const uint32_t quads = (D + 3) / 4;
+    const uint32_t phases = kAttnThreads / quads;
+    const size_t lds = (static_cast<size_t>(GMAX) * D + kMaxSplitTokens * GMAX + 4 * GMAX +
+                        static_cast<size_t>(phases) * GMAX * D) * sizeof(float);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attention_split_kernel<GMAX, FAST>), dim3(args.nsplit, args.c.kv_heads),
+                       dim3(kAttnThreads), lds, stream, args);
+    return hipGetLastError();
+}
+
+template <int GMAX>
+hipError_t launch_fast_or_not(const AttnArgs &args, hipStream_t stream) {
+    const uint32_t D = args.c.head_dim;
+    if (D % 16 == 0 && D <= 256) return launch_split<GMAX, true>(args, stream);
+    return launch_split<GMAX, false>(args, stream);
+}
+
+}  // namespace
+
+hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
+                            hipStream_t stream) {
+    if (token >= c.max_tokens) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2), dim3(64), 0, stream, c, key, value, token);
+    return hipGetLastError();
+}
+
+size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t position) {
+    const uint32_t tokens = position + 1;
+    const uint32_t s = split_tokens(c, tokens);
+    const uint32_t nsplit = (tokens + s - 1) / s;
+    return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
+}
+
+hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
+    const KvCache &c = *a.cache;
+    if (a.position >= c.tokens || a.query_heads % c.kv_heads != 0 || c.head_dim > 1024)
+        return hipErrorInvalidValue;
+    AttnArgs args{};
+    args.c = c;
+    args.query = a.query;
+    args.partials = a.partials;
+    args.query_heads = a.query_heads;
+    args.group = a.query_heads / c.kv_heads;
+    args.tokens = a.position + 1;
+    args.split = split_tokens(c, args.tokens);
+    args.nsplit = (args.tokens + args.split - 1) / args.split;
+    args.scale = a.scale;
+    hipError_t e;
+    if (args.group <= 1) e = launch_fast_or_not<1>(args, stream);
+    else if (args.group <= 2) e = launch_fast_or_not<2>(args, stream);
+    else if (args.group <= 4) e = launch_fast_or_not<4>(args, stream);
+    else if (args.group <= 8) e = launch_fast_or_not<8>(args, stream);
+    else return hipErrorInvalidValue;
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(a.query_heads), dim3(256), 0, stream, a.partials,
+                       a.output, args.nsplit, c.head_dim);
+    return hipGetLastError();
+}
+
+}  // namespace qwn

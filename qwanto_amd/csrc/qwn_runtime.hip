@@ -1,0 +1,971 @@
+// qwn_hip: the qwnrun GPU ABI (qwn_cuda_abi.h) on one MI355X.
+//
+// Replaces c/cuda/qwn_hypervsq2_cuda_abi.cu.  Same contract: versioned
+// struct headers validated on every call, resident weights charged against
+// a memory budget, synchronous host-pointer GEMV/GEMM and Q8-KV calls,
+// cumulative telemetry copied out on every call, one process-wide last
+// error string.  Different machinery: weights are repacked on upload into
+// 16-byte aligned planes, host buffers are staged through pinned memory,
+// every call runs on the context's own non-blocking stream, and each
+// context has its own lock.
+#include "qwn_cuda_abi.h"
+#include "qwn_hip_ext.h"
+#include "qwn_internal.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+using qwn::DeviceTensor;
+using qwn::KvCache;
+
+std::mutex g_error_mutex;
+std::string g_last_error;
+
+void set_error(const char *fmt, ...) {
+    char buffer[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buffer, sizeof(buffer), fmt, ap);
+    va_end(ap);
+    std::lock_guard<std::mutex> lock(g_error_mutex);
+    g_last_error = buffer;
+}
+
+int hip_fail(const char *what, hipError_t e, int status = QWN_CUDA_STATUS_RUNTIME_ERROR) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return status;
+}
+
+template <typename T>
+bool header_ok(const T &s) {
+    return s.header.abi_version == QWN_CUDA_ABI_VERSION && s.header.struct_size >= sizeof(T);
+}
+
+struct PinnedBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t want) {
+        if (want <= bytes) return hipSuccess;
+        if (ptr) (void)hipHostFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+        hipError_t e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
+        if (e == hipSuccess) bytes = want;
+        return e;
+    }
+    void release() {
+        if (ptr) (void)hipHostFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+};
+
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t want) {
+        if (want <= bytes) return hipSuccess;
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+        hipError_t e = hipMalloc(&ptr, want);
+        if (e == hipSuccess) bytes = want;
+        return e;
+    }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+};
+
+struct ResidentTensor {
+    DeviceTensor t;
+    void *allocation = nullptr;
+};
+
+struct ResidentKv {
+    KvCache c;
+    void *allocation = nullptr;
+};
+
+struct Context {
+    std::mutex mutex;
+    int device = -1;
+    uint64_t budget = 0;
+    uint64_t resident = 0;  // logical bytes charged against the budget
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_start = nullptr, ev_end = nullptr;
+    PinnedBuffer host_in, host_out;
+    DeviceBuffer dev_in, dev_out, dev_scales, dev_work;
+    std::vector<ResidentTensor *> tensors;
+    std::vector<ResidentKv *> caches;
+    QwnCudaTelemetry telemetry{};
+};
+
+Context *context_of(const QwnCudaContextHandle *h) {
+    if (!h || !header_ok(*h) || !h->opaque) return nullptr;
+    return static_cast<Context *>(h->opaque);
+}
+
+ResidentTensor *tensor_of(Context *ctx, const QwnCudaTensorHandle &h) {
+    if (!header_ok(h) || !h.opaque) return nullptr;
+    auto *t = static_cast<ResidentTensor *>(h.opaque);
+    // only handles this context issued are accepted
+    return std::find(ctx->tensors.begin(), ctx->tensors.end(), t) != ctx->tensors.end() ? t : nullptr;
+}
+
+ResidentKv *cache_of(Context *ctx, const QwnCudaKvCacheHandle &h) {
+    if (!header_ok(h) || !h.opaque) return nullptr;
+    auto *c = static_cast<ResidentKv *>(h.opaque);
+    return std::find(ctx->caches.begin(), ctx->caches.end(), c) != ctx->caches.end() ? c : nullptr;
+}
+
+double ms_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void copy_telemetry(const Context *ctx, QwnCudaTelemetry *out) {
+    if (out) *out = ctx->telemetry;
+}
+
+const char *kernel_name(int kind) {
+    switch (kind) {
+    case qwn::kHvsq2: return "hvsq2-74-q8-gfx950";
+    case qwn::kQ4_0: return "q4_0-18-q8-gfx950";
+    case qwn::kF16: return "f16-f32-gfx950";
+    default: return "none";
+    }
+}
+
+// Validates a GEMV/GEMM request against a resident tensor; returns the
+// tensor or null (error set).
+ResidentTensor *check_request(Context *ctx, const QwnCudaGemmRequest *r) {
+    if (!r || !header_ok(*r) || !r->input_q8 || !r->output || r->batch == 0 || r->rows == 0 ||
+        r->cols == 0) {
+        set_error("invalid GEMV/GEMM request");
+        return nullptr;
+    }
+    ResidentTensor *rt = tensor_of(ctx, r->tensor);
+    if (!rt || rt->t.rows != r->rows || rt->t.cols != r->cols) {
+        set_error("tensor handle unknown or dimensions do not match the request");
+        return nullptr;
+    }
+    const uint32_t in_stride = r->input_stride ? r->input_stride : r->cols;
+    const uint32_t out_stride = r->output_stride ? r->output_stride : r->rows;
+    if (in_stride < r->cols || out_stride < r->rows) {
+        set_error("input/output stride smaller than the tensor shape");
+        return nullptr;
+    }
+    const bool f16 = rt->t.kind == qwn::kF16;
+    if ((f16 && r->input_mode != QWN_CUDA_INPUT_F32) || (!f16 && r->input_mode != QWN_CUDA_INPUT_Q8)) {
+        set_error("input mode %u does not match the tensor dtype", r->input_mode);
+        return nullptr;
+    }
+    return rt;
+}
+
+int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *telemetry) {
+    ResidentTensor *rt = check_request(ctx, r);
+    if (!rt) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    const DeviceTensor &t = rt->t;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+
+    const bool f16 = t.kind == qwn::kF16;
+    const size_t elem = f16 ? 4 : 1;
+    const uint32_t in_stride = r->input_stride ? r->input_stride : r->cols;
+    const uint32_t out_stride = r->output_stride ? r->output_stride : r->rows;
+    // device copy of the activations with a 16-byte aligned row stride
+    const uint32_t dev_stride = (r->cols + 255u) & ~255u;
+    const size_t in_bytes = static_cast<size_t>(r->batch) * dev_stride * elem;
+    const size_t scale_bytes = static_cast<size_t>(r->batch) * sizeof(float);
+    const size_t out_bytes = static_cast<size_t>(r->batch) * r->rows * sizeof(float);
+    if ((e = ctx->host_in.ensure(in_bytes + scale_bytes)) != hipSuccess ||
+        (e = ctx->host_out.ensure(out_bytes)) != hipSuccess ||
+        (e = ctx->dev_in.ensure(in_bytes)) != hipSuccess ||
+        (e = ctx->dev_scales.ensure(scale_bytes)) != hipSuccess ||
+        (e = ctx->dev_out.ensure(out_bytes)) != hipSuccess)
+        return hip_fail("GEMV workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+
+    const auto t_transfer = std::chrono::steady_clock::now();
+    uint8_t *hin = static_cast<uint8_t *>(ctx->host_in.ptr);
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(r->input_q8);
+    for (uint32_t b = 0; b < r->batch; ++b) {
+        std::memcpy(hin + static_cast<size_t>(b) * dev_stride * elem,
+                    src + static_cast<size_t>(b) * in_stride * elem, static_cast<size_t>(r->cols) * elem);
+        std::memset(hin + (static_cast<size_t>(b) * dev_stride + r->cols) * elem, 0,
+                    static_cast<size_t>(dev_stride - r->cols) * elem);
+    }
+    float *hscales = reinterpret_cast<float *>(hin + in_bytes);
+    for (uint32_t b = 0; b < r->batch; ++b) hscales[b] = r->input_scales ? r->input_scales[b] : r->input_scale;
+    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, in_bytes + 0, hipMemcpyHostToDevice, ctx->stream)) !=
+            hipSuccess ||
+        (e = hipMemcpyAsync(ctx->dev_scales.ptr, hscales, scale_bytes, hipMemcpyHostToDevice,
+                            ctx->stream)) != hipSuccess)
+        return hip_fail("activation upload", e);
+    const double transfer_ms = ms_since(t_transfer);
+
+    qwn::GemvLaunch g{};
+    g.tensor = &t;
+    g.input = ctx->dev_in.ptr;
+    g.scales = static_cast<const float *>(ctx->dev_scales.ptr);
+    g.scale = r->input_scale;
+    g.output = static_cast<float *>(ctx->dev_out.ptr);
+    g.batch = r->batch;
+    g.input_stride = dev_stride;
+    g.output_stride = r->rows;
+    (void)hipEventRecord(ctx->ev_start, ctx->stream);
+    if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
+    (void)hipEventRecord(ctx->ev_end, ctx->stream);
+    if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,
+                            ctx->stream)) != hipSuccess)
+        return hip_fail("result download", e);
+    const auto t_sync = std::chrono::steady_clock::now();
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail("GEMV synchronize", e);
+    const double sync_ms = ms_since(t_sync);
+    const float *hout = static_cast<const float *>(ctx->host_out.ptr);
+    for (uint32_t b = 0; b < r->batch; ++b)
+        std::memcpy(r->output + static_cast<size_t>(b) * out_stride, hout + static_cast<size_t>(b) * r->rows,
+                    static_cast<size_t>(r->rows) * sizeof(float));
+    float kernel_ms = 0.0f;
+    if (hipEventElapsedTime(&kernel_ms, ctx->ev_start, ctx->ev_end) != hipSuccess) kernel_ms = 0.0f;
+
+    QwnCudaTelemetry &tm = ctx->telemetry;
+    tm.gpu_matmul_count++;
+    tm.gpu_kernel_launch_count += (r->batch + qwn::kMaxTokensPerLaunch - 1) / qwn::kMaxTokensPerLaunch;
+    tm.gpu_projection_count++;
+    tm.gpu_kernel_ms += kernel_ms;
+    tm.gpu_transfer_ms += transfer_ms;
+    tm.gpu_sync_ms += sync_ms;
+    tm.gpu_resident_bytes = ctx->resident;
+    tm.device_id = ctx->device;
+    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", kernel_name(t.kind));
+    copy_telemetry(ctx, telemetry);
+    return QWN_CUDA_STATUS_OK;
+}
+
+void free_tensor(ResidentTensor *rt) {
+    if (rt->allocation) (void)hipFree(rt->allocation);
+    delete rt;
+}
+
+void free_cache(ResidentKv *rk) {
+    if (rk->allocation) (void)hipFree(rk->allocation);
+    delete rk;
+}
+
+bool budget_allows(Context *ctx, uint64_t bytes, uint64_t device_bytes) {
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return false;
+    if (ctx->budget && ctx->resident + bytes > ctx->budget) return false;
+    return device_bytes <= free_b;
+}
+
+}  // namespace
+
+extern "C" {
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_query(QwnCudaAbiInfo *info) {
+    if (!info || !header_ok(*info)) {
+        set_error("invalid ABI query structure");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::memset(info, 0, sizeof(*info));
+    qwn_cuda_abi_header_init(&info->header, sizeof(*info));
+    info->capability_bits = QWN_CUDA_CAP_HYPERVSQ2_GEMV | QWN_CUDA_CAP_HYPERVSQ2_GEMM |
+                            QWN_CUDA_CAP_RESIDENT_WEIGHTS | QWN_CUDA_CAP_TELEMETRY |
+                            QWN_CUDA_CAP_DEVICE_ENUMERATION | QWN_CUDA_CAP_Q8_KV |
+                            QWN_CUDA_CAP_Q4_0_GEMV | QWN_CUDA_CAP_F16_GEMV |
+                            QWN_CUDA_CAP_DEVICE_POINTERS;
+    info->max_devices = 16;
+    info->max_resident_tensors = QWN_CUDA_MAX_RESIDENT_TENSORS;
+    info->hypervsq2_block_bytes = QWN_CUDA_HYPERVSQ2_BLOCK_BYTES;
+    info->hypervsq2_block_elements = QWN_CUDA_HYPERVSQ2_BLOCK_ELEMENTS;
+    std::snprintf(info->abi_name, sizeof(info->abi_name), "%s", QWN_CUDA_ABI_NAME);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_get_capabilities(QwnCudaAbiInfo *info) {
+    return qwn_cuda_abi_query(info);
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_enumerate_devices(QwnCudaDeviceInfo *devices, uint32_t capacity,
+                                                    uint32_t *count) {
+    if (!count) {
+        set_error("enumerate_devices: null count");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        *count = 0;
+        return hip_fail("hipGetDeviceCount", e, QWN_CUDA_STATUS_UNAVAILABLE);
+    }
+    *count = static_cast<uint32_t>(n);
+    if (!devices || capacity == 0) return QWN_CUDA_STATUS_OK;
+    int driver = 0;
+    (void)hipDriverGetVersion(&driver);
+    int current = 0;
+    (void)hipGetDevice(&current);
+    const uint32_t limit = std::min<uint32_t>(capacity, *count);
+    for (uint32_t i = 0; i < limit; ++i) {
+        QwnCudaDeviceInfo &d = devices[i];
+        std::memset(&d, 0, sizeof(d));
+        qwn_cuda_abi_header_init(&d.header, sizeof(d));
+        hipDeviceProp_t p{};
+        if (hipGetDeviceProperties(&p, static_cast<int>(i)) != hipSuccess) continue;
+        d.device_id = static_cast<int32_t>(i);
+        // gfx950 -> compute 9.5 (the gfx major/minor digits)
+        d.compute_major = p.major;
+        d.compute_minor = p.minor;
+        d.total_vram_bytes = p.totalGlobalMem;
+        size_t free_b = 0, total_b = 0;
+        if (hipSetDevice(static_cast<int>(i)) == hipSuccess && hipMemGetInfo(&free_b, &total_b) == hipSuccess)
+            d.free_vram_bytes = free_b;
+        std::snprintf(d.name, sizeof(d.name), "%s (%s)", p.name, p.gcnArchName);
+        std::snprintf(d.driver, sizeof(d.driver), "hip %d", driver);
+    }
+    (void)hipSetDevice(current);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *options,
+                                                 QwnCudaContextHandle *handle) {
+    if (!options || !handle || !header_ok(*options) || !header_ok(*handle) || options->device_id < 0) {
+        set_error("invalid context options");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || options->device_id >= n) {
+        set_error("device %d is not available", options->device_id);
+        return QWN_CUDA_STATUS_UNAVAILABLE;
+    }
+    auto *ctx = new (std::nothrow) Context();
+    if (!ctx) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    ctx->device = options->device_id;
+    ctx->budget = options->memory_budget_bytes;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_end);
+    if (e != hipSuccess) {
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail("context creation", e, QWN_CUDA_STATUS_UNAVAILABLE);
+    }
+    QwnCudaTelemetry &tm = ctx->telemetry;
+    std::memset(&tm, 0, sizeof(tm));
+    qwn_cuda_abi_header_init(&tm.header, sizeof(tm));
+    tm.device_id = ctx->device;
+    hipDeviceProp_t p{};
+    if (hipGetDeviceProperties(&p, ctx->device) == hipSuccess)
+        std::snprintf(tm.device_name, sizeof(tm.device_name), "%s (%s)", p.name, p.gcnArchName);
+    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", kernel_name(qwn::kHvsq2));
+    std::snprintf(tm.kv_cache_kernel_type, sizeof(tm.kv_cache_kernel_type), "Unavailable");
+    std::memset(handle, 0, sizeof(*handle));
+    qwn_cuda_abi_header_init(&handle->header, sizeof(*handle));
+    handle->opaque = ctx;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *handle) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    {
+        std::lock_guard<std::mutex> lock(ctx->mutex);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        for (ResidentTensor *t : ctx->tensors) free_tensor(t);
+        for (ResidentKv *c : ctx->caches) free_cache(c);
+        ctx->tensors.clear();
+        ctx->caches.clear();
+        ctx->host_in.release();
+        ctx->host_out.release();
+        ctx->dev_in.release();
+        ctx->dev_out.release();
+        ctx->dev_scales.release();
+        ctx->dev_work.release();
+        (void)hipEventDestroy(ctx->ev_start);
+        (void)hipEventDestroy(ctx->ev_end);
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+    handle->opaque = nullptr;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
+                                                const QwnCudaTensorUpload *up,
+                                                QwnCudaTensorHandle *out) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !up || !out || !header_ok(*up) || !header_ok(*out) || !up->host_data || up->rows == 0 ||
+        up->cols == 0) {
+        set_error("invalid tensor upload request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    DeviceTensor t;
+    t.rows = up->rows;
+    t.cols = up->cols;
+    switch (up->dtype) {
+    case QWN_CUDA_TENSOR_HYPERVSQ2_74:
+        if (up->block_bytes != QWN_CUDA_HYPERVSQ2_BLOCK_BYTES) break;
+        t.kind = qwn::kHvsq2;
+        t.units = (up->cols + 255u) / 256u;
+        t.logical_bytes = static_cast<uint64_t>(up->rows) * t.units * 74u;
+        t.payload_row_bytes = static_cast<size_t>(t.units) * 64u;
+        t.meta_row_bytes = static_cast<size_t>(t.units) * 8u;
+        break;
+    case QWN_CUDA_TENSOR_Q4_0_18: {
+        if (up->block_bytes != QWN_CUDA_Q4_0_BLOCK_BYTES) break;
+        const uint32_t nb = (up->cols + 31u) / 32u;
+        t.kind = qwn::kQ4_0;
+        t.units = (nb + 3u) / 4u;
+        t.logical_bytes = static_cast<uint64_t>(up->rows) * nb * 18u;
+        t.payload_row_bytes = static_cast<size_t>(t.units) * 64u;
+        t.meta_row_bytes = static_cast<size_t>(t.units) * 8u;
+        break;
+    }
+    case QWN_CUDA_TENSOR_F16:
+        if (up->block_bytes != 2) break;
+        t.kind = qwn::kF16;
+        t.units = (up->cols + 7u) / 8u;
+        t.logical_bytes = static_cast<uint64_t>(up->rows) * up->cols * 2u;
+        t.payload_row_bytes = static_cast<size_t>(t.units) * 16u;
+        t.meta_row_bytes = 0;
+        break;
+    default:
+        break;
+    }
+    if (t.kind == 0) {
+        set_error("unsupported tensor dtype %u / block_bytes %u", up->dtype, up->block_bytes);
+        return QWN_CUDA_STATUS_UNSUPPORTED;
+    }
+    if (up->data_bytes < t.logical_bytes) {
+        set_error("tensor upload is shorter than its shape (%llu < %llu bytes)",
+                  static_cast<unsigned long long>(up->data_bytes),
+                  static_cast<unsigned long long>(t.logical_bytes));
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    if (qwn::plan_gemv(t, 1).upl == 0) {
+        set_error("tensor rows of %u columns exceed the GEMV lane plan", up->cols);
+        return QWN_CUDA_STATUS_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    if (ctx->tensors.size() >= QWN_CUDA_MAX_RESIDENT_TENSORS) {
+        set_error("resident tensor limit (%u) reached", QWN_CUDA_MAX_RESIDENT_TENSORS);
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+    const size_t payload = t.payload_row_bytes * t.rows;
+    const size_t meta = t.meta_row_bytes * t.rows;
+    const size_t meta_off = (payload + 255) & ~static_cast<size_t>(255);
+    t.device_bytes = meta_off + meta;
+    if (!budget_allows(ctx, t.logical_bytes, t.device_bytes + t.logical_bytes)) {
+        set_error("tensor does not fit the configured GPU memory budget");
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+    auto *rt = new (std::nothrow) ResidentTensor();
+    if (!rt) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    void *staging = nullptr;
+    if ((e = hipMalloc(&rt->allocation, t.device_bytes)) != hipSuccess ||
+        (e = hipMalloc(&staging, t.logical_bytes)) != hipSuccess) {
+        if (rt->allocation) (void)hipFree(rt->allocation);
+        delete rt;
+        return hip_fail("tensor allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+    }
+    t.payload = static_cast<uint8_t *>(rt->allocation);
+    t.meta = meta ? t.payload + meta_off : nullptr;
+    rt->t = t;
+    const auto t0 = std::chrono::steady_clock::now();
+    e = hipMemcpyAsync(staging, up->host_data, t.logical_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = qwn::repack_tensor(rt->t, static_cast<const uint8_t *>(staging), ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(staging);
+    if (e != hipSuccess) {
+        free_tensor(rt);
+        return hip_fail("tensor upload", e);
+    }
+    ctx->tensors.push_back(rt);
+    ctx->resident += t.logical_bytes;
+    QwnCudaTelemetry &tm = ctx->telemetry;
+    tm.gpu_upload_count++;
+    tm.gpu_upload_bytes += t.logical_bytes;
+    tm.gpu_resident_bytes = ctx->resident;
+    tm.gpu_transfer_ms += ms_since(t0);
+    std::memset(out, 0, sizeof(*out));
+    qwn_cuda_abi_header_init(&out->header, sizeof(*out));
+    out->opaque = rt;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *handle, QwnCudaTensorHandle *h) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h) {
+        set_error("invalid release request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = tensor_of(ctx, *h);
+    if (!rt) {
+        set_error("tensor handle is not resident in this context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->resident -= std::min(ctx->resident, rt->t.logical_bytes);
+    ctx->tensors.erase(std::find(ctx->tensors.begin(), ctx->tensors.end(), rt));
+    free_tensor(rt);
+    ctx->telemetry.gpu_resident_bytes = ctx->resident;
+    h->opaque = nullptr;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_create(QwnCudaContextHandle *handle,
+                                                  const QwnCudaKvCacheOptions *opt,
+                                                  QwnCudaKvCacheHandle *out) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !opt || !out || !header_ok(*opt) || !header_ok(*out) || opt->max_tokens == 0 ||
+        opt->kv_heads == 0 || opt->head_dim == 0) {
+        set_error("invalid Q8 KV-cache options");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    KvCache c;
+    c.max_tokens = opt->max_tokens;
+    c.kv_heads = opt->kv_heads;
+    c.head_dim = opt->head_dim;
+    c.channels = opt->kv_heads * opt->head_dim;
+    c.groups = (c.channels + 63u) / 64u;
+    c.pages = (c.max_tokens + qwn::kKvPageTokens - 1) / qwn::kKvPageTokens;
+    const size_t slots = static_cast<size_t>(c.pages) * qwn::kKvPageTokens;
+    const size_t value_bytes = (slots * c.channels + 255) & ~static_cast<size_t>(255);
+    const size_t scale_bytes = (slots * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
+    const size_t total = 2 * value_bytes + 2 * scale_bytes;
+    // charged like the reference (c/cuda/qwn_hypervsq2_cuda_abi.cu:624-626)
+    c.bytes = static_cast<uint64_t>(c.max_tokens) * c.channels * 2u +
+              static_cast<uint64_t>(c.max_tokens) * c.groups * sizeof(float) * 2u;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    if (ctx->caches.size() >= QWN_CUDA_MAX_RESIDENT_KV_CACHES) {
+        set_error("resident KV-cache limit reached");
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+    if (!budget_allows(ctx, c.bytes, total)) {
+        set_error("Q8 KV-cache does not fit the configured GPU memory budget");
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+    auto *rk = new (std::nothrow) ResidentKv();
+    if (!rk) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    if ((e = hipMalloc(&rk->allocation, total)) != hipSuccess) {
+        delete rk;
+        return hip_fail("Q8 KV-cache allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+    }
+    uint8_t *base = static_cast<uint8_t *>(rk->allocation);
+    c.keys = reinterpret_cast<int8_t *>(base);
+    c.values = reinterpret_cast<int8_t *>(base + value_bytes);
+    c.key_scales = reinterpret_cast<float *>(base + 2 * value_bytes);
+    c.value_scales = reinterpret_cast<float *>(base + 2 * value_bytes + scale_bytes);
+    if ((e = hipMemsetAsync(base, 0, total, ctx->stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+        free_cache(rk);
+        return hip_fail("Q8 KV-cache clear", e);
+    }
+    rk->c = c;
+    ctx->caches.push_back(rk);
+    ctx->resident += c.bytes;
+    ctx->telemetry.kv_cache_resident_bytes += c.bytes;
+    std::memset(out, 0, sizeof(*out));
+    qwn_cuda_abi_header_init(&out->header, sizeof(*out));
+    out->opaque = rk;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_destroy(QwnCudaContextHandle *handle, QwnCudaKvCacheHandle *h) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h) {
+        set_error("invalid KV-cache destroy request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, *h);
+    if (!rk) {
+        set_error("KV-cache handle is not resident in this context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    const uint64_t bytes = rk->c.bytes;
+    ctx->caches.erase(std::find(ctx->caches.begin(), ctx->caches.end(), rk));
+    free_cache(rk);
+    ctx->resident -= std::min(ctx->resident, bytes);
+    ctx->telemetry.kv_cache_resident_bytes -= std::min(ctx->telemetry.kv_cache_resident_bytes, bytes);
+    h->opaque = nullptr;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_append(QwnCudaContextHandle *handle,
+                                                  const QwnCudaKvAppendRequest *r,
+                                                  QwnCudaTelemetry *telemetry) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !r || !header_ok(*r) || !r->host_key || !r->host_value) {
+        set_error("invalid Q8 KV-cache append request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, r->cache);
+    if (!rk || r->n_channels != rk->c.channels || r->token != rk->c.tokens || r->token >= rk->c.max_tokens) {
+        set_error("invalid Q8 KV-cache append request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    KvCache &c = rk->c;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+    const size_t bytes = static_cast<size_t>(c.channels) * sizeof(float);
+    if ((e = ctx->host_in.ensure(2 * bytes)) != hipSuccess || (e = ctx->dev_in.ensure(2 * bytes)) != hipSuccess)
+        return hip_fail("KV workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+    const auto t0 = std::chrono::steady_clock::now();
+    uint8_t *hin = static_cast<uint8_t *>(ctx->host_in.ptr);
+    std::memcpy(hin, r->host_key, bytes);
+    std::memcpy(hin + bytes, r->host_value, bytes);
+    const float *dk = static_cast<const float *>(ctx->dev_in.ptr);
+    const float *dv = reinterpret_cast<const float *>(static_cast<uint8_t *>(ctx->dev_in.ptr) + bytes);
+    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, 2 * bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+        return hip_fail("Q8 KV upload", e);
+    (void)hipEventRecord(ctx->ev_start, ctx->stream);
+    if ((e = qwn::launch_kv_append(c, dk, dv, c.tokens, ctx->stream)) != hipSuccess)
+        return hip_fail("Q8 KV quantize launch", e);
+    (void)hipEventRecord(ctx->ev_end, ctx->stream);
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail("Q8 KV quantize", e);
+    float kms = 0.0f;
+    if (hipEventElapsedTime(&kms, ctx->ev_start, ctx->ev_end) != hipSuccess) kms = 0.0f;
+    c.tokens++;
+    QwnCudaTelemetry &tm = ctx->telemetry;
+    tm.kv_cache_kernel_count += 2;  // one quantization each for K and V (one fused launch)
+    tm.kv_cache_upload_bytes += 2 * bytes;
+    tm.kv_cache_kernel_ms += kms;
+    tm.kv_cache_transfer_ms += ms_since(t0) - kms;
+    std::snprintf(tm.kv_cache_kernel_type, sizeof(tm.kv_cache_kernel_type), "q8-paged-gfx950");
+    copy_telemetry(ctx, telemetry);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *handle,
+                                                     const QwnCudaKvAttentionRequest *r,
+                                                     QwnCudaTelemetry *telemetry) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !r || !header_ok(*r) || !r->host_query || !r->host_output || r->query_heads == 0) {
+        set_error("invalid Q8 KV-cache attention request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, r->cache);
+    if (!rk || r->kv_heads != rk->c.kv_heads || r->head_dim != rk->c.head_dim || r->position >= rk->c.tokens ||
+        r->query_heads % r->kv_heads != 0) {
+        set_error("invalid Q8 KV-cache attention request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const KvCache &c = rk->c;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail("hipSetDevice", e);
+    const size_t qbytes = static_cast<size_t>(r->query_heads) * c.head_dim * sizeof(float);
+    const size_t work = qwn::attention_workspace_floats(c, r->query_heads, r->position) * sizeof(float);
+    if ((e = ctx->host_in.ensure(qbytes)) != hipSuccess || (e = ctx->host_out.ensure(qbytes)) != hipSuccess ||
+        (e = ctx->dev_in.ensure(qbytes)) != hipSuccess || (e = ctx->dev_out.ensure(qbytes)) != hipSuccess ||
+        (e = ctx->dev_work.ensure(work)) != hipSuccess)
+        return hip_fail("attention workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+    const auto t0 = std::chrono::steady_clock::now();
+    std::memcpy(ctx->host_in.ptr, r->host_query, qbytes);
+    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, ctx->host_in.ptr, qbytes, hipMemcpyHostToDevice, ctx->stream)) !=
+        hipSuccess)
+        return hip_fail("Q8 KV query upload", e);
+    qwn::AttentionLaunch a{};
+    a.cache = &c;
+    a.query = static_cast<const float *>(ctx->dev_in.ptr);
+    a.output = static_cast<float *>(ctx->dev_out.ptr);
+    a.query_heads = r->query_heads;
+    a.position = r->position;
+    a.scale = r->scale;
+    a.partials = static_cast<float *>(ctx->dev_work.ptr);
+    (void)hipEventRecord(ctx->ev_start, ctx->stream);
+    if ((e = qwn::launch_attention(a, ctx->stream)) != hipSuccess) return hip_fail("Q8 KV attention launch", e);
+    (void)hipEventRecord(ctx->ev_end, ctx->stream);
+    if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, qbytes, hipMemcpyDeviceToHost, ctx->stream)) !=
+            hipSuccess ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
+        return hip_fail("Q8 KV attention", e);
+    std::memcpy(r->host_output, ctx->host_out.ptr, qbytes);
+    float kms = 0.0f;
+    if (hipEventElapsedTime(&kms, ctx->ev_start, ctx->ev_end) != hipSuccess) kms = 0.0f;
+    QwnCudaTelemetry &tm = ctx->telemetry;
+    tm.kv_cache_kernel_count++;
+    tm.kv_cache_kernel_ms += kms;
+    tm.kv_cache_transfer_ms += ms_since(t0) - kms;
+    std::snprintf(tm.kv_cache_kernel_type, sizeof(tm.kv_cache_kernel_type), "q8-paged-gfx950");
+    copy_telemetry(ctx, telemetry);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_reset(QwnCudaContextHandle *handle, QwnCudaKvCacheHandle *h) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h) {
+        set_error("invalid KV-cache reset request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, *h);
+    if (!rk) {
+        set_error("KV-cache handle is not resident in this context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    rk->c.tokens = 0;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_hypervsq2_gemv(QwnCudaContextHandle *handle, const QwnCudaGemmRequest *r,
+                                                 QwnCudaTelemetry *telemetry) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !r || r->batch != 1) {
+        set_error("hypervsq2_gemv needs a context and batch == 1");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return execute_gemm(ctx, r, telemetry);
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_hypervsq2_gemm(QwnCudaContextHandle *handle, const QwnCudaGemmRequest *r,
+                                                 QwnCudaTelemetry *telemetry) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return execute_gemm(ctx, r, telemetry);
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_synchronize(QwnCudaContextHandle *handle) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("stream synchronize", e);
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_get_telemetry(QwnCudaContextHandle *handle, QwnCudaTelemetry *telemetry) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !telemetry || !header_ok(*telemetry)) {
+        set_error("invalid telemetry request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    *telemetry = ctx->telemetry;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_last_error(char *buffer, uint32_t size) {
+    if (!buffer || size == 0) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lock(g_error_mutex);
+    std::snprintf(buffer, size, "%s", g_last_error.c_str());
+    return QWN_CUDA_STATUS_OK;
+}
+
+// ---- extensions (qwn_hip_ext.h) --------------------------------------------
+
+QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHipTensorInfo *info) {
+    if (!h || !header_ok(*h) || !h->opaque || !info || !header_ok(*info)) {
+        set_error("invalid tensor info request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const DeviceTensor &t = static_cast<const ResidentTensor *>(h->opaque)->t;
+    std::memset(info, 0, sizeof(*info));
+    qwn_cuda_abi_header_init(&info->header, sizeof(*info));
+    info->dtype = t.kind == qwn::kHvsq2 ? QWN_CUDA_TENSOR_HYPERVSQ2_74
+                                        : (t.kind == qwn::kQ4_0 ? QWN_CUDA_TENSOR_Q4_0_18 : QWN_CUDA_TENSOR_F16);
+    info->rows = t.rows;
+    info->cols = t.cols;
+    info->units_per_row = t.units;
+    info->logical_bytes = t.logical_bytes;
+    info->device_bytes = t.device_bytes;
+    const qwn::GemvPlan p = qwn::plan_gemv(t, 1);
+    info->lanes_per_row = p.lanes;
+    info->units_per_lane = p.upl;
+    info->rows_per_wave = p.rows_per_wave;
+    info->grid = p.grid;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_device(QwnCudaContextHandle *handle, const QwnCudaGemmRequest *r,
+                                             void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = check_request(ctx, r);
+    if (!rt) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    const size_t elem = rt->t.kind == qwn::kF16 ? 4 : 1;
+    const uint32_t in_stride = r->input_stride ? r->input_stride : r->cols;
+    if ((reinterpret_cast<uintptr_t>(r->input_q8) & 15u) || ((in_stride * elem) & 15u)) {
+        set_error("device activations must be 16-byte aligned (pointer and row stride)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    qwn::GemvLaunch g{};
+    g.tensor = &rt->t;
+    g.input = r->input_q8;
+    g.scales = r->input_scales;
+    g.scale = r->input_scale;
+    g.output = r->output;
+    g.batch = r->batch;
+    g.input_stride = in_stride;
+    g.output_stride = r->output_stride ? r->output_stride : r->rows;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_gemv(g, s);
+    if (e != hipSuccess) return hip_fail("device GEMV launch", e);
+    ctx->telemetry.gpu_matmul_count++;
+    ctx->telemetry.gpu_kernel_launch_count++;
+    ctx->telemetry.gpu_projection_count++;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *handle, const float *x, uint32_t batch,
+                                                 uint32_t cols, uint32_t x_stride, int8_t *q8,
+                                                 uint32_t q8_stride, float *scales, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !x || !q8 || !scales || batch == 0 || cols == 0 || x_stride < cols || q8_stride < cols) {
+        set_error("invalid device quantize request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_quantize_tokens(x, static_cast<int>(batch), static_cast<int>(cols),
+                                               static_cast<int>(x_stride), q8, static_cast<int>(q8_stride),
+                                               scales, s);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("quantize launch", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_kv_append_device(QwnCudaContextHandle *handle, QwnCudaKvCacheHandle *h,
+                                                  const float *keys, const float *values, uint32_t count,
+                                                  void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h || !keys || !values || count == 0) {
+        set_error("invalid device KV append request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, *h);
+    if (!rk || rk->c.tokens + count > rk->c.max_tokens) {
+        set_error("device KV append exceeds the cache");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    KvCache &c = rk->c;
+    for (uint32_t i = 0; i < count; ++i) {
+        hipError_t e = qwn::launch_kv_append(c, keys + static_cast<size_t>(i) * c.channels,
+                                             values + static_cast<size_t>(i) * c.channels, c.tokens, s);
+        if (e != hipSuccess) return hip_fail("device KV append launch", e);
+        c.tokens++;
+        ctx->telemetry.kv_cache_kernel_count += 2;
+    }
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API uint64_t qwn_hip_ext_attention_workspace_bytes(QwnCudaKvCacheHandle *h, uint32_t query_heads,
+                                                                 uint32_t position) {
+    if (!h || !header_ok(*h) || !h->opaque) return 0;
+    const KvCache &c = static_cast<ResidentKv *>(h->opaque)->c;
+    return qwn::attention_workspace_floats(c, query_heads, position) * sizeof(float);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device(QwnCudaContextHandle *handle, QwnCudaKvCacheHandle *h,
+                                                     const float *query, float *output, uint32_t query_heads,
+                                                     uint32_t position, float scale, void *workspace,
+                                                     void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h || !query || !output || !workspace || query_heads == 0) {
+        set_error("invalid device attention request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, *h);
+    if (!rk || position >= rk->c.tokens || query_heads % rk->c.kv_heads != 0) {
+        set_error("invalid device attention request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    qwn::AttentionLaunch a{};
+    a.cache = &rk->c;
+    a.query = query;
+    a.output = output;
+    a.query_heads = query_heads;
+    a.position = position;
+    a.scale = scale;
+    a.partials = static_cast<float *>(workspace);
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_attention(a, s);
+    if (e != hipSuccess) return hip_fail("device attention launch", e);
+    ctx->telemetry.kv_cache_kernel_count++;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_debug_int_sums(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                const int8_t *host_q8, int32_t *host_out,
+                                                uint64_t out_capacity) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !th || !host_q8 || !host_out) {
+        set_error("invalid debug request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = tensor_of(ctx, *th);
+    if (!rt || rt->t.kind == qwn::kF16) {
+        set_error("debug sums need a resident HyperVSQ-2 or Q4_0 tensor");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const DeviceTensor &t = rt->t;
+    const uint64_t per_row = t.kind == qwn::kHvsq2 ? t.units * 8ull : (t.cols + 31ull) / 32ull;
+    const uint64_t n = per_row * t.rows;
+    if (out_capacity < n) {
+        set_error("debug output needs %llu int32 values", static_cast<unsigned long long>(n));
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipError_t e = hipSetDevice(ctx->device);
+    const uint32_t stride = (t.cols + 255u) & ~255u;
+    void *dx = nullptr, *dout = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&dx, stride);
+    if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMemsetAsync(dx, 0, stride, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, host_q8, t.cols, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) {
+        qwn::GemvLaunch g{};
+        g.tensor = &t;
+        g.input = dx;
+        g.batch = 1;
+        g.input_stride = stride;
+        g.debug_sums = static_cast<int32_t *>(dout);
+        e = qwn::launch_gemv(g, ctx->stream);
+    }
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(host_out, dout, n * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (dx) (void)hipFree(dx);
+    if (dout) (void)hipFree(dout);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("debug integer sums", e);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+"""Seeded synthetic inputs for the quantized decode path.
+
+Byte layouts follow the reference writers: Q4_0 blocks are
+``[fp16 d][16 bytes of nibbles, element 2j = low nibble of byte j]``
+(c/qwanto_native.h:35, c/tools/qwn_convert.py:65-110) and HyperVSQ-2 blocks
+are ``[fp16 d_base][fp16 m_base][4 bytes of octant multipliers][2 reserved]
+[64 bytes of 2-bit codes]`` (c/qwanto_native.h:96-103,
+c/tools/qwn_convert.py:365-469).  Values are random rather than quantized
+from real weights; the distributions are the ones the benchmark
+configurations name:
+
+* Q4_0: ``d = fp16(|N(0, 0.02)|)``, uniform random nibble bytes.
+* HyperVSQ-2: ``d_base = fp16(|N(0, 0.02)|)``, ``m_base = fp16(N(0, 0.02))``,
+  octant multipliers uniform in 1..8 (the converter's range,
+  c/tools/qwn_convert.py:397), random reserved bytes (they must be ignored),
+  uniform random code bytes.
+* activations ``x ~ N(0, 1)`` in fp32; fp16 tensors ``N(0, 0.02)``.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4_0_BLOCK_BYTES = 18
+Q4_0_BLOCK_ELEMS = 32
+HVSQ2_BLOCK_BYTES = 74
+HVSQ2_BLOCK_ELEMS = 256
+
+# Qwen2-1.5B projection shapes (rows N x cols K)
+QWEN2_1P5B_SHAPES = {
+    "q": (1536, 1536), "k": (256, 1536), "v": (256, 1536), "o": (1536, 1536),
+    "gate": (8960, 1536), "up": (8960, 1536), "down": (1536, 8960),
+}
+# Qwen3-4B projection shapes (rows N x cols K)
+QWEN3_4B_SHAPES = {
+    "q": (4096, 2560), "k": (1024, 2560), "v": (1024, 2560), "o": (2560, 4096),
+    "gate": (9728, 2560), "up": (9728, 2560), "down": (2560, 9728),
+}
+PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def q4_0_row_bytes(cols: int) -> int:
+    return (cols + 31) // 32 * Q4_0_BLOCK_BYTES
+
+
+def hvsq2_row_bytes(cols: int) -> int:
+    return (cols + 255) // 256 * HVSQ2_BLOCK_BYTES
+
+
+def _half_bytes(values: np.ndarray) -> np.ndarray:
+    return values.astype(np.float16).view(np.uint8).reshape(values.shape + (2,))
+
+
+def q4_0_weights(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """Row-major Q4_0 matrix as a flat uint8 array."""
+    blocks = rows * ((cols + 31) // 32)
+    out = np.empty((blocks, Q4_0_BLOCK_BYTES), dtype=np.uint8)
+    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, 0.02, blocks)).astype(np.float32))
+    out[:, 2:] = rng.integers(0, 256, (blocks, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def hvsq2_weights(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """Row-major HyperVSQ-2 matrix as a flat uint8 array."""
+    blocks = rows * ((cols + 255) // 256)
+    out = np.empty((blocks, HVSQ2_BLOCK_BYTES), dtype=np.uint8)
+    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, 0.02, blocks)).astype(np.float32))
+    out[:, 2:4] = _half_bytes(rng.normal(0.0, 0.02, blocks).astype(np.float32))
+    sub = rng.integers(1, 9, (blocks, 8), dtype=np.uint8)
+    out[:, 4:8] = sub[:, 0::2] | (sub[:, 1::2] << 4)
+    out[:, 8:10] = rng.integers(0, 256, (blocks, 2), dtype=np.uint8)
+    out[:, 10:] = rng.integers(0, 256, (blocks, 64), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def f16_weights(rng: np.random.Generator, rows: int, cols: int,
+                std: float = 0.02) -> np.ndarray:
+    return rng.normal(0.0, std, (rows, cols)).astype(np.float16)
+
+
+def activations(rng: np.random.Generator, batch: int, cols: int) -> np.ndarray:
+    return rng.standard_normal((batch, cols), dtype=np.float32)
+
+
+def weights(dtype: str, rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    if dtype == "q4_0":
+        return q4_0_weights(rng, rows, cols)
+    if dtype == "hvsq2":
+        return hvsq2_weights(rng, rows, cols)
+    raise ValueError(f"unknown weight dtype {dtype!r}")
+
+
+def weight_bytes(dtype: str, rows: int, cols: int) -> int:
+    """Algorithmic (on-disk) bytes of one matrix."""
+    if dtype == "q4_0":
+        return rows * q4_0_row_bytes(cols)
+    if dtype == "hvsq2":
+        return rows * hvsq2_row_bytes(cols)
+    if dtype == "f16":
+        return rows * cols * 2
+    raise ValueError(dtype)
