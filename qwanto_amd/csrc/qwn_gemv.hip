@@ -1,11 +1,23 @@
 // Quantized GEMV / small-batch GEMM kernels for gfx950 (CDNA4).
 //
 // Decode at batch 1 reads every weight exactly once, so the kernel is an
-// HBM stream: each lane loads whole 64-byte units with 128-bit loads (all
-// of its loads issued before it touches the activations), the int8
-// activations are staged once per workgroup in LDS in the byte order the
-// unpack produces, the 2-/4-bit codes are widened with shift+mask and fed
-// to v_dot4_i32_i8, and per-row partial sums are combined through LDS.
+// HBM stream.  Each wave owns a tile of rows stored contiguously in the
+// order its lanes load it (qwn_internal.h), so every 128-bit load
+// instruction of the wave reads one contiguous span.  The int8 activations
+// are staged once per workgroup in LDS, already split for the dot product
+// (below), and per-row partial sums are combined with wave shuffles.
+//
+// Integer core.  An int8 activation is written a = 16*h + l with h = a >> 4
+// in [-8, 7] (signed nibble) and l = a & 15 in [0, 15] (unsigned nibble), so
+//   sum c*a = 16 * sdot8(c, h) + udot8(c, l)          (v_dot8_i32_i4 / v_dot8_u32_u4)
+// exactly, for any 4-bit weight field c.
+//   HyperVSQ-2: a code dword holds weights 4j+i at bits 8j+2i; masking with
+//     0x33333333 leaves weights {0,2,..,14} in nibbles 0..7 and
+//     (w >> 2) & 0x33333333 the odd ones, so two masks feed four dot8s
+//     (16 weights).  sum (c-1)*a = that - sum a.
+//   Q4_0: the nibble dword already holds weights 0..7 in nibbles 0..7;
+//     (n - 8) is n ^ 8 as a signed nibble, and
+//     sum (n-8)*a = 16*sdot8(n^0x88888888, h) + udot8(n, l) - 8*sum l.
 //
 // Semantics follow the reference CPU kernels:
 //   HyperVSQ-2  y = xs * sum_blocks (d/8 * sum_oct s_oct*(sum code*a - sum a)
@@ -22,8 +34,8 @@
 namespace qwn {
 namespace {
 
-constexpr uint32_t kMask2 = 0x03030303u;
-constexpr uint32_t kMask4 = 0x0f0f0f0fu;
+constexpr uint32_t kMask33 = 0x33333333u;
+constexpr uint32_t kFlip8 = 0x88888888u;
 
 __device__ __forceinline__ float half_to_float(uint32_t bits) {
     // v_cvt_f32_f16 keeps fp16 subnormals (the default f16 denormal mode),
@@ -31,78 +43,113 @@ __device__ __forceinline__ float half_to_float(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
-__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+__device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot8(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+__device__ __forceinline__ int udot8(uint32_t a, uint32_t b, int c) {
+    return static_cast<int>(__builtin_amdgcn_udot8(a, b, static_cast<uint32_t>(c), false));
+}
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+// ---- activation staging ----------------------------------------------------
 
-// ---- activation staging ------------------------------------------------
-//
-// HyperVSQ-2: a code dword holds 16 consecutive weights, weight 4j+i in
-// bits 2i of byte j, so (w >> 2i) & 0x03030303 holds weights {i, 4+i, 8+i,
-// 12+i}.  Each 16-activation group is stored transposed to match:
-// dword i = bytes {a_i, a_{4+i}, a_{8+i}, a_{12+i}}.
-// Q4_0: a nibble dword holds 8 weights, low nibbles = even elements, so
-// each 8-activation group is stored as {a0,a2,a4,a6},{a1,a3,a5,a7}.
+// Nibble-pack 8 int8 values (two dwords, element order) into the high
+// (signed, a >> 4) and low (a & 15) nibble words, nibble k = element k.
+__device__ __forceinline__ void split8(uint32_t a, uint32_t b, uint32_t &hi, uint32_t &lo) {
+    hi = lo = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t byte = ((k < 4 ? a : b) >> (8 * (k & 3))) & 0xffu;
+        hi |= ((byte >> 4) & 0xfu) << (4 * k);  // arithmetic >> 4 of the int8, as a nibble
+        lo |= (byte & 0xfu) << (4 * k);
+    }
+}
 
-template <int KIND>
-__device__ __forceinline__ void store_block32(uint8_t *act_token, uint32_t e0,
-                                              const uint32_t w[8]) {
-    if (KIND == kHvsq2) {
-        const uint32_t u = e0 / 256, off = e0 % 256;
+// Even/odd split of 16 int8 values for the HyperVSQ-2 masks: returns the
+// high/low nibble words of elements {0,2,..,14} and {1,3,..,15}.
+__device__ __forceinline__ uint4 split16_evenodd(const uint32_t w[4]) {
+    uint32_t he = 0, le = 0, ho = 0, lo = 0;
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            uint32_t p[4];
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t ev = (w[k >> 1] >> (16 * (k & 1))) & 0xffu;        // element 2k
+        const uint32_t od = (w[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;    // element 2k+1
+        he |= ((ev >> 4) & 0xfu) << (4 * k);
+        le |= (ev & 0xfu) << (4 * k);
+        ho |= ((od >> 4) & 0xfu) << (4 * k);
+        lo |= (od & 0xfu) << (4 * k);
+    }
+    return make_uint4(he, le, ho, lo);
+}
+
+// Staging of `ntok` int8 tokens (row stride `stride` bytes, 16-byte
+// aligned) of K valid activations, zero padded to units*unit_elems, one
+// 32-element block per thread and step.  Per block it also stores the
+// correction term: sum a (HyperVSQ-2) or 8 * sum l (Q4_0).  The load half
+// is separate so a kernel can issue a thread's first block before its
+// weight loads (vmcnt waits are in issue order).
+__device__ __forceinline__ void load_block32(const int8_t *__restrict__ x, uint32_t stride, uint32_t K,
+                                             uint32_t ntok, uint32_t t, uint32_t e0, uint32_t w[8]) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                p[i] = byte_of(w[4 * g + 0], i) | (byte_of(w[4 * g + 1], i) << 8) |
-                       (byte_of(w[4 * g + 2], i) << 16) | (byte_of(w[4 * g + 3], i) << 24);
-            *reinterpret_cast<uint4 *>(act_token + u * 272 + (off / 16 + g) * 16) =
-                make_uint4(p[0], p[1], p[2], p[3]);
-        }
-    } else {
-        const uint32_t u = e0 / 128, off = e0 % 128;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const uint32_t a = w[2 * g], b = w[2 * g + 1];
-            const uint32_t lo = byte_of(a, 0) | (byte_of(a, 2) << 8) | (byte_of(b, 0) << 16) |
-                                (byte_of(b, 2) << 24);
-            const uint32_t hi = byte_of(a, 1) | (byte_of(a, 3) << 8) | (byte_of(b, 1) << 16) |
-                                (byte_of(b, 3) << 24);
-            *reinterpret_cast<uint2 *>(act_token + u * 144 + (off / 8 + g) * 8) = make_uint2(lo, hi);
+    for (int i = 0; i < 8; ++i) w[i] = 0;
+    if (t < ntok && e0 < K) {
+        const int8_t *src = x + static_cast<size_t>(t) * stride + e0;
+        if (e0 + 32 <= K) {
+            const uint4 v0 = *reinterpret_cast<const uint4 *>(src);
+            const uint4 v1 = *reinterpret_cast<const uint4 *>(src + 16);
+            w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+            w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+        } else {
+            for (uint32_t i = 0; i < K - e0; ++i)
+                w[i >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(src[i]))) << (8 * (i & 3));
         }
     }
 }
 
-// Stage `ntok` int8 tokens (row stride `stride` bytes, 16-byte aligned) of
-// K valid activations, zero padded to units*unit_elems, plus the sum of
-// every 32-activation block.
+template <int KIND>
+__device__ __forceinline__ void store_block32(uint8_t *tok, int32_t *sum, uint32_t e0, const uint32_t w[8]) {
+    if (KIND == kHvsq2) {
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4(w[i], 0x01010101u, s);
+        *sum = s;
+        const uint32_t u = e0 / 256, off = e0 % 256;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+            *reinterpret_cast<uint4 *>(tok + u * 272 + (off / 16 + g) * 16) = split16_evenodd(w + 4 * g);
+    } else {
+        const uint32_t u = e0 / 128, off = e0 % 128;
+        int lsum = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t hi, lo;
+            split8(w[2 * g], w[2 * g + 1], hi, lo);
+            lsum = static_cast<int>(__builtin_amdgcn_udot8(lo, 0x11111111u, static_cast<uint32_t>(lsum), false));
+            *reinterpret_cast<uint2 *>(tok + u * 144 + (off / 8 + g) * 8) = make_uint2(hi, lo);
+        }
+        *sum = 8 * lsum;
+    }
+}
+
+// Stage every block; `first` holds the already loaded block of index
+// threadIdx.x (when that index is in range).
 template <int KIND, int MT>
 __device__ void stage_int8(const int8_t *__restrict__ x, uint32_t stride, uint32_t K,
-                           uint32_t units, uint32_t ntok, uint8_t *act, int32_t *sums) {
+                           uint32_t units, uint32_t ntok, uint8_t *act, int32_t *sums,
+                           const uint32_t first[8]) {
     const uint32_t nblk = units * unit_elems(KIND) / 32;
     const uint32_t token_bytes = units * unit_lds_bytes(KIND);
     for (uint32_t idx = threadIdx.x; idx < MT * nblk; idx += blockDim.x) {
         const uint32_t t = idx / nblk, b = idx % nblk, e0 = b * 32;
-        uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (t < ntok && e0 < K) {
-            const int8_t *src = x + static_cast<size_t>(t) * stride + e0;
-            if (e0 + 32 <= K) {
-                const uint4 v0 = *reinterpret_cast<const uint4 *>(src);
-                const uint4 v1 = *reinterpret_cast<const uint4 *>(src + 16);
-                w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
-                w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
-            } else {
-                for (uint32_t i = 0; i < K - e0; ++i)
-                    w[i >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(src[i]))) << (8 * (i & 3));
-            }
-        }
-        int s = 0;
+        uint32_t w[8];
+        if (idx == threadIdx.x) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s = dot4(w[i], 0x01010101u, s);
-        sums[t * nblk + b] = s;
-        store_block32<KIND>(act + t * token_bytes, e0, w);
+            for (int i = 0; i < 8; ++i) w[i] = first[i];
+        } else {
+            load_block32(x, stride, K, ntok, t, e0, w);
+        }
+        store_block32<KIND>(act + t * token_bytes, sums + t * nblk + b, e0, w);
     }
 }
 
@@ -133,38 +180,41 @@ __device__ void stage_f32(const float *__restrict__ x, uint32_t stride, uint32_t
 
 // ---- per-unit integer cores (shared by the GEMV and the dump kernel) ----
 
-// sum over one octant of code*a (codes 0..3), octant = two code dwords.
+// sum over one octant of code*a: w0/w1 = the octant's code dwords, a0/a1 =
+// staged activations of its two 16-element groups.
 __device__ __forceinline__ int hv_octant_dot(uint32_t w0, uint32_t w1, uint4 a0, uint4 a1) {
-    int d = dot4(w0 & kMask2, a0.x, 0);
-    d = dot4((w0 >> 2) & kMask2, a0.y, d);
-    d = dot4((w0 >> 4) & kMask2, a0.z, d);
-    d = dot4((w0 >> 6) & kMask2, a0.w, d);
-    d = dot4(w1 & kMask2, a1.x, d);
-    d = dot4((w1 >> 2) & kMask2, a1.y, d);
-    d = dot4((w1 >> 4) & kMask2, a1.z, d);
-    d = dot4((w1 >> 6) & kMask2, a1.w, d);
-    return d;
+    const uint32_t e0 = w0 & kMask33, o0 = (w0 >> 2) & kMask33;
+    const uint32_t e1 = w1 & kMask33, o1 = (w1 >> 2) & kMask33;
+    int hi = sdot8(e0, a0.x, 0);
+    hi = sdot8(o0, a0.z, hi);
+    hi = sdot8(e1, a1.x, hi);
+    hi = sdot8(o1, a1.z, hi);
+    int lo = udot8(e0, a0.y, 0);
+    lo = udot8(o0, a0.w, lo);
+    lo = udot8(e1, a1.y, lo);
+    lo = udot8(o1, a1.w, lo);
+    return hi * 16 + lo;
 }
 
-// sum over one Q4_0 block of nibble*a; a0/a1 hold the staged activations
-// of nibble dwords (0,1) and (2,3).
+// sum over one Q4_0 block of (nibble-8)*a + 8*sum l, i.e. before the
+// staged correction; a0 = (h,l) of nibble dwords 0,1, a1 = of dwords 2,3.
 __device__ __forceinline__ int q4_block_dot(uint4 n, uint4 a0, uint4 a1) {
-    int d = dot4(n.x & kMask4, a0.x, 0);
-    d = dot4((n.x >> 4) & kMask4, a0.y, d);
-    d = dot4(n.y & kMask4, a0.z, d);
-    d = dot4((n.y >> 4) & kMask4, a0.w, d);
-    d = dot4(n.z & kMask4, a1.x, d);
-    d = dot4((n.z >> 4) & kMask4, a1.y, d);
-    d = dot4(n.w & kMask4, a1.z, d);
-    d = dot4((n.w >> 4) & kMask4, a1.w, d);
-    return d;
+    int hi = sdot8(n.x ^ kFlip8, a0.x, 0);
+    hi = sdot8(n.y ^ kFlip8, a0.z, hi);
+    hi = sdot8(n.z ^ kFlip8, a1.x, hi);
+    hi = sdot8(n.w ^ kFlip8, a1.z, hi);
+    int lo = udot8(n.x, a0.y, 0);
+    lo = udot8(n.y, a0.w, lo);
+    lo = udot8(n.z, a1.y, lo);
+    lo = udot8(n.w, a1.w, lo);
+    return hi * 16 + lo;
 }
 
 struct GemvArgs {
     const uint8_t *payload;
     const uint8_t *meta;
-    size_t payload_row_bytes;
-    size_t meta_row_bytes;
+    size_t tile_payload_bytes;
+    size_t tile_meta_bytes;
     const void *input;
     const float *scales;
     float scale;
@@ -174,6 +224,7 @@ struct GemvArgs {
     uint32_t units;
     uint32_t lanes;
     uint32_t rows_per_wave;
+    uint32_t slots;
     uint32_t ntok;
     uint32_t input_stride;
     uint32_t output_stride;
@@ -182,38 +233,51 @@ struct GemvArgs {
 template <int KIND, int MT, int UPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int CH = KIND == kF16 ? 1 : 4;
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = threadIdx.x / kWaveSize;
     const uint32_t L = a.lanes;
     const uint32_t grp = lane / L;
     const uint32_t j = lane - grp * L;
-    const uint32_t row = (blockIdx.x * kGemvWaves + wave) * a.rows_per_wave + grp;
+    const uint32_t tile = blockIdx.x * kGemvWaves + wave;
+    const uint32_t row = tile * a.rows_per_wave + grp;
     const bool active = grp < a.rows_per_wave && row < a.rows;
 
-    // 1. Issue every weight load of this lane before anything else.
-    uint4 pay[UPL][KIND == kF16 ? 1 : 4];
+    // 0. This thread's first activation block (int8 kinds), issued before
+    //    the weights so that waiting for it does not wait for them.
+    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
+    uint32_t first[8];
+    if (KIND != kF16)
+        load_block32(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, a.ntok,
+                     threadIdx.x / nblk, (threadIdx.x % nblk) * 32, first);
+
+    // 1. Issue every weight load of this lane, metadata before codes
+    //    (the first octant needs its scales).  Lanes without a unit load
+    //    from the tile start instead of branching around the load, so the
+    //    loads stay one unconditional burst.
+    const uint8_t *tile_p = a.payload + tile * a.tile_payload_bytes;
+    const uint8_t *tile_m = a.meta + tile * a.tile_meta_bytes;
+    const uint8_t *tp = tile_p + lane * 16;
+    const uint8_t *tm = tile_m + lane * 8;
     uint2 met[UPL];
+    uint4 pay[UPL][CH];
 #pragma unroll
     for (int i = 0; i < UPL; ++i) {
-        const uint32_t u = j + i * L;
-        const bool ok = active && u < a.units;
-        if (KIND == kF16) {
-            pay[i][0] = ok ? *reinterpret_cast<const uint4 *>(
-                                 a.payload + row * a.payload_row_bytes + u * 16)
-                           : make_uint4(0, 0, 0, 0);
-        } else {
-            const uint4 *src = reinterpret_cast<const uint4 *>(
-                a.payload + row * a.payload_row_bytes + static_cast<size_t>(u) * 64);
+        const bool ok = active && j + i * L < a.units;
+        if (KIND != kF16)
+            met[i] = *reinterpret_cast<const uint2 *>(
+                ok ? tm + static_cast<size_t>(i) * a.slots * 8 : tile_m);
+    }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) pay[i][q] = ok ? src[q] : make_uint4(0, 0, 0, 0);
-            met[i] = ok ? *reinterpret_cast<const uint2 *>(a.meta + row * a.meta_row_bytes +
-                                                           static_cast<size_t>(u) * 8)
-                        : make_uint2(0, 0);
-        }
+    for (int i = 0; i < UPL; ++i) {
+        const bool ok = active && j + i * L < a.units;
+#pragma unroll
+        for (int q = 0; q < CH; ++q)
+            pay[i][q] = *reinterpret_cast<const uint4 *>(
+                ok ? tp + static_cast<size_t>(i * CH + q) * a.slots * 16 : tile_p);
     }
 
     // 2. Stage the activations of all tokens in LDS.
-    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
     uint8_t *act = smem;
     int32_t *sums = reinterpret_cast<int32_t *>(smem + MT * a.units * unit_lds_bytes(KIND));
     float *red = reinterpret_cast<float *>(
@@ -223,7 +287,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
                       a.ntok, reinterpret_cast<float *>(act));
     else
         stage_int8<KIND, MT>(static_cast<const int8_t *>(a.input), a.input_stride, a.cols,
-                             a.units, a.ntok, act, sums);
+                             a.units, a.ntok, act, sums, first);
     __syncthreads();
 
     // 3. Dot products.
@@ -243,16 +307,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) s1[t] = sa[t] = 0;
 #pragma unroll
-            for (int o = 0; o < 8; ++o) {
-                const int s = static_cast<int>((subs >> (4 * o)) & 15u);
+            for (int t = 0; t < MT; ++t) {
+                // all 16 activation groups and 8 octant sums of this unit at once
+                const uint4 *at = reinterpret_cast<const uint4 *>(act + (t * a.units + u) * 272);
+                uint4 av[16];
 #pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const uint8_t *at = act + (t * a.units + u) * 272 + o * 32;
-                    const uint4 a0 = *reinterpret_cast<const uint4 *>(at);
-                    const uint4 a1 = *reinterpret_cast<const uint4 *>(at + 16);
-                    const int so = sums[t * nblk + u * 8 + o];
-                    s1[t] += s * (hv_octant_dot(cw[2 * o], cw[2 * o + 1], a0, a1) - so);
-                    sa[t] += so;
+                for (int g = 0; g < 16; ++g) av[g] = at[g];
+                const int4 *sp = reinterpret_cast<const int4 *>(sums + t * nblk + u * 8);
+                const int4 sv0 = sp[0], sv1 = sp[1];
+                const int so[8] = {sv0.x, sv0.y, sv0.z, sv0.w, sv1.x, sv1.y, sv1.z, sv1.w};
+#pragma unroll
+                for (int o = 0; o < 8; ++o) {
+                    const int s = static_cast<int>((subs >> (4 * o)) & 15u);
+                    s1[t] += s * (hv_octant_dot(cw[2 * o], cw[2 * o + 1], av[2 * o], av[2 * o + 1]) - so[o]);
+                    sa[t] += so[o];
                 }
             }
 #pragma unroll
@@ -270,7 +338,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
                     const uint8_t *at = act + (t * a.units + u) * 144 + b * 32;
                     const uint4 a0 = *reinterpret_cast<const uint4 *>(at);
                     const uint4 a1 = *reinterpret_cast<const uint4 *>(at + 16);
-                    const int raw = q4_block_dot(pay[i][b], a0, a1) - 8 * sums[t * nblk + u * 4 + b];
+                    const int raw = q4_block_dot(pay[i][b], a0, a1) - sums[t * nblk + u * 4 + b];
                     acc[t] = fmaf(static_cast<float>(raw), d, acc[t]);
                 }
             }
@@ -297,20 +365,41 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
         }
     }
 
-    // 4. Combine the L partials of each row through LDS.
-    float *my = red + threadIdx.x * MT;
+    // 4. Combine the L partials of each row inside the wave (ds_bpermute,
+    //    no workgroup barrier).
+    float tot[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) my[t] = acc[t];
-    __syncthreads();
+    for (int t = 0; t < MT; ++t) {
+        float s = 0.0f;
+        for (uint32_t l = 0; l < L; ++l) s += __shfl(acc[t], static_cast<int>(grp * L + l));
+        tot[t] = s;
+    }
     if (active) {
-        const float *base = red + (wave * kWaveSize + grp * L) * MT;
-        for (uint32_t t = j; t < a.ntok && t < MT; t += L) {
-            float s = 0.0f;
-            for (uint32_t l = 0; l < L; ++l) s += base[l * MT + t];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (static_cast<uint32_t>(t) % L != j || static_cast<uint32_t>(t) >= a.ntok) continue;
+            float s = tot[t];
             if (KIND != kF16) s *= a.scales ? a.scales[t] : a.scale;
             a.output[static_cast<size_t>(t) * a.output_stride + row] = s;
         }
     }
+    (void)red;
+}
+
+// Byte address of chunk q of unit u of a row, and of its metadata.
+struct UnitAddr {
+    size_t payload, meta;
+};
+__host__ __device__ inline UnitAddr unit_addr(uint32_t row, uint32_t u, uint32_t q, uint32_t lanes,
+                                              uint32_t rows_per_wave, uint32_t slots, uint32_t chunks,
+                                              size_t tile_payload, size_t tile_meta) {
+    const uint32_t tile = row / rows_per_wave, grp = row % rows_per_wave;
+    const uint32_t i = u / lanes, jj = u % lanes;
+    const uint32_t slot = grp * lanes + jj;
+    UnitAddr r;
+    r.payload = tile * tile_payload + (static_cast<size_t>(i * chunks + q) * slots + slot) * 16;
+    r.meta = tile * tile_meta + (static_cast<size_t>(i) * slots + slot) * 8;
+    return r;
 }
 
 // Integer dump: one thread per (row, unit), token 0 only.  Same staging
@@ -321,18 +410,24 @@ template <int KIND>
 __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t *out,
                                                             uint32_t out_row) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
     uint8_t *act = smem;
     int32_t *sums = reinterpret_cast<int32_t *>(smem + a.units * unit_lds_bytes(KIND));
+    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
+    uint32_t first[8];
+    load_block32(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, 1, threadIdx.x / nblk,
+                 (threadIdx.x % nblk) * 32, first);
     stage_int8<KIND, 1>(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, a.units,
-                        1, act, sums);
+                        1, act, sums, first);
     __syncthreads();
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= a.rows * a.units) return;
     const uint32_t row = idx / a.units, u = idx % a.units;
-    const uint4 *src = reinterpret_cast<const uint4 *>(a.payload + row * a.payload_row_bytes +
-                                                       static_cast<size_t>(u) * 64);
-    uint4 pay[4] = {src[0], src[1], src[2], src[3]};
+    uint4 pay[4];
+    for (uint32_t q = 0; q < 4; ++q) {
+        const UnitAddr ad = unit_addr(row, u, q, a.lanes, a.rows_per_wave, a.slots, 4,
+                                      a.tile_payload_bytes, a.tile_meta_bytes);
+        pay[q] = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
+    }
     if (KIND == kHvsq2) {
         const uint32_t *cw = reinterpret_cast<const uint32_t *>(pay);
         for (int o = 0; o < 8; ++o) {
@@ -349,45 +444,71 @@ __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t 
             out[static_cast<size_t>(row) * out_row + u * 4 + b] =
                 q4_block_dot(pay[b], *reinterpret_cast<const uint4 *>(at),
                              *reinterpret_cast<const uint4 *>(at + 16)) -
-                8 * sums[u * 4 + b];
+                sums[u * 4 + b];
         }
     }
-    (void)nblk;
 }
 
-// ---- repack --------------------------------------------------------------
+// ---- repack: on-disk blocks -> wave-tile layout -----------------------------
+// One thread per (row, unit); the destination was zero filled.
 
-__global__ void repack_hvsq2(const uint8_t *__restrict__ src, uint8_t *codes, uint8_t *meta,
-                             uint32_t rows, uint32_t nb, size_t codes_row, size_t meta_row) {
-    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= static_cast<size_t>(rows) * nb) return;
-    const uint32_t r = idx / nb, b = idx % nb;
-    const uint8_t *blk = src + idx * 74;
-    uint8_t *dc = codes + r * codes_row + static_cast<size_t>(b) * 64;
-    for (int i = 0; i < 64; i += 4) {
-        const uint32_t v = blk[10 + i] | (blk[11 + i] << 8) | (blk[12 + i] << 16) |
-                           (static_cast<uint32_t>(blk[13 + i]) << 24);
-        *reinterpret_cast<uint32_t *>(dc + i) = v;
-    }
-    const uint32_t m0 = blk[0] | (blk[1] << 8) | (blk[2] << 16) | (static_cast<uint32_t>(blk[3]) << 24);
-    const uint32_t m1 = blk[4] | (blk[5] << 8) | (blk[6] << 16) | (static_cast<uint32_t>(blk[7]) << 24);
-    *reinterpret_cast<uint2 *>(meta + r * meta_row + static_cast<size_t>(b) * 8) = make_uint2(m0, m1);
+struct RepackArgs {
+    const uint8_t *src;
+    uint8_t *payload;
+    uint8_t *meta;
+    uint32_t rows, cols, units, lanes, rows_per_wave, slots;
+    size_t tile_payload, tile_meta;
+};
+
+__device__ inline uint32_t load_u32_unaligned(const uint8_t *p) {
+    return p[0] | (p[1] << 8) | (p[2] << 16) | (static_cast<uint32_t>(p[3]) << 24);
 }
 
-__global__ void repack_q4_0(const uint8_t *__restrict__ src, uint8_t *nibbles, uint8_t *scales,
-                            uint32_t rows, uint32_t nb, size_t nib_row, size_t scale_row) {
+template <int KIND>
+__global__ void repack_kernel(RepackArgs r) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= static_cast<size_t>(rows) * nb) return;
-    const uint32_t r = idx / nb, b = idx % nb;
-    const uint8_t *blk = src + idx * 18;
-    uint8_t *dn = nibbles + r * nib_row + static_cast<size_t>(b) * 16;
-    for (int i = 0; i < 16; i += 4) {
-        const uint32_t v = blk[2 + i] | (blk[3 + i] << 8) | (blk[4 + i] << 16) |
-                           (static_cast<uint32_t>(blk[5 + i]) << 24);
-        *reinterpret_cast<uint32_t *>(dn + i) = v;
+    if (idx >= static_cast<size_t>(r.rows) * r.units) return;
+    const uint32_t row = idx / r.units, u = idx % r.units;
+    const uint32_t chunks = KIND == kF16 ? 1 : 4;
+    UnitAddr ad[4];
+    for (uint32_t q = 0; q < chunks; ++q)
+        ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.slots, chunks, r.tile_payload, r.tile_meta);
+    if (KIND == kHvsq2) {
+        const uint8_t *blk = r.src + idx * 74;  // [row][unit] blocks, unit == block
+        for (uint32_t q = 0; q < 4; ++q) {
+            uint4 v;
+            v.x = load_u32_unaligned(blk + 10 + 16 * q);
+            v.y = load_u32_unaligned(blk + 14 + 16 * q);
+            v.z = load_u32_unaligned(blk + 18 + 16 * q);
+            v.w = load_u32_unaligned(blk + 22 + 16 * q);
+            *reinterpret_cast<uint4 *>(r.payload + ad[q].payload) = v;
+        }
+        *reinterpret_cast<uint2 *>(r.meta + ad[0].meta) =
+            make_uint2(load_u32_unaligned(blk), load_u32_unaligned(blk + 4));
+    } else if (KIND == kQ4_0) {
+        const uint32_t nb = (r.cols + 31) / 32;
+        uint32_t sc[2] = {0, 0};
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t b = u * 4 + q;
+            if (b >= nb) break;
+            const uint8_t *blk = r.src + (static_cast<size_t>(row) * nb + b) * 18;
+            uint4 v;
+            v.x = load_u32_unaligned(blk + 2);
+            v.y = load_u32_unaligned(blk + 6);
+            v.z = load_u32_unaligned(blk + 10);
+            v.w = load_u32_unaligned(blk + 14);
+            *reinterpret_cast<uint4 *>(r.payload + ad[q].payload) = v;
+            sc[q >> 1] |= static_cast<uint32_t>(blk[0] | (blk[1] << 8)) << (16 * (q & 1));
+        }
+        *reinterpret_cast<uint2 *>(r.meta + ad[0].meta) = make_uint2(sc[0], sc[1]);
+    } else {
+        const uint8_t *src = r.src + (static_cast<size_t>(row) * r.cols + u * 8) * 2;
+        const uint32_t n = min(8u, r.cols - u * 8);
+        uint32_t h[4] = {0, 0, 0, 0};
+        for (uint32_t i = 0; i < n; ++i)
+            h[i >> 1] |= static_cast<uint32_t>(src[2 * i] | (src[2 * i + 1] << 8)) << (16 * (i & 1));
+        *reinterpret_cast<uint4 *>(r.payload + ad[0].payload) = make_uint4(h[0], h[1], h[2], h[3]);
     }
-    *reinterpret_cast<uint16_t *>(scales + r * scale_row + static_cast<size_t>(b) * 2) =
-        static_cast<uint16_t>(blk[0] | (blk[1] << 8));
 }
 
 // ---- per-token quantization ---------------------------------------------
@@ -428,8 +549,8 @@ hipError_t launch_one(const GemvPlan &p, const GemvArgs &args, hipStream_t strea
 }
 
 template <int KIND, int MT>
-hipError_t dispatch_upl(const GemvPlan &p, const GemvArgs &args, hipStream_t stream) {
-    switch (p.upl) {
+hipError_t dispatch_upl(const GemvPlan &p, const GemvArgs &args, int upl, hipStream_t stream) {
+    switch (upl) {
     case 1: return launch_one<KIND, MT, 1>(p, args, stream);
     case 2: return launch_one<KIND, MT, 2>(p, args, stream);
     case 3: return launch_one<KIND, MT, 3>(p, args, stream);
@@ -441,13 +562,13 @@ hipError_t dispatch_upl(const GemvPlan &p, const GemvArgs &args, hipStream_t str
 }
 
 template <int KIND>
-hipError_t dispatch_mt(const GemvPlan &p, const GemvArgs &args, hipStream_t stream) {
+hipError_t dispatch_mt(const GemvPlan &p, const GemvArgs &args, int upl, hipStream_t stream) {
     switch (p.tokens) {
-    case 1: return dispatch_upl<KIND, 1>(p, args, stream);
-    case 2: return dispatch_upl<KIND, 2>(p, args, stream);
-    case 4: return dispatch_upl<KIND, 4>(p, args, stream);
-    case 8: return dispatch_upl<KIND, 8>(p, args, stream);
-    case 16: return dispatch_upl<KIND, 16>(p, args, stream);
+    case 1: return dispatch_upl<KIND, 1>(p, args, upl, stream);
+    case 2: return dispatch_upl<KIND, 2>(p, args, upl, stream);
+    case 4: return dispatch_upl<KIND, 4>(p, args, upl, stream);
+    case 8: return dispatch_upl<KIND, 8>(p, args, upl, stream);
+    case 16: return dispatch_upl<KIND, 16>(p, args, upl, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -455,16 +576,42 @@ hipError_t dispatch_mt(const GemvPlan &p, const GemvArgs &args, hipStream_t stre
 size_t lds_for(int kind, uint32_t units, int mt) {
     const size_t act = static_cast<size_t>(mt) * units * unit_lds_bytes(kind);
     const size_t sums = kind == kF16 ? 0 : static_cast<size_t>(mt) * units * unit_elems(kind) / 32 * 4;
-    const size_t red = static_cast<size_t>(kGemvThreads) * mt * 4;
-    return act + sums + red;
+    return act + sums;
+}
+
+GemvArgs args_of(const DeviceTensor &t) {
+    GemvArgs a{};
+    a.payload = t.payload;
+    a.meta = t.meta;
+    a.tile_payload_bytes = t.tile_payload_bytes;
+    a.tile_meta_bytes = t.tile_meta_bytes;
+    a.rows = t.rows;
+    a.cols = t.cols;
+    a.units = t.units;
+    a.lanes = t.lanes;
+    a.rows_per_wave = t.rows_per_wave;
+    a.slots = t.slots;
+    return a;
 }
 
 }  // namespace
 
-GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
-    GemvPlan p;
+bool layout_tensor(DeviceTensor &t) {
+    if (t.kind == kHvsq2) {
+        t.units = (t.cols + 255u) / 256u;
+        t.chunks = 4;
+    } else if (t.kind == kQ4_0) {
+        t.units = ((t.cols + 31u) / 32u + 3u) / 4u;
+        t.chunks = 4;
+    } else if (t.kind == kF16) {
+        t.units = (t.cols + 7u) / 8u;
+        t.chunks = 1;
+    } else {
+        return false;
+    }
     static const int kUpl[] = {1, 2, 3, 4, 6, 8};
     double best = -1.0;
+    t.upl = 0;
     for (int upl : kUpl) {
         const int L = static_cast<int>((t.units + upl - 1) / upl);
         if (L > kWaveSize) continue;
@@ -474,61 +621,62 @@ GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
                            (static_cast<double>(rpw) * L) / kWaveSize;
         if (eff > best + 0.04) {
             best = eff;
-            p.upl = upl;
-            p.lanes = L;
-            p.rows_per_wave = rpw;
+            t.upl = upl;
+            t.lanes = L;
+            t.rows_per_wave = rpw;
         }
     }
-    if (p.upl == 0) return p;  // too many units per row
+    if (t.upl == 0) return false;
+    t.slots = t.lanes * t.rows_per_wave;
+    t.tiles = (t.rows + t.rows_per_wave - 1) / t.rows_per_wave;
+    // whole workgroups of tiles, so a workgroup never reads past the end
+    t.tiles = (t.tiles + kGemvWaves - 1) / kGemvWaves * kGemvWaves;
+    t.tile_payload_bytes = static_cast<size_t>(t.upl) * t.chunks * t.slots * 16;
+    t.tile_meta_bytes = t.kind == kF16 ? 0 : static_cast<size_t>(t.upl) * t.slots * 8;
+    const size_t payload = t.tile_payload_bytes * t.tiles;
+    const size_t meta = t.tile_meta_bytes * t.tiles;
+    t.device_bytes = ((payload + 255) & ~static_cast<size_t>(255)) + meta;
+    return true;
+}
+
+GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
+    GemvPlan p;
     int mt = 1;
     const int want = std::min(batch, kMaxTokensPerLaunch);
     while (mt < want) mt *= 2;
     while (mt > 1 && lds_for(t.kind, t.units, mt) > kGemvLdsLimit) mt /= 2;
     p.tokens = mt;
     p.lds_bytes = lds_for(t.kind, t.units, mt);
-    const int rows_per_wg = p.rows_per_wave * kGemvWaves;
-    p.grid = static_cast<int>((t.rows + rows_per_wg - 1) / rows_per_wg);
+    p.grid = static_cast<int>(t.tiles / kGemvWaves);
     return p;
 }
 
 hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging, hipStream_t stream) {
-    if (t.kind == kHvsq2) {
-        const uint32_t nb = t.units;
-        const size_t n = static_cast<size_t>(t.rows) * nb;
-        hipLaunchKernelGGL(repack_hvsq2, dim3((n + 255) / 256), dim3(256), 0, stream, staging,
-                           t.payload, t.meta, t.rows, nb, t.payload_row_bytes, t.meta_row_bytes);
-        return hipGetLastError();
-    }
-    if (t.kind == kQ4_0) {
-        const uint32_t nb = (t.cols + 31) / 32;
-        const size_t n = static_cast<size_t>(t.rows) * nb;
-        hipError_t e = hipMemsetAsync(t.payload, 0, t.payload_row_bytes * t.rows, stream);
-        if (e == hipSuccess) e = hipMemsetAsync(t.meta, 0, t.meta_row_bytes * t.rows, stream);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(repack_q4_0, dim3((n + 255) / 256), dim3(256), 0, stream, staging,
-                           t.payload, t.meta, t.rows, nb, t.payload_row_bytes, t.meta_row_bytes);
-        return hipGetLastError();
-    }
-    if (t.kind == kF16) {
-        hipError_t e = hipMemsetAsync(t.payload, 0, t.payload_row_bytes * t.rows, stream);
-        if (e != hipSuccess) return e;
-        return hipMemcpy2DAsync(t.payload, t.payload_row_bytes, staging,
-                                static_cast<size_t>(t.cols) * 2, static_cast<size_t>(t.cols) * 2,
-                                t.rows, hipMemcpyDeviceToDevice, stream);
-    }
-    return hipErrorInvalidValue;
+    hipError_t e = hipMemsetAsync(t.payload, 0, t.device_bytes, stream);
+    if (e != hipSuccess) return e;
+    RepackArgs r{};
+    r.src = staging;
+    r.payload = t.payload;
+    r.meta = t.meta;
+    r.rows = t.rows;
+    r.cols = t.cols;
+    r.units = t.units;
+    r.lanes = t.lanes;
+    r.rows_per_wave = t.rows_per_wave;
+    r.slots = t.slots;
+    r.tile_payload = t.tile_payload_bytes;
+    r.tile_meta = t.tile_meta_bytes;
+    const size_t n = static_cast<size_t>(t.rows) * t.units;
+    const dim3 grid((n + 255) / 256);
+    if (t.kind == kHvsq2) hipLaunchKernelGGL(repack_kernel<kHvsq2>, grid, dim3(256), 0, stream, r);
+    else if (t.kind == kQ4_0) hipLaunchKernelGGL(repack_kernel<kQ4_0>, grid, dim3(256), 0, stream, r);
+    else hipLaunchKernelGGL(repack_kernel<kF16>, grid, dim3(256), 0, stream, r);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
     const DeviceTensor &t = *g.tensor;
-    GemvArgs args{};
-    args.payload = t.payload;
-    args.meta = t.meta;
-    args.payload_row_bytes = t.payload_row_bytes;
-    args.meta_row_bytes = t.meta_row_bytes;
-    args.rows = t.rows;
-    args.cols = t.cols;
-    args.units = t.units;
+    GemvArgs args = args_of(t);
     args.input_stride = g.input_stride;
     args.output_stride = g.output_stride;
 
@@ -550,9 +698,7 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
     }
 
     const GemvPlan p = plan_gemv(t, static_cast<int>(g.batch));
-    if (p.upl == 0 || p.tokens == 0 || p.lds_bytes > kGemvLdsLimit) return hipErrorInvalidValue;
-    args.lanes = p.lanes;
-    args.rows_per_wave = p.rows_per_wave;
+    if (p.tokens == 0 || p.lds_bytes > kGemvLdsLimit) return hipErrorInvalidValue;
     const size_t elem = t.kind == kF16 ? 4 : 1;
     for (uint32_t t0 = 0; t0 < g.batch; t0 += p.tokens) {
         args.ntok = std::min<uint32_t>(p.tokens, g.batch - t0);
@@ -561,9 +707,9 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
         args.scale = g.scale;
         args.output = g.output + static_cast<size_t>(t0) * g.output_stride;
         hipError_t e;
-        if (t.kind == kHvsq2) e = dispatch_mt<kHvsq2>(p, args, stream);
-        else if (t.kind == kQ4_0) e = dispatch_mt<kQ4_0>(p, args, stream);
-        else e = dispatch_mt<kF16>(p, args, stream);
+        if (t.kind == kHvsq2) e = dispatch_mt<kHvsq2>(p, args, t.upl, stream);
+        else if (t.kind == kQ4_0) e = dispatch_mt<kQ4_0>(p, args, t.upl, stream);
+        else e = dispatch_mt<kF16>(p, args, t.upl, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -1,21 +1,27 @@
 // Internal declarations shared by the qwn_hip translation units.
 //
-// Device layouts (chosen at upload; the ABI keeps them private):
+// Device layouts (chosen at upload; the ABI keeps them private).
 //
-//  HyperVSQ-2 (74-byte blocks of 256 weights, c/qwanto_native.h:96-103)
-//    codes plane  [rows][nb][64 B]   the 2-bit codes, 16-byte aligned
-//    meta  plane  [rows][nb][8 B]    {fp16 d_base, fp16 m_base, 4 bytes of
-//                                     octant multipliers}; the two reserved
-//                                     bytes are dropped (never read by the
-//                                     reference kernels either)
-//  Q4_0 (18-byte blocks of 32 weights, c/qwanto_native.h:35)
-//    nibble plane [rows][nu*4][16 B] nibbles, rows padded to a multiple of
-//                                     four blocks with zero blocks
-//    scale  plane [rows][nu*4] fp16  zero for padding blocks
-//  F16: [rows][cols] binary16, row stride padded to 16 bytes
+// Every GEMV launch maps a matrix onto waves the same way: a row is split
+// across `lanes` lanes, each lane owning `upl` units (strided by `lanes`),
+// and a wave holds `rows_per_wave` row groups.  A "unit" is one HyperVSQ-2
+// block (256 weights), four Q4_0 blocks (128 weights) or eight F16 weights.
+// Weights are stored wave tile by wave tile in exactly the order the lanes
+// load them, so every load instruction of a wave reads one contiguous span
+// (slots*16 bytes):
 //
-// A "unit" is what one lane consumes per step: one HyperVSQ-2 block (256
-// weights), four Q4_0 blocks (128 weights) or eight F16 weights.
+//   tile t (rows t*rows_per_wave ...), slot s = group*lanes + lane (s < slots)
+//   payload: [tile][unit slot i < upl][chunk q < chunks][slot s][16 B]
+//   meta:    [tile][unit slot i < upl][slot s][8 B]
+//
+//   HyperVSQ-2: chunk q = codes of octants 2q, 2q+1 (16 B); meta = fp16
+//               d_base, fp16 m_base, four bytes of octant multipliers (the
+//               two reserved bytes of the 74-byte block are dropped: the
+//               reference kernels never read them either)
+//   Q4_0:       chunk q = the 16 nibble bytes of block 4u+q; meta = the
+//               four fp16 block scales (zero for padding blocks)
+//   F16:        one chunk of eight halves, no meta
+// Padding slots (units past the row end, rows past the matrix) are zero.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -48,25 +54,31 @@ struct DeviceTensor {
     uint32_t rows = 0;
     uint32_t cols = 0;
     uint32_t units = 0;          // units per row
-    uint8_t *payload = nullptr;  // codes / nibbles / halves plane
-    uint8_t *meta = nullptr;     // meta / scale plane (null for F16)
-    size_t payload_row_bytes = 0;
-    size_t meta_row_bytes = 0;
+    // lane plan, fixed at upload because it defines the layout
+    uint32_t lanes = 0;
+    uint32_t upl = 0;
+    uint32_t rows_per_wave = 0;
+    uint32_t slots = 0;          // lanes * rows_per_wave
+    uint32_t chunks = 0;         // 16-byte payload chunks per unit
+    uint32_t tiles = 0;
+    size_t tile_payload_bytes = 0;
+    size_t tile_meta_bytes = 0;
+    uint8_t *payload = nullptr;
+    uint8_t *meta = nullptr;     // null for F16
     uint64_t device_bytes = 0;   // bytes allocated on the device
     uint64_t logical_bytes = 0;  // algorithmic (on-disk) bytes
 };
 
-// Lane mapping of one GEMV launch: each row is split across `lanes` lanes
-// of a wave, each lane handling `upl` units strided by `lanes`, and a wave
-// holds `rows_per_wave` such row groups.
+// Launch shape of one GEMV call.
 struct GemvPlan {
-    int lanes = 0;
-    int upl = 0;
-    int rows_per_wave = 0;
     int tokens = 0;        // tokens per launch (template width)
     int grid = 0;
     size_t lds_bytes = 0;
 };
+
+// Fills units/lanes/upl/rows_per_wave/slots/chunks/tiles and the tile sizes
+// of a tensor whose kind/rows/cols are set; false if no plan fits.
+bool layout_tensor(DeviceTensor &t);
 
 GemvPlan plan_gemv(const DeviceTensor &t, int batch);
 

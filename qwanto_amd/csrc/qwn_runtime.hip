@@ -423,28 +423,17 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
     case QWN_CUDA_TENSOR_HYPERVSQ2_74:
         if (up->block_bytes != QWN_CUDA_HYPERVSQ2_BLOCK_BYTES) break;
         t.kind = qwn::kHvsq2;
-        t.units = (up->cols + 255u) / 256u;
-        t.logical_bytes = static_cast<uint64_t>(up->rows) * t.units * 74u;
-        t.payload_row_bytes = static_cast<size_t>(t.units) * 64u;
-        t.meta_row_bytes = static_cast<size_t>(t.units) * 8u;
+        t.logical_bytes = static_cast<uint64_t>(up->rows) * ((up->cols + 255u) / 256u) * 74u;
         break;
-    case QWN_CUDA_TENSOR_Q4_0_18: {
+    case QWN_CUDA_TENSOR_Q4_0_18:
         if (up->block_bytes != QWN_CUDA_Q4_0_BLOCK_BYTES) break;
-        const uint32_t nb = (up->cols + 31u) / 32u;
         t.kind = qwn::kQ4_0;
-        t.units = (nb + 3u) / 4u;
-        t.logical_bytes = static_cast<uint64_t>(up->rows) * nb * 18u;
-        t.payload_row_bytes = static_cast<size_t>(t.units) * 64u;
-        t.meta_row_bytes = static_cast<size_t>(t.units) * 8u;
+        t.logical_bytes = static_cast<uint64_t>(up->rows) * ((up->cols + 31u) / 32u) * 18u;
         break;
-    }
     case QWN_CUDA_TENSOR_F16:
         if (up->block_bytes != 2) break;
         t.kind = qwn::kF16;
-        t.units = (up->cols + 7u) / 8u;
         t.logical_bytes = static_cast<uint64_t>(up->rows) * up->cols * 2u;
-        t.payload_row_bytes = static_cast<size_t>(t.units) * 16u;
-        t.meta_row_bytes = 0;
         break;
     default:
         break;
@@ -459,7 +448,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
                   static_cast<unsigned long long>(t.logical_bytes));
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
-    if (qwn::plan_gemv(t, 1).upl == 0) {
+    if (!qwn::layout_tensor(t)) {
         set_error("tensor rows of %u columns exceed the GEMV lane plan", up->cols);
         return QWN_CUDA_STATUS_UNSUPPORTED;
     }
@@ -470,10 +459,6 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
     }
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hip_fail("hipSetDevice", e);
-    const size_t payload = t.payload_row_bytes * t.rows;
-    const size_t meta = t.meta_row_bytes * t.rows;
-    const size_t meta_off = (payload + 255) & ~static_cast<size_t>(255);
-    t.device_bytes = meta_off + meta;
     if (!budget_allows(ctx, t.logical_bytes, t.device_bytes + t.logical_bytes)) {
         set_error("tensor does not fit the configured GPU memory budget");
         return QWN_CUDA_STATUS_OUT_OF_MEMORY;
@@ -488,7 +473,8 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
         return hip_fail("tensor allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
     }
     t.payload = static_cast<uint8_t *>(rt->allocation);
-    t.meta = meta ? t.payload + meta_off : nullptr;
+    const size_t meta_off = (t.tile_payload_bytes * t.tiles + 255) & ~static_cast<size_t>(255);
+    t.meta = t.tile_meta_bytes ? t.payload + meta_off : nullptr;
     rt->t = t;
     const auto t0 = std::chrono::steady_clock::now();
     e = hipMemcpyAsync(staging, up->host_data, t.logical_bytes, hipMemcpyHostToDevice, ctx->stream);
@@ -803,11 +789,10 @@ QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHi
     info->units_per_row = t.units;
     info->logical_bytes = t.logical_bytes;
     info->device_bytes = t.device_bytes;
-    const qwn::GemvPlan p = qwn::plan_gemv(t, 1);
-    info->lanes_per_row = p.lanes;
-    info->units_per_lane = p.upl;
-    info->rows_per_wave = p.rows_per_wave;
-    info->grid = p.grid;
+    info->lanes_per_row = t.lanes;
+    info->units_per_lane = t.upl;
+    info->rows_per_wave = t.rows_per_wave;
+    info->grid = static_cast<uint32_t>(qwn::plan_gemv(t, 1).grid);
     return QWN_CUDA_STATUS_OK;
 }
 
