@@ -4,7 +4,8 @@ Workload (one "step"): every batch-1 GEMV of a decode token of a Qwen3-4B
 shaped HyperVSQ-2 model -- 36 layers x {q, k, v, o, gate, up, down}, 252
 launches over 1.05 GB of distinct resident weights (four times the 256 MB
 infinity cache, so no step is served from cache) -- each launch reading its
-own int8 activation vector, quantized on the device from N(0,1) fp32.  The
+own activation image (int8 token quantized on the device from N(0,1)
+fp32, in the layout the kernel stages into LDS).  The
 252 launches are captured once in a HIP graph and replayed.
 
 value = algorithmic weight bytes per step / step time (GB/s); roofline is
@@ -61,21 +62,21 @@ class Sweep:
                 N, K = shapes[proj]
                 w = synth.weights(dtype, rng, N, K)
                 h = ctx.upload(w, dtype, N, K)
-                stride = (K + 255) // 256 * 256
+                ib = ctx.image_bytes(h)
                 x = torch.randn(1, K, device=dev, dtype=torch.float32)
-                q8 = torch.zeros(1, stride, device=dev, dtype=torch.int8)
+                img = torch.zeros(1, ib, device=dev, dtype=torch.uint8)
                 sc = torch.zeros(1, device=dev, dtype=torch.float32)
                 y = torch.zeros(1, N, device=dev, dtype=torch.float32)
-                ctx.quantize_device(x.data_ptr(), 1, K, K, q8.data_ptr(), stride, sc.data_ptr(),
-                                    torch.cuda.current_stream().cuda_stream)
-                self.items.append((proj, N, K, h, q8, sc, y, stride))
+                ctx.quantize_image_device(h, x.data_ptr(), 1, K, img.data_ptr(), ib, sc.data_ptr(),
+                                          stream=torch.cuda.current_stream().cuda_stream)
+                self.items.append((proj, N, K, h, img, sc, y, ib))
                 self.weight_bytes += synth.weight_bytes(dtype, N, K)
         torch.cuda.synchronize()
 
     def launch(self, item, stream):
-        proj, N, K, h, q8, sc, y, stride = item
-        self.ctx.gemm_device(h, q8.data_ptr(), y.data_ptr(), N, K, 1, stride,
-                             scales_ptr=sc.data_ptr(), stream=stream)
+        proj, N, K, h, img, sc, y, ib = item
+        self.ctx.gemm_image_device(h, img.data_ptr(), ib, y.data_ptr(), 1, N,
+                                   scales_ptr=sc.data_ptr(), stream=stream)
 
     def step(self, stream, only=None):
         for it in self.items:

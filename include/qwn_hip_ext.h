@@ -41,16 +41,48 @@ typedef struct {
 QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *tensor,
                                              QwnHipTensorInfo *info);
 
-/* GEMV/GEMM with device pointers: request->input_q8 / input_scales /
- * output are device addresses (input_q8 is fp32 for F16 tensors with
- * QWN_CUDA_INPUT_F32).  Any batch; weights are read once per 16 tokens. */
-QWN_CUDA_ABI_API int qwn_hip_ext_gemm_device(QwnCudaContextHandle *context,
-                                             const QwnCudaGemmRequest *request,
-                                             void *stream);
+/* Activation images.  The GEMV reads activations from an "image": per token
+ * the exact LDS layout its dot products use (int8 values split into signed
+ * high and unsigned low nibbles in the order the weight unpack produces,
+ * plus per-32 correction sums; fp32 for F16 tensors).  Images depend only
+ * on the tensor's dtype and column count, so one image serves every tensor
+ * with the same input (q/k/v, gate/up).  Image strides and pointers must be
+ * 16-byte aligned. */
+QWN_CUDA_ABI_API uint64_t qwn_hip_ext_activation_image_bytes(const QwnCudaTensorHandle *tensor);
 
-/* Per-token int8 quantization on the device, the activation step of
- * c/qwanto_kernels.c:354-433: x fp32 [batch][x_stride] -> q8
- * [batch][q8_stride] (zero padded past cols), scales [batch]. */
+/* Image from int8 tokens (HyperVSQ-2, Q4_0 tensors) or fp32 tokens (F16
+ * tensors): x [batch][x_stride elements] -> image [batch][image_stride]. */
+QWN_CUDA_ABI_API int qwn_hip_ext_prepare_image_device(QwnCudaContextHandle *context,
+                                                      const QwnCudaTensorHandle *tensor,
+                                                      const void *x, uint32_t batch,
+                                                      uint32_t x_stride, void *image,
+                                                      uint32_t image_stride, void *stream);
+
+/* Per-token int8 quantization of fp32 x (the activation step of
+ * c/qwanto_kernels.c:354-433) fused with the image build: writes scales
+ * [batch], the images and, if q8 is not NULL, the int8 tokens
+ * [batch][q8_stride] zero padded. */
+QWN_CUDA_ABI_API int qwn_hip_ext_quantize_image_device(QwnCudaContextHandle *context,
+                                                       const QwnCudaTensorHandle *tensor,
+                                                       const float *x, uint32_t batch,
+                                                       uint32_t x_stride, void *image,
+                                                       uint32_t image_stride, float *scales,
+                                                       int8_t *q8, uint32_t q8_stride,
+                                                       void *stream);
+
+/* GEMV/GEMM on images: output [batch][output_stride] = W x_t * scale_t
+ * (scales[t], or `scale` when scales is NULL; ignored for F16).  Weights
+ * are read once per 16 tokens. */
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *context,
+                                                   const QwnCudaTensorHandle *tensor,
+                                                   const void *image, uint32_t image_stride,
+                                                   const float *scales, float scale,
+                                                   float *output, uint32_t batch,
+                                                   uint32_t output_stride, void *stream);
+
+/* Per-token int8 quantization on the device without an image:
+ * x fp32 [batch][x_stride] -> q8 [batch][q8_stride] (zero padded past
+ * cols), scales [batch]. */
 QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *context,
                                                  const float *x, uint32_t batch,
                                                  uint32_t cols, uint32_t x_stride,

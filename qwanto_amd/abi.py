@@ -47,7 +47,9 @@ EXPORTS = (
     "qwn_cuda_abi_get_telemetry", "qwn_cuda_abi_last_error",
 )
 EXT_EXPORTS = (
-    "qwn_hip_ext_tensor_info", "qwn_hip_ext_gemm_device", "qwn_hip_ext_quantize_device",
+    "qwn_hip_ext_tensor_info", "qwn_hip_ext_activation_image_bytes",
+    "qwn_hip_ext_prepare_image_device", "qwn_hip_ext_quantize_image_device",
+    "qwn_hip_ext_gemm_image_device", "qwn_hip_ext_quantize_device",
     "qwn_hip_ext_kv_append_device", "qwn_hip_ext_attention_workspace_bytes",
     "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
 )
@@ -206,7 +208,15 @@ class Library:
         lib.qwn_cuda_abi_get_telemetry.argtypes = [P(Handle), P(Telemetry)]
         lib.qwn_cuda_abi_last_error.argtypes = [ctypes.c_char_p, ctypes.c_uint32]
         lib.qwn_hip_ext_tensor_info.argtypes = [P(Handle), P(TensorInfo)]
-        lib.qwn_hip_ext_gemm_device.argtypes = [P(Handle), P(GemmRequest), ctypes.c_void_p]
+        V, U32 = ctypes.c_void_p, ctypes.c_uint32
+        lib.qwn_hip_ext_activation_image_bytes.argtypes = [P(Handle)]
+        lib.qwn_hip_ext_activation_image_bytes.restype = ctypes.c_uint64
+        lib.qwn_hip_ext_prepare_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V,
+                                                         U32, V]
+        lib.qwn_hip_ext_quantize_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V,
+                                                          U32, V, V, U32, V]
+        lib.qwn_hip_ext_gemm_image_device.argtypes = [P(Handle), P(Handle), V, U32, V,
+                                                      ctypes.c_float, V, U32, U32, V]
         lib.qwn_hip_ext_quantize_device.argtypes = [P(Handle), ctypes.c_void_p, ctypes.c_uint32,
                                                     ctypes.c_uint32, ctypes.c_uint32,
                                                     ctypes.c_void_p, ctypes.c_uint32,
@@ -320,15 +330,29 @@ class Context:
             self._h, ctypes.byref(h), _p(q8), _p(out), count))
         return out
 
-    def gemm_device(self, h: Handle, x_ptr: int, out_ptr: int, rows: int, cols: int,
-                    batch: int, input_stride: int, scales_ptr: int | None = None,
-                    scale: float = 0.0, f32: bool = False, stream: int | None = None) -> None:
-        req = GemmRequest(tensor=h, input_q8=x_ptr, input_scale=scale, input_scales=scales_ptr,
-                          output=out_ptr, batch=batch, rows=rows, cols=cols,
-                          input_stride=input_stride, output_stride=rows,
-                          input_mode=INPUT_F32 if f32 else INPUT_Q8)
-        self.lib.check("gemm_device", self.lib.lib.qwn_hip_ext_gemm_device(
-            self._h, ctypes.byref(req), stream))
+    def image_bytes(self, h: Handle) -> int:
+        """Bytes of one token's activation image for tensor h."""
+        return int(self.lib.lib.qwn_hip_ext_activation_image_bytes(ctypes.byref(h)))
+
+    def prepare_image_device(self, h: Handle, x_ptr: int, batch: int, x_stride: int,
+                             image_ptr: int, image_stride: int, stream: int | None = None) -> None:
+        self.lib.check("prepare_image_device", self.lib.lib.qwn_hip_ext_prepare_image_device(
+            self._h, ctypes.byref(h), x_ptr, batch, x_stride, image_ptr, image_stride, stream))
+
+    def quantize_image_device(self, h: Handle, x_ptr: int, batch: int, x_stride: int,
+                              image_ptr: int | None, image_stride: int, scales_ptr: int,
+                              q8_ptr: int | None = None, q8_stride: int = 0,
+                              stream: int | None = None) -> None:
+        self.lib.check("quantize_image_device", self.lib.lib.qwn_hip_ext_quantize_image_device(
+            self._h, ctypes.byref(h), x_ptr, batch, x_stride, image_ptr, image_stride, scales_ptr,
+            q8_ptr, q8_stride, stream))
+
+    def gemm_image_device(self, h: Handle, image_ptr: int, image_stride: int, out_ptr: int,
+                          batch: int, output_stride: int, scales_ptr: int | None = None,
+                          scale: float = 0.0, stream: int | None = None) -> None:
+        self.lib.check("gemm_image_device", self.lib.lib.qwn_hip_ext_gemm_image_device(
+            self._h, ctypes.byref(h), image_ptr, image_stride, scales_ptr, scale, out_ptr, batch,
+            output_stride, stream))
 
     def quantize_device(self, x_ptr: int, batch: int, cols: int, x_stride: int, q8_ptr: int,
                         q8_stride: int, scales_ptr: int, stream: int | None = None) -> None:
@@ -405,7 +429,15 @@ _LIB: Library | None = None
 
 
 def load() -> Library:
+    """Load the library once per process.  When torch is importable it is
+    imported first: torch bundles a HIP runtime with the same soname as the
+    one the library links, and whichever loads first serves both, so loading
+    torch first lets torch device tensors be passed as device buffers."""
     global _LIB
     if _LIB is None:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         _LIB = Library()
     return _LIB

@@ -3,9 +3,14 @@
 // Decode at batch 1 reads every weight exactly once, so the kernel is an
 // HBM stream.  Each wave owns a tile of rows stored contiguously in the
 // order its lanes load it (qwn_internal.h), so every 128-bit load
-// instruction of the wave reads one contiguous span.  The int8 activations
-// are staged once per workgroup in LDS, already split for the dot product
-// (below), and per-row partial sums are combined with wave shuffles.
+// instruction of the wave reads one contiguous span.
+//
+// Activations arrive as an "activation image": the exact LDS byte layout
+// the dot products read (below), built once per token by a producer kernel
+// (from int8, from fp32, or fused with the int8 quantization).  A workgroup
+// copies the image into LDS with direct global->LDS loads issued before its
+// weight loads, waits only for those, and reduces each row's lane partials
+// with DPP adds.
 //
 // Integer core.  An int8 activation is written a = 16*h + l with h = a >> 4
 // in [-8, 7] (signed nibble) and l = a & 15 in [0, 15] (unsigned nibble), so
@@ -18,6 +23,13 @@
 //   Q4_0: the nibble dword already holds weights 0..7 in nibbles 0..7;
 //     (n - 8) is n ^ 8 as a signed nibble, and
 //     sum (n-8)*a = 16*sdot8(n^0x88888888, h) + udot8(n, l) - 8*sum l.
+//
+// Image layout per token (padded to 16 bytes):
+//   HyperVSQ-2: per unit 16 groups x {h even, l even, h odd, l odd} nibble
+//               words (256 B) + 16 B pad; then sum a per 32 activations
+//   Q4_0:       per unit 16 groups x {h, l} nibble words (128 B) + 16 B pad;
+//               then 8 * sum l per 32 activations
+//   F16:        per unit 32 floats (128 B) + 16 B pad
 //
 // Semantics follow the reference CPU kernels:
 //   HyperVSQ-2  y = xs * sum_blocks (d/8 * sum_oct s_oct*(sum code*a - sum a)
@@ -32,10 +44,22 @@
 #include <algorithm>
 
 namespace qwn {
+
+size_t image_act_bytes(int kind, uint32_t units) {
+    return static_cast<size_t>(units) * unit_lds_bytes(kind);
+}
+
+size_t image_bytes(int kind, uint32_t units) {
+    const size_t sums = kind == kF16 ? 0 : static_cast<size_t>(units) * unit_elems(kind) / 32 * 4;
+    return (image_act_bytes(kind, units) + sums + 15) & ~static_cast<size_t>(15);
+}
+
 namespace {
 
 constexpr uint32_t kMask33 = 0x33333333u;
 constexpr uint32_t kFlip8 = 0x88888888u;
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ float half_to_float(uint32_t bits) {
     // v_cvt_f32_f16 keeps fp16 subnormals (the default f16 denormal mode),
@@ -53,7 +77,26 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// ---- activation staging ----------------------------------------------------
+// Sum over aligned groups of `lanes` consecutive lanes (a power of two);
+// the total lands in the last lane of each group.  row_shr steps add the
+// lanes 1, 2, 4, 8 below within each 16-lane row; row_bcast:15/31 carry
+// row totals into the next row for groups of 32 and 64.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, true);
+    return v + __builtin_bit_cast(float, moved);
+}
+__device__ __forceinline__ float group_sum(float v, uint32_t lanes) {
+    if (lanes >= 2) v = dpp_add<0x111, 0xf>(v);   // row_shr:1
+    if (lanes >= 4) v = dpp_add<0x112, 0xf>(v);   // row_shr:2
+    if (lanes >= 8) v = dpp_add<0x114, 0xf>(v);   // row_shr:4
+    if (lanes >= 16) v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    if (lanes >= 32) v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    if (lanes >= 64) v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// ---- activation images --------------------------------------------------------
 
 // Nibble-pack 8 int8 values (two dwords, element order) into the high
 // (signed, a >> 4) and low (a & 15) nibble words, nibble k = element k.
@@ -83,41 +126,21 @@ __device__ __forceinline__ uint4 split16_evenodd(const uint32_t w[4]) {
     return make_uint4(he, le, ho, lo);
 }
 
-// Staging of `ntok` int8 tokens (row stride `stride` bytes, 16-byte
-// aligned) of K valid activations, zero padded to units*unit_elems, one
-// 32-element block per thread and step.  Per block it also stores the
-// correction term: sum a (HyperVSQ-2) or 8 * sum l (Q4_0).  The load half
-// is separate so a kernel can issue a thread's first block before its
-// weight loads (vmcnt waits are in issue order).
-__device__ __forceinline__ void load_block32(const int8_t *__restrict__ x, uint32_t stride, uint32_t K,
-                                             uint32_t ntok, uint32_t t, uint32_t e0, uint32_t w[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = 0;
-    if (t < ntok && e0 < K) {
-        const int8_t *src = x + static_cast<size_t>(t) * stride + e0;
-        if (e0 + 32 <= K) {
-            const uint4 v0 = *reinterpret_cast<const uint4 *>(src);
-            const uint4 v1 = *reinterpret_cast<const uint4 *>(src + 16);
-            w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
-            w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
-        } else {
-            for (uint32_t i = 0; i < K - e0; ++i)
-                w[i >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(src[i]))) << (8 * (i & 3));
-        }
-    }
-}
-
+// Write one 32-activation block (8 dwords of int8, element order) into a
+// token image: its nibble words and its correction term.
 template <int KIND>
-__device__ __forceinline__ void store_block32(uint8_t *tok, int32_t *sum, uint32_t e0, const uint32_t w[8]) {
+__device__ __forceinline__ void put_block32(uint8_t *img, uint32_t units, uint32_t b, const uint32_t w[8]) {
+    const uint32_t e0 = b * 32;
+    int32_t *sums = reinterpret_cast<int32_t *>(img + units * unit_lds_bytes(KIND));
     if (KIND == kHvsq2) {
         int s = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) s = sdot4(w[i], 0x01010101u, s);
-        *sum = s;
+        sums[b] = s;
         const uint32_t u = e0 / 256, off = e0 % 256;
 #pragma unroll
         for (int g = 0; g < 2; ++g)
-            *reinterpret_cast<uint4 *>(tok + u * 272 + (off / 16 + g) * 16) = split16_evenodd(w + 4 * g);
+            *reinterpret_cast<uint4 *>(img + u * 272 + (off / 16 + g) * 16) = split16_evenodd(w + 4 * g);
     } else {
         const uint32_t u = e0 / 128, off = e0 % 128;
         int lsum = 0;
@@ -126,62 +149,128 @@ __device__ __forceinline__ void store_block32(uint8_t *tok, int32_t *sum, uint32
             uint32_t hi, lo;
             split8(w[2 * g], w[2 * g + 1], hi, lo);
             lsum = static_cast<int>(__builtin_amdgcn_udot8(lo, 0x11111111u, static_cast<uint32_t>(lsum), false));
-            *reinterpret_cast<uint2 *>(tok + u * 144 + (off / 8 + g) * 8) = make_uint2(hi, lo);
+            *reinterpret_cast<uint2 *>(img + u * 144 + (off / 8 + g) * 8) = make_uint2(hi, lo);
         }
-        *sum = 8 * lsum;
+        sums[b] = 8 * lsum;
     }
 }
 
-// Stage every block; `first` holds the already loaded block of index
-// threadIdx.x (when that index is in range).
-template <int KIND, int MT>
-__device__ void stage_int8(const int8_t *__restrict__ x, uint32_t stride, uint32_t K,
-                           uint32_t units, uint32_t ntok, uint8_t *act, int32_t *sums,
-                           const uint32_t first[8]) {
+// int8 tokens [M][stride] (K valid, zero padded) -> images.  grid (blocks, M).
+template <int KIND>
+__global__ __launch_bounds__(256) void image_from_int8_kernel(const int8_t *__restrict__ x, uint32_t stride,
+                                                              uint32_t K, uint32_t units, uint8_t *image,
+                                                              uint32_t image_stride) {
     const uint32_t nblk = units * unit_elems(KIND) / 32;
-    const uint32_t token_bytes = units * unit_lds_bytes(KIND);
-    for (uint32_t idx = threadIdx.x; idx < MT * nblk; idx += blockDim.x) {
-        const uint32_t t = idx / nblk, b = idx % nblk, e0 = b * 32;
-        uint32_t w[8];
-        if (idx == threadIdx.x) {
+    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    if (b >= nblk) return;
+    const uint32_t e0 = b * 32;
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int8_t *src = x + static_cast<size_t>(t) * stride + e0;
+    if (e0 + 32 <= K && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        const uint4 v0 = *reinterpret_cast<const uint4 *>(src);
+        const uint4 v1 = *reinterpret_cast<const uint4 *>(src + 16);
+        w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+        w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+    } else {
+        for (uint32_t i = 0; i < 32 && e0 + i < K; ++i)
+            w[i >> 2] |= (static_cast<uint32_t>(static_cast<uint8_t>(src[i]))) << (8 * (i & 3));
+    }
+    put_block32<KIND>(image + static_cast<size_t>(t) * image_stride, units, b, w);
+}
+
+// fp32 tokens [M][stride] (K valid) -> F16 images.  grid (groups of 8, M).
+__global__ __launch_bounds__(256) void image_from_f32_kernel(const float *__restrict__ x, uint32_t stride,
+                                                             uint32_t K, uint32_t units, uint8_t *image,
+                                                             uint32_t image_stride) {
+    const uint32_t gi = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    if (gi >= units * 4) return;
+    const uint32_t e0 = gi * 8;
+    float v[8];
+    const float *src = x + static_cast<size_t>(t) * stride + e0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) w[i] = first[i];
-        } else {
-            load_block32(x, stride, K, ntok, t, e0, w);
+    for (int i = 0; i < 8; ++i) v[i] = e0 + i < K ? src[i] : 0.0f;
+    float4 *dst = reinterpret_cast<float4 *>(image + static_cast<size_t>(t) * image_stride + (gi / 4) * 144 +
+                                             (gi % 4) * 32);
+    dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+    dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// Per-token int8 quantization (c/qwanto_kernels.c:354-433) fused with the
+// image: x fp32 [M][x_stride] -> scales [M], image [M][image_stride] and,
+// when q8 is given, the int8 token [M][q8_stride] zero padded.  grid (M).
+template <int KIND>
+__global__ __launch_bounds__(256) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
+                                                             uint32_t x_stride, uint32_t units, uint8_t *image,
+                                                             uint32_t image_stride, float *scales, int8_t *q8,
+                                                             uint32_t q8_stride) {
+    __shared__ float wave_max[256 / kWaveSize];
+    const uint32_t t = blockIdx.x;
+    const float *row = x + static_cast<size_t>(t) * x_stride;
+    float amax = 0.0f;
+    for (uint32_t k = threadIdx.x; k < K; k += blockDim.x) amax = fmaxf(amax, fabsf(row[k]));
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (threadIdx.x % kWaveSize == 0) wave_max[threadIdx.x / kWaveSize] = amax;
+    __syncthreads();
+    amax = wave_max[0];
+    for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) amax = fmaxf(amax, wave_max[w]);
+    // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
+    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / scale;
+    if (threadIdx.x == 0) scales[t] = scale;
+    const uint32_t nblk = units * unit_elems(KIND) / 32;
+    uint8_t *img = image ? image + static_cast<size_t>(t) * image_stride : nullptr;
+    for (uint32_t b = threadIdx.x; b < nblk; b += blockDim.x) {
+        uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t i = 0; i < 32; ++i) {
+            const uint32_t k = b * 32 + i;
+            if (k >= K) break;
+            const float v = fminf(127.0f, fmaxf(-127.0f, row[k] * inv));
+            const uint32_t q = static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(v)));
+            w[i >> 2] |= q << (8 * (i & 3));
         }
-        store_block32<KIND>(act + t * token_bytes, sums + t * nblk + b, e0, w);
+        if (image) put_block32<KIND>(img, units, b, w);
+        if (q8) {
+            int8_t *dst = q8 + static_cast<size_t>(t) * q8_stride;
+            for (uint32_t i = 0; i < 32 && b * 32 + i < q8_stride; ++i)
+                dst[b * 32 + i] = static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
+        }
+    }
+    if (q8)
+        for (uint32_t k = nblk * 32 + threadIdx.x; k < q8_stride; k += blockDim.x)
+            q8[static_cast<size_t>(t) * q8_stride + k] = 0;
+}
+
+// Copy `ntok` token images (global stride `stride`, `bytes` each, a
+// multiple of 16) into LDS back to back, one 16-byte direct load per lane;
+// returns after issuing (the caller waits).
+__device__ __forceinline__ void issue_image_copy(const uint8_t *__restrict__ image, uint32_t stride,
+                                                 uint32_t bytes, uint32_t ntok, uint8_t *lds) {
+    const uint32_t per_tok = bytes / 16;
+    const uint32_t total = per_tok * ntok;
+    const uint32_t lane = threadIdx.x % kWaveSize;
+    for (uint32_t c0 = (threadIdx.x / kWaveSize) * kWaveSize; c0 < total; c0 += blockDim.x) {
+        const uint32_t c = c0 + lane;
+        if (c < total) {
+            const uint32_t t = c / per_tok, r = c - t * per_tok;
+            __builtin_amdgcn_global_load_lds(image + static_cast<size_t>(t) * stride + r * 16,
+                                             (lds_void *)(lds + c0 * 16), 16, 0, 0);
+        }
     }
 }
 
-// fp32 activations for F16 weights: unit = 8 floats, zero padded.
-template <int MT>
-__device__ void stage_f32(const float *__restrict__ x, uint32_t stride, uint32_t K,
-                          uint32_t units, uint32_t ntok, float *act) {
-    for (uint32_t idx = threadIdx.x; idx < MT * units; idx += blockDim.x) {
-        const uint32_t t = idx / units, u = idx % units, e0 = u * 8;
-        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-        if (t < ntok && e0 < K) {
-            const float *src = x + static_cast<size_t>(t) * stride + e0;
-            if (e0 + 8 <= K) {
-                v0 = *reinterpret_cast<const float4 *>(src);
-                v1 = *reinterpret_cast<const float4 *>(src + 4);
-            } else {
-                float tmp[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                for (uint32_t i = 0; i < K - e0; ++i) tmp[i] = src[i];
-                v0 = make_float4(tmp[0], tmp[1], tmp[2], tmp[3]);
-                v1 = make_float4(tmp[4], tmp[5], tmp[6], tmp[7]);
-            }
-        }
-        float4 *dst = reinterpret_cast<float4 *>(act + (static_cast<size_t>(t) * units + u) * 8);
-        dst[0] = v0;
-        dst[1] = v1;
-    }
+// s_waitcnt vmcnt(n) (n <= 63), expcnt and lgkmcnt left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    constexpr int n = N > 63 ? 63 : N;
+    __builtin_amdgcn_s_waitcnt((n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
 // ---- per-unit integer cores (shared by the GEMV and the dump kernel) ----
 
 // sum over one octant of code*a: w0/w1 = the octant's code dwords, a0/a1 =
-// staged activations of its two 16-element groups.
+// the image words of its two 16-element groups.
 __device__ __forceinline__ int hv_octant_dot(uint32_t w0, uint32_t w1, uint4 a0, uint4 a1) {
     const uint32_t e0 = w0 & kMask33, o0 = (w0 >> 2) & kMask33;
     const uint32_t e1 = w1 & kMask33, o1 = (w1 >> 2) & kMask33;
@@ -197,7 +286,7 @@ __device__ __forceinline__ int hv_octant_dot(uint32_t w0, uint32_t w1, uint4 a0,
 }
 
 // sum over one Q4_0 block of (nibble-8)*a + 8*sum l, i.e. before the
-// staged correction; a0 = (h,l) of nibble dwords 0,1, a1 = of dwords 2,3.
+// image's correction; a0 = (h,l) of nibble dwords 0,1, a1 = of dwords 2,3.
 __device__ __forceinline__ int q4_block_dot(uint4 n, uint4 a0, uint4 a1) {
     int hi = sdot8(n.x ^ kFlip8, a0.x, 0);
     hi = sdot8(n.y ^ kFlip8, a0.z, hi);
@@ -215,25 +304,25 @@ struct GemvArgs {
     const uint8_t *meta;
     size_t tile_payload_bytes;
     size_t tile_meta_bytes;
-    const void *input;
+    const uint8_t *image;
     const float *scales;
     float scale;
     float *output;
     uint32_t rows;
-    uint32_t cols;
     uint32_t units;
     uint32_t lanes;
     uint32_t rows_per_wave;
     uint32_t slots;
     uint32_t ntok;
-    uint32_t input_stride;
+    uint32_t image_stride;
+    uint32_t image_bytes;
     uint32_t output_stride;
 };
 
 template <int KIND, int MT, int UPL>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int CH = KIND == kF16 ? 1 : 4;
+    constexpr int CH = 4;
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = threadIdx.x / kWaveSize;
     const uint32_t L = a.lanes;
@@ -243,18 +332,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     const uint32_t row = tile * a.rows_per_wave + grp;
     const bool active = grp < a.rows_per_wave && row < a.rows;
 
-    // 0. This thread's first activation block (int8 kinds), issued before
-    //    the weights so that waiting for it does not wait for them.
-    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
-    uint32_t first[8];
-    if (KIND != kF16)
-        load_block32(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, a.ntok,
-                     threadIdx.x / nblk, (threadIdx.x % nblk) * 32, first);
+    // 0. Activation images -> LDS (direct loads, issued first).
+    issue_image_copy(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 1. Issue every weight load of this lane, metadata before codes
-    //    (the first octant needs its scales).  Lanes without a unit load
-    //    from the tile start instead of branching around the load, so the
-    //    loads stay one unconditional burst.
+    // 1. Every weight load of this lane, metadata before codes.  Lanes
+    //    without a unit load from the tile start instead of branching, so
+    //    the loads stay one unconditional burst.
     const uint8_t *tile_p = a.payload + tile * a.tile_payload_bytes;
     const uint8_t *tile_m = a.meta + tile * a.tile_meta_bytes;
     const uint8_t *tp = tile_p + lane * 16;
@@ -276,21 +360,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
             pay[i][q] = *reinterpret_cast<const uint4 *>(
                 ok ? tp + static_cast<size_t>(i * CH + q) * a.slots * 16 : tile_p);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 2. Stage the activations of all tokens in LDS.
-    uint8_t *act = smem;
-    int32_t *sums = reinterpret_cast<int32_t *>(smem + MT * a.units * unit_lds_bytes(KIND));
-    float *red = reinterpret_cast<float *>(
-        smem + MT * a.units * unit_lds_bytes(KIND) + (KIND == kF16 ? 0 : MT * nblk * 4));
-    if (KIND == kF16)
-        stage_f32<MT>(static_cast<const float *>(a.input), a.input_stride, a.cols, a.units,
-                      a.ntok, reinterpret_cast<float *>(act));
-    else
-        stage_int8<KIND, MT>(static_cast<const int8_t *>(a.input), a.input_stride, a.cols,
-                             a.units, a.ntok, act, sums, first);
+    // 2. Wait for the image loads only (vmcnt counts in issue order), then
+    //    for every wave's share of the copy.
+    wait_vmcnt<(KIND == kF16 ? 4 : 5) * UPL>();
     __syncthreads();
 
     // 3. Dot products.
+    const uint32_t ib = a.image_bytes;
+    const uint32_t act_bytes = a.units * unit_lds_bytes(KIND);
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -303,87 +382,79 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
             const float d = half_to_float(met[i].x & 0xffffu);
             const float m = half_to_float(met[i].x >> 16);
             const uint32_t subs = met[i].y;
-            int s1[MT], sa[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t) s1[t] = sa[t] = 0;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                // all 16 activation groups and 8 octant sums of this unit at once
-                const uint4 *at = reinterpret_cast<const uint4 *>(act + (t * a.units + u) * 272);
+                const uint8_t *img = smem + t * ib;
+                const uint4 *at = reinterpret_cast<const uint4 *>(img + u * 272);
                 uint4 av[16];
 #pragma unroll
                 for (int g = 0; g < 16; ++g) av[g] = at[g];
-                const int4 *sp = reinterpret_cast<const int4 *>(sums + t * nblk + u * 8);
+                const int4 *sp = reinterpret_cast<const int4 *>(img + act_bytes + u * 32);
                 const int4 sv0 = sp[0], sv1 = sp[1];
                 const int so[8] = {sv0.x, sv0.y, sv0.z, sv0.w, sv1.x, sv1.y, sv1.z, sv1.w};
+                int s1 = 0, sa = 0;
 #pragma unroll
                 for (int o = 0; o < 8; ++o) {
                     const int s = static_cast<int>((subs >> (4 * o)) & 15u);
-                    s1[t] += s * (hv_octant_dot(cw[2 * o], cw[2 * o + 1], av[2 * o], av[2 * o + 1]) - so[o]);
-                    sa[t] += so[o];
+                    s1 += s * (hv_octant_dot(cw[2 * o], cw[2 * o + 1], av[2 * o], av[2 * o + 1]) - so[o]);
+                    sa += so[o];
                 }
-            }
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                acc[t] = fmaf(d, static_cast<float>(s1[t]) * 0.125f, acc[t]);
-                acc[t] = fmaf(m, static_cast<float>(sa[t]), acc[t]);
+                acc[t] = fmaf(d, static_cast<float>(s1) * 0.125f, acc[t]);
+                acc[t] = fmaf(m, static_cast<float>(sa), acc[t]);
             }
         } else if (KIND == kQ4_0) {
             const uint32_t sc[2] = {met[i].x, met[i].y};
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const float d = half_to_float(sc[b >> 1] >> (16 * (b & 1)));
+            for (int t = 0; t < MT; ++t) {
+                const uint8_t *img = smem + t * ib;
+                const uint4 *at = reinterpret_cast<const uint4 *>(img + u * 144);
+                const int4 corr = *reinterpret_cast<const int4 *>(img + act_bytes + u * 16);
+                const int cb[4] = {corr.x, corr.y, corr.z, corr.w};
 #pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const uint8_t *at = act + (t * a.units + u) * 144 + b * 32;
-                    const uint4 a0 = *reinterpret_cast<const uint4 *>(at);
-                    const uint4 a1 = *reinterpret_cast<const uint4 *>(at + 16);
-                    const int raw = q4_block_dot(pay[i][b], a0, a1) - sums[t * nblk + u * 4 + b];
+                for (int b = 0; b < 4; ++b) {
+                    const float d = half_to_float(sc[b >> 1] >> (16 * (b & 1)));
+                    const int raw = q4_block_dot(pay[i][b], at[2 * b], at[2 * b + 1]) - cb[b];
                     acc[t] = fmaf(static_cast<float>(raw), d, acc[t]);
                 }
             }
         } else {
-            const uint32_t h[4] = {pay[i][0].x, pay[i][0].y, pay[i][0].z, pay[i][0].w};
-            float wf[8];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                wf[2 * q] = half_to_float(h[q] & 0xffffu);
-                wf[2 * q + 1] = half_to_float(h[q] >> 16);
-            }
-            const float *xa = reinterpret_cast<const float *>(act);
+                const uint32_t h[4] = {pay[i][q].x, pay[i][q].y, pay[i][q].z, pay[i][q].w};
+                float wf[8];
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const float4 x0 = *reinterpret_cast<const float4 *>(xa + (t * a.units + u) * 8);
-                const float4 x1 = *reinterpret_cast<const float4 *>(xa + (t * a.units + u) * 8 + 4);
-                float s = acc[t];
-                s = fmaf(wf[0], x0.x, s); s = fmaf(wf[1], x0.y, s);
-                s = fmaf(wf[2], x0.z, s); s = fmaf(wf[3], x0.w, s);
-                s = fmaf(wf[4], x1.x, s); s = fmaf(wf[5], x1.y, s);
-                s = fmaf(wf[6], x1.z, s); s = fmaf(wf[7], x1.w, s);
-                acc[t] = s;
+                for (int k = 0; k < 4; ++k) {
+                    wf[2 * k] = half_to_float(h[k] & 0xffffu);
+                    wf[2 * k + 1] = half_to_float(h[k] >> 16);
+                }
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const float4 *xa = reinterpret_cast<const float4 *>(smem + t * ib + u * 144 + q * 32);
+                    const float4 x0 = xa[0], x1 = xa[1];
+                    float s = acc[t];
+                    s = fmaf(wf[0], x0.x, s); s = fmaf(wf[1], x0.y, s);
+                    s = fmaf(wf[2], x0.z, s); s = fmaf(wf[3], x0.w, s);
+                    s = fmaf(wf[4], x1.x, s); s = fmaf(wf[5], x1.y, s);
+                    s = fmaf(wf[6], x1.z, s); s = fmaf(wf[7], x1.w, s);
+                    acc[t] = s;
+                }
             }
         }
     }
 
-    // 4. Combine the L partials of each row inside the wave (ds_bpermute,
-    //    no workgroup barrier).
-    float tot[MT];
+    // 4. Combine the L partials of each row with DPP; the group's last lane
+    //    holds the row total and writes it.
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        float s = 0.0f;
-        for (uint32_t l = 0; l < L; ++l) s += __shfl(acc[t], static_cast<int>(grp * L + l));
-        tot[t] = s;
-    }
-    if (active) {
+    for (int t = 0; t < MT; ++t) acc[t] = group_sum(acc[t], L);
+    if (active && j == L - 1) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            if (static_cast<uint32_t>(t) % L != j || static_cast<uint32_t>(t) >= a.ntok) continue;
-            float s = tot[t];
+            if (static_cast<uint32_t>(t) >= a.ntok) break;
+            float s = acc[t];
             if (KIND != kF16) s *= a.scales ? a.scales[t] : a.scale;
             a.output[static_cast<size_t>(t) * a.output_stride + row] = s;
         }
     }
-    (void)red;
 }
 
 // Byte address of chunk q of unit u of a row, and of its metadata.
@@ -402,23 +473,12 @@ __host__ __device__ inline UnitAddr unit_addr(uint32_t row, uint32_t u, uint32_t
     return r;
 }
 
-// Integer dump: one thread per (row, unit), token 0 only.  Same staging
-// and per-unit cores as gemv_kernel; used by the bit-exactness tests.
+// Integer dump: one thread per (row, unit), token 0 only.  Same image and
+// per-unit cores as gemv_kernel; used by the bit-exactness tests.
 //   HyperVSQ-2: out[row][unit*8 + oct] = sum (code-1)*a
 //   Q4_0:       out[row][block]       = sum (nibble-8)*a
 template <int KIND>
-__global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t *out,
-                                                            uint32_t out_row) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *act = smem;
-    int32_t *sums = reinterpret_cast<int32_t *>(smem + a.units * unit_lds_bytes(KIND));
-    const uint32_t nblk = a.units * unit_elems(KIND) / 32;
-    uint32_t first[8];
-    load_block32(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, 1, threadIdx.x / nblk,
-                 (threadIdx.x % nblk) * 32, first);
-    stage_int8<KIND, 1>(static_cast<const int8_t *>(a.input), a.input_stride, a.cols, a.units,
-                        1, act, sums, first);
-    __syncthreads();
+__global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t *out, uint32_t out_row) {
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= a.rows * a.units) return;
     const uint32_t row = idx / a.units, u = idx % a.units;
@@ -428,23 +488,21 @@ __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t 
                                       a.tile_payload_bytes, a.tile_meta_bytes);
         pay[q] = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
     }
+    const uint8_t *img = a.image;
+    const int32_t *sums = reinterpret_cast<const int32_t *>(img + a.units * unit_lds_bytes(KIND));
     if (KIND == kHvsq2) {
         const uint32_t *cw = reinterpret_cast<const uint32_t *>(pay);
         for (int o = 0; o < 8; ++o) {
-            const uint8_t *at = act + u * 272 + o * 32;
-            const int v = hv_octant_dot(cw[2 * o], cw[2 * o + 1], *reinterpret_cast<const uint4 *>(at),
-                                        *reinterpret_cast<const uint4 *>(at + 16)) -
-                          sums[u * 8 + o];
-            out[static_cast<size_t>(row) * out_row + u * 8 + o] = v;
+            const uint4 *at = reinterpret_cast<const uint4 *>(img + u * 272 + o * 32);
+            out[static_cast<size_t>(row) * out_row + u * 8 + o] =
+                hv_octant_dot(cw[2 * o], cw[2 * o + 1], at[0], at[1]) - sums[u * 8 + o];
         }
     } else {
         for (int b = 0; b < 4; ++b) {
             if (u * 4 + b >= out_row) break;
-            const uint8_t *at = act + u * 144 + b * 32;
+            const uint4 *at = reinterpret_cast<const uint4 *>(img + u * 144 + b * 32);
             out[static_cast<size_t>(row) * out_row + u * 4 + b] =
-                q4_block_dot(pay[b], *reinterpret_cast<const uint4 *>(at),
-                             *reinterpret_cast<const uint4 *>(at + 16)) -
-                sums[u * 4 + b];
+                q4_block_dot(pay[b], at[0], at[1]) - sums[u * 4 + b];
         }
     }
 }
@@ -469,10 +527,9 @@ __global__ void repack_kernel(RepackArgs r) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= static_cast<size_t>(r.rows) * r.units) return;
     const uint32_t row = idx / r.units, u = idx % r.units;
-    const uint32_t chunks = KIND == kF16 ? 1 : 4;
     UnitAddr ad[4];
-    for (uint32_t q = 0; q < chunks; ++q)
-        ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.slots, chunks, r.tile_payload, r.tile_meta);
+    for (uint32_t q = 0; q < 4; ++q)
+        ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.slots, 4, r.tile_payload, r.tile_meta);
     if (KIND == kHvsq2) {
         const uint8_t *blk = r.src + idx * 74;  // [row][unit] blocks, unit == block
         for (uint32_t q = 0; q < 4; ++q) {
@@ -502,42 +559,17 @@ __global__ void repack_kernel(RepackArgs r) {
         }
         *reinterpret_cast<uint2 *>(r.meta + ad[0].meta) = make_uint2(sc[0], sc[1]);
     } else {
-        const uint8_t *src = r.src + (static_cast<size_t>(row) * r.cols + u * 8) * 2;
-        const uint32_t n = min(8u, r.cols - u * 8);
-        uint32_t h[4] = {0, 0, 0, 0};
-        for (uint32_t i = 0; i < n; ++i)
-            h[i >> 1] |= static_cast<uint32_t>(src[2 * i] | (src[2 * i + 1] << 8)) << (16 * (i & 1));
-        *reinterpret_cast<uint4 *>(r.payload + ad[0].payload) = make_uint4(h[0], h[1], h[2], h[3]);
-    }
-}
-
-// ---- per-token quantization ---------------------------------------------
-
-__global__ __launch_bounds__(256) void quantize_tokens_kernel(const float *__restrict__ x, int K,
-                                                              int x_stride, int8_t *q8,
-                                                              int out_stride, float *scales) {
-    __shared__ float wave_max[256 / kWaveSize];
-    const int t = blockIdx.x;
-    const float *row = x + static_cast<size_t>(t) * x_stride;
-    float amax = 0.0f;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) amax = fmaxf(amax, fabsf(row[k]));
-    for (int off = kWaveSize / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    if (threadIdx.x % kWaveSize == 0) wave_max[threadIdx.x / kWaveSize] = amax;
-    __syncthreads();
-    amax = wave_max[0];
-    for (int w = 1; w < static_cast<int>(blockDim.x / kWaveSize); ++w) amax = fmaxf(amax, wave_max[w]);
-    // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
-    const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    const float inv = 1.0f / scale;
-    if (threadIdx.x == 0) scales[t] = scale;
-    int8_t *out = q8 + static_cast<size_t>(t) * out_stride;
-    for (int k = threadIdx.x; k < out_stride; k += blockDim.x) {
-        int8_t q = 0;
-        if (k < K) {
-            const float v = fminf(127.0f, fmaxf(-127.0f, row[k] * inv));
-            q = static_cast<int8_t>(__builtin_rintf(v));
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t k0 = u * 32 + q * 8;
+            uint32_t h[4] = {0, 0, 0, 0};
+            if (k0 < r.cols) {
+                const uint8_t *src = r.src + (static_cast<size_t>(row) * r.cols + k0) * 2;
+                const uint32_t n = min(8u, r.cols - k0);
+                for (uint32_t i = 0; i < n; ++i)
+                    h[i >> 1] |= static_cast<uint32_t>(src[2 * i] | (src[2 * i + 1] << 8)) << (16 * (i & 1));
+            }
+            *reinterpret_cast<uint4 *>(r.payload + ad[q].payload) = make_uint4(h[0], h[1], h[2], h[3]);
         }
-        out[k] = q;
     }
 }
 
@@ -555,8 +587,12 @@ hipError_t dispatch_upl(const GemvPlan &p, const GemvArgs &args, int upl, hipStr
     case 2: return launch_one<KIND, MT, 2>(p, args, stream);
     case 3: return launch_one<KIND, MT, 3>(p, args, stream);
     case 4: return launch_one<KIND, MT, 4>(p, args, stream);
+    case 5: return launch_one<KIND, MT, 5>(p, args, stream);
     case 6: return launch_one<KIND, MT, 6>(p, args, stream);
     case 8: return launch_one<KIND, MT, 8>(p, args, stream);
+    case 10: return launch_one<KIND, MT, 10>(p, args, stream);
+    case 12: return launch_one<KIND, MT, 12>(p, args, stream);
+    case 16: return launch_one<KIND, MT, 16>(p, args, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -573,12 +609,6 @@ hipError_t dispatch_mt(const GemvPlan &p, const GemvArgs &args, int upl, hipStre
     }
 }
 
-size_t lds_for(int kind, uint32_t units, int mt) {
-    const size_t act = static_cast<size_t>(mt) * units * unit_lds_bytes(kind);
-    const size_t sums = kind == kF16 ? 0 : static_cast<size_t>(mt) * units * unit_elems(kind) / 32 * 4;
-    return act + sums;
-}
-
 GemvArgs args_of(const DeviceTensor &t) {
     GemvArgs a{};
     a.payload = t.payload;
@@ -586,48 +616,36 @@ GemvArgs args_of(const DeviceTensor &t) {
     a.tile_payload_bytes = t.tile_payload_bytes;
     a.tile_meta_bytes = t.tile_meta_bytes;
     a.rows = t.rows;
-    a.cols = t.cols;
     a.units = t.units;
     a.lanes = t.lanes;
     a.rows_per_wave = t.rows_per_wave;
     a.slots = t.slots;
+    a.image_bytes = static_cast<uint32_t>(image_bytes(t.kind, t.units));
     return a;
+}
+
+constexpr int kUplWidths[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+
+bool set_units(DeviceTensor &t) {
+    if (t.kind == kHvsq2) t.units = (t.cols + 255u) / 256u;
+    else if (t.kind == kQ4_0) t.units = ((t.cols + 31u) / 32u + 3u) / 4u;
+    else if (t.kind == kF16) t.units = (t.cols + 31u) / 32u;
+    else return false;
+    t.chunks = 4;
+    return true;
 }
 
 }  // namespace
 
-bool layout_tensor(DeviceTensor &t) {
-    if (t.kind == kHvsq2) {
-        t.units = (t.cols + 255u) / 256u;
-        t.chunks = 4;
-    } else if (t.kind == kQ4_0) {
-        t.units = ((t.cols + 31u) / 32u + 3u) / 4u;
-        t.chunks = 4;
-    } else if (t.kind == kF16) {
-        t.units = (t.cols + 7u) / 8u;
-        t.chunks = 1;
-    } else {
-        return false;
-    }
-    static const int kUpl[] = {1, 2, 3, 4, 6, 8};
-    double best = -1.0;
-    t.upl = 0;
-    for (int upl : kUpl) {
-        const int L = static_cast<int>((t.units + upl - 1) / upl);
-        if (L > kWaveSize) continue;
-        const int rpw = kWaveSize / L;
-        // fraction of lane-unit slots doing real work
-        const double eff = static_cast<double>(t.units) / (static_cast<double>(L) * upl) *
-                           (static_cast<double>(rpw) * L) / kWaveSize;
-        if (eff > best + 0.04) {
-            best = eff;
-            t.upl = upl;
-            t.lanes = L;
-            t.rows_per_wave = rpw;
-        }
-    }
-    if (t.upl == 0) return false;
-    t.slots = t.lanes * t.rows_per_wave;
+bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
+    if (!set_units(t)) return false;
+    bool upl_ok = false;
+    for (int w : kUplWidths) upl_ok |= static_cast<uint32_t>(w) == upl;
+    if (!upl_ok || lanes == 0 || lanes > 64 || (lanes & (lanes - 1)) || lanes * upl < t.units) return false;
+    t.lanes = lanes;
+    t.upl = upl;
+    t.rows_per_wave = kWaveSize / lanes;
+    t.slots = kWaveSize;
     t.tiles = (t.rows + t.rows_per_wave - 1) / t.rows_per_wave;
     // whole workgroups of tiles, so a workgroup never reads past the end
     t.tiles = (t.tiles + kGemvWaves - 1) / kGemvWaves * kGemvWaves;
@@ -639,14 +657,40 @@ bool layout_tensor(DeviceTensor &t) {
     return true;
 }
 
+// Lane plan: the power-of-two lane count whose unit slots waste least,
+// preferring more lanes per row (more waves, shorter per-lane chains)
+// among plans within 3% of the best.
+bool layout_tensor(DeviceTensor &t) {
+    if (!set_units(t)) return false;
+    double best = -1.0;
+    uint32_t best_l = 0, best_u = 0;
+    for (uint32_t L = 64; L >= 1; L /= 2) {
+        uint32_t upl = 0;
+        for (int w : kUplWidths)
+            if (static_cast<uint32_t>(w) * L >= t.units) {
+                upl = static_cast<uint32_t>(w);
+                break;
+            }
+        if (upl == 0) continue;
+        const double eff = static_cast<double>(t.units) / (static_cast<double>(L) * upl);
+        if (eff > best + 0.03) {
+            best = eff;
+            best_l = L;
+            best_u = upl;
+        }
+    }
+    return best_l && layout_tensor_with(t, best_l, best_u);
+}
+
 GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
     GemvPlan p;
     int mt = 1;
     const int want = std::min(batch, kMaxTokensPerLaunch);
     while (mt < want) mt *= 2;
-    while (mt > 1 && lds_for(t.kind, t.units, mt) > kGemvLdsLimit) mt /= 2;
+    const size_t ib = image_bytes(t.kind, t.units);
+    while (mt > 1 && ib * mt > kGemvLdsLimit) mt /= 2;
     p.tokens = mt;
-    p.lds_bytes = lds_for(t.kind, t.units, mt);
+    p.lds_bytes = ib * mt;
     p.grid = static_cast<int>(t.tiles / kGemvWaves);
     return p;
 }
@@ -674,35 +718,64 @@ hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging, hipStrea
     return hipGetLastError();
 }
 
+hipError_t launch_image(const DeviceTensor &t, const void *x, uint32_t batch, uint32_t x_stride,
+                        uint8_t *image, uint32_t image_stride, hipStream_t stream) {
+    if (t.kind == kF16) {
+        const dim3 grid((t.units * 4 + 255) / 256, batch);
+        hipLaunchKernelGGL(image_from_f32_kernel, grid, dim3(256), 0, stream, static_cast<const float *>(x),
+                           x_stride, t.cols, t.units, image, image_stride);
+    } else {
+        const uint32_t nblk = t.units * unit_elems(t.kind) / 32;
+        const dim3 grid((nblk + 255) / 256, batch);
+        if (t.kind == kHvsq2)
+            hipLaunchKernelGGL(image_from_int8_kernel<kHvsq2>, grid, dim3(256), 0, stream,
+                               static_cast<const int8_t *>(x), x_stride, t.cols, t.units, image, image_stride);
+        else
+            hipLaunchKernelGGL(image_from_int8_kernel<kQ4_0>, grid, dim3(256), 0, stream,
+                               static_cast<const int8_t *>(x), x_stride, t.cols, t.units, image, image_stride);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_image(const DeviceTensor &t, const float *x, uint32_t batch, uint32_t x_stride,
+                                 uint8_t *image, uint32_t image_stride, float *scales, int8_t *q8,
+                                 uint32_t q8_stride, hipStream_t stream) {
+    if (t.kind == kHvsq2)
+        hipLaunchKernelGGL(quantize_image_kernel<kHvsq2>, dim3(batch), dim3(256), 0, stream, x, t.cols, x_stride,
+                           t.units, image, image_stride, scales, q8, q8_stride);
+    else if (t.kind == kQ4_0)
+        hipLaunchKernelGGL(quantize_image_kernel<kQ4_0>, dim3(batch), dim3(256), 0, stream, x, t.cols, x_stride,
+                           t.units, image, image_stride, scales, q8, q8_stride);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
     const DeviceTensor &t = *g.tensor;
     GemvArgs args = args_of(t);
-    args.input_stride = g.input_stride;
     args.output_stride = g.output_stride;
+    args.image = static_cast<const uint8_t *>(g.image);
+    args.image_stride = g.image_stride;
 
     if (g.debug_sums) {
         if (t.kind == kF16) return hipErrorInvalidValue;
-        args.input = g.input;
-        const size_t lds = static_cast<size_t>(t.units) * unit_lds_bytes(t.kind) +
-                           static_cast<size_t>(t.units) * unit_elems(t.kind) / 32 * 4;
-        if (lds > kGemvLdsLimit) return hipErrorInvalidValue;
         const size_t n = static_cast<size_t>(t.rows) * t.units;
         const uint32_t out_row = t.kind == kHvsq2 ? t.units * 8 : (t.cols + 31) / 32;
         if (t.kind == kHvsq2)
             hipLaunchKernelGGL(dump_kernel<kHvsq2>, dim3((n + kGemvThreads - 1) / kGemvThreads),
-                               dim3(kGemvThreads), lds, stream, args, g.debug_sums, out_row);
+                               dim3(kGemvThreads), 0, stream, args, g.debug_sums, out_row);
         else
             hipLaunchKernelGGL(dump_kernel<kQ4_0>, dim3((n + kGemvThreads - 1) / kGemvThreads),
-                               dim3(kGemvThreads), lds, stream, args, g.debug_sums, out_row);
+                               dim3(kGemvThreads), 0, stream, args, g.debug_sums, out_row);
         return hipGetLastError();
     }
 
     const GemvPlan p = plan_gemv(t, static_cast<int>(g.batch));
     if (p.tokens == 0 || p.lds_bytes > kGemvLdsLimit) return hipErrorInvalidValue;
-    const size_t elem = t.kind == kF16 ? 4 : 1;
     for (uint32_t t0 = 0; t0 < g.batch; t0 += p.tokens) {
         args.ntok = std::min<uint32_t>(p.tokens, g.batch - t0);
-        args.input = static_cast<const uint8_t *>(g.input) + static_cast<size_t>(t0) * g.input_stride * elem;
+        args.image = static_cast<const uint8_t *>(g.image) + static_cast<size_t>(t0) * g.image_stride;
         args.scales = g.scales ? g.scales + t0 : nullptr;
         args.scale = g.scale;
         args.output = g.output + static_cast<size_t>(t0) * g.output_stride;
@@ -713,13 +786,6 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
-}
-
-hipError_t launch_quantize_tokens(const float *x, int M, int K, int x_stride, int8_t *q8,
-                                  int out_stride, float *scales, hipStream_t stream) {
-    hipLaunchKernelGGL(quantize_tokens_kernel, dim3(M), dim3(256), 0, stream, x, K, x_stride, q8,
-                       out_stride, scales);
-    return hipGetLastError();
 }
 
 }  // namespace qwn

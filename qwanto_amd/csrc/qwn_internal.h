@@ -3,9 +3,11 @@
 // Device layouts (chosen at upload; the ABI keeps them private).
 //
 // Every GEMV launch maps a matrix onto waves the same way: a row is split
-// across `lanes` lanes, each lane owning `upl` units (strided by `lanes`),
-// and a wave holds `rows_per_wave` row groups.  A "unit" is one HyperVSQ-2
-// block (256 weights), four Q4_0 blocks (128 weights) or eight F16 weights.
+// across `lanes` lanes (a power of two, so the row sum is a DPP reduction),
+// each lane owning `upl` units (strided by `lanes`), and a wave holds
+// 64/lanes row groups.  A "unit" is one HyperVSQ-2 block (256 weights),
+// four Q4_0 blocks (128 weights) or 32 F16 weights -- 64 payload bytes in
+// four 16-byte chunks for every kind.
 // Weights are stored wave tile by wave tile in exactly the order the lanes
 // load them, so every load instruction of a wave reads one contiguous span
 // (slots*16 bytes):
@@ -20,7 +22,7 @@
 //               reference kernels never read them either)
 //   Q4_0:       chunk q = the 16 nibble bytes of block 4u+q; meta = the
 //               four fp16 block scales (zero for padding blocks)
-//   F16:        one chunk of eight halves, no meta
+//   F16:        chunk q = halves 8q..8q+7 of the unit, no meta
 // Padding slots (units past the row end, rows past the matrix) are zero.
 #pragma once
 
@@ -43,10 +45,10 @@ constexpr size_t kGemvLdsLimit = 64 * 1024;
 // (activation bytes plus 16 bytes of padding so that lanes reading
 // consecutive units hit different LDS banks).
 __host__ __device__ constexpr int unit_elems(int kind) {
-    return kind == kHvsq2 ? 256 : (kind == kQ4_0 ? 128 : 8);
+    return kind == kHvsq2 ? 256 : (kind == kQ4_0 ? 128 : 32);
 }
 __host__ __device__ constexpr int unit_lds_bytes(int kind) {
-    return kind == kHvsq2 ? 272 : (kind == kQ4_0 ? 144 : 32);
+    return kind == kHvsq2 ? 272 : 144;
 }
 
 struct DeviceTensor {
@@ -79,6 +81,9 @@ struct GemvPlan {
 // Fills units/lanes/upl/rows_per_wave/slots/chunks/tiles and the tile sizes
 // of a tensor whose kind/rows/cols are set; false if no plan fits.
 bool layout_tensor(DeviceTensor &t);
+// Same with a forced lane plan (lanes a power of two <= 64, upl one of the
+// compiled widths); false if it does not cover the row.
+bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl);
 
 GemvPlan plan_gemv(const DeviceTensor &t, int batch);
 
@@ -87,25 +92,36 @@ GemvPlan plan_gemv(const DeviceTensor &t, int batch);
 hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging,
                          hipStream_t stream);
 
+// Bytes of one token's activation image for a tensor kind / unit count
+// (the LDS layout the GEMV reads, padded to 16 bytes).
+size_t image_bytes(int kind, uint32_t units);
+
+// Build images from int8 tokens (HyperVSQ-2, Q4_0) or fp32 tokens (F16):
+// x [batch][x_stride] elements -> image [batch][image_stride bytes].
+hipError_t launch_image(const DeviceTensor &t, const void *x, uint32_t batch, uint32_t x_stride,
+                        uint8_t *image, uint32_t image_stride, hipStream_t stream);
+
+// Per-token int8 quantization (c/qwanto_kernels.c:354-433) fused with the
+// image build: fp32 x [batch][x_stride] -> scales [batch], image, and the
+// int8 tokens q8 [batch][q8_stride] when q8 is not null.  With a null
+// image only the int8 tokens are produced (t gives the padding width).
+hipError_t launch_quantize_image(const DeviceTensor &t, const float *x, uint32_t batch, uint32_t x_stride,
+                                 uint8_t *image, uint32_t image_stride, float *scales, int8_t *q8,
+                                 uint32_t q8_stride, hipStream_t stream);
+
 struct GemvLaunch {
     const DeviceTensor *tensor;
-    const void *input;        // int8 [batch][input_stride] or fp32 for F16
+    const void *image;        // activation images [batch][image_stride]
+    uint32_t image_stride;    // bytes
     const float *scales;      // per-token scales (null -> scalar `scale`)
     float scale;
     float *output;            // fp32 [batch][output_stride]
     uint32_t batch;
-    uint32_t input_stride;    // elements
     uint32_t output_stride;   // elements
-    int32_t *debug_sums;      // non-null: dump integer sums instead
+    int32_t *debug_sums;      // non-null: dump integer sums of token 0 instead
 };
 
 hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream);
-
-// Per-token quantization on the device (c/qwanto_kernels.c:354-433):
-// x fp32 [M][K] -> q8 [M][out_stride] zero padded, scales [M].
-hipError_t launch_quantize_tokens(const float *x, int M, int K, int x_stride,
-                                  int8_t *q8, int out_stride, float *scales,
-                                  hipStream_t stream);
 
 // ---- Q8 KV cache ------------------------------------------------------
 struct KvCache {

@@ -5,7 +5,8 @@
 // a memory budget, synchronous host-pointer GEMV/GEMM and Q8-KV calls,
 // cumulative telemetry copied out on every call, one process-wide last
 // error string.  Different machinery: weights are repacked on upload into
-// 16-byte aligned planes, host buffers are staged through pinned memory,
+// the wave-tile layout of qwn_internal.h, activations are turned into an
+// activation image on the device, host buffers are staged through pinned memory,
 // every call runs on the context's own non-blocking stream, and each
 // context has its own lock.
 #include "qwn_cuda_abi.h"
@@ -106,7 +107,7 @@ struct Context {
     hipStream_t stream = nullptr;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     PinnedBuffer host_in, host_out;
-    DeviceBuffer dev_in, dev_out, dev_scales, dev_work;
+    DeviceBuffer dev_in, dev_out, dev_scales, dev_work, dev_img;
     std::vector<ResidentTensor *> tensors;
     std::vector<ResidentKv *> caches;
     QwnCudaTelemetry telemetry{};
@@ -190,11 +191,14 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     const size_t in_bytes = static_cast<size_t>(r->batch) * dev_stride * elem;
     const size_t scale_bytes = static_cast<size_t>(r->batch) * sizeof(float);
     const size_t out_bytes = static_cast<size_t>(r->batch) * r->rows * sizeof(float);
+    const uint32_t img_stride = static_cast<uint32_t>(qwn::image_bytes(t.kind, t.units));
+    const size_t img_bytes = static_cast<size_t>(r->batch) * img_stride;
     if ((e = ctx->host_in.ensure(in_bytes + scale_bytes)) != hipSuccess ||
         (e = ctx->host_out.ensure(out_bytes)) != hipSuccess ||
         (e = ctx->dev_in.ensure(in_bytes)) != hipSuccess ||
         (e = ctx->dev_scales.ensure(scale_bytes)) != hipSuccess ||
-        (e = ctx->dev_out.ensure(out_bytes)) != hipSuccess)
+        (e = ctx->dev_out.ensure(out_bytes)) != hipSuccess ||
+        (e = ctx->dev_img.ensure(img_bytes)) != hipSuccess)
         return hip_fail("GEMV workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
 
     const auto t_transfer = std::chrono::steady_clock::now();
@@ -217,14 +221,17 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
 
     qwn::GemvLaunch g{};
     g.tensor = &t;
-    g.input = ctx->dev_in.ptr;
+    g.image = ctx->dev_img.ptr;
+    g.image_stride = img_stride;
     g.scales = static_cast<const float *>(ctx->dev_scales.ptr);
     g.scale = r->input_scale;
     g.output = static_cast<float *>(ctx->dev_out.ptr);
     g.batch = r->batch;
-    g.input_stride = dev_stride;
     g.output_stride = r->rows;
     (void)hipEventRecord(ctx->ev_start, ctx->stream);
+    if ((e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
+                               img_stride, ctx->stream)) != hipSuccess)
+        return hip_fail("activation image launch", e);
     if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
     (void)hipEventRecord(ctx->ev_end, ctx->stream);
     if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,
@@ -242,7 +249,7 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
 
     QwnCudaTelemetry &tm = ctx->telemetry;
     tm.gpu_matmul_count++;
-    tm.gpu_kernel_launch_count += (r->batch + qwn::kMaxTokensPerLaunch - 1) / qwn::kMaxTokensPerLaunch;
+    tm.gpu_kernel_launch_count += 1 + (r->batch + qwn::kMaxTokensPerLaunch - 1) / qwn::kMaxTokensPerLaunch;
     tm.gpu_projection_count++;
     tm.gpu_kernel_ms += kernel_ms;
     tm.gpu_transfer_ms += transfer_ms;
@@ -398,6 +405,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *handle) 
         ctx->dev_out.release();
         ctx->dev_scales.release();
         ctx->dev_work.release();
+        ctx->dev_img.release();
         (void)hipEventDestroy(ctx->ev_start);
         (void)hipEventDestroy(ctx->ev_end);
         (void)hipStreamDestroy(ctx->stream);
@@ -796,34 +804,91 @@ QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHi
     return QWN_CUDA_STATUS_OK;
 }
 
-QWN_CUDA_ABI_API int qwn_hip_ext_gemm_device(QwnCudaContextHandle *handle, const QwnCudaGemmRequest *r,
-                                             void *stream) {
+QWN_CUDA_ABI_API uint64_t qwn_hip_ext_activation_image_bytes(const QwnCudaTensorHandle *h) {
+    if (!h || !header_ok(*h) || !h->opaque) return 0;
+    const DeviceTensor &t = static_cast<const ResidentTensor *>(h->opaque)->t;
+    return qwn::image_bytes(t.kind, t.units);
+}
+
+namespace {
+// Tensor of a handle issued by this context (lock held by the caller).
+ResidentTensor *ext_tensor(Context *ctx, const QwnCudaTensorHandle *h) {
+    return h ? tensor_of(ctx, *h) : nullptr;
+}
+}  // namespace
+
+QWN_CUDA_ABI_API int qwn_hip_ext_prepare_image_device(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                      const void *x, uint32_t batch, uint32_t x_stride,
+                                                      void *image, uint32_t image_stride, void *stream) {
     Context *ctx = context_of(handle);
-    if (!ctx) {
-        set_error("invalid context handle");
+    if (!ctx || !x || !image || batch == 0) {
+        set_error("invalid image request");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
-    ResidentTensor *rt = check_request(ctx, r);
-    if (!rt) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
-    const size_t elem = rt->t.kind == qwn::kF16 ? 4 : 1;
-    const uint32_t in_stride = r->input_stride ? r->input_stride : r->cols;
-    if ((reinterpret_cast<uintptr_t>(r->input_q8) & 15u) || ((in_stride * elem) & 15u)) {
-        set_error("device activations must be 16-byte aligned (pointer and row stride)");
+    ResidentTensor *rt = ext_tensor(ctx, th);
+    if (!rt || x_stride < rt->t.cols || image_stride < qwn::image_bytes(rt->t.kind, rt->t.units) ||
+        (image_stride & 15u) || (reinterpret_cast<uintptr_t>(image) & 15u)) {
+        set_error("image request does not fit the tensor (strides, 16-byte alignment)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_image(rt->t, x, batch, x_stride, static_cast<uint8_t *>(image), image_stride, s);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("image launch", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_quantize_image_device(QwnCudaContextHandle *handle,
+                                                       const QwnCudaTensorHandle *th, const float *x,
+                                                       uint32_t batch, uint32_t x_stride, void *image,
+                                                       uint32_t image_stride, float *scales, int8_t *q8,
+                                                       uint32_t q8_stride, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !x || !image || !scales || batch == 0) {
+        set_error("invalid quantize-image request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = ext_tensor(ctx, th);
+    if (!rt || rt->t.kind == qwn::kF16 || x_stride < rt->t.cols ||
+        image_stride < qwn::image_bytes(rt->t.kind, rt->t.units) || (image_stride & 15u) ||
+        (reinterpret_cast<uintptr_t>(image) & 15u) || (q8 && q8_stride < rt->t.cols)) {
+        set_error("quantize-image request does not fit the tensor");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_quantize_image(rt->t, x, batch, x_stride, static_cast<uint8_t *>(image),
+                                              image_stride, scales, q8, q8_stride, s);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("quantize-image launch", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                   const void *image, uint32_t image_stride,
+                                                   const float *scales, float scale, float *output,
+                                                   uint32_t batch, uint32_t output_stride, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !image || !output || batch == 0) {
+        set_error("invalid image GEMV request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = ext_tensor(ctx, th);
+    if (!rt || image_stride < qwn::image_bytes(rt->t.kind, rt->t.units) || (image_stride & 15u) ||
+        (reinterpret_cast<uintptr_t>(image) & 15u) || (output_stride && output_stride < rt->t.rows)) {
+        set_error("image GEMV request does not fit the tensor");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     qwn::GemvLaunch g{};
     g.tensor = &rt->t;
-    g.input = r->input_q8;
-    g.scales = r->input_scales;
-    g.scale = r->input_scale;
-    g.output = r->output;
-    g.batch = r->batch;
-    g.input_stride = in_stride;
-    g.output_stride = r->output_stride ? r->output_stride : r->rows;
+    g.image = image;
+    g.image_stride = image_stride;
+    g.scales = scales;
+    g.scale = scale;
+    g.output = output;
+    g.batch = batch;
+    g.output_stride = output_stride ? output_stride : rt->t.rows;
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
     hipError_t e = qwn::launch_gemv(g, s);
-    if (e != hipSuccess) return hip_fail("device GEMV launch", e);
+    if (e != hipSuccess) return hip_fail("image GEMV launch", e);
     ctx->telemetry.gpu_matmul_count++;
     ctx->telemetry.gpu_kernel_launch_count++;
     ctx->telemetry.gpu_projection_count++;
@@ -839,9 +904,11 @@ QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *handle, c
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
-    hipError_t e = qwn::launch_quantize_tokens(x, static_cast<int>(batch), static_cast<int>(cols),
-                                               static_cast<int>(x_stride), q8, static_cast<int>(q8_stride),
-                                               scales, s);
+    DeviceTensor shape;  // only the padding width matters without an image
+    shape.kind = qwn::kHvsq2;
+    shape.cols = cols;
+    shape.units = (cols + 255u) / 256u;
+    hipError_t e = qwn::launch_quantize_image(shape, x, batch, x_stride, nullptr, 0, scales, q8, q8_stride, s);
     return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("quantize launch", e);
 }
 
@@ -931,17 +998,21 @@ QWN_CUDA_ABI_API int qwn_hip_ext_debug_int_sums(QwnCudaContextHandle *handle, co
     }
     hipError_t e = hipSetDevice(ctx->device);
     const uint32_t stride = (t.cols + 255u) & ~255u;
-    void *dx = nullptr, *dout = nullptr;
+    const size_t img = qwn::image_bytes(t.kind, t.units);
+    void *dx = nullptr, *dimg = nullptr, *dout = nullptr;
     if (e == hipSuccess) e = hipMalloc(&dx, stride);
+    if (e == hipSuccess) e = hipMalloc(&dimg, img);
     if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(int32_t));
     if (e == hipSuccess) e = hipMemsetAsync(dx, 0, stride, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(dx, host_q8, t.cols, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = qwn::launch_image(t, dx, 1, stride, static_cast<uint8_t *>(dimg), static_cast<uint32_t>(img), ctx->stream);
     if (e == hipSuccess) {
         qwn::GemvLaunch g{};
         g.tensor = &t;
-        g.input = dx;
+        g.image = dimg;
+        g.image_stride = static_cast<uint32_t>(img);
         g.batch = 1;
-        g.input_stride = stride;
         g.debug_sums = static_cast<int32_t *>(dout);
         e = qwn::launch_gemv(g, ctx->stream);
     }
@@ -949,6 +1020,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_debug_int_sums(QwnCudaContextHandle *handle, co
         e = hipMemcpyAsync(host_out, dout, n * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (dx) (void)hipFree(dx);
+    if (dimg) (void)hipFree(dimg);
     if (dout) (void)hipFree(dout);
     return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("debug integer sums", e);
 }

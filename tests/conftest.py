@@ -32,6 +32,10 @@ def ref_lib():
 
 @pytest.fixture(scope="session")
 def hip_lib():
+    # torch first: its bundled HIP runtime has the same soname as the one the
+    # library links, so loading torch first makes both share one runtime and
+    # torch device tensors usable as the library's device buffers.
+    import torch  # noqa: F401
     from qwanto_amd import abi
     return abi.load()
 

@@ -173,3 +173,84 @@ def test_device_enumeration(hip_lib):
     d = devs[0]
     assert d.total_vram_bytes > 0 and d.free_vram_bytes > 0
     assert b"gfx" in d.name
+
+
+@pytest.mark.parametrize("kind,K,M", [("hvsq2", 2560, 1), ("hvsq2", 9728, 3), ("hvsq2", 300, 16),
+                                      ("q4_0", 1536, 1), ("q4_0", 8960, 5), ("q4_0", 100, 16)])
+def test_device_image_path(gpu_ctx, oracle_lib, kind, K, M):
+    """Device pointers end to end: fp32 x -> quantize_image_device (scales,
+    int8 tokens, image) -> gemm_image_device for two tensors of the same width
+    sharing the one image.  Scales and int8 tokens bit-exact against the
+    oracle's quantizer, outputs against the oracle GEMV."""
+    import torch
+    rng = np.random.default_rng(K * 31 + M)
+    x = synth.activations(rng, M, K)
+    q8_ref, xs_ref, sums = quantize(oracle_lib, x)
+    dev = torch.device("cuda:0")
+    rows = (129, 64)
+    ws = [synth.weights(kind, rng, n, K) for n in rows]
+    hs = [gpu_ctx.upload(w, kind, n, K) for w, n in zip(ws, rows)]
+    try:
+        ib = gpu_ctx.image_bytes(hs[0])
+        assert ib == gpu_ctx.image_bytes(hs[1]) and ib % 16 == 0
+        xs_stride = (K + 3) // 4 * 4
+        xd = torch.zeros(M, xs_stride, dtype=torch.float32)
+        xd[:, :K] = torch.from_numpy(x)
+        xd = xd.to(dev)
+        q8_stride = q8_ref.shape[1]
+        q8 = torch.full((M, q8_stride), 77, dtype=torch.int8, device=dev)
+        sc = torch.zeros(M, dtype=torch.float32, device=dev)
+        img = torch.zeros(M, ib, dtype=torch.uint8, device=dev)
+        s = torch.cuda.current_stream().cuda_stream
+        gpu_ctx.quantize_image_device(hs[0], xd.data_ptr(), M, xs_stride, img.data_ptr(), ib,
+                                      sc.data_ptr(), q8.data_ptr(), q8_stride, stream=s)
+        torch.cuda.synchronize()
+        assert np.array_equal(sc.cpu().numpy(), xs_ref)
+        assert np.array_equal(q8.cpu().numpy(), q8_ref)
+        # an image prepared from the int8 tokens is the same image
+        img2 = torch.zeros_like(img)
+        gpu_ctx.prepare_image_device(hs[1], q8.data_ptr(), M, q8_stride, img2.data_ptr(), ib,
+                                     stream=s)
+        torch.cuda.synchronize()
+        assert torch.equal(img, img2)
+        for h, w, n in zip(hs, ws, rows):
+            y = torch.full((M, n + 3), float("nan"), dtype=torch.float32, device=dev)
+            gpu_ctx.gemm_image_device(h, img.data_ptr(), ib, y.data_ptr(), M, n + 3,
+                                      scales_ptr=sc.data_ptr(), stream=s)
+            torch.cuda.synchronize()
+            yh = y.cpu().numpy()
+            assert np.isnan(yh[:, n:]).all(), "wrote past the row end"
+            for t in range(M):
+                if kind == "hvsq2":
+                    ref = oracle_lib.gemv_hvsq2(w, q8_ref[t], sums[t], float(xs_ref[t]), K, n)
+                else:
+                    ref = oracle_lib.gemv_q4_0_q8(w, q8_ref[t], float(xs_ref[t]), K, n)
+                ok, worst = gemv_close(yh[t, :n], ref)
+                assert ok, f"{kind} K={K} rows={n} token {t}: worst {worst:.3g}"
+    finally:
+        for h in hs:
+            gpu_ctx.release(h)
+
+
+def test_device_image_f16(gpu_ctx, oracle_lib):
+    import torch
+    rng = np.random.default_rng(5)
+    N, K, M = 300, 1000, 4
+    w = synth.f16_weights(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    h = gpu_ctx.upload(w, "f16", N, K)
+    try:
+        ib = gpu_ctx.image_bytes(h)
+        dev = torch.device("cuda:0")
+        xd = torch.from_numpy(x).to(dev)
+        img = torch.zeros(M, ib, dtype=torch.uint8, device=dev)
+        y = torch.zeros(M, N, dtype=torch.float32, device=dev)
+        s = torch.cuda.current_stream().cuda_stream
+        gpu_ctx.prepare_image_device(h, xd.data_ptr(), M, K, img.data_ptr(), ib, stream=s)
+        gpu_ctx.gemm_image_device(h, img.data_ptr(), ib, y.data_ptr(), M, N, stream=s)
+        torch.cuda.synchronize()
+        ref = oracle_lib.matmul_f16(w, x)
+        ok, worst = gemv_close(y.cpu().numpy(), ref)
+        assert ok, f"F16 image path: worst {worst:.3g}"
+    finally:
+        gpu_ctx.release(h)
