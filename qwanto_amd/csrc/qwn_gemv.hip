@@ -312,7 +312,6 @@ struct GemvArgs {
     uint32_t units;
     uint32_t lanes;
     uint32_t rows_per_wave;
-    uint32_t slots;
     uint32_t ntok;
     uint32_t image_stride;
     uint32_t image_bytes;
@@ -332,7 +331,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     const uint32_t row = tile * a.rows_per_wave + grp;
     const bool active = grp < a.rows_per_wave && row < a.rows;
 
-    // 0. Activation images -> LDS (direct loads, issued first).
+    // 0. Token scales (uniform loads, needed only at the very end but
+    //    issued first so their latency hides under the weight stream), then
+    //    the activation images -> LDS (direct loads).
+    float tok_scale[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tok_scale[t] = a.scales ? a.scales[t < static_cast<int>(a.ntok) ? t : 0] : a.scale;
     issue_image_copy(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -341,31 +345,37 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     //    the loads stay one unconditional burst.
     const uint8_t *tile_p = a.payload + tile * a.tile_payload_bytes;
     const uint8_t *tile_m = a.meta + tile * a.tile_meta_bytes;
-    const uint8_t *tp = tile_p + lane * 16;
-    const uint8_t *tm = tile_m + lane * 8;
+    // Unit slot i holds units i*L + j, n = min(L, units - i*L) of them,
+    // stored compactly (qwn_internal.h).
+    const size_t R = a.rows_per_wave;
     uint2 met[UPL];
     uint4 pay[UPL][CH];
 #pragma unroll
     for (int i = 0; i < UPL; ++i) {
-        const bool ok = active && j + i * L < a.units;
+        const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
+        const bool ok = active && j < n;
         if (KIND != kF16)
             met[i] = *reinterpret_cast<const uint2 *>(
-                ok ? tm + static_cast<size_t>(i) * a.slots * 8 : tile_m);
+                ok ? tile_m + 8 * R * L * i + (grp * n + j) * 8 : tile_m);
     }
 #pragma unroll
     for (int i = 0; i < UPL; ++i) {
-        const bool ok = active && j + i * L < a.units;
+        const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
+        const bool ok = active && j < n;
+        const uint8_t *base = tile_p + 64 * R * L * i + (grp * n + j) * 16;
 #pragma unroll
         for (int q = 0; q < CH; ++q)
-            pay[i][q] = *reinterpret_cast<const uint4 *>(
-                ok ? tp + static_cast<size_t>(i * CH + q) * a.slots * 16 : tile_p);
+            pay[i][q] = *reinterpret_cast<const uint4 *>(ok ? base + q * R * n * 16 : tile_p);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. Wait for the image loads only (vmcnt counts in issue order), then
-    //    for every wave's share of the copy.
+    // 2. Wait for this wave's image loads only (vector memory loads retire
+    //    in issue order), then for every wave's share of the copy.  A bare
+    //    s_barrier: __syncthreads() would also wait for the weight loads.
     wait_vmcnt<(KIND == kF16 ? 4 : 5) * UPL>();
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
 
     // 3. Dot products.
     const uint32_t ib = a.image_bytes;
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
         for (int t = 0; t < MT; ++t) {
             if (static_cast<uint32_t>(t) >= a.ntok) break;
             float s = acc[t];
-            if (KIND != kF16) s *= a.scales ? a.scales[t] : a.scale;
+            if (KIND != kF16) s *= tok_scale[t];
             a.output[static_cast<size_t>(t) * a.output_stride + row] = s;
         }
     }
@@ -462,14 +472,16 @@ struct UnitAddr {
     size_t payload, meta;
 };
 __host__ __device__ inline UnitAddr unit_addr(uint32_t row, uint32_t u, uint32_t q, uint32_t lanes,
-                                              uint32_t rows_per_wave, uint32_t slots, uint32_t chunks,
-                                              size_t tile_payload, size_t tile_meta) {
+                                              uint32_t rows_per_wave, uint32_t units, size_t tile_payload,
+                                              size_t tile_meta) {
     const uint32_t tile = row / rows_per_wave, grp = row % rows_per_wave;
     const uint32_t i = u / lanes, jj = u % lanes;
-    const uint32_t slot = grp * lanes + jj;
+    const uint32_t n = units - i * lanes < lanes ? units - i * lanes : lanes;  // units in plane i
     UnitAddr r;
-    r.payload = tile * tile_payload + (static_cast<size_t>(i * chunks + q) * slots + slot) * 16;
-    r.meta = tile * tile_meta + (static_cast<size_t>(i) * slots + slot) * 8;
+    r.payload = tile * tile_payload + static_cast<size_t>(64) * rows_per_wave * lanes * i +
+                (static_cast<size_t>(q) * rows_per_wave * n + grp * n + jj) * 16;
+    r.meta = tile * tile_meta + static_cast<size_t>(8) * rows_per_wave * lanes * i +
+             (static_cast<size_t>(grp) * n + jj) * 8;
     return r;
 }
 
@@ -484,8 +496,8 @@ __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t 
     const uint32_t row = idx / a.units, u = idx % a.units;
     uint4 pay[4];
     for (uint32_t q = 0; q < 4; ++q) {
-        const UnitAddr ad = unit_addr(row, u, q, a.lanes, a.rows_per_wave, a.slots, 4,
-                                      a.tile_payload_bytes, a.tile_meta_bytes);
+        const UnitAddr ad = unit_addr(row, u, q, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
+                                      a.tile_meta_bytes);
         pay[q] = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
     }
     const uint8_t *img = a.image;
@@ -514,7 +526,7 @@ struct RepackArgs {
     const uint8_t *src;
     uint8_t *payload;
     uint8_t *meta;
-    uint32_t rows, cols, units, lanes, rows_per_wave, slots;
+    uint32_t rows, cols, units, lanes, rows_per_wave;
     size_t tile_payload, tile_meta;
 };
 
@@ -529,7 +541,7 @@ __global__ void repack_kernel(RepackArgs r) {
     const uint32_t row = idx / r.units, u = idx % r.units;
     UnitAddr ad[4];
     for (uint32_t q = 0; q < 4; ++q)
-        ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.slots, 4, r.tile_payload, r.tile_meta);
+        ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.units, r.tile_payload, r.tile_meta);
     if (KIND == kHvsq2) {
         const uint8_t *blk = r.src + idx * 74;  // [row][unit] blocks, unit == block
         for (uint32_t q = 0; q < 4; ++q) {
@@ -619,7 +631,6 @@ GemvArgs args_of(const DeviceTensor &t) {
     a.units = t.units;
     a.lanes = t.lanes;
     a.rows_per_wave = t.rows_per_wave;
-    a.slots = t.slots;
     a.image_bytes = static_cast<uint32_t>(image_bytes(t.kind, t.units));
     return a;
 }
@@ -645,41 +656,30 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     t.lanes = lanes;
     t.upl = upl;
     t.rows_per_wave = kWaveSize / lanes;
-    t.slots = kWaveSize;
     t.tiles = (t.rows + t.rows_per_wave - 1) / t.rows_per_wave;
     // whole workgroups of tiles, so a workgroup never reads past the end
     t.tiles = (t.tiles + kGemvWaves - 1) / kGemvWaves * kGemvWaves;
-    t.tile_payload_bytes = static_cast<size_t>(t.upl) * t.chunks * t.slots * 16;
-    t.tile_meta_bytes = t.kind == kF16 ? 0 : static_cast<size_t>(t.upl) * t.slots * 8;
+    // compact tiles: only real units are stored (idle lanes load nothing new)
+    t.tile_payload_bytes = static_cast<size_t>(t.rows_per_wave) * t.units * t.chunks * 16;
+    t.tile_meta_bytes = t.kind == kF16 ? 0 : static_cast<size_t>(t.rows_per_wave) * t.units * 8;
     const size_t payload = t.tile_payload_bytes * t.tiles;
     const size_t meta = t.tile_meta_bytes * t.tiles;
     t.device_bytes = ((payload + 255) & ~static_cast<size_t>(255)) + meta;
     return true;
 }
 
-// Lane plan: the power-of-two lane count whose unit slots waste least,
-// preferring more lanes per row (more waves, shorter per-lane chains)
-// among plans within 3% of the best.
+// Lane plan: one unit per lane where the row allows it (L = the power of
+// two covering the row, at most 64), so the post-load work per lane is
+// short and the grid is large; longer rows take more units per lane.
+// Idle lanes cost VALU slots but no memory traffic (compact tiles).
 bool layout_tensor(DeviceTensor &t) {
     if (!set_units(t)) return false;
-    double best = -1.0;
-    uint32_t best_l = 0, best_u = 0;
-    for (uint32_t L = 64; L >= 1; L /= 2) {
-        uint32_t upl = 0;
-        for (int w : kUplWidths)
-            if (static_cast<uint32_t>(w) * L >= t.units) {
-                upl = static_cast<uint32_t>(w);
-                break;
-            }
-        if (upl == 0) continue;
-        const double eff = static_cast<double>(t.units) / (static_cast<double>(L) * upl);
-        if (eff > best + 0.03) {
-            best = eff;
-            best_l = L;
-            best_u = upl;
-        }
-    }
-    return best_l && layout_tensor_with(t, best_l, best_u);
+    uint32_t L = 1;
+    while (L < t.units && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
+    const uint32_t need = (t.units + L - 1) / L;
+    for (int w : kUplWidths)
+        if (static_cast<uint32_t>(w) >= need) return layout_tensor_with(t, L, static_cast<uint32_t>(w));
+    return false;
 }
 
 GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
@@ -707,7 +707,6 @@ hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging, hipStrea
     r.units = t.units;
     r.lanes = t.lanes;
     r.rows_per_wave = t.rows_per_wave;
-    r.slots = t.slots;
     r.tile_payload = t.tile_payload_bytes;
     r.tile_meta = t.tile_meta_bytes;
     const size_t n = static_cast<size_t>(t.rows) * t.units;

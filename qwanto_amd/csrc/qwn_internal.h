@@ -3,18 +3,19 @@
 // Device layouts (chosen at upload; the ABI keeps them private).
 //
 // Every GEMV launch maps a matrix onto waves the same way: a row is split
-// across `lanes` lanes (a power of two, so the row sum is a DPP reduction),
-// each lane owning `upl` units (strided by `lanes`), and a wave holds
-// 64/lanes row groups.  A "unit" is one HyperVSQ-2 block (256 weights),
-// four Q4_0 blocks (128 weights) or 32 F16 weights -- 64 payload bytes in
-// four 16-byte chunks for every kind.
+// across `lanes` lanes L (a power of two, so the row sum is a DPP reduction),
+// each lane owning up to `upl` units (strided by L), and a wave holds
+// R = 64/L rows.  A "unit" is one HyperVSQ-2 block (256 weights), four Q4_0
+// blocks (128 weights) or 32 F16 weights -- 64 payload bytes in four
+// 16-byte chunks for every kind.
 // Weights are stored wave tile by wave tile in exactly the order the lanes
-// load them, so every load instruction of a wave reads one contiguous span
-// (slots*16 bytes):
+// load them, and only real units are stored, so every load instruction of a
+// wave reads one contiguous span with no padding:
 //
-//   tile t (rows t*rows_per_wave ...), slot s = group*lanes + lane (s < slots)
-//   payload: [tile][unit slot i < upl][chunk q < chunks][slot s][16 B]
-//   meta:    [tile][unit slot i < upl][slot s][8 B]
+//   tile t = rows t*R .. t*R+R-1; unit slot i holds units i*L + j (j < L),
+//   n_i = min(L, units - i*L) of them (the last slots may be partial/empty)
+//   payload: [tile][slot i][chunk q < 4][row g < R][j < n_i][16 B]
+//   meta:    [tile][slot i][row g < R][j < n_i][8 B]
 //
 //   HyperVSQ-2: chunk q = codes of octants 2q, 2q+1 (16 B); meta = fp16
 //               d_base, fp16 m_base, four bytes of octant multipliers (the
@@ -23,7 +24,7 @@
 //   Q4_0:       chunk q = the 16 nibble bytes of block 4u+q; meta = the
 //               four fp16 block scales (zero for padding blocks)
 //   F16:        chunk q = halves 8q..8q+7 of the unit, no meta
-// Padding slots (units past the row end, rows past the matrix) are zero.
+// Rows past the matrix end (the last tile) are stored as zeros.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -60,7 +61,6 @@ struct DeviceTensor {
     uint32_t lanes = 0;
     uint32_t upl = 0;
     uint32_t rows_per_wave = 0;
-    uint32_t slots = 0;          // lanes * rows_per_wave
     uint32_t chunks = 0;         // 16-byte payload chunks per unit
     uint32_t tiles = 0;
     size_t tile_payload_bytes = 0;
@@ -78,11 +78,11 @@ struct GemvPlan {
     size_t lds_bytes = 0;
 };
 
-// Fills units/lanes/upl/rows_per_wave/slots/chunks/tiles and the tile sizes
+// Fills units/lanes/upl/rows_per_wave/chunks/tiles and the tile sizes
 // of a tensor whose kind/rows/cols are set; false if no plan fits.
 bool layout_tensor(DeviceTensor &t);
 // Same with a forced lane plan (lanes a power of two <= 64, upl one of the
-// compiled widths); false if it does not cover the row.
+// compiled widths, lanes * upl >= units); false if it does not fit.
 bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl);
 
 GemvPlan plan_gemv(const DeviceTensor &t, int batch);
