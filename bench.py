@@ -41,6 +41,9 @@ def parse():
     p.add_argument("--q4", action="store_true", help="also sweep the Qwen2-1.5B Q4_0 shapes")
     p.add_argument("--only-gate", action="store_true",
                    help="profiling mode: launch only the gate projection sweep")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="profiling mode: a plain 64 MiB device copy, the reference point that "
+                        "scales the FETCH_SIZE / WRITE_SIZE counters to bytes")
     return p.parse_args()
 
 
@@ -190,6 +193,15 @@ def main():
     from qwanto_amd import abi, synth
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs the GPU (no CPU fallback)")
+    if args.copy_probe:
+        n = 64 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_mode": "copy", "bytes_read": n, "bytes_written": n}), flush=True)
+        return
     lib = abi.load()
     ctx = abi.Context(lib, device=0)
     t_setup = time.perf_counter()
