@@ -36,6 +36,75 @@ def ptr(a: np.ndarray, ctype):
     return a.ctypes.data_as(ctypes.POINTER(ctype))
 
 
+class QoModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("hidden", "intermediate", "layers", "heads",
+                                            "kv_heads", "head_dim", "vocab", "max_ctx")] + \
+               [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
+                ("proj_dtype", ctypes.c_int)]
+
+
+class QoModel(ctypes.Structure):
+    _fields_ = [("cfg", QoModelConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
+                ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p))]
+
+
+PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def model_struct(model: dict) -> tuple:
+    """ctypes view of a qwanto_amd.synth.decoder_model dict (the arrays stay
+    owned by the dict; keep it alive)."""
+    cfg = model["cfg"]
+    c = QoModelConfig(hidden=cfg["hidden"], intermediate=cfg["intermediate"], layers=cfg["layers"],
+                      heads=cfg["heads"], kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"],
+                      vocab=cfg["vocab"], max_ctx=cfg["max_ctx"], rope_theta=cfg["rope_theta"],
+                      rms_eps=cfg["rms_eps"], proj_dtype=2 if model["dtype"] == "q4_0" else 1)
+    L = cfg["layers"]
+    proj = (ctypes.c_void_p * (7 * L))(*[model["layers"][l][p].ctypes.data
+                                         for l in range(L) for p in PROJ_ORDER])
+    norms = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data
+                                          for l in range(L) for n in ("input_norm", "post_norm")])
+    m = QoModel(cfg=c, embed=model["embed"].ctypes.data, final_norm=model["final_norm"].ctypes.data,
+                proj=ctypes.cast(proj, ctypes.POINTER(ctypes.c_void_p)),
+                norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)))
+    return m, (proj, norms)
+
+
+class Decoder:
+    """The oracle decoder (qwn_oracle_decoder.c) over a synthetic model."""
+
+    def __init__(self, oracle: "Oracle", model: dict, threads: int = 0):
+        self.o, self.model = oracle, model
+        self.struct, self._keep = model_struct(model)
+        self.h = oracle.lib.qo_decoder_create(ctypes.byref(self.struct), threads)
+        if not self.h:
+            raise MemoryError("qo_decoder_create failed")
+        self.vocab = model["cfg"]["vocab"]
+
+    def close(self):
+        if self.h:
+            self.o.lib.qo_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def forward(self, token: int) -> np.ndarray:
+        logits = np.empty(self.vocab, dtype=np.float32)
+        rc = self.o.lib.qo_decoder_forward(self.h, int(token), ptr(logits, ctypes.c_float))
+        assert rc == 0, "oracle forward failed"
+        return logits
+
+    def generate(self, prompt: np.ndarray, max_new: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        tokens = np.zeros(max_new, dtype=np.int32)
+        margins = np.zeros(max_new, dtype=np.float32)
+        rc = self.o.lib.qo_decoder_generate(self.h, ptr(prompt, ctypes.c_int32), prompt.size, max_new,
+                                            ptr(tokens, ctypes.c_int32), ptr(margins, ctypes.c_float))
+        assert rc == max_new, "oracle generate failed"
+        return tokens, margins
+
+
 class Oracle:
     """Typed numpy front end of liboracle.so."""
 
@@ -71,6 +140,34 @@ class Oracle:
         lib.qo_q8_attention.argtypes = [_c_f32p, _c_i8p, _c_i8p, _c_f32p, _c_f32p,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_float, _c_f32p, ctypes.c_int]
+        lib.qo_rmsnorm.argtypes = [_c_f32p, _c_f32p, _c_f32p, ctypes.c_int, ctypes.c_float]
+        lib.qo_rope_table.argtypes = [_c_f32p, _c_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        lib.qo_rope_apply.argtypes = [_c_f32p, ctypes.c_int, ctypes.c_int, _c_f32p, _c_f32p]
+        lib.qo_argmax.argtypes = [_c_f32p, ctypes.c_int]
+        lib.qo_decoder_create.argtypes = [ctypes.POINTER(QoModel), ctypes.c_int]
+        lib.qo_decoder_create.restype = ctypes.c_void_p
+        lib.qo_decoder_free.argtypes = [ctypes.c_void_p]
+        lib.qo_decoder_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, _c_f32p]
+        lib.qo_decoder_generate.argtypes = [ctypes.c_void_p, _c_i32p, ctypes.c_int, ctypes.c_int,
+                                            _c_i32p, _c_f32p]
+
+    # -- decoder pieces -------------------------------------------------
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        self.lib.qo_rmsnorm(ptr(out, ctypes.c_float), ptr(x, ctypes.c_float), ptr(w, ctypes.c_float),
+                            x.size, eps)
+        return out
+
+    def rope_table(self, max_ctx: int, half: int, theta: float):
+        c = np.empty((max_ctx, half), dtype=np.float32)
+        s = np.empty((max_ctx, half), dtype=np.float32)
+        self.lib.qo_rope_table(ptr(c, ctypes.c_float), ptr(s, ctypes.c_float), max_ctx, half, theta)
+        return c, s
+
+    def decoder(self, model: dict, threads: int = 0) -> "Decoder":
+        return Decoder(self, model, threads)
 
     # -- scalar helpers -------------------------------------------------
     def half_to_float(self, h: int) -> float:
@@ -289,3 +386,44 @@ def load() -> Oracle:
 
 def load_ref():
     return Reference() if os.path.exists(REF_SO) else None
+
+
+REF_DECODER_SO = os.path.join(HERE, "_ref", "libqwn_ref_decoder.so")
+
+
+class RefDecoder:
+    """The reference decoder (c/qwanto_decode.c) compiled in place, CPU
+    backend with the Q8 KV cache, over a .qwn file."""
+
+    def __init__(self, path: str, context: int, threads: int = 0):
+        lib = ctypes.CDLL(REF_DECODER_SO)
+        lib.qrd_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
+                                 ctypes.c_int]
+        lib.qrd_open.restype = ctypes.c_void_p
+        lib.qrd_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, _c_f32p, ctypes.c_int]
+        lib.qrd_close.argtypes = [ctypes.c_void_p]
+        lib.qrd_cpu_fallback_count.argtypes = [ctypes.c_void_p]
+        lib.qrd_cpu_fallback_count.restype = ctypes.c_uint64
+        self.lib = lib
+        err = ctypes.create_string_buffer(256)
+        self.h = lib.qrd_open(path.encode(), context, threads, err, 256)
+        if not self.h:
+            raise RuntimeError(f"reference decoder open failed: {err.value.decode()}")
+
+    def forward(self, token: int, vocab: int) -> np.ndarray:
+        logits = np.empty(vocab, dtype=np.float32)
+        rc = self.lib.qrd_forward(self.h, int(token), ptr(logits, ctypes.c_float), vocab)
+        assert rc == 0, f"reference forward failed ({rc})"
+        return logits
+
+    def close(self):
+        if self.h:
+            self.lib.qrd_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+def load_ref_decoder(path: str, context: int, threads: int = 0):
+    return RefDecoder(path, context, threads) if os.path.exists(REF_DECODER_SO) else None

@@ -120,6 +120,45 @@ void qo_q8_attention(const float *query, const int8_t *keys,
                      int head_dim, int pos, float scale, float *out,
                      int threads);
 
+/* ---- dense decoder (qwn_oracle_decoder.c) ------------------------------ */
+
+#define QO_PROJ_HVSQ2 1
+#define QO_PROJ_Q4_0 2
+
+typedef struct {
+    int hidden, intermediate, layers, heads, kv_heads, head_dim, vocab, max_ctx;
+    float rope_theta, rms_eps;
+    int proj_dtype; /* QO_PROJ_* */
+} qo_model_config;
+
+typedef struct {
+    qo_model_config cfg;
+    const uint16_t *embed;          /* F16 [vocab][hidden], tied LM head */
+    const float *final_norm;        /* [hidden] */
+    const uint8_t *const *proj;     /* [layers * 7]: q k v o gate up down blocks */
+    const float *const *norms;      /* [layers * 2]: input, post attention */
+} qo_model;
+
+typedef struct qo_decoder qo_decoder;
+
+/* rmsnorm (c/qwanto_decode.c:627-652). */
+void qo_rmsnorm(float *out, const float *x, const float *w, int n, float eps);
+/* RoPE tables [max_ctx][half] (c/qwanto_decode.c:601-625). */
+void qo_rope_table(float *cos_t, float *sin_t, int max_ctx, int half, float theta);
+/* NeoX half-split rotation of `heads` rows (c/qwanto_decode.c:686-729). */
+void qo_rope_apply(float *v, int heads, int dim, const float *ct, const float *st);
+/* First index of the maximum (c/qwanto_decode.c:2043-2065). */
+int qo_argmax(const float *logits, int n);
+
+qo_decoder *qo_decoder_create(const qo_model *m, int threads);
+void qo_decoder_free(qo_decoder *d);
+int qo_decoder_position(const qo_decoder *d);
+/* One forward step (c/qwanto_decode.c:1566-2032); logits_out may be NULL. */
+int qo_decoder_forward(qo_decoder *d, int token, float *logits_out);
+/* Greedy generate (c/qwanto_decode.c:2085-2125). */
+int qo_decoder_generate(qo_decoder *d, const int *prompt, int prompt_count, int max_new, int *tokens,
+                        float *margins);
+
 #ifdef __cplusplus
 }
 #endif

@@ -168,7 +168,9 @@ ResidentTensor *check_request(Context *ctx, const QwnCudaGemmRequest *r) {
         return nullptr;
     }
     const bool f16 = rt->t.kind == qwn::kF16;
-    if ((f16 && r->input_mode != QWN_CUDA_INPUT_F32) || (!f16 && r->input_mode != QWN_CUDA_INPUT_Q8)) {
+    // F16 tensors take fp32 activations; quantized tensors take int8 tokens
+    // with their scales, or fp32 activations quantized on the device.
+    if (r->input_mode != QWN_CUDA_INPUT_F32 && (f16 || r->input_mode != QWN_CUDA_INPUT_Q8)) {
         set_error("input mode %u does not match the tensor dtype", r->input_mode);
         return nullptr;
     }
@@ -183,7 +185,9 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     if (e != hipSuccess) return hip_fail("hipSetDevice", e);
 
     const bool f16 = t.kind == qwn::kF16;
-    const size_t elem = f16 ? 4 : 1;
+    const bool f32_in = r->input_mode == QWN_CUDA_INPUT_F32;
+    const bool quantize = f32_in && !f16;  // per-token int8 quantization on the device
+    const size_t elem = f32_in ? 4 : 1;
     const uint32_t in_stride = r->input_stride ? r->input_stride : r->cols;
     const uint32_t out_stride = r->output_stride ? r->output_stride : r->rows;
     // device copy of the activations with a 16-byte aligned row stride
@@ -212,10 +216,9 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     }
     float *hscales = reinterpret_cast<float *>(hin + in_bytes);
     for (uint32_t b = 0; b < r->batch; ++b) hscales[b] = r->input_scales ? r->input_scales[b] : r->input_scale;
-    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, in_bytes + 0, hipMemcpyHostToDevice, ctx->stream)) !=
-            hipSuccess ||
-        (e = hipMemcpyAsync(ctx->dev_scales.ptr, hscales, scale_bytes, hipMemcpyHostToDevice,
-                            ctx->stream)) != hipSuccess)
+    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, in_bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (!quantize && (e = hipMemcpyAsync(ctx->dev_scales.ptr, hscales, scale_bytes, hipMemcpyHostToDevice,
+                                          ctx->stream)) != hipSuccess))
         return hip_fail("activation upload", e);
     const double transfer_ms = ms_since(t_transfer);
 
@@ -229,9 +232,14 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     g.batch = r->batch;
     g.output_stride = r->rows;
     (void)hipEventRecord(ctx->ev_start, ctx->stream);
-    if ((e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
-                               img_stride, ctx->stream)) != hipSuccess)
-        return hip_fail("activation image launch", e);
+    if (quantize)
+        e = qwn::launch_quantize_image(t, static_cast<const float *>(ctx->dev_in.ptr), r->batch, dev_stride,
+                                       static_cast<uint8_t *>(ctx->dev_img.ptr), img_stride,
+                                       static_cast<float *>(ctx->dev_scales.ptr), nullptr, 0, ctx->stream);
+    else
+        e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
+                              img_stride, ctx->stream);
+    if (e != hipSuccess) return hip_fail("activation image launch", e);
     if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
     (void)hipEventRecord(ctx->ev_end, ctx->stream);
     if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,

@@ -98,3 +98,37 @@ def weight_bytes(dtype: str, rows: int, cols: int) -> int:
     if dtype == "f16":
         return rows * cols * 2
     raise ValueError(dtype)
+
+
+# ---- synthetic decoder models ------------------------------------------------
+
+# Qwen2-1.5B shaped dense decoder (the Q4_0 decode workload): tied F16
+# embedding / LM head, no biases, no q/k norms, F32 norm weights of 1.
+QWEN2_1P5B_CONFIG = {
+    "hidden": 1536, "intermediate": 8960, "layers": 28, "heads": 12, "kv_heads": 2,
+    "head_dim": 128, "vocab": 151936, "max_ctx": 512, "rope_theta": 1.0e6, "rms_eps": 1.0e-6,
+}
+
+
+def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0") -> dict:
+    """Random decoder weights with the layout of a .qwn dense model: per layer
+    q, k, v, o, gate, up, down quantized matrices ([out][in] row-major
+    blocks), input/post norm vectors; a tied F16 embedding [vocab][hidden]
+    and the final norm."""
+    D, I = cfg["hidden"], cfg["intermediate"]
+    Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
+    shapes = {"q": (Q, D), "k": (KV, D), "v": (KV, D), "o": (D, Q),
+              "gate": (I, D), "up": (I, D), "down": (D, I)}
+    layers = []
+    for _ in range(cfg["layers"]):
+        layer = {p: weights(dtype, rng, *shapes[p]) for p in PROJECTIONS}
+        layer["input_norm"] = np.ones(D, dtype=np.float32)
+        layer["post_norm"] = np.ones(D, dtype=np.float32)
+        layers.append(layer)
+    embed = f16_weights(rng, cfg["vocab"], D)
+    return {"cfg": dict(cfg), "dtype": dtype, "shapes": shapes, "layers": layers,
+            "embed": embed, "final_norm": np.ones(D, dtype=np.float32)}
+
+
+def prompt_tokens(rng: np.random.Generator, vocab: int, count: int = 32) -> np.ndarray:
+    return rng.integers(0, vocab, count, dtype=np.int32)

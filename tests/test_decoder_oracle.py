@@ -1,0 +1,100 @@
+"""The oracle decoder (oracle/qwn_oracle_decoder.c) against the reference's
+own decoder compiled in place (oracle/_ref/libqwn_ref_decoder.so from
+c/qwanto_decode.c and its library sources), and the .qwn container writer
+against the reference's reader: the same synthetic model is written as a
+.qwn file, opened by qwn_decoder_open_with_config (CPU backend, Q8 KV
+cache) and stepped token by token; the logits must be bit-identical."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from qwanto_amd import qwn_file, synth
+
+SMALL = dict(hidden=256, intermediate=512, layers=2, heads=4, kv_heads=2, head_dim=64, vocab=1000,
+             max_ctx=64, rope_theta=1e6, rms_eps=1e-6)
+# head_dim 128 and GQA 6:1 as the 1.5B shape, fewer/narrower layers
+QWEN2_LIKE = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, head_dim=128, vocab=4096,
+                  max_ctx=64, rope_theta=1e6, rms_eps=1e-6)
+
+
+def ref_decoder_or_skip(path, ctx):
+    if not os.path.exists(oracle.REF_DECODER_SO):
+        pytest.skip("reference decoder build (oracle/_ref) absent")
+    return oracle.load_ref_decoder(path, ctx)
+
+
+@pytest.mark.parametrize("cfg,dtype,steps", [(SMALL, "q4_0", 12), (SMALL, "hvsq2", 8),
+                                             (QWEN2_LIKE, "q4_0", 10)])
+def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dtype, steps):
+    rng = np.random.default_rng(11)
+    model = synth.decoder_model(rng, cfg, dtype)
+    path = str(tmp_path / "m.qwn")
+    qwn_file.write_decoder_model(path, model)
+    ref = ref_decoder_or_skip(path, cfg["max_ctx"])
+    dec = oracle_lib.decoder(model)
+    token = 3
+    for step in range(steps):
+        a = ref.forward(token, cfg["vocab"])
+        b = dec.forward(token)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+            f"step {step}: logits differ by up to {np.abs(a - b).max()}"
+        token = int(np.argmax(a))
+    ref.close()
+    dec.close()
+
+
+def test_qwn_roundtrip(tmp_path):
+    rng = np.random.default_rng(2)
+    model = synth.decoder_model(rng, SMALL, "hvsq2")
+    path = str(tmp_path / "m.qwn")
+    size = qwn_file.write_decoder_model(path, model)
+    assert os.path.getsize(path) == size
+    back = qwn_file.read_decoder_model(path)
+    assert back["cfg"] == {k: SMALL[k] for k in back["cfg"]}
+    assert back["dtype"] == "hvsq2" and back["shapes"] == model["shapes"]
+    for l in range(SMALL["layers"]):
+        for p in synth.PROJECTIONS:
+            assert np.array_equal(back["layers"][l][p], model["layers"][l][p])
+    assert np.array_equal(back["embed"], model["embed"])
+    f = back["file"]
+    # 2 + 2 norms*layers + 7*layers + embed + final norm descriptors; 29 inline, rest in the tail
+    assert len(f.tensors) == 2 + 9 * SMALL["layers"] + 2
+    assert all(t["offset"] % 4096 == 0 and t["size"] % 64 == 0 for t in f.tensors.values())
+    f.close()
+
+
+def test_fnv1a64_known_values():
+    # FNV-1a 64 test vectors (offset basis for "", published values for "a", "foobar")
+    assert qwn_file.fnv1a64("") == 0xCBF29CE484222325
+    assert qwn_file.fnv1a64("a") == 0xAF63DC4C8601EC8C
+    assert qwn_file.fnv1a64("foobar") == 0x85944171F73967E8
+
+
+def test_rmsnorm_closed_form(oracle_lib):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1536).astype(np.float32) * 3
+    w = rng.uniform(0.5, 1.5, 1536).astype(np.float32)
+    got = oracle_lib.rmsnorm(x, w, 1e-6)
+    ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w
+    assert np.allclose(got, ref, rtol=3e-7, atol=0)
+    # constant input: x * 1/sqrt(x^2 + eps)
+    c = np.full(16, 2.0, dtype=np.float32)
+    assert np.allclose(oracle_lib.rmsnorm(c, np.ones(16, np.float32), 0.0), 1.0, rtol=0, atol=1e-7)
+
+
+def test_rope_table_closed_form(oracle_lib):
+    c, s = oracle_lib.rope_table(64, 64, 1e6)
+    # angle = (float)pos * powf(theta, -2i/dim), both steps in fp32
+    pos = np.arange(64, dtype=np.float32)[:, None]
+    freq = np.power(np.float32(1e6), (-2.0 * np.arange(64) / 128.0).astype(np.float32))
+    ang = (pos * freq).astype(np.float64)
+    assert np.allclose(c, np.cos(ang), atol=2e-6) and np.allclose(s, np.sin(ang), atol=2e-6)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+
+
+def test_greedy_is_first_maximum(oracle_lib):
+    import ctypes
+    logits = np.array([0.5, 2.0, -1.0, 2.0, 1.0], dtype=np.float32)
+    assert oracle_lib.lib.qo_argmax(logits.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 5) == 1

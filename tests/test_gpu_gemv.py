@@ -142,8 +142,10 @@ def test_request_validation(gpu_ctx, hip_lib):
     assert e.value.status == -1
     with pytest.raises(abi.AbiError):               # gemv demands batch == 1
         gpu_ctx.gemm(h, q8, 8, 256, scale=1.0, gemv=True)
-    with pytest.raises(abi.AbiError):               # fp32 input for an int8 tensor
-        gpu_ctx.gemm(h, q8.astype(np.float32), 8, 256)
+    hf = gpu_ctx.upload(synth.f16_weights(rng, 8, 256), "f16", 8, 256)
+    with pytest.raises(abi.AbiError):               # int8 input for an F16 tensor
+        gpu_ctx.gemm(hf, q8[:1], 8, 256, scale=1.0)
+    gpu_ctx.release(hf)
     gpu_ctx.release(h)
     with pytest.raises(abi.AbiError):               # released handle
         gpu_ctx.gemm(h, q8[:1], 8, 256, scale=1.0)
@@ -252,5 +254,25 @@ def test_device_image_f16(gpu_ctx, oracle_lib):
         ref = oracle_lib.matmul_f16(w, x)
         ok, worst = gemv_close(y.cpu().numpy(), ref)
         assert ok, f"F16 image path: worst {worst:.3g}"
+    finally:
+        gpu_ctx.release(h)
+
+
+@pytest.mark.parametrize("kind,N,K,M", [("hvsq2", 1024, 2560, 1), ("hvsq2", 77, 700, 3),
+                                        ("q4_0", 1536, 1536, 1), ("q4_0", 40, 8960, 2)])
+def test_abi_fp32_input_quantized_on_device(gpu_ctx, oracle_lib, kind, N, K, M):
+    """INPUT_F32 with a quantized tensor: the library quantizes per token on
+    the device (c/qwanto_kernels.c:354-433) -- the whole CPU matmul
+    (qwn_matmul_*_f32) is the reference."""
+    rng = np.random.default_rng(N + K + M)
+    w = synth.weights(kind, rng, N, K)
+    x = synth.activations(rng, M, K)
+    h = gpu_ctx.upload(w, kind, N, K)
+    try:
+        y = gpu_ctx.gemm(h, x, N, K, gemv=(M == 1))
+        ref = oracle_lib.matmul_hvsq2(w, x, N) if kind == "hvsq2" else oracle_lib.matmul_q4_0(w, x, N)
+        for t in range(M):
+            ok, worst = gemv_close(y[t], ref[t])
+            assert ok, f"{kind} {N}x{K} token {t}: worst {worst:.3g}"
     finally:
         gpu_ctx.release(h)
