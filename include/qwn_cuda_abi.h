@@ -102,8 +102,9 @@ typedef enum {
 
 typedef enum {
     QWN_CUDA_INPUT_Q8 = 1,
-    /* EXT: input_q8 points at fp32 activations [batch x input_stride]
-     * (only valid for QWN_CUDA_TENSOR_F16). */
+    /* EXT: input_q8 points at fp32 activations [batch x input_stride];
+     * F16 tensors take them as is, quantized tensors quantize them per
+     * token on the device (the reference's host-side arithmetic). */
     QWN_CUDA_INPUT_F32 = 2
 } QwnCudaInputMode;
 

@@ -58,9 +58,25 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     shutil.copyfile(LIB, LOADER_NAME + ".tmp")
     os.replace(LOADER_NAME + ".tmp", LOADER_NAME)
+    build_host_decoder()
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+HOST_DECODER = os.path.join(LIBDIR, "libqwn_host_decoder.so")
+
+
+def build_host_decoder() -> str:
+    """The host-side decoder (plain C, above the ABI): gcc, no contraction so
+    its explicit fused multiply-adds are the only ones."""
+    tmp = HOST_DECODER + ".tmp"
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-std=gnu11", "-fPIC", "-shared", "-ffp-contract=off",
+           "-Wall", "-Wextra", "-I" + os.path.join(ROOT, "include"),
+           os.path.join(PKG, "host", "qwn_host_decoder.c"), "-o", tmp, "-ldl", "-lm"]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, HOST_DECODER)
+    return HOST_DECODER
 
 
 if __name__ == "__main__":

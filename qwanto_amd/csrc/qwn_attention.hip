@@ -36,7 +36,10 @@ __device__ __forceinline__ size_t scale_offset(const KvCache &c, uint32_t token)
 // grid (groups, 2): y = 0 quantizes K, y = 1 quantizes V.  64 threads, one
 // per channel of the group.
 __global__ __launch_bounds__(64) void kv_append_kernel(KvCache c, const float *__restrict__ key,
-                                                       const float *__restrict__ value, uint32_t token) {
+                                                       const float *__restrict__ value, uint32_t token,
+                                                       const int32_t *__restrict__ token_ptr) {
+    if (token_ptr) token = static_cast<uint32_t>(*token_ptr);
+    if (token >= c.max_tokens) return;
     const uint32_t g = blockIdx.x;
     const bool is_v = blockIdx.y == 1;
     const float *src = is_v ? value : key;
@@ -68,6 +71,7 @@ struct AttnArgs {
     uint32_t split;   // tokens per split
     uint32_t nsplit;
     float scale;
+    const int32_t *position_ptr;  // non-null: tokens = *position_ptr + 1 (fixed split grid)
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -94,8 +98,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     const uint32_t kvh = blockIdx.y;
     const uint32_t split = blockIdx.x;
     const uint32_t t0 = split * a.split;
-    const uint32_t n = min(a.split, a.tokens - t0);
+    const uint32_t tokens = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) + 1u : a.tokens;
     const uint32_t G = a.group;
+    if (t0 >= tokens) {
+        // a split past the current position (fixed grid): an empty partial
+        for (uint32_t i = threadIdx.x; i < G * D; i += blockDim.x) {
+            const uint32_t g = i / D, d = i % D;
+            float *dst = a.partials + (static_cast<size_t>(kvh * G + g) * a.nsplit + split) * (D + 2);
+            dst[2 + d] = 0.0f;
+            if (d == 0) {
+                dst[0] = -INFINITY;
+                dst[1] = 0.0f;
+            }
+        }
+        return;
+    }
+    const uint32_t n = min(a.split, tokens - t0);
     float *q = sm;                              // [GMAX][D]
     float *p = q + GMAX * D;                    // [split][GMAX]
     float *wred = p + kMaxSplitTokens * GMAX;   // [4 waves][GMAX]
@@ -239,7 +257,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     }
 }
 
-// grid (query_heads): merge the split partials of one head.
+// grid (query_heads): merge the split partials of one head (empty splits
+// carry m = -inf, l = 0 and drop out).
 __global__ __launch_bounds__(256) void attention_merge_kernel(const float *__restrict__ partials,
                                                               float *out, uint32_t nsplit, uint32_t D) {
     const uint32_t head = blockIdx.x;
@@ -290,7 +309,14 @@ hipError_t launch_fast_or_not(const AttnArgs &args, hipStream_t stream) {
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
                             hipStream_t stream) {
     if (token >= c.max_tokens) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2), dim3(64), 0, stream, c, key, value, token);
+    hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2), dim3(64), 0, stream, c, key, value, token,
+                       static_cast<const int32_t *>(nullptr));
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append_at(const KvCache &c, const float *key, const float *value, const int32_t *token_ptr,
+                               hipStream_t stream) {
+    hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2), dim3(64), 0, stream, c, key, value, 0u, token_ptr);
     return hipGetLastError();
 }
 
@@ -299,6 +325,42 @@ size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32
     const uint32_t s = split_tokens(c, tokens);
     const uint32_t nsplit = (tokens + s - 1) / s;
     return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
+}
+
+namespace {
+hipError_t launch_split_and_merge(AttnArgs &args, float *output, hipStream_t stream) {
+    hipError_t e;
+    if (args.group <= 1) e = launch_fast_or_not<1>(args, stream);
+    else if (args.group <= 2) e = launch_fast_or_not<2>(args, stream);
+    else if (args.group <= 4) e = launch_fast_or_not<4>(args, stream);
+    else if (args.group <= 8) e = launch_fast_or_not<8>(args, stream);
+    else return hipErrorInvalidValue;
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(args.query_heads), dim3(256), 0, stream, args.partials, output,
+                       args.nsplit, args.c.head_dim);
+    return hipGetLastError();
+}
+}  // namespace
+
+size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads) {
+    const uint32_t nsplit = (c.max_tokens + kDevicePositionSplit - 1) / kDevicePositionSplit;
+    return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
+}
+
+hipError_t launch_attention_at(const KvCache &c, const float *query, float *output, uint32_t query_heads,
+                               const int32_t *position_ptr, float scale, float *partials, hipStream_t stream) {
+    if (query_heads % c.kv_heads != 0 || c.head_dim > 1024) return hipErrorInvalidValue;
+    AttnArgs args{};
+    args.c = c;
+    args.query = query;
+    args.partials = partials;
+    args.query_heads = query_heads;
+    args.group = query_heads / c.kv_heads;
+    args.split = kDevicePositionSplit;
+    args.nsplit = (c.max_tokens + kDevicePositionSplit - 1) / kDevicePositionSplit;
+    args.scale = scale;
+    args.position_ptr = position_ptr;
+    return launch_split_and_merge(args, output, stream);
 }
 
 hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
@@ -315,16 +377,8 @@ hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
     args.split = split_tokens(c, args.tokens);
     args.nsplit = (args.tokens + args.split - 1) / args.split;
     args.scale = a.scale;
-    hipError_t e;
-    if (args.group <= 1) e = launch_fast_or_not<1>(args, stream);
-    else if (args.group <= 2) e = launch_fast_or_not<2>(args, stream);
-    else if (args.group <= 4) e = launch_fast_or_not<4>(args, stream);
-    else if (args.group <= 8) e = launch_fast_or_not<8>(args, stream);
-    else return hipErrorInvalidValue;
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(a.query_heads), dim3(256), 0, stream, a.partials,
-                       a.output, args.nsplit, c.head_dim);
-    return hipGetLastError();
+    args.position_ptr = nullptr;
+    return launch_split_and_merge(args, a.output, stream);
 }
 
 }  // namespace qwn

@@ -1,0 +1,100 @@
+// Device-side helpers shared by the qwn_hip kernels: fp16 decode, the
+// activation-image packing of one 32-element block, and the address of a
+// weight unit in the wave-tile layout (qwn_internal.h).
+#pragma once
+
+#include "qwn_internal.h"
+
+namespace qwn {
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+    // v_cvt_f32_f16 keeps fp16 subnormals (the default f16 denormal mode),
+    // matching the CPU's exact conversion (c/qwanto_kernels.c:264-285).
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+
+// ---- activation images --------------------------------------------------------
+
+// Nibble-pack 8 int8 values (two dwords, element order) into the high
+// (signed, a >> 4) and low (a & 15) nibble words, nibble k = element k.
+__device__ __forceinline__ void split8(uint32_t a, uint32_t b, uint32_t &hi, uint32_t &lo) {
+    hi = lo = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t byte = ((k < 4 ? a : b) >> (8 * (k & 3))) & 0xffu;
+        hi |= ((byte >> 4) & 0xfu) << (4 * k);  // arithmetic >> 4 of the int8, as a nibble
+        lo |= (byte & 0xfu) << (4 * k);
+    }
+}
+
+// Even/odd split of 16 int8 values for the HyperVSQ-2 masks: returns the
+// high/low nibble words of elements {0,2,..,14} and {1,3,..,15}.
+__device__ __forceinline__ uint4 split16_evenodd(const uint32_t w[4]) {
+    uint32_t he = 0, le = 0, ho = 0, lo = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t ev = (w[k >> 1] >> (16 * (k & 1))) & 0xffu;        // element 2k
+        const uint32_t od = (w[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;    // element 2k+1
+        he |= ((ev >> 4) & 0xfu) << (4 * k);
+        le |= (ev & 0xfu) << (4 * k);
+        ho |= ((od >> 4) & 0xfu) << (4 * k);
+        lo |= (od & 0xfu) << (4 * k);
+    }
+    return make_uint4(he, le, ho, lo);
+}
+
+// Write one 32-activation block (8 dwords of int8, element order) into a
+// token image: its nibble words and its correction term.
+template <int KIND>
+__device__ __forceinline__ void put_block32(uint8_t *img, uint32_t units, uint32_t b, const uint32_t w[8]) {
+    const uint32_t e0 = b * 32;
+    int32_t *sums = reinterpret_cast<int32_t *>(img + units * unit_lds_bytes(KIND));
+    if (KIND == kHvsq2) {
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = sdot4(w[i], 0x01010101u, s);
+        sums[b] = s;
+        const uint32_t u = e0 / 256, off = e0 % 256;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+            *reinterpret_cast<uint4 *>(img + u * 272 + (off / 16 + g) * 16) = split16_evenodd(w + 4 * g);
+    } else {
+        const uint32_t u = e0 / 128, off = e0 % 128;
+        int lsum = 0;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t hi, lo;
+            split8(w[2 * g], w[2 * g + 1], hi, lo);
+            lsum = static_cast<int>(__builtin_amdgcn_udot8(lo, 0x11111111u, static_cast<uint32_t>(lsum), false));
+            *reinterpret_cast<uint2 *>(img + u * 144 + (off / 8 + g) * 8) = make_uint2(hi, lo);
+        }
+        sums[b] = 8 * lsum;
+    }
+}
+
+
+// Byte address of chunk q of unit u of a row, and of its metadata.
+struct UnitAddr {
+    size_t payload, meta;
+};
+__host__ __device__ inline UnitAddr unit_addr(uint32_t row, uint32_t u, uint32_t q, uint32_t lanes,
+                                              uint32_t rows_per_wave, uint32_t units, size_t tile_payload,
+                                              size_t tile_meta) {
+    const uint32_t tile = row / rows_per_wave, grp = row % rows_per_wave;
+    const uint32_t i = u / lanes, jj = u % lanes;
+    const uint32_t n = units - i * lanes < lanes ? units - i * lanes : lanes;  // units in plane i
+    UnitAddr r;
+    r.payload = tile * tile_payload + static_cast<size_t>(64) * rows_per_wave * lanes * i +
+                (static_cast<size_t>(q) * rows_per_wave * n + grp * n + jj) * 16;
+    r.meta = tile * tile_meta + static_cast<size_t>(8) * rows_per_wave * lanes * i +
+             (static_cast<size_t>(grp) * n + jj) * 8;
+    return r;
+}
+
+
+}  // namespace qwn

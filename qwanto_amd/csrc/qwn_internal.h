@@ -160,4 +160,16 @@ size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads,
                                   uint32_t position);
 hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream);
 
+// Device-position variants for graph replay: the token index / position is
+// read from device memory when the kernels run; attention uses a fixed grid
+// of kDevicePositionSplit-token splits over the whole cache, splits past
+// the position writing empty partials.
+constexpr uint32_t kDevicePositionSplit = 64;
+hipError_t launch_kv_append_at(const KvCache &c, const float *key, const float *value,
+                               const int32_t *token_ptr, hipStream_t stream);
+size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads);
+hipError_t launch_attention_at(const KvCache &c, const float *query, float *output,
+                               uint32_t query_heads, const int32_t *position_ptr, float scale,
+                               float *partials, hipStream_t stream);
+
 }  // namespace qwn
