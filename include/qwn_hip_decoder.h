@@ -1,0 +1,89 @@
+#ifndef QWN_HIP_DECODER_H
+#define QWN_HIP_DECODER_H
+
+/*
+ * Resident greedy decoder on one MI355X (extension; no counterpart in
+ * c/cuda/qwn_cuda_abi.h).
+ *
+ * The reference host runs the dense decoder step on the CPU and calls the
+ * GPU ABI once per projection and KV operation, synchronously, with host
+ * buffers (c/qwanto_decode.c:776-924, :1657-1724).  This decoder keeps the
+ * whole step on the device: the residual stream, RMSNorm, RoPE, the Q8 KV
+ * cache, SwiGLU, the tied F16 LM head and the greedy argmax, with the same
+ * semantics as the reference forward/generate (c/qwanto_decode.c:1566-2032,
+ * 2043-2125).  One step is a fixed sequence of kernels that read the token
+ * and position from device memory, captured once as a HIP graph; a greedy
+ * generation replays it without host synchronisation between tokens.
+ *
+ * Weights are the tensors of qwn_cuda_abi.h, already uploaded to the same
+ * context (qwn_cuda_abi_upload_tensor): seven projections per layer
+ * (HyperVSQ-2 or Q4_0, one dtype per decoder) and the F16 embedding, which
+ * is also the tied LM head.  Norm weights are copied from the host at
+ * creation.  Biases and q/k norms are not supported (the configurations
+ * this decoder serves have none).
+ */
+
+#include "qwn_cuda_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    QwnCudaAbiHeader header;
+    uint32_t hidden;
+    uint32_t intermediate;
+    uint32_t layers;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t vocab;
+    uint32_t max_ctx;         /* KV-cache capacity in tokens */
+    float rope_theta;
+    float rms_eps;
+    const QwnCudaTensorHandle *projections; /* [layers * 7]: q, k, v, o, gate, up, down */
+    const QwnCudaTensorHandle *embedding;   /* F16 [vocab][hidden] */
+    const float *input_norms;               /* host [layers][hidden] */
+    const float *post_norms;                /* host [layers][hidden] */
+    const float *final_norm;                /* host [hidden] */
+} QwnHipDecoderDesc;
+
+typedef struct {
+    QwnCudaAbiHeader header;
+    void *opaque;
+} QwnHipDecoderHandle;
+
+typedef struct {
+    QwnCudaAbiHeader header;
+    uint32_t prompt_tokens;
+    uint32_t generated_tokens;
+    uint32_t position;            /* tokens in the KV cache */
+    uint32_t launches_per_step;   /* kernels in one step */
+    double prefill_ms;            /* wall clock, prompt steps */
+    double decode_ms;             /* wall clock, generated steps */
+    uint64_t weight_bytes_per_step; /* algorithmic weight bytes one step reads */
+    uint32_t graph;               /* 1 if steps replay a captured HIP graph */
+    uint32_t reserved;
+} QwnHipDecoderStats;
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *context, const QwnHipDecoderDesc *desc,
+                                            QwnHipDecoderHandle *out);
+QWN_CUDA_ABI_API int qwn_hip_decoder_destroy(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder);
+/* Empties the KV cache (position 0). */
+QWN_CUDA_ABI_API int qwn_hip_decoder_reset(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder);
+/* One step on `token` at the current position (synchronous).  `logits`
+ * (vocab floats) and `next_token` (the greedy choice) may be NULL. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                             int32_t token, float *logits, int32_t *next_token);
+/* Greedy generation as c/qwanto_decode.c:2085-2125: one step per prompt
+ * token, then max_new times: tokens[s] = argmax of the last logits, one
+ * step on it.  Synchronises once after the prompt and once at the end. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                              const int32_t *prompt, uint32_t prompt_count, uint32_t max_new,
+                                              int32_t *tokens, QwnHipDecoderStats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWN_HIP_DECODER_H */

@@ -80,6 +80,58 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *context
                                                    float *output, uint32_t batch,
                                                    uint32_t output_stride, void *stream);
 
+/* Grouped GEMV: up to 4 tensors of one dtype and column count that share
+ * one input (q/k/v, gate/up) in a single launch.  Input modes:
+ *   IMAGE    prebuilt activation images [batch][image_stride], scales
+ *   F32      one fp32 token x [cols] (cols a multiple of 32); every
+ *            workgroup quantizes it per token itself (c/qwanto_kernels.c:
+ *            354-433) into its LDS image -- no separate quantize launch
+ *   RMSNORM  y = (x * 1/sqrt(mean(x^2) + eps)) * norm, then as F32
+ *            (c/qwanto_decode.c:627-652)
+ *   SWIGLU   y = (x / (1 + exp(-x))) * x2, then as F32
+ *            (c/qwanto_decode.c:1946-1949)
+ * Output modes: STORE; ADD (outputs += result, one token: the residual
+ * stream); ARGMAX (store, and one packed key per workgroup in
+ * argmax_partials -- qwn_hip_ext_gemv_group_partials() of them -- reduced
+ * by qwn_hip_ext_argmax_device to the first index of the largest output).
+ * Device pointers, caller's stream, no allocation. */
+#define QWN_HIP_GEMV_INPUT_IMAGE 0u
+#define QWN_HIP_GEMV_INPUT_F32 1u
+#define QWN_HIP_GEMV_INPUT_RMSNORM 2u
+#define QWN_HIP_GEMV_INPUT_SWIGLU 3u
+#define QWN_HIP_GEMV_OUTPUT_STORE 0u
+#define QWN_HIP_GEMV_OUTPUT_ADD 1u
+#define QWN_HIP_GEMV_OUTPUT_ARGMAX 2u
+#define QWN_HIP_GEMV_MAX_GROUP 4u
+
+typedef struct {
+    QwnCudaAbiHeader header;
+    uint32_t count;                       /* tensors, 1..4 */
+    uint32_t input_mode;                  /* QWN_HIP_GEMV_INPUT_* */
+    uint32_t output_mode;                 /* QWN_HIP_GEMV_OUTPUT_* */
+    uint32_t batch;                       /* tokens (image input); 1 otherwise */
+    const QwnCudaTensorHandle *tensors;   /* [count] */
+    float *const *outputs;                /* [count] device fp32 [batch][output_stride] */
+    uint32_t output_stride;               /* 0: rows of each tensor */
+    uint32_t image_stride;
+    const void *image;
+    const float *scales;                  /* image input: per-token scales or NULL */
+    float scale;                          /* image input without scales */
+    float eps;                            /* RMSNORM */
+    const float *x;                       /* fp32 input [cols] */
+    const float *x2;                      /* SWIGLU: the up projection [cols] */
+    const float *norm;                    /* RMSNORM weights [cols] */
+    float *scale_out;                     /* optional: the activation scale (one float) */
+    uint64_t *argmax_partials;            /* ARGMAX */
+} QwnHipGemvGroupRequest;
+
+QWN_CUDA_ABI_API uint32_t qwn_hip_ext_gemv_group_partials(QwnCudaContextHandle *context,
+                                                          const QwnHipGemvGroupRequest *request);
+QWN_CUDA_ABI_API int qwn_hip_ext_gemv_group_device(QwnCudaContextHandle *context,
+                                                   const QwnHipGemvGroupRequest *request, void *stream);
+QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *context, const uint64_t *partials,
+                                               uint32_t count, int32_t *index, void *stream);
+
 /* Per-token int8 quantization on the device without an image:
  * x fp32 [batch][x_stride] -> q8 [batch][q8_stride] (zero padded past
  * cols), scales [batch]. */

@@ -52,7 +52,15 @@ EXT_EXPORTS = (
     "qwn_hip_ext_gemm_image_device", "qwn_hip_ext_quantize_device",
     "qwn_hip_ext_kv_append_device", "qwn_hip_ext_attention_workspace_bytes",
     "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
+    "qwn_hip_ext_gemv_group_partials", "qwn_hip_ext_gemv_group_device", "qwn_hip_ext_argmax_device",
 )
+DECODER_EXPORTS = (
+    "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
+    "qwn_hip_decoder_forward", "qwn_hip_decoder_generate",
+)
+
+GEMV_INPUT = {"image": 0, "f32": 1, "rmsnorm": 2, "swiglu": 3}
+GEMV_OUTPUT = {"store": 0, "add": 1, "argmax": 2}
 
 
 class Header(ctypes.Structure):
@@ -153,6 +161,35 @@ class TensorInfo(_Versioned):
                 ("rows_per_wave", ctypes.c_uint32), ("grid", ctypes.c_uint32)]
 
 
+class GemvGroupRequest(_Versioned):
+    _fields_ = [("header", Header), ("count", ctypes.c_uint32), ("input_mode", ctypes.c_uint32),
+                ("output_mode", ctypes.c_uint32), ("batch", ctypes.c_uint32),
+                ("tensors", ctypes.c_void_p), ("outputs", ctypes.c_void_p),
+                ("output_stride", ctypes.c_uint32), ("image_stride", ctypes.c_uint32),
+                ("image", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("scale", ctypes.c_float),
+                ("eps", ctypes.c_float), ("x", ctypes.c_void_p), ("x2", ctypes.c_void_p),
+                ("norm", ctypes.c_void_p), ("scale_out", ctypes.c_void_p),
+                ("argmax_partials", ctypes.c_void_p)]
+
+
+class DecoderDesc(_Versioned):
+    _fields_ = [("header", Header)] + \
+               [(n, ctypes.c_uint32) for n in ("hidden", "intermediate", "layers", "heads", "kv_heads",
+                                               "head_dim", "vocab", "max_ctx")] + \
+               [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
+                ("projections", ctypes.c_void_p), ("embedding", ctypes.c_void_p),
+                ("input_norms", ctypes.c_void_p), ("post_norms", ctypes.c_void_p),
+                ("final_norm", ctypes.c_void_p)]
+
+
+class DecoderStats(_Versioned):
+    _fields_ = [("header", Header), ("prompt_tokens", ctypes.c_uint32),
+                ("generated_tokens", ctypes.c_uint32), ("position", ctypes.c_uint32),
+                ("launches_per_step", ctypes.c_uint32), ("prefill_ms", ctypes.c_double),
+                ("decode_ms", ctypes.c_double), ("weight_bytes_per_step", ctypes.c_uint64),
+                ("graph", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
 STRUCTS = {
     "QwnCudaAbiHeader": Header, "QwnCudaAbiInfo": AbiInfo, "QwnCudaDeviceInfo": DeviceInfo,
     "QwnCudaContextOptions": ContextOptions, "QwnCudaContextHandle": Handle,
@@ -233,6 +270,15 @@ class Library:
                                                         ctypes.c_void_p, ctypes.c_void_p]
         lib.qwn_hip_ext_debug_int_sums.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
                                                    ctypes.c_void_p, ctypes.c_uint64]
+        lib.qwn_hip_ext_gemv_group_partials.argtypes = [P(Handle), P(GemvGroupRequest)]
+        lib.qwn_hip_ext_gemv_group_partials.restype = ctypes.c_uint32
+        lib.qwn_hip_ext_gemv_group_device.argtypes = [P(Handle), P(GemvGroupRequest), V]
+        lib.qwn_hip_ext_argmax_device.argtypes = [P(Handle), V, U32, V, V]
+        lib.qwn_hip_decoder_create.argtypes = [P(Handle), P(DecoderDesc), P(Handle)]
+        lib.qwn_hip_decoder_destroy.argtypes = [P(Handle), P(Handle)]
+        lib.qwn_hip_decoder_reset.argtypes = [P(Handle), P(Handle)]
+        lib.qwn_hip_decoder_forward.argtypes = [P(Handle), P(Handle), ctypes.c_int32, V, V]
+        lib.qwn_hip_decoder_generate.argtypes = [P(Handle), P(Handle), V, U32, U32, V, P(DecoderStats)]
 
     def last_error(self) -> str:
         buf = ctypes.create_string_buffer(512)
@@ -359,6 +405,36 @@ class Context:
         self.lib.check("quantize_device", self.lib.lib.qwn_hip_ext_quantize_device(
             self._h, x_ptr, batch, cols, x_stride, q8_ptr, q8_stride, scales_ptr, stream))
 
+    def gemv_group_request(self, handles: list, outputs: list[int], input_mode: str = "image",
+                           output_mode: str = "store", batch: int = 1, image_ptr: int | None = None,
+                           image_stride: int = 0, scales_ptr: int | None = None, scale: float = 0.0,
+                           x_ptr: int | None = None, x2_ptr: int | None = None,
+                           norm_ptr: int | None = None, eps: float = 0.0,
+                           scale_out_ptr: int | None = None, partials_ptr: int | None = None,
+                           output_stride: int = 0):
+        """A QwnHipGemvGroupRequest plus the arrays it points into (keep both alive)."""
+        hs = (Handle * len(handles))(*handles)
+        outs = (ctypes.c_void_p * len(outputs))(*outputs)
+        req = GemvGroupRequest(count=len(handles), input_mode=GEMV_INPUT[input_mode],
+                               output_mode=GEMV_OUTPUT[output_mode], batch=batch,
+                               tensors=ctypes.cast(hs, ctypes.c_void_p).value,
+                               outputs=ctypes.cast(outs, ctypes.c_void_p).value,
+                               output_stride=output_stride, image_stride=image_stride, image=image_ptr,
+                               scales=scales_ptr, scale=scale, eps=eps, x=x_ptr, x2=x2_ptr, norm=norm_ptr,
+                               scale_out=scale_out_ptr, argmax_partials=partials_ptr)
+        return req, (hs, outs)
+
+    def gemv_group_partials(self, req: GemvGroupRequest) -> int:
+        return int(self.lib.lib.qwn_hip_ext_gemv_group_partials(self._h, ctypes.byref(req)))
+
+    def gemv_group_device(self, req: GemvGroupRequest, stream: int | None = None) -> None:
+        self.lib.check("gemv_group_device",
+                       self.lib.lib.qwn_hip_ext_gemv_group_device(self._h, ctypes.byref(req), stream))
+
+    def argmax_device(self, partials_ptr: int, count: int, index_ptr: int, stream: int | None = None) -> None:
+        self.lib.check("argmax_device", self.lib.lib.qwn_hip_ext_argmax_device(
+            self._h, partials_ptr, count, index_ptr, stream))
+
     # -- KV cache ---------------------------------------------------------------
     def kv_create(self, max_tokens: int, kv_heads: int, head_dim: int) -> Handle:
         opts = KvCacheOptions(max_tokens=max_tokens, kv_heads=kv_heads, head_dim=head_dim)
@@ -423,6 +499,76 @@ class Context:
 
     def synchronize(self) -> None:
         self.lib.check("synchronize", self.lib.lib.qwn_cuda_abi_synchronize(self._h))
+
+
+class ResidentDecoder:
+    """The library's resident greedy decoder (include/qwn_hip_decoder.h) over a
+    synth.decoder_model / qwn_file model dict: uploads the seven projections
+    per layer and the F16 embedding to `ctx`, then creates the decoder."""
+
+    PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, ctx: Context, model: dict):
+        self.ctx = ctx
+        cfg = model["cfg"]
+        self.cfg = cfg
+        dtype = model["dtype"]
+        D, I = cfg["hidden"], cfg["intermediate"]
+        Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
+        shapes = {"q": (Q, D), "k": (KV, D), "v": (KV, D), "o": (D, Q), "gate": (I, D), "up": (I, D),
+                  "down": (D, I)}
+        L = cfg["layers"]
+        self._tensors = []
+        for l in range(L):
+            for p in self.PROJ_ORDER:
+                rows, cols = shapes[p]
+                self._tensors.append(ctx.upload(model["layers"][l][p], dtype, rows, cols))
+        self._embed = ctx.upload(model["embed"], "f16", cfg["vocab"], D)
+        self._proj_arr = (Handle * len(self._tensors))(*self._tensors)
+        self._norm_in = np.ascontiguousarray(np.stack([model["layers"][l]["input_norm"] for l in range(L)]),
+                                             dtype=np.float32)
+        self._norm_post = np.ascontiguousarray(np.stack([model["layers"][l]["post_norm"] for l in range(L)]),
+                                               dtype=np.float32)
+        self._final = np.ascontiguousarray(model["final_norm"], dtype=np.float32)
+        desc = DecoderDesc(hidden=D, intermediate=I, layers=L, heads=cfg["heads"], kv_heads=cfg["kv_heads"],
+                           head_dim=cfg["head_dim"], vocab=cfg["vocab"], max_ctx=cfg["max_ctx"],
+                           rope_theta=cfg["rope_theta"], rms_eps=cfg["rms_eps"],
+                           projections=ctypes.cast(self._proj_arr, ctypes.c_void_p).value,
+                           embedding=ctypes.addressof(self._embed), input_norms=_p(self._norm_in),
+                           post_norms=_p(self._norm_post), final_norm=_p(self._final))
+        self.handle = Handle()
+        lib = ctx.lib
+        lib.check("decoder_create", lib.lib.qwn_hip_decoder_create(ctx._h, ctypes.byref(desc),
+                                                                   ctypes.byref(self.handle)))
+
+    def forward(self, token: int, logits: bool = True):
+        """One step; returns (logits or None, greedy next token)."""
+        out = np.zeros(self.cfg["vocab"], dtype=np.float32) if logits else None
+        nxt = ctypes.c_int32(0)
+        self.ctx.lib.check("decoder_forward", self.ctx.lib.lib.qwn_hip_decoder_forward(
+            self.ctx._h, ctypes.byref(self.handle), int(token), _p(out), ctypes.addressof(nxt)))
+        return out, nxt.value
+
+    def generate(self, prompt, max_new: int):
+        """Greedy generation; returns (tokens[max_new], DecoderStats)."""
+        pr = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.zeros(max_new, dtype=np.int32)
+        st = DecoderStats()
+        self.ctx.lib.check("decoder_generate", self.ctx.lib.lib.qwn_hip_decoder_generate(
+            self.ctx._h, ctypes.byref(self.handle), _p(pr), pr.size, max_new, _p(toks), ctypes.byref(st)))
+        return toks, st
+
+    def reset(self) -> None:
+        self.ctx.lib.check("decoder_reset", self.ctx.lib.lib.qwn_hip_decoder_reset(
+            self.ctx._h, ctypes.byref(self.handle)))
+
+    def close(self) -> None:
+        if self.handle.opaque:
+            self.ctx.lib.check("decoder_destroy", self.ctx.lib.lib.qwn_hip_decoder_destroy(
+                self.ctx._h, ctypes.byref(self.handle)))
+        for t in self._tensors + [self._embed]:
+            self.ctx.release(t)
+        self._tensors = []
 
 
 _LIB: Library | None = None

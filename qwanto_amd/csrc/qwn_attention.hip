@@ -306,6 +306,91 @@ hipError_t launch_fast_or_not(const AttnArgs &args, hipStream_t stream) {
 
 }  // namespace
 
+namespace {
+
+// One workgroup: RoPE on the query heads (in place) and on the key, then the
+// Q8 append of the rotated key and of the value at slot *pos_ptr.  The
+// rotation is the reference's NeoX half split with its fused multiply-adds
+// (c/qwanto_decode.c:686-729):
+//   r[i] = fma(a, cos_i, -(b * sin_i)),  r[i + half] = fma(a, sin_i, b * cos_i)
+// with a = x[i], b = x[i + half] and the cos/sin table row of the position;
+// the append quantizes per 64-channel group as kv_append_kernel.
+__global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__restrict__ q, uint32_t q_heads,
+                                                           const float *__restrict__ k,
+                                                           const float *__restrict__ v,
+                                                           const float *__restrict__ cos_tab,
+                                                           const float *__restrict__ sin_tab,
+                                                           const int32_t *__restrict__ pos_ptr) {
+    extern __shared__ float kr[];  // [channels] rotated key
+    const uint32_t pos = static_cast<uint32_t>(*pos_ptr);
+    const uint32_t D = c.head_dim, half = D / 2;
+    const uint32_t row = pos < c.max_tokens ? pos : 0;
+    const float *ct = cos_tab + static_cast<size_t>(row) * half;
+    const float *st = sin_tab + static_cast<size_t>(row) * half;
+    for (uint32_t p = threadIdx.x; p < q_heads * half; p += blockDim.x) {
+        const uint32_t h = p / half, i = p % half;
+        float *r = q + static_cast<size_t>(h) * D;
+        const float a = r[i], b = r[i + half];
+        r[i] = fmaf(a, ct[i], -(b * st[i]));
+        r[i + half] = fmaf(a, st[i], b * ct[i]);
+    }
+    for (uint32_t p = threadIdx.x; p < c.kv_heads * half; p += blockDim.x) {
+        const uint32_t h = p / half, i = p % half;
+        const float a = k[h * D + i], b = k[h * D + i + half];
+        kr[h * D + i] = fmaf(a, ct[i], -(b * st[i]));
+        kr[h * D + i + half] = fmaf(a, st[i], b * ct[i]);
+    }
+    __syncthreads();
+    if (pos >= c.max_tokens) return;
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, nwaves = blockDim.x / 64;
+    for (uint32_t gi = wave; gi < 2 * c.groups; gi += nwaves) {
+        const bool is_v = gi >= c.groups;
+        const uint32_t g = is_v ? gi - c.groups : gi;
+        const uint32_t ch = g * 64 + lane;
+        const bool valid = ch < c.channels;
+        const float x = valid ? (is_v ? v[ch] : kr[ch]) : 0.0f;
+        float amax = (valid && isfinite(x)) ? fabsf(x) : 0.0f;
+        for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        if (lane == 0) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, pos) + g] = scale;
+        if (valid) {
+            int8_t qv = 0;
+            if (isfinite(x)) {
+                const float sq = x / scale;  // IEEE division, like the CPU path
+                qv = sq >= 127.0f ? 127 : (sq <= -127.0f ? -127 : static_cast<int8_t>(__builtin_rintf(sq)));
+            }
+            (is_v ? c.values : c.keys)[kv_offset(c, pos, ch / D) + ch % D] = qv;
+        }
+    }
+}
+
+}  // namespace
+
+size_t kv_cache_layout(KvCache &c, uint8_t *base) {
+    c.channels = c.kv_heads * c.head_dim;
+    c.groups = (c.channels + 63u) / 64u;
+    c.pages = (c.max_tokens + kKvPageTokens - 1) / kKvPageTokens;
+    const size_t slots = static_cast<size_t>(c.pages) * kKvPageTokens;
+    const size_t value_bytes = (slots * c.channels + 255) & ~static_cast<size_t>(255);
+    const size_t scale_bytes = (slots * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
+    if (base) {
+        c.keys = reinterpret_cast<int8_t *>(base);
+        c.values = reinterpret_cast<int8_t *>(base + value_bytes);
+        c.key_scales = reinterpret_cast<float *>(base + 2 * value_bytes);
+        c.value_scales = reinterpret_cast<float *>(base + 2 * value_bytes + scale_bytes);
+    }
+    return 2 * value_bytes + 2 * scale_bytes;
+}
+
+hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
+                              const float *value, const float *cos_tab, const float *sin_tab,
+                              const int32_t *pos_ptr, hipStream_t stream) {
+    if (c.head_dim % 2 || c.channels > 8192) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(1024), c.channels * sizeof(float), stream, c, query,
+                       query_heads, key, value, cos_tab, sin_tab, pos_ptr);
+    return hipGetLastError();
+}
+
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
                             hipStream_t stream) {
     if (token >= c.max_tokens) return hipErrorInvalidValue;

@@ -1,0 +1,543 @@
+// Resident greedy decoder (include/qwn_hip_decoder.h).
+//
+// One decode step is a fixed kernel sequence that reads the input token and
+// the position from device memory, so it is captured once as a HIP graph and
+// replayed for every token.  Per layer (dense Qwen2-style, semantics of
+// c/qwanto_decode.c:1566-2032):
+//
+//   q,k,v   = W_qkv rmsnorm(x)        one grouped GEMV: every workgroup
+//                                     normalizes and int8-quantizes x itself
+//   RoPE(q, k); Q8 append of k, v     one workgroup
+//   ctx     = attention over the Q8 cache (split-T partials + merge)
+//   x      += W_o ctx                 GEMV quantizing ctx in its prologue,
+//                                     residual added in its epilogue
+//   g,u     = W_gu rmsnorm(x)         grouped GEMV
+//   x      += W_down (silu(g) * u)    GEMV with the SwiGLU in its prologue
+//
+// then logits = E rmsnorm(x) (F16 tied LM head, per-workgroup argmax
+// partials in the epilogue) and one kernel that picks the greedy token,
+// records it and advances the position.  Nothing crosses PCIe per token.
+#include "qwn_context.h"
+#include "qwn_device.h"
+#include "qwn_hip_decoder.h"
+#include "qwn_internal.h"
+
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace qwn {
+
+namespace {
+
+constexpr int kProj = 7;
+enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN };
+
+// x = embedding row of the step's token (feed[pos] when the host supplied
+// one, else the previous step's greedy choice): F16 -> fp32 straight from
+// the LM head's wave-tile layout.  One thread per 8 halves.
+struct EmbedArgs {
+    const uint8_t *payload;
+    size_t tile_payload;
+    uint32_t lanes, rows_per_wave, units, hidden, vocab, max_ctx;
+    const int32_t *feed;
+    const int32_t *state;  // [0] = last greedy token, [1] = position
+    float *x;
+};
+
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= a.units * 4) return;
+    const int32_t pos = a.state[1];
+    int32_t token = (pos >= 0 && static_cast<uint32_t>(pos) < a.max_ctx) ? a.feed[pos] : -1;
+    if (token < 0) token = a.state[0];
+    if (token < 0 || static_cast<uint32_t>(token) >= a.vocab) token = 0;
+    const uint32_t u = idx / 4, q = idx % 4;
+    const UnitAddr ad = unit_addr(static_cast<uint32_t>(token), u, q, a.lanes, a.rows_per_wave, a.units,
+                                  a.tile_payload, 0);
+    const uint4 h = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
+    const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t k0 = u * 32 + q * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (k0 + e < a.hidden) a.x[k0 + e] = half_to_float((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+}
+
+// Greedy token of the step (largest logit, first index on ties), recorded
+// at out_tokens[pos]; the position advances.  One workgroup.
+__global__ __launch_bounds__(1024) void step_end_kernel(const uint64_t *__restrict__ partials, uint32_t n,
+                                                        int32_t *state, int32_t *out_tokens, uint32_t max_ctx) {
+    __shared__ uint64_t red[1024 / kWaveSize];
+    uint64_t key = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) key = partials[i] > key ? partials[i] : key;
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), off);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(key >> 32), off);
+        const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+        key = o > key ? o : key;
+    }
+    if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t best = red[0];
+        for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) best = red[w] > best ? red[w] : best;
+        const int32_t token = best ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+        const int32_t pos = state[1];
+        if (pos >= 0 && static_cast<uint32_t>(pos) < max_ctx) out_tokens[pos] = token;
+        state[0] = token;
+        state[1] = pos + 1;
+    }
+}
+
+}  // namespace
+
+struct Decoder {
+    Context *ctx = nullptr;
+    uint32_t hidden = 0, inter = 0, layers = 0, heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, max_ctx = 0;
+    float eps = 0.0f, attn_scale = 0.0f;
+    std::vector<const DeviceTensor *> proj;
+    const DeviceTensor *embed = nullptr;
+    void *allocation = nullptr;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gate = nullptr,
+          *up = nullptr, *logits = nullptr, *partials = nullptr;
+    float *norms_in = nullptr, *norms_post = nullptr, *final_norm = nullptr, *cos_tab = nullptr,
+          *sin_tab = nullptr;
+    uint64_t *argmax = nullptr;
+    uint32_t argmax_n = 0;
+    int32_t *state = nullptr, *feed = nullptr, *out_tokens = nullptr;
+    std::vector<KvCache> caches;
+    hipGraphExec_t exec = nullptr;
+    bool graph_tried = false;
+    uint32_t position = 0;
+    uint32_t launches = 0;
+    uint64_t weight_bytes = 0;
+};
+
+void destroy_decoder(Decoder *d) {
+    if (!d) return;
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->allocation) (void)hipFree(d->allocation);
+    delete d;
+}
+
+namespace {
+
+Decoder *decoder_of(Context *ctx, const QwnHipDecoderHandle *h) {
+    if (!h || !header_ok(*h) || !h->opaque) return nullptr;
+    auto *d = static_cast<Decoder *>(h->opaque);
+    return std::find(ctx->decoders.begin(), ctx->decoders.end(), d) != ctx->decoders.end() ? d : nullptr;
+}
+
+GemvGroupLaunch group(std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs) {
+    GemvGroupLaunch g;
+    for (const DeviceTensor *t : ts) g.tensors[g.njobs++] = t;
+    int i = 0;
+    for (float *o : outs) g.outputs[i++] = o;
+    return g;
+}
+
+// The launches of one step, in order; `count` only counts them.
+hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
+    uint32_t n = 0;
+    hipError_t e;
+    EmbedArgs ea{};
+    ea.payload = d->embed->payload;
+    ea.tile_payload = d->embed->tile_payload_bytes;
+    ea.lanes = d->embed->lanes;
+    ea.rows_per_wave = d->embed->rows_per_wave;
+    ea.units = d->embed->units;
+    ea.hidden = d->hidden;
+    ea.vocab = d->vocab;
+    ea.max_ctx = d->max_ctx;
+    ea.feed = d->feed;
+    ea.state = d->state;
+    ea.x = d->x;
+    hipLaunchKernelGGL(embed_kernel, dim3((ea.units * 4 + 255) / 256), dim3(256), 0, s, ea);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    ++n;
+    int32_t *pos = d->state + 1;
+    for (uint32_t l = 0; l < d->layers; ++l) {
+        const DeviceTensor *const *w = d->proj.data() + static_cast<size_t>(l) * kProj;
+        GemvGroupLaunch qkv = group({w[P_Q], w[P_K], w[P_V]}, {d->q, d->k, d->v});
+        qkv.input_mode = kInNorm;
+        qkv.x = d->x;
+        qkv.norm = d->norms_in + static_cast<size_t>(l) * d->hidden;
+        qkv.eps = d->eps;
+        if ((e = launch_gemv_group(qkv, s)) != hipSuccess) return e;
+        if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s)) !=
+            hipSuccess)
+            return e;
+        if ((e = launch_attention_at(d->caches[l], d->q, d->attn, d->heads, pos, d->attn_scale, d->partials, s)) !=
+            hipSuccess)
+            return e;
+        GemvGroupLaunch o = group({w[P_O]}, {d->x});
+        o.input_mode = kInF32;
+        o.output_mode = kOutAdd;
+        o.x = d->attn;
+        if ((e = launch_gemv_group(o, s)) != hipSuccess) return e;
+        GemvGroupLaunch gu = group({w[P_GATE], w[P_UP]}, {d->gate, d->up});
+        gu.input_mode = kInNorm;
+        gu.x = d->x;
+        gu.norm = d->norms_post + static_cast<size_t>(l) * d->hidden;
+        gu.eps = d->eps;
+        if ((e = launch_gemv_group(gu, s)) != hipSuccess) return e;
+        GemvGroupLaunch down = group({w[P_DOWN]}, {d->x});
+        down.input_mode = kInSwiglu;
+        down.output_mode = kOutAdd;
+        down.x = d->gate;
+        down.x2 = d->up;
+        if ((e = launch_gemv_group(down, s)) != hipSuccess) return e;
+        n += 7;  // qkv, rope/append, attention split + merge, o, gate/up, down
+    }
+    GemvGroupLaunch head = group({d->embed}, {d->logits});
+    head.input_mode = kInNorm;
+    head.output_mode = kOutArgmax;
+    head.x = d->x;
+    head.norm = d->final_norm;
+    head.eps = d->eps;
+    head.argmax_partials = d->argmax;
+    if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, s, d->argmax, d->argmax_n, d->state,
+                       d->out_tokens, d->max_ctx);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    n += 2;
+    if (count) *count = n;
+    return hipSuccess;
+}
+
+// Runs one step: the captured graph when capture worked, else the kernels.
+hipError_t run_step(Decoder *d) {
+    hipStream_t s = d->ctx->stream;
+    if (!d->graph_tried) {
+        d->graph_tried = true;
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            const hipError_t le = enqueue_step(d, s, nullptr);
+            e = hipStreamEndCapture(s, &g);
+            if (le != hipSuccess) e = le;
+        }
+        if (e == hipSuccess && g) e = hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0);
+        if (g) (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            d->exec = nullptr;
+            (void)hipGetLastError();
+        }
+    }
+    if (d->exec) return hipGraphLaunch(d->exec, s);
+    return enqueue_step(d, s, nullptr);
+}
+
+const DeviceTensor *check_shape(Context *ctx, const QwnCudaTensorHandle &h, int kind, uint32_t rows, uint32_t cols) {
+    ResidentTensor *rt = tensor_of(ctx, h);
+    if (!rt || rt->t.kind != kind || rt->t.rows != rows || rt->t.cols != cols) return nullptr;
+    return &rt->t;
+}
+
+uint64_t logical_bytes(const DeviceTensor &t) { return t.logical_bytes; }
+
+}  // namespace
+
+}  // namespace qwn
+
+using namespace qwn;
+
+extern "C" {
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const QwnHipDecoderDesc *desc,
+                                            QwnHipDecoderHandle *out) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !desc || !out || !header_ok(*desc) || !header_ok(*out) || !desc->projections ||
+        !desc->embedding || !desc->input_norms || !desc->post_norms || !desc->final_norm || desc->hidden == 0 ||
+        desc->layers == 0 || desc->heads == 0 || desc->kv_heads == 0 || desc->heads % desc->kv_heads ||
+        desc->head_dim == 0 || desc->head_dim % 2 || desc->vocab == 0 || desc->max_ctx == 0 ||
+        desc->intermediate == 0) {
+        set_error("invalid decoder description");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    auto *d = new (std::nothrow) Decoder();
+    if (!d) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    d->ctx = ctx;
+    d->hidden = desc->hidden;
+    d->inter = desc->intermediate;
+    d->layers = desc->layers;
+    d->heads = desc->heads;
+    d->kv_heads = desc->kv_heads;
+    d->head_dim = desc->head_dim;
+    d->vocab = desc->vocab;
+    d->max_ctx = desc->max_ctx;
+    d->eps = desc->rms_eps;
+    d->attn_scale = 1.0f / sqrtf(static_cast<float>(desc->head_dim));
+    const uint32_t D = d->hidden, Q = d->heads * d->head_dim, KV = d->kv_heads * d->head_dim, I = d->inter;
+    // weights: one quantized dtype for every projection, shapes of the config
+    ResidentTensor *first = tensor_of(ctx, desc->projections[0]);
+    const int kind = first ? first->t.kind : 0;
+    bool ok = kind == kHvsq2 || kind == kQ4_0;
+    const uint32_t shapes[kProj][2] = {{Q, D}, {KV, D}, {KV, D}, {D, Q}, {I, D}, {I, D}, {D, I}};
+    for (uint32_t l = 0; ok && l < d->layers; ++l)
+        for (int p = 0; ok && p < kProj; ++p) {
+            const DeviceTensor *t = check_shape(ctx, desc->projections[l * kProj + p], kind, shapes[p][0],
+                                                shapes[p][1]);
+            ok = t != nullptr;
+            d->proj.push_back(t);
+            if (t) d->weight_bytes += logical_bytes(*t);
+        }
+    d->embed = ok ? check_shape(ctx, *desc->embedding, kF16, d->vocab, D) : nullptr;
+    if (!ok || !d->embed) {
+        delete d;
+        set_error("decoder weights do not match the configuration (one quantized dtype for all projections, "
+                  "F16 [vocab][hidden] embedding)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    d->weight_bytes += d->embed->logical_bytes;
+
+    // device memory: activations, tables, caches, state
+    std::vector<std::pair<void **, size_t>> parts;
+    auto part = [&](void **p, size_t bytes) { parts.push_back({p, (bytes + 255) & ~static_cast<size_t>(255)}); };
+    part(reinterpret_cast<void **>(&d->x), D * 4);
+    part(reinterpret_cast<void **>(&d->q), Q * 4);
+    part(reinterpret_cast<void **>(&d->k), KV * 4);
+    part(reinterpret_cast<void **>(&d->v), KV * 4);
+    part(reinterpret_cast<void **>(&d->attn), Q * 4);
+    part(reinterpret_cast<void **>(&d->gate), static_cast<size_t>(I) * 4);
+    part(reinterpret_cast<void **>(&d->up), static_cast<size_t>(I) * 4);
+    part(reinterpret_cast<void **>(&d->logits), static_cast<size_t>(d->vocab) * 4);
+    part(reinterpret_cast<void **>(&d->norms_in), static_cast<size_t>(d->layers) * D * 4);
+    part(reinterpret_cast<void **>(&d->norms_post), static_cast<size_t>(d->layers) * D * 4);
+    part(reinterpret_cast<void **>(&d->final_norm), D * 4);
+    const uint32_t half = d->head_dim / 2;
+    part(reinterpret_cast<void **>(&d->cos_tab), static_cast<size_t>(d->max_ctx) * half * 4);
+    part(reinterpret_cast<void **>(&d->sin_tab), static_cast<size_t>(d->max_ctx) * half * 4);
+    part(reinterpret_cast<void **>(&d->state), 2 * 4);
+    part(reinterpret_cast<void **>(&d->feed), static_cast<size_t>(d->max_ctx) * 4);
+    part(reinterpret_cast<void **>(&d->out_tokens), static_cast<size_t>(d->max_ctx) * 4);
+    // attention partials of the device-position kernels
+    KvCache proto;
+    proto.max_tokens = d->max_ctx;
+    proto.kv_heads = d->kv_heads;
+    proto.head_dim = d->head_dim;
+    const size_t cache_bytes = (kv_cache_layout(proto, nullptr) + 255) & ~static_cast<size_t>(255);
+    part(reinterpret_cast<void **>(&d->partials), attention_at_workspace_floats(proto, d->heads) * 4);
+    GemvGroupLaunch head = group({d->embed}, {nullptr});
+    head.outputs[0] = reinterpret_cast<float *>(16);  // validity only: a non-null placeholder
+    head.input_mode = kInNorm;
+    head.output_mode = kOutArgmax;
+    head.x = reinterpret_cast<const float *>(16);
+    head.norm = reinterpret_cast<const float *>(16);
+    head.argmax_partials = reinterpret_cast<uint64_t *>(16);
+    d->argmax_n = gemv_group_grid(head);
+    part(reinterpret_cast<void **>(&d->argmax), static_cast<size_t>(d->argmax_n) * 8);
+    // every grouped launch of the step must accept its fused input
+    bool fits = d->argmax_n > 0;
+    {
+        auto probe = [&](std::initializer_list<const DeviceTensor *> ts, uint32_t mode) {
+            GemvGroupLaunch g = group(ts, {});
+            for (int i = 0; i < g.njobs; ++i) g.outputs[i] = reinterpret_cast<float *>(16);
+            g.input_mode = mode;
+            g.x = g.x2 = g.norm = reinterpret_cast<const float *>(16);
+            return gemv_group_grid(g) > 0;
+        };
+        const DeviceTensor *const *w = d->proj.data();
+        fits = fits && probe({w[P_Q], w[P_K], w[P_V]}, kInNorm) && probe({w[P_O]}, kInF32) &&
+               probe({w[P_GATE], w[P_UP]}, kInNorm) && probe({w[P_DOWN]}, kInSwiglu);
+    }
+    if (!fits || KV > 8192) {
+        delete d;
+        set_error("decoder shapes exceed the fused GEMV limits (columns a multiple of 32, at most 16384)");
+        return QWN_CUDA_STATUS_UNSUPPORTED;
+    }
+    size_t total = 0;
+    for (auto &p : parts) total += p.second;
+    const size_t act_bytes = total;
+    total += cache_bytes * d->layers;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc(&d->allocation, total);
+    if (e != hipSuccess) {
+        delete d;
+        return hip_fail("decoder allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+    }
+    uint8_t *base = static_cast<uint8_t *>(d->allocation);
+    size_t off = 0;
+    for (auto &p : parts) {
+        *p.first = base + off;
+        off += p.second;
+    }
+    for (uint32_t l = 0; l < d->layers; ++l) {
+        KvCache c;
+        c.max_tokens = d->max_ctx;
+        c.kv_heads = d->kv_heads;
+        c.head_dim = d->head_dim;
+        kv_cache_layout(c, base + act_bytes + static_cast<size_t>(l) * cache_bytes);
+        d->caches.push_back(c);
+    }
+    // host tables: norms, RoPE (c/qwanto_decode.c:601-625), empty feed
+    std::vector<float> cs(static_cast<size_t>(d->max_ctx) * half), sn(cs.size());
+    for (uint32_t p = 0; p < d->max_ctx; ++p)
+        for (uint32_t i = 0; i < half; ++i) {
+            const float angle = static_cast<float>(p) *
+                                powf(desc->rope_theta, -2.0f * static_cast<float>(i) / static_cast<float>(2 * half));
+            cs[static_cast<size_t>(p) * half + i] = cosf(angle);
+            sn[static_cast<size_t>(p) * half + i] = sinf(angle);
+        }
+    std::vector<int32_t> feed(d->max_ctx, -1);
+    const int32_t state0[2] = {0, 0};
+    hipStream_t s = ctx->stream;
+    if (e == hipSuccess) e = hipMemsetAsync(base, 0, total, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->norms_in, desc->input_norms, static_cast<size_t>(d->layers) * D * 4,
+                           hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->norms_post, desc->post_norms, static_cast<size_t>(d->layers) * D * 4,
+                           hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->final_norm, desc->final_norm, D * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->feed, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->state, state0, sizeof(state0), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        destroy_decoder(d);
+        return hip_fail("decoder set-up", e);
+    }
+    d->launches = 7 * d->layers + 3;  // embed, 7 per layer, LM head, step end
+    ctx->decoders.push_back(d);
+    std::memset(out, 0, sizeof(*out));
+    qwn_cuda_abi_header_init(&out->header, sizeof(*out));
+    out->opaque = d;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_destroy(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d) {
+        set_error("invalid decoder handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->decoders.erase(std::find(ctx->decoders.begin(), ctx->decoders.end(), d));
+    destroy_decoder(d);
+    h->opaque = nullptr;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_reset(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d) {
+        set_error("invalid decoder handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const int32_t state0[2] = {0, 0};
+    std::vector<int32_t> feed(d->max_ctx, -1);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->state, state0, sizeof(state0), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->feed, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail("decoder reset", e);
+    d->position = 0;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h, int32_t token,
+                                             float *logits, int32_t *next_token) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || token < 0 || static_cast<uint32_t>(token) >= d->vocab || d->position >= d->max_ctx) {
+        set_error("invalid decoder step (token out of range or context full)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = ctx->stream;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->feed + d->position, &token, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = run_step(d);
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, d->logits, static_cast<size_t>(d->vocab) * 4, hipMemcpyDeviceToHost, s);
+    int32_t st[2] = {0, 0};
+    if (e == hipSuccess) e = hipMemcpyAsync(st, d->state, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail("decoder step", e);
+    d->position++;
+    if (next_token) *next_token = st[0];
+    ctx->telemetry.gpu_matmul_count += 4ull * d->layers + 1;
+    ctx->telemetry.gpu_kernel_launch_count += d->launches;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                              const int32_t *prompt, uint32_t prompt_count, uint32_t max_new,
+                                              int32_t *tokens, QwnHipDecoderStats *stats) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !prompt || prompt_count == 0 || (max_new && !tokens) || (stats && !header_ok(*stats))) {
+        set_error("invalid generate request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || static_cast<uint64_t>(d->position) + prompt_count + max_new > d->max_ctx) {
+        set_error("generation does not fit the decoder's context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < prompt_count; ++i)
+        if (prompt[i] < 0 || static_cast<uint32_t>(prompt[i]) >= d->vocab) {
+            set_error("prompt token %u out of range", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+    hipStream_t s = ctx->stream;
+    const uint32_t p0 = d->position;
+    std::vector<int32_t> feed(d->max_ctx - p0, -1);
+    std::memcpy(feed.data(), prompt, static_cast<size_t>(prompt_count) * 4);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->feed + p0, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t i = 0; e == hipSuccess && i < prompt_count; ++i) e = run_step(d);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    const auto t1 = std::chrono::steady_clock::now();
+    for (uint32_t i = 0; e == hipSuccess && i < max_new; ++i) e = run_step(d);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    const auto t2 = std::chrono::steady_clock::now();
+    if (e == hipSuccess && max_new)
+        e = hipMemcpy(tokens, d->out_tokens + p0 + prompt_count - 1, static_cast<size_t>(max_new) * 4,
+                      hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail("decoder generate", e);
+    d->position = p0 + prompt_count + max_new;
+    const uint64_t steps = prompt_count + max_new;
+    ctx->telemetry.gpu_matmul_count += steps * (4ull * d->layers + 1);
+    ctx->telemetry.gpu_kernel_launch_count += steps * d->launches;
+    if (stats) {
+        std::memset(stats, 0, sizeof(*stats));
+        qwn_cuda_abi_header_init(&stats->header, sizeof(*stats));
+        stats->prompt_tokens = prompt_count;
+        stats->generated_tokens = max_new;
+        stats->position = d->position;
+        stats->launches_per_step = d->launches;
+        stats->prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        stats->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+        stats->weight_bytes_per_step = d->weight_bytes;
+        stats->graph = d->exec ? 1u : 0u;
+    }
+    return QWN_CUDA_STATUS_OK;
+}
+
+}  // extern "C"

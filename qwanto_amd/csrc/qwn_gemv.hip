@@ -233,51 +233,170 @@ __device__ __forceinline__ int q4_block_dot(uint4 n, uint4 a0, uint4 a1) {
 }
 
 struct GemvArgs {
-    const uint8_t *payload;
-    const uint8_t *meta;
+    // jobs (tensors sharing the input); job i owns workgroups
+    // [job_block[i], job_block[i+1]), job_block[njobs] = grid
+    const uint8_t *payload[kMaxGroup];
+    const uint8_t *meta[kMaxGroup];
+    float *output[kMaxGroup];
+    uint32_t rows[kMaxGroup];
+    uint32_t job_block[kMaxGroup + 1];
+    uint32_t njobs;
+    // lane plan shared by the jobs
     size_t tile_payload_bytes;
     size_t tile_meta_bytes;
-    const uint8_t *image;
-    const float *scales;
-    float scale;
-    float *output;
-    uint32_t rows;
     uint32_t units;
     uint32_t lanes;
     uint32_t rows_per_wave;
+    uint32_t input_mode;
+    uint32_t output_mode;
+    // image input
+    const uint8_t *image;
+    const float *scales;
+    float scale;
     uint32_t ntok;
     uint32_t image_stride;
     uint32_t image_bytes;
+    // fp32 input
+    const float *x;
+    const float *x2;
+    const float *norm;
+    float eps;
+    uint32_t cols;
+    float *scale_out;
+    // output
     uint32_t output_stride;
+    uint64_t *argmax_partials;
 };
 
-template <int KIND, int MT, int UPL>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+// Separately rounded product and sum (never contracted into an fma).
+__device__ __forceinline__ float mul_rounded(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float add_rounded(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+
+// Compiler-level fence plus the hardware barrier, without the vmcnt(0)
+// that __syncthreads() implies (the weight stream stays in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Workgroup reductions for the fused prologue: every thread gets the same
+// result, combined in wave order (identical in every workgroup).
+__device__ __forceinline__ float wg_sum(float v, float *red, uint32_t waves) {
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = v;
+    lds_barrier();
+    float s = red[0];
+    for (uint32_t w = 1; w < waves; ++w) s += red[w];
+    return s;
+}
+__device__ __forceinline__ float wg_max(float v, float *red, uint32_t waves) {
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = v;
+    lds_barrier();
+    float s = red[0];
+    for (uint32_t w = 1; w < waves; ++w) s = fmaxf(s, red[w]);
+    return s;
+}
+
+// Argmax key: larger value wins, then the smaller row (the CPU's
+// first-maximum rule, c/qwanto_decode.c:2048-2065); NaN never wins.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t row) {
+    if (v != v) return 0;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (static_cast<uint64_t>(ord) << 32) | (0xffffffffu - row);
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// FUSED (one token only): the input is an fp32 vector turned into the LDS
+// image by every workgroup; otherwise prebuilt images are copied to LDS.
+// Workgroups of up to kGemvMaxWaves waves where a lane's registers allow it
+// (UPL <= 4), else kGemvWaves.
+__host__ __device__ constexpr int max_waves_for(int upl) { return upl <= 4 ? kGemvMaxWaves : kGemvWaves; }
+
+template <int KIND, int MT, int UPL, bool FUSED>
+__global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float red[2][kGemvMaxWaves];
+    __shared__ uint64_t red_key[kGemvMaxWaves];
     constexpr int CH = 4;
+    const uint32_t W = blockDim.x / kWaveSize;
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = threadIdx.x / kWaveSize;
     const uint32_t L = a.lanes;
     const uint32_t grp = lane / L;
     const uint32_t j = lane - grp * L;
-    const uint32_t tile = blockIdx.x * kGemvWaves + wave;
-    const uint32_t row = tile * a.rows_per_wave + grp;
-    const bool active = grp < a.rows_per_wave && row < a.rows;
 
-    // 0. Token scales (uniform loads, needed only at the very end but
-    //    issued first so their latency hides under the weight stream), then
-    //    the activation images -> LDS (direct loads).
+    // Job of this workgroup (uniform select chain over kernel arguments).
+    uint32_t job = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (static_cast<uint32_t>(i) < a.njobs && blockIdx.x >= a.job_block[i]) job = i;
+    const uint8_t *payload = a.payload[0];
+    const uint8_t *meta = a.meta[0];
+    float *output = a.output[0];
+    uint32_t rows = a.rows[0], first = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (job == static_cast<uint32_t>(i)) {
+            payload = a.payload[i];
+            meta = a.meta[i];
+            output = a.output[i];
+            rows = a.rows[i];
+            first = a.job_block[i];
+        }
+    const uint32_t tile = (blockIdx.x - first) * W + wave;
+    const uint32_t row = tile * a.rows_per_wave + grp;
+    const bool active = grp < a.rows_per_wave && row < rows;
+    const bool writer = active && j == L - 1;
+    constexpr bool fused = FUSED && MT == 1;
+
+    // 0. Loads whose results are needed late (token scales, the residual),
+    //    then the input: image -> LDS by direct loads, or this thread's
+    //    32-element block of the fp32 vector(s) into registers.
     float tok_scale[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) tok_scale[t] = a.scales ? a.scales[t < static_cast<int>(a.ntok) ? t : 0] : a.scale;
-    issue_image_copy(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
+    float resid = 0.0f;
+    if (a.output_mode == kOutAdd && writer) resid = output[row];
+    const uint32_t nblk = a.units * unit_elems(KIND) / 32;  // 32-blocks in the image
+    const uint32_t nvalid = a.cols / 32;                     // blocks holding input values
+    const uint32_t b = threadIdx.x;
+    float4 xv[8], x2v[8];
+    if constexpr (fused) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (b < nvalid ? b * 32 : 0));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = src[i];
+        if (a.input_mode != kInF32) {
+            const float *p2 = a.input_mode == kInNorm ? a.norm : a.x2;
+            const float4 *src2 = reinterpret_cast<const float4 *>(p2 + (b < nvalid ? b * 32 : 0));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x2v[i] = src2[i];
+        }
+    } else {
+        issue_image_copy(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 1. Every weight load of this lane, metadata before codes.  Lanes
     //    without a unit load from the tile start instead of branching, so
     //    the loads stay one unconditional burst.
-    const uint8_t *tile_p = a.payload + tile * a.tile_payload_bytes;
-    const uint8_t *tile_m = a.meta + tile * a.tile_meta_bytes;
+    const uint8_t *tile_p = payload + tile * a.tile_payload_bytes;
+    const uint8_t *tile_m = meta + tile * a.tile_meta_bytes;
     // Unit slot i holds units i*L + j, n = min(L, units - i*L) of them,
     // stored compactly (qwn_internal.h).
     const size_t R = a.rows_per_wave;
@@ -302,13 +421,78 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. Wait for this wave's image loads only (vector memory loads retire
-    //    in issue order), then for every wave's share of the copy.  A bare
-    //    s_barrier: __syncthreads() would also wait for the weight loads.
-    wait_vmcnt<(KIND == kF16 ? 4 : 5) * UPL>();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
+    // 2. The LDS image.  Fused: this thread's block after the norm/SwiGLU,
+    //    quantized with the workgroup-wide scale (c/qwanto_kernels.c:354-433)
+    //    while the weight loads are in flight.  Image: wait for this wave's
+    //    direct loads only (vector loads retire in issue order), then for
+    //    every wave's share.
+    if constexpr (fused) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[4 * i] = xv[i].x; v[4 * i + 1] = xv[i].y; v[4 * i + 2] = xv[i].z; v[4 * i + 3] = xv[i].w;
+        }
+        const bool has = b < nvalid;
+        if (a.input_mode == kInNorm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
+            ss = wg_sum(has ? ss : 0.0f, red[0], W);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.cols) + a.eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[4 * i] = (v[4 * i] * inv) * x2v[i].x;
+                v[4 * i + 1] = (v[4 * i + 1] * inv) * x2v[i].y;
+                v[4 * i + 2] = (v[4 * i + 2] * inv) * x2v[i].z;
+                v[4 * i + 3] = (v[4 * i + 3] * inv) * x2v[i].w;
+            }
+        } else if (a.input_mode == kInSwiglu) {
+            const float u[32] = {x2v[0].x, x2v[0].y, x2v[0].z, x2v[0].w, x2v[1].x, x2v[1].y, x2v[1].z, x2v[1].w,
+                                 x2v[2].x, x2v[2].y, x2v[2].z, x2v[2].w, x2v[3].x, x2v[3].y, x2v[3].z, x2v[3].w,
+                                 x2v[4].x, x2v[4].y, x2v[4].z, x2v[4].w, x2v[5].x, x2v[5].y, x2v[5].z, x2v[5].w,
+                                 x2v[6].x, x2v[6].y, x2v[6].z, x2v[6].w, x2v[7].x, x2v[7].y, x2v[7].z, x2v[7].w};
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = (v[i] / (1.0f + expf(-v[i]))) * u[i];
+        }
+        if (!has) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+        }
+        if (KIND == kF16) {
+            if (b < nblk) {
+                float4 *dst = reinterpret_cast<float4 *>(smem + b * 144);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            }
+        } else {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            amax = wg_max(amax, red[1], W);
+            // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
+            const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / scale;
+            tok_scale[0] = scale;
+            if (a.scale_out && blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = scale;
+            if (b < nblk) {
+                uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const float c = fminf(127.0f, fmaxf(-127.0f, v[i] * inv));
+                    w[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(c))))
+                                 << (8 * (i & 3));
+                }
+                put_block32<KIND>(smem, a.units, b, w);
+            }
+        }
+        lds_barrier();
+    } else {
+        wait_vmcnt<(KIND == kF16 ? 4 : 5) * UPL>();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
 
     // 3. Dot products.
     const uint32_t ib = a.image_bytes;
@@ -354,9 +538,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
                 const int4 corr = *reinterpret_cast<const int4 *>(img + act_bytes + u * 16);
                 const int cb[4] = {corr.x, corr.y, corr.z, corr.w};
 #pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const float d = half_to_float(sc[b >> 1] >> (16 * (b & 1)));
-                    const int raw = q4_block_dot(pay[i][b], at[2 * b], at[2 * b + 1]) - cb[b];
+                for (int b4 = 0; b4 < 4; ++b4) {
+                    const float d = half_to_float(sc[b4 >> 1] >> (16 * (b4 & 1)));
+                    const int raw = q4_block_dot(pay[i][b4], at[2 * b4], at[2 * b4 + 1]) - cb[b4];
                     acc[t] = fmaf(static_cast<float>(raw), d, acc[t]);
                 }
             }
@@ -389,14 +573,53 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     //    holds the row total and writes it.
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = group_sum(acc[t], L);
-    if (active && j == L - 1) {
+    float first_out = 0.0f;
+    if (writer) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             if (static_cast<uint32_t>(t) >= a.ntok) break;
             float s = acc[t];
-            if (KIND != kF16) s *= tok_scale[t];
-            a.output[static_cast<size_t>(t) * a.output_stride + row] = s;
+            // rounded product, then the residual add: the CPU stores the
+            // projection before vec_add(x, y) (c/qwanto_decode.c:1925, 1955), so no
+            // contraction into one fused multiply-add here
+            if (KIND != kF16) s = mul_rounded(s, tok_scale[t]);
+            if (MT == 1 && a.output_mode == kOutAdd) s = add_rounded(resid, s);
+            if (t == 0) first_out = s;
+            output[static_cast<size_t>(t) * a.output_stride + row] = s;
         }
+    }
+    if (MT == 1 && a.output_mode == kOutArgmax) {
+        uint64_t key = writer ? argmax_key(first_out, row) : 0;
+        for (int off = kWaveSize / 2; off > 0; off >>= 1) {
+            const uint64_t o = shfl_xor_u64(key, off);
+            key = o > key ? o : key;
+        }
+        if (lane == 0) red_key[wave] = key;
+        lds_barrier();
+        if (threadIdx.x == 0) {
+            uint64_t best = red_key[0];
+            for (uint32_t w = 1; w < W; ++w) best = red_key[w] > best ? red_key[w] : best;
+            a.argmax_partials[blockIdx.x] = best;
+        }
+    }
+}
+
+// Winner of the argmax partials: one workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void argmax_finish_kernel(const uint64_t *__restrict__ partials, uint32_t n,
+                                                             int32_t *index_out) {
+    __shared__ uint64_t red_key[1024 / kWaveSize];
+    uint64_t key = 0;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) key = partials[i] > key ? partials[i] : key;
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) {
+        const uint64_t o = shfl_xor_u64(key, off);
+        key = o > key ? o : key;
+    }
+    if (threadIdx.x % kWaveSize == 0) red_key[threadIdx.x / kWaveSize] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t best = red_key[0];
+        for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) best = red_key[w] > best ? red_key[w] : best;
+        *index_out = best ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
     }
 }
 
@@ -407,13 +630,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 template <int KIND>
 __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t *out, uint32_t out_row) {
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= a.rows * a.units) return;
+    if (idx >= a.rows[0] * a.units) return;
     const uint32_t row = idx / a.units, u = idx % a.units;
     uint4 pay[4];
     for (uint32_t q = 0; q < 4; ++q) {
         const UnitAddr ad = unit_addr(row, u, q, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
                                       a.tile_meta_bytes);
-        pay[q] = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
+        pay[q] = *reinterpret_cast<const uint4 *>(a.payload[0] + ad.payload);
     }
     const uint8_t *img = a.image;
     const int32_t *sums = reinterpret_cast<const int32_t *>(img + a.units * unit_lds_bytes(KIND));
@@ -501,52 +724,62 @@ __global__ void repack_kernel(RepackArgs r) {
 }
 
 template <int KIND, int MT, int UPL>
-hipError_t launch_one(const GemvPlan &p, const GemvArgs &args, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_kernel<KIND, MT, UPL>), dim3(p.grid), dim3(kGemvThreads), p.lds_bytes,
-                       stream, args);
+hipError_t launch_one(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, hipStream_t stream) {
+    if constexpr (MT == 1) {
+        if (args.input_mode != kInImage) {
+            hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, true>), dim3(grid), dim3(threads), lds, stream, args);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv_kernel<KIND, MT, UPL, false>), dim3(grid), dim3(threads), lds, stream, args);
     return hipGetLastError();
 }
 
 template <int KIND, int MT>
-hipError_t dispatch_upl(const GemvPlan &p, const GemvArgs &args, int upl, hipStream_t stream) {
+hipError_t dispatch_upl(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int upl,
+                        hipStream_t stream) {
     switch (upl) {
-    case 1: return launch_one<KIND, MT, 1>(p, args, stream);
-    case 2: return launch_one<KIND, MT, 2>(p, args, stream);
-    case 3: return launch_one<KIND, MT, 3>(p, args, stream);
-    case 4: return launch_one<KIND, MT, 4>(p, args, stream);
-    case 5: return launch_one<KIND, MT, 5>(p, args, stream);
-    case 6: return launch_one<KIND, MT, 6>(p, args, stream);
-    case 8: return launch_one<KIND, MT, 8>(p, args, stream);
-    case 10: return launch_one<KIND, MT, 10>(p, args, stream);
-    case 12: return launch_one<KIND, MT, 12>(p, args, stream);
-    case 16: return launch_one<KIND, MT, 16>(p, args, stream);
+    case 1: return launch_one<KIND, MT, 1>(grid, threads, lds, args, stream);
+    case 2: return launch_one<KIND, MT, 2>(grid, threads, lds, args, stream);
+    case 3: return launch_one<KIND, MT, 3>(grid, threads, lds, args, stream);
+    case 4: return launch_one<KIND, MT, 4>(grid, threads, lds, args, stream);
+    case 5: return launch_one<KIND, MT, 5>(grid, threads, lds, args, stream);
+    case 6: return launch_one<KIND, MT, 6>(grid, threads, lds, args, stream);
+    case 8: return launch_one<KIND, MT, 8>(grid, threads, lds, args, stream);
+    case 10: return launch_one<KIND, MT, 10>(grid, threads, lds, args, stream);
+    case 12: return launch_one<KIND, MT, 12>(grid, threads, lds, args, stream);
+    case 16: return launch_one<KIND, MT, 16>(grid, threads, lds, args, stream);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <int KIND>
-hipError_t dispatch_mt(const GemvPlan &p, const GemvArgs &args, int upl, hipStream_t stream) {
-    switch (p.tokens) {
-    case 1: return dispatch_upl<KIND, 1>(p, args, upl, stream);
-    case 2: return dispatch_upl<KIND, 2>(p, args, upl, stream);
-    case 4: return dispatch_upl<KIND, 4>(p, args, upl, stream);
-    case 8: return dispatch_upl<KIND, 8>(p, args, upl, stream);
-    case 16: return dispatch_upl<KIND, 16>(p, args, upl, stream);
+hipError_t dispatch_mt(int mt, uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int upl,
+                       hipStream_t stream) {
+    switch (mt) {
+    case 1: return dispatch_upl<KIND, 1>(grid, threads, lds, args, upl, stream);
+    case 2: return dispatch_upl<KIND, 2>(grid, threads, lds, args, upl, stream);
+    case 4: return dispatch_upl<KIND, 4>(grid, threads, lds, args, upl, stream);
+    case 8: return dispatch_upl<KIND, 8>(grid, threads, lds, args, upl, stream);
+    case 16: return dispatch_upl<KIND, 16>(grid, threads, lds, args, upl, stream);
     default: return hipErrorInvalidValue;
     }
 }
 
 GemvArgs args_of(const DeviceTensor &t) {
     GemvArgs a{};
-    a.payload = t.payload;
-    a.meta = t.meta;
+    a.payload[0] = t.payload;
+    a.meta[0] = t.meta;
+    a.rows[0] = t.rows;
+    a.njobs = 1;
     a.tile_payload_bytes = t.tile_payload_bytes;
     a.tile_meta_bytes = t.tile_meta_bytes;
-    a.rows = t.rows;
     a.units = t.units;
     a.lanes = t.lanes;
     a.rows_per_wave = t.rows_per_wave;
     a.image_bytes = static_cast<uint32_t>(image_bytes(t.kind, t.units));
+    a.cols = t.cols;
+    a.scale = 1.0f;
     return a;
 }
 
@@ -572,8 +805,9 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     t.upl = upl;
     t.rows_per_wave = kWaveSize / lanes;
     t.tiles = (t.rows + t.rows_per_wave - 1) / t.rows_per_wave;
-    // whole workgroups of tiles, so a workgroup never reads past the end
-    t.tiles = (t.tiles + kGemvWaves - 1) / kGemvWaves * kGemvWaves;
+    // whole workgroups of tiles for every launch width, so a workgroup
+    // never reads past the end
+    t.tiles = (t.tiles + kTilePad - 1) / kTilePad * kTilePad;
     // compact tiles: only real units are stored (idle lanes load nothing new)
     t.tile_payload_bytes = static_cast<size_t>(t.rows_per_wave) * t.units * t.chunks * 16;
     t.tile_meta_bytes = t.kind == kF16 ? 0 : static_cast<size_t>(t.rows_per_wave) * t.units * 8;
@@ -587,10 +821,13 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
 // two covering the row, at most 64), so the post-load work per lane is
 // short and the grid is large; longer rows take more units per lane.
 // Idle lanes cost VALU slots but no memory traffic (compact tiles).
+//   F16 rows (the LM head) take about four units per lane instead: more rows
+//   per workgroup share one fp32 activation image.
 bool layout_tensor(DeviceTensor &t) {
     if (!set_units(t)) return false;
+    const uint32_t target = t.kind == kF16 ? (t.units + 3) / 4 : t.units;
     uint32_t L = 1;
-    while (L < t.units && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
+    while (L < target && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
     const uint32_t need = (t.units + L - 1) / L;
     for (int w : kUplWidths)
         if (static_cast<uint32_t>(w) >= need) return layout_tensor_with(t, L, static_cast<uint32_t>(w));
@@ -667,13 +904,11 @@ hipError_t launch_quantize_image(const DeviceTensor &t, const float *x, uint32_t
 
 hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
     const DeviceTensor &t = *g.tensor;
-    GemvArgs args = args_of(t);
-    args.output_stride = g.output_stride;
-    args.image = static_cast<const uint8_t *>(g.image);
-    args.image_stride = g.image_stride;
-
     if (g.debug_sums) {
         if (t.kind == kF16) return hipErrorInvalidValue;
+        GemvArgs args = args_of(t);
+        args.image = static_cast<const uint8_t *>(g.image);
+        args.image_stride = g.image_stride;
         const size_t n = static_cast<size_t>(t.rows) * t.units;
         const uint32_t out_row = t.kind == kHvsq2 ? t.units * 8 : (t.cols + 31) / 32;
         if (t.kind == kHvsq2)
@@ -684,22 +919,130 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
                                dim3(kGemvThreads), 0, stream, args, g.debug_sums, out_row);
         return hipGetLastError();
     }
+    GemvGroupLaunch gg;
+    gg.njobs = 1;
+    gg.tensors[0] = g.tensor;
+    gg.outputs[0] = g.output;
+    gg.image = g.image;
+    gg.image_stride = g.image_stride;
+    gg.scales = g.scales;
+    gg.scale = g.scale;
+    gg.batch = g.batch;
+    gg.output_stride = g.output_stride;
+    return launch_gemv_group(gg, stream);
+}
 
+namespace {
+
+// Workgroup width: the fused prologue needs a thread per 32-block of the
+// input; otherwise wider workgroups only when the grid stays >= 2 per CU.
+int choose_waves(const GemvGroupLaunch &g, uint32_t total_tiles) {
+    const DeviceTensor &t = *g.tensors[0];
+    if (g.waves) return g.waves;
+    const int wmax = max_waves_for(static_cast<int>(t.upl));
+    const uint32_t nblk = t.units * unit_elems(t.kind) / 32;
+    int w = kGemvWaves;
+    if (g.input_mode != kInImage)
+        while (static_cast<uint32_t>(w) * kWaveSize < nblk && w < wmax) w *= 2;
+    while (w < wmax && total_tiles / (2 * w) >= 512) w *= 2;
+    return w;
+}
+
+bool group_valid(const GemvGroupLaunch &g) {
+    if (g.njobs < 1 || g.njobs > kMaxGroup) return false;
+    const DeviceTensor &t0 = *g.tensors[0];
+    for (int i = 0; i < g.njobs; ++i) {
+        const DeviceTensor &t = *g.tensors[i];
+        if (!g.tensors[i] || !g.outputs[i] || t.kind != t0.kind || t.cols != t0.cols || t.units != t0.units ||
+            t.lanes != t0.lanes || t.upl != t0.upl || t.rows_per_wave != t0.rows_per_wave)
+            return false;
+    }
+    if (g.input_mode != kInImage) {
+        if (g.batch != 1 || !g.x || t0.cols % 32 != 0) return false;
+        if (g.input_mode == kInNorm && !g.norm) return false;
+        if (g.input_mode == kInSwiglu && !g.x2) return false;
+        if (t0.units * unit_elems(t0.kind) / 32 >
+            static_cast<uint32_t>(kWaveSize * max_waves_for(static_cast<int>(t0.upl))))
+            return false;
+    } else if (!g.image) {
+        return false;
+    }
+    if (g.output_mode == kOutArgmax && (g.batch != 1 || !g.argmax_partials || g.njobs != 1)) return false;
+    if (g.output_mode == kOutAdd && g.batch != 1) return false;
+    return true;
+}
+
+}  // namespace
+
+uint32_t gemv_group_grid(const GemvGroupLaunch &g) {
+    if (!group_valid(g)) return 0;
+    uint32_t tiles = 0;
+    for (int i = 0; i < g.njobs; ++i) tiles += g.tensors[i]->tiles;
+    const int w = choose_waves(g, tiles);
+    return tiles / w;
+}
+
+hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
+    if (!group_valid(g)) return hipErrorInvalidValue;
+    const DeviceTensor &t = *g.tensors[0];
+    GemvArgs args = args_of(t);
+    uint32_t tiles = 0;
+    for (int i = 0; i < g.njobs; ++i) tiles += g.tensors[i]->tiles;
+    const int w = choose_waves(g, tiles);
+    if ((w != 4 && w != 8) || w > max_waves_for(static_cast<int>(t.upl))) return hipErrorInvalidValue;
+    args.njobs = static_cast<uint32_t>(g.njobs);
+    uint32_t blk = 0;
+    for (int i = 0; i < g.njobs; ++i) {
+        const DeviceTensor &ti = *g.tensors[i];
+        if (ti.tiles % w) return hipErrorInvalidValue;
+        args.payload[i] = ti.payload;
+        args.meta[i] = ti.meta;
+        args.output[i] = g.outputs[i];
+        args.rows[i] = ti.rows;
+        args.job_block[i] = blk;
+        blk += ti.tiles / w;
+    }
+    for (int i = g.njobs; i <= kMaxGroup; ++i) args.job_block[i] = blk;
+    const uint32_t grid = blk;
+    const uint32_t threads = static_cast<uint32_t>(w) * kWaveSize;
+    args.input_mode = g.input_mode;
+    args.output_mode = g.output_mode;
+    args.output_stride = g.output_stride;
+    args.argmax_partials = g.argmax_partials;
+    if (g.input_mode != kInImage) {
+        args.x = g.x;
+        args.x2 = g.x2;
+        args.norm = g.norm;
+        args.eps = g.eps;
+        args.scale_out = g.scale_out;
+        args.ntok = 1;
+        const size_t lds = image_bytes(t.kind, t.units);
+        if (lds > kGemvLdsLimit) return hipErrorInvalidValue;
+        if (t.kind == kHvsq2) return dispatch_mt<kHvsq2>(1, grid, threads, lds, args, t.upl, stream);
+        if (t.kind == kQ4_0) return dispatch_mt<kQ4_0>(1, grid, threads, lds, args, t.upl, stream);
+        return dispatch_mt<kF16>(1, grid, threads, lds, args, t.upl, stream);
+    }
     const GemvPlan p = plan_gemv(t, static_cast<int>(g.batch));
     if (p.tokens == 0 || p.lds_bytes > kGemvLdsLimit) return hipErrorInvalidValue;
     for (uint32_t t0 = 0; t0 < g.batch; t0 += p.tokens) {
         args.ntok = std::min<uint32_t>(p.tokens, g.batch - t0);
         args.image = static_cast<const uint8_t *>(g.image) + static_cast<size_t>(t0) * g.image_stride;
+        args.image_stride = g.image_stride;
         args.scales = g.scales ? g.scales + t0 : nullptr;
         args.scale = g.scale;
-        args.output = g.output + static_cast<size_t>(t0) * g.output_stride;
+        for (int i = 0; i < g.njobs; ++i) args.output[i] = g.outputs[i] + static_cast<size_t>(t0) * g.output_stride;
         hipError_t e;
-        if (t.kind == kHvsq2) e = dispatch_mt<kHvsq2>(p, args, t.upl, stream);
-        else if (t.kind == kQ4_0) e = dispatch_mt<kQ4_0>(p, args, t.upl, stream);
-        else e = dispatch_mt<kF16>(p, args, t.upl, stream);
+        if (t.kind == kHvsq2) e = dispatch_mt<kHvsq2>(p.tokens, grid, threads, p.lds_bytes, args, t.upl, stream);
+        else if (t.kind == kQ4_0) e = dispatch_mt<kQ4_0>(p.tokens, grid, threads, p.lds_bytes, args, t.upl, stream);
+        else e = dispatch_mt<kF16>(p.tokens, grid, threads, p.lds_bytes, args, t.upl, stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, stream, partials, n, index_out);
+    return hipGetLastError();
 }
 
 }  // namespace qwn

@@ -37,10 +37,14 @@ namespace qwn {
 enum WeightKind : int { kHvsq2 = 1, kQ4_0 = 2, kF16 = 3 };
 
 constexpr int kWaveSize = 64;
-constexpr int kGemvWaves = 4;                     // waves per workgroup
+constexpr int kGemvWaves = 4;                     // waves per workgroup (default launch)
 constexpr int kGemvThreads = kWaveSize * kGemvWaves;
+constexpr int kGemvMaxWaves = 8;                  // waves per workgroup (largest launch)
+constexpr int kGemvMaxThreads = kWaveSize * kGemvMaxWaves;
+constexpr int kTilePad = 16;                      // tiles are stored in multiples of this
 constexpr int kMaxTokensPerLaunch = 16;
 constexpr size_t kGemvLdsLimit = 64 * 1024;
+constexpr int kMaxGroup = 4;                      // tensors sharing one input in one launch
 
 // Elements covered by one unit, and LDS bytes one token's unit occupies
 // (activation bytes plus 16 bytes of padding so that lanes reading
@@ -123,6 +127,53 @@ struct GemvLaunch {
 
 hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream);
 
+// ---- grouped GEMV ---------------------------------------------------------
+// One launch over up to kMaxGroup tensors that share an input (same kind and
+// column count, hence the same lane plan): q/k/v, gate/up.  The input is
+// either prebuilt activation images or, for one token, an fp32 vector that
+// every workgroup turns into its own LDS image (optionally after an RMSNorm
+// or a SwiGLU), so no separate quantization launch is needed.
+enum GemvInput : uint32_t {
+    kInImage = 0,    // images [ntok][image_stride], scales per token
+    kInF32 = 1,      // y = x
+    kInNorm = 2,     // y = (x * 1/sqrt(mean(x^2) + eps)) * norm
+    kInSwiglu = 3,   // y = (x / (1 + exp(-x))) * x2
+};
+enum GemvOutput : uint32_t {
+    kOutStore = 0,   // out = W y * scale
+    kOutAdd = 1,     // out += W y * scale (residual stream)
+    kOutArgmax = 2,  // store, plus per-workgroup (value, first index) maxima
+};
+
+struct GemvGroupLaunch {
+    int njobs = 0;
+    const DeviceTensor *tensors[kMaxGroup] = {};
+    float *outputs[kMaxGroup] = {};
+    uint32_t input_mode = kInImage;
+    uint32_t output_mode = kOutStore;
+    // kInImage
+    const void *image = nullptr;
+    uint32_t image_stride = 0;
+    const float *scales = nullptr;
+    float scale = 1.0f;
+    uint32_t batch = 1;
+    // fp32 modes (one token, cols % 32 == 0)
+    const float *x = nullptr;
+    const float *x2 = nullptr;
+    const float *norm = nullptr;
+    float eps = 0.0f;
+    float *scale_out = nullptr;           // workgroup 0 stores its activation scale here
+    uint64_t *argmax_partials = nullptr;  // kOutArgmax: [grid] packed keys
+    uint32_t output_stride = 0;           // elements between tokens
+    int waves = 0;                        // workgroup size in waves (0: chosen here)
+};
+
+// Workgroups a grouped launch uses (the argmax partial count).
+uint32_t gemv_group_grid(const GemvGroupLaunch &g);
+hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream);
+// Reduce argmax partials [n] to the winning row index (first index on ties).
+hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream);
+
 // ---- Q8 KV cache ------------------------------------------------------
 struct KvCache {
     uint32_t max_tokens = 0;
@@ -140,6 +191,18 @@ struct KvCache {
 };
 
 constexpr int kKvPageTokens = 16;
+
+// Geometry of a cache whose max_tokens/kv_heads/head_dim are set: fills
+// channels/groups/pages and, when base is given, the four arrays inside one
+// allocation of the returned size.
+size_t kv_cache_layout(KvCache &c, uint8_t *base);
+
+// RoPE (c/qwanto_decode.c:686-729) on q [query_heads][head_dim] in place and
+// on key [channels], then the Q8 append of the rotated key and of value at
+// slot *pos_ptr (one workgroup; cos/sin tables [max_tokens][head_dim/2]).
+hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
+                              const float *value, const float *cos_tab, const float *sin_tab,
+                              const int32_t *pos_ptr, hipStream_t stream);
 
 // Quantize one token's fp32 K and V [channels] into slot `token`.
 hipError_t launch_kv_append(const KvCache &c, const float *key,

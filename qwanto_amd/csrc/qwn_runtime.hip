@@ -9,6 +9,7 @@
 // activation image on the device, host buffers are staged through pinned memory,
 // every call runs on the context's own non-blocking stream, and each
 // context has its own lock.
+#include "qwn_context.h"
 #include "qwn_cuda_abi.h"
 #include "qwn_hip_ext.h"
 #include "qwn_internal.h"
@@ -23,10 +24,7 @@
 #include <string>
 #include <vector>
 
-namespace {
-
-using qwn::DeviceTensor;
-using qwn::KvCache;
+namespace qwn {
 
 std::mutex g_error_mutex;
 std::string g_last_error;
@@ -41,77 +39,10 @@ void set_error(const char *fmt, ...) {
     g_last_error = buffer;
 }
 
-int hip_fail(const char *what, hipError_t e, int status = QWN_CUDA_STATUS_RUNTIME_ERROR) {
+int hip_fail(const char *what, hipError_t e, int status) {
     set_error("%s: %s", what, hipGetErrorString(e));
     return status;
 }
-
-template <typename T>
-bool header_ok(const T &s) {
-    return s.header.abi_version == QWN_CUDA_ABI_VERSION && s.header.struct_size >= sizeof(T);
-}
-
-struct PinnedBuffer {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-    hipError_t ensure(size_t want) {
-        if (want <= bytes) return hipSuccess;
-        if (ptr) (void)hipHostFree(ptr);
-        ptr = nullptr;
-        bytes = 0;
-        hipError_t e = hipHostMalloc(&ptr, want, hipHostMallocDefault);
-        if (e == hipSuccess) bytes = want;
-        return e;
-    }
-    void release() {
-        if (ptr) (void)hipHostFree(ptr);
-        ptr = nullptr;
-        bytes = 0;
-    }
-};
-
-struct DeviceBuffer {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-    hipError_t ensure(size_t want) {
-        if (want <= bytes) return hipSuccess;
-        if (ptr) (void)hipFree(ptr);
-        ptr = nullptr;
-        bytes = 0;
-        hipError_t e = hipMalloc(&ptr, want);
-        if (e == hipSuccess) bytes = want;
-        return e;
-    }
-    void release() {
-        if (ptr) (void)hipFree(ptr);
-        ptr = nullptr;
-        bytes = 0;
-    }
-};
-
-struct ResidentTensor {
-    DeviceTensor t;
-    void *allocation = nullptr;
-};
-
-struct ResidentKv {
-    KvCache c;
-    void *allocation = nullptr;
-};
-
-struct Context {
-    std::mutex mutex;
-    int device = -1;
-    uint64_t budget = 0;
-    uint64_t resident = 0;  // logical bytes charged against the budget
-    hipStream_t stream = nullptr;
-    hipEvent_t ev_start = nullptr, ev_end = nullptr;
-    PinnedBuffer host_in, host_out;
-    DeviceBuffer dev_in, dev_out, dev_scales, dev_work, dev_img;
-    std::vector<ResidentTensor *> tensors;
-    std::vector<ResidentKv *> caches;
-    QwnCudaTelemetry telemetry{};
-};
 
 Context *context_of(const QwnCudaContextHandle *h) {
     if (!h || !header_ok(*h) || !h->opaque) return nullptr;
@@ -130,6 +61,12 @@ ResidentKv *cache_of(Context *ctx, const QwnCudaKvCacheHandle &h) {
     auto *c = static_cast<ResidentKv *>(h.opaque);
     return std::find(ctx->caches.begin(), ctx->caches.end(), c) != ctx->caches.end() ? c : nullptr;
 }
+
+}  // namespace qwn
+
+namespace {
+
+using namespace qwn;
 
 double ms_since(std::chrono::steady_clock::time_point t0) {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
@@ -403,6 +340,8 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *handle) 
         std::lock_guard<std::mutex> lock(ctx->mutex);
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
+        for (Decoder *d : ctx->decoders) destroy_decoder(d);
+        ctx->decoders.clear();
         for (ResidentTensor *t : ctx->tensors) free_tensor(t);
         for (ResidentKv *c : ctx->caches) free_cache(c);
         ctx->tensors.clear();
@@ -901,6 +840,109 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *handle,
     ctx->telemetry.gpu_kernel_launch_count++;
     ctx->telemetry.gpu_projection_count++;
     return QWN_CUDA_STATUS_OK;
+}
+
+namespace {
+// Translates a group request (context lock held); false with the error set.
+bool group_of(Context *ctx, const QwnHipGemvGroupRequest *r, qwn::GemvGroupLaunch &g) {
+    if (!r || !header_ok(*r) || !r->tensors || !r->outputs || r->count == 0 || r->count > QWN_HIP_GEMV_MAX_GROUP ||
+        r->input_mode > QWN_HIP_GEMV_INPUT_SWIGLU || r->output_mode > QWN_HIP_GEMV_OUTPUT_ARGMAX) {
+        set_error("invalid grouped GEMV request");
+        return false;
+    }
+    g = qwn::GemvGroupLaunch();
+    g.njobs = static_cast<int>(r->count);
+    uint32_t max_rows = 0;
+    for (uint32_t i = 0; i < r->count; ++i) {
+        ResidentTensor *rt = tensor_of(ctx, r->tensors[i]);
+        if (!rt || !r->outputs[i]) {
+            set_error("grouped GEMV: unknown tensor handle or null output %u", i);
+            return false;
+        }
+        g.tensors[i] = &rt->t;
+        g.outputs[i] = r->outputs[i];
+        max_rows = std::max(max_rows, rt->t.rows);
+    }
+    g.input_mode = r->input_mode;
+    g.output_mode = r->output_mode;
+    g.batch = r->input_mode == QWN_HIP_GEMV_INPUT_IMAGE ? r->batch : 1u;
+    g.image = r->image;
+    g.image_stride = r->image_stride;
+    g.scales = r->scales;
+    g.scale = r->scale;
+    g.x = r->x;
+    g.x2 = r->x2;
+    g.norm = r->norm;
+    g.eps = r->eps;
+    g.scale_out = r->scale_out;
+    g.argmax_partials = r->argmax_partials;
+    g.output_stride = r->output_stride ? r->output_stride : max_rows;
+    const qwn::DeviceTensor &t0 = *g.tensors[0];
+    if (r->input_mode == QWN_HIP_GEMV_INPUT_IMAGE &&
+        (r->batch == 0 || r->image_stride < qwn::image_bytes(t0.kind, t0.units) || (r->image_stride & 15u) ||
+         (reinterpret_cast<uintptr_t>(r->image) & 15u))) {
+        set_error("grouped GEMV: image does not fit the tensors (strides, 16-byte alignment)");
+        return false;
+    }
+    if (r->input_mode != QWN_HIP_GEMV_INPUT_IMAGE &&
+        ((reinterpret_cast<uintptr_t>(r->x) & 15u) || (reinterpret_cast<uintptr_t>(r->x2) & 15u) ||
+         (reinterpret_cast<uintptr_t>(r->norm) & 15u))) {
+        set_error("grouped GEMV: fp32 inputs must be 16-byte aligned");
+        return false;
+    }
+    for (uint32_t i = 0; i < r->count; ++i)
+        if (r->output_stride && r->output_stride < g.tensors[i]->rows) {
+            set_error("grouped GEMV: output stride below the rows of tensor %u", i);
+            return false;
+        }
+    if (qwn::gemv_group_grid(g) == 0) {
+        set_error("grouped GEMV: tensors differ in dtype/columns, or the mode does not fit them "
+                  "(fp32 input needs one token and columns a multiple of 32)");
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
+QWN_CUDA_ABI_API uint32_t qwn_hip_ext_gemv_group_partials(QwnCudaContextHandle *handle,
+                                                          const QwnHipGemvGroupRequest *r) {
+    Context *ctx = context_of(handle);
+    if (!ctx) return 0;
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    qwn::GemvGroupLaunch g;
+    if (!group_of(ctx, r, g)) return 0;
+    return qwn::gemv_group_grid(g);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_gemv_group_device(QwnCudaContextHandle *handle, const QwnHipGemvGroupRequest *r,
+                                                   void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    qwn::GemvGroupLaunch g;
+    if (!group_of(ctx, r, g)) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_gemv_group(g, s);
+    if (e != hipSuccess) return hip_fail("grouped GEMV launch", e);
+    ctx->telemetry.gpu_matmul_count += r->count;
+    ctx->telemetry.gpu_kernel_launch_count++;
+    ctx->telemetry.gpu_projection_count += r->count;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *handle, const uint64_t *partials,
+                                               uint32_t count, int32_t *index, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !partials || !index || count == 0) {
+        set_error("invalid argmax request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_argmax_finish(partials, count, index, s);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("argmax launch", e);
 }
 
 QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *handle, const float *x, uint32_t batch,

@@ -17,7 +17,7 @@ FIXTURE = os.path.join(ROOT, "tests", "golden", "abi_layout.json")
 
 def declared_symbols():
     names = []
-    for h in ("qwn_cuda_abi.h", "qwn_hip_ext.h"):
+    for h in ("qwn_cuda_abi.h", "qwn_hip_ext.h", "qwn_hip_decoder.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         names += re.findall(r"QWN_CUDA_ABI_API\s+[\w\s\*]+?\b(qwn_\w+)\s*\(", text)
     return names
@@ -44,7 +44,33 @@ def test_all_declared_symbols_exported(hip_lib):
     assert len([n for n in names if n.startswith("qwn_cuda_abi_")]) == 17
     for n in names:
         assert hasattr(hip_lib.lib, n), n
-    assert set(abi.EXPORTS) | set(abi.EXT_EXPORTS) == set(names)
+    assert set(abi.EXPORTS) | set(abi.EXT_EXPORTS) | set(abi.DECODER_EXPORTS) == set(names)
+
+
+def test_extension_struct_layouts():
+    """The ctypes mirrors of the extension structs against the C headers,
+    compiled here with gcc."""
+    import subprocess
+    import tempfile
+    fields = {"QwnHipGemvGroupRequest": abi.GemvGroupRequest, "QwnHipDecoderDesc": abi.DecoderDesc,
+              "QwnHipDecoderStats": abi.DecoderStats}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qwn_hip_ext.h"',
+             '#include "qwn_hip_decoder.h"', 'int main(void) {']
+    for cname, cls in fields.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0; }")
+    with tempfile.TemporaryDirectory() as tmp:
+        src, exe = os.path.join(tmp, "p.c"), os.path.join(tmp, "p")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-I" + os.path.join(ROOT, "include"), src, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    for line in out.splitlines():
+        cname, field, value = line.split()
+        cls = fields[cname]
+        got = ctypes.sizeof(cls) if field == "size" else getattr(cls, field).offset
+        assert got == int(value), (cname, field)
 
 
 def test_loader_file_name_present():
