@@ -41,6 +41,11 @@ def parse():
     p.add_argument("--q4", action="store_true", help="also sweep the Qwen2-1.5B Q4_0 shapes")
     p.add_argument("--only-gate", action="store_true",
                    help="profiling mode: launch only the gate projection sweep")
+    p.add_argument("--decode-only", action="store_true",
+                   help="profiling mode: only the Qwen2-1.5B Q4_0 greedy decode")
+    p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
+    p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
+    p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
     p.add_argument("--copy-probe", action="store_true",
                    help="profiling mode: a plain 64 MiB device copy, the reference point that "
                         "scales the FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -120,6 +125,41 @@ def time_launches(torch, sweep, proj, steps, warmup):
     n = sum(1 for it in sweep.items if it[0] == proj)
     ms, _ = time_graph(torch, lambda s: sweep.step(s, only=proj), steps, warmup)
     return ms / n
+
+
+def decode_bench(ctx, new_tokens=128, prompt_len=32, seed=2026):
+    """Greedy decode of the Qwen2-1.5B shaped random Q4_0 model (28 layers,
+    tied F16 LM head, Q8 KV) on the resident decoder: a 32-token prompt, then
+    `new_tokens` greedy steps; tok/s = generated / decode wall time, as
+    c/qwanto_decode.c:2121-2122 reports it.  Run twice: the first pass
+    captures the step graph."""
+    import numpy as np
+
+    from qwanto_amd import abi, synth
+    cfg = synth.QWEN2_1P5B_CONFIG
+    rng = np.random.default_rng(seed)
+    model = synth.decoder_model(rng, cfg, "q4_0")
+    prompt = synth.prompt_tokens(rng, cfg["vocab"], prompt_len)
+    dec = abi.ResidentDecoder(ctx, model)
+    try:
+        toks, st = dec.generate(prompt, new_tokens)
+        dec.reset()
+        toks2, st = dec.generate(prompt, new_tokens)
+        assert toks.tolist() == toks2.tolist()
+    finally:
+        dec.close()
+    ms_tok = st.decode_ms / st.generated_tokens
+    return {
+        "tok_s": round(st.generated_tokens / (st.decode_ms / 1e3), 1),
+        "ms_per_token": round(ms_tok, 4),
+        "prefill_tok_s": round(st.prompt_tokens / (st.prefill_ms / 1e3), 1),
+        "weight_bytes_per_token": int(st.weight_bytes_per_step),
+        "weight_gbps": round(st.weight_bytes_per_step / (ms_tok / 1e3) / 1e9, 1),
+        "kernels_per_token": int(st.launches_per_step),
+        "prompt_tokens": int(st.prompt_tokens), "generated_tokens": int(st.generated_tokens),
+        "first_ids": toks[:8].tolist(),
+        "workload": "qwen2_1p5b_q4_0 random-init, tied F16 LM head, Q8 KV, greedy, HIP graph per token",
+    }
 
 
 def cpu_baseline(seconds: float):
@@ -204,6 +244,10 @@ def main():
         return
     lib = abi.load()
     ctx = abi.Context(lib, device=0)
+    if args.decode_only:
+        print(json.dumps({"profile_mode": "decode",
+                          **decode_bench(ctx, args.decode_new, args.decode_prompt)}), flush=True)
+        return
     t_setup = time.perf_counter()
     sweep = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, args.layers, seed=1)
     setup_s = time.perf_counter() - t_setup
@@ -244,6 +288,8 @@ def main():
             "gbps": round(q4.weight_bytes / (ms_q4 / 1e3) / 1e9, 1), "ms_per_step": round(ms_q4, 4),
             "weight_bytes": q4.weight_bytes}
 
+    if not args.no_decode:
+        extra["decode_qwen2_1p5b_q4_0"] = decode_bench(ctx, args.decode_new, args.decode_prompt)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     dev = lib.devices()[0].name.decode()
     line = {

@@ -14,6 +14,7 @@
 // Layout: 16-token pages, K/V int8 [page][kv_head][16][head_dim], scales
 // fp32 [page][16][groups] with groups over the flattened kv_head*head_dim
 // channels (the reference's token-major grouping).
+#include "qwn_device.h"
 #include "qwn_internal.h"
 
 #include <algorithm>
@@ -364,6 +365,345 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
     }
 }
 
+// ---- decode attention -------------------------------------------------------
+//
+// One workgroup per (query head or KV head, split of `split` tokens), 256
+// threads: while one split spans the context (<= 1024 tokens) a workgroup
+// serves one query head (short contexts are latency-bound; the K/V rows are
+// re-read per query head from L2), past that all G query heads of the KV
+// head share each K/V load (long contexts are bandwidth-bound); online softmax over chunks of 256
+// tokens, so one split covers contexts up to 1024 tokens and no merge pass
+// is needed (nsplit == 1 writes the output).  Each chunk is one memory round
+// trip: a thread loads one token's whole key row (scores) and, at the same
+// time, the value bytes it needs later; nothing waits on a cross-lane
+// reduction per token.
+//   scores: thread = token, s_g = sum over 64-channel groups of
+//           k_scale * sum q_g,c * k_c (the group scale factored out)
+//   P.V:    thread = (4-channel quad, token phase), V prefetched, phases
+//           summed through LDS at the end
+//
+// Decode mode (key != null): the workgroup also applies RoPE to its query
+// heads (c/qwanto_decode.c:686-729) and, for the split holding the current
+// position, rotates and Q8-quantizes the current key and value
+// (c/qwanto_turboquant.c:555-600), stores them in the cache for later steps
+// and attends to them from LDS.
+constexpr int kChunk = 256;
+
+struct DecodeAttnArgs {
+    KvCache c;
+    const float *query;      // [H][D]
+    float *output;           // [H][D] (nsplit == 1)
+    float *partials;         // [H][nsplit][D + 2] (nsplit > 1)
+    uint32_t group;          // query heads per KV head
+    uint32_t heads_per_wg;   // query heads one workgroup handles (divides group)
+    uint32_t split;
+    uint32_t nsplit;
+    float scale;
+    uint32_t position;
+    const int32_t *position_ptr;
+    const float *key;        // decode mode: current token fp32 [channels]
+    const float *value;
+    const float *cos_tab;    // [max_tokens][D/2]
+    const float *sin_tab;
+};
+
+__device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *ct, const float *st) {
+    const uint32_t i = d < half ? d : d - half;
+    const float a = x[i], b = x[i + half];
+    return d < half ? fmaf(a, ct[i], -(b * st[i])) : fmaf(a, st[i], b * ct[i]);
+}
+
+__device__ __forceinline__ int8_t q8_of(float x, float scale) {
+    if (!isfinite(x)) return 0;
+    const float s = x / scale;  // IEEE division, like the CPU path
+    return s >= 127.0f ? 127 : (s <= -127.0f ? -127 : static_cast<int8_t>(__builtin_rintf(s)));
+}
+
+__device__ __forceinline__ float i8f(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xffu));
+}
+
+template <int D, int GMAX>
+__global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a) {
+    constexpr int NG = D / 64;            // Q8 scale groups per head
+    constexpr int KW = D / 16;            // uint4 words of one key row
+    constexpr int QUADS = D / 4;          // P.V: 4-channel quads
+    constexpr int PH = 256 / QUADS;       // P.V: token phases
+    constexpr int TPT = kChunk / PH;      // P.V: tokens per thread per chunk
+    __shared__ __align__(16) float q_s[GMAX * D];
+    __shared__ float s_s[GMAX * kChunk];
+    __shared__ float red[2][4][GMAX];
+    __shared__ __align__(16) float pv_s[PH * GMAX * D];
+    __shared__ __align__(16) int8_t kcur[D];
+    __shared__ __align__(16) int8_t vcur[D];
+    __shared__ float kcur_s[NG], vcur_s[NG];
+    const KvCache &c = a.c;
+    // this workgroup: KV head kvh, its query heads h0 .. h0 + G - 1
+    const uint32_t G = a.heads_per_wg, wgs_per_kv = a.group / G;
+    const uint32_t kvh = blockIdx.y / wgs_per_kv, split = blockIdx.x;
+    const uint32_t h0 = kvh * a.group + (blockIdx.y % wgs_per_kv) * G;
+    const bool writer = blockIdx.y % wgs_per_kv == 0;  // appends the current token
+    const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) : a.position;
+    if (pos >= c.max_tokens) return;
+    const uint32_t tokens = pos + 1;
+    const uint32_t t0 = split * a.split;
+    if (t0 >= tokens) {
+        // a split past the position (fixed grid): an empty partial
+        for (uint32_t i = tid; i < G * D; i += blockDim.x) {
+            const uint32_t g = i / D, d = i % D;
+            float *dst = a.partials + (static_cast<size_t>(h0 + g) * a.nsplit + split) * (D + 2);
+            dst[2 + d] = 0.0f;
+            if (d == 0) {
+                dst[0] = -INFINITY;
+                dst[1] = 0.0f;
+            }
+        }
+        return;
+    }
+    const uint32_t t1 = min(tokens, t0 + a.split);
+    const bool rope = a.key != nullptr;
+    const bool cur = rope && pos >= t0 && pos < t1;
+    constexpr uint32_t half = D / 2;
+    const float *ct = rope ? a.cos_tab + static_cast<size_t>(pos) * half : nullptr;
+    const float *st = rope ? a.sin_tab + static_cast<size_t>(pos) * half : nullptr;
+
+    // 1. query heads of this KV head (rotated in decode mode) -> LDS
+    for (uint32_t i = tid; i < GMAX * D; i += blockDim.x) {
+        const uint32_t g = i / D, d = i % D;
+        float v = 0.0f;
+        if (g < G) {
+            const float *qh = a.query + static_cast<size_t>(h0 + g) * D;
+            v = rope ? rope_at(qh, d, half, ct, st) : qh[d];
+        }
+        q_s[i] = v;
+    }
+    // the current token's key (rotated) and value: one wave per 64-channel group
+    if (cur) {
+        for (uint32_t gi = wave; gi < 2 * NG; gi += 4) {
+            const bool is_v = gi >= NG;
+            const uint32_t grp = is_v ? gi - NG : gi;
+            const uint32_t d = grp * 64 + lane;
+            const float *src = (is_v ? a.value : a.key) + static_cast<size_t>(kvh) * D;
+            const float x = is_v ? src[d] : rope_at(src, d, half, ct, st);
+            const float amax = wave_max_all(isfinite(x) ? fabsf(x) : 0.0f);
+            const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+            const int8_t qv = q8_of(x, scale);
+            (is_v ? vcur : kcur)[d] = qv;
+            if (writer) (is_v ? c.values : c.keys)[kv_offset(c, pos, kvh) + d] = qv;
+            if (lane == 0) {
+                (is_v ? vcur_s : kcur_s)[grp] = scale;
+                if (writer) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, pos) + kvh * NG + grp] = scale;
+            }
+        }
+    }
+    __syncthreads();
+
+    const uint32_t quad = tid % QUADS, ph = tid / QUADS;
+    const uint32_t vgrp = (quad * 4) / 64;
+    float m_run[GMAX], l_run[GMAX], acc[GMAX][4];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[g][i] = 0.0f;
+    }
+
+    for (uint32_t c0 = t0; c0 < t1; c0 += kChunk) {
+        const uint32_t n = min(static_cast<uint32_t>(kChunk), t1 - c0);
+        // 2. one round trip: this thread's key row (token c0 + tid) and its
+        //    P.V values (tokens c0 + ph + PH*j), with their scales
+        const bool has_k = tid < n;
+        const uint32_t tk = has_k ? c0 + tid : t0;
+        const bool k_cur = cur && has_k && tk == pos;
+        uint4 kr[KW];
+        float ks[NG];
+        {
+            const uint4 *src = reinterpret_cast<const uint4 *>(k_cur ? static_cast<const int8_t *>(kcur)
+                                                                     : c.keys + kv_offset(c, tk, kvh));
+#pragma unroll
+            for (int w = 0; w < KW; ++w) kr[w] = src[w];
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                ks[g] = k_cur ? kcur_s[g] : c.key_scales[scale_offset(c, tk) + kvh * NG + g];
+        }
+        uint32_t vw[TPT];
+        float vs[TPT];
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const uint32_t tl = ph + PH * j;
+            const uint32_t t = tl < n ? c0 + tl : t0;
+            const bool v_cur = cur && tl < n && t == pos;
+            vw[j] = v_cur ? *reinterpret_cast<const uint32_t *>(vcur + quad * 4)
+                          : *reinterpret_cast<const uint32_t *>(c.values + kv_offset(c, t, kvh) + quad * 4);
+            vs[j] = v_cur ? vcur_s[vgrp] : c.value_scales[scale_offset(c, t) + kvh * NG + vgrp];
+        }
+        // 3. scores of this thread's token
+        float sc[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) sc[g] = 0.0f;
+#pragma unroll
+        for (int grp = 0; grp < NG; ++grp) {
+            float part[GMAX];
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) part[g] = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint4 kw = kr[grp * 4 + w];
+                const uint32_t k4[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float k0 = i8f(k4[e], 0), k1 = i8f(k4[e], 1), k2 = i8f(k4[e], 2), k3 = i8f(k4[e], 3);
+                    const uint32_t d0 = grp * 64 + w * 16 + e * 4;
+#pragma unroll
+                    for (int g = 0; g < GMAX; ++g) {
+                        if (static_cast<uint32_t>(g) >= G) break;
+                        const float4 qq = *reinterpret_cast<const float4 *>(q_s + g * D + d0);
+                        part[g] = fmaf(qq.x, k0, part[g]);
+                        part[g] = fmaf(qq.y, k1, part[g]);
+                        part[g] = fmaf(qq.z, k2, part[g]);
+                        part[g] = fmaf(qq.w, k3, part[g]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) sc[g] = fmaf(part[g], ks[grp], sc[g]);
+        }
+        // 4. chunk softmax, running max and sum
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            sc[g] = (has_k && static_cast<uint32_t>(g) < G) ? sc[g] * a.scale : -INFINITY;
+            const float m = wave_max_all(sc[g]);
+            if (lane == 0) red[0][wave][g] = m;
+        }
+        __syncthreads();
+        float alpha[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            const float mc = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+            const float mn = fmaxf(m_run[g], mc);
+            alpha[g] = m_run[g] == -INFINITY ? 0.0f : expf(m_run[g] - mn);
+            m_run[g] = mn;
+            const float p = (has_k && static_cast<uint32_t>(g) < G) ? expf(sc[g] - mn) : 0.0f;
+            s_s[g * kChunk + tid] = p;
+            const float ps = wave_sum_all(p);
+            if (lane == 0) red[1][wave][g] = ps;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            l_run[g] = l_run[g] * alpha[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[g][i] *= alpha[g];
+        }
+        // 5. P.V of this thread's quad over its tokens (p = 0 past the chunk)
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const uint32_t tl = ph + PH * j;
+            const float v0 = i8f(vw[j], 0) * vs[j], v1 = i8f(vw[j], 1) * vs[j];
+            const float v2 = i8f(vw[j], 2) * vs[j], v3 = i8f(vw[j], 3) * vs[j];
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                if (static_cast<uint32_t>(g) >= G) break;
+                const float p = s_s[g * kChunk + tl];
+                acc[g][0] = fmaf(p, v0, acc[g][0]);
+                acc[g][1] = fmaf(p, v1, acc[g][1]);
+                acc[g][2] = fmaf(p, v2, acc[g][2]);
+                acc[g][3] = fmaf(p, v3, acc[g][3]);
+            }
+        }
+        __syncthreads();
+    }
+
+    // 6. sum the token phases; output or partial
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+        if (static_cast<uint32_t>(g) < G)
+            *reinterpret_cast<float4 *>(pv_s + (ph * GMAX + g) * D + quad * 4) =
+                make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+    __syncthreads();
+    for (uint32_t i = tid; i < G * D; i += blockDim.x) {
+        const uint32_t g = i / D, d = i % D;
+        float o = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PH; ++p) o += pv_s[(p * GMAX + g) * D + d];
+        const uint32_t head = h0 + g;
+        if (a.nsplit == 1) {
+            a.output[static_cast<size_t>(head) * D + d] = o / l_run[g];
+        } else {
+            float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
+            dst[2 + d] = o;
+            if (d == 0) {
+                dst[0] = m_run[g];
+                dst[1] = l_run[g];
+            }
+        }
+    }
+}
+
+// grid (query heads): the split partials of one head, weighted by
+// exp(m_s - max m) (empty splits carry m = -inf, l = 0 and drop out).
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restrict__ partials, float *out,
+                                                           uint32_t nsplit, uint32_t D) {
+    __shared__ float w_s[1024];
+    __shared__ float total_s;
+    const uint32_t head = blockIdx.x;
+    const float *base = partials + static_cast<size_t>(head) * nsplit * (D + 2);
+    for (uint32_t sidx = threadIdx.x; sidx < nsplit; sidx += blockDim.x) w_s[sidx] = base[sidx * (D + 2)];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (uint32_t sidx = 0; sidx < nsplit; ++sidx) mx = fmaxf(mx, w_s[sidx]);
+    __syncthreads();
+    for (uint32_t sidx = threadIdx.x; sidx < nsplit; sidx += blockDim.x) {
+        const float m = base[sidx * (D + 2)];
+        w_s[sidx] = m == -INFINITY ? 0.0f : expf(m - mx);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.0f;
+        for (uint32_t sidx = 0; sidx < nsplit; ++sidx) total = fmaf(base[sidx * (D + 2) + 1], w_s[sidx], total);
+        total_s = total;
+    }
+    __syncthreads();
+    const float inv = total_s > 0.0f ? 1.0f / total_s : 0.0f;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float o = 0.0f;
+        for (uint32_t sidx = 0; sidx < nsplit; ++sidx) o = fmaf(base[sidx * (D + 2) + 2 + d], w_s[sidx], o);
+        out[static_cast<size_t>(head) * D + d] = o * inv;
+    }
+}
+
+template <int D, int GMAX>
+hipError_t launch_decode_kernel(const DecodeAttnArgs &args, hipStream_t stream) {
+    const uint32_t wgs_per_kv = args.group / args.heads_per_wg;
+    hipLaunchKernelGGL((decode_attention_kernel<D, GMAX>), dim3(args.nsplit, args.c.kv_heads * wgs_per_kv),
+                       dim3(256), 0, stream, args);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_decode_g(const DecodeAttnArgs &args, hipStream_t stream) {
+    if (args.heads_per_wg <= 1) return launch_decode_kernel<D, 1>(args, stream);
+    if (args.heads_per_wg <= 2) return launch_decode_kernel<D, 2>(args, stream);
+    if (args.heads_per_wg <= 4) return launch_decode_kernel<D, 4>(args, stream);
+    return launch_decode_kernel<D, 8>(args, stream);
+}
+
+hipError_t launch_decode_attention_args(const DecodeAttnArgs &args, float *output, hipStream_t stream) {
+    hipError_t e;
+    switch (args.c.head_dim) {
+    case 64: e = launch_decode_g<64>(args, stream); break;
+    case 128: e = launch_decode_g<128>(args, stream); break;
+    case 256: e = launch_decode_g<256>(args, stream); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess || args.nsplit == 1) return e;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(args.c.kv_heads * args.group), dim3(256), 0, stream, args.partials,
+                       output, args.nsplit, args.c.head_dim);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t kv_cache_layout(KvCache &c, uint8_t *base) {
@@ -391,6 +731,55 @@ hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_hea
     return hipGetLastError();
 }
 
+bool decode_attention_supported(const KvCache &c, uint32_t query_heads) {
+    return (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256) && query_heads % c.kv_heads == 0 &&
+           query_heads / c.kv_heads <= 8;
+}
+
+// Tokens per workgroup: the whole context up to 1024 tokens (one workgroup
+// per KV head, no merge); beyond that, splits sized for ~512 workgroups.
+uint32_t decode_split_tokens(const KvCache &c, uint32_t tokens) {
+    if (tokens <= 1024) return std::max<uint32_t>(tokens, 1);
+    uint32_t s = 64;
+    while (s < 8192 && static_cast<uint64_t>(tokens) * c.kv_heads > static_cast<uint64_t>(s) * 512) s *= 2;
+    return s;
+}
+
+size_t decode_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t tokens) {
+    const uint32_t s = decode_split_tokens(c, tokens);
+    const uint32_t nsplit = (tokens + s - 1) / s;
+    return nsplit > 1 ? static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2) : 0;
+}
+
+hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t stream) {
+    const KvCache &c = *l.cache;
+    if (!decode_attention_supported(c, l.query_heads) || (l.key && (c.head_dim % 64 || !l.value || !l.cos_tab ||
+                                                                    !l.sin_tab)))
+        return hipErrorInvalidValue;
+    DecodeAttnArgs args{};
+    args.c = c;
+    args.query = l.query;
+    args.output = l.output;
+    args.partials = l.partials;
+    args.group = l.query_heads / c.kv_heads;
+    args.split = decode_split_tokens(c, l.span_tokens);
+    args.nsplit = (l.span_tokens + args.split - 1) / args.split;
+    // one query head per workgroup while a workgroup spans the context (the
+    // latency case: K/V are re-read per head from L2); all heads of a KV
+    // head together once the context is split (the bandwidth case)
+    args.heads_per_wg = args.nsplit == 1 ? 1 : args.group;
+    if (args.nsplit > 1 && !l.partials) return hipErrorInvalidValue;
+    if (args.nsplit > 1024) return hipErrorInvalidValue;
+    args.scale = l.scale;
+    args.position = l.position;
+    args.position_ptr = l.position_ptr;
+    args.key = l.key;
+    args.value = l.value;
+    args.cos_tab = l.cos_tab;
+    args.sin_tab = l.sin_tab;
+    return launch_decode_attention_args(args, l.output, stream);
+}
+
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
                             hipStream_t stream) {
     if (token >= c.max_tokens) return hipErrorInvalidValue;
@@ -409,7 +798,8 @@ size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32
     const uint32_t tokens = position + 1;
     const uint32_t s = split_tokens(c, tokens);
     const uint32_t nsplit = (tokens + s - 1) / s;
-    return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
+    return std::max(static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2),
+                    decode_attention_workspace_floats(c, query_heads, tokens));
 }
 
 namespace {
@@ -452,6 +842,18 @@ hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
     const KvCache &c = *a.cache;
     if (a.position >= c.tokens || a.query_heads % c.kv_heads != 0 || c.head_dim > 1024)
         return hipErrorInvalidValue;
+    if (decode_attention_supported(c, a.query_heads)) {
+        DecodeAttentionLaunch l;
+        l.cache = &c;
+        l.query = a.query;
+        l.output = a.output;
+        l.partials = a.partials;
+        l.query_heads = a.query_heads;
+        l.position = a.position;
+        l.span_tokens = a.position + 1;
+        l.scale = a.scale;
+        return launch_decode_attention(l, stream);
+    }
     AttnArgs args{};
     args.c = c;
     args.query = a.query;

@@ -106,12 +106,15 @@ struct Decoder {
           *sin_tab = nullptr;
     uint64_t *argmax = nullptr;
     uint32_t argmax_n = 0;
+    uint8_t *head_image = nullptr;  // fp32 image of the final-norm output
     int32_t *state = nullptr, *feed = nullptr, *out_tokens = nullptr;
     std::vector<KvCache> caches;
     hipGraphExec_t exec = nullptr;
     bool graph_tried = false;
     uint32_t position = 0;
     uint32_t launches = 0;
+    uint32_t layer_launches = 0;  // kernels per layer
+    bool fused_attention = false; // RoPE + append + attention in one kernel
     uint64_t weight_bytes = 0;
 };
 
@@ -166,12 +169,29 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         qkv.norm = d->norms_in + static_cast<size_t>(l) * d->hidden;
         qkv.eps = d->eps;
         if ((e = launch_gemv_group(qkv, s)) != hipSuccess) return e;
-        if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s)) !=
-            hipSuccess)
-            return e;
-        if ((e = launch_attention_at(d->caches[l], d->q, d->attn, d->heads, pos, d->attn_scale, d->partials, s)) !=
-            hipSuccess)
-            return e;
+        if (d->fused_attention) {
+            DecodeAttentionLaunch at;
+            at.cache = &d->caches[l];
+            at.query = d->q;
+            at.output = d->attn;
+            at.partials = d->partials;
+            at.query_heads = d->heads;
+            at.position_ptr = pos;
+            at.span_tokens = d->max_ctx;
+            at.scale = d->attn_scale;
+            at.key = d->k;
+            at.value = d->v;
+            at.cos_tab = d->cos_tab;
+            at.sin_tab = d->sin_tab;
+            if ((e = launch_decode_attention(at, s)) != hipSuccess) return e;
+        } else {
+            if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s)) !=
+                hipSuccess)
+                return e;
+            if ((e = launch_attention_at(d->caches[l], d->q, d->attn, d->heads, pos, d->attn_scale, d->partials,
+                                         s)) != hipSuccess)
+                return e;
+        }
         GemvGroupLaunch o = group({w[P_O]}, {d->x});
         o.input_mode = kInF32;
         o.output_mode = kOutAdd;
@@ -189,20 +209,21 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         down.x = d->gate;
         down.x2 = d->up;
         if ((e = launch_gemv_group(down, s)) != hipSuccess) return e;
-        n += 7;  // qkv, rope/append, attention split + merge, o, gate/up, down
+        n += d->layer_launches;
     }
+    // LM head: final RMSNorm into the F16 image, then the image-mode GEMV
+    // (fewer registers than the fused prologue: more waves per CU in flight)
+    if ((e = launch_norm_image(*d->embed, d->x, d->final_norm, d->eps, d->head_image, s)) != hipSuccess) return e;
     GemvGroupLaunch head = group({d->embed}, {d->logits});
-    head.input_mode = kInNorm;
+    head.image = d->head_image;
+    head.image_stride = static_cast<uint32_t>(image_bytes(kF16, d->embed->units));
     head.output_mode = kOutArgmax;
-    head.x = d->x;
-    head.norm = d->final_norm;
-    head.eps = d->eps;
     head.argmax_partials = d->argmax;
     if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
     hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, s, d->argmax, d->argmax_n, d->state,
                        d->out_tokens, d->max_ctx);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    n += 2;
+    n += 3;
     if (count) *count = n;
     return hipSuccess;
 }
@@ -320,16 +341,19 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     proto.kv_heads = d->kv_heads;
     proto.head_dim = d->head_dim;
     const size_t cache_bytes = (kv_cache_layout(proto, nullptr) + 255) & ~static_cast<size_t>(255);
-    part(reinterpret_cast<void **>(&d->partials), attention_at_workspace_floats(proto, d->heads) * 4);
+    d->fused_attention = decode_attention_supported(proto, d->heads) && d->head_dim % 64 == 0;
+    part(reinterpret_cast<void **>(&d->partials),
+         std::max<size_t>(d->fused_attention ? decode_attention_workspace_floats(proto, d->heads, d->max_ctx)
+                                             : attention_at_workspace_floats(proto, d->heads),
+                          1) * 4);
     GemvGroupLaunch head = group({d->embed}, {nullptr});
     head.outputs[0] = reinterpret_cast<float *>(16);  // validity only: a non-null placeholder
-    head.input_mode = kInNorm;
+    head.image = reinterpret_cast<const void *>(16);
     head.output_mode = kOutArgmax;
-    head.x = reinterpret_cast<const float *>(16);
-    head.norm = reinterpret_cast<const float *>(16);
     head.argmax_partials = reinterpret_cast<uint64_t *>(16);
     d->argmax_n = gemv_group_grid(head);
     part(reinterpret_cast<void **>(&d->argmax), static_cast<size_t>(d->argmax_n) * 8);
+    part(reinterpret_cast<void **>(&d->head_image), image_bytes(kF16, d->embed->units));
     // every grouped launch of the step must accept its fused input
     bool fits = d->argmax_n > 0;
     {
@@ -402,7 +426,14 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         destroy_decoder(d);
         return hip_fail("decoder set-up", e);
     }
-    d->launches = 7 * d->layers + 3;  // embed, 7 per layer, LM head, step end
+    // qkv, attention (+ merge past one split; RoPE/append and split + merge
+    // as three kernels without the fused kernel), o, gate/up, down
+    const uint32_t nsplit = d->fused_attention
+                                ? (d->max_ctx + decode_split_tokens(proto, d->max_ctx) - 1) /
+                                      decode_split_tokens(proto, d->max_ctx)
+                                : 2;
+    d->layer_launches = 4 + (d->fused_attention ? (nsplit > 1 ? 2 : 1) : 3);
+    d->launches = d->layer_launches * d->layers + 4;  // + embed, norm image, LM head, step end
     ctx->decoders.push_back(d);
     std::memset(out, 0, sizeof(*out));
     qwn_cuda_abi_header_init(&out->header, sizeof(*out));

@@ -18,6 +18,59 @@ __device__ __forceinline__ float half_to_float(uint32_t bits) {
 }
 
 
+// ---- cross-lane reductions (DPP) -----------------------------------------
+
+// Sum over aligned groups of `lanes` consecutive lanes (a power of two);
+// the total lands in the last lane of each group.  row_shr steps add the
+// lanes 1, 2, 4, 8 below within each 16-lane row; row_bcast:15/31 carry
+// row totals into the next row for groups of 32 and 64.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, true);
+    return v + __builtin_bit_cast(float, moved);
+}
+__device__ __forceinline__ float group_sum(float v, uint32_t lanes) {
+    if (lanes >= 2) v = dpp_add<0x111, 0xf>(v);   // row_shr:1
+    if (lanes >= 4) v = dpp_add<0x112, 0xf>(v);   // row_shr:2
+    if (lanes >= 8) v = dpp_add<0x114, 0xf>(v);   // row_shr:4
+    if (lanes >= 16) v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+    if (lanes >= 32) v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    if (lanes >= 64) v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// Max over each 16-lane row, in the row's last lane: lanes with no source
+// lane keep their own value (bound_ctrl off, old = v).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), CTRL,
+                                                  0xf, 0xf, false);
+    return fmaxf(v, __builtin_bit_cast(float, moved));
+}
+
+// Whole-wave sum / max, returned to every lane (row reductions by DPP, then
+// the four row totals read as scalars and combined in row order).
+__device__ __forceinline__ float wave_sum_all(float v) {
+    v = group_sum(v, 16);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 47));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    return (r0 + r1) + (r2 + r3);
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+    v = dpp_max_step<0x111>(v);
+    v = dpp_max_step<0x112>(v);
+    v = dpp_max_step<0x114>(v);
+    v = dpp_max_step<0x118>(v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 15));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 31));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 47));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+
 // ---- activation images --------------------------------------------------------
 
 // Nibble-pack 8 int8 values (two dwords, element order) into the high

