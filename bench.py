@@ -1,17 +1,24 @@
 """Benchmark of the quantized decode path on one MI355X.
 
-Workload (one "step"): every batch-1 GEMV of a decode token of a Qwen3-4B
-shaped HyperVSQ-2 model -- 36 layers x {q, k, v, o, gate, up, down}, 252
-launches over 1.05 GB of distinct resident weights (four times the 256 MB
-infinity cache, so no step is served from cache) -- each launch reading its
-own activation image (int8 token quantized on the device from N(0,1)
-fp32, in the layout the kernel stages into LDS).  The
-252 launches are captured once in a HIP graph and replayed.
+Headline workload (one "step"): every batch-1 GEMV of a decode token of a
+Qwen3-4B shaped HyperVSQ-2 model (36 layers x {q, k, v, o, gate, up, down},
+1.05 GB of distinct resident weights, four times the 256 MB infinity cache,
+so no step is served from cache), launched the way the decoder issues them:
+per layer q/k/v as one grouped launch (one input), o, gate/up as one grouped
+launch, down -- 144 launches, captured once in a HIP graph and replayed.
+Each launch reads its own activation image (an int8 token quantized on the
+device from N(0,1) fp32) already resident in HBM.
 
-value = algorithmic weight bytes per step / step time (GB/s); roofline is
-the per-launch kernel time of the dominant shape (gate/up 9728x2560,
-7,198,720 B) from HIP events on the launch stream; cpu_baseline times the
-reference's CPU kernels (or the oracle port) on this host.
+value = algorithmic weight bytes per step / step time (GB/s).  roofline is
+the dominant kernel of that step (the gate/up launch, 2 x 9728x2560,
+14,397,440 B) from HIP events on the launch stream; cpu_baseline times the
+reference's CPU GEMV (oracle/_ref, or the oracle port) on this host.
+
+Also reported: the same sweep with one launch per tensor, the Qwen2-1.5B
+Q4_0 sweep, the Q4_0 greedy decode (tok/s, with the reference CPU decoder
+on a bounded sample beside it), Q8-KV decode attention at the Qwen3-4B
+shape for 4096 and 32768 cached tokens, and the HyperVSQ-2 batch sweep
+M = 1..16 (weights read once per launch).
 """
 from __future__ import annotations
 
@@ -19,6 +26,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -26,7 +34,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "quant GEMV effective weight GB/s (% HBM peak); decode tok/s 1.5B-shape Q4_0"
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "hvsq2_gemv_gate_9728x2560_traffic.json")
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "hvsq2_gemv_gate_up_2x9728x2560_traffic.json")
 
 
 def parse():
@@ -35,65 +43,105 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--layers", type=int, default=36)
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     p.add_argument("--cpu-seconds", type=float, default=4.0,
-                   help="CPU work per thread setting in the baseline leg")
-    p.add_argument("--q4", action="store_true", help="also sweep the Qwen2-1.5B Q4_0 shapes")
-    p.add_argument("--only-gate", action="store_true",
-                   help="profiling mode: launch only the gate projection sweep")
-    p.add_argument("--decode-only", action="store_true",
-                   help="profiling mode: only the Qwen2-1.5B Q4_0 greedy decode")
+                   help="CPU GEMV work per thread setting in the baseline leg")
+    p.add_argument("--no-extras", action="store_true",
+                   help="only the headline sweep (no Q4_0 sweep, decode, attention, batch sweep)")
     p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
     p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
-    p.add_argument("--copy-probe", action="store_true",
-                   help="profiling mode: a plain 64 MiB device copy, the reference point that "
-                        "scales the FETCH_SIZE / WRITE_SIZE counters to bytes")
+    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "copy"),
+                   help="profiling mode: run only one workload (for rocprofv3)")
     return p.parse_args()
 
 
 class Sweep:
-    """Resident weights, activations and outputs of one GEMV sweep."""
+    """Resident weights, activation images and outputs of a GEMV sweep over
+    `layers` layers of one model shape."""
 
-    def __init__(self, torch, ctx, dtype, shapes, layers, seed):
+    def __init__(self, torch, ctx, dtype, shapes, layers, seed, batch=1):
         import numpy as np
 
         from qwanto_amd import synth
-        self.torch, self.ctx, self.dtype = torch, ctx, dtype
+        self.torch, self.ctx, self.dtype, self.batch = torch, ctx, dtype, batch
         rng = np.random.default_rng(seed)
         torch.manual_seed(seed)
-        self.items = []
-        self.weight_bytes = 0
         dev = torch.device("cuda:0")
-        for layer in range(layers):
+        self.layers = []
+        self.weight_bytes = 0
+        self.shapes = shapes
+        for _ in range(layers):
+            layer = {}
             for proj in synth.PROJECTIONS:
                 N, K = shapes[proj]
                 w = synth.weights(dtype, rng, N, K)
-                h = ctx.upload(w, dtype, N, K)
-                ib = ctx.image_bytes(h)
-                x = torch.randn(1, K, device=dev, dtype=torch.float32)
-                img = torch.zeros(1, ib, device=dev, dtype=torch.uint8)
-                sc = torch.zeros(1, device=dev, dtype=torch.float32)
-                y = torch.zeros(1, N, device=dev, dtype=torch.float32)
-                ctx.quantize_image_device(h, x.data_ptr(), 1, K, img.data_ptr(), ib, sc.data_ptr(),
-                                          stream=torch.cuda.current_stream().cuda_stream)
-                self.items.append((proj, N, K, h, img, sc, y, ib))
+                layer[proj] = ctx.upload(w, dtype, N, K)
                 self.weight_bytes += synth.weight_bytes(dtype, N, K)
+            # one image per distinct input: qkv (hidden), o (attention), gu (hidden), down (ffn)
+            imgs = {}
+            for key, proj in (("qkv", "q"), ("o", "o"), ("gu", "gate"), ("down", "down")):
+                h = layer[proj]
+                K = shapes[proj][1]
+                ib = ctx.image_bytes(h)
+                x = torch.randn(batch, K, device=dev, dtype=torch.float32)
+                img = torch.zeros(batch, ib, device=dev, dtype=torch.uint8)
+                sc = torch.zeros(batch, device=dev, dtype=torch.float32)
+                ctx.quantize_image_device(h, x.data_ptr(), batch, K, img.data_ptr(), ib, sc.data_ptr(),
+                                          stream=torch.cuda.current_stream().cuda_stream)
+                imgs[key] = (img, sc, ib)
+            layer["images"] = imgs
+            layer["out"] = {p: torch.zeros(batch, shapes[p][0], device=dev, dtype=torch.float32)
+                            for p in synth.PROJECTIONS}
+            self.layers.append(layer)
         torch.cuda.synchronize()
+        self._requests = []
+        for layer in self.layers:
+            for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")),
+                               ("down", ("down",))):
+                img, sc, ib = layer["images"][key]
+                req, keep = ctx.gemv_group_request(
+                    [layer[p] for p in projs], [layer["out"][p].data_ptr() for p in projs], "image",
+                    batch=batch, image_ptr=img.data_ptr(), image_stride=ib, scales_ptr=sc.data_ptr())
+                self._requests.append((key, req, keep))
 
-    def launch(self, item, stream):
-        proj, N, K, h, img, sc, y, ib = item
-        self.ctx.gemm_image_device(h, img.data_ptr(), ib, y.data_ptr(), 1, N,
-                                   scales_ptr=sc.data_ptr(), stream=stream)
+    def grouped(self, stream, only=None):
+        """Decode-order launches: qkv, o, gate/up, down per layer."""
+        for key, req, _ in self._requests:
+            if only is None or key == only:
+                self.ctx.gemv_group_device(req, stream=stream)
 
-    def step(self, stream, only=None):
-        for it in self.items:
-            if only is None or it[0] == only:
-                self.launch(it, stream)
+    def per_tensor(self, stream, only=None):
+        """One launch per tensor."""
+        from qwanto_amd import synth
+        for layer in self.layers:
+            for proj in synth.PROJECTIONS:
+                if only is not None and proj != only:
+                    continue
+                key = {"q": "qkv", "k": "qkv", "v": "qkv", "o": "o", "gate": "gu", "up": "gu",
+                       "down": "down"}[proj]
+                img, sc, ib = layer["images"][key]
+                N = self.shapes[proj][0]
+                self.ctx.gemm_image_device(layer[proj], img.data_ptr(), ib, layer["out"][proj].data_ptr(),
+                                           self.batch, N, scales_ptr=sc.data_ptr(), stream=stream)
+
+    def bytes_of(self, projs):
+        from qwanto_amd import synth
+        return sum(synth.weight_bytes(self.dtype, *self.shapes[p]) for p in projs)
+
+    def close(self):
+        """Release the resident tensors (the ABI holds at most 512)."""
+        from qwanto_amd import synth
+        for layer in self.layers:
+            for proj in synth.PROJECTIONS:
+                self.ctx.release(layer[proj])
+        self.layers = []
+        self._requests = []
 
 
 def time_graph(torch, fn, steps, warmup):
-    """Capture fn(stream) once, replay warmup + steps times; ms per replay."""
+    """Capture fn(stream) once, replay warmup + steps times; ms per replay
+    (HIP events on the replay stream)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -114,32 +162,27 @@ def time_graph(torch, fn, steps, warmup):
         g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, g
+    return start.elapsed_time(end) / steps
 
 
-def time_launches(torch, sweep, proj, steps, warmup):
-    """Mean time per launch of one projection: a graph of its 36 launches
-    (distinct weights, 36 x 7.2 MB for gate) replayed `steps` times between
-    HIP events on the launch stream.  Includes the graph's per-kernel
-    dispatch, so it bounds the profiler's kernel duration from above."""
-    n = sum(1 for it in sweep.items if it[0] == proj)
-    ms, _ = time_graph(torch, lambda s: sweep.step(s, only=proj), steps, warmup)
-    return ms / n
-
-
-def decode_bench(ctx, new_tokens=128, prompt_len=32, seed=2026):
-    """Greedy decode of the Qwen2-1.5B shaped random Q4_0 model (28 layers,
-    tied F16 LM head, Q8 KV) on the resident decoder: a 32-token prompt, then
-    `new_tokens` greedy steps; tok/s = generated / decode wall time, as
-    c/qwanto_decode.c:2121-2122 reports it.  Run twice: the first pass
-    captures the step graph."""
+def decode_model(seed=2026, prompt_len=32):
     import numpy as np
 
-    from qwanto_amd import abi, synth
+    from qwanto_amd import synth
     cfg = synth.QWEN2_1P5B_CONFIG
     rng = np.random.default_rng(seed)
     model = synth.decoder_model(rng, cfg, "q4_0")
     prompt = synth.prompt_tokens(rng, cfg["vocab"], prompt_len)
+    return model, prompt
+
+
+def decode_bench(ctx, model, prompt, new_tokens=128):
+    """Greedy decode of the Qwen2-1.5B shaped random Q4_0 model (28 layers,
+    tied F16 LM head, Q8 KV) on the resident decoder: the prompt, then
+    `new_tokens` greedy steps; tok/s = generated / decode wall time, as
+    c/qwanto_decode.c:2121-2122 reports it.  Run twice: the first pass
+    captures the step graph."""
+    from qwanto_amd import abi
     dec = abi.ResidentDecoder(ctx, model)
     try:
         toks, st = dec.generate(prompt, new_tokens)
@@ -158,8 +201,81 @@ def decode_bench(ctx, new_tokens=128, prompt_len=32, seed=2026):
         "kernels_per_token": int(st.launches_per_step),
         "prompt_tokens": int(st.prompt_tokens), "generated_tokens": int(st.generated_tokens),
         "first_ids": toks[:8].tolist(),
-        "workload": "qwen2_1p5b_q4_0 random-init, tied F16 LM head, Q8 KV, greedy, HIP graph per token",
+        "workload": "qwen2_1p5b_q4_0 random-init (seed 2026), tied F16 LM head, Q8 KV, greedy, "
+                    "HIP graph per token",
     }
+
+
+def cpu_decode_baseline(model, prompt, steps=6, threads=None):
+    """The reference decoder (c/qwanto_decode.c built in place, CPU backend,
+    Q8 KV) on the same model from a .qwn file: the first 4 prompt tokens,
+    then `steps` greedy steps, timed; tok/s over the greedy steps."""
+    import numpy as np
+
+    import oracle
+    from qwanto_amd import qwn_file, synth
+    if not os.path.exists(oracle.REF_DECODER_SO):
+        return None
+    threads = threads or len(os.sched_getaffinity(0))
+    V = synth.QWEN2_1P5B_CONFIG["vocab"]
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "m.qwn")
+        qwn_file.write_decoder_model(path, model)
+        ref = oracle.load_ref_decoder(path, synth.QWEN2_1P5B_CONFIG["max_ctx"], threads)
+        try:
+            for t in prompt[:4]:
+                logits = ref.forward(int(t), V)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                logits = ref.forward(int(np.argmax(logits)), V)
+            dt = time.perf_counter() - t0
+        finally:
+            ref.close()
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"reference CPU decoder, 4 prompt tokens then {steps} greedy steps of the same model"}
+
+
+def attention_bench(torch, ctx, steps=50):
+    """Q8-KV decode attention at the Qwen3-4B shape (32 query heads, 8 KV
+    heads, head_dim 128) over 4096 and 32768 cached tokens; K/V N(0,1)
+    quantized into the cache on the device, q N(0,1).  Bytes = 2176 per
+    cached token (K and V int8 plus the per-group scales), read once."""
+    H, HK, D = 32, 8, 128
+    dev = torch.device("cuda:0")
+    s = torch.cuda.current_stream()
+    out = {}
+    for T in (4096, 32768):
+        cache = ctx.kv_create(T, HK, D)
+        k = torch.randn(T, HK * D, device=dev)
+        v = torch.randn(T, HK * D, device=dev)
+        ctx.kv_append_device(cache, k.data_ptr(), v.data_ptr(), T, stream=s.cuda_stream)
+        q = torch.randn(H * D, device=dev)
+        o = torch.zeros(H * D, device=dev)
+        work = torch.zeros(max(ctx.attention_workspace_bytes(cache, H, T - 1) // 4, 1), device=dev)
+        fn = lambda st: ctx.kv_attention_device(cache, q.data_ptr(), o.data_ptr(), H, T - 1,
+                                                float(D ** -0.5), work.data_ptr(), stream=st)
+        ms = time_graph(torch, fn, steps, 5)
+        bytes_ = 2176 * T
+        out[str(T)] = {"us_per_call": round(ms * 1e3, 3), "gbps": round(bytes_ / (ms / 1e3) / 1e9, 1),
+                       "kv_bytes": bytes_}
+        ctx.kv_destroy(cache)
+        del k, v
+    return out
+
+
+def batch_sweep(torch, ctx, steps, warmup):
+    """HyperVSQ-2 GEMV at M = 1, 2, 4, 8, 16 tokens per launch over 4
+    layers of the Qwen3-4B shapes (weights read once per launch)."""
+    from qwanto_amd import synth
+    out = {}
+    for M in (1, 2, 4, 8, 16):
+        sw = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
+        ms = time_graph(torch, sw.grouped, steps, warmup)
+        out[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
+                       "us_per_layer": round(ms * 1e3 / 4, 3),
+                       "tokens_per_s": round(M * 4 / (ms / 1e3) / 36, 1)}
+        sw.close()
+    return out
 
 
 def cpu_baseline(seconds: float):
@@ -187,11 +303,10 @@ def cpu_baseline(seconds: float):
         layers.append(layer)
     layer_bytes = sum(synth.weight_bytes("hvsq2", N, x.shape[1]) for _, x, N in layers[0])
     gomp = None
-    for name in ("libgomp.so.1",):
-        try:
-            gomp = ctypes.CDLL(name)
-        except OSError:
-            pass
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+    except OSError:
+        pass
     ncpu = len(os.sched_getaffinity(0))
     results = {}
     for threads in sorted({8, ncpu}):
@@ -210,10 +325,8 @@ def cpu_baseline(seconds: float):
                 break
         dt = time.perf_counter() - t0
         results[threads] = layer_bytes * done / dt / 1e9
-    best_threads = ncpu
     return {
-        "value": round(results[best_threads], 3), "unit": "GB/s", "cores": best_threads,
-        "kind": kind,
+        "value": round(results[ncpu], 3), "unit": "GB/s", "cores": ncpu, "kind": kind,
         "kernel": (ref.cpu_kernel_name() if ref is not None else ora.variant_name(ora.best_variant())),
         "sample": f"Qwen3-4B layer, 7 HyperVSQ-2 projections x 4 distinct copies (117 MB), batch 1, "
                   f"fp32 N(0,1) input quantized per call, ~{seconds:.0f}s per thread count",
@@ -233,7 +346,7 @@ def main():
     from qwanto_amd import abi, synth
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs the GPU (no CPU fallback)")
-    if args.copy_probe:
+    if args.profile == "copy":
         n = 64 << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
@@ -244,66 +357,79 @@ def main():
         return
     lib = abi.load()
     ctx = abi.Context(lib, device=0)
-    if args.decode_only:
-        print(json.dumps({"profile_mode": "decode",
-                          **decode_bench(ctx, args.decode_new, args.decode_prompt)}), flush=True)
+    if args.profile == "decode":
+        model, prompt = decode_model(prompt_len=args.decode_prompt)
+        print(json.dumps({"profile_mode": "decode", **decode_bench(ctx, model, prompt, args.decode_new)}),
+              flush=True)
+        return
+    if args.profile == "attention":
+        print(json.dumps({"profile_mode": "attention", **attention_bench(torch, ctx, args.steps)}), flush=True)
         return
     t_setup = time.perf_counter()
     sweep = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, args.layers, seed=1)
-    setup_s = time.perf_counter() - t_setup
-    print(f"# setup: {len(sweep.items)} HyperVSQ-2 tensors, {sweep.weight_bytes / 1e9:.3f} GB "
-          f"resident in {setup_s:.1f}s", file=sys.stderr, flush=True)
-
-    if args.only_gate:
-        ms, _ = time_graph(torch, lambda s: sweep.step(s, only="gate"), args.steps, args.warmup)
-        print(json.dumps({"profile_mode": "gate", "ms_per_replay": ms}), flush=True)
+    print(f"# setup: {7 * args.layers} HyperVSQ-2 tensors, {sweep.weight_bytes / 1e9:.3f} GB "
+          f"resident in {time.perf_counter() - t_setup:.1f}s", file=sys.stderr, flush=True)
+    if args.profile == "gate-up":
+        ms = time_graph(torch, lambda st: sweep.grouped(st, only="gu"), args.steps, args.warmup)
+        print(json.dumps({"profile_mode": "gate-up", "ms_per_replay": ms}), flush=True)
         return
 
-    ms_per_step, _ = time_graph(torch, sweep.step, args.steps, args.warmup)
-    value = sweep.weight_bytes / (ms_per_step / 1e3) / 1e9
-    print(f"# sweep: {ms_per_step:.4f} ms/step -> {value:.1f} GB/s", file=sys.stderr, flush=True)
+    ms_step = time_graph(torch, sweep.grouped, args.steps, args.warmup)
+    value = sweep.weight_bytes / (ms_step / 1e3) / 1e9
+    print(f"# grouped sweep: {ms_step:.4f} ms/step -> {value:.1f} GB/s", file=sys.stderr, flush=True)
+    ms_tensor = time_graph(torch, sweep.per_tensor, args.steps, args.warmup)
 
-    per_shape = {}
-    for proj in ("gate", "down", "q", "o", "k"):
-        N, K = synth.QWEN3_4B_SHAPES[proj]
-        ms = time_launches(torch, sweep, proj, args.steps, args.warmup)
-        per_shape[f"{proj} {N}x{K}"] = {
-            "kernel_us": round(ms * 1e3, 3),
-            "gbps": round(synth.weight_bytes("hvsq2", N, K) / (ms / 1e3) / 1e9, 1)}
-    gate = per_shape["gate 9728x2560"]
-    gate_bytes = synth.weight_bytes("hvsq2", 9728, 2560)
+    # per-launch kernel times (graph of the 36 launches of one kind / 36)
+    per_launch = {}
+    for key, projs in (("gu", ("gate", "up")), ("qkv", ("q", "k", "v")), ("down", ("down",)), ("o", ("o",))):
+        ms = time_graph(torch, lambda st, k=key: sweep.grouped(st, only=k), args.steps, args.warmup) / args.layers
+        b = sweep.bytes_of(projs)
+        per_launch[key] = {"us": round(ms * 1e3, 3), "bytes": b, "gbps": round(b / (ms / 1e3) / 1e9, 1)}
+    gu = per_launch["gu"]
     traffic = None
     if os.path.exists(PROFILE_TRAFFIC):
         traffic = json.load(open(PROFILE_TRAFFIC)).get("hbm_bytes_per_launch")
-    roofline = {"bound": "hbm", "achieved": gate["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gate["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "gemv_kernel<hvsq2> gate 9728x2560",
-                "bytes_per_launch": gate_bytes, "avg_launch_us": gate["kernel_us"]}
+    roofline = {"bound": "hbm", "achieved": gu["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "gemv_kernel<hvsq2> gate+up grouped launch, 2 x 9728x2560",
+                "bytes_per_launch": gu["bytes"], "avg_launch_us": gu["us"]}
 
-    extra = {}
-    if args.q4:
+    extra = {"per_tensor_launches": {"gbps": round(sweep.weight_bytes / (ms_tensor / 1e3) / 1e9, 1),
+                                     "ms_per_step": round(ms_tensor, 4), "launches_per_step": 7 * args.layers},
+             "per_launch_kernel": per_launch}
+    sweep_bytes = sweep.weight_bytes
+    sweep.close()
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    if not args.no_extras:
         q4 = Sweep(torch, ctx, "q4_0", synth.QWEN2_1P5B_SHAPES, 28, seed=2)
-        ms_q4, _ = time_graph(torch, q4.step, args.steps, args.warmup)
+        ms_q4 = time_graph(torch, q4.grouped, args.steps, args.warmup)
         extra["q4_0_sweep_qwen2_1p5b"] = {
             "gbps": round(q4.weight_bytes / (ms_q4 / 1e3) / 1e9, 1), "ms_per_step": round(ms_q4, 4),
-            "weight_bytes": q4.weight_bytes}
+            "weight_bytes": q4.weight_bytes, "launches_per_step": 4 * 28}
+        q4.close()
+        if not args.no_decode:
+            model, prompt = decode_model(prompt_len=args.decode_prompt)
+            dec = decode_bench(ctx, model, prompt, args.decode_new)
+            if not args.no_cpu:
+                dec["cpu_baseline"] = cpu_decode_baseline(model, prompt)
+            extra["decode_qwen2_1p5b_q4_0"] = dec
+            del model
+        extra["attention_q8_qwen3_4b"] = attention_bench(torch, ctx, args.steps)
+        extra["batch_sweep_hvsq2_qwen3_4b"] = batch_sweep(torch, ctx, args.steps, args.warmup)
 
-    if not args.no_decode:
-        extra["decode_qwen2_1p5b_q4_0"] = decode_bench(ctx, args.decode_new, args.decode_prompt)
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     dev = lib.devices()[0].name.decode()
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": "hvsq2_gemv_sweep_qwen3_4b_batch1", "layers": args.layers,
+        "config": {"workload": "hvsq2_gemv_qwen3_4b_batch1_decode_order", "layers": args.layers,
                    "projections": {p: list(synth.QWEN3_4B_SHAPES[p]) for p in synth.PROJECTIONS},
-                   "launches_per_step": len(sweep.items), "weight_bytes_per_step": sweep.weight_bytes,
+                   "launches_per_step": 4 * args.layers,
+                   "weight_bytes_per_step": sweep_bytes,
                    "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4), "device": dev},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "per_shape_kernel": per_shape,
         **extra,
     }
     print(json.dumps(line), flush=True)

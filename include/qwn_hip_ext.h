@@ -93,7 +93,10 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *context
  * Output modes: STORE; ADD (outputs += result, one token: the residual
  * stream); ARGMAX (store, and one packed key per workgroup in
  * argmax_partials -- qwn_hip_ext_gemv_group_partials() of them -- reduced
- * by qwn_hip_ext_argmax_device to the first index of the largest output).
+ * by qwn_hip_ext_argmax_device to the first index of the largest output);
+ * SWIGLU (two tensors of one shape, gate and up, one token: outputs[0] =
+ * (g / (1 + exp(-g))) * u per row, c/qwanto_decode.c:1946-1949; outputs[1]
+ * is not written).
  * Device pointers, caller's stream, no allocation. */
 #define QWN_HIP_GEMV_INPUT_IMAGE 0u
 #define QWN_HIP_GEMV_INPUT_F32 1u
@@ -102,6 +105,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_image_device(QwnCudaContextHandle *context
 #define QWN_HIP_GEMV_OUTPUT_STORE 0u
 #define QWN_HIP_GEMV_OUTPUT_ADD 1u
 #define QWN_HIP_GEMV_OUTPUT_ARGMAX 2u
+#define QWN_HIP_GEMV_OUTPUT_SWIGLU 3u
 #define QWN_HIP_GEMV_MAX_GROUP 4u
 
 typedef struct {

@@ -60,7 +60,7 @@ DECODER_EXPORTS = (
 )
 
 GEMV_INPUT = {"image": 0, "f32": 1, "rmsnorm": 2, "swiglu": 3}
-GEMV_OUTPUT = {"store": 0, "add": 1, "argmax": 2}
+GEMV_OUTPUT = {"store": 0, "add": 1, "argmax": 2, "swiglu": 3}
 
 
 class Header(ctypes.Structure):

@@ -387,8 +387,6 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
 // position, rotates and Q8-quantizes the current key and value
 // (c/qwanto_turboquant.c:555-600), stores them in the cache for later steps
 // and attends to them from LDS.
-constexpr int kChunk = 256;
-
 struct DecodeAttnArgs {
     KvCache c;
     const float *query;      // [H][D]
@@ -425,15 +423,17 @@ __device__ __forceinline__ float i8f(uint32_t w, int i) {
 
 template <int D, int GMAX>
 __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a) {
-    constexpr int NG = D / 64;            // Q8 scale groups per head
-    constexpr int KW = D / 16;            // uint4 words of one key row
-    constexpr int QUADS = D / 4;          // P.V: 4-channel quads
-    constexpr int PH = 256 / QUADS;       // P.V: token phases
-    constexpr int TPT = kChunk / PH;      // P.V: tokens per thread per chunk
+    constexpr int NG = D / 64;                 // Q8 scale groups per head
+    constexpr int KW = D / 16;                 // uint4 words of one K or V row
+    constexpr int CH = D <= 128 ? 256 : 128;   // tokens per chunk (V rows staged in LDS)
+    constexpr int QUADS = D / 4;               // P.V: 4-channel quads
+    constexpr int PH = 256 / QUADS;            // P.V: token phases
     __shared__ __align__(16) float q_s[GMAX * D];
-    __shared__ float s_s[GMAX * kChunk];
+    __shared__ float s_s[GMAX * CH];
     __shared__ float red[2][4][GMAX];
     __shared__ __align__(16) float pv_s[PH * GMAX * D];
+    __shared__ __align__(16) uint4 v_s[CH * KW];   // the chunk's V rows
+    __shared__ float vsc_s[CH * NG];               // and their scales
     __shared__ __align__(16) int8_t kcur[D];
     __shared__ __align__(16) int8_t vcur[D];
     __shared__ float kcur_s[NG], vcur_s[NG];
@@ -510,35 +510,59 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
         for (int i = 0; i < 4; ++i) acc[g][i] = 0.0f;
     }
 
-    for (uint32_t c0 = t0; c0 < t1; c0 += kChunk) {
-        const uint32_t n = min(static_cast<uint32_t>(kChunk), t1 - c0);
-        // 2. one round trip: this thread's key row (token c0 + tid) and its
-        //    P.V values (tokens c0 + ph + PH*j), with their scales
-        const bool has_k = tid < n;
-        const uint32_t tk = has_k ? c0 + tid : t0;
-        const bool k_cur = cur && has_k && tk == pos;
-        uint4 kr[KW];
-        float ks[NG];
+    for (uint32_t c0 = t0; c0 < t1; c0 += CH) {
+        const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
+        // 2. one round trip: thread tid takes token c0 + tid -- its key row,
+        //    value row and scales (global loads; the current token from LDS)
+        const bool has = tid < n;
+        const uint32_t tk = has ? c0 + tid : t0;
+        const bool is_cur = cur && has && tk == pos;
+        uint4 kr[KW], vr[KW];
+        float ks[NG], vsc[NG];
         {
-            const uint4 *src = reinterpret_cast<const uint4 *>(k_cur ? static_cast<const int8_t *>(kcur)
-                                                                     : c.keys + kv_offset(c, tk, kvh));
+            // the current token's slot is being written by this launch: load
+            // any written row instead and take the token from LDS below
+            const uint32_t tl = is_cur ? t0 : tk;
+            const uint4 *kp = reinterpret_cast<const uint4 *>(c.keys + kv_offset(c, tl, kvh));
+            const uint4 *vp = reinterpret_cast<const uint4 *>(c.values + kv_offset(c, tl, kvh));
 #pragma unroll
-            for (int w = 0; w < KW; ++w) kr[w] = src[w];
+            for (int w = 0; w < KW; ++w) {
+                kr[w] = kp[w];
+                vr[w] = vp[w];
+            }
+            const size_t so = scale_offset(c, tl) + kvh * NG;
 #pragma unroll
-            for (int g = 0; g < NG; ++g)
-                ks[g] = k_cur ? kcur_s[g] : c.key_scales[scale_offset(c, tk) + kvh * NG + g];
+            for (int g = 0; g < NG; ++g) {
+                ks[g] = c.key_scales[so + g];
+                vsc[g] = c.value_scales[so + g];
+            }
         }
-        uint32_t vw[TPT];
-        float vs[TPT];
+        if (cur) {
 #pragma unroll
-        for (int j = 0; j < TPT; ++j) {
-            const uint32_t tl = ph + PH * j;
-            const uint32_t t = tl < n ? c0 + tl : t0;
-            const bool v_cur = cur && tl < n && t == pos;
-            vw[j] = v_cur ? *reinterpret_cast<const uint32_t *>(vcur + quad * 4)
-                          : *reinterpret_cast<const uint32_t *>(c.values + kv_offset(c, t, kvh) + quad * 4);
-            vs[j] = v_cur ? vcur_s[vgrp] : c.value_scales[scale_offset(c, t) + kvh * NG + vgrp];
+            for (int w = 0; w < KW; ++w) {
+                // component selects (a select of the uint4 struct goes through scratch)
+                const uint4 kc = reinterpret_cast<const uint4 *>(kcur)[w];
+                const uint4 vc = reinterpret_cast<const uint4 *>(vcur)[w];
+                kr[w].x = is_cur ? kc.x : kr[w].x;
+                kr[w].y = is_cur ? kc.y : kr[w].y;
+                kr[w].z = is_cur ? kc.z : kr[w].z;
+                kr[w].w = is_cur ? kc.w : kr[w].w;
+                vr[w].x = is_cur ? vc.x : vr[w].x;
+                vr[w].y = is_cur ? vc.y : vr[w].y;
+                vr[w].z = is_cur ? vc.z : vr[w].z;
+                vr[w].w = is_cur ? vc.w : vr[w].w;
+            }
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                ks[g] = is_cur ? kcur_s[g] : ks[g];
+                vsc[g] = is_cur ? vcur_s[g] : vsc[g];
+            }
         }
+        // the value row and its scales -> LDS for the P.V phase
+#pragma unroll
+        for (int w = 0; w < KW; ++w) v_s[tid % CH * KW + w] = vr[w];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) vsc_s[tid % CH * NG + g] = has ? vsc[g] : 0.0f;
         // 3. scores of this thread's token
         float sc[GMAX];
 #pragma unroll
@@ -573,7 +597,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
         // 4. chunk softmax, running max and sum
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
-            sc[g] = (has_k && static_cast<uint32_t>(g) < G) ? sc[g] * a.scale : -INFINITY;
+            sc[g] = (has && static_cast<uint32_t>(g) < G) ? sc[g] * a.scale : -INFINITY;
             const float m = wave_max_all(sc[g]);
             if (lane == 0) red[0][wave][g] = m;
         }
@@ -585,8 +609,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             const float mn = fmaxf(m_run[g], mc);
             alpha[g] = m_run[g] == -INFINITY ? 0.0f : expf(m_run[g] - mn);
             m_run[g] = mn;
-            const float p = (has_k && static_cast<uint32_t>(g) < G) ? expf(sc[g] - mn) : 0.0f;
-            s_s[g * kChunk + tid] = p;
+            const float p = (has && static_cast<uint32_t>(g) < G) ? expf(sc[g] - mn) : 0.0f;
+            if (tid < CH) s_s[g * CH + tid] = p;
             const float ps = wave_sum_all(p);
             if (lane == 0) red[1][wave][g] = ps;
         }
@@ -597,16 +621,15 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[g][i] *= alpha[g];
         }
-        // 5. P.V of this thread's quad over its tokens (p = 0 past the chunk)
-#pragma unroll
-        for (int j = 0; j < TPT; ++j) {
-            const uint32_t tl = ph + PH * j;
-            const float v0 = i8f(vw[j], 0) * vs[j], v1 = i8f(vw[j], 1) * vs[j];
-            const float v2 = i8f(vw[j], 2) * vs[j], v3 = i8f(vw[j], 3) * vs[j];
+        // 5. P.V of this thread's quad over its tokens (from LDS)
+        for (uint32_t tl = ph; tl < n; tl += PH) {
+            const uint32_t vw = reinterpret_cast<const uint32_t *>(v_s + tl * KW)[quad];
+            const float vs = vsc_s[tl * NG + vgrp];
+            const float v0 = i8f(vw, 0) * vs, v1 = i8f(vw, 1) * vs, v2 = i8f(vw, 2) * vs, v3 = i8f(vw, 3) * vs;
 #pragma unroll
             for (int g = 0; g < GMAX; ++g) {
                 if (static_cast<uint32_t>(g) >= G) break;
-                const float p = s_s[g * kChunk + tl];
+                const float p = s_s[g * CH + tl];
                 acc[g][0] = fmaf(p, v0, acc[g][0]);
                 acc[g][1] = fmaf(p, v1, acc[g][1]);
                 acc[g][2] = fmaf(p, v2, acc[g][2]);

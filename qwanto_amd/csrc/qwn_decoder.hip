@@ -11,8 +11,10 @@
 //   ctx     = attention over the Q8 cache (split-T partials + merge)
 //   x      += W_o ctx                 GEMV quantizing ctx in its prologue,
 //                                     residual added in its epilogue
-//   g,u     = W_gu rmsnorm(x)         grouped GEMV
-//   x      += W_down (silu(g) * u)    GEMV with the SwiGLU in its prologue
+//   h       = silu(W_g rmsnorm(x)) * W_u rmsnorm(x)
+//                                     grouped GEMV, gate and up rows paired
+//                                     in each workgroup, SwiGLU in the epilogue
+//   x      += W_down h                GEMV quantizing h in its prologue
 //
 // then logits = E rmsnorm(x) (F16 tied LM head, per-workgroup argmax
 // partials in the epilogue) and one kernel that picks the greedy token,
@@ -197,17 +199,19 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         o.output_mode = kOutAdd;
         o.x = d->attn;
         if ((e = launch_gemv_group(o, s)) != hipSuccess) return e;
+        // gate and up rows paired in each workgroup: the epilogue writes
+        // silu(gate) * up, so the down projection only quantizes it
         GemvGroupLaunch gu = group({w[P_GATE], w[P_UP]}, {d->gate, d->up});
         gu.input_mode = kInNorm;
+        gu.output_mode = kOutSwiglu;
         gu.x = d->x;
         gu.norm = d->norms_post + static_cast<size_t>(l) * d->hidden;
         gu.eps = d->eps;
         if ((e = launch_gemv_group(gu, s)) != hipSuccess) return e;
         GemvGroupLaunch down = group({w[P_DOWN]}, {d->x});
-        down.input_mode = kInSwiglu;
+        down.input_mode = kInF32;
         down.output_mode = kOutAdd;
         down.x = d->gate;
-        down.x2 = d->up;
         if ((e = launch_gemv_group(down, s)) != hipSuccess) return e;
         n += d->layer_launches;
     }
@@ -365,8 +369,13 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
             return gemv_group_grid(g) > 0;
         };
         const DeviceTensor *const *w = d->proj.data();
+        GemvGroupLaunch gu = group({w[P_GATE], w[P_UP]}, {});
+        gu.outputs[0] = gu.outputs[1] = reinterpret_cast<float *>(16);
+        gu.input_mode = kInNorm;
+        gu.output_mode = kOutSwiglu;
+        gu.x = gu.norm = reinterpret_cast<const float *>(16);
         fits = fits && probe({w[P_Q], w[P_K], w[P_V]}, kInNorm) && probe({w[P_O]}, kInF32) &&
-               probe({w[P_GATE], w[P_UP]}, kInNorm) && probe({w[P_DOWN]}, kInSwiglu);
+               gemv_group_grid(gu) > 0 && probe({w[P_DOWN]}, kInF32);
     }
     if (!fits || KV > 8192) {
         delete d;

@@ -179,15 +179,16 @@ __global__ __launch_bounds__(256) void quantize_image_kernel(const float *__rest
 // Copy `ntok` token images (global stride `stride`, `bytes` each, a
 // multiple of 16) into LDS back to back, one 16-byte direct load per lane;
 // returns after issuing (the caller waits).
+template <int MT>
 __device__ __forceinline__ void issue_image_copy(const uint8_t *__restrict__ image, uint32_t stride,
                                                  uint32_t bytes, uint32_t ntok, uint8_t *lds) {
     const uint32_t per_tok = bytes / 16;
-    const uint32_t total = per_tok * ntok;
+    const uint32_t total = MT == 1 ? per_tok : per_tok * ntok;
     const uint32_t lane = threadIdx.x % kWaveSize;
     for (uint32_t c0 = (threadIdx.x / kWaveSize) * kWaveSize; c0 < total; c0 += blockDim.x) {
         const uint32_t c = c0 + lane;
         if (c < total) {
-            const uint32_t t = c / per_tok, r = c - t * per_tok;
+            const uint32_t t = MT == 1 ? 0 : c / per_tok, r = c - t * per_tok;
             __builtin_amdgcn_global_load_lds(image + static_cast<size_t>(t) * stride + r * 16,
                                              (lds_void *)(lds + c0 * 16), 16, 0, 0);
         }
@@ -247,6 +248,7 @@ struct GemvArgs {
     size_t tile_meta_bytes;
     uint32_t units;
     uint32_t lanes;
+    uint32_t lanes_log2;
     uint32_t rows_per_wave;
     uint32_t input_mode;
     uint32_t output_mode;
@@ -265,7 +267,7 @@ struct GemvArgs {
     uint32_t cols;
     float *scale_out;
     // output
-    uint32_t output_stride;
+    uint32_t output_stride[kMaxGroup];  // elements between tokens, per job
     uint64_t *argmax_partials;
 };
 
@@ -334,46 +336,71 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red[2][kGemvMaxWaves];
     __shared__ uint64_t red_key[kGemvMaxWaves];
+    __shared__ float up_s[kGemvMaxWaves / 2 * kWaveSize];
     constexpr int CH = 4;
+    // Wave-uniform values are kept in scalar registers (readfirstlane): a
+    // per-lane job index would turn the pointer selection below into vector
+    // loads of the kernel arguments and a full memory round trip ahead of the
+    // weight stream.
     const uint32_t W = blockDim.x / kWaveSize;
     const uint32_t lane = threadIdx.x % kWaveSize;
-    const uint32_t wave = threadIdx.x / kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
     const uint32_t L = a.lanes;
-    const uint32_t grp = lane / L;
-    const uint32_t j = lane - grp * L;
+    const uint32_t grp = lane >> a.lanes_log2;
+    const uint32_t j = lane & (L - 1);
 
-    // Job of this workgroup (uniform select chain over kernel arguments).
-    uint32_t job = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i)
-        if (static_cast<uint32_t>(i) < a.njobs && blockIdx.x >= a.job_block[i]) job = i;
-    const uint8_t *payload = a.payload[0];
-    const uint8_t *meta = a.meta[0];
-    float *output = a.output[0];
-    uint32_t rows = a.rows[0], first = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i)
-        if (job == static_cast<uint32_t>(i)) {
-            payload = a.payload[i];
-            meta = a.meta[i];
-            output = a.output[i];
-            rows = a.rows[i];
-            first = a.job_block[i];
+    // Job of this workgroup.  Every job field is read unconditionally and
+    // chosen by selects, so all kernel-argument loads issue in one batch
+    // (a field loaded only once the job is known would add a dependent
+    // scalar round trip ahead of the weight stream).  Paired jobs (SwiGLU):
+    // the first half of the waves takes a tile of job 0, the second half the
+    // same tile of job 1.
+    // Pin the argument fields the prologue needs: one batch of scalar loads
+    // and a single wait, instead of loads issued one by one at first use.
+    {
+        const uint64_t p0 = reinterpret_cast<uint64_t>(a.payload[0]), p1 = reinterpret_cast<uint64_t>(a.payload[1]);
+        const uint64_t p2 = reinterpret_cast<uint64_t>(a.payload[2]), p3 = reinterpret_cast<uint64_t>(a.payload[3]);
+        const uint64_t m0 = reinterpret_cast<uint64_t>(a.meta[0]), m1 = reinterpret_cast<uint64_t>(a.meta[1]);
+        const uint64_t m2 = reinterpret_cast<uint64_t>(a.meta[2]), m3 = reinterpret_cast<uint64_t>(a.meta[3]);
+        const uint64_t img = reinterpret_cast<uint64_t>(FUSED ? static_cast<const void *>(a.x)
+                                                              : static_cast<const void *>(a.image));
+        if constexpr (FUSED) {
+            const uint64_t x2 = reinterpret_cast<uint64_t>(a.x2), nrm = reinterpret_cast<uint64_t>(a.norm);
+            asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(p3), "s"(m0), "s"(m1), "s"(m2), "s"(m3), "s"(img),
+                         "s"(a.job_block[1]), "s"(a.job_block[2]), "s"(a.job_block[3]), "s"(a.rows[0]),
+                         "s"(a.tile_payload_bytes), "s"(a.tile_meta_bytes), "s"(a.units), "s"(a.lanes_log2),
+                         "s"(a.rows_per_wave), "s"(a.output_mode), "s"(W), "s"(x2), "s"(nrm), "s"(a.cols),
+                         "s"(a.input_mode), "s"(a.eps));
+        } else {
+            asm volatile("" ::"s"(p0), "s"(p1), "s"(p2), "s"(p3), "s"(m0), "s"(m1), "s"(m2), "s"(m3), "s"(img),
+                         "s"(a.job_block[1]), "s"(a.job_block[2]), "s"(a.job_block[3]), "s"(a.rows[0]),
+                         "s"(a.tile_payload_bytes), "s"(a.tile_meta_bytes), "s"(a.units), "s"(a.lanes_log2),
+                         "s"(a.rows_per_wave), "s"(a.output_mode), "s"(a.image_bytes), "s"(W));
         }
-    const uint32_t tile = (blockIdx.x - first) * W + wave;
+    }
+    const bool paired = MT == 1 && a.output_mode == kOutSwiglu;
+    const uint32_t half_w = W / 2;
+    const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
+    uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
+    if (paired) job = wave >= half_w ? 1u : 0u;
+    job = __builtin_amdgcn_readfirstlane(job);
+    const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
+    const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
+    float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
+    const uint32_t rows = job == 0 ? a.rows[0] : job == 1 ? a.rows[1] : job == 2 ? a.rows[2] : a.rows[3];
+    const uint32_t out_stride = job == 0   ? a.output_stride[0]
+                                : job == 1 ? a.output_stride[1]
+                                : job == 2 ? a.output_stride[2]
+                                           : a.output_stride[3];
+    const uint32_t first = paired ? 0u : (job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3);
+    const uint32_t tile = paired ? blockIdx.x * half_w + wave % half_w : (blockIdx.x - first) * W + wave;
     const uint32_t row = tile * a.rows_per_wave + grp;
     const bool active = grp < a.rows_per_wave && row < rows;
     const bool writer = active && j == L - 1;
     constexpr bool fused = FUSED && MT == 1;
 
-    // 0. Loads whose results are needed late (token scales, the residual),
-    //    then the input: image -> LDS by direct loads, or this thread's
-    //    32-element block of the fp32 vector(s) into registers.
-    float tok_scale[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) tok_scale[t] = a.scales ? a.scales[t < static_cast<int>(a.ntok) ? t : 0] : a.scale;
-    float resid = 0.0f;
-    if (a.output_mode == kOutAdd && writer) resid = output[row];
+    // 0. The input: image -> LDS by direct loads, or this thread's 32-element
+    //    block of the fp32 vector(s) into registers.
     const uint32_t nblk = a.units * unit_elems(KIND) / 32;  // 32-blocks in the image
     const uint32_t nvalid = a.cols / 32;                     // blocks holding input values
     const uint32_t b = threadIdx.x;
@@ -389,7 +416,7 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             for (int i = 0; i < 8; ++i) x2v[i] = src2[i];
         }
     } else {
-        issue_image_copy(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
+        issue_image_copy<MT>(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -421,6 +448,18 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             pay[i][q] = *reinterpret_cast<const uint4 *>(ok ? base + q * R * n * 16 : tile_p);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    // Loads whose results are needed only at the end: token scales (a
+    // dependent scalar load, issued after the weight burst) and the residual.
+    float tok_scale[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tok_scale[t] = a.scale;
+    if (a.scales) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) tok_scale[t] = a.scales[t < static_cast<int>(a.ntok) ? t : 0];
+    }
+    float resid = 0.0f;
+    if (a.output_mode == kOutAdd && writer) resid = output[row];
 
     // 2. The LDS image.  Fused: this thread's block after the norm/SwiGLU,
     //    quantized with the workgroup-wide scale (c/qwanto_kernels.c:354-433)
@@ -575,7 +614,16 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = group_sum(acc[t], L);
     float first_out = 0.0f;
-    if (writer) {
+    if (paired) {
+        // up rows -> LDS; the gate lane of the same row forms the SwiGLU
+        const float sv = mul_rounded(acc[0], tok_scale[0]);
+        if (job == 1 && writer) up_s[(wave - half_w) * kWaveSize + lane] = sv;
+        lds_barrier();
+        if (job == 0 && writer) {
+            const float u = up_s[wave * kWaveSize + lane];
+            output[row] = mul_rounded(sv / (1.0f + expf(-sv)), u);
+        }
+    } else if (writer) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             if (static_cast<uint32_t>(t) >= a.ntok) break;
@@ -586,7 +634,7 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             if (KIND != kF16) s = mul_rounded(s, tok_scale[t]);
             if (MT == 1 && a.output_mode == kOutAdd) s = add_rounded(resid, s);
             if (t == 0) first_out = s;
-            output[static_cast<size_t>(t) * a.output_stride + row] = s;
+            output[static_cast<size_t>(t) * out_stride + row] = s;
         }
     }
     if (MT == 1 && a.output_mode == kOutArgmax) {
@@ -777,6 +825,7 @@ GemvArgs args_of(const DeviceTensor &t) {
     a.tile_meta_bytes = t.tile_meta_bytes;
     a.units = t.units;
     a.lanes = t.lanes;
+    a.lanes_log2 = static_cast<uint32_t>(__builtin_ctz(t.lanes));
     a.rows_per_wave = t.rows_per_wave;
     a.image_bytes = static_cast<uint32_t>(image_bytes(t.kind, t.units));
     a.cols = t.cols;
@@ -818,15 +867,16 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     return true;
 }
 
-// Lane plan: one unit per lane where the row allows it (L = the power of
-// two covering the row, at most 64), so the post-load work per lane is
-// short and the grid is large; longer rows take more units per lane.
-// Idle lanes cost VALU slots but no memory traffic (compact tiles).
-//   F16 rows (the LM head) take about four units per lane instead: more rows
-//   per workgroup share one fp32 activation image.
+// Lane plan: L lanes per row (a power of two, at most 64) holding about two
+// units each once a row has 8 or more (F16 rows, the LM head: about four):
+// half the waves of one unit per lane for the same bytes in flight, so a
+// decode-size GEMV fits in one residency round of the chip and more rows
+// share each workgroup's activation image; shorter rows take one unit per
+// lane.  Idle lanes cost VALU slots but no memory traffic (compact tiles).
 bool layout_tensor(DeviceTensor &t) {
     if (!set_units(t)) return false;
-    const uint32_t target = t.kind == kF16 ? (t.units + 3) / 4 : t.units;
+    const uint32_t per_lane = t.kind == kF16 ? 4 : (t.units >= 8 ? 2 : 1);
+    const uint32_t target = (t.units + per_lane - 1) / per_lane;
     uint32_t L = 1;
     while (L < target && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
     const uint32_t need = (t.units + L - 1) / L;
@@ -929,7 +979,7 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
     gg.scales = g.scales;
     gg.scale = g.scale;
     gg.batch = g.batch;
-    gg.output_stride = g.output_stride;
+    gg.output_stride[0] = g.output_stride;
     return launch_gemv_group(gg, stream);
 }
 
@@ -969,6 +1019,9 @@ bool group_valid(const GemvGroupLaunch &g) {
         return false;
     }
     if (g.output_mode == kOutArgmax && (g.batch != 1 || !g.argmax_partials || g.njobs != 1)) return false;
+    if (g.output_mode == kOutSwiglu &&
+        (g.batch != 1 || g.njobs != 2 || g.tensors[0]->rows != g.tensors[1]->rows))
+        return false;
     if (g.output_mode == kOutAdd && g.batch != 1) return false;
     return true;
 }
@@ -980,7 +1033,7 @@ uint32_t gemv_group_grid(const GemvGroupLaunch &g) {
     uint32_t tiles = 0;
     for (int i = 0; i < g.njobs; ++i) tiles += g.tensors[i]->tiles;
     const int w = choose_waves(g, tiles);
-    return tiles / w;
+    return tiles / w;  // paired jobs: tiles of one job / (w / 2), the same
 }
 
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
@@ -1000,6 +1053,7 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         args.meta[i] = ti.meta;
         args.output[i] = g.outputs[i];
         args.rows[i] = ti.rows;
+        args.output_stride[i] = g.output_stride[i] ? g.output_stride[i] : ti.rows;
         args.job_block[i] = blk;
         blk += ti.tiles / w;
     }
@@ -1008,7 +1062,6 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
     const uint32_t threads = static_cast<uint32_t>(w) * kWaveSize;
     args.input_mode = g.input_mode;
     args.output_mode = g.output_mode;
-    args.output_stride = g.output_stride;
     args.argmax_partials = g.argmax_partials;
     if (g.input_mode != kInImage) {
         args.x = g.x;
@@ -1031,7 +1084,7 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         args.image_stride = g.image_stride;
         args.scales = g.scales ? g.scales + t0 : nullptr;
         args.scale = g.scale;
-        for (int i = 0; i < g.njobs; ++i) args.output[i] = g.outputs[i] + static_cast<size_t>(t0) * g.output_stride;
+        for (int i = 0; i < g.njobs; ++i) args.output[i] = g.outputs[i] + static_cast<size_t>(t0) * args.output_stride[i];
         hipError_t e;
         if (t.kind == kHvsq2) e = dispatch_mt<kHvsq2>(p.tokens, grid, threads, p.lds_bytes, args, t.upl, stream);
         else if (t.kind == kQ4_0) e = dispatch_mt<kQ4_0>(p.tokens, grid, threads, p.lds_bytes, args, t.upl, stream);

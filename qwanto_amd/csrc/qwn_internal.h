@@ -143,6 +143,9 @@ enum GemvOutput : uint32_t {
     kOutStore = 0,   // out = W y * scale
     kOutAdd = 1,     // out += W y * scale (residual stream)
     kOutArgmax = 2,  // store, plus per-workgroup (value, first index) maxima
+    kOutSwiglu = 3,  // two jobs of one shape (gate, up) paired row by row in
+                     // each workgroup: outputs[0] = silu(gate) * up
+                     // (c/qwanto_decode.c:1946-1949), outputs[1] unused
 };
 
 struct GemvGroupLaunch {
@@ -164,7 +167,7 @@ struct GemvGroupLaunch {
     float eps = 0.0f;
     float *scale_out = nullptr;           // workgroup 0 stores its activation scale here
     uint64_t *argmax_partials = nullptr;  // kOutArgmax: [grid] packed keys
-    uint32_t output_stride = 0;           // elements between tokens
+    uint32_t output_stride[kMaxGroup] = {};  // elements between tokens per job (0: its rows)
     int waves = 0;                        // workgroup size in waves (0: chosen here)
 };
 

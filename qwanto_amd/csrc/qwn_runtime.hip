@@ -846,13 +846,12 @@ namespace {
 // Translates a group request (context lock held); false with the error set.
 bool group_of(Context *ctx, const QwnHipGemvGroupRequest *r, qwn::GemvGroupLaunch &g) {
     if (!r || !header_ok(*r) || !r->tensors || !r->outputs || r->count == 0 || r->count > QWN_HIP_GEMV_MAX_GROUP ||
-        r->input_mode > QWN_HIP_GEMV_INPUT_SWIGLU || r->output_mode > QWN_HIP_GEMV_OUTPUT_ARGMAX) {
+        r->input_mode > QWN_HIP_GEMV_INPUT_SWIGLU || r->output_mode > QWN_HIP_GEMV_OUTPUT_SWIGLU) {
         set_error("invalid grouped GEMV request");
         return false;
     }
     g = qwn::GemvGroupLaunch();
     g.njobs = static_cast<int>(r->count);
-    uint32_t max_rows = 0;
     for (uint32_t i = 0; i < r->count; ++i) {
         ResidentTensor *rt = tensor_of(ctx, r->tensors[i]);
         if (!rt || !r->outputs[i]) {
@@ -861,7 +860,6 @@ bool group_of(Context *ctx, const QwnHipGemvGroupRequest *r, qwn::GemvGroupLaunc
         }
         g.tensors[i] = &rt->t;
         g.outputs[i] = r->outputs[i];
-        max_rows = std::max(max_rows, rt->t.rows);
     }
     g.input_mode = r->input_mode;
     g.output_mode = r->output_mode;
@@ -876,7 +874,7 @@ bool group_of(Context *ctx, const QwnHipGemvGroupRequest *r, qwn::GemvGroupLaunc
     g.eps = r->eps;
     g.scale_out = r->scale_out;
     g.argmax_partials = r->argmax_partials;
-    g.output_stride = r->output_stride ? r->output_stride : max_rows;
+    for (uint32_t i = 0; i < r->count; ++i) g.output_stride[i] = r->output_stride;  // 0: each tensor's rows
     const qwn::DeviceTensor &t0 = *g.tensors[0];
     if (r->input_mode == QWN_HIP_GEMV_INPUT_IMAGE &&
         (r->batch == 0 || r->image_stride < qwn::image_bytes(t0.kind, t0.units) || (r->image_stride & 15u) ||
@@ -897,7 +895,8 @@ bool group_of(Context *ctx, const QwnHipGemvGroupRequest *r, qwn::GemvGroupLaunc
         }
     if (qwn::gemv_group_grid(g) == 0) {
         set_error("grouped GEMV: tensors differ in dtype/columns, or the mode does not fit them "
-                  "(fp32 input needs one token and columns a multiple of 32)");
+                  "(fp32 input needs one token and columns a multiple of 32; SwiGLU output needs two "
+                  "tensors of one shape)");
         return false;
     }
     return true;

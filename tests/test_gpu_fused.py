@@ -173,6 +173,28 @@ def test_swiglu_input(gpu_ctx, oracle_lib, kind, N, K):
         gpu_ctx.release(h)
 
 
+@pytest.mark.parametrize("kind,N,K", [("hvsq2", 9728, 2560), ("q4_0", 8960, 1536), ("q4_0", 70, 512)])
+def test_swiglu_output_pairs_gate_and_up(gpu_ctx, oracle_lib, kind, N, K):
+    """Gate and up in one launch, SwiGLU in the epilogue: outputs[0] =
+    silu(g) * u of the two GEMV outputs (exp within an ulp of numpy's)."""
+    rng = np.random.default_rng(N + 11 * K)
+    wg, wu = synth.weights(kind, rng, N, K), synth.weights(kind, rng, N, K)
+    hg, hu = gpu_ctx.upload(wg, kind, N, K), gpu_ctx.upload(wu, kind, N, K)
+    try:
+        x = rng.standard_normal(K).astype(np.float32)
+        xd = dev(x)
+        ys, _ = run_group(gpu_ctx, [hg, hu], [N, N], "f32", "swiglu", x_ptr=xd.data_ptr())
+        g, _ = abi_gemv(gpu_ctx, hg, oracle_lib, x, N, K)
+        u, _ = abi_gemv(gpu_ctx, hu, oracle_lib, x, N, K)
+        h = ((g / (np.float32(1.0) + np.exp(-g))) * u).astype(np.float32)
+        ok, worst = gemv_close(ys[0], h, rtol=1e-5)
+        assert ok, f"worst {worst:.3g} of tolerance"
+        assert np.all(ys[1] == 0.0), "the up output must not be written"
+    finally:
+        gpu_ctx.release(hg)
+        gpu_ctx.release(hu)
+
+
 @pytest.mark.parametrize("kind,N,K", [("hvsq2", 2560, 4096), ("q4_0", 1536, 1536)])
 def test_residual_add_output(gpu_ctx, oracle_lib, kind, N, K):
     rng = np.random.default_rng(N + 5 * K)
