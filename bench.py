@@ -263,17 +263,79 @@ def attention_bench(torch, ctx, steps=50):
     return out
 
 
+class MfmaSweep:
+    """Resident HyperVSQ-2 tensors of `layers` layers with MFMA images of M
+    tokens (8..16): one int8-MFMA GEMM launch per tensor."""
+
+    def __init__(self, torch, ctx, shapes, layers, seed, batch):
+        import numpy as np
+
+        from qwanto_amd import synth
+        self.ctx, self.batch, self.shapes = ctx, batch, shapes
+        rng = np.random.default_rng(seed)
+        torch.manual_seed(seed)
+        dev = torch.device("cuda:0")
+        s = torch.cuda.current_stream().cuda_stream
+        self.items, self.handles = [], []
+        self.weight_bytes = 0
+        for _ in range(layers):
+            layer = {p: ctx.upload(synth.hvsq2_weights(rng, *shapes[p]), "hvsq2", *shapes[p])
+                     for p in synth.PROJECTIONS}
+            self.handles += list(layer.values())
+            for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")),
+                               ("down", ("down",))):
+                h0 = layer[projs[0]]
+                K = shapes[projs[0]][1]
+                x = torch.randn(batch, K, device=dev)
+                q8 = torch.zeros(batch, (K + 255) // 256 * 256, dtype=torch.int8, device=dev)
+                sc = torch.zeros(batch, device=dev)
+                ctx.quantize_device(x.data_ptr(), batch, K, K, q8.data_ptr(), q8.shape[1], sc.data_ptr(), stream=s)
+                img = torch.zeros(ctx.mfma_image_bytes(h0), dtype=torch.uint8, device=dev)
+                ctx.mfma_image_device(h0, q8.data_ptr(), batch, q8.shape[1], img.data_ptr(), stream=s)
+                for p in projs:
+                    out = torch.zeros(batch, shapes[p][0], device=dev)
+                    self.items.append((layer[p], img, sc, out))
+                    self.weight_bytes += synth.weight_bytes("hvsq2", *shapes[p])
+        torch.cuda.synchronize()
+        self.flops = 2 * batch * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * layers
+
+    def run(self, stream):
+        for h, img, sc, out in self.items:
+            self.ctx.gemm_mfma_device(h, img.data_ptr(), sc.data_ptr(), out.data_ptr(), self.batch, stream=stream)
+
+    def close(self):
+        for h in self.handles:
+            self.ctx.release(h)
+        self.items, self.handles = [], []
+
+
+INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
+
+
 def batch_sweep(torch, ctx, steps, warmup):
-    """HyperVSQ-2 GEMV at M = 1, 2, 4, 8, 16 tokens per launch over 4
-    layers of the Qwen3-4B shapes (weights read once per launch)."""
+    """HyperVSQ-2 GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers
+    of the Qwen3-4B shapes (weights read once per launch): dot8 grouped
+    launches below 8 tokens, one int8-MFMA launch per tensor from 8 up
+    (MFMA utilisation = useful int8 ops / dense int8 peak)."""
     from qwanto_amd import synth
     out = {}
     for M in (1, 2, 4, 8, 16):
-        sw = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
-        ms = time_graph(torch, sw.grouped, steps, warmup)
+        if M < 8:
+            sw = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
+            ms = time_graph(torch, sw.grouped, steps, warmup)
+            path = "dot8"
+            flops = 2 * M * sum(n * k for n, k in synth.QWEN3_4B_SHAPES.values()) * 4
+        else:
+            sw = MfmaSweep(torch, ctx, synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
+            ms = time_graph(torch, sw.run, steps, warmup)
+            path = "mfma-i8"
+            flops = sw.flops
+        tops = flops / (ms / 1e3) / 1e12
         out[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
                        "us_per_layer": round(ms * 1e3 / 4, 3),
-                       "tokens_per_s": round(M * 4 / (ms / 1e3) / 36, 1)}
+                       "tokens_per_s": round(M * 4 / (ms / 1e3) / 36, 1),
+                       "path": path, "int8_tops": round(tops, 2),
+                       "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5) if M >= 8 else None}
         sw.close()
     return out
 

@@ -53,6 +53,7 @@ EXT_EXPORTS = (
     "qwn_hip_ext_kv_append_device", "qwn_hip_ext_attention_workspace_bytes",
     "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
     "qwn_hip_ext_gemv_group_partials", "qwn_hip_ext_gemv_group_device", "qwn_hip_ext_argmax_device",
+    "qwn_hip_ext_mfma_image_bytes", "qwn_hip_ext_mfma_image_device", "qwn_hip_ext_gemm_mfma_device",
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
@@ -274,6 +275,10 @@ class Library:
         lib.qwn_hip_ext_gemv_group_partials.restype = ctypes.c_uint32
         lib.qwn_hip_ext_gemv_group_device.argtypes = [P(Handle), P(GemvGroupRequest), V]
         lib.qwn_hip_ext_argmax_device.argtypes = [P(Handle), V, U32, V, V]
+        lib.qwn_hip_ext_mfma_image_bytes.argtypes = [P(Handle)]
+        lib.qwn_hip_ext_mfma_image_bytes.restype = ctypes.c_uint64
+        lib.qwn_hip_ext_mfma_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V, V]
+        lib.qwn_hip_ext_gemm_mfma_device.argtypes = [P(Handle), P(Handle), V, V, V, U32, U32, V]
         lib.qwn_hip_decoder_create.argtypes = [P(Handle), P(DecoderDesc), P(Handle)]
         lib.qwn_hip_decoder_destroy.argtypes = [P(Handle), P(Handle)]
         lib.qwn_hip_decoder_reset.argtypes = [P(Handle), P(Handle)]
@@ -434,6 +439,19 @@ class Context:
     def argmax_device(self, partials_ptr: int, count: int, index_ptr: int, stream: int | None = None) -> None:
         self.lib.check("argmax_device", self.lib.lib.qwn_hip_ext_argmax_device(
             self._h, partials_ptr, count, index_ptr, stream))
+
+    def mfma_image_bytes(self, h: Handle) -> int:
+        return int(self.lib.lib.qwn_hip_ext_mfma_image_bytes(ctypes.byref(h)))
+
+    def mfma_image_device(self, h: Handle, q8_ptr: int, batch: int, q8_stride: int, image_ptr: int,
+                          stream: int | None = None) -> None:
+        self.lib.check("mfma_image_device", self.lib.lib.qwn_hip_ext_mfma_image_device(
+            self._h, ctypes.byref(h), q8_ptr, batch, q8_stride, image_ptr, stream))
+
+    def gemm_mfma_device(self, h: Handle, image_ptr: int, scales_ptr: int, out_ptr: int, batch: int,
+                         output_stride: int = 0, stream: int | None = None) -> None:
+        self.lib.check("gemm_mfma_device", self.lib.lib.qwn_hip_ext_gemm_mfma_device(
+            self._h, ctypes.byref(h), image_ptr, scales_ptr, out_ptr, batch, output_stride, stream))
 
     # -- KV cache ---------------------------------------------------------------
     def kv_create(self, max_tokens: int, kv_heads: int, head_dim: int) -> Handle:

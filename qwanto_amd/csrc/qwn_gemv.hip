@@ -653,6 +653,153 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     }
 }
 
+// ---- int8 MFMA batch GEMM (HyperVSQ-2, 8..16 tokens) ----------------------
+//
+// With the octant multiplier folded into the weight, w = s_oct * (code - 1)
+// lies in [-15, 30], so a whole 256-weight block is one exact int8 dot
+// product per (row, token):
+//   y[t][n] = xs_t * sum_blocks (d/8 * sum_i w_i a_t,i + m * sum_i a_t,i)
+// (the same combination as the dot8 path).  A wave computes 16 rows x 16
+// tokens with v_mfma_i32_16x16x64_i8, four instructions per block: lane l
+// holds A row l%16 and B column (token) l%16 for k-bytes 16*(l/16)..+15, and
+// C[4*(l/16)+r][l%16] (layout checked on the device).  Lane group g = l/16
+// takes the block's code chunk g (octants 2g, 2g+1); instruction s takes
+// its code dword s.  The A bytes come out of the code dword through a byte
+// permute over the table [-s, 0, s, 2s]: output dword k holds the weights of
+// code fields k of bytes 0..3, i.e. elements 4*byte + k, so the MFMA image
+// stores each 16-element group of activations in that transposed order:
+//   image [block][s][g][token 0..15][16 B] (byte 4k+b = element 16s+4b+k of
+//   the group 64g..64g+63), then int32 sums [block][token 0..15].
+constexpr int kMfmaTokens = 16;
+
+__host__ __device__ constexpr size_t mfma_image_block_bytes() { return 16 * 256 + 16 * 4; }
+
+__global__ __launch_bounds__(256) void mfma_image_kernel(const int8_t *__restrict__ q8, uint32_t q8_stride,
+                                                         uint32_t K, uint32_t M, uint32_t units, uint8_t *img) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < units * 256) {
+        const uint32_t m = idx % 16, g = (idx / 16) % 4, sl = (idx / 64) % 4, b = idx / 256;
+        uint32_t w[4] = {0, 0, 0, 0};
+        if (m < M) {
+            const uint32_t e0 = b * 256 + 64 * g + 16 * sl;
+            const int8_t *src = q8 + static_cast<size_t>(m) * q8_stride;
+#pragma unroll
+            for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t e = e0 + 4 * bi + k;
+                    const uint32_t v = e < K ? static_cast<uint8_t>(src[e]) : 0u;
+                    w[k] |= v << (8 * bi);
+                }
+        }
+        *reinterpret_cast<uint4 *>(img + static_cast<size_t>(idx) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    if (idx < units * 16) {
+        const uint32_t b = idx / 16, m = idx % 16;
+        int sum = 0;
+        if (m < M) {
+            const int8_t *src = q8 + static_cast<size_t>(m) * q8_stride;
+            for (uint32_t i = 0; i < 256; ++i) {
+                const uint32_t e = b * 256 + i;
+                if (e < K) sum += src[e];
+            }
+        }
+        reinterpret_cast<int32_t *>(img + static_cast<size_t>(units) * 4096)[idx] = sum;
+    }
+}
+
+typedef int mfma_v4i __attribute__((ext_vector_type(4)));
+
+struct MfmaArgs {
+    const uint8_t *payload;
+    const uint8_t *meta;
+    size_t tile_payload_bytes;
+    size_t tile_meta_bytes;
+    uint32_t rows, units, lanes, rows_per_wave;
+    const uint8_t *image;   // mfma image of up to 16 tokens
+    const float *scales;    // [ntok]
+    float *output;          // [ntok][output_stride]
+    uint32_t ntok;
+    uint32_t output_stride;
+};
+
+// A workgroup computes one 16-row x 16-token tile; its four waves split the
+// K blocks (wave w takes blocks w, w+4, ...) and the partial tiles are
+// summed through LDS, so a matrix yields four times the waves and each
+// wave's chain of dependent block iterations is a quarter as long.
+__global__ __launch_bounds__(256) void mfma_hvsq2_kernel(MfmaArgs a) {
+    __shared__ float part_s[3][kWaveSize][4];
+    const uint32_t lane = threadIdx.x % kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+    const uint32_t row0 = blockIdx.x * 16;
+    const uint32_t g = lane / 16, m = lane % 16;
+    const uint32_t na = row0 + m;              // A-operand row of this lane
+    const bool va = na < a.rows;
+    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.units) * 4096);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+    for (uint32_t b = wave; b < a.units; b += 4) {
+        uint4 codes = make_uint4(0, 0, 0, 0);
+        uint32_t subs = 0;
+        if (va) {
+            const UnitAddr ad = unit_addr(na, b, g, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
+                                          a.tile_meta_bytes);
+            codes = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
+            subs = a.meta[ad.meta + 4 + g];
+        }
+        float dsc[4], msc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t no = row0 + 4 * g + r;
+            uint32_t dm = 0;
+            if (no < a.rows) {
+                const UnitAddr ad = unit_addr(no, b, 0, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
+                                              a.tile_meta_bytes);
+                dm = *reinterpret_cast<const uint32_t *>(a.meta + ad.meta);
+            }
+            dsc[r] = half_to_float(dm & 0xffffu) * 0.125f;
+            msc[r] = half_to_float(dm >> 16);
+        }
+        const uint8_t *ib = a.image + static_cast<size_t>(b) * 4096 + lane * 16;
+        mfma_v4i bv[4];
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) bv[sl] = *reinterpret_cast<const mfma_v4i *>(ib + sl * 1024);
+        const float sa = static_cast<float>(sums[b * 16 + m]);
+        const uint32_t cw[4] = {codes.x, codes.y, codes.z, codes.w};
+        mfma_v4i ci = {0, 0, 0, 0};
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            const uint32_t sub = (subs >> (4 * (sl >> 1))) & 15u;
+            // table bytes: code 0 -> -s, 1 -> 0, 2 -> s, 3 -> 2s (zero rows: all 0)
+            const uint32_t lut = ((0u - sub) & 0xffu) | (sub << 16) | ((2u * sub) << 24);
+            const uint32_t c = cw[sl];
+            mfma_v4i av;
+            av.x = static_cast<int>(__builtin_amdgcn_perm(0u, lut, c & 0x03030303u));
+            av.y = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 2) & 0x03030303u));
+            av.z = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 4) & 0x03030303u));
+            av.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
+            ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[sl], ci, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[r] = fmaf(static_cast<float>(ci[r]), dsc[r], fmaf(msc[r], sa, acc[r]));
+    }
+    // sum the four waves' partial tiles (in wave order)
+    if (wave > 0)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part_s[wave - 1][lane][r] = acc[r];
+    __syncthreads();
+    if (wave == 0 && m < a.ntok) {
+        const float xs = a.scales[m];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float tot = ((acc[r] + part_s[0][lane][r]) + part_s[1][lane][r]) + part_s[2][lane][r];
+            const uint32_t no = row0 + 4 * g + r;
+            if (no < a.rows) a.output[static_cast<size_t>(m) * a.output_stride + no] = mul_rounded(tot, xs);
+        }
+    }
+}
+
 // Winner of the argmax partials: one workgroup of 1024 threads.
 __global__ __launch_bounds__(1024) void argmax_finish_kernel(const uint64_t *__restrict__ partials, uint32_t n,
                                                              int32_t *index_out) {
@@ -1092,6 +1239,42 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+size_t mfma_image_bytes(const DeviceTensor &t) {
+    return static_cast<size_t>(t.units) * mfma_image_block_bytes();
+}
+
+hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t batch, uint32_t q8_stride,
+                             uint8_t *image, hipStream_t stream) {
+    if (t.kind != kHvsq2 || batch == 0 || batch > static_cast<uint32_t>(kMfmaTokens)) return hipErrorInvalidValue;
+    const uint32_t n = t.units * 256;
+    hipLaunchKernelGGL(mfma_image_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, q8, q8_stride, t.cols, batch,
+                       t.units, image);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
+                            uint32_t batch, uint32_t output_stride, hipStream_t stream) {
+    if (t.kind != kHvsq2 || batch == 0 || batch > static_cast<uint32_t>(kMfmaTokens) || !scales)
+        return hipErrorInvalidValue;
+    MfmaArgs a{};
+    a.payload = t.payload;
+    a.meta = t.meta;
+    a.tile_payload_bytes = t.tile_payload_bytes;
+    a.tile_meta_bytes = t.tile_meta_bytes;
+    a.rows = t.rows;
+    a.units = t.units;
+    a.lanes = t.lanes;
+    a.rows_per_wave = t.rows_per_wave;
+    a.image = image;
+    a.scales = scales;
+    a.output = output;
+    a.ntok = batch;
+    a.output_stride = output_stride ? output_stride : t.rows;
+    const uint32_t grid = (t.rows + 15) / 16;
+    hipLaunchKernelGGL(mfma_hvsq2_kernel, dim3(grid), dim3(256), 0, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,

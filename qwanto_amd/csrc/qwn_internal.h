@@ -174,6 +174,17 @@ struct GemvGroupLaunch {
 // Workgroups a grouped launch uses (the argmax partial count).
 uint32_t gemv_group_grid(const GemvGroupLaunch &g);
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream);
+// int8 MFMA batch GEMM of a HyperVSQ-2 tensor for 1..16 tokens (used from 8
+// tokens up): the activation layout its tiles read (the "MFMA image"), built
+// from int8 tokens [batch][q8_stride] (values past cols ignored), and the
+// GEMM on it: output [batch][output_stride] = W x_t * scales[t].
+size_t mfma_image_bytes(const DeviceTensor &t);
+hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t batch, uint32_t q8_stride,
+                             uint8_t *image, hipStream_t stream);
+hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
+                            uint32_t batch, uint32_t output_stride, hipStream_t stream);
+constexpr uint32_t kMfmaMinTokens = 8;
+
 // RMSNorm of one fp32 token into the fp32 image of an F16 tensor.
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,
                              hipStream_t stream);

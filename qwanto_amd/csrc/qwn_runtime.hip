@@ -168,16 +168,44 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     g.output = static_cast<float *>(ctx->dev_out.ptr);
     g.batch = r->batch;
     g.output_stride = r->rows;
+    // HyperVSQ-2 from 8 tokens: int8 MFMA tiles of 16 tokens
+    const bool mfma = t.kind == qwn::kHvsq2 && r->batch >= qwn::kMfmaMinTokens;
+    const size_t mfma_img = qwn::mfma_image_bytes(t);
+    if (mfma && ((e = ctx->dev_work.ensure(mfma_img + (quantize ? in_bytes / 4 : 0))) != hipSuccess))
+        return hip_fail("MFMA workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
     (void)hipEventRecord(ctx->ev_start, ctx->stream);
-    if (quantize)
-        e = qwn::launch_quantize_image(t, static_cast<const float *>(ctx->dev_in.ptr), r->batch, dev_stride,
-                                       static_cast<uint8_t *>(ctx->dev_img.ptr), img_stride,
-                                       static_cast<float *>(ctx->dev_scales.ptr), nullptr, 0, ctx->stream);
-    else
-        e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
-                              img_stride, ctx->stream);
-    if (e != hipSuccess) return hip_fail("activation image launch", e);
-    if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
+    if (mfma) {
+        // int8 tokens on the device: as given, or quantized from fp32 per token
+        const int8_t *q8 = static_cast<const int8_t *>(ctx->dev_in.ptr);
+        if (quantize) {
+            int8_t *dq = reinterpret_cast<int8_t *>(static_cast<uint8_t *>(ctx->dev_work.ptr) + mfma_img);
+            e = qwn::launch_quantize_image(t, static_cast<const float *>(ctx->dev_in.ptr), r->batch, dev_stride,
+                                           nullptr, 0, static_cast<float *>(ctx->dev_scales.ptr), dq, dev_stride,
+                                           ctx->stream);
+            if (e != hipSuccess) return hip_fail("activation quantize launch", e);
+            q8 = dq;
+        }
+        uint8_t *img = static_cast<uint8_t *>(ctx->dev_work.ptr);
+        for (uint32_t t0 = 0; t0 < r->batch; t0 += 16) {
+            const uint32_t nt = std::min<uint32_t>(16, r->batch - t0);
+            if ((e = qwn::launch_mfma_image(t, q8 + static_cast<size_t>(t0) * dev_stride, nt, dev_stride, img,
+                                            ctx->stream)) != hipSuccess ||
+                (e = qwn::launch_gemm_mfma(t, img, static_cast<const float *>(ctx->dev_scales.ptr) + t0,
+                                           static_cast<float *>(ctx->dev_out.ptr) + static_cast<size_t>(t0) * r->rows,
+                                           nt, r->rows, ctx->stream)) != hipSuccess)
+                return hip_fail("MFMA GEMM launch", e);
+        }
+    } else {
+        if (quantize)
+            e = qwn::launch_quantize_image(t, static_cast<const float *>(ctx->dev_in.ptr), r->batch, dev_stride,
+                                           static_cast<uint8_t *>(ctx->dev_img.ptr), img_stride,
+                                           static_cast<float *>(ctx->dev_scales.ptr), nullptr, 0, ctx->stream);
+        else
+            e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
+                                  img_stride, ctx->stream);
+        if (e != hipSuccess) return hip_fail("activation image launch", e);
+        if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
+    }
     (void)hipEventRecord(ctx->ev_end, ctx->stream);
     if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,
                             ctx->stream)) != hipSuccess)
@@ -942,6 +970,55 @@ QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *handle, con
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
     hipError_t e = qwn::launch_argmax_finish(partials, count, index, s);
     return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("argmax launch", e);
+}
+
+QWN_CUDA_ABI_API uint64_t qwn_hip_ext_mfma_image_bytes(const QwnCudaTensorHandle *h) {
+    if (!h || !header_ok(*h) || !h->opaque) return 0;
+    const DeviceTensor &t = static_cast<const ResidentTensor *>(h->opaque)->t;
+    return t.kind == qwn::kHvsq2 ? qwn::mfma_image_bytes(t) : 0;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_mfma_image_device(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                   const int8_t *q8, uint32_t batch, uint32_t q8_stride,
+                                                   void *image, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !q8 || !image || batch == 0 || batch > 16) {
+        set_error("invalid MFMA image request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = ext_tensor(ctx, th);
+    if (!rt || rt->t.kind != qwn::kHvsq2 || q8_stride < rt->t.cols || (reinterpret_cast<uintptr_t>(image) & 15u)) {
+        set_error("MFMA image request does not fit the tensor (HyperVSQ-2 only)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_mfma_image(rt->t, q8, batch, q8_stride, static_cast<uint8_t *>(image), s);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("MFMA image launch", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                  const void *image, const float *scales, float *output,
+                                                  uint32_t batch, uint32_t output_stride, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !image || !scales || !output || batch == 0 || batch > 16) {
+        set_error("invalid MFMA GEMM request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = ext_tensor(ctx, th);
+    if (!rt || rt->t.kind != qwn::kHvsq2 || (output_stride && output_stride < rt->t.rows)) {
+        set_error("MFMA GEMM request does not fit the tensor (HyperVSQ-2 only)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_gemm_mfma(rt->t, static_cast<const uint8_t *>(image), scales, output, batch,
+                                         output_stride, s);
+    if (e != hipSuccess) return hip_fail("MFMA GEMM launch", e);
+    ctx->telemetry.gpu_matmul_count++;
+    ctx->telemetry.gpu_kernel_launch_count++;
+    ctx->telemetry.gpu_projection_count++;
+    return QWN_CUDA_STATUS_OK;
 }
 
 QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *handle, const float *x, uint32_t batch,

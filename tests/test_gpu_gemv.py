@@ -114,6 +114,61 @@ def test_q4_0_batched(gpu_ctx, oracle_lib, M):
     check_q4_0(gpu_ctx, oracle_lib, 1536, 8960, seed=200 + M, M=M)
 
 
+@pytest.mark.parametrize("N,K,M", [(77, 700, 8), (130, 513, 9), (1, 256, 8), (64, 256, 16), (300, 7936, 12),
+                                   (2560, 4096, 16)])
+def test_hvsq2_mfma_ragged(gpu_ctx, oracle_lib, N, K, M):
+    """HyperVSQ-2 from 8 tokens runs on int8 MFMA tiles (16 rows x 16
+    tokens): ragged rows, partial blocks, partial token tiles."""
+    check_hvsq2(gpu_ctx, oracle_lib, N, K, seed=N + K + M, M=M)
+
+
+def test_hvsq2_mfma_fp32_input(gpu_ctx, oracle_lib):
+    """INPUT_F32 at 10 tokens: quantized per token on the device, then the
+    MFMA path; the whole CPU matmul is the reference."""
+    rng = np.random.default_rng(91)
+    N, K, M = 1024, 2560, 10
+    w = synth.hvsq2_weights(rng, N, K)
+    x = synth.activations(rng, M, K)
+    h = gpu_ctx.upload(w, "hvsq2", N, K)
+    try:
+        y = gpu_ctx.gemm(h, x, N, K)
+        ref = oracle_lib.matmul_hvsq2(w, x, N)
+        for t in range(M):
+            ok, worst = gemv_close(y[t], ref[t])
+            assert ok, f"token {t}: worst {worst:.3g}"
+    finally:
+        gpu_ctx.release(h)
+
+
+def test_hvsq2_mfma_device_entry_points(gpu_ctx, oracle_lib):
+    """qwn_hip_ext_mfma_image_device + qwn_hip_ext_gemm_mfma_device on device
+    pointers, against the oracle."""
+    import torch
+    rng = np.random.default_rng(92)
+    N, K, M = 2560, 9728, 16
+    w = synth.hvsq2_weights(rng, N, K)
+    x = synth.activations(rng, M, K)
+    q8, xs, sums = oracle_lib.quantize(x)
+    h = gpu_ctx.upload(w, "hvsq2", N, K)
+    try:
+        dev = torch.device("cuda:0")
+        q8d = torch.from_numpy(q8).to(dev)
+        xsd = torch.from_numpy(xs).to(dev)
+        img = torch.zeros(gpu_ctx.mfma_image_bytes(h), dtype=torch.uint8, device=dev)
+        y = torch.zeros(M, N, dtype=torch.float32, device=dev)
+        s = torch.cuda.current_stream().cuda_stream
+        gpu_ctx.mfma_image_device(h, q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
+        gpu_ctx.gemm_mfma_device(h, img.data_ptr(), xsd.data_ptr(), y.data_ptr(), M, stream=s)
+        torch.cuda.synchronize()
+        yh = y.cpu().numpy()
+        for t in range(M):
+            ref = oracle_lib.gemv_hvsq2(w, q8[t], sums[t], float(xs[t]), K, N)
+            ok, worst = gemv_close(yh[t], ref)
+            assert ok, f"token {t}: worst {worst:.3g}"
+    finally:
+        gpu_ctx.release(h)
+
+
 def test_hvsq2_batched_down_proj(gpu_ctx, oracle_lib):
     check_hvsq2(gpu_ctx, oracle_lib, 2560, 9728, seed=77, M=8)
 
