@@ -11,9 +11,14 @@
 // loaded once per KV head and reused by all query heads of its group, and a
 // second pass merges the per-split (max, sum, output) triples.
 //
-// Layout: 16-token pages, K/V int8 [page][kv_head][16][head_dim], scales
-// fp32 [page][16][groups] with groups over the flattened kv_head*head_dim
-// channels (the reference's token-major grouping).
+// Layout: 16-token pages, each laid out for the MFMA operands:
+//   K int8 [page][kv_head][head_dim/16][16 tokens][16 channels]: 16 channels
+//     of one token are one 16-byte word and the 16 tokens of a chunk are
+//     256 contiguous bytes (head_dim padded to a multiple of 16);
+//   V int8 [page][kv_head][head_dim][16 tokens]: the 16 tokens of one
+//     channel are one 16-byte word;
+//   scales fp32 [page][group][16 tokens], groups of 64 channels over the
+//     flattened kv_head*head_dim channels (the reference's grouping).
 #include "qwn_device.h"
 #include "qwn_internal.h"
 
@@ -25,13 +30,35 @@ namespace {
 constexpr int kAttnThreads = 256;
 constexpr int kMaxSplitTokens = 256;
 
-__device__ __forceinline__ size_t kv_offset(const KvCache &c, uint32_t token, uint32_t head) {
+// key byte of (token, head, channel); channels 16q .. 16q + 15 of a token
+// are the 16 bytes at k_index(token, head, 16q)
+__device__ __forceinline__ size_t k_index(const KvCache &c, uint32_t token, uint32_t head, uint32_t dim) {
     const uint32_t page = token / kKvPageTokens, slot = token % kKvPageTokens;
-    return ((static_cast<size_t>(page) * c.kv_heads + head) * kKvPageTokens + slot) * c.head_dim;
+    const uint32_t chunks = (c.head_dim + 15) / 16;
+    return (((static_cast<size_t>(page) * c.kv_heads + head) * chunks + dim / 16) * kKvPageTokens + slot) * 16 +
+           dim % 16;
 }
 
-__device__ __forceinline__ size_t scale_offset(const KvCache &c, uint32_t token) {
-    return static_cast<size_t>(token) * c.groups;  // pages are contiguous: [page][16][groups]
+// value byte of (token, head, channel)
+__device__ __forceinline__ size_t v_offset(const KvCache &c, uint32_t token, uint32_t head, uint32_t dim) {
+    const uint32_t page = token / kKvPageTokens, slot = token % kKvPageTokens;
+    return ((static_cast<size_t>(page) * c.kv_heads + head) * c.head_dim + dim) * kKvPageTokens + slot;
+}
+
+// the 16 value bytes of (page, head, channel)
+__device__ __forceinline__ size_t v_page_offset(const KvCache &c, uint32_t page, uint32_t head, uint32_t dim) {
+    return ((static_cast<size_t>(page) * c.kv_heads + head) * c.head_dim + dim) * kKvPageTokens;
+}
+
+__device__ __forceinline__ void store_q8(const KvCache &c, bool is_v, uint32_t token, uint32_t head, uint32_t dim,
+                                         int8_t q) {
+    if (is_v) c.values[v_offset(c, token, head, dim)] = q;
+    else c.keys[k_index(c, token, head, dim)] = q;
+}
+
+// scale of (token, group)
+__device__ __forceinline__ size_t scale_index(const KvCache &c, uint32_t token, uint32_t group) {
+    return (static_cast<size_t>(token / kKvPageTokens) * c.groups + group) * kKvPageTokens + token % kKvPageTokens;
 }
 
 // grid (groups, 2): y = 0 quantizes K, y = 1 quantizes V.  64 threads, one
@@ -50,15 +77,14 @@ __global__ __launch_bounds__(64) void kv_append_kernel(KvCache c, const float *_
     float amax = (valid && isfinite(v)) ? fabsf(v) : 0.0f;
     for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (threadIdx.x == 0) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, token) + g] = scale;
+    if (threadIdx.x == 0) (is_v ? c.value_scales : c.key_scales)[scale_index(c, token, g)] = scale;
     if (valid) {
         int8_t q = 0;
         if (isfinite(v)) {
             const float s = v / scale;  // IEEE division, like the CPU path
             q = s >= 127.0f ? 127 : (s <= -127.0f ? -127 : static_cast<int8_t>(__builtin_rintf(s)));
         }
-        const uint32_t head = ch / c.head_dim, dim = ch % c.head_dim;
-        (is_v ? c.values : c.keys)[kv_offset(c, token, head) + dim] = q;
+        store_q8(c, is_v, token, ch / c.head_dim, ch % c.head_dim, q);
     }
 }
 
@@ -133,15 +159,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     for (int g = 0; g < GMAX; ++g) s[g] = -INFINITY;
     if (t < n) {
         const uint32_t tok = t0 + t;
-        const int8_t *krow = c.keys + kv_offset(c, tok, kvh);
-        const float *ks = c.key_scales + scale_offset(c, tok);
         float dot[GMAX];
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) dot[g] = 0.0f;
         if (FAST) {
             for (uint32_t c0 = 0; c0 < D; c0 += 16) {
-                const uint4 kw = *reinterpret_cast<const uint4 *>(krow + c0);
-                const float sc = ks[(kvh * D + c0) / 64];
+                const uint4 kw = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tok, kvh, c0));
+                const float sc = c.key_scales[scale_index(c, tok, (kvh * D + c0) / 64)];
                 const uint32_t w[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
@@ -161,7 +185,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
             }
         } else {
             for (uint32_t d = 0; d < D; ++d) {
-                const float kf = static_cast<float>(krow[d]) * ks[(kvh * D + d) / 64];
+                const float kf = static_cast<float>(c.keys[k_index(c, tok, kvh, d)]) *
+                                 c.key_scales[scale_index(c, tok, (kvh * D + d) / 64)];
 #pragma unroll
                 for (int g = 0; g < GMAX; ++g)
                     if (g < static_cast<int>(G)) dot[g] = fmaf(q[g * D + d], kf, dot[g]);
@@ -207,20 +232,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     if (phase < phases) {
         for (uint32_t tt = phase; tt < n; tt += phases) {
             const uint32_t tok = t0 + tt;
-            const int8_t *vrow = c.values + kv_offset(c, tok, kvh);
-            const float *vs = c.value_scales + scale_offset(c, tok);
             float vf[4];
-            if (FAST) {
-                const uint32_t w = *reinterpret_cast<const uint32_t *>(vrow + quad * 4);
-                const float sc = vs[(kvh * D + quad * 4) / 64];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vf[i] = i8(w, i) * sc;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t d = quad * 4 + i;
-                    vf[i] = d < D ? static_cast<float>(vrow[d]) * vs[(kvh * D + d) / 64] : 0.0f;
-                }
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t d = quad * 4 + i;
+                vf[i] = d < D ? static_cast<float>(c.values[v_offset(c, tok, kvh, d)]) *
+                                    c.value_scales[scale_index(c, tok, (kvh * D + d) / 64)]
+                              : 0.0f;
             }
 #pragma unroll
             for (int g = 0; g < GMAX; ++g) {
@@ -353,34 +371,35 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
         float amax = (valid && isfinite(x)) ? fabsf(x) : 0.0f;
         for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-        if (lane == 0) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, pos) + g] = scale;
+        if (lane == 0) (is_v ? c.value_scales : c.key_scales)[scale_index(c, pos, g)] = scale;
         if (valid) {
             int8_t qv = 0;
             if (isfinite(x)) {
                 const float sq = x / scale;  // IEEE division, like the CPU path
                 qv = sq >= 127.0f ? 127 : (sq <= -127.0f ? -127 : static_cast<int8_t>(__builtin_rintf(sq)));
             }
-            (is_v ? c.values : c.keys)[kv_offset(c, pos, ch / D) + ch % D] = qv;
+            store_q8(c, is_v, pos, ch / D, ch % D, qv);
         }
     }
 }
 
 // ---- decode attention -------------------------------------------------------
 //
-// One workgroup per (query head or KV head, split of `split` tokens), 256
-// threads: while one split spans the context (<= 1024 tokens) a workgroup
-// serves one query head (short contexts are latency-bound; the K/V rows are
-// re-read per query head from L2), past that all G query heads of the KV
-// head share each K/V load (long contexts are bandwidth-bound); online softmax over chunks of 256
-// tokens, so one split covers contexts up to 1024 tokens and no merge pass
-// is needed (nsplit == 1 writes the output).  Each chunk is one memory round
+// One workgroup per query head, 256 threads, for contexts up to 1024 tokens
+// (latency-bound: the K/V rows are re-read per query head from L2; longer
+// contexts use the MFMA kernel below).  The kernel also handles splits with
+// all G query heads of a KV head per workgroup (heads_per_wg), which the
+// launcher does not use.  Online softmax over chunks of 256 tokens; one
+// split writes the output.  Each chunk is one memory round
 // trip: a thread loads one token's whole key row (scores) and, at the same
 // time, the value bytes it needs later; nothing waits on a cross-lane
 // reduction per token.
 //   scores: thread = token, s_g = sum over 64-channel groups of
 //           k_scale * sum q_g,c * k_c (the group scale factored out)
-//   P.V:    thread = (4-channel quad, token phase), V prefetched, phases
-//           summed through LDS at the end
+//   P.V:    thread = (channel, phase of 4-token groups); the chunk's value
+//           words (16 tokens of one channel) are staged in LDS in the
+//           cache's own channel-major page order; phases summed through
+//           LDS at the end
 //
 // Decode mode (key != null): the workgroup also applies RoPE to its query
 // heads (c/qwanto_decode.c:686-729) and, for the split holding the current
@@ -424,16 +443,16 @@ __device__ __forceinline__ float i8f(uint32_t w, int i) {
 template <int D, int GMAX>
 __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a) {
     constexpr int NG = D / 64;                 // Q8 scale groups per head
-    constexpr int KW = D / 16;                 // uint4 words of one K or V row
-    constexpr int CH = D <= 128 ? 256 : 128;   // tokens per chunk (V rows staged in LDS)
-    constexpr int QUADS = D / 4;               // P.V: 4-channel quads
-    constexpr int PH = 256 / QUADS;            // P.V: token phases
+    constexpr int KW = D / 16;                 // uint4 words of one key row
+    constexpr int CH = D <= 128 ? 256 : 128;   // tokens per chunk (V staged in LDS)
+    constexpr int VW = CH * D / 16 / 256;      // value words (16 tokens x 1 channel) per thread
+    constexpr int PH = 256 / D;                // P.V: phases of 4-token groups
     __shared__ __align__(16) float q_s[GMAX * D];
-    __shared__ float s_s[GMAX * CH];
+    __shared__ __align__(16) float s_s[GMAX * CH];
     __shared__ float red[2][4][GMAX];
     __shared__ __align__(16) float pv_s[PH * GMAX * D];
-    __shared__ __align__(16) uint4 v_s[CH * KW];   // the chunk's V rows
-    __shared__ float vsc_s[CH * NG];               // and their scales
+    __shared__ __align__(16) uint4 v_s[CH / 16 * D];   // the chunk's values [page][channel][16 tokens]
+    __shared__ float vsc_s[CH * NG];                   // and their scales
     __shared__ __align__(16) int8_t kcur[D];
     __shared__ __align__(16) int8_t vcur[D];
     __shared__ float kcur_s[NG], vcur_s[NG];
@@ -490,51 +509,52 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const int8_t qv = q8_of(x, scale);
             (is_v ? vcur : kcur)[d] = qv;
-            if (writer) (is_v ? c.values : c.keys)[kv_offset(c, pos, kvh) + d] = qv;
+            if (writer) store_q8(c, is_v, pos, kvh, d, qv);
             if (lane == 0) {
                 (is_v ? vcur_s : kcur_s)[grp] = scale;
-                if (writer) (is_v ? c.value_scales : c.key_scales)[scale_offset(c, pos) + kvh * NG + grp] = scale;
+                if (writer) (is_v ? c.value_scales : c.key_scales)[scale_index(c, pos, kvh * NG + grp)] = scale;
             }
         }
     }
     __syncthreads();
 
-    const uint32_t quad = tid % QUADS, ph = tid / QUADS;
-    const uint32_t vgrp = (quad * 4) / 64;
-    float m_run[GMAX], l_run[GMAX], acc[GMAX][4];
+    const uint32_t vch = tid % D, ph = tid / D;   // P.V channel and phase
+    const uint32_t vgrp = vch / 64;
+    float m_run[GMAX], l_run[GMAX], acc[GMAX];
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
         m_run[g] = -INFINITY;
         l_run[g] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[g][i] = 0.0f;
+        acc[g] = 0.0f;
     }
 
     for (uint32_t c0 = t0; c0 < t1; c0 += CH) {
         const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
-        // 2. one round trip: thread tid takes token c0 + tid -- its key row,
-        //    value row and scales (global loads; the current token from LDS)
+        // 2. one round trip: thread tid takes token c0 + tid -- its key row
+        //    and scales -- and VW value words (page, channel) of the chunk
+        //    (global loads; the current token from LDS)
         const bool has = tid < n;
         const uint32_t tk = has ? c0 + tid : t0;
         const bool is_cur = cur && has && tk == pos;
-        uint4 kr[KW], vr[KW];
+        uint4 kr[KW], vr[VW];
         float ks[NG], vsc[NG];
         {
             // the current token's slot is being written by this launch: load
             // any written row instead and take the token from LDS below
             const uint32_t tl = is_cur ? t0 : tk;
-            const uint4 *kp = reinterpret_cast<const uint4 *>(c.keys + kv_offset(c, tl, kvh));
-            const uint4 *vp = reinterpret_cast<const uint4 *>(c.values + kv_offset(c, tl, kvh));
 #pragma unroll
-            for (int w = 0; w < KW; ++w) {
-                kr[w] = kp[w];
-                vr[w] = vp[w];
+            for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, 16 * w));
+#pragma unroll
+            for (int w = 0; w < VW; ++w) {
+                const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
+                // a page with no token of the chunk: read the first page instead
+                const uint32_t pg = pl * kKvPageTokens < n ? c0 / kKvPageTokens + pl : t0 / kKvPageTokens;
+                vr[w] = *reinterpret_cast<const uint4 *>(c.values + v_page_offset(c, pg, kvh, ch));
             }
-            const size_t so = scale_offset(c, tl) + kvh * NG;
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
-                ks[g] = c.key_scales[so + g];
-                vsc[g] = c.value_scales[so + g];
+                ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
+                vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
             }
         }
         if (cur) {
@@ -542,15 +562,24 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             for (int w = 0; w < KW; ++w) {
                 // component selects (a select of the uint4 struct goes through scratch)
                 const uint4 kc = reinterpret_cast<const uint4 *>(kcur)[w];
-                const uint4 vc = reinterpret_cast<const uint4 *>(vcur)[w];
                 kr[w].x = is_cur ? kc.x : kr[w].x;
                 kr[w].y = is_cur ? kc.y : kr[w].y;
                 kr[w].z = is_cur ? kc.z : kr[w].z;
                 kr[w].w = is_cur ? kc.w : kr[w].w;
-                vr[w].x = is_cur ? vc.x : vr[w].x;
-                vr[w].y = is_cur ? vc.y : vr[w].y;
-                vr[w].z = is_cur ? vc.z : vr[w].z;
-                vr[w].w = is_cur ? vc.w : vr[w].w;
+            }
+            // the current token's byte in the value words of its page
+            const uint32_t cur_page = pos / kKvPageTokens - c0 / kKvPageTokens;
+            const uint32_t cw = (pos % kKvPageTokens) / 4, shift = 8 * (pos % 4);
+#pragma unroll
+            for (int w = 0; w < VW; ++w) {
+                const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
+                const bool hit = pl == cur_page;
+                const uint32_t b = static_cast<uint32_t>(static_cast<uint8_t>(vcur[ch])) << shift;
+                const uint32_t keep = ~(0xffu << shift);
+                vr[w].x = hit && cw == 0 ? (vr[w].x & keep) | b : vr[w].x;
+                vr[w].y = hit && cw == 1 ? (vr[w].y & keep) | b : vr[w].y;
+                vr[w].z = hit && cw == 2 ? (vr[w].z & keep) | b : vr[w].z;
+                vr[w].w = hit && cw == 3 ? (vr[w].w & keep) | b : vr[w].w;
             }
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
@@ -558,9 +587,9 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
                 vsc[g] = is_cur ? vcur_s[g] : vsc[g];
             }
         }
-        // the value row and its scales -> LDS for the P.V phase
+        // the value words and the token's scales -> LDS for the P.V phase
 #pragma unroll
-        for (int w = 0; w < KW; ++w) v_s[tid % CH * KW + w] = vr[w];
+        for (int w = 0; w < VW; ++w) v_s[tid + 256 * w] = vr[w];
 #pragma unroll
         for (int g = 0; g < NG; ++g) vsc_s[tid % CH * NG + g] = has ? vsc[g] : 0.0f;
         // 3. scores of this thread's token
@@ -618,22 +647,24 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
 #pragma unroll
         for (int g = 0; g < GMAX; ++g) {
             l_run[g] = l_run[g] * alpha[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[g][i] *= alpha[g];
+            acc[g] *= alpha[g];
         }
-        // 5. P.V of this thread's quad over its tokens (from LDS)
-        for (uint32_t tl = ph; tl < n; tl += PH) {
-            const uint32_t vw = reinterpret_cast<const uint32_t *>(v_s + tl * KW)[quad];
-            const float vs = vsc_s[tl * NG + vgrp];
-            const float v0 = i8f(vw, 0) * vs, v1 = i8f(vw, 1) * vs, v2 = i8f(vw, 2) * vs, v3 = i8f(vw, 3) * vs;
+        // 5. P.V of this thread's channel over its 4-token groups (from LDS)
+        const uint32_t *v_u32 = reinterpret_cast<const uint32_t *>(v_s);
+        for (uint32_t tl = 4 * ph; tl < n; tl += 4 * PH) {
+            const uint32_t vw = v_u32[((tl / kKvPageTokens) * D + vch) * 4 + (tl % kKvPageTokens) / 4];
+            const float v0 = i8f(vw, 0) * vsc_s[tl * NG + vgrp];
+            const float v1 = i8f(vw, 1) * vsc_s[(tl + 1) * NG + vgrp];
+            const float v2 = i8f(vw, 2) * vsc_s[(tl + 2) * NG + vgrp];
+            const float v3 = i8f(vw, 3) * vsc_s[(tl + 3) * NG + vgrp];
 #pragma unroll
             for (int g = 0; g < GMAX; ++g) {
                 if (static_cast<uint32_t>(g) >= G) break;
-                const float p = s_s[g * CH + tl];
-                acc[g][0] = fmaf(p, v0, acc[g][0]);
-                acc[g][1] = fmaf(p, v1, acc[g][1]);
-                acc[g][2] = fmaf(p, v2, acc[g][2]);
-                acc[g][3] = fmaf(p, v3, acc[g][3]);
+                const float4 p = *reinterpret_cast<const float4 *>(s_s + g * CH + tl);
+                acc[g] = fmaf(p.x, v0, acc[g]);
+                acc[g] = fmaf(p.y, v1, acc[g]);
+                acc[g] = fmaf(p.z, v2, acc[g]);
+                acc[g] = fmaf(p.w, v3, acc[g]);
             }
         }
         __syncthreads();
@@ -642,9 +673,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
     // 6. sum the token phases; output or partial
 #pragma unroll
     for (int g = 0; g < GMAX; ++g)
-        if (static_cast<uint32_t>(g) < G)
-            *reinterpret_cast<float4 *>(pv_s + (ph * GMAX + g) * D + quad * 4) =
-                make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        if (static_cast<uint32_t>(g) < G) pv_s[(ph * GMAX + g) * D + vch] = acc[g];
     __syncthreads();
     for (uint32_t i = tid; i < G * D; i += blockDim.x) {
         const uint32_t g = i / D, d = i % D;
@@ -666,35 +695,412 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
 }
 
 // grid (query heads): the split partials of one head, weighted by
-// exp(m_s - max m) (empty splits carry m = -inf, l = 0 and drop out).
+// exp(m_s - max m) (empty splits carry m = -inf, l = 0 and drop out).  The
+// split statistics are staged in LDS and reduced by the whole workgroup;
+// each output channel is summed over the splits by 256 / D threads.
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restrict__ partials, float *out,
                                                            uint32_t nsplit, uint32_t D) {
     __shared__ float w_s[1024];
-    __shared__ float total_s;
-    const uint32_t head = blockIdx.x;
+    __shared__ float l_s[1024];
+    __shared__ float red_s[2][4];
+    __shared__ float part_s[256];
+    const uint32_t head = blockIdx.x, tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const float *base = partials + static_cast<size_t>(head) * nsplit * (D + 2);
-    for (uint32_t sidx = threadIdx.x; sidx < nsplit; sidx += blockDim.x) w_s[sidx] = base[sidx * (D + 2)];
-    __syncthreads();
     float mx = -INFINITY;
-    for (uint32_t sidx = 0; sidx < nsplit; ++sidx) mx = fmaxf(mx, w_s[sidx]);
-    __syncthreads();
-    for (uint32_t sidx = threadIdx.x; sidx < nsplit; sidx += blockDim.x) {
+    for (uint32_t sidx = tid; sidx < nsplit; sidx += blockDim.x) {
         const float m = base[sidx * (D + 2)];
-        w_s[sidx] = m == -INFINITY ? 0.0f : expf(m - mx);
+        w_s[sidx] = m;
+        l_s[sidx] = base[sidx * (D + 2) + 1];
+        mx = fmaxf(mx, m);
     }
+    mx = wave_max_all(mx);
+    if (lane == 0) red_s[0][wave] = mx;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float total = 0.0f;
-        for (uint32_t sidx = 0; sidx < nsplit; ++sidx) total = fmaf(base[sidx * (D + 2) + 1], w_s[sidx], total);
-        total_s = total;
+    mx = fmaxf(fmaxf(red_s[0][0], red_s[0][1]), fmaxf(red_s[0][2], red_s[0][3]));
+    float total = 0.0f;
+    for (uint32_t sidx = tid; sidx < nsplit; sidx += blockDim.x) {
+        const float m = w_s[sidx];
+        const float w = m == -INFINITY ? 0.0f : expf(m - mx);
+        w_s[sidx] = w;
+        total = fmaf(l_s[sidx], w, total);
     }
+    total = wave_sum_all(total);
+    if (lane == 0) red_s[1][wave] = total;
     __syncthreads();
-    const float inv = total_s > 0.0f ? 1.0f / total_s : 0.0f;
-    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+    total = (red_s[1][0] + red_s[1][1]) + (red_s[1][2] + red_s[1][3]);
+    const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+    // channel d = tid % D, splits part, part + parts, ...
+    const uint32_t parts = D <= 256 ? 256 / D : 1;
+    for (uint32_t d0 = 0; d0 < D; d0 += 256 / parts) {
+        const uint32_t d = d0 + tid % D, part = tid / D;
         float o = 0.0f;
-        for (uint32_t sidx = 0; sidx < nsplit; ++sidx) o = fmaf(base[sidx * (D + 2) + 2 + d], w_s[sidx], o);
-        out[static_cast<size_t>(head) * D + d] = o * inv;
+        if (part < parts && d < D) {
+            uint32_t sidx = part;
+            for (; sidx + 3 * parts < nsplit; sidx += 4 * parts) {
+                const float p0 = base[sidx * (D + 2) + 2 + d], p1 = base[(sidx + parts) * (D + 2) + 2 + d];
+                const float p2 = base[(sidx + 2 * parts) * (D + 2) + 2 + d];
+                const float p3 = base[(sidx + 3 * parts) * (D + 2) + 2 + d];
+                o = fmaf(p0, w_s[sidx], o);
+                o = fmaf(p1, w_s[sidx + parts], o);
+                o = fmaf(p2, w_s[sidx + 2 * parts], o);
+                o = fmaf(p3, w_s[sidx + 3 * parts], o);
+            }
+            for (; sidx < nsplit; sidx += parts) o = fmaf(base[sidx * (D + 2) + 2 + d], w_s[sidx], o);
+        }
+        __syncthreads();
+        part_s[tid] = o;
+        __syncthreads();
+        if (part == 0 && d < D) {
+            float sum = 0.0f;
+            for (uint32_t pi = 0; pi < parts; ++pi) sum += part_s[pi * D + tid % D];
+            out[static_cast<size_t>(head) * D + d] = sum * inv;
+        }
     }
+}
+
+// ---- int8 MFMA attention (no RoPE/append; any context length) --------------
+//
+// Both products run on v_mfma_i32_16x16x64_i8 (lane l holds A row l%16 and
+// B column l%16 for k-bytes 16*(l/16)..+15; C[4*(l/16)+r][l%16]):
+//   scores  A = query pieces [head*4 + piece][64 channels of one scale group],
+//           B = keys [64 channels][16 tokens of one page] (key rows are
+//           contiguous), C = [head, piece][token]
+//   P.V     A = probability pieces [head*4 + piece][64 tokens],
+//           B = values [64 tokens][16 channels] (the channel-major page word),
+//           C = [head, piece][channel]
+// A float operand x is split into three int8 pieces with one scale per
+// (head, 64-group): x ~= s1*q1 + s2*q2 + s3*q3, s1 = amax/127,
+// s2 = s1/254, s3 = s2/254, each residual taken exactly with an fma, so
+// |x - sum| <= amax * 6e-8; the integer dots are exact and are combined in
+// fp32.  The fourth piece row is zero.  The value scale of each token is
+// folded into its probability before the split (p' = p * vs).
+//
+// A workgroup = one KV head x `split` tokens, NW waves; wave w takes the
+// 64-token blocks w, w+NW, ... with its own online softmax (per query head:
+// max, sum, output), and the waves merge through LDS.
+// With one split the workgroup writes the output, else (max, sum, output)
+// partials for decode_merge_kernel.
+typedef int att_v4i __attribute__((ext_vector_type(4)));
+
+struct MfmaAttnArgs {
+    KvCache c;
+    const float *query;       // [H][D]
+    float *output;            // [H][D] (nsplit == 1)
+    float *partials;          // [H][nsplit][D + 2] (nsplit > 1)
+    uint32_t group;           // query heads per KV head (<= 4 * RT)
+    uint32_t split;           // tokens per workgroup, a multiple of 64 * waves
+    uint32_t nsplit;
+    float scale;
+    uint32_t position;
+    const int32_t *position_ptr;
+};
+
+__device__ __forceinline__ int piece_round(float v) {
+    return static_cast<int>(fminf(fmaxf(__builtin_rintf(v), -127.0f), 127.0f));
+}
+
+// the three pieces of x for scale s1 (inv1 = 1/s1), packed one byte each
+__device__ __forceinline__ uint32_t three_pieces(float x, float s1, float inv1) {
+    const float s2 = s1 * (1.0f / 254.0f), s3 = s2 * (1.0f / 254.0f);
+    const int q1 = piece_round(x * inv1);
+    const float r1 = fmaf(-static_cast<float>(q1), s1, x);
+    const int q2 = piece_round(r1 * (inv1 * 254.0f));
+    const float r2 = fmaf(-static_cast<float>(q2), s2, r1);
+    const int q3 = piece_round(r2 * (inv1 * 64516.0f));
+    (void)s3;
+    return (static_cast<uint32_t>(q1) & 0xffu) | ((static_cast<uint32_t>(q2) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(q3) & 0xffu) << 16);
+}
+
+__device__ __forceinline__ float pieces_dot(att_v4i cacc, float s1) {
+    const float s2 = s1 * (1.0f / 254.0f), s3 = s2 * (1.0f / 254.0f);
+    return fmaf(s3, static_cast<float>(cacc[2]), fmaf(s2, static_cast<float>(cacc[1]), s1 * static_cast<float>(cacc[0])));
+}
+
+// Reductions over each 16-lane row by DPP row rotations (row_ror 8, 4, 2,
+// 1): every lane of the row ends with the row's max / sum (the sum's
+// association differs between lanes; callers read one lane).
+template <int CTRL>
+__device__ __forceinline__ float dpp_rot(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_rot<0x128>(v));
+    v = fmaxf(v, dpp_rot<0x124>(v));
+    v = fmaxf(v, dpp_rot<0x122>(v));
+    return fmaxf(v, dpp_rot<0x121>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_rot<0x128>(v);
+    v += dpp_rot<0x124>(v);
+    v += dpp_rot<0x122>(v);
+    return v + dpp_rot<0x121>(v);
+}
+
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+constexpr uint32_t kMfmaMaxSplits = 512;
+
+// waves per workgroup (four: eight, two per SIMD, measured slower at 4K and
+// 32K-token contexts on MI355X)
+__host__ __device__ constexpr int mfma_attention_waves(int, int) { return 4; }
+
+template <int D, int RT>
+__global__ __launch_bounds__(64 * mfma_attention_waves(D, RT)) void mfma_attention_kernel(MfmaAttnArgs a) {
+    constexpr int NW = mfma_attention_waves(D, RT);
+    constexpr int NG = D / 64;   // scale groups per head = MFMA k-steps
+    constexpr int NT = 4;        // pages (16-token tiles) per 64-token block
+    constexpr int HR = 4 * RT;   // query-head rows
+    __shared__ __align__(16) int8_t pp_s[NW][RT][NG][4][3][64];  // per wave: p' pieces [head][piece][token]
+    __shared__ float ml_s[NW][HR][2];
+    __shared__ __align__(16) float o_s[NW][HR][D];
+    const KvCache &c = a.c;
+    const uint32_t tid = threadIdx.x, lane = tid % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const uint32_t kvh = blockIdx.y, split = blockIdx.x, G = a.group;
+    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) : a.position;
+    if (pos >= c.max_tokens) return;
+    const uint32_t tokens = pos + 1;
+    const uint32_t t0 = split * a.split;
+    if (t0 >= tokens) {
+        // a split past the position (fixed grid): an empty partial
+        for (uint32_t i = tid; i < G * D; i += blockDim.x) {
+            const uint32_t g = i / D, d = i % D;
+            float *dst = a.partials + (static_cast<size_t>(kvh * G + g) * a.nsplit + split) * (D + 2);
+            dst[2 + d] = 0.0f;
+            if (d == 0) {
+                dst[0] = -INFINITY;
+                dst[1] = 0.0f;
+            }
+        }
+        return;
+    }
+    const uint32_t t1 = min(tokens, t0 + a.split);
+    const uint32_t col = lane % 16, kq = lane / 16;   // MFMA column / k-quarter of this lane
+
+    // 1. query pieces (A of the scores), this lane: head (col / 4) of row
+    //    tile rt, piece col % 4, channels 64g + 16kq .. +15
+    att_v4i qa[RT][NG];
+    float qs1[RT][NG];   // s1 of head kq (+ 4rt): the C-layout head of this lane
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const uint32_t hl = rt * 4 + col / 4, piece = col % 4;
+            float x[16];
+            if (hl < G) {
+                const float4 *src = reinterpret_cast<const float4 *>(
+                    a.query + static_cast<size_t>(kvh * G + hl) * D + 64 * g + 16 * kq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 v = src[i];
+                    x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const float s1 = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
+            const float inv1 = amax > 0.0f ? 127.0f / amax : 1.0f;
+            uint32_t w[4] = {0, 0, 0, 0};
+            if (piece < 3) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    w[i / 4] |= ((three_pieces(x[i], s1, inv1) >> (8 * piece)) & 0xffu) << (8 * (i % 4));
+            }
+            qa[rt][g] = att_v4i{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
+                                static_cast<int>(w[3])};
+            // head h's scale sits in lane 4h (kq 0, piece 0)
+            qs1[rt][g] = __shfl(s1, 4 * kq);
+        }
+
+    float m_run[RT], l_run[RT], o_acc[RT][NG][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) o_acc[rt][g][n] = 0.0f;
+    }
+
+    // 2. loads of a block: keys (B of the scores) for token b0 + 16i + col
+    //    and its scales; value words (B of P.V) of page b0/16 + kq, channel
+    //    64g + 16n + col.  Tokens past t1 read a valid token (t0) and are
+    //    masked.  The next block's loads are issued before this block's
+    //    arithmetic.
+    struct BlockLoads {
+        att_v4i kb[NG][NT], vb[NG][4];
+        float ks[NG][NT], vs[NG][NT];
+    };
+    auto load_block = [&](uint32_t b0, BlockLoads &L) {
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const uint32_t t = b0 + 16 * i + col;
+            const uint32_t tl = t < t1 ? t : t0;
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                L.kb[g][i] = *reinterpret_cast<const att_v4i *>(c.keys + k_index(c, tl, kvh, 64 * g + 16 * kq));
+                L.ks[g][i] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
+                L.vs[g][i] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
+            }
+        }
+        const uint32_t pt = b0 + 16 * kq;
+        const uint32_t pg = (pt < t1 ? pt : t0) / kKvPageTokens;
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+                L.vb[g][n] = *reinterpret_cast<const att_v4i *>(c.values + v_page_offset(c, pg, kvh, 64 * g + 16 * n + col));
+    };
+    // (at head_dim 256 two blocks of loads do not fit the registers: no prefetch)
+    constexpr bool kPrefetch = D <= 128;
+    BlockLoads cur, nxt;
+    if (kPrefetch && t0 + 64 * wave < t1) load_block(t0 + 64 * wave, cur);
+    for (uint32_t b0 = t0 + 64 * wave; b0 < t1; b0 += 64 * NW) {
+        if (!kPrefetch) load_block(b0, cur);
+        else if (b0 + 64 * NW < t1) load_block(b0 + 64 * NW, nxt);
+        const att_v4i (&kb)[NG][NT] = cur.kb;
+        const att_v4i (&vb)[NG][4] = cur.vb;
+        const float (&ks)[NG][NT] = cur.ks;
+        const float (&vs)[NG][NT] = cur.vs;
+        bool valid[NT];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) valid[i] = b0 + 16 * i + col < t1;
+
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            // 3. scores of head kq (+4rt) for token b0 + 16i + col
+            float sc[NT];
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    const att_v4i cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[rt][g], kb[g][i],
+                                                                               att_v4i{0, 0, 0, 0}, 0, 0, 0);
+                    dot = fmaf(pieces_dot(cacc, qs1[rt][g]), ks[g][i], dot);
+                }
+                sc[i] = valid[i] ? dot * a.scale : -INFINITY;
+            }
+            // 4. online softmax of the block (per head: one 16-lane row)
+            float cm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            cm = row16_max(cm);
+            const float mn = fmaxf(m_run[rt], cm);
+            const float alpha = m_run[rt] == -INFINITY ? 0.0f : expf(m_run[rt] - mn);
+            m_run[rt] = mn;
+            float p[NT], ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                p[i] = valid[i] ? expf(sc[i] - mn) : 0.0f;
+                ps += p[i];
+            }
+            l_run[rt] = fmaf(l_run[rt], alpha, row16_sum(ps));
+            // 5. p' = p * vs per scale group, split into pieces -> LDS
+            float ps1[NG];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                float pv[NT], am = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    pv[i] = p[i] * vs[g][i];
+                    am = fmaxf(am, pv[i]);
+                }
+                am = row16_max(am);
+                const float s1 = am > 0.0f ? am * (1.0f / 127.0f) : 1.0f;
+                const float inv1 = am > 0.0f ? 127.0f / am : 1.0f;
+                ps1[g] = s1;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    const uint32_t pc = three_pieces(pv[i], s1, inv1);
+                    int8_t *dst = &pp_s[wave][rt][g][kq][0][16 * i + col];
+                    dst[0] = static_cast<int8_t>(pc & 0xffu);
+                    dst[64] = static_cast<int8_t>((pc >> 8) & 0xffu);
+                    dst[128] = static_cast<int8_t>((pc >> 16) & 0xffu);
+                }
+            }
+            lds_wave_sync();
+            // 6. P.V: A lane = head col/4, piece col%4, tokens 16kq .. +15
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                att_v4i pa = {0, 0, 0, 0};
+                if (col % 4 < 3)
+                    pa = *reinterpret_cast<const att_v4i *>(&pp_s[wave][rt][g][col / 4][col % 4][16 * kq]);
+#pragma unroll
+                for (int n = 0; n < 4; ++n) {
+                    const att_v4i cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb[g][n], att_v4i{0, 0, 0, 0},
+                                                                               0, 0, 0);
+                    o_acc[rt][g][n] = fmaf(o_acc[rt][g][n], alpha, pieces_dot(cacc, ps1[g]));
+                }
+            }
+            lds_wave_sync();
+        }
+        if (kPrefetch) cur = nxt;
+    }
+
+    // 7. merge the four waves: lane (kq, col) holds head kq (+4rt), channel
+    //    64g + 16n + col
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        if (col == 0) {
+            ml_s[wave][rt * 4 + kq][0] = m_run[rt];
+            ml_s[wave][rt * 4 + kq][1] = l_run[rt];
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) o_s[wave][rt * 4 + kq][64 * g + 16 * n + col] = o_acc[rt][g][n];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < G * D; i += blockDim.x) {
+        const uint32_t hl = i / D, d = i % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, ml_s[w][hl][0]);
+        float l = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float m = ml_s[w][hl][0];
+            const float f = m == -INFINITY ? 0.0f : expf(m - mx);
+            l = fmaf(ml_s[w][hl][1], f, l);
+            o = fmaf(o_s[w][hl][d], f, o);
+        }
+        const uint32_t head = kvh * G + hl;
+        if (a.nsplit == 1) {
+            a.output[static_cast<size_t>(head) * D + d] = o / l;
+        } else {
+            float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
+            dst[2 + d] = o;
+            if (d == 0) {
+                dst[0] = mx;
+                dst[1] = l;
+            }
+        }
+    }
+}
+
+template <int D, int RT>
+hipError_t launch_mfma_attention_kernel(const MfmaAttnArgs &args, hipStream_t stream) {
+    hipLaunchKernelGGL((mfma_attention_kernel<D, RT>), dim3(args.nsplit, args.c.kv_heads),
+                       dim3(64 * mfma_attention_waves(D, RT)), 0, stream,
+                       args);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_mfma_attention_rt(const MfmaAttnArgs &args, hipStream_t stream) {
+    return args.group <= 4 ? launch_mfma_attention_kernel<D, 1>(args, stream)
+                           : launch_mfma_attention_kernel<D, 2>(args, stream);
 }
 
 template <int D, int GMAX>
@@ -705,12 +1111,12 @@ hipError_t launch_decode_kernel(const DecodeAttnArgs &args, hipStream_t stream) 
     return hipGetLastError();
 }
 
+// One query head per workgroup (the split attention of longer contexts is
+// the MFMA kernel).
 template <int D>
 hipError_t launch_decode_g(const DecodeAttnArgs &args, hipStream_t stream) {
-    if (args.heads_per_wg <= 1) return launch_decode_kernel<D, 1>(args, stream);
-    if (args.heads_per_wg <= 2) return launch_decode_kernel<D, 2>(args, stream);
-    if (args.heads_per_wg <= 4) return launch_decode_kernel<D, 4>(args, stream);
-    return launch_decode_kernel<D, 8>(args, stream);
+    if (args.heads_per_wg != 1) return hipErrorInvalidValue;
+    return launch_decode_kernel<D, 1>(args, stream);
 }
 
 hipError_t launch_decode_attention_args(const DecodeAttnArgs &args, float *output, hipStream_t stream) {
@@ -734,15 +1140,17 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base) {
     c.groups = (c.channels + 63u) / 64u;
     c.pages = (c.max_tokens + kKvPageTokens - 1) / kKvPageTokens;
     const size_t slots = static_cast<size_t>(c.pages) * kKvPageTokens;
+    const size_t padded_dim = (c.head_dim + 15u) / 16u * 16u;
+    const size_t key_bytes = (slots * c.kv_heads * padded_dim + 255) & ~static_cast<size_t>(255);
     const size_t value_bytes = (slots * c.channels + 255) & ~static_cast<size_t>(255);
     const size_t scale_bytes = (slots * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
     if (base) {
         c.keys = reinterpret_cast<int8_t *>(base);
-        c.values = reinterpret_cast<int8_t *>(base + value_bytes);
-        c.key_scales = reinterpret_cast<float *>(base + 2 * value_bytes);
-        c.value_scales = reinterpret_cast<float *>(base + 2 * value_bytes + scale_bytes);
+        c.values = reinterpret_cast<int8_t *>(base + key_bytes);
+        c.key_scales = reinterpret_cast<float *>(base + key_bytes + value_bytes);
+        c.value_scales = reinterpret_cast<float *>(base + key_bytes + value_bytes + scale_bytes);
     }
-    return 2 * value_bytes + 2 * scale_bytes;
+    return key_bytes + value_bytes + 2 * scale_bytes;
 }
 
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
@@ -774,6 +1182,66 @@ size_t decode_attention_workspace_floats(const KvCache &c, uint32_t query_heads,
     return nsplit > 1 ? static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2) : 0;
 }
 
+bool mfma_attention_supported(const KvCache &c, uint32_t query_heads) {
+    return (c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256) && query_heads >= c.kv_heads &&
+           query_heads % c.kv_heads == 0 && query_heads / c.kv_heads <= 8;
+}
+
+// Tokens per workgroup: one 64-token block per wave, doubled while the grid
+// would exceed 256 workgroups (one per CU, every workgroup resident in one
+// round, each wave streaming its blocks with the next block's loads in
+// flight, and few partials to merge); so at most kMfmaMaxSplits splits per
+// KV head.
+uint32_t mfma_split_tokens(const KvCache &c, uint32_t span, uint32_t waves) {
+    uint32_t s = 64 * waves;
+    while (static_cast<uint64_t>((span + s - 1) / s) * c.kv_heads > 256) s *= 2;
+    return s;
+}
+
+uint32_t mfma_waves(const KvCache &c, uint32_t query_heads) {
+    const int rt = query_heads / c.kv_heads <= 4 ? 1 : 2;
+    return static_cast<uint32_t>(mfma_attention_waves(static_cast<int>(c.head_dim), rt));
+}
+
+uint32_t mfma_attention_launches(const KvCache &c, uint32_t query_heads, uint32_t span) {
+    const uint32_t s = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
+    return (span + s - 1) / s > 1 ? 2 : 1;
+}
+
+size_t mfma_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t span) {
+    const uint32_t s = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
+    const uint32_t nsplit = (span + s - 1) / s;
+    return nsplit > 1 ? static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2) : 0;
+}
+
+hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *output, float *partials,
+                                 uint32_t query_heads, uint32_t position, const int32_t *position_ptr,
+                                 uint32_t span, float scale, hipStream_t stream) {
+    if (!mfma_attention_supported(c, query_heads) || span == 0 || span > c.max_tokens) return hipErrorInvalidValue;
+    MfmaAttnArgs args{};
+    args.c = c;
+    args.query = query;
+    args.output = output;
+    args.partials = partials;
+    args.group = query_heads / c.kv_heads;
+    args.split = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
+    args.nsplit = (span + args.split - 1) / args.split;
+    if ((args.nsplit > 1 && !partials) || args.nsplit > kMfmaMaxSplits) return hipErrorInvalidValue;
+    args.scale = scale;
+    args.position = position;
+    args.position_ptr = position_ptr;
+    hipError_t e;
+    switch (c.head_dim) {
+    case 64: e = launch_mfma_attention_rt<64>(args, stream); break;
+    case 128: e = launch_mfma_attention_rt<128>(args, stream); break;
+    default: e = launch_mfma_attention_rt<256>(args, stream); break;
+    }
+    if (e != hipSuccess || args.nsplit == 1) return e;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(query_heads), dim3(256), 0, stream, partials, output, args.nsplit,
+                       c.head_dim);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t stream) {
     const KvCache &c = *l.cache;
     if (!decode_attention_supported(c, l.query_heads) || (l.key && (c.head_dim % 64 || !l.value || !l.cos_tab ||
@@ -787,12 +1255,11 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.group = l.query_heads / c.kv_heads;
     args.split = decode_split_tokens(c, l.span_tokens);
     args.nsplit = (l.span_tokens + args.split - 1) / args.split;
-    // one query head per workgroup while a workgroup spans the context (the
-    // latency case: K/V are re-read per head from L2); all heads of a KV
-    // head together once the context is split (the bandwidth case)
-    args.heads_per_wg = args.nsplit == 1 ? 1 : args.group;
-    if (args.nsplit > 1 && !l.partials) return hipErrorInvalidValue;
-    if (args.nsplit > 1024) return hipErrorInvalidValue;
+    // one query head per workgroup, the whole context in one split (K/V are
+    // re-read per head from L2: the latency case); longer contexts take the
+    // RoPE/append kernel and the MFMA attention
+    if (args.nsplit != 1) return hipErrorInvalidValue;
+    args.heads_per_wg = 1;
     args.scale = l.scale;
     args.position = l.position;
     args.position_ptr = l.position_ptr;
@@ -819,10 +1286,10 @@ hipError_t launch_kv_append_at(const KvCache &c, const float *key, const float *
 
 size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t position) {
     const uint32_t tokens = position + 1;
+    if (mfma_attention_supported(c, query_heads)) return mfma_attention_workspace_floats(c, query_heads, tokens);
     const uint32_t s = split_tokens(c, tokens);
     const uint32_t nsplit = (tokens + s - 1) / s;
-    return std::max(static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2),
-                    decode_attention_workspace_floats(c, query_heads, tokens));
+    return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
 }
 
 namespace {
@@ -841,6 +1308,8 @@ hipError_t launch_split_and_merge(AttnArgs &args, float *output, hipStream_t str
 }  // namespace
 
 size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads) {
+    if (mfma_attention_supported(c, query_heads))
+        return mfma_attention_workspace_floats(c, query_heads, c.max_tokens);
     const uint32_t nsplit = (c.max_tokens + kDevicePositionSplit - 1) / kDevicePositionSplit;
     return static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2);
 }
@@ -848,6 +1317,9 @@ size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads) {
 hipError_t launch_attention_at(const KvCache &c, const float *query, float *output, uint32_t query_heads,
                                const int32_t *position_ptr, float scale, float *partials, hipStream_t stream) {
     if (query_heads % c.kv_heads != 0 || c.head_dim > 1024) return hipErrorInvalidValue;
+    if (mfma_attention_supported(c, query_heads))
+        return launch_mfma_attention(c, query, output, partials, query_heads, 0, position_ptr, c.max_tokens, scale,
+                                     stream);
     AttnArgs args{};
     args.c = c;
     args.query = query;
@@ -865,18 +1337,9 @@ hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
     const KvCache &c = *a.cache;
     if (a.position >= c.tokens || a.query_heads % c.kv_heads != 0 || c.head_dim > 1024)
         return hipErrorInvalidValue;
-    if (decode_attention_supported(c, a.query_heads)) {
-        DecodeAttentionLaunch l;
-        l.cache = &c;
-        l.query = a.query;
-        l.output = a.output;
-        l.partials = a.partials;
-        l.query_heads = a.query_heads;
-        l.position = a.position;
-        l.span_tokens = a.position + 1;
-        l.scale = a.scale;
-        return launch_decode_attention(l, stream);
-    }
+    if (mfma_attention_supported(c, a.query_heads))
+        return launch_mfma_attention(c, a.query, a.output, a.partials, a.query_heads, a.position, nullptr,
+                                     a.position + 1, a.scale, stream);
     AttnArgs args{};
     args.c = c;
     args.query = a.query;

@@ -345,7 +345,11 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     proto.kv_heads = d->kv_heads;
     proto.head_dim = d->head_dim;
     const size_t cache_bytes = (kv_cache_layout(proto, nullptr) + 255) & ~static_cast<size_t>(255);
-    d->fused_attention = decode_attention_supported(proto, d->heads) && d->head_dim % 64 == 0;
+    // contexts of one split: RoPE, append and attention in one kernel; longer
+    // ones: the RoPE/append kernel, then the split attention (MFMA where the
+    // shape allows) and its merge
+    d->fused_attention = decode_attention_supported(proto, d->heads) && d->head_dim % 64 == 0 &&
+                         decode_split_tokens(proto, d->max_ctx) >= d->max_ctx;
     part(reinterpret_cast<void **>(&d->partials),
          std::max<size_t>(d->fused_attention ? decode_attention_workspace_floats(proto, d->heads, d->max_ctx)
                                              : attention_at_workspace_floats(proto, d->heads),
@@ -437,11 +441,11 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     }
     // qkv, attention (+ merge past one split; RoPE/append and split + merge
     // as three kernels without the fused kernel), o, gate/up, down
-    const uint32_t nsplit = d->fused_attention
-                                ? (d->max_ctx + decode_split_tokens(proto, d->max_ctx) - 1) /
-                                      decode_split_tokens(proto, d->max_ctx)
-                                : 2;
-    d->layer_launches = 4 + (d->fused_attention ? (nsplit > 1 ? 2 : 1) : 3);
+    const uint32_t attention_launches =
+        d->fused_attention ? 1
+                           : 1 + (mfma_attention_supported(proto, d->heads) ? mfma_attention_launches(proto, d->heads, d->max_ctx)
+                                                                           : 2);
+    d->layer_launches = 4 + attention_launches;
     d->launches = d->layer_launches * d->layers + 4;  // + embed, norm image, LM head, step end
     ctx->decoders.push_back(d);
     std::memset(out, 0, sizeof(*out));

@@ -200,9 +200,9 @@ struct KvCache {
     uint32_t groups = 0;       // ceil(channels / 64) scale groups per token
     uint32_t pages = 0;        // ceil(max_tokens / 16)
     uint32_t tokens = 0;
-    int8_t *keys = nullptr;    // [pages][kv_heads][16][head_dim]
-    int8_t *values = nullptr;
-    float *key_scales = nullptr;    // [pages][16][groups]
+    int8_t *keys = nullptr;    // [pages][kv_heads][head_dim/16][16 tokens][16 channels]
+    int8_t *values = nullptr;  // [pages][kv_heads][head_dim][16 tokens]
+    float *key_scales = nullptr;    // [pages][groups][16 tokens]
     float *value_scales = nullptr;
     uint64_t bytes = 0;
 };
@@ -263,6 +263,16 @@ struct DecodeAttentionLaunch {
     const float *cos_tab = nullptr;
     const float *sin_tab = nullptr;
 };
+// int8 MFMA attention (no RoPE/append) over span tokens of the cache: the
+// position from position_ptr when non-null; partials of
+// mfma_attention_workspace_floats floats when the span needs more than one
+// split, merged into output by a second kernel (mfma_attention_launches).
+bool mfma_attention_supported(const KvCache &c, uint32_t query_heads);
+size_t mfma_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t span);
+uint32_t mfma_attention_launches(const KvCache &c, uint32_t query_heads, uint32_t span);
+hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *output, float *partials,
+                                 uint32_t query_heads, uint32_t position, const int32_t *position_ptr,
+                                 uint32_t span, float scale, hipStream_t stream);
 bool decode_attention_supported(const KvCache &c, uint32_t query_heads);
 uint32_t decode_split_tokens(const KvCache &c, uint32_t tokens);
 size_t decode_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t tokens);

@@ -516,13 +516,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_create(QwnCudaContextHandle *handle,
     c.max_tokens = opt->max_tokens;
     c.kv_heads = opt->kv_heads;
     c.head_dim = opt->head_dim;
-    c.channels = opt->kv_heads * opt->head_dim;
-    c.groups = (c.channels + 63u) / 64u;
-    c.pages = (c.max_tokens + qwn::kKvPageTokens - 1) / qwn::kKvPageTokens;
-    const size_t slots = static_cast<size_t>(c.pages) * qwn::kKvPageTokens;
-    const size_t value_bytes = (slots * c.channels + 255) & ~static_cast<size_t>(255);
-    const size_t scale_bytes = (slots * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
-    const size_t total = 2 * value_bytes + 2 * scale_bytes;
+    const size_t total = qwn::kv_cache_layout(c, nullptr);
     // charged like the reference (c/cuda/qwn_hypervsq2_cuda_abi.cu:624-626)
     c.bytes = static_cast<uint64_t>(c.max_tokens) * c.channels * 2u +
               static_cast<uint64_t>(c.max_tokens) * c.groups * sizeof(float) * 2u;
@@ -544,10 +538,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_create(QwnCudaContextHandle *handle,
         return hip_fail("Q8 KV-cache allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
     }
     uint8_t *base = static_cast<uint8_t *>(rk->allocation);
-    c.keys = reinterpret_cast<int8_t *>(base);
-    c.values = reinterpret_cast<int8_t *>(base + value_bytes);
-    c.key_scales = reinterpret_cast<float *>(base + 2 * value_bytes);
-    c.value_scales = reinterpret_cast<float *>(base + 2 * value_bytes + scale_bytes);
+    qwn::kv_cache_layout(c, base);
     if ((e = hipMemsetAsync(base, 0, total, ctx->stream)) != hipSuccess ||
         (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
         free_cache(rk);

@@ -70,6 +70,9 @@ def test_head_dim_65_and_nonfinite(gpu_ctx, oracle_lib):
 @pytest.mark.parametrize("T,H,HK,D,pos", [
     (1, 4, 2, 128, None), (15, 32, 8, 128, None), (17, 32, 8, 128, 9), (300, 12, 2, 128, None),
     (1000, 32, 8, 128, 999), (4096, 32, 8, 128, None), (33, 8, 8, 64, None), (40, 16, 2, 96, 31),
+    # MFMA path: 8 query heads per KV head (two row tiles) at D 256, one KV
+    # head at D 64 over ten splits, the Qwen3-4B heads over 79 splits
+    (70, 16, 2, 256, None), (2500, 8, 1, 64, 2400), (20000, 32, 8, 128, None),
 ])
 def test_shapes(gpu_ctx, oracle_lib, T, H, HK, D, pos):
     run_case(gpu_ctx, oracle_lib, T, H, HK, D, pos=pos, seed=T + H + D)

@@ -41,8 +41,12 @@ def with_norms(rng, model):
     return model
 
 
+# a context of more than one split: RoPE/append kernel + MFMA split attention
+LONG_CTX = dict(SMALL, max_ctx=1500)
+
+
 @pytest.mark.parametrize("cfg,dtype", [(SMALL, "q4_0"), (SMALL, "hvsq2"), (QWEN2_LIKE, "q4_0"),
-                                       (QWEN2_LIKE, "hvsq2")])
+                                       (QWEN2_LIKE, "hvsq2"), (LONG_CTX, "q4_0")])
 def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype):
     rng = np.random.default_rng(31)
     model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
