@@ -131,6 +131,38 @@ __device__ __forceinline__ void put_block32(uint8_t *img, uint32_t units, uint32
 }
 
 
+// Sub-block sb (E = 16 int8 for HyperVSQ-2, 8 for Q4_0, four per word) of
+// the fused prologue's image: its nibble words, and the per-32 correction
+// term summed over the 32/E adjacent lanes holding one 32-block (every lane
+// takes part in the exchange; only sub-blocks below nsub are written).
+template <int KIND>
+__device__ __forceinline__ void put_sub_block(uint8_t *img, uint32_t units, uint32_t sb, uint32_t nsub,
+                                              const uint32_t *w) {
+    int32_t *sums = reinterpret_cast<int32_t *>(img + units * unit_lds_bytes(KIND));
+    if (KIND == kHvsq2) {
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = sdot4(w[i], 0x01010101u, s);
+        s += __shfl_xor(s, 1);
+        if (sb < nsub) {
+            const uint32_t e0 = sb * 16, u = e0 / 256, off = e0 % 256;
+            *reinterpret_cast<uint4 *>(img + u * 272 + off) = split16_evenodd(w);
+            if (sb % 2 == 0) sums[sb / 2] = s;
+        }
+    } else {
+        uint32_t hi, lo;
+        split8(w[0], w[1], hi, lo);
+        int lsum = static_cast<int>(__builtin_amdgcn_udot8(lo, 0x11111111u, 0u, false));
+        lsum += __shfl_xor(lsum, 1);
+        lsum += __shfl_xor(lsum, 2);
+        if (sb < nsub) {
+            const uint32_t e0 = sb * 8, u = e0 / 128, off = e0 % 128;
+            *reinterpret_cast<uint2 *>(img + u * 144 + off) = make_uint2(hi, lo);
+            if (sb % 4 == 0) sums[sb / 4] = 8 * lsum;
+        }
+    }
+}
+
 // Byte address of chunk q of unit u of a row, and of its metadata.
 struct UnitAddr {
     size_t payload, meta;

@@ -325,14 +325,20 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-// FUSED (one token only): the input is an fp32 vector turned into the LDS
-// image by every workgroup; otherwise prebuilt images are copied to LDS.
+// FR (fused, one token only): the input is an fp32 vector turned into the
+// LDS image by every workgroup, in sub-blocks of E elements (16 for
+// HyperVSQ-2, 8 otherwise): FR 1 = one sub-block per thread (the vector fits
+// the workgroup), FR 2 = 32/E sub-blocks per thread.  FR 0: prebuilt images
+// are copied to LDS.
 // Workgroups of up to kGemvMaxWaves waves where a lane's registers allow it
 // (UPL <= 4), else kGemvWaves.
 __host__ __device__ constexpr int max_waves_for(int upl) { return upl <= 4 ? kGemvMaxWaves : kGemvWaves; }
 
-template <int KIND, int MT, int UPL, bool FUSED>
+__host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHvsq2 ? 16 : 8; }
+
+template <int KIND, int MT, int UPL, int FR>
 __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(GemvArgs a) {
+    constexpr bool FUSED = FR != 0;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red[2][kGemvMaxWaves];
     __shared__ uint64_t red_key[kGemvMaxWaves];
@@ -399,21 +405,33 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     const bool writer = active && j == L - 1;
     constexpr bool fused = FUSED && MT == 1;
 
-    // 0. The input: image -> LDS by direct loads, or this thread's 32-element
-    //    block of the fp32 vector(s) into registers.
+    // 0. The input: image -> LDS by direct loads, or the fp32 vector(s) into
+    //    registers: thread t takes the E-element sub-blocks t, t + blockDim,
+    //    ... (the 32/E sub-blocks of a 32-block sit in adjacent lanes).
+    constexpr int E = fused_sub_elems(KIND);
+    constexpr int SR = FR == 1 ? 1 : 32 / E;                 // sub-blocks per thread
+    constexpr int EW = E / 4;                                // float4 / int8 words per sub-block
     const uint32_t nblk = a.units * unit_elems(KIND) / 32;  // 32-blocks in the image
-    const uint32_t nvalid = a.cols / 32;                     // blocks holding input values
-    const uint32_t b = threadIdx.x;
-    float4 xv[8], x2v[8];
+    const uint32_t nsub = nblk * (32 / E);                   // sub-blocks in the image
+    const uint32_t nvalid = a.cols / E;                      // sub-blocks holding input values
+    float4 xv[SR][EW], x2v[SR][EW];
     if constexpr (fused) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (b < nvalid ? b * 32 : 0));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = src[i];
+        for (int r = 0; r < SR; ++r) {
+            const uint32_t sb = threadIdx.x + r * blockDim.x;
+            const float4 *src = reinterpret_cast<const float4 *>(a.x + (sb < nvalid ? sb * E : 0));
+#pragma unroll
+            for (int i = 0; i < EW; ++i) xv[r][i] = src[i];
+        }
         if (a.input_mode != kInF32) {
             const float *p2 = a.input_mode == kInNorm ? a.norm : a.x2;
-            const float4 *src2 = reinterpret_cast<const float4 *>(p2 + (b < nvalid ? b * 32 : 0));
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x2v[i] = src2[i];
+            for (int r = 0; r < SR; ++r) {
+                const uint32_t sb = threadIdx.x + r * blockDim.x;
+                const float4 *src2 = reinterpret_cast<const float4 *>(p2 + (sb < nvalid ? sb * E : 0));
+#pragma unroll
+                for (int i = 0; i < EW; ++i) x2v[r][i] = src2[i];
+            }
         }
     } else {
         issue_image_copy<MT>(a.image, a.image_stride, a.image_bytes, a.ntok, smem);
@@ -467,62 +485,92 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     //    direct loads only (vector loads retire in issue order), then for
     //    every wave's share.
     if constexpr (fused) {
-        float v[32];
+        float v[SR][E];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            v[4 * i] = xv[i].x; v[4 * i + 1] = xv[i].y; v[4 * i + 2] = xv[i].z; v[4 * i + 3] = xv[i].w;
-        }
-        const bool has = b < nvalid;
+        for (int r = 0; r < SR; ++r)
+#pragma unroll
+            for (int i = 0; i < EW; ++i) {
+                v[r][4 * i] = xv[r][i].x; v[r][4 * i + 1] = xv[r][i].y;
+                v[r][4 * i + 2] = xv[r][i].z; v[r][4 * i + 3] = xv[r][i].w;
+            }
+        bool has[SR];
+#pragma unroll
+        for (int r = 0; r < SR; ++r) has[r] = threadIdx.x + r * blockDim.x < nvalid;
         if (a.input_mode == kInNorm) {
             float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
-            ss = wg_sum(has ? ss : 0.0f, red[0], W);
+            for (int r = 0; r < SR; ++r) {
+                float sr = 0.0f;
+#pragma unroll
+                for (int i = 0; i < E; ++i) sr = fmaf(v[r][i], v[r][i], sr);
+                ss += has[r] ? sr : 0.0f;
+            }
+            ss = wg_sum(ss, red[0], W);
             const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.cols) + a.eps);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                v[4 * i] = (v[4 * i] * inv) * x2v[i].x;
-                v[4 * i + 1] = (v[4 * i + 1] * inv) * x2v[i].y;
-                v[4 * i + 2] = (v[4 * i + 2] * inv) * x2v[i].z;
-                v[4 * i + 3] = (v[4 * i + 3] * inv) * x2v[i].w;
-            }
+            for (int r = 0; r < SR; ++r)
+#pragma unroll
+                for (int i = 0; i < EW; ++i) {
+                    v[r][4 * i] = (v[r][4 * i] * inv) * x2v[r][i].x;
+                    v[r][4 * i + 1] = (v[r][4 * i + 1] * inv) * x2v[r][i].y;
+                    v[r][4 * i + 2] = (v[r][4 * i + 2] * inv) * x2v[r][i].z;
+                    v[r][4 * i + 3] = (v[r][4 * i + 3] * inv) * x2v[r][i].w;
+                }
         } else if (a.input_mode == kInSwiglu) {
-            const float u[32] = {x2v[0].x, x2v[0].y, x2v[0].z, x2v[0].w, x2v[1].x, x2v[1].y, x2v[1].z, x2v[1].w,
-                                 x2v[2].x, x2v[2].y, x2v[2].z, x2v[2].w, x2v[3].x, x2v[3].y, x2v[3].z, x2v[3].w,
-                                 x2v[4].x, x2v[4].y, x2v[4].z, x2v[4].w, x2v[5].x, x2v[5].y, x2v[5].z, x2v[5].w,
-                                 x2v[6].x, x2v[6].y, x2v[6].z, x2v[6].w, x2v[7].x, x2v[7].y, x2v[7].z, x2v[7].w};
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = (v[i] / (1.0f + expf(-v[i]))) * u[i];
-        }
-        if (!has) {
+            for (int r = 0; r < SR; ++r)
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+                for (int i = 0; i < EW; ++i) {
+                    const float u[4] = {x2v[r][i].x, x2v[r][i].y, x2v[r][i].z, x2v[r][i].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float g = v[r][4 * i + k];
+                        v[r][4 * i + k] = (g / (1.0f + expf(-g))) * u[k];
+                    }
+                }
         }
+#pragma unroll
+        for (int r = 0; r < SR; ++r)
+            if (!has[r]) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) v[r][i] = 0.0f;
+            }
         if (KIND == kF16) {
-            if (b < nblk) {
-                float4 *dst = reinterpret_cast<float4 *>(smem + b * 144);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) dst[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            for (int r = 0; r < SR; ++r) {
+                const uint32_t sb = threadIdx.x + r * blockDim.x;
+                if (sb < nsub) {
+                    const uint32_t e0 = sb * E;
+                    float4 *dst = reinterpret_cast<float4 *>(smem + (e0 / 32) * 144 + (e0 % 32) * 4);
+#pragma unroll
+                    for (int i = 0; i < EW; ++i)
+                        dst[i] = make_float4(v[r][4 * i], v[r][4 * i + 1], v[r][4 * i + 2], v[r][4 * i + 3]);
+                }
             }
         } else {
             float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            for (int r = 0; r < SR; ++r)
+#pragma unroll
+                for (int i = 0; i < E; ++i) amax = fmaxf(amax, fabsf(v[r][i]));
             amax = wg_max(amax, red[1], W);
             // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
             const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const float inv = 1.0f / scale;
             tok_scale[0] = scale;
             if (a.scale_out && blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = scale;
-            if (b < nblk) {
-                uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const float c = fminf(127.0f, fmaxf(-127.0f, v[i] * inv));
+            for (int r = 0; r < SR; ++r) {
+                uint32_t w[EW];
+#pragma unroll
+                for (int i = 0; i < EW; ++i) w[i] = 0;
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    const float c = fminf(127.0f, fmaxf(-127.0f, v[r][i] * inv));
                     w[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(c))))
                                  << (8 * (i & 3));
                 }
-                put_block32<KIND>(smem, a.units, b, w);
+                put_sub_block<KIND>(smem, a.units, threadIdx.x + r * blockDim.x, nsub, w);
             }
         }
         lds_barrier();
@@ -923,11 +971,16 @@ template <int KIND, int MT, int UPL>
 hipError_t launch_one(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, hipStream_t stream) {
     if constexpr (MT == 1) {
         if (args.input_mode != kInImage) {
-            hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, true>), dim3(grid), dim3(threads), lds, stream, args);
+            // one sub-block per thread when the vector fits the workgroup
+            const uint32_t nsub = args.units * unit_elems(KIND) / fused_sub_elems(KIND);
+            if (nsub <= threads)
+                hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 1>), dim3(grid), dim3(threads), lds, stream, args);
+            else
+                hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 2>), dim3(grid), dim3(threads), lds, stream, args);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<KIND, MT, UPL, false>), dim3(grid), dim3(threads), lds, stream, args);
+    hipLaunchKernelGGL((gemv_kernel<KIND, MT, UPL, 0>), dim3(grid), dim3(threads), lds, stream, args);
     return hipGetLastError();
 }
 
@@ -1133,15 +1186,16 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
 namespace {
 
 // Workgroup width: the fused prologue needs a thread per 32-block of the
-// input; otherwise wider workgroups only when the grid stays >= 2 per CU.
+// input (and runs shortest with a thread per sub-block); otherwise wider
+// workgroups only when the grid stays >= 2 per CU.
 int choose_waves(const GemvGroupLaunch &g, uint32_t total_tiles) {
     const DeviceTensor &t = *g.tensors[0];
     if (g.waves) return g.waves;
     const int wmax = max_waves_for(static_cast<int>(t.upl));
-    const uint32_t nblk = t.units * unit_elems(t.kind) / 32;
+    const uint32_t nsub = t.units * unit_elems(t.kind) / fused_sub_elems(t.kind);
     int w = kGemvWaves;
     if (g.input_mode != kInImage)
-        while (static_cast<uint32_t>(w) * kWaveSize < nblk && w < wmax) w *= 2;
+        while (static_cast<uint32_t>(w) * kWaveSize < nsub && w < wmax) w *= 2;
     while (w < wmax && total_tiles / (2 * w) >= 512) w *= 2;
     return w;
 }
