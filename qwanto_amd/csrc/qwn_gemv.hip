@@ -327,9 +327,8 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
 
 // FR (fused, one token only): the input is an fp32 vector turned into the
 // LDS image by every workgroup, in sub-blocks of E elements (16 for
-// HyperVSQ-2, 8 otherwise): FR 1 = one sub-block per thread (the vector fits
-// the workgroup), FR 2 = 32/E sub-blocks per thread.  FR 0: prebuilt images
-// are copied to LDS.
+// HyperVSQ-2, 8 otherwise), FR (1 .. 32/E) sub-blocks per thread: the fewer,
+// the shorter each thread's chain.  FR 0: prebuilt images are copied to LDS.
 // Workgroups of up to kGemvMaxWaves waves where a lane's registers allow it
 // (UPL <= 4), else kGemvWaves.
 __host__ __device__ constexpr int max_waves_for(int upl) { return upl <= 4 ? kGemvMaxWaves : kGemvWaves; }
@@ -409,7 +408,7 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     //    registers: thread t takes the E-element sub-blocks t, t + blockDim,
     //    ... (the 32/E sub-blocks of a 32-block sit in adjacent lanes).
     constexpr int E = fused_sub_elems(KIND);
-    constexpr int SR = FR == 1 ? 1 : 32 / E;                 // sub-blocks per thread
+    constexpr int SR = FR > 0 ? FR : 1;                      // sub-blocks per thread
     constexpr int EW = E / 4;                                // float4 / int8 words per sub-block
     const uint32_t nblk = a.units * unit_elems(KIND) / 32;  // 32-blocks in the image
     const uint32_t nsub = nblk * (32 / E);                   // sub-blocks in the image
@@ -971,12 +970,22 @@ template <int KIND, int MT, int UPL>
 hipError_t launch_one(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, hipStream_t stream) {
     if constexpr (MT == 1) {
         if (args.input_mode != kInImage) {
-            // one sub-block per thread when the vector fits the workgroup
+            // as few sub-blocks per thread as the workgroup allows
             const uint32_t nsub = args.units * unit_elems(KIND) / fused_sub_elems(KIND);
-            if (nsub <= threads)
+            const uint32_t per_thread = (nsub + threads - 1) / threads;
+            if (per_thread <= 1)
                 hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 1>), dim3(grid), dim3(threads), lds, stream, args);
-            else
+            else if (per_thread <= 2)
                 hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 2>), dim3(grid), dim3(threads), lds, stream, args);
+            else if constexpr (fused_sub_elems(KIND) == 8) {
+                if (per_thread <= 3)
+                    hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 3>), dim3(grid), dim3(threads), lds, stream, args);
+                else
+                    hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 4>), dim3(grid), dim3(threads), lds, stream,
+                                       args);
+            } else {
+                return hipErrorInvalidValue;
+            }
             return hipGetLastError();
         }
     }
