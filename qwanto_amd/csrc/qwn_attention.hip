@@ -420,8 +420,9 @@ struct DecodeAttnArgs {
     const int32_t *position_ptr;
     const float *key;        // decode mode: current token fp32 [channels]
     const float *value;
-    const float *cos_tab;    // [max_tokens][D/2]
+    const float *cos_tab;    // [max_tokens][D/2], or [D/2] for the current position (rope_row_only)
     const float *sin_tab;
+    uint32_t rope_row_only;
 };
 
 __device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *ct, const float *st) {
@@ -463,10 +464,34 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
     const uint32_t h0 = kvh * a.group + (blockIdx.y % wgs_per_kv) * G;
     const bool writer = blockIdx.y % wgs_per_kv == 0;  // appends the current token
     const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const uint32_t t0 = split * a.split;
+    // One round trip per chunk: thread tid takes token c0 + tid -- its key
+    // row and scales -- and VW value words (page, channel) of the chunk;
+    // threads past the chunk's n tokens, and pages without one, read the
+    // split's first token or page again (cache hits), and are masked.  The
+    // current token's slot is being written by this launch: its key, value
+    // bytes and scales come from LDS.
+    uint4 kr[KW], vr[VW];
+    float ks[NG], vsc[NG];
+    auto load_chunk = [&](uint32_t c0, uint32_t n) {
+        const uint32_t tl = tid < n ? c0 + tid : t0;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, 16 * w));
+#pragma unroll
+        for (int w = 0; w < VW; ++w) {
+            const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
+            const uint32_t pg = pl * kKvPageTokens < n ? c0 / kKvPageTokens + pl : t0 / kKvPageTokens;
+            vr[w] = *reinterpret_cast<const uint4 *>(c.values + v_page_offset(c, pg, kvh, ch));
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
+            vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
+        }
+    };
     const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) : a.position;
     if (pos >= c.max_tokens) return;
     const uint32_t tokens = pos + 1;
-    const uint32_t t0 = split * a.split;
     if (t0 >= tokens) {
         // a split past the position (fixed grid): an empty partial
         for (uint32_t i = tid; i < G * D; i += blockDim.x) {
@@ -484,8 +509,9 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
     const bool rope = a.key != nullptr;
     const bool cur = rope && pos >= t0 && pos < t1;
     constexpr uint32_t half = D / 2;
-    const float *ct = rope ? a.cos_tab + static_cast<size_t>(pos) * half : nullptr;
-    const float *st = rope ? a.sin_tab + static_cast<size_t>(pos) * half : nullptr;
+    const size_t rope_off = a.rope_row_only ? 0 : static_cast<size_t>(pos) * half;
+    const float *ct = rope ? a.cos_tab + rope_off : nullptr;
+    const float *st = rope ? a.sin_tab + rope_off : nullptr;
 
     // 1. query heads of this KV head (rotated in decode mode) -> LDS
     for (uint32_t i = tid; i < GMAX * D; i += blockDim.x) {
@@ -530,33 +556,10 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
 
     for (uint32_t c0 = t0; c0 < t1; c0 += CH) {
         const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
-        // 2. one round trip: thread tid takes token c0 + tid -- its key row
-        //    and scales -- and VW value words (page, channel) of the chunk
-        //    (global loads; the current token from LDS)
+        // 2. the chunk's loads
+        load_chunk(c0, n);
         const bool has = tid < n;
-        const uint32_t tk = has ? c0 + tid : t0;
-        const bool is_cur = cur && has && tk == pos;
-        uint4 kr[KW], vr[VW];
-        float ks[NG], vsc[NG];
-        {
-            // the current token's slot is being written by this launch: load
-            // any written row instead and take the token from LDS below
-            const uint32_t tl = is_cur ? t0 : tk;
-#pragma unroll
-            for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, 16 * w));
-#pragma unroll
-            for (int w = 0; w < VW; ++w) {
-                const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
-                // a page with no token of the chunk: read the first page instead
-                const uint32_t pg = pl * kKvPageTokens < n ? c0 / kKvPageTokens + pl : t0 / kKvPageTokens;
-                vr[w] = *reinterpret_cast<const uint4 *>(c.values + v_page_offset(c, pg, kvh, ch));
-            }
-#pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
-                vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
-            }
-        }
+        const bool is_cur = cur && has && c0 + tid == pos;
         if (cur) {
 #pragma unroll
             for (int w = 0; w < KW; ++w) {
@@ -1267,6 +1270,7 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.value = l.value;
     args.cos_tab = l.cos_tab;
     args.sin_tab = l.sin_tab;
+    args.rope_row_only = l.rope_row_only ? 1u : 0u;
     return launch_decode_attention_args(args, l.output, stream);
 }
 

@@ -47,12 +47,23 @@ struct EmbedArgs {
     const int32_t *feed;
     const int32_t *state;  // [0] = last greedy token, [1] = position
     float *x;
+    // RoPE: the table rows of the step's position copied to rope_row
+    // ([cos | sin], 2 * half floats) for the attention kernels to read at a
+    // fixed address
+    const float *cos_tab, *sin_tab;
+    uint32_t half;
+    float *rope_row;
 };
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= a.units * 4) return;
     const int32_t pos = a.state[1];
+    if (idx < 2 * a.half) {
+        const uint32_t row = (pos >= 0 && static_cast<uint32_t>(pos) < a.max_ctx) ? static_cast<uint32_t>(pos) : 0u;
+        const float *tab = idx < a.half ? a.cos_tab : a.sin_tab;
+        a.rope_row[idx] = tab[static_cast<size_t>(row) * a.half + idx % a.half];
+    }
+    if (idx >= a.units * 4) return;
     int32_t token = (pos >= 0 && static_cast<uint32_t>(pos) < a.max_ctx) ? a.feed[pos] : -1;
     if (token < 0) token = a.state[0];
     if (token < 0 || static_cast<uint32_t>(token) >= a.vocab) token = 0;
@@ -105,7 +116,7 @@ struct Decoder {
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gate = nullptr,
           *up = nullptr, *logits = nullptr, *partials = nullptr;
     float *norms_in = nullptr, *norms_post = nullptr, *final_norm = nullptr, *cos_tab = nullptr,
-          *sin_tab = nullptr;
+          *sin_tab = nullptr, *rope_row = nullptr;
     uint64_t *argmax = nullptr;
     uint32_t argmax_n = 0;
     uint8_t *head_image = nullptr;  // fp32 image of the final-norm output
@@ -159,7 +170,11 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
     ea.feed = d->feed;
     ea.state = d->state;
     ea.x = d->x;
-    hipLaunchKernelGGL(embed_kernel, dim3((ea.units * 4 + 255) / 256), dim3(256), 0, s, ea);
+    ea.cos_tab = d->cos_tab;
+    ea.sin_tab = d->sin_tab;
+    ea.half = d->head_dim / 2;
+    ea.rope_row = d->rope_row;
+    hipLaunchKernelGGL(embed_kernel, dim3((std::max(ea.units * 4, 2 * ea.half) + 255) / 256), dim3(256), 0, s, ea);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     ++n;
     int32_t *pos = d->state + 1;
@@ -183,8 +198,9 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
             at.scale = d->attn_scale;
             at.key = d->k;
             at.value = d->v;
-            at.cos_tab = d->cos_tab;
-            at.sin_tab = d->sin_tab;
+            at.cos_tab = d->rope_row;
+            at.sin_tab = d->rope_row + d->head_dim / 2;
+            at.rope_row_only = true;
             if ((e = launch_decode_attention(at, s)) != hipSuccess) return e;
         } else {
             if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s)) !=
@@ -336,6 +352,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     const uint32_t half = d->head_dim / 2;
     part(reinterpret_cast<void **>(&d->cos_tab), static_cast<size_t>(d->max_ctx) * half * 4);
     part(reinterpret_cast<void **>(&d->sin_tab), static_cast<size_t>(d->max_ctx) * half * 4);
+    part(reinterpret_cast<void **>(&d->rope_row), static_cast<size_t>(half) * 2 * 4);
     part(reinterpret_cast<void **>(&d->state), 2 * 4);
     part(reinterpret_cast<void **>(&d->feed), static_cast<size_t>(d->max_ctx) * 4);
     part(reinterpret_cast<void **>(&d->out_tokens), static_cast<size_t>(d->max_ctx) * 4);

@@ -260,8 +260,9 @@ struct DecodeAttentionLaunch {
     float scale = 1.0f;
     const float *key = nullptr;
     const float *value = nullptr;
-    const float *cos_tab = nullptr;
+    const float *cos_tab = nullptr;   // [max_tokens][head_dim / 2], or the position's row only:
     const float *sin_tab = nullptr;
+    bool rope_row_only = false;       // cos_tab / sin_tab hold just the current position's row
 };
 // int8 MFMA attention (no RoPE/append) over span tokens of the cache: the
 // position from position_ptr when non-null; partials of
