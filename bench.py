@@ -51,7 +51,7 @@ def parse():
     p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
     p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
-    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "copy"),
+    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "batch", "copy"),
                    help="profiling mode: run only one workload (for rocprofv3)")
     return p.parse_args()
 
@@ -276,7 +276,8 @@ def attention_bench(torch, ctx, steps=50):
 
 class MfmaSweep:
     """Resident HyperVSQ-2 tensors of `layers` layers with MFMA images of M
-    tokens (8..16): one int8-MFMA GEMM launch per tensor."""
+    tokens (8..16): int8-MFMA GEMM launches grouped as the decoder groups its
+    GEMVs (q/k/v, o, gate/up, down: four per layer)."""
 
     def __init__(self, torch, ctx, shapes, layers, seed, batch):
         import numpy as np
@@ -303,16 +304,16 @@ class MfmaSweep:
                 ctx.quantize_device(x.data_ptr(), batch, K, K, q8.data_ptr(), q8.shape[1], sc.data_ptr(), stream=s)
                 img = torch.zeros(ctx.mfma_image_bytes(h0), dtype=torch.uint8, device=dev)
                 ctx.mfma_image_device(h0, q8.data_ptr(), batch, q8.shape[1], img.data_ptr(), stream=s)
-                for p in projs:
-                    out = torch.zeros(batch, shapes[p][0], device=dev)
-                    self.items.append((layer[p], img, sc, out))
-                    self.weight_bytes += synth.weight_bytes("hvsq2", *shapes[p])
+                outs = [torch.zeros(batch, shapes[p][0], device=dev) for p in projs]
+                self.items.append(([layer[p] for p in projs], img, sc, outs))
+                self.weight_bytes += sum(synth.weight_bytes("hvsq2", *shapes[p]) for p in projs)
         torch.cuda.synchronize()
         self.flops = 2 * batch * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * layers
 
     def run(self, stream):
-        for h, img, sc, out in self.items:
-            self.ctx.gemm_mfma_device(h, img.data_ptr(), sc.data_ptr(), out.data_ptr(), self.batch, stream=stream)
+        for hs, img, sc, outs in self.items:
+            self.ctx.gemm_mfma_group_device(hs, img.data_ptr(), sc.data_ptr(), [o.data_ptr() for o in outs],
+                                            self.batch, stream=stream)
 
     def close(self):
         for h in self.handles:
@@ -326,7 +327,7 @@ INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
 def batch_sweep(torch, ctx, steps, warmup):
     """HyperVSQ-2 GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers
     of the Qwen3-4B shapes (weights read once per launch): dot8 grouped
-    launches below 8 tokens, one int8-MFMA launch per tensor from 8 up
+    launches below 8 tokens, grouped int8-MFMA launches from 8 up
     (MFMA utilisation = useful int8 ops / dense int8 peak)."""
     from qwanto_amd import synth
     out = {}
@@ -437,6 +438,10 @@ def main():
         return
     if args.profile == "attention":
         print(json.dumps({"profile_mode": "attention", **attention_bench(torch, ctx, args.steps)}), flush=True)
+        return
+    if args.profile == "batch":
+        print(json.dumps({"profile_mode": "batch", **batch_sweep(torch, ctx, args.steps, args.warmup)}),
+              flush=True)
         return
     t_setup = time.perf_counter()
     sweep = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, args.layers, seed=1)

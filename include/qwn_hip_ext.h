@@ -153,6 +153,14 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *context,
                                                   const QwnCudaTensorHandle *tensor, const void *image,
                                                   const float *scales, float *output, uint32_t batch,
                                                   uint32_t output_stride, void *stream);
+/* The same GEMM over `count` (1..4) HyperVSQ-2 tensors with the same
+ * column count that share one MFMA image (q/k/v, gate/up), in one launch:
+ * outputs[i] [batch][output_stride or the tensor's rows]. */
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *context,
+                                                        const QwnCudaTensorHandle *tensors, uint32_t count,
+                                                        const void *image, const float *scales,
+                                                        float *const *outputs, uint32_t batch,
+                                                        uint32_t output_stride, void *stream);
 
 /* Per-token int8 quantization on the device without an image:
  * x fp32 [batch][x_stride] -> q8 [batch][q8_stride] (zero padded past

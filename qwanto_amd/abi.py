@@ -54,6 +54,7 @@ EXT_EXPORTS = (
     "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
     "qwn_hip_ext_gemv_group_partials", "qwn_hip_ext_gemv_group_device", "qwn_hip_ext_argmax_device",
     "qwn_hip_ext_mfma_image_bytes", "qwn_hip_ext_mfma_image_device", "qwn_hip_ext_gemm_mfma_device",
+    "qwn_hip_ext_gemm_mfma_group_device",
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
@@ -279,6 +280,7 @@ class Library:
         lib.qwn_hip_ext_mfma_image_bytes.restype = ctypes.c_uint64
         lib.qwn_hip_ext_mfma_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V, V]
         lib.qwn_hip_ext_gemm_mfma_device.argtypes = [P(Handle), P(Handle), V, V, V, U32, U32, V]
+        lib.qwn_hip_ext_gemm_mfma_group_device.argtypes = [P(Handle), P(Handle), U32, V, V, V, U32, U32, V]
         lib.qwn_hip_decoder_create.argtypes = [P(Handle), P(DecoderDesc), P(Handle)]
         lib.qwn_hip_decoder_destroy.argtypes = [P(Handle), P(Handle)]
         lib.qwn_hip_decoder_reset.argtypes = [P(Handle), P(Handle)]
@@ -452,6 +454,15 @@ class Context:
                          output_stride: int = 0, stream: int | None = None) -> None:
         self.lib.check("gemm_mfma_device", self.lib.lib.qwn_hip_ext_gemm_mfma_device(
             self._h, ctypes.byref(h), image_ptr, scales_ptr, out_ptr, batch, output_stride, stream))
+
+    def gemm_mfma_group_device(self, handles, image_ptr: int, scales_ptr: int, out_ptrs, batch: int,
+                               output_stride: int = 0, stream: int | None = None) -> None:
+        """One MFMA launch over 1..4 tensors of equal columns sharing an image."""
+        n = len(handles)
+        hs = (Handle * n)(*handles)
+        outs = (ctypes.c_void_p * n)(*out_ptrs)
+        self.lib.check("gemm_mfma_group_device", self.lib.lib.qwn_hip_ext_gemm_mfma_group_device(
+            self._h, hs, n, image_ptr, scales_ptr, outs, batch, output_stride, stream))
 
     # -- KV cache ---------------------------------------------------------------
     def kv_create(self, max_tokens: int, kv_heads: int, head_dim: int) -> Handle:

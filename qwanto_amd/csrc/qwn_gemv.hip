@@ -706,17 +706,23 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 // lies in [-15, 30], so a whole 256-weight block is one exact int8 dot
 // product per (row, token):
 //   y[t][n] = xs_t * sum_blocks (d/8 * sum_i w_i a_t,i + m * sum_i a_t,i)
-// (the same combination as the dot8 path).  A wave computes 16 rows x 16
-// tokens with v_mfma_i32_16x16x64_i8, four instructions per block: lane l
-// holds A row l%16 and B column (token) l%16 for k-bytes 16*(l/16)..+15, and
-// C[4*(l/16)+r][l%16] (layout checked on the device).  Lane group g = l/16
-// takes the block's code chunk g (octants 2g, 2g+1); instruction s takes
-// its code dword s.  The A bytes come out of the code dword through a byte
-// permute over the table [-s, 0, s, 2s]: output dword k holds the weights of
-// code fields k of bytes 0..3, i.e. elements 4*byte + k, so the MFMA image
-// stores each 16-element group of activations in that transposed order:
+// (the same combination as the dot8 path).  A 16-row x 16-token tile takes
+// four v_mfma_i32_16x16x64_i8 per block: lane l holds A row l%16 and B
+// column (token) l%16 for k-bytes 16*(l/16)..+15, and C[4*(l/16)+r][l%16].
+// Lane group g = l/16 takes the block's code chunk g (octants 2g, 2g+1);
+// instruction s takes its code dword s.  The A bytes come out of the code
+// dword through a byte permute over the table [-s, 0, s, 2s]: output dword
+// k holds the weights of code fields k of bytes 0..3, i.e. elements
+// 4*byte + k, so the MFMA image stores each 16-element group of activations
+// in that transposed order:
 //   image [block][s][g][token 0..15][16 B] (byte 4k+b = element 16s+4b+k of
 //   the group 64g..64g+63), then int32 sums [block][token 0..15].
+// The weights stay in the GEMV wave-tile layout (one resident copy).  A
+// wave owns RT row tiles (16*RT rows, sharing each image load) and a range
+// of K blocks, and issues every load of up to five blocks before its first
+// MFMA, as the batch-1 GEMV issues its whole weight share at once; the
+// waves that split one row group's K combine their partial tiles through
+// LDS in wave order.
 constexpr int kMfmaTokens = 16;
 
 __host__ __device__ constexpr size_t mfma_image_block_bytes() { return 16 * 256 + 16 * 4; }
@@ -757,92 +763,238 @@ __global__ __launch_bounds__(256) void mfma_image_kernel(const int8_t *__restric
 
 typedef int mfma_v4i __attribute__((ext_vector_type(4)));
 
+// One launch over up to kMaxGroup HyperVSQ-2 tensors that share the image
+// (same K, so the same wave-tile plan).  Job i owns workgroups
+// [job_block[i], job_block[i+1]).  A workgroup computes one row group of
+// 16*RT rows; its 2^ks_log2 waves split the K blocks (wave ks takes blocks
+// [ks*nb, ks*nb + nb)).
 struct MfmaArgs {
-    const uint8_t *payload;
-    const uint8_t *meta;
+    const uint8_t *payload[kMaxGroup];
+    const uint8_t *meta[kMaxGroup];
+    float *output[kMaxGroup];
+    uint32_t rows[kMaxGroup];
+    uint32_t tiles[kMaxGroup];  // wave tiles allocated per job
+    uint32_t output_stride[kMaxGroup];
+    uint32_t job_block[kMaxGroup + 1];
     size_t tile_payload_bytes;
     size_t tile_meta_bytes;
-    uint32_t rows, units, lanes, rows_per_wave;
-    const uint8_t *image;   // mfma image of up to 16 tokens
-    const float *scales;    // [ntok]
-    float *output;          // [ntok][output_stride]
+    uint32_t units, lanes_log2, rows_per_wave_log2;
+    uint32_t ks_log2;      // waves per workgroup (log2)
+    uint32_t nb;           // K blocks per wave
+    uint32_t stage_bytes;  // LDS bytes of the staged weight region (STAGE)
+    const uint8_t *image;  // mfma image of up to 16 tokens
+    const float *scales;   // [ntok]
     uint32_t ntok;
-    uint32_t output_stride;
+    uint32_t vec_out;      // bit i: job i's rows may be stored 4 at a time (16-byte aligned)
 };
 
-// A workgroup computes one 16-row x 16-token tile; its four waves split the
-// K blocks (wave w takes blocks w, w+4, ...) and the partial tiles are
-// summed through LDS, so a matrix yields four times the waves and each
-// wave's chain of dependent block iterations is a quarter as long.
-__global__ __launch_bounds__(256) void mfma_hvsq2_kernel(MfmaArgs a) {
-    __shared__ float part_s[3][kWaveSize][4];
+constexpr int kMfmaMaxWaves = 8;
+
+// Byte offsets of (row, unit, chunk g) in the wave-tile layout, relative to
+// the first tile `t0`:
+//   payload (tile - t0) * tile_payload + 64*R*L*slot + (g*R*n + grp*n + jj) * 16
+//   meta    (tile - t0) * tile_meta    +  8*R*L*slot + (grp*n + jj) * 8
+// with slot = unit / L, jj = unit % L, n = units in the slot.
+struct MfmaUnit {
+    size_t payload, meta;
+};
+__device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, uint32_t t0, uint32_t b, uint32_t g) {
+    const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+    const uint32_t slot = b >> a.lanes_log2, jj = b & (L - 1);
+    const uint32_t n = min(L, a.units - slot * L);
+    const uint32_t tile = (row >> a.rows_per_wave_log2) - t0, grp = row & (R - 1);
+    MfmaUnit u;
+    u.payload = tile * a.tile_payload_bytes + static_cast<size_t>(64) * R * L * slot +
+                (static_cast<size_t>(g) * R * n + grp * n + jj) * 16;
+    u.meta = tile * a.tile_meta_bytes + static_cast<size_t>(8) * R * L * slot + (grp * n + jj) * 8;
+    return u;
+}
+
+// One chunk of up to NB blocks.  The image loads (and, without STAGE, the
+// weight loads) of the whole chunk are issued before the first MFMA.
+// STAGE: the row group's weight tiles were copied to LDS (payload at 0, meta
+// at `meta_lds`) and the A operands are read from there.
+template <int NB, int RT, bool STAGE>
+__device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
+                                           const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
+                                           uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
+                                           float (&acc)[RT][4]) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.units) * 4096);
+    uint4 A[NB][RT];
+    uint2 Mt[NB][RT];
+    mfma_v4i B[NB][4];
+    int SA[NB];
+    if constexpr (!STAGE) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const uint32_t row = r0 + 16 * t + m;
+                const MfmaUnit u = mfma_unit(a, row < rows ? row : 0, 0, b, g);
+                A[i][t] = *reinterpret_cast<const uint4 *>(payload + u.payload);
+                Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
+        const uint8_t *ib = a.image + static_cast<size_t>(b) * 4096 + lane * 16;
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) B[i][sl] = *reinterpret_cast<const mfma_v4i *>(ib + sl * 1024);
+        SA[i] = sums[b * 16 + m];
+    }
+    if constexpr (STAGE) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) {
+                const uint32_t row = r0 + 16 * t + m;
+                const MfmaUnit u = mfma_unit(a, row < rows ? row : r0, t0, b, g);
+                A[i][t] = *reinterpret_cast<const uint4 *>(lds + u.payload);
+                Mt[i][t] = *reinterpret_cast<const uint2 *>(lds + meta_lds + u.meta);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            if (r0 + 16 * t + m >= rows) Mt[i][t] = make_uint2(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (static_cast<uint32_t>(i) >= nblk) break;
+        const float sa = static_cast<float>(SA[i]);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t subs = (Mt[i][t].y >> (8 * g)) & 0xffu;
+            const uint32_t cw[4] = {A[i][t].x, A[i][t].y, A[i][t].z, A[i][t].w};
+            mfma_v4i ci = {0, 0, 0, 0};
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const uint32_t sub = (subs >> (4 * (sl >> 1))) & 15u;
+                // table bytes: code 0 -> -s, 1 -> 0, 2 -> s, 3 -> 2s
+                const uint32_t lut = ((0u - sub) & 0xffu) | (sub << 16) | ((2u * sub) << 24);
+                const uint32_t c = cw[sl];
+                mfma_v4i av;
+                av.x = static_cast<int>(__builtin_amdgcn_perm(0u, lut, c & 0x03030303u));
+                av.y = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 2) & 0x03030303u));
+                av.z = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 4) & 0x03030303u));
+                av.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
+                ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B[i][sl], ci, 0, 0, 0);
+            }
+            // C element r of this lane is row 4g + r of the tile: its
+            // d_base / m_base were loaded by lane 4g + r
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t dm = static_cast<uint32_t>(__shfl(static_cast<int>(Mt[i][t].x), 4 * g + r));
+                const float dsc = half_to_float(dm & 0xffffu) * 0.125f;
+                const float msc = half_to_float(dm >> 16);
+                acc[t][r] = fmaf(static_cast<float>(ci[r]), dsc, fmaf(msc, sa, acc[t][r]));
+            }
+        }
+    }
+}
+
+template <int NB, int RT, bool STAGE>
+__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(MfmaArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-    const uint32_t row0 = blockIdx.x * 16;
-    const uint32_t g = lane / 16, m = lane % 16;
-    const uint32_t na = row0 + m;              // A-operand row of this lane
-    const bool va = na < a.rows;
-    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.units) * 4096);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-    for (uint32_t b = wave; b < a.units; b += 4) {
-        uint4 codes = make_uint4(0, 0, 0, 0);
-        uint32_t subs = 0;
-        if (va) {
-            const UnitAddr ad = unit_addr(na, b, g, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
-                                          a.tile_meta_bytes);
-            codes = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
-            subs = a.meta[ad.meta + 4 + g];
-        }
-        float dsc[4], msc[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t no = row0 + 4 * g + r;
-            uint32_t dm = 0;
-            if (no < a.rows) {
-                const UnitAddr ad = unit_addr(no, b, 0, a.lanes, a.rows_per_wave, a.units, a.tile_payload_bytes,
-                                              a.tile_meta_bytes);
-                dm = *reinterpret_cast<const uint32_t *>(a.meta + ad.meta);
-            }
-            dsc[r] = half_to_float(dm & 0xffffu) * 0.125f;
-            msc[r] = half_to_float(dm >> 16);
-        }
-        const uint8_t *ib = a.image + static_cast<size_t>(b) * 4096 + lane * 16;
-        mfma_v4i bv[4];
-#pragma unroll
-        for (int sl = 0; sl < 4; ++sl) bv[sl] = *reinterpret_cast<const mfma_v4i *>(ib + sl * 1024);
-        const float sa = static_cast<float>(sums[b * 16 + m]);
-        const uint32_t cw[4] = {codes.x, codes.y, codes.z, codes.w};
-        mfma_v4i ci = {0, 0, 0, 0};
-#pragma unroll
-        for (int sl = 0; sl < 4; ++sl) {
-            const uint32_t sub = (subs >> (4 * (sl >> 1))) & 15u;
-            // table bytes: code 0 -> -s, 1 -> 0, 2 -> s, 3 -> 2s (zero rows: all 0)
-            const uint32_t lut = ((0u - sub) & 0xffu) | (sub << 16) | ((2u * sub) << 24);
-            const uint32_t c = cw[sl];
-            mfma_v4i av;
-            av.x = static_cast<int>(__builtin_amdgcn_perm(0u, lut, c & 0x03030303u));
-            av.y = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 2) & 0x03030303u));
-            av.z = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 4) & 0x03030303u));
-            av.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
-            ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[sl], ci, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            acc[r] = fmaf(static_cast<float>(ci[r]), dsc[r], fmaf(msc[r], sa, acc[r]));
+    const uint32_t KS = 1u << a.ks_log2;
+    const uint32_t ks = wave;
+    const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
+    uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
+    job = __builtin_amdgcn_readfirstlane(job);
+    const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
+    const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
+    float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
+    const uint32_t rows = job == 0 ? a.rows[0] : job == 1 ? a.rows[1] : job == 2 ? a.rows[2] : a.rows[3];
+    const uint32_t tiles = job == 0 ? a.tiles[0] : job == 1 ? a.tiles[1] : job == 2 ? a.tiles[2] : a.tiles[3];
+    const uint32_t stride = job == 0   ? a.output_stride[0]
+                            : job == 1 ? a.output_stride[1]
+                            : job == 2 ? a.output_stride[2]
+                                       : a.output_stride[3];
+    const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
+    const uint32_t r0 = (blockIdx.x - first) * (16 * RT);
+    const uint32_t kb0 = ks * a.nb;
+    const uint32_t kb1 = min(a.units, kb0 + a.nb);
+
+    // STAGE: the row group's wave tiles (16*RT rows = a whole number of
+    // tiles) are contiguous in HBM; copy payload and meta into LDS with
+    // direct 16-byte loads, every load instruction one contiguous 1 KB span
+    const uint32_t t0 = r0 >> a.rows_per_wave_log2;
+    uint32_t meta_lds = 0;
+    if constexpr (STAGE) {
+        const uint32_t ntile = min((16u * RT) >> a.rows_per_wave_log2, tiles - t0);
+        const uint32_t pbytes = ntile * static_cast<uint32_t>(a.tile_payload_bytes);
+        const uint32_t mbytes = ntile * static_cast<uint32_t>(a.tile_meta_bytes);
+        meta_lds = ((16u * RT) >> a.rows_per_wave_log2) * static_cast<uint32_t>(a.tile_payload_bytes);
+        const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
+        const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
+        for (uint32_t c0 = wave * kWaveSize * 16; c0 < pbytes; c0 += blockDim.x * 16)
+            if (c0 + lane * 16 < pbytes)
+                __builtin_amdgcn_global_load_lds(psrc + c0 + lane * 16, (lds_void *)(smem + c0), 16, 0, 0);
+        for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
+            if (c0 + lane * 16 < mbytes)
+                __builtin_amdgcn_global_load_lds(msrc + c0 + lane * 16, (lds_void *)(smem + meta_lds + c0), 16, 0,
+                                                 0);
+        wait_vmcnt<0>();               // this wave's copies landed
+        __builtin_amdgcn_s_barrier();  // ... and every wave's
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-    // sum the four waves' partial tiles (in wave order)
-    if (wave > 0)
+
+    float acc[RT][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part_s[wave - 1][lane][r] = acc[r];
-    __syncthreads();
-    if (wave == 0 && m < a.ntok) {
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB)
+        mfma_chunk<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+                                  min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
+
+    // the K-split partials, summed in wave order (LDS after the staged tiles)
+    if (KS > 1) {
+        float *part_s = reinterpret_cast<float *>(smem + a.stage_bytes);
+        if (ks > 0) {
+            float *dst = part_s + ((ks - 1) * kWaveSize + lane) * 4 * RT;
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dst[4 * t + r] = acc[t][r];
+        }
+        __syncthreads();
+        if (ks == 0)
+            for (uint32_t k = 1; k < KS; ++k) {
+                const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4 * RT;
+#pragma unroll
+                for (int t = 0; t < RT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[t][r] += src[4 * t + r];
+            }
+    }
+    // lane (g, m) holds rows 4g .. 4g+3 of each tile for token m: one
+    // 16-byte store where the rows are whole and the output row aligned
+    const uint32_t g = lane >> 4, m = lane & 15;
+    if (ks == 0 && m < a.ntok) {
         const float xs = a.scales[m];
+        const bool vec = (a.vec_out >> job) & 1u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float tot = ((acc[r] + part_s[0][lane][r]) + part_s[1][lane][r]) + part_s[2][lane][r];
-            const uint32_t no = row0 + 4 * g + r;
-            if (no < a.rows) a.output[static_cast<size_t>(m) * a.output_stride + no] = mul_rounded(tot, xs);
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t n0 = r0 + 16 * t + 4 * g;
+            float *dst = output + static_cast<size_t>(m) * stride + n0;
+            if (vec && n0 + 4 <= rows) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(mul_rounded(acc[t][0], xs), mul_rounded(acc[t][1], xs),
+                                                               mul_rounded(acc[t][2], xs), mul_rounded(acc[t][3], xs));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (n0 + r < rows) dst[r] = mul_rounded(acc[t][r], xs);
+            }
         }
     }
 }
@@ -1317,27 +1469,120 @@ hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t b
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
-                            uint32_t batch, uint32_t output_stride, hipStream_t stream) {
-    if (t.kind != kHvsq2 || batch == 0 || batch > static_cast<uint32_t>(kMfmaTokens) || !scales)
+namespace {
+
+// Launch shape of an MFMA GEMM over `total_rows` rows of K = units blocks:
+// a workgroup per 16-row group (one row tile per wave measured faster than
+// two or four sharing the image loads: more waves, shorter chains), its
+// waves splitting the K blocks -- the fewest that keep a wave's blocks
+// within the unrolled chunk of 5, then more (up to 8) while the launch has
+// fewer than 2048 waves and every wave keeps two blocks or more.  STAGE
+// where the row group is a whole number of wave tiles and they fit in LDS
+// (64 KB with the partial tiles).
+struct MfmaPlan {
+    int nbt = 0, rt = 1;
+    bool stage = false;
+    uint32_t ks_log2 = 0, nb = 0, waves = 0, stage_bytes = 0, lds_bytes = 0;
+};
+
+MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
+    MfmaPlan p;
+    const uint32_t units = t.units;
+    const uint64_t groups = (total_rows + 16 * p.rt - 1) / (16 * p.rt);
+    auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
+    while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
+    while (p.ks_log2 < 3 && (groups << p.ks_log2) < 2048 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+    p.nb = per_wave(p.ks_log2);
+    p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
+    p.waves = 1u << p.ks_log2;
+    const uint32_t part = (p.waves - 1) * kWaveSize * 4 * p.rt * 4;
+    const uint32_t rows_grp = 16u * p.rt;
+    const uint64_t stage = rows_grp % t.rows_per_wave == 0
+                               ? static_cast<uint64_t>(rows_grp / t.rows_per_wave) *
+                                     (t.tile_payload_bytes + t.tile_meta_bytes)
+                               : ~0ull;
+    p.stage = stage + part <= 65536;
+    p.stage_bytes = p.stage ? static_cast<uint32_t>(stage) : 0;
+    p.lds_bytes = p.stage_bytes + part;
+    return p;
+}
+
+template <int NB, int RT>
+hipError_t launch_mfma_rt(bool stage, uint32_t grid, uint32_t threads, size_t lds, const MfmaArgs &a,
+                          hipStream_t stream) {
+    if (stage)
+        hipLaunchKernelGGL((mfma_hvsq2_kernel<NB, RT, true>), dim3(grid), dim3(threads), lds, stream, a);
+    else
+        hipLaunchKernelGGL((mfma_hvsq2_kernel<NB, RT, false>), dim3(grid), dim3(threads), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int NB>
+hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, hipStream_t stream) {
+    return launch_mfma_rt<NB, 1>(p.stage, grid, p.waves * kWaveSize, p.lds_bytes, a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
+                                  const uint8_t *image, const float *scales, uint32_t batch,
+                                  const uint32_t *output_strides, hipStream_t stream) {
+    if (count == 0 || count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
+        batch > static_cast<uint32_t>(kMfmaTokens))
         return hipErrorInvalidValue;
+    const DeviceTensor &t0 = *tensors[0];
+    uint64_t total_rows = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const DeviceTensor &t = *tensors[i];
+        if (t.kind != kHvsq2 || t.cols != t0.cols || t.units != t0.units || t.lanes != t0.lanes ||
+            t.rows_per_wave != t0.rows_per_wave || t.tile_payload_bytes != t0.tile_payload_bytes ||
+            t.tile_meta_bytes != t0.tile_meta_bytes || !outputs[i])
+            return hipErrorInvalidValue;
+        total_rows += t.rows;
+    }
+    const MfmaPlan p = mfma_plan(t0, total_rows);
     MfmaArgs a{};
-    a.payload = t.payload;
-    a.meta = t.meta;
-    a.tile_payload_bytes = t.tile_payload_bytes;
-    a.tile_meta_bytes = t.tile_meta_bytes;
-    a.rows = t.rows;
-    a.units = t.units;
-    a.lanes = t.lanes;
-    a.rows_per_wave = t.rows_per_wave;
+    uint32_t grid = 0;
+    for (uint32_t i = 0; i < static_cast<uint32_t>(kMaxGroup); ++i) {
+        a.job_block[i] = grid;
+        if (i < count) {
+            const DeviceTensor &t = *tensors[i];
+            a.payload[i] = t.payload;
+            a.meta[i] = t.meta;
+            a.output[i] = outputs[i];
+            a.rows[i] = t.rows;
+            a.tiles[i] = t.tiles;
+            a.output_stride[i] = output_strides && output_strides[i] ? output_strides[i] : t.rows;
+            if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0)
+                a.vec_out |= 1u << i;
+            grid += (t.rows + 16 * p.rt - 1) / (16 * p.rt);
+        }
+    }
+    a.job_block[kMaxGroup] = grid;
+    a.tile_payload_bytes = t0.tile_payload_bytes;
+    a.tile_meta_bytes = t0.tile_meta_bytes;
+    a.units = t0.units;
+    a.lanes_log2 = static_cast<uint32_t>(__builtin_ctz(t0.lanes));
+    a.rows_per_wave_log2 = static_cast<uint32_t>(__builtin_ctz(t0.rows_per_wave));
+    a.ks_log2 = p.ks_log2;
+    a.nb = p.nb;
+    a.stage_bytes = p.stage_bytes;
     a.image = image;
     a.scales = scales;
-    a.output = output;
     a.ntok = batch;
-    a.output_stride = output_stride ? output_stride : t.rows;
-    const uint32_t grid = (t.rows + 15) / 16;
-    hipLaunchKernelGGL(mfma_hvsq2_kernel, dim3(grid), dim3(256), 0, stream, a);
-    return hipGetLastError();
+    switch (p.nbt) {
+    case 2: return launch_mfma_nb<2>(p, grid, a, stream);
+    case 3: return launch_mfma_nb<3>(p, grid, a, stream);
+    default: return launch_mfma_nb<5>(p, grid, a, stream);
+    }
+}
+
+hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
+                            uint32_t batch, uint32_t output_stride, hipStream_t stream) {
+    const DeviceTensor *ts[1] = {&t};
+    float *outs[1] = {output};
+    const uint32_t strides[1] = {output_stride};
+    return launch_gemm_mfma_group(ts, outs, 1, image, scales, batch, strides, stream);
 }
 
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,

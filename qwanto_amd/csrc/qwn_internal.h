@@ -183,6 +183,11 @@ hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t b
                              uint8_t *image, hipStream_t stream);
 hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
                             uint32_t batch, uint32_t output_stride, hipStream_t stream);
+// The same over up to kMaxGroup tensors of equal K sharing one image (one
+// launch); output_strides may be null (0 entries: each tensor's rows).
+hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
+                                  const uint8_t *image, const float *scales, uint32_t batch,
+                                  const uint32_t *output_strides, hipStream_t stream);
 constexpr uint32_t kMfmaMinTokens = 8;
 
 // RMSNorm of one fp32 token into the fp32 image of an F16 tensor.

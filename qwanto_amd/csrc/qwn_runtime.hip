@@ -1012,6 +1012,40 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *handle, 
     return QWN_CUDA_STATUS_OK;
 }
 
+QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *handle,
+                                                        const QwnCudaTensorHandle *tensors, uint32_t count,
+                                                        const void *image, const float *scales,
+                                                        float *const *outputs, uint32_t batch,
+                                                        uint32_t output_stride, void *stream) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !tensors || !outputs || !image || !scales || count == 0 || count > qwn::kMaxGroup || batch == 0 ||
+        batch > 16 || (reinterpret_cast<uintptr_t>(image) & 15u)) {
+        set_error("invalid MFMA group GEMM request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    const DeviceTensor *ts[qwn::kMaxGroup] = {};
+    uint32_t strides[qwn::kMaxGroup] = {};
+    for (uint32_t i = 0; i < count; ++i) {
+        ResidentTensor *rt = ext_tensor(ctx, &tensors[i]);
+        if (!rt || rt->t.kind != qwn::kHvsq2 || !outputs[i] || (output_stride && output_stride < rt->t.rows) ||
+            (i > 0 && rt->t.cols != ts[0]->cols)) {
+            set_error("MFMA group GEMM tensor %u does not fit (HyperVSQ-2, equal columns, output stride)", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+        ts[i] = &rt->t;
+        strides[i] = output_stride;
+    }
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+    hipError_t e = qwn::launch_gemm_mfma_group(ts, outputs, count, static_cast<const uint8_t *>(image), scales, batch,
+                                               strides, s);
+    if (e != hipSuccess) return hip_fail("MFMA group GEMM launch", e);
+    ctx->telemetry.gpu_matmul_count += count;
+    ctx->telemetry.gpu_kernel_launch_count++;
+    ctx->telemetry.gpu_projection_count += count;
+    return QWN_CUDA_STATUS_OK;
+}
+
 QWN_CUDA_ABI_API int qwn_hip_ext_quantize_device(QwnCudaContextHandle *handle, const float *x, uint32_t batch,
                                                  uint32_t cols, uint32_t x_stride, int8_t *q8,
                                                  uint32_t q8_stride, float *scales, void *stream) {

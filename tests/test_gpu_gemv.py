@@ -97,6 +97,43 @@ def test_q4_0_qwen2_1p5b_shapes(gpu_ctx, oracle_lib, N, K):
     check_q4_0(gpu_ctx, oracle_lib, N, K, seed=N * 7 + K)
 
 
+@pytest.mark.parametrize("Ns,K,M", [((4096, 1024, 1024), 2560, 16), ((9728, 9728), 2560, 16),
+                                    ((8200, 77), 777, 9), ((16390, 5), 520, 11), ((300,), 16384, 8),
+                                    ((2560,), 9728, 12)])
+def test_hvsq2_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
+    """qwn_hip_ext_gemm_mfma_group_device: one MFMA launch over tensors of
+    equal columns sharing one image (q/k/v and gate/up shapes, 32- and
+    64-row-group launches with ragged rows, unaligned row counts and partial
+    blocks, K beyond one chunk of blocks per wave), every token of every
+    tensor against the oracle."""
+    import torch
+    rng = np.random.default_rng(sum(Ns) + K + M)
+    ws = [synth.hvsq2_weights(rng, N, K) for N in Ns]
+    x = synth.activations(rng, M, K)
+    q8, xs, sums = oracle_lib.quantize(x)
+    hs = [gpu_ctx.upload(w, "hvsq2", N, K) for w, N in zip(ws, Ns)]
+    try:
+        dev = torch.device("cuda:0")
+        q8d = torch.from_numpy(q8).to(dev)
+        xsd = torch.from_numpy(xs).to(dev)
+        img = torch.zeros(gpu_ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
+        ys = [torch.full((M, N), float("nan"), dtype=torch.float32, device=dev) for N in Ns]
+        s = torch.cuda.current_stream().cuda_stream
+        gpu_ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
+        gpu_ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
+                                       stream=s)
+        torch.cuda.synchronize()
+        for w, N, y in zip(ws, Ns, ys):
+            yh = y.cpu().numpy()
+            for t in range(M):
+                ref = oracle_lib.gemv_hvsq2(w, q8[t], sums[t], float(xs[t]), K, N)
+                ok, worst = gemv_close(yh[t], ref)
+                assert ok, f"tensor {N}x{K} token {t}: worst {worst:.3g}"
+    finally:
+        for h in hs:
+            gpu_ctx.release(h)
+
+
 @pytest.mark.parametrize("N,K", [(1, 1), (3, 31), (5, 32), (7, 100), (65, 129), (130, 520),
                                  (64, 4064), (2, 16384)])
 def test_q4_0_edge_shapes(gpu_ctx, oracle_lib, N, K):
