@@ -63,7 +63,7 @@ typedef struct {
     double decode_ms;             /* wall clock, generated steps */
     uint64_t weight_bytes_per_step; /* algorithmic weight bytes one step reads */
     uint32_t graph;               /* 1 if steps replay a captured HIP graph */
-    uint32_t reserved;
+    uint32_t prefill_block_tokens; /* prompt tokens per prefill block */
 } QwnHipDecoderStats;
 
 QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *context, const QwnHipDecoderDesc *desc,
@@ -75,9 +75,20 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_reset(QwnCudaContextHandle *context, QwnHip
  * (vocab floats) and `next_token` (the greedy choice) may be NULL. */
 QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
                                              int32_t token, float *logits, int32_t *next_token);
-/* Greedy generation as c/qwanto_decode.c:2085-2125: one step per prompt
- * token, then max_new times: tokens[s] = argmax of the last logits, one
- * step on it.  Synchronises once after the prompt and once at the end. */
+/* `count` prompt tokens at the current position in prefill blocks of up to
+ * 16 tokens: each projection of a block is one batched GEMV (the weights
+ * are read once per block instead of once per token), then RoPE, the Q8
+ * append and causal attention per token.  Same cache contents and, up to
+ * the fp32 summation order of the norms, the same logits as `count`
+ * forward() calls (c/qwanto_decode.c:2093 steps the prompt token by token).
+ * `logits` / `next_token`: those of the last token (may be NULL). */
+QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                             const int32_t *tokens, uint32_t count, float *logits,
+                                             int32_t *next_token);
+/* Greedy generation as c/qwanto_decode.c:2085-2125: the prompt (in prefill
+ * blocks, as qwn_hip_decoder_prefill), then max_new times: tokens[s] =
+ * argmax of the last logits, one step on it.  Synchronises once after the
+ * prompt and once at the end. */
 QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
                                               const int32_t *prompt, uint32_t prompt_count, uint32_t max_new,
                                               int32_t *tokens, QwnHipDecoderStats *stats);

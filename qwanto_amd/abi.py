@@ -58,7 +58,7 @@ EXT_EXPORTS = (
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
-    "qwn_hip_decoder_forward", "qwn_hip_decoder_generate",
+    "qwn_hip_decoder_forward", "qwn_hip_decoder_generate", "qwn_hip_decoder_prefill",
 )
 
 GEMV_INPUT = {"image": 0, "f32": 1, "rmsnorm": 2, "swiglu": 3}
@@ -189,7 +189,7 @@ class DecoderStats(_Versioned):
                 ("generated_tokens", ctypes.c_uint32), ("position", ctypes.c_uint32),
                 ("launches_per_step", ctypes.c_uint32), ("prefill_ms", ctypes.c_double),
                 ("decode_ms", ctypes.c_double), ("weight_bytes_per_step", ctypes.c_uint64),
-                ("graph", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("graph", ctypes.c_uint32), ("prefill_block_tokens", ctypes.c_uint32)]
 
 
 STRUCTS = {
@@ -286,6 +286,7 @@ class Library:
         lib.qwn_hip_decoder_reset.argtypes = [P(Handle), P(Handle)]
         lib.qwn_hip_decoder_forward.argtypes = [P(Handle), P(Handle), ctypes.c_int32, V, V]
         lib.qwn_hip_decoder_generate.argtypes = [P(Handle), P(Handle), V, U32, U32, V, P(DecoderStats)]
+        lib.qwn_hip_decoder_prefill.argtypes = [P(Handle), P(Handle), V, U32, V, V]
 
     def last_error(self) -> str:
         buf = ctypes.create_string_buffer(512)
@@ -576,6 +577,16 @@ class ResidentDecoder:
         nxt = ctypes.c_int32(0)
         self.ctx.lib.check("decoder_forward", self.ctx.lib.lib.qwn_hip_decoder_forward(
             self.ctx._h, ctypes.byref(self.handle), int(token), _p(out), ctypes.addressof(nxt)))
+        return out, nxt.value
+
+    def prefill(self, tokens, logits: bool = True):
+        """Prompt tokens in prefill blocks; returns (last logits or None,
+        greedy next token)."""
+        tk = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(self.cfg["vocab"], dtype=np.float32) if logits else None
+        nxt = ctypes.c_int32(0)
+        self.ctx.lib.check("decoder_prefill", self.ctx.lib.lib.qwn_hip_decoder_prefill(
+            self.ctx._h, ctypes.byref(self.handle), _p(tk), tk.size, _p(out), ctypes.addressof(nxt)))
         return out, nxt.value
 
     def generate(self, prompt, max_new: int):

@@ -333,15 +333,21 @@ namespace {
 // (c/qwanto_decode.c:686-729):
 //   r[i] = fma(a, cos_i, -(b * sin_i)),  r[i + half] = fma(a, sin_i, b * cos_i)
 // with a = x[i], b = x[i + half] and the cos/sin table row of the position;
-// the append quantizes per 64-channel group as kv_append_kernel.
+// the append quantizes per 64-channel group as kv_append_kernel.  grid (n):
+// workgroup i takes token i of a block -- q + i*q_stride, k/v + i*kv_stride,
+// position pos_ptr[i].
 __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__restrict__ q, uint32_t q_heads,
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
                                                            const float *__restrict__ cos_tab,
                                                            const float *__restrict__ sin_tab,
-                                                           const int32_t *__restrict__ pos_ptr) {
+                                                           const int32_t *__restrict__ pos_ptr, uint32_t q_stride,
+                                                           uint32_t kv_stride) {
     extern __shared__ float kr[];  // [channels] rotated key
-    const uint32_t pos = static_cast<uint32_t>(*pos_ptr);
+    q += static_cast<size_t>(blockIdx.x) * q_stride;
+    k += static_cast<size_t>(blockIdx.x) * kv_stride;
+    v += static_cast<size_t>(blockIdx.x) * kv_stride;
+    const uint32_t pos = static_cast<uint32_t>(pos_ptr[blockIdx.x]);
     const uint32_t D = c.head_dim, half = D / 2;
     const uint32_t row = pos < c.max_tokens ? pos : 0;
     const float *ct = cos_tab + static_cast<size_t>(row) * half;
@@ -423,6 +429,8 @@ struct DecodeAttnArgs {
     const float *cos_tab;    // [max_tokens][D/2], or [D/2] for the current position (rope_row_only)
     const float *sin_tab;
     uint32_t rope_row_only;
+    uint32_t token_stride;   // floats between the query (and output) rows of a token block
+    uint32_t count;          // query tokens (grid z)
 };
 
 __device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *ct, const float *st) {
@@ -489,7 +497,11 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
         }
     };
-    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) : a.position;
+    // grid z: the query token of a block (token_stride floats apart, its
+    // position position_ptr[z]); one split only
+    const float *query = a.query + static_cast<size_t>(blockIdx.z) * a.token_stride;
+    float *out = a.output + static_cast<size_t>(blockIdx.z) * a.token_stride;
+    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(a.position_ptr[blockIdx.z]) : a.position;
     if (pos >= c.max_tokens) return;
     const uint32_t tokens = pos + 1;
     if (t0 >= tokens) {
@@ -518,7 +530,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
         const uint32_t g = i / D, d = i % D;
         float v = 0.0f;
         if (g < G) {
-            const float *qh = a.query + static_cast<size_t>(h0 + g) * D;
+            const float *qh = query + static_cast<size_t>(h0 + g) * D;
             v = rope ? rope_at(qh, d, half, ct, st) : qh[d];
         }
         q_s[i] = v;
@@ -685,7 +697,7 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
         for (int p = 0; p < PH; ++p) o += pv_s[(p * GMAX + g) * D + d];
         const uint32_t head = h0 + g;
         if (a.nsplit == 1) {
-            a.output[static_cast<size_t>(head) * D + d] = o / l_run[g];
+            out[static_cast<size_t>(head) * D + d] = o / l_run[g];
         } else {
             float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
             dst[2 + d] = o;
@@ -1109,8 +1121,9 @@ hipError_t launch_mfma_attention_rt(const MfmaAttnArgs &args, hipStream_t stream
 template <int D, int GMAX>
 hipError_t launch_decode_kernel(const DecodeAttnArgs &args, hipStream_t stream) {
     const uint32_t wgs_per_kv = args.group / args.heads_per_wg;
-    hipLaunchKernelGGL((decode_attention_kernel<D, GMAX>), dim3(args.nsplit, args.c.kv_heads * wgs_per_kv),
-                       dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((decode_attention_kernel<D, GMAX>),
+                       dim3(args.nsplit, args.c.kv_heads * wgs_per_kv, std::max(args.count, 1u)), dim3(256), 0,
+                       stream, args);
     return hipGetLastError();
 }
 
@@ -1158,10 +1171,10 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base) {
 
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
-                              const int32_t *pos_ptr, hipStream_t stream) {
-    if (c.head_dim % 2 || c.channels > 8192) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_append_kernel, dim3(1), dim3(1024), c.channels * sizeof(float), stream, c, query,
-                       query_heads, key, value, cos_tab, sin_tab, pos_ptr);
+                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count) {
+    if (c.head_dim % 2 || c.channels > 8192 || count == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_append_kernel, dim3(count), dim3(1024), c.channels * sizeof(float), stream, c, query,
+                       query_heads, key, value, cos_tab, sin_tab, pos_ptr, query_heads * c.head_dim, c.channels);
     return hipGetLastError();
 }
 
@@ -1248,7 +1261,8 @@ hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *ou
 hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t stream) {
     const KvCache &c = *l.cache;
     if (!decode_attention_supported(c, l.query_heads) || (l.key && (c.head_dim % 64 || !l.value || !l.cos_tab ||
-                                                                    !l.sin_tab)))
+                                                                    !l.sin_tab)) ||
+        l.count == 0 || (l.count > 1 && (l.key || !l.position_ptr)))
         return hipErrorInvalidValue;
     DecodeAttnArgs args{};
     args.c = c;
@@ -1271,6 +1285,8 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.cos_tab = l.cos_tab;
     args.sin_tab = l.sin_tab;
     args.rope_row_only = l.rope_row_only ? 1u : 0u;
+    args.count = l.count;
+    args.token_stride = l.query_heads * c.head_dim;
     return launch_decode_attention_args(args, l.output, stream);
 }
 

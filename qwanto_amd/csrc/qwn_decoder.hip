@@ -35,6 +35,7 @@ namespace qwn {
 namespace {
 
 constexpr int kProj = 7;
+constexpr uint32_t kPrefillTokens = 16;  // prompt tokens per prefill block (the GEMV's widest launch)
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN };
 
 // x = embedding row of the step's token (feed[pos] when the host supplied
@@ -76,6 +77,37 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
         if (k0 + e < a.hidden) a.x[k0 + e] = half_to_float((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+}
+
+// Prefill block: x[i] = embedding row of feed[p0 + i] for the block's
+// tokens i < count (p0 = the device position), and the positions p0 + i
+// recorded for the block's kernels.  grid (ceil(units*4 / 256), count).
+__global__ __launch_bounds__(256) void prefill_embed_kernel(EmbedArgs a, uint32_t count, float *x,
+                                                            int32_t *positions) {
+    const uint32_t i = blockIdx.y;
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t pos = a.state[1] + static_cast<int32_t>(i);
+    if (idx == 0) positions[i] = pos;
+    if (idx >= a.units * 4) return;
+    int32_t token = (pos >= 0 && static_cast<uint32_t>(pos) < a.max_ctx) ? a.feed[pos] : -1;
+    if (token < 0 || static_cast<uint32_t>(token) >= a.vocab) token = 0;
+    const uint32_t u = idx / 4, q = idx % 4;
+    const UnitAddr ad = unit_addr(static_cast<uint32_t>(token), u, q, a.lanes, a.rows_per_wave, a.units,
+                                  a.tile_payload, 0);
+    const uint4 h = *reinterpret_cast<const uint4 *>(a.payload + ad.payload);
+    const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t k0 = u * 32 + q * 8;
+    float *xi = x + static_cast<size_t>(i) * a.hidden;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (k0 + e < a.hidden) xi[k0 + e] = half_to_float((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+}
+
+// End of a prefill block: the device position moves past the block, or, in
+// the block that ends the prompt, to its last token, which the greedy step
+// end then records and passes.
+__global__ void prefill_advance_kernel(int32_t *state, const int32_t *positions, uint32_t count, uint32_t last) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) state[1] = positions[count - 1] + (last ? 0 : 1);
 }
 
 // Greedy token of the step (largest logit, first index on ties), recorded
@@ -124,6 +156,16 @@ struct Decoder {
     std::vector<KvCache> caches;
     hipGraphExec_t exec = nullptr;
     bool graph_tried = false;
+    // prefill: blocks of up to kPrefillTokens prompt tokens through the
+    // batched GEMV ([token][...] buffers), one graph per (block size, ends
+    // the prompt)
+    float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pattn = nullptr, *pgate = nullptr,
+          *pup = nullptr, *pscales = nullptr;
+    uint8_t *pimg = nullptr;
+    uint32_t pimg_stride = 0;
+    int32_t *ppos = nullptr;
+    hipGraphExec_t prefill_exec[kPrefillTokens + 1][2] = {};
+    bool prefill_tried[kPrefillTokens + 1][2] = {};
     uint32_t position = 0;
     uint32_t launches = 0;
     uint32_t layer_launches = 0;  // kernels per layer
@@ -134,6 +176,9 @@ struct Decoder {
 void destroy_decoder(Decoder *d) {
     if (!d) return;
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    for (auto &row : d->prefill_exec)
+        for (hipGraphExec_t x : row)
+            if (x) (void)hipGraphExecDestroy(x);
     if (d->allocation) (void)hipFree(d->allocation);
     delete d;
 }
@@ -154,10 +199,7 @@ GemvGroupLaunch group(std::initializer_list<const DeviceTensor *> ts, std::initi
     return g;
 }
 
-// The launches of one step, in order; `count` only counts them.
-hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
-    uint32_t n = 0;
-    hipError_t e;
+EmbedArgs embed_args(const Decoder *d) {
     EmbedArgs ea{};
     ea.payload = d->embed->payload;
     ea.tile_payload = d->embed->tile_payload_bytes;
@@ -174,6 +216,101 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
     ea.sin_tab = d->sin_tab;
     ea.half = d->head_dim / 2;
     ea.rope_row = d->rope_row;
+    return ea;
+}
+
+// The LM head on the fp32 residual x: final RMSNorm into the F16 image,
+// the image-mode GEMV with per-workgroup argmax partials (fewer registers
+// than the fused prologue: more waves per CU in flight), and the step end
+// that records the greedy token at the device position and advances it.
+hipError_t enqueue_head(Decoder *d, const float *x, hipStream_t s) {
+    hipError_t e;
+    if ((e = launch_norm_image(*d->embed, x, d->final_norm, d->eps, d->head_image, s)) != hipSuccess) return e;
+    GemvGroupLaunch head = group({d->embed}, {d->logits});
+    head.image = d->head_image;
+    head.image_stride = static_cast<uint32_t>(image_bytes(kF16, d->embed->units));
+    head.output_mode = kOutArgmax;
+    head.argmax_partials = d->argmax;
+    if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, s, d->argmax, d->argmax_n, d->state,
+                       d->out_tokens, d->max_ctx);
+    return hipGetLastError();
+}
+
+// One prefill block of `m` prompt tokens at the device position (their ids
+// in feed): per layer the projections of all m tokens in one batched GEMV
+// each (weights read once per launch), RoPE and the Q8 append of the m
+// keys/values, causal attention of every token over the cache up to its
+// own position, residual adds in the GEMV epilogues.  `last`: the block
+// ends the prompt, so the LM head runs on its last token and the greedy
+// token is recorded as a decode step would.
+hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
+    hipError_t e;
+    const EmbedArgs ea = embed_args(d);
+    hipLaunchKernelGGL(prefill_embed_kernel, dim3((ea.units * 4 + 255) / 256, m), dim3(256), 0, s, ea, m, d->px,
+                       d->ppos);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const uint32_t D = d->hidden, Q = d->heads * d->head_dim, I = d->inter;
+    auto batched = [&](GemvGroupLaunch g, uint32_t mode) {
+        g.input_mode = kInImage;
+        g.output_mode = mode;
+        g.image = d->pimg;
+        g.image_stride = d->pimg_stride;
+        g.scales = d->pscales;
+        g.batch = m;
+        return launch_gemv_group(g, s);
+    };
+    for (uint32_t l = 0; l < d->layers; ++l) {
+        const DeviceTensor *const *w = d->proj.data() + static_cast<size_t>(l) * kProj;
+        const float *nin = d->norms_in + static_cast<size_t>(l) * D;
+        const float *npost = d->norms_post + static_cast<size_t>(l) * D;
+        if ((e = launch_prepare_image(*w[P_Q], kInNorm, d->px, nullptr, nin, d->eps, m, D, d->pimg, d->pimg_stride,
+                                      d->pscales, nullptr, 0, s)) != hipSuccess ||
+            (e = batched(group({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}), kOutStore)) != hipSuccess ||
+            (e = launch_rope_append(d->caches[l], d->pq, d->heads, d->pk, d->pv, d->cos_tab, d->sin_tab, d->ppos, s,
+                                    m)) != hipSuccess)
+            return e;
+        if (d->fused_attention) {
+            DecodeAttentionLaunch at;
+            at.cache = &d->caches[l];
+            at.query = d->pq;
+            at.output = d->pattn;
+            at.partials = d->partials;
+            at.query_heads = d->heads;
+            at.position_ptr = d->ppos;
+            at.span_tokens = d->max_ctx;
+            at.scale = d->attn_scale;
+            at.count = m;
+            if ((e = launch_decode_attention(at, s)) != hipSuccess) return e;
+        } else {
+            for (uint32_t i = 0; i < m; ++i)
+                if ((e = launch_attention_at(d->caches[l], d->pq + static_cast<size_t>(i) * Q,
+                                             d->pattn + static_cast<size_t>(i) * Q, d->heads, d->ppos + i,
+                                             d->attn_scale, d->partials, s)) != hipSuccess)
+                    return e;
+        }
+        if ((e = launch_prepare_image(*w[P_O], kInF32, d->pattn, nullptr, nullptr, 0.0f, m, Q, d->pimg,
+                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
+            (e = batched(group({w[P_O]}, {d->px}), kOutAdd)) != hipSuccess ||
+            (e = launch_prepare_image(*w[P_GATE], kInNorm, d->px, nullptr, npost, d->eps, m, D, d->pimg,
+                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
+            (e = batched(group({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}), kOutStore)) != hipSuccess ||
+            (e = launch_prepare_image(*w[P_DOWN], kInSwiglu, d->pgate, d->pup, nullptr, 0.0f, m, I, d->pimg,
+                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
+            (e = batched(group({w[P_DOWN]}, {d->px}), kOutAdd)) != hipSuccess)
+            return e;
+    }
+    hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(64), 0, s, d->state, d->ppos, m, last ? 1u : 0u);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (last) return enqueue_head(d, d->px + static_cast<size_t>(m - 1) * D, s);
+    return hipSuccess;
+}
+
+// The launches of one step, in order; `count` only counts them.
+hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
+    uint32_t n = 0;
+    hipError_t e;
+    const EmbedArgs ea = embed_args(d);
     hipLaunchKernelGGL(embed_kernel, dim3((std::max(ea.units * 4, 2 * ea.half) + 255) / 256), dim3(256), 0, s, ea);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     ++n;
@@ -231,20 +368,46 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         if ((e = launch_gemv_group(down, s)) != hipSuccess) return e;
         n += d->layer_launches;
     }
-    // LM head: final RMSNorm into the F16 image, then the image-mode GEMV
-    // (fewer registers than the fused prologue: more waves per CU in flight)
-    if ((e = launch_norm_image(*d->embed, d->x, d->final_norm, d->eps, d->head_image, s)) != hipSuccess) return e;
-    GemvGroupLaunch head = group({d->embed}, {d->logits});
-    head.image = d->head_image;
-    head.image_stride = static_cast<uint32_t>(image_bytes(kF16, d->embed->units));
-    head.output_mode = kOutArgmax;
-    head.argmax_partials = d->argmax;
-    if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, s, d->argmax, d->argmax_n, d->state,
-                       d->out_tokens, d->max_ctx);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = enqueue_head(d, d->x, s)) != hipSuccess) return e;
     n += 3;
     if (count) *count = n;
+    return hipSuccess;
+}
+
+// Captures `enqueue` once into *exec (left null when capture fails, so the
+// caller launches the kernels directly) and launches it.
+template <typename F>
+hipError_t run_captured(hipStream_t s, hipGraphExec_t *exec, bool *tried, F enqueue) {
+    if (!*tried) {
+        *tried = true;
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            const hipError_t le = enqueue();
+            e = hipStreamEndCapture(s, &g);
+            if (le != hipSuccess) e = le;
+        }
+        if (e == hipSuccess && g) e = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+        if (g) (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            *exec = nullptr;
+            (void)hipGetLastError();
+        }
+    }
+    if (*exec) return hipGraphLaunch(*exec, s);
+    return enqueue();
+}
+
+// The prompt, already in feed at the device position, in prefill blocks.
+hipError_t run_prefill(Decoder *d, uint32_t count) {
+    hipStream_t s = d->ctx->stream;
+    for (uint32_t i = 0; i < count; i += kPrefillTokens) {
+        const uint32_t m = std::min(kPrefillTokens, count - i);
+        const bool last = i + m == count;
+        const hipError_t e = run_captured(s, &d->prefill_exec[m][last], &d->prefill_tried[m][last],
+                                          [&] { return enqueue_prefill(d, m, last, s); });
+        if (e != hipSuccess) return e;
+    }
     return hipSuccess;
 }
 
@@ -356,6 +519,23 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     part(reinterpret_cast<void **>(&d->state), 2 * 4);
     part(reinterpret_cast<void **>(&d->feed), static_cast<size_t>(d->max_ctx) * 4);
     part(reinterpret_cast<void **>(&d->out_tokens), static_cast<size_t>(d->max_ctx) * 4);
+    // prefill blocks: [token][...] activations, images of the widest input
+    {
+        const size_t P = kPrefillTokens;
+        part(reinterpret_cast<void **>(&d->px), P * D * 4);
+        part(reinterpret_cast<void **>(&d->pq), P * Q * 4);
+        part(reinterpret_cast<void **>(&d->pk), P * KV * 4);
+        part(reinterpret_cast<void **>(&d->pv), P * KV * 4);
+        part(reinterpret_cast<void **>(&d->pattn), P * Q * 4);
+        part(reinterpret_cast<void **>(&d->pgate), P * I * 4);
+        part(reinterpret_cast<void **>(&d->pup), P * I * 4);
+        part(reinterpret_cast<void **>(&d->pscales), P * 4);
+        part(reinterpret_cast<void **>(&d->ppos), P * 4);
+        size_t stride = 0;
+        for (int p : {P_Q, P_O, P_DOWN}) stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
+        d->pimg_stride = static_cast<uint32_t>((stride + 15) & ~static_cast<size_t>(15));
+        part(reinterpret_cast<void **>(&d->pimg), P * d->pimg_stride);
+    }
     // attention partials of the device-position kernels
     KvCache proto;
     proto.max_tokens = d->max_ctx;
@@ -545,6 +725,43 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *handle, QwnHi
     return QWN_CUDA_STATUS_OK;
 }
 
+QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                             const int32_t *tokens, uint32_t count, float *logits,
+                                             int32_t *next_token) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !tokens || count == 0) {
+        set_error("invalid prefill request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || static_cast<uint64_t>(d->position) + count > d->max_ctx) {
+        set_error("prefill does not fit the decoder's context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < count; ++i)
+        if (tokens[i] < 0 || static_cast<uint32_t>(tokens[i]) >= d->vocab) {
+            set_error("prefill token %u out of range", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+    hipStream_t s = ctx->stream;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->feed + d->position, tokens, static_cast<size_t>(count) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = run_prefill(d, count);
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, d->logits, static_cast<size_t>(d->vocab) * 4, hipMemcpyDeviceToHost, s);
+    int32_t st[2] = {0, 0};
+    if (e == hipSuccess) e = hipMemcpyAsync(st, d->state, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail("decoder prefill", e);
+    d->position += count;
+    if (next_token) *next_token = st[0];
+    const uint64_t blocks = (count + kPrefillTokens - 1) / kPrefillTokens;
+    ctx->telemetry.gpu_matmul_count += blocks * 4ull * d->layers + 1;
+    return QWN_CUDA_STATUS_OK;
+}
+
 QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
                                               const int32_t *prompt, uint32_t prompt_count, uint32_t max_new,
                                               int32_t *tokens, QwnHipDecoderStats *stats) {
@@ -572,7 +789,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnH
     if (e == hipSuccess) e = hipMemcpyAsync(d->feed + p0, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     const auto t0 = std::chrono::steady_clock::now();
-    for (uint32_t i = 0; e == hipSuccess && i < prompt_count; ++i) e = run_step(d);
+    if (e == hipSuccess) e = run_prefill(d, prompt_count);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     const auto t1 = std::chrono::steady_clock::now();
     for (uint32_t i = 0; e == hipSuccess && i < max_new; ++i) e = run_step(d);
@@ -597,6 +814,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnH
         stats->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
         stats->weight_bytes_per_step = d->weight_bytes;
         stats->graph = d->exec ? 1u : 0u;
+        stats->prefill_block_tokens = kPrefillTokens;
     }
     return QWN_CUDA_STATUS_OK;
 }

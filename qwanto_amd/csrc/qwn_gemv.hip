@@ -131,49 +131,94 @@ __global__ __launch_bounds__(1024) void norm_image_kernel(const float *__restric
     }
 }
 
+// Elements per image sub-block written by one lane (a quarter or half of a
+// 32-block: the per-32 sums are combined across adjacent lanes).
+__host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHvsq2 ? 16 : 8; }
+
 // Per-token int8 quantization (c/qwanto_kernels.c:354-433) fused with the
 // image: x fp32 [M][x_stride] -> scales [M], image [M][image_stride] and,
-// when q8 is given, the int8 token [M][q8_stride] zero padded.  grid (M).
+// when q8 is given, the int8 token [M][q8_stride] zero padded.  grid (M),
+// one workgroup per token.  The quantized value is the input (kInF32), its
+// RMSNorm with weights `norm` (kInNorm, c/qwanto_decode.c:627-652) or
+// silu(x) * x2 (kInSwiglu, c/qwanto_decode.c:1946-1949): the arithmetic of
+// the fused one-token GEMV prologue for a block of tokens.  The values are
+// staged in LDS (dynamic, K floats) with coalesced loads where they fit
+// (`staged`), else recomputed from global memory; the image is written in
+// E-element sub-blocks by adjacent lanes, as the prologue does.
 template <int KIND>
-__global__ __launch_bounds__(256) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
-                                                             uint32_t x_stride, uint32_t units, uint8_t *image,
-                                                             uint32_t image_stride, float *scales, int8_t *q8,
-                                                             uint32_t q8_stride) {
-    __shared__ float wave_max[256 / kWaveSize];
-    const uint32_t t = blockIdx.x;
+__global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
+                                                              uint32_t x_stride, uint32_t units, uint8_t *image,
+                                                              uint32_t image_stride, float *scales, int8_t *q8,
+                                                              uint32_t q8_stride, uint32_t mode,
+                                                              const float *__restrict__ x2,
+                                                              const float *__restrict__ norm, float eps,
+                                                              uint32_t staged) {
+    extern __shared__ float vals[];  // [K] when staged
+    __shared__ float wave_red[1024 / kWaveSize];
+    constexpr uint32_t E = fused_sub_elems(KIND);
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const uint32_t W = blockDim.x / kWaveSize;
     const float *row = x + static_cast<size_t>(t) * x_stride;
+    float inv_rms = 1.0f;
+    if (mode == kInNorm) {
+        float ss = 0.0f;
+        for (uint32_t k = tid; k < K; k += blockDim.x) ss = fmaf(row[k], row[k], ss);
+        ss = wave_sum_all(ss);
+        if (tid % kWaveSize == 0) wave_red[tid / kWaveSize] = ss;
+        __syncthreads();
+        float tot = wave_red[0];
+        for (uint32_t w = 1; w < W; ++w) tot += wave_red[w];
+        inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+        __syncthreads();
+    }
+    auto value = [&](uint32_t k) {
+        const float v = row[k];
+        if (mode == kInNorm) return (v * inv_rms) * norm[k];
+        if (mode == kInSwiglu) return (v / (1.0f + expf(-v))) * x2[static_cast<size_t>(t) * x_stride + k];
+        return v;
+    };
     float amax = 0.0f;
-    for (uint32_t k = threadIdx.x; k < K; k += blockDim.x) amax = fmaxf(amax, fabsf(row[k]));
-    for (int off = kWaveSize / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    if (threadIdx.x % kWaveSize == 0) wave_max[threadIdx.x / kWaveSize] = amax;
+    for (uint32_t k = tid; k < K; k += blockDim.x) {
+        const float v = value(k);
+        if (staged) vals[k] = v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+    amax = wave_max_all(amax);
+    if (tid % kWaveSize == 0) wave_red[tid / kWaveSize] = amax;
     __syncthreads();
-    amax = wave_max[0];
-    for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) amax = fmaxf(amax, wave_max[w]);
+    amax = wave_red[0];
+    for (uint32_t w = 1; w < W; ++w) amax = fmaxf(amax, wave_red[w]);
     // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / scale;
-    if (threadIdx.x == 0) scales[t] = scale;
-    const uint32_t nblk = units * unit_elems(KIND) / 32;
+    if (tid == 0) scales[t] = scale;
+    const uint32_t nsub = units * unit_elems(KIND) / E;
     uint8_t *img = image ? image + static_cast<size_t>(t) * image_stride : nullptr;
-    for (uint32_t b = threadIdx.x; b < nblk; b += blockDim.x) {
-        uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (uint32_t i = 0; i < 32; ++i) {
-            const uint32_t k = b * 32 + i;
-            if (k >= K) break;
-            const float v = fminf(127.0f, fmaxf(-127.0f, row[k] * inv));
-            const uint32_t q = static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(v)));
-            w[i >> 2] |= q << (8 * (i & 3));
+    int8_t *q8row = q8 ? q8 + static_cast<size_t>(t) * q8_stride : nullptr;
+    // every lane runs the sub-block step (its cross-lane sums), those past
+    // the image write nothing
+    for (uint32_t base = 0; base < nsub; base += blockDim.x) {
+        const uint32_t sb = base + tid;
+        uint32_t w[E / 4];
+#pragma unroll
+        for (uint32_t i = 0; i < E / 4; ++i) w[i] = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < E; ++i) {
+            const uint32_t k = sb * E + i;
+            if (sb < nsub && k < K) {
+                const float c = fminf(127.0f, fmaxf(-127.0f, (staged ? vals[k] : value(k)) * inv));
+                w[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(c))))
+                             << (8 * (i & 3));
+            }
         }
-        if (image) put_block32<KIND>(img, units, b, w);
-        if (q8) {
-            int8_t *dst = q8 + static_cast<size_t>(t) * q8_stride;
-            for (uint32_t i = 0; i < 32 && b * 32 + i < q8_stride; ++i)
-                dst[b * 32 + i] = static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
-        }
+        if (img) put_sub_block<KIND>(img, units, sb, nsub, w);
+        if (q8row && sb < nsub)
+#pragma unroll
+            for (uint32_t i = 0; i < E; ++i)
+                if (sb * E + i < q8_stride) q8row[sb * E + i] = static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
     }
-    if (q8)
-        for (uint32_t k = nblk * 32 + threadIdx.x; k < q8_stride; k += blockDim.x)
-            q8[static_cast<size_t>(t) * q8_stride + k] = 0;
+    if (q8row)
+        for (uint32_t k = nsub * E + tid; k < q8_stride; k += blockDim.x) q8row[k] = 0;
 }
 
 // Copy `ntok` token images (global stride `stride`, `bytes` each, a
@@ -333,7 +378,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
 // (UPL <= 4), else kGemvWaves.
 __host__ __device__ constexpr int max_waves_for(int upl) { return upl <= 4 ? kGemvMaxWaves : kGemvWaves; }
 
-__host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHvsq2 ? 16 : 8; }
 
 template <int KIND, int MT, int UPL, int FR>
 __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(GemvArgs a) {
@@ -679,7 +723,8 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             // projection before vec_add(x, y) (c/qwanto_decode.c:1925, 1955), so no
             // contraction into one fused multiply-add here
             if (KIND != kF16) s = mul_rounded(s, tok_scale[t]);
-            if (MT == 1 && a.output_mode == kOutAdd) s = add_rounded(resid, s);
+            if (a.output_mode == kOutAdd)
+                s = add_rounded(t == 0 ? resid : output[static_cast<size_t>(t) * out_stride + row], s);
             if (t == 0) first_out = s;
             output[static_cast<size_t>(t) * out_stride + row] = s;
         }
@@ -1303,12 +1348,25 @@ hipError_t launch_image(const DeviceTensor &t, const void *x, uint32_t batch, ui
 hipError_t launch_quantize_image(const DeviceTensor &t, const float *x, uint32_t batch, uint32_t x_stride,
                                  uint8_t *image, uint32_t image_stride, float *scales, int8_t *q8,
                                  uint32_t q8_stride, hipStream_t stream) {
+    return launch_prepare_image(t, kInF32, x, nullptr, nullptr, 0.0f, batch, x_stride, image, image_stride, scales,
+                                q8, q8_stride, stream);
+}
+
+hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const float *x, const float *x2,
+                                const float *norm, float eps, uint32_t batch, uint32_t x_stride, uint8_t *image,
+                                uint32_t image_stride, float *scales, int8_t *q8, uint32_t q8_stride,
+                                hipStream_t stream) {
+    if (batch == 0 || mode > kInSwiglu || mode == kInImage || (mode == kInNorm && !norm) ||
+        (mode == kInSwiglu && !x2))
+        return hipErrorInvalidValue;
+    const uint32_t staged = static_cast<size_t>(t.cols) * sizeof(float) <= kGemvLdsLimit ? 1u : 0u;
+    const size_t lds = staged ? static_cast<size_t>(t.cols) * sizeof(float) : 0;
     if (t.kind == kHvsq2)
-        hipLaunchKernelGGL(quantize_image_kernel<kHvsq2>, dim3(batch), dim3(256), 0, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride);
+        hipLaunchKernelGGL(quantize_image_kernel<kHvsq2>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
+                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged);
     else if (t.kind == kQ4_0)
-        hipLaunchKernelGGL(quantize_image_kernel<kQ4_0>, dim3(batch), dim3(256), 0, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride);
+        hipLaunchKernelGGL(quantize_image_kernel<kQ4_0>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
+                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1384,7 +1442,6 @@ bool group_valid(const GemvGroupLaunch &g) {
     if (g.output_mode == kOutSwiglu &&
         (g.batch != 1 || g.njobs != 2 || g.tensors[0]->rows != g.tensors[1]->rows))
         return false;
-    if (g.output_mode == kOutAdd && g.batch != 1) return false;
     return true;
 }
 

@@ -174,6 +174,13 @@ struct GemvGroupLaunch {
 // Workgroups a grouped launch uses (the argmax partial count).
 uint32_t gemv_group_grid(const GemvGroupLaunch &g);
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream);
+// Images of a block of fp32 tokens after the input transform of `mode`
+// (kInF32, kInNorm with `norm` and eps, kInSwiglu with x2 at the same
+// stride), quantized per token as launch_quantize_image.
+hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const float *x, const float *x2,
+                                const float *norm, float eps, uint32_t batch, uint32_t x_stride, uint8_t *image,
+                                uint32_t image_stride, float *scales, int8_t *q8, uint32_t q8_stride,
+                                hipStream_t stream);
 // int8 MFMA batch GEMM of a HyperVSQ-2 tensor for 1..16 tokens (used from 8
 // tokens up): the activation layout its tiles read (the "MFMA image"), built
 // from int8 tokens [batch][q8_stride] (values past cols ignored), and the
@@ -221,10 +228,12 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base);
 
 // RoPE (c/qwanto_decode.c:686-729) on q [query_heads][head_dim] in place and
 // on key [channels], then the Q8 append of the rotated key and of value at
-// slot *pos_ptr (one workgroup; cos/sin tables [max_tokens][head_dim/2]).
+// slot *pos_ptr (one workgroup per token; cos/sin tables
+// [max_tokens][head_dim/2]).  count > 1: a block of tokens, q/key/value
+// [count][...] back to back, token i at slot pos_ptr[i].
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
-                              const int32_t *pos_ptr, hipStream_t stream);
+                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count = 1);
 
 // Quantize one token's fp32 K and V [channels] into slot `token`.
 hipError_t launch_kv_append(const KvCache &c, const float *key,
@@ -268,6 +277,9 @@ struct DecodeAttentionLaunch {
     const float *cos_tab = nullptr;   // [max_tokens][head_dim / 2], or the position's row only:
     const float *sin_tab = nullptr;
     bool rope_row_only = false;       // cos_tab / sin_tab hold just the current position's row
+    uint32_t count = 1;               // > 1: a block of query tokens (no key/value): query and
+                                      // output [count][query_heads][head_dim], positions
+                                      // position_ptr[count], one split
 };
 // int8 MFMA attention (no RoPE/append) over span tokens of the cache: the
 // position from position_ptr when non-null; partials of
