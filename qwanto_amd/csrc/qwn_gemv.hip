@@ -1533,7 +1533,7 @@ namespace {
 // two or four sharing the image loads: more waves, shorter chains), its
 // waves splitting the K blocks -- the fewest that keep a wave's blocks
 // within the unrolled chunk of 5, then more (up to 8) while the launch has
-// fewer than 2048 waves and every wave keeps two blocks or more.  STAGE
+// fewer than 4096 waves and every wave keeps two blocks or more.  STAGE
 // where the row group is a whole number of wave tiles and they fit in LDS
 // (64 KB with the partial tiles).
 struct MfmaPlan {
@@ -1548,7 +1548,7 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     const uint64_t groups = (total_rows + 16 * p.rt - 1) / (16 * p.rt);
     auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
     while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
-    while (p.ks_log2 < 3 && (groups << p.ks_log2) < 2048 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+    while (p.ks_log2 < 3 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
     p.nb = per_wave(p.ks_log2);
     p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
     p.waves = 1u << p.ks_log2;
