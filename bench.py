@@ -51,7 +51,7 @@ def parse():
     p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
     p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
-    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "batch", "copy"),
+    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "batch", "upload", "copy"),
                    help="profiling mode: run only one workload (for rocprofv3)")
     return p.parse_args()
 
@@ -324,6 +324,37 @@ class MfmaSweep:
 INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
 
 
+def upload_bench(ctx, layers=36, seed=3):
+    """Weight upload from host memory (as qwnrun's mmap'd .qwn payloads):
+    the 252 HyperVSQ-2 tensors of a Qwen3-4B-shaped model (1.05 GB), once
+    through qwn_hip_ext_upload_batch (one pipelined call) and once tensor
+    by tensor through qwn_cuda_abi_upload_tensor; GB/s of on-disk bytes
+    including the repack into the wave-tile layout."""
+    import numpy as np
+
+    from qwanto_amd import synth
+    rng = np.random.default_rng(seed)
+    items = []
+    for _ in range(layers):
+        for proj in synth.PROJECTIONS:
+            N, K = synth.QWEN3_4B_SHAPES[proj]
+            items.append((synth.hvsq2_weights(rng, N, K), "hvsq2", N, K))
+    total = sum(w.nbytes for w, _, _, _ in items)
+    t0 = time.perf_counter()
+    hs = ctx.upload_batch(items)
+    t_batch = time.perf_counter() - t0
+    for h in hs:
+        ctx.release(h)
+    t0 = time.perf_counter()
+    hs = [ctx.upload(*it) for it in items]
+    t_single = time.perf_counter() - t0
+    for h in hs:
+        ctx.release(h)
+    return {"bytes": total, "tensors": len(items),
+            "batch_gbps": round(total / t_batch / 1e9, 2), "batch_s": round(t_batch, 3),
+            "per_tensor_gbps": round(total / t_single / 1e9, 2), "per_tensor_s": round(t_single, 3)}
+
+
 def batch_sweep(torch, ctx, steps, warmup):
     """HyperVSQ-2 GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers
     of the Qwen3-4B shapes (weights read once per launch): dot8 grouped
@@ -439,6 +470,9 @@ def main():
     if args.profile == "attention":
         print(json.dumps({"profile_mode": "attention", **attention_bench(torch, ctx, args.steps)}), flush=True)
         return
+    if args.profile == "upload":
+        print(json.dumps({"profile_mode": "upload", **upload_bench(ctx)}), flush=True)
+        return
     if args.profile == "batch":
         print(json.dumps({"profile_mode": "batch", **batch_sweep(torch, ctx, args.steps, args.warmup)}),
               flush=True)
@@ -493,6 +527,7 @@ def main():
             extra["decode_qwen2_1p5b_q4_0"] = dec
             del model
         extra["attention_q8_qwen3_4b"] = attention_bench(torch, ctx, args.steps)
+        extra["upload_hvsq2_qwen3_4b"] = upload_bench(ctx)
         extra["batch_sweep_hvsq2_qwen3_4b"] = batch_sweep(torch, ctx, args.steps, args.warmup)
 
     dev = lib.devices()[0].name.decode()

@@ -162,6 +162,46 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *co
                                                         float *const *outputs, uint32_t batch,
                                                         uint32_t output_stride, void *stream);
 
+/* Upload `count` tensors, each as qwn_cuda_abi_upload_tensor
+ * (c/cuda/qwn_cuda_abi.h:244-246), through one pipeline: whole-row chunks
+ * of each host buffer (an mmap'd .qwn payload, say) are copied into one of
+ * two pinned staging slots while the other slot's DMA and repack run; the
+ * call synchronises once for the batch.  out[i] receives tensor i's handle;
+ * on failure nothing of the batch stays resident.  (No counterpart in the
+ * reference: its host uploads tensor by tensor, c/qwanto_decode.c:790-830.) */
+QWN_CUDA_ABI_API int qwn_hip_ext_upload_batch(QwnCudaContextHandle *context,
+                                              const QwnCudaTensorUpload *uploads, uint32_t count,
+                                              QwnCudaTensorHandle *out);
+
+/* Tensor placement with a GPU tier, as the reference's qwn_plan_residency
+ * (c/qwanto_native.c:379-435, replaced here): tensors in the order of their
+ * name's priority (embedding / LM head 255, norms 245, attention 230, dense
+ * gate 210, other 160, experts 80), then smaller first, then index; each
+ * goes to the GPU while the GPU budget has room, else to RAM while the RAM
+ * budget has room, else stays file-backed.  items[count] receive the plan
+ * in that order (the reference's QwnPlacement layout), totals[3] the GPU,
+ * RAM and file bytes.  gpu_budget QWN_HIP_GPU_BUDGET_AUTO: 90% of the free
+ * memory of the context's device (context required), as the reference host
+ * sizes its GPU tier (c/qwanto_decode.c:202-216); otherwise context may be
+ * NULL. */
+#define QWN_HIP_TIER_GPU 0u
+#define QWN_HIP_TIER_RAM 1u
+#define QWN_HIP_TIER_FILE 2u
+#define QWN_HIP_GPU_BUDGET_AUTO UINT64_MAX
+typedef struct {
+    uint64_t name_hash;       /* FNV-1a 64 of the name (the .qwn index hash) */
+    uint64_t byte_offset;
+    uint64_t byte_size;
+    uint32_t tensor_index;
+    uint8_t tier;             /* QWN_HIP_TIER_* */
+    uint8_t priority;
+    uint16_t reserved;
+} QwnHipPlacement;
+QWN_CUDA_ABI_API int qwn_hip_ext_plan_residency(QwnCudaContextHandle *context, const char *const *names,
+                                                const uint64_t *byte_offsets, const uint64_t *byte_sizes,
+                                                uint32_t count, uint64_t gpu_budget, uint64_t ram_budget,
+                                                QwnHipPlacement *items, uint64_t *totals);
+
 /* Per-token int8 quantization on the device without an image:
  * x fp32 [batch][x_stride] -> q8 [batch][q8_stride] (zero padded past
  * cols), scales [batch]. */

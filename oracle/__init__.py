@@ -319,6 +319,26 @@ class Reference:
     def cpu_kernel_name(self) -> str:
         return self.lib.ref_cpu_kernel_name().decode()
 
+    def plan_residency(self, path: str, gpu_budget: int, ram_budget: int, capacity: int):
+        """The reference's qwn_plan_residency of a .qwn file: ([(name_hash,
+        byte_offset, byte_size, tensor_index, tier, priority)] in plan order,
+        (gpu, ram, file bytes))."""
+        class Placement(ctypes.Structure):
+            _fields_ = [("name_hash", ctypes.c_uint64), ("byte_offset", ctypes.c_uint64),
+                        ("byte_size", ctypes.c_uint64), ("tensor_index", ctypes.c_uint32),
+                        ("tier", ctypes.c_uint8), ("priority", ctypes.c_uint8),
+                        ("reserved", ctypes.c_uint16)]
+        fn = self.lib.qrh_plan_residency
+        fn.argtypes = [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint32,
+                       ctypes.c_void_p]
+        items = (Placement * capacity)()
+        totals = (ctypes.c_uint64 * 3)()
+        n = fn(path.encode(), int(gpu_budget), int(ram_budget), items, capacity, totals)
+        assert n >= 0, "reference residency plan failed"
+        rows = [(p.name_hash, p.byte_offset, p.byte_size, p.tensor_index, p.tier, p.priority)
+                for p in items[:n]]
+        return rows, (totals[0], totals[1], totals[2])
+
     def _matmul(self, fn, w: np.ndarray, x: np.ndarray, N: int) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)
         M, K = x.shape

@@ -122,3 +122,24 @@ int ref_q8_attention(const float *keys, const float *values, int tokens,
     qwn_q8_cache_free(&c);
     return 0;
 }
+
+/* The reference's placement plan (qwn_plan_residency,
+ * c/qwanto_native.c:400-435) of a .qwn file: items[capacity] in plan order
+ * and totals[3] (GPU, RAM, file-backed bytes); returns the tensor count, or
+ * -1 when the file does not open or the plan fails. */
+int qrh_plan_residency(const char *path, uint64_t gpu_budget, uint64_t ram_budget, QwnPlacement *items,
+                       uint32_t capacity, uint64_t *totals) {
+    QwnModel m;
+    const char *err = NULL;
+    if (qwn_open(path, &m, &err) != 0) return -1;
+    QwnResidencyPlan plan;
+    memset(&plan, 0, sizeof(plan));
+    plan.items = items;
+    plan.capacity = capacity;
+    const int rc = qwn_plan_residency(&m, gpu_budget, ram_budget, &plan);
+    totals[0] = plan.gpu_bytes;
+    totals[1] = plan.ram_bytes;
+    totals[2] = plan.nvme_bytes;
+    qwn_close(&m);
+    return rc == 0 ? (int)plan.count : -1;
+}

@@ -54,7 +54,7 @@ EXT_EXPORTS = (
     "qwn_hip_ext_kv_attention_device", "qwn_hip_ext_debug_int_sums",
     "qwn_hip_ext_gemv_group_partials", "qwn_hip_ext_gemv_group_device", "qwn_hip_ext_argmax_device",
     "qwn_hip_ext_mfma_image_bytes", "qwn_hip_ext_mfma_image_device", "qwn_hip_ext_gemm_mfma_device",
-    "qwn_hip_ext_gemm_mfma_group_device",
+    "qwn_hip_ext_gemm_mfma_group_device", "qwn_hip_ext_upload_batch", "qwn_hip_ext_plan_residency",
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
@@ -192,6 +192,34 @@ class DecoderStats(_Versioned):
                 ("graph", ctypes.c_uint32), ("prefill_block_tokens", ctypes.c_uint32)]
 
 
+class Placement(ctypes.Structure):
+    """QwnHipPlacement (the reference's QwnPlacement layout)."""
+    _fields_ = [("name_hash", ctypes.c_uint64), ("byte_offset", ctypes.c_uint64),
+                ("byte_size", ctypes.c_uint64), ("tensor_index", ctypes.c_uint32),
+                ("tier", ctypes.c_uint8), ("priority", ctypes.c_uint8), ("reserved", ctypes.c_uint16)]
+
+
+TIER_GPU, TIER_RAM, TIER_FILE = 0, 1, 2
+GPU_BUDGET_AUTO = (1 << 64) - 1
+
+
+def plan_residency(lib: "Library", names, offsets, sizes, gpu_budget: int, ram_budget: int,
+                   ctx: "Context | None" = None):
+    """qwn_hip_ext_plan_residency: returns ([Placement] in plan order,
+    (gpu_bytes, ram_bytes, file_bytes))."""
+    n = len(names)
+    enc = [str(x).encode() for x in names]
+    arr_names = (ctypes.c_char_p * n)(*enc)
+    offs = (ctypes.c_uint64 * n)(*[int(v) for v in offsets])
+    szs = (ctypes.c_uint64 * n)(*[int(v) for v in sizes])
+    items = (Placement * n)()
+    totals = (ctypes.c_uint64 * 3)()
+    lib.check("plan_residency", lib.lib.qwn_hip_ext_plan_residency(
+        ctx._h if ctx is not None else None, arr_names, offs, szs, n, int(gpu_budget),
+        int(ram_budget), items, totals))
+    return [items[i] for i in range(n)], (totals[0], totals[1], totals[2])
+
+
 STRUCTS = {
     "QwnCudaAbiHeader": Header, "QwnCudaAbiInfo": AbiInfo, "QwnCudaDeviceInfo": DeviceInfo,
     "QwnCudaContextOptions": ContextOptions, "QwnCudaContextHandle": Handle,
@@ -281,6 +309,8 @@ class Library:
         lib.qwn_hip_ext_mfma_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V, V]
         lib.qwn_hip_ext_gemm_mfma_device.argtypes = [P(Handle), P(Handle), V, V, V, U32, U32, V]
         lib.qwn_hip_ext_gemm_mfma_group_device.argtypes = [P(Handle), P(Handle), U32, V, V, V, U32, U32, V]
+        lib.qwn_hip_ext_upload_batch.argtypes = [P(Handle), P(TensorUpload), U32, P(Handle)]
+        lib.qwn_hip_ext_plan_residency.argtypes = [V, V, V, V, U32, ctypes.c_uint64, ctypes.c_uint64, V, V]
         lib.qwn_hip_decoder_create.argtypes = [P(Handle), P(DecoderDesc), P(Handle)]
         lib.qwn_hip_decoder_destroy.argtypes = [P(Handle), P(Handle)]
         lib.qwn_hip_decoder_reset.argtypes = [P(Handle), P(Handle)]
@@ -348,6 +378,21 @@ class Context:
         self.lib.check("upload_tensor", self.lib.lib.qwn_cuda_abi_upload_tensor(
             self._h, ctypes.byref(up), ctypes.byref(h)))
         return h
+
+    def upload_batch(self, items) -> list:
+        """Upload [(data, dtype, rows, cols), ...] through one pipelined call
+        (qwn_hip_ext_upload_batch); returns the handles in order."""
+        keep = [np.ascontiguousarray(d) for d, _, _, _ in items]
+        n = len(items)
+        ups = (TensorUpload * n)()
+        hs = (Handle * n)()
+        for i, (d, (_, dtype, rows, cols)) in enumerate(zip(keep, items)):
+            code, block = DTYPES[dtype]
+            ups[i] = TensorUpload(host_data=_p(d), data_bytes=d.nbytes, dtype=code, rows=rows, cols=cols,
+                                  block_bytes=block)
+            hs[i] = Handle()
+        self.lib.check("upload_batch", self.lib.lib.qwn_hip_ext_upload_batch(self._h, ups, n, hs))
+        return [hs[i] for i in range(n)]
 
     def release(self, h: Handle) -> None:
         self.lib.check("release_tensor",

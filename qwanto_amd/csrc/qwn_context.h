@@ -62,6 +62,17 @@ struct ResidentKv {
 
 struct Decoder;  // qwn_decoder.hip
 
+// Weight upload pipeline: whole-row chunks of a host buffer are copied into
+// one of two pinned slots while the other slot's DMA and repack run.
+constexpr size_t kUploadSlotBytes = 32u << 20;
+struct UploadPipe {
+    PinnedBuffer host[2];
+    DeviceBuffer dev[2];
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    int next = 0;
+};
+
 struct Context {
     std::mutex mutex;
     int device = -1;
@@ -74,6 +85,7 @@ struct Context {
     std::vector<ResidentTensor *> tensors;
     std::vector<ResidentKv *> caches;
     std::vector<Decoder *> decoders;
+    UploadPipe upload;
     QwnCudaTelemetry telemetry{};
 };
 

@@ -1101,10 +1101,10 @@ __global__ __launch_bounds__(kGemvThreads) void dump_kernel(GemvArgs a, int32_t 
 // One thread per (row, unit); the destination was zero filled.
 
 struct RepackArgs {
-    const uint8_t *src;
+    const uint8_t *src;  // the on-disk blocks of rows [row0, row0 + rows)
     uint8_t *payload;
     uint8_t *meta;
-    uint32_t rows, cols, units, lanes, rows_per_wave;
+    uint32_t row0, rows, cols, units, lanes, rows_per_wave;
     size_t tile_payload, tile_meta;
 };
 
@@ -1116,7 +1116,7 @@ template <int KIND>
 __global__ void repack_kernel(RepackArgs r) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= static_cast<size_t>(r.rows) * r.units) return;
-    const uint32_t row = idx / r.units, u = idx % r.units;
+    const uint32_t lrow = idx / r.units, u = idx % r.units, row = r.row0 + lrow;
     UnitAddr ad[4];
     for (uint32_t q = 0; q < 4; ++q)
         ad[q] = unit_addr(row, u, q, r.lanes, r.rows_per_wave, r.units, r.tile_payload, r.tile_meta);
@@ -1138,7 +1138,7 @@ __global__ void repack_kernel(RepackArgs r) {
         for (uint32_t q = 0; q < 4; ++q) {
             const uint32_t b = u * 4 + q;
             if (b >= nb) break;
-            const uint8_t *blk = r.src + (static_cast<size_t>(row) * nb + b) * 18;
+            const uint8_t *blk = r.src + (static_cast<size_t>(lrow) * nb + b) * 18;
             uint4 v;
             v.x = load_u32_unaligned(blk + 2);
             v.y = load_u32_unaligned(blk + 6);
@@ -1153,7 +1153,7 @@ __global__ void repack_kernel(RepackArgs r) {
             const uint32_t k0 = u * 32 + q * 8;
             uint32_t h[4] = {0, 0, 0, 0};
             if (k0 < r.cols) {
-                const uint8_t *src = r.src + (static_cast<size_t>(row) * r.cols + k0) * 2;
+                const uint8_t *src = r.src + (static_cast<size_t>(lrow) * r.cols + k0) * 2;
                 const uint32_t n = min(8u, r.cols - k0);
                 for (uint32_t i = 0; i < n; ++i)
                     h[i >> 1] |= static_cast<uint32_t>(src[2 * i] | (src[2 * i + 1] << 8)) << (16 * (i & 1));
@@ -1304,26 +1304,37 @@ GemvPlan plan_gemv(const DeviceTensor &t, int batch) {
     return p;
 }
 
-hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging, hipStream_t stream) {
-    hipError_t e = hipMemsetAsync(t.payload, 0, t.device_bytes, stream);
-    if (e != hipSuccess) return e;
+hipError_t clear_tensor(const DeviceTensor &t, hipStream_t stream) {
+    return hipMemsetAsync(t.payload, 0, t.device_bytes, stream);
+}
+
+hipError_t repack_rows(const DeviceTensor &t, const uint8_t *src, uint32_t row0, uint32_t nrows,
+                       hipStream_t stream) {
+    if (row0 + nrows > t.rows || nrows == 0) return hipErrorInvalidValue;
     RepackArgs r{};
-    r.src = staging;
+    r.src = src;
     r.payload = t.payload;
     r.meta = t.meta;
-    r.rows = t.rows;
+    r.row0 = row0;
+    r.rows = nrows;
     r.cols = t.cols;
     r.units = t.units;
     r.lanes = t.lanes;
     r.rows_per_wave = t.rows_per_wave;
     r.tile_payload = t.tile_payload_bytes;
     r.tile_meta = t.tile_meta_bytes;
-    const size_t n = static_cast<size_t>(t.rows) * t.units;
+    const size_t n = static_cast<size_t>(nrows) * t.units;
     const dim3 grid((n + 255) / 256);
     if (t.kind == kHvsq2) hipLaunchKernelGGL(repack_kernel<kHvsq2>, grid, dim3(256), 0, stream, r);
     else if (t.kind == kQ4_0) hipLaunchKernelGGL(repack_kernel<kQ4_0>, grid, dim3(256), 0, stream, r);
     else hipLaunchKernelGGL(repack_kernel<kF16>, grid, dim3(256), 0, stream, r);
     return hipGetLastError();
+}
+
+hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging, hipStream_t stream) {
+    hipError_t e = clear_tensor(t, stream);
+    if (e != hipSuccess) return e;
+    return repack_rows(t, staging, 0, t.rows, stream);
 }
 
 hipError_t launch_image(const DeviceTensor &t, const void *x, uint32_t batch, uint32_t x_stride,

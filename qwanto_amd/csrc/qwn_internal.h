@@ -95,6 +95,11 @@ GemvPlan plan_gemv(const DeviceTensor &t, int batch);
 // on the device) into the device layout of `t`.
 hipError_t repack_tensor(const DeviceTensor &t, const uint8_t *staging,
                          hipStream_t stream);
+// The same in pieces: zero the device layout (padding slots stay zero),
+// then repack rows [row0, row0 + nrows) from their on-disk bytes at `src`.
+hipError_t clear_tensor(const DeviceTensor &t, hipStream_t stream);
+hipError_t repack_rows(const DeviceTensor &t, const uint8_t *src, uint32_t row0, uint32_t nrows,
+                       hipStream_t stream);
 
 // Bytes of one token's activation image for a tensor kind / unit count
 // (the LDS layout the GEMV reads, padded to 16 bytes).

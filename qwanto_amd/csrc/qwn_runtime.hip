@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <new>
 #include <string>
 #include <vector>
@@ -381,6 +382,11 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *handle) 
         ctx->dev_scales.release();
         ctx->dev_work.release();
         ctx->dev_img.release();
+        for (int i = 0; i < 2; ++i) {
+            ctx->upload.host[i].release();
+            ctx->upload.dev[i].release();
+            if (ctx->upload.done[i]) (void)hipEventDestroy(ctx->upload.done[i]);
+        }
         (void)hipEventDestroy(ctx->ev_start);
         (void)hipEventDestroy(ctx->ev_end);
         (void)hipStreamDestroy(ctx->stream);
@@ -390,16 +396,15 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *handle) 
     return QWN_CUDA_STATUS_OK;
 }
 
-QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
-                                                const QwnCudaTensorUpload *up,
-                                                QwnCudaTensorHandle *out) {
-    Context *ctx = context_of(handle);
-    if (!ctx || !up || !out || !header_ok(*up) || !header_ok(*out) || !up->host_data || up->rows == 0 ||
-        up->cols == 0) {
+namespace {
+
+// Validates an upload and lays the tensor out (no device memory yet).
+int describe_upload(const QwnCudaTensorUpload *up, DeviceTensor &t) {
+    if (!up || !header_ok(*up) || !up->host_data || up->rows == 0 || up->cols == 0) {
         set_error("invalid tensor upload request");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
-    DeviceTensor t;
+    t = DeviceTensor{};
     t.rows = up->rows;
     t.cols = up->cols;
     switch (up->dtype) {
@@ -435,50 +440,166 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
         set_error("tensor rows of %u columns exceed the GEMV lane plan", up->cols);
         return QWN_CUDA_STATUS_UNSUPPORTED;
     }
-    std::lock_guard<std::mutex> lock(ctx->mutex);
-    if (ctx->tensors.size() >= QWN_CUDA_MAX_RESIDENT_TENSORS) {
+    return QWN_CUDA_STATUS_OK;
+}
+
+// Host copy into a pinned slot, split over up to 8 threads for large chunks
+// (one core's copy rate is below what the DMA engines take).
+void copy_parallel(void *dst, const uint8_t *src, size_t bytes) {
+    constexpr size_t kPerThread = 4u << 20;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency() / 2);
+    const size_t n = std::min<size_t>({8, hw, (bytes + kPerThread - 1) / kPerThread});
+    if (n <= 1) {
+        std::memcpy(dst, src, bytes);
+        return;
+    }
+    const size_t part = (bytes / n + 63) & ~static_cast<size_t>(63);
+    std::vector<std::thread> workers;
+    for (size_t i = 1; i < n; ++i) {
+        const size_t off = i * part;
+        if (off >= bytes) break;
+        workers.emplace_back([=] { std::memcpy(static_cast<uint8_t *>(dst) + off, src + off, std::min(part, bytes - off)); });
+    }
+    std::memcpy(dst, src, std::min(part, bytes));
+    for (auto &w : workers) w.join();
+}
+
+// Enqueues the upload of one allocated tensor through the pipeline (context
+// lock held): the layout is zeroed, then chunks of whole rows go host ->
+// pinned slot (CPU copy, after that slot's previous DMA and repack ended)
+// -> device slot (DMA) -> wave-tile layout (repack kernel), alternating
+// slots so the CPU copy of one chunk overlaps the DMA and repack of the
+// previous one.  Nothing here waits for the last chunk.
+hipError_t enqueue_upload(Context *ctx, const DeviceTensor &t, const uint8_t *host) {
+    UploadPipe &p = ctx->upload;
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        if (!p.done[i]) e = hipEventCreateWithFlags(&p.done[i], hipEventDisableTiming);
+        if (e == hipSuccess) e = p.host[i].ensure(kUploadSlotBytes);
+        if (e == hipSuccess) e = p.dev[i].ensure(kUploadSlotBytes);
+    }
+    if (e == hipSuccess) e = qwn::clear_tensor(t, ctx->stream);
+    const uint64_t row_bytes = t.logical_bytes / t.rows;
+    const uint32_t per_chunk = static_cast<uint32_t>(std::max<uint64_t>(1, kUploadSlotBytes / row_bytes));
+    if (row_bytes > kUploadSlotBytes) {
+        for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+            if (p.pending[i]) e = hipEventSynchronize(p.done[i]);
+            p.pending[i] = false;
+            if (e == hipSuccess) e = p.host[i].ensure(row_bytes);
+            if (e == hipSuccess) e = p.dev[i].ensure(row_bytes);
+        }
+    }
+    for (uint32_t r0 = 0; e == hipSuccess && r0 < t.rows; r0 += per_chunk) {
+        const int s = p.next;
+        p.next ^= 1;
+        const uint32_t n = std::min(per_chunk, t.rows - r0);
+        const size_t bytes = static_cast<size_t>(n) * row_bytes;
+        if (p.pending[s] && (e = hipEventSynchronize(p.done[s])) != hipSuccess) break;
+        p.pending[s] = false;
+        copy_parallel(p.host[s].ptr, host + static_cast<size_t>(r0) * row_bytes, bytes);
+        if ((e = hipMemcpyAsync(p.dev[s].ptr, p.host[s].ptr, bytes, hipMemcpyHostToDevice, ctx->stream)) !=
+                hipSuccess ||
+            (e = qwn::repack_rows(t, static_cast<const uint8_t *>(p.dev[s].ptr), r0, n, ctx->stream)) !=
+                hipSuccess ||
+            (e = hipEventRecord(p.done[s], ctx->stream)) != hipSuccess)
+            break;
+        p.pending[s] = true;
+    }
+    return e;
+}
+
+// Uploads `count` tensors (context lock held): describe and allocate all,
+// pipeline all, one synchronisation; on failure none stays resident.
+int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count, QwnCudaTensorHandle *out) {
+    std::vector<ResidentTensor *> made;
+    uint64_t bytes = 0, device_bytes = 0;
+    auto fail = [&](int status) {
+        (void)hipStreamSynchronize(ctx->stream);
+        for (ResidentTensor *rt : made) free_tensor(rt);
+        return status;
+    };
+    if (ctx->tensors.size() + count > QWN_CUDA_MAX_RESIDENT_TENSORS) {
         set_error("resident tensor limit (%u) reached", QWN_CUDA_MAX_RESIDENT_TENSORS);
         return QWN_CUDA_STATUS_OUT_OF_MEMORY;
     }
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hip_fail("hipSetDevice", e);
-    if (!budget_allows(ctx, t.logical_bytes, t.device_bytes + t.logical_bytes)) {
-        set_error("tensor does not fit the configured GPU memory budget");
-        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!header_ok(out[i])) {
+            set_error("invalid tensor handle %u", i);
+            return fail(QWN_CUDA_STATUS_INVALID_ARGUMENT);
+        }
+        DeviceTensor t;
+        const int st = describe_upload(&ups[i], t);
+        if (st != QWN_CUDA_STATUS_OK) return fail(st);
+        bytes += t.logical_bytes;
+        device_bytes += t.device_bytes;
+        if (!budget_allows(ctx, bytes, device_bytes)) {
+            set_error("tensor upload does not fit the configured GPU memory budget");
+            return fail(QWN_CUDA_STATUS_OUT_OF_MEMORY);
+        }
+        auto *rt = new (std::nothrow) ResidentTensor();
+        if (!rt) return fail(QWN_CUDA_STATUS_OUT_OF_MEMORY);
+        if ((e = hipMalloc(&rt->allocation, t.device_bytes)) != hipSuccess) {
+            delete rt;
+            (void)hip_fail("tensor allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
+            return fail(QWN_CUDA_STATUS_OUT_OF_MEMORY);
+        }
+        t.payload = static_cast<uint8_t *>(rt->allocation);
+        const size_t meta_off = (t.tile_payload_bytes * t.tiles + 255) & ~static_cast<size_t>(255);
+        t.meta = t.tile_meta_bytes ? t.payload + meta_off : nullptr;
+        rt->t = t;
+        made.push_back(rt);
     }
-    auto *rt = new (std::nothrow) ResidentTensor();
-    if (!rt) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
-    void *staging = nullptr;
-    if ((e = hipMalloc(&rt->allocation, t.device_bytes)) != hipSuccess ||
-        (e = hipMalloc(&staging, t.logical_bytes)) != hipSuccess) {
-        if (rt->allocation) (void)hipFree(rt->allocation);
-        delete rt;
-        return hip_fail("tensor allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
-    }
-    t.payload = static_cast<uint8_t *>(rt->allocation);
-    const size_t meta_off = (t.tile_payload_bytes * t.tiles + 255) & ~static_cast<size_t>(255);
-    t.meta = t.tile_meta_bytes ? t.payload + meta_off : nullptr;
-    rt->t = t;
     const auto t0 = std::chrono::steady_clock::now();
-    e = hipMemcpyAsync(staging, up->host_data, t.logical_bytes, hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess) e = qwn::repack_tensor(rt->t, static_cast<const uint8_t *>(staging), ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    (void)hipFree(staging);
-    if (e != hipSuccess) {
-        free_tensor(rt);
-        return hip_fail("tensor upload", e);
+    for (uint32_t i = 0; i < count; ++i)
+        if ((e = enqueue_upload(ctx, made[i]->t, static_cast<const uint8_t *>(ups[i].host_data))) != hipSuccess) {
+            (void)hip_fail("tensor upload", e);
+            return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
+        }
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+        (void)hip_fail("tensor upload", e);
+        return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
     }
-    ctx->tensors.push_back(rt);
-    ctx->resident += t.logical_bytes;
+    ctx->upload.pending[0] = ctx->upload.pending[1] = false;
     QwnCudaTelemetry &tm = ctx->telemetry;
-    tm.gpu_upload_count++;
-    tm.gpu_upload_bytes += t.logical_bytes;
+    for (uint32_t i = 0; i < count; ++i) {
+        ctx->tensors.push_back(made[i]);
+        ctx->resident += made[i]->t.logical_bytes;
+        tm.gpu_upload_count++;
+        tm.gpu_upload_bytes += made[i]->t.logical_bytes;
+        std::memset(&out[i], 0, sizeof(out[i]));
+        qwn_cuda_abi_header_init(&out[i].header, sizeof(out[i]));
+        out[i].opaque = made[i];
+    }
     tm.gpu_resident_bytes = ctx->resident;
     tm.gpu_transfer_ms += ms_since(t0);
-    std::memset(out, 0, sizeof(*out));
-    qwn_cuda_abi_header_init(&out->header, sizeof(*out));
-    out->opaque = rt;
     return QWN_CUDA_STATUS_OK;
+}
+
+}  // namespace
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
+                                                const QwnCudaTensorUpload *up,
+                                                QwnCudaTensorHandle *out) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !up || !out || !header_ok(*up) || !header_ok(*out)) {
+        set_error("invalid tensor upload request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return upload_tensors(ctx, up, 1, out);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_upload_batch(QwnCudaContextHandle *handle, const QwnCudaTensorUpload *uploads,
+                                              uint32_t count, QwnCudaTensorHandle *out) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !uploads || !out || count == 0) {
+        set_error("invalid batch upload request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    return upload_tensors(ctx, uploads, count, out);
 }
 
 QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *handle, QwnCudaTensorHandle *h) {
@@ -1043,6 +1164,94 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *ha
     ctx->telemetry.gpu_matmul_count += count;
     ctx->telemetry.gpu_kernel_launch_count++;
     ctx->telemetry.gpu_projection_count += count;
+    return QWN_CUDA_STATUS_OK;
+}
+
+namespace {
+
+uint64_t fnv1a64(const char *s) {
+    uint64_t h = 0xcbf29ce484222325ull;  // FNV-1a 64 offset basis
+    for (; *s; ++s) {
+        h ^= static_cast<uint8_t>(*s);
+        h *= 0x100000001b3ull;  // FNV-1a 64 prime
+    }
+    return h;
+}
+
+// Placement priority of a tensor name (c/qwanto_native.c:379-389).
+uint8_t name_priority(const char *n) {
+    auto has = [n](const char *p) { return std::strstr(n, p) != nullptr; };
+    if (has("embed") || has("lm_head")) return 255;
+    if (has("norm")) return 245;
+    if (has("q_proj") || has("k_proj") || has("v_proj") || has("o_proj") || has("attn")) return 230;
+    if (has("gate") && !has("expert")) return 210;
+    if (has("expert")) return 80;
+    return 160;
+}
+
+}  // namespace
+
+QWN_CUDA_ABI_API int qwn_hip_ext_plan_residency(QwnCudaContextHandle *handle, const char *const *names,
+                                                const uint64_t *byte_offsets, const uint64_t *byte_sizes,
+                                                uint32_t count, uint64_t gpu_budget, uint64_t ram_budget,
+                                                QwnHipPlacement *items, uint64_t *totals) {
+    if (!names || !byte_offsets || !byte_sizes || !items || !totals || (count && !names)) {
+        set_error("invalid residency plan request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < count; ++i)
+        if (!names[i]) {
+            set_error("tensor %u has no name", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+    if (gpu_budget == QWN_HIP_GPU_BUDGET_AUTO) {
+        Context *ctx = context_of(handle);
+        if (!ctx) {
+            set_error("an automatic GPU budget needs a context");
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+        std::lock_guard<std::mutex> lock(ctx->mutex);
+        size_t free_b = 0, total_b = 0;
+        hipError_t e = hipSetDevice(ctx->device);
+        if (e == hipSuccess) e = hipMemGetInfo(&free_b, &total_b);
+        if (e != hipSuccess) return hip_fail("device memory query", e);
+        gpu_budget = static_cast<uint64_t>(static_cast<double>(free_b) * 0.90);
+        if (ctx->budget) gpu_budget = std::min(gpu_budget, ctx->budget - std::min(ctx->budget, ctx->resident));
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+        QwnHipPlacement &p = items[i];
+        std::memset(&p, 0, sizeof(p));
+        p.name_hash = fnv1a64(names[i]);
+        p.byte_offset = byte_offsets[i];
+        p.byte_size = byte_sizes[i];
+        p.tensor_index = i;
+        p.priority = name_priority(names[i]);
+        p.tier = QWN_HIP_TIER_FILE;
+    }
+    // a total order (priority desc, size asc, index asc): any sort gives the
+    // reference's qsort result
+    std::sort(items, items + count, [](const QwnHipPlacement &x, const QwnHipPlacement &y) {
+        if (x.priority != y.priority) return x.priority > y.priority;
+        if (x.byte_size != y.byte_size) return x.byte_size < y.byte_size;
+        return x.tensor_index < y.tensor_index;
+    });
+    uint64_t gpu = 0, ram = 0, file = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        QwnHipPlacement &p = items[i];
+        if (gpu <= gpu_budget && p.byte_size <= gpu_budget - gpu) {
+            p.tier = QWN_HIP_TIER_GPU;
+            gpu += p.byte_size;
+        } else if (ram <= ram_budget && p.byte_size <= ram_budget - ram) {
+            p.tier = QWN_HIP_TIER_RAM;
+            ram += p.byte_size;
+        } else {
+            p.tier = QWN_HIP_TIER_FILE;
+            file += p.byte_size;
+        }
+    }
+    totals[0] = gpu;
+    totals[1] = ram;
+    totals[2] = file;
     return QWN_CUDA_STATUS_OK;
 }
 

@@ -152,8 +152,13 @@ class QwnFile:
         descs = [struct.unpack_from(DESC_FMT, self.mm, PREFIX_SIZE + i * DESC_SIZE)
                  for i in range(inline_count)]
         tail = struct.unpack_from("<Q", self.mm, len(self.mm) - 8)[0]
-        count, dsize, doff, _, _ = struct.unpack_from(TAIL_FMT, self.mm, tail)
-        descs += [struct.unpack_from(DESC_FMT, self.mm, doff + i * dsize) for i in range(count)]
+        count, dsize, doff, index_off, _ = struct.unpack_from(TAIL_FMT, self.mm, tail)
+        # overflow tensors in the order of the hash-sorted index, as the
+        # reference enumerates them (c/qwanto_native.c:286-305, 374-378), so
+        # tensor indices agree with qwn_tensor_at
+        for i in range(count):
+            _, off = struct.unpack_from("<QQ", self.mm, index_off + 16 * i)
+            descs.append(struct.unpack_from(DESC_FMT, self.mm, off))
         if len(descs) != n_tensors:
             raise ValueError("descriptor count mismatch")
         self.tensors = {}

@@ -86,6 +86,8 @@ def weights(dtype: str, rng: np.random.Generator, rows: int, cols: int) -> np.nd
         return q4_0_weights(rng, rows, cols)
     if dtype == "hvsq2":
         return hvsq2_weights(rng, rows, cols)
+    if dtype == "f16":
+        return f16_weights(rng, rows, cols)
     raise ValueError(f"unknown weight dtype {dtype!r}")
 
 
