@@ -155,12 +155,14 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *context,
                                                   uint32_t output_stride, void *stream);
 /* The same GEMM over `count` (1..4) HyperVSQ-2 tensors with the same
  * column count that share one MFMA image (q/k/v, gate/up), in one launch:
- * outputs[i] [batch][output_stride or the tensor's rows]. */
+ * outputs[i] [batch][output_stride or the tensor's rows]; accumulate != 0
+ * adds the product to the outputs (a residual stream) instead. */
 QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *context,
                                                         const QwnCudaTensorHandle *tensors, uint32_t count,
                                                         const void *image, const float *scales,
                                                         float *const *outputs, uint32_t batch,
-                                                        uint32_t output_stride, void *stream);
+                                                        uint32_t output_stride, uint32_t accumulate,
+                                                        void *stream);
 
 /* Upload `count` tensors, each as qwn_cuda_abi_upload_tensor
  * (c/cuda/qwn_cuda_abi.h:244-246), through one pipeline: whole-row chunks

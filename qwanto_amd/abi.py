@@ -308,7 +308,7 @@ class Library:
         lib.qwn_hip_ext_mfma_image_bytes.restype = ctypes.c_uint64
         lib.qwn_hip_ext_mfma_image_device.argtypes = [P(Handle), P(Handle), V, U32, U32, V, V]
         lib.qwn_hip_ext_gemm_mfma_device.argtypes = [P(Handle), P(Handle), V, V, V, U32, U32, V]
-        lib.qwn_hip_ext_gemm_mfma_group_device.argtypes = [P(Handle), P(Handle), U32, V, V, V, U32, U32, V]
+        lib.qwn_hip_ext_gemm_mfma_group_device.argtypes = [P(Handle), P(Handle), U32, V, V, V, U32, U32, U32, V]
         lib.qwn_hip_ext_upload_batch.argtypes = [P(Handle), P(TensorUpload), U32, P(Handle)]
         lib.qwn_hip_ext_plan_residency.argtypes = [V, V, V, V, U32, ctypes.c_uint64, ctypes.c_uint64, V, V]
         lib.qwn_hip_decoder_create.argtypes = [P(Handle), P(DecoderDesc), P(Handle)]
@@ -502,13 +502,15 @@ class Context:
             self._h, ctypes.byref(h), image_ptr, scales_ptr, out_ptr, batch, output_stride, stream))
 
     def gemm_mfma_group_device(self, handles, image_ptr: int, scales_ptr: int, out_ptrs, batch: int,
-                               output_stride: int = 0, stream: int | None = None) -> None:
-        """One MFMA launch over 1..4 tensors of equal columns sharing an image."""
+                               output_stride: int = 0, stream: int | None = None,
+                               accumulate: bool = False) -> None:
+        """One MFMA launch over 1..4 tensors of equal columns sharing an image
+        (accumulate: outputs += the product)."""
         n = len(handles)
         hs = (Handle * n)(*handles)
         outs = (ctypes.c_void_p * n)(*out_ptrs)
         self.lib.check("gemm_mfma_group_device", self.lib.lib.qwn_hip_ext_gemm_mfma_group_device(
-            self._h, hs, n, image_ptr, scales_ptr, outs, batch, output_stride, stream))
+            self._h, hs, n, image_ptr, scales_ptr, outs, batch, output_stride, int(accumulate), stream))
 
     # -- KV cache ---------------------------------------------------------------
     def kv_create(self, max_tokens: int, kv_heads: int, head_dim: int) -> Handle:

@@ -163,6 +163,11 @@ struct Decoder {
           *pup = nullptr, *pscales = nullptr;
     uint8_t *pimg = nullptr;
     uint32_t pimg_stride = 0;
+    // HyperVSQ-2 blocks of kMfmaMinTokens or more go through the int8 MFMA
+    // GEMM: int8 tokens [16][pq8_stride] and one MFMA image
+    int8_t *pq8 = nullptr;
+    uint32_t pq8_stride = 0;
+    uint8_t *pmimg = nullptr;
     int32_t *ppos = nullptr;
     hipGraphExec_t prefill_exec[kPrefillTokens + 1][2] = {};
     bool prefill_tried[kPrefillTokens + 1][2] = {};
@@ -251,9 +256,35 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
                        d->ppos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const uint32_t D = d->hidden, Q = d->heads * d->head_dim, I = d->inter;
-    auto batched = [&](GemvGroupLaunch g, uint32_t mode) {
+    // one projection group of the block: its input prepared per token
+    // (mode: fp32 / RMSNorm / SwiGLU of x), then the batched dot8 GEMV on
+    // activation images, or for HyperVSQ-2 from kMfmaMinTokens tokens the
+    // int8 MFMA GEMM on the MFMA image; add: residual stream
+    const bool mfma = d->pq8 && m >= kMfmaMinTokens;
+    auto project = [&](std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs,
+                       uint32_t mode, const float *x, const float *x2, const float *norm, uint32_t x_stride,
+                       bool add) {
+        const DeviceTensor &t0 = **ts.begin();
+        hipError_t e2;
+        if (mfma) {
+            if ((e2 = launch_prepare_image(t0, mode, x, x2, norm, d->eps, m, x_stride, nullptr, 0, d->pscales,
+                                           d->pq8, d->pq8_stride, s)) != hipSuccess ||
+                (e2 = launch_mfma_image(t0, d->pq8, m, d->pq8_stride, d->pmimg, s)) != hipSuccess)
+                return e2;
+            const DeviceTensor *tv[kMaxGroup];
+            float *ov[kMaxGroup];
+            uint32_t n = 0;
+            for (const DeviceTensor *t : ts) tv[n++] = t;
+            n = 0;
+            for (float *o : outs) ov[n++] = o;
+            return launch_gemm_mfma_group(tv, ov, n, d->pmimg, d->pscales, m, nullptr, s, add);
+        }
+        if ((e2 = launch_prepare_image(t0, mode, x, x2, norm, d->eps, m, x_stride, d->pimg, d->pimg_stride,
+                                       d->pscales, nullptr, 0, s)) != hipSuccess)
+            return e2;
+        GemvGroupLaunch g = group(ts, outs);
         g.input_mode = kInImage;
-        g.output_mode = mode;
+        g.output_mode = add ? kOutAdd : kOutStore;
         g.image = d->pimg;
         g.image_stride = d->pimg_stride;
         g.scales = d->pscales;
@@ -264,9 +295,8 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
         const DeviceTensor *const *w = d->proj.data() + static_cast<size_t>(l) * kProj;
         const float *nin = d->norms_in + static_cast<size_t>(l) * D;
         const float *npost = d->norms_post + static_cast<size_t>(l) * D;
-        if ((e = launch_prepare_image(*w[P_Q], kInNorm, d->px, nullptr, nin, d->eps, m, D, d->pimg, d->pimg_stride,
-                                      d->pscales, nullptr, 0, s)) != hipSuccess ||
-            (e = batched(group({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}), kOutStore)) != hipSuccess ||
+        if ((e = project({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}, kInNorm, d->px, nullptr, nin, D,
+                         false)) != hipSuccess ||
             (e = launch_rope_append(d->caches[l], d->pq, d->heads, d->pk, d->pv, d->cos_tab, d->sin_tab, d->ppos, s,
                                     m)) != hipSuccess)
             return e;
@@ -289,15 +319,10 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
                                              d->attn_scale, d->partials, s)) != hipSuccess)
                     return e;
         }
-        if ((e = launch_prepare_image(*w[P_O], kInF32, d->pattn, nullptr, nullptr, 0.0f, m, Q, d->pimg,
-                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
-            (e = batched(group({w[P_O]}, {d->px}), kOutAdd)) != hipSuccess ||
-            (e = launch_prepare_image(*w[P_GATE], kInNorm, d->px, nullptr, npost, d->eps, m, D, d->pimg,
-                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
-            (e = batched(group({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}), kOutStore)) != hipSuccess ||
-            (e = launch_prepare_image(*w[P_DOWN], kInSwiglu, d->pgate, d->pup, nullptr, 0.0f, m, I, d->pimg,
-                                      d->pimg_stride, d->pscales, nullptr, 0, s)) != hipSuccess ||
-            (e = batched(group({w[P_DOWN]}, {d->px}), kOutAdd)) != hipSuccess)
+        if ((e = project({w[P_O]}, {d->px}, kInF32, d->pattn, nullptr, nullptr, Q, true)) != hipSuccess ||
+            (e = project({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}, kInNorm, d->px, nullptr, npost, D, false)) !=
+                hipSuccess ||
+            (e = project({w[P_DOWN]}, {d->px}, kInSwiglu, d->pgate, d->pup, nullptr, I, true)) != hipSuccess)
             return e;
     }
     hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(64), 0, s, d->state, d->ppos, m, last ? 1u : 0u);
@@ -532,9 +557,20 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         part(reinterpret_cast<void **>(&d->pscales), P * 4);
         part(reinterpret_cast<void **>(&d->ppos), P * 4);
         size_t stride = 0;
-        for (int p : {P_Q, P_O, P_DOWN}) stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
+        uint32_t units = 0;
+        for (int p : {P_Q, P_O, P_DOWN}) {
+            stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
+            units = std::max(units, d->proj[p]->units);
+        }
         d->pimg_stride = static_cast<uint32_t>((stride + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->pimg), P * d->pimg_stride);
+        if (kind == kHvsq2) {
+            d->pq8_stride = units * 256;
+            part(reinterpret_cast<void **>(&d->pq8), P * d->pq8_stride);
+            part(reinterpret_cast<void **>(&d->pmimg), mfma_image_bytes(*d->proj[P_DOWN]) +
+                                                           mfma_image_bytes(*d->proj[P_Q]) +
+                                                           mfma_image_bytes(*d->proj[P_O]));
+        }
     }
     // attention partials of the device-position kernels
     KvCache proto;

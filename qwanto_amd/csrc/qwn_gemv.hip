@@ -831,6 +831,7 @@ struct MfmaArgs {
     const float *scales;   // [ntok]
     uint32_t ntok;
     uint32_t vec_out;      // bit i: job i's rows may be stored 4 at a time (16-byte aligned)
+    uint32_t accumulate;   // out += W x (residual add) instead of out = W x
 };
 
 constexpr int kMfmaMaxWaves = 8;
@@ -1024,6 +1025,8 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
     }
     // lane (g, m) holds rows 4g .. 4g+3 of each tile for token m: one
     // 16-byte store where the rows are whole and the output row aligned
+    // accumulate: out += the rounded product (the residual stream), in two
+    // roundings as the dot8 epilogue
     const uint32_t g = lane >> 4, m = lane & 15;
     if (ks == 0 && m < a.ntok) {
         const float xs = a.scales[m];
@@ -1033,12 +1036,21 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
             const uint32_t n0 = r0 + 16 * t + 4 * g;
             float *dst = output + static_cast<size_t>(m) * stride + n0;
             if (vec && n0 + 4 <= rows) {
-                *reinterpret_cast<float4 *>(dst) = make_float4(mul_rounded(acc[t][0], xs), mul_rounded(acc[t][1], xs),
-                                                               mul_rounded(acc[t][2], xs), mul_rounded(acc[t][3], xs));
+                float4 v = make_float4(mul_rounded(acc[t][0], xs), mul_rounded(acc[t][1], xs),
+                                       mul_rounded(acc[t][2], xs), mul_rounded(acc[t][3], xs));
+                if (a.accumulate) {
+                    const float4 o = *reinterpret_cast<const float4 *>(dst);
+                    v = make_float4(add_rounded(o.x, v.x), add_rounded(o.y, v.y), add_rounded(o.z, v.z),
+                                    add_rounded(o.w, v.w));
+                }
+                *reinterpret_cast<float4 *>(dst) = v;
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (n0 + r < rows) dst[r] = mul_rounded(acc[t][r], xs);
+                    if (n0 + r < rows) {
+                        const float v = mul_rounded(acc[t][r], xs);
+                        dst[r] = a.accumulate ? add_rounded(dst[r], v) : v;
+                    }
             }
         }
     }
@@ -1594,7 +1606,7 @@ hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, h
 
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
-                                  const uint32_t *output_strides, hipStream_t stream) {
+                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate) {
     if (count == 0 || count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
         batch > static_cast<uint32_t>(kMfmaTokens))
         return hipErrorInvalidValue;
@@ -1638,6 +1650,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.image = image;
     a.scales = scales;
     a.ntok = batch;
+    a.accumulate = accumulate ? 1u : 0u;
     switch (p.nbt) {
     case 2: return launch_mfma_nb<2>(p, grid, a, stream);
     case 3: return launch_mfma_nb<3>(p, grid, a, stream);

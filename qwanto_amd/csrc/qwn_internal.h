@@ -196,10 +196,11 @@ hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t b
 hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const float *scales, float *output,
                             uint32_t batch, uint32_t output_stride, hipStream_t stream);
 // The same over up to kMaxGroup tensors of equal K sharing one image (one
-// launch); output_strides may be null (0 entries: each tensor's rows).
+// launch); output_strides may be null (0 entries: each tensor's rows);
+// accumulate: outputs += W x_t * scales[t] (the residual stream).
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
-                                  const uint32_t *output_strides, hipStream_t stream);
+                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate = false);
 constexpr uint32_t kMfmaMinTokens = 8;
 
 // RMSNorm of one fp32 token into the fp32 image of an F16 tensor.

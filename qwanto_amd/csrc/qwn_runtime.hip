@@ -1137,7 +1137,8 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *ha
                                                         const QwnCudaTensorHandle *tensors, uint32_t count,
                                                         const void *image, const float *scales,
                                                         float *const *outputs, uint32_t batch,
-                                                        uint32_t output_stride, void *stream) {
+                                                        uint32_t output_stride, uint32_t accumulate,
+                                                        void *stream) {
     Context *ctx = context_of(handle);
     if (!ctx || !tensors || !outputs || !image || !scales || count == 0 || count > qwn::kMaxGroup || batch == 0 ||
         batch > 16 || (reinterpret_cast<uintptr_t>(image) & 15u)) {
@@ -1159,7 +1160,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *ha
     }
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
     hipError_t e = qwn::launch_gemm_mfma_group(ts, outputs, count, static_cast<const uint8_t *>(image), scales, batch,
-                                               strides, s);
+                                               strides, s, accumulate != 0);
     if (e != hipSuccess) return hip_fail("MFMA group GEMM launch", e);
     ctx->telemetry.gpu_matmul_count += count;
     ctx->telemetry.gpu_kernel_launch_count++;

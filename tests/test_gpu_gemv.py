@@ -134,6 +134,39 @@ def test_hvsq2_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
             gpu_ctx.release(h)
 
 
+@pytest.mark.parametrize("Ns,K,M", [((2560,), 4096, 16), ((77, 1030), 9728, 9)])
+def test_hvsq2_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
+    """accumulate = 1: outputs += the product (the decoder's residual adds),
+    against the oracle product added to the prior contents."""
+    import torch
+    rng = np.random.default_rng(sum(Ns) + K + M + 1)
+    ws = [synth.hvsq2_weights(rng, N, K) for N in Ns]
+    x = synth.activations(rng, M, K)
+    q8, xs, sums = oracle_lib.quantize(x)
+    hs = [gpu_ctx.upload(w, "hvsq2", N, K) for w, N in zip(ws, Ns)]
+    try:
+        dev = torch.device("cuda:0")
+        q8d = torch.from_numpy(q8).to(dev)
+        xsd = torch.from_numpy(xs).to(dev)
+        img = torch.zeros(gpu_ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
+        init = [rng.standard_normal((M, N)).astype(np.float32) for N in Ns]
+        ys = [torch.from_numpy(i.copy()).to(dev) for i in init]
+        s = torch.cuda.current_stream().cuda_stream
+        gpu_ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
+        gpu_ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
+                                       stream=s, accumulate=True)
+        torch.cuda.synchronize()
+        for w, N, y, i0 in zip(ws, Ns, ys, init):
+            yh = y.cpu().numpy()
+            for t in range(M):
+                ref = oracle_lib.gemv_hvsq2(w, q8[t], sums[t], float(xs[t]), K, N)
+                ok, worst = gemv_close(yh[t] - i0[t], ref)
+                assert ok, f"tensor {N}x{K} token {t}: worst {worst:.3g}"
+    finally:
+        for h in hs:
+            gpu_ctx.release(h)
+
+
 @pytest.mark.parametrize("N,K", [(1, 1), (3, 31), (5, 32), (7, 100), (65, 129), (130, 520),
                                  (64, 4064), (2, 16384)])
 def test_q4_0_edge_shapes(gpu_ctx, oracle_lib, N, K):

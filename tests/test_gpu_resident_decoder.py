@@ -79,6 +79,7 @@ PREFILL_ORACLE_RTOL = 2e-2  # gross errors (positions, causal mask, cache layout
 
 
 @pytest.mark.parametrize("cfg,dtype,P", [(SMALL, "q4_0", 21), (SMALL, "hvsq2", 16), (QWEN2_LIKE, "q4_0", 37),
+                                         (QWEN2_LIKE, "hvsq2", 37),
                                          (QWEN2_LIKE, "hvsq2", 5), (LONG_CTX, "q4_0", 18), (SMALL, "q4_0", 1)])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P):
     """qwn_hip_decoder_prefill (prompt blocks of up to 16 tokens through the
