@@ -16,9 +16,10 @@ reference's CPU GEMV (oracle/_ref, or the oracle port) on this host.
 
 Also reported: the same sweep with one launch per tensor, the Qwen2-1.5B
 Q4_0 sweep, the Q4_0 greedy decode (tok/s, with the reference CPU decoder
-on a bounded sample beside it), Q8-KV decode attention at the Qwen3-4B
-shape for 4096 and 32768 cached tokens, and the HyperVSQ-2 batch sweep
-M = 1..16 (weights read once per launch).
+on a bounded sample beside it), the same decode at the Qwen3-4B layer
+shapes in HyperVSQ-2, Q8-KV decode attention at the Qwen3-4B shape for 4096
+and 32768 cached tokens, the weight upload rate, and the HyperVSQ-2 batch
+sweep M = 1..16 (weights read once per launch).
 """
 from __future__ import annotations
 
@@ -51,7 +52,7 @@ def parse():
     p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
     p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
-    p.add_argument("--profile", choices=("gate-up", "decode", "attention", "batch", "upload", "copy"),
+    p.add_argument("--profile", choices=("gate-up", "decode", "decode-4b", "attention", "batch", "upload", "copy"),
                    help="profiling mode: run only one workload (for rocprofv3)")
     return p.parse_args()
 
@@ -165,18 +166,23 @@ def time_graph(torch, fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def decode_model(seed=2026, prompt_len=32):
+def decode_model(seed=2026, prompt_len=32, cfg=None, dtype="q4_0"):
     import numpy as np
 
     from qwanto_amd import synth
-    cfg = synth.QWEN2_1P5B_CONFIG
+    cfg = cfg or synth.QWEN2_1P5B_CONFIG
     rng = np.random.default_rng(seed)
-    model = synth.decoder_model(rng, cfg, "q4_0")
+    model = synth.decoder_model(rng, cfg, dtype)
     prompt = synth.prompt_tokens(rng, cfg["vocab"], prompt_len)
     return model, prompt
 
 
-def decode_bench(ctx, model, prompt, new_tokens=128):
+DECODE_1P5B = "qwen2_1p5b_q4_0 random-init (seed 2026), tied F16 LM head, Q8 KV, greedy, HIP graph per token"
+DECODE_4B = ("qwen3_4b-shaped hvsq2 dense decoder (no q/k norms), random-init (seed 2027), tied F16 LM head, "
+             "Q8 KV, greedy, HIP graph per token")
+
+
+def decode_bench(ctx, model, prompt, new_tokens=128, workload=DECODE_1P5B):
     """Greedy decode of the Qwen2-1.5B shaped random Q4_0 model (28 layers,
     tied F16 LM head, Q8 KV) on the resident decoder: the prompt, then
     `new_tokens` greedy steps; tok/s = generated / decode wall time, as
@@ -201,8 +207,7 @@ def decode_bench(ctx, model, prompt, new_tokens=128):
         "kernels_per_token": int(st.launches_per_step),
         "prompt_tokens": int(st.prompt_tokens), "generated_tokens": int(st.generated_tokens),
         "first_ids": toks[:8].tolist(),
-        "workload": "qwen2_1p5b_q4_0 random-init (seed 2026), tied F16 LM head, Q8 KV, greedy, "
-                    "HIP graph per token",
+        "workload": workload,
     }
 
 
@@ -467,6 +472,12 @@ def main():
         print(json.dumps({"profile_mode": "decode", **decode_bench(ctx, model, prompt, args.decode_new)}),
               flush=True)
         return
+    if args.profile == "decode-4b":
+        model, prompt = decode_model(seed=2027, prompt_len=args.decode_prompt,
+                                     cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2")
+        print(json.dumps({"profile_mode": "decode-4b",
+                          **decode_bench(ctx, model, prompt, args.decode_new, DECODE_4B)}), flush=True)
+        return
     if args.profile == "attention":
         print(json.dumps({"profile_mode": "attention", **attention_bench(torch, ctx, args.steps)}), flush=True)
         return
@@ -525,6 +536,11 @@ def main():
             if not args.no_cpu:
                 dec["cpu_baseline"] = cpu_decode_baseline(model, prompt)
             extra["decode_qwen2_1p5b_q4_0"] = dec
+            del model
+            # the HyperVSQ-2 GEMV workload's shapes as a dense decoder
+            model, prompt = decode_model(seed=2027, prompt_len=args.decode_prompt,
+                                         cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2")
+            extra["decode_qwen3_4b_shaped_hvsq2"] = decode_bench(ctx, model, prompt, args.decode_new, DECODE_4B)
             del model
         extra["attention_q8_qwen3_4b"] = attention_bench(torch, ctx, args.steps)
         extra["upload_hvsq2_qwen3_4b"] = upload_bench(ctx)

@@ -110,6 +110,13 @@ QWEN2_1P5B_CONFIG = {
     "hidden": 1536, "intermediate": 8960, "layers": 28, "heads": 12, "kv_heads": 2,
     "head_dim": 128, "vocab": 151936, "max_ctx": 512, "rope_theta": 1.0e6, "rms_eps": 1.0e-6,
 }
+# the Qwen3-4B layer shapes of the HyperVSQ-2 GEMV workload as a dense
+# decoder (no q/k norms: the resident decoder serves dense Qwen2-style
+# layers), tied F16 embedding
+QWEN3_4B_SHAPED_CONFIG = {
+    "hidden": 2560, "intermediate": 9728, "layers": 36, "heads": 32, "kv_heads": 8,
+    "head_dim": 128, "vocab": 151936, "max_ctx": 512, "rope_theta": 1.0e6, "rms_eps": 1.0e-6,
+}
 
 
 def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0") -> dict:
