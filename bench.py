@@ -166,20 +166,20 @@ def time_graph(torch, fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def decode_model(seed=2026, prompt_len=32, cfg=None, dtype="q4_0"):
+def decode_model(seed=2026, prompt_len=32, cfg=None, dtype="q4_0", qk_norm=False):
     import numpy as np
 
     from qwanto_amd import synth
     cfg = cfg or synth.QWEN2_1P5B_CONFIG
     rng = np.random.default_rng(seed)
-    model = synth.decoder_model(rng, cfg, dtype)
+    model = synth.decoder_model(rng, cfg, dtype, qk_norm=qk_norm)
     prompt = synth.prompt_tokens(rng, cfg["vocab"], prompt_len)
     return model, prompt
 
 
 DECODE_1P5B = "qwen2_1p5b_q4_0 random-init (seed 2026), tied F16 LM head, Q8 KV, greedy, HIP graph per token"
-DECODE_4B = ("qwen3_4b-shaped hvsq2 dense decoder (no q/k norms), random-init (seed 2027), tied F16 LM head, "
-             "Q8 KV, greedy, HIP graph per token")
+DECODE_4B = ("qwen3_4b-shaped hvsq2 decoder with per-head q/k norms, random-init (seed 2027), tied F16 LM "
+             "head, Q8 KV, greedy, HIP graph per token")
 
 
 def decode_bench(ctx, model, prompt, new_tokens=128, workload=DECODE_1P5B):
@@ -474,7 +474,7 @@ def main():
         return
     if args.profile == "decode-4b":
         model, prompt = decode_model(seed=2027, prompt_len=args.decode_prompt,
-                                     cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2")
+                                     cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2", qk_norm=True)
         print(json.dumps({"profile_mode": "decode-4b",
                           **decode_bench(ctx, model, prompt, args.decode_new, DECODE_4B)}), flush=True)
         return
@@ -539,7 +539,7 @@ def main():
             del model
             # the HyperVSQ-2 GEMV workload's shapes as a dense decoder
             model, prompt = decode_model(seed=2027, prompt_len=args.decode_prompt,
-                                         cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2")
+                                         cfg=synth.QWEN3_4B_SHAPED_CONFIG, dtype="hvsq2", qk_norm=True)
             extra["decode_qwen3_4b_shaped_hvsq2"] = decode_bench(ctx, model, prompt, args.decode_new, DECODE_4B)
             del model
         extra["attention_q8_qwen3_4b"] = attention_bench(torch, ctx, args.steps)

@@ -19,8 +19,9 @@
  * context (qwn_cuda_abi_upload_tensor): seven projections per layer
  * (HyperVSQ-2 or Q4_0, one dtype per decoder) and the F16 embedding, which
  * is also the tied LM head.  Norm weights are copied from the host at
- * creation.  Biases and q/k norms are not supported (the configurations
- * this decoder serves have none).
+ * creation, and so are the optional per-head q/k norm weights of Qwen3
+ * layers.  Biases are not supported (the configurations this decoder
+ * serves have none).
  */
 
 #include "qwn_cuda_abi.h"
@@ -46,6 +47,10 @@ typedef struct {
     const float *input_norms;               /* host [layers][hidden] */
     const float *post_norms;                /* host [layers][hidden] */
     const float *final_norm;                /* host [hidden] */
+    const float *q_norms;                   /* NULL, or host [layers][head_dim]: Qwen3 per-head q norm */
+    const float *k_norms;                   /* NULL, or host [layers][head_dim]: Qwen3 per-head k norm
+                                               (self_attn.q_norm / k_norm, c/qwanto_decode.c:975-976,
+                                               1652-1655; both or neither) */
 } QwnHipDecoderDesc;
 
 typedef struct {

@@ -45,7 +45,8 @@ class QoModelConfig(ctypes.Structure):
 
 class QoModel(ctypes.Structure):
     _fields_ = [("cfg", QoModelConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
-                ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p))]
+                ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p)),
+                ("qk_norms", ctypes.POINTER(ctypes.c_void_p))]
 
 
 PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
@@ -64,10 +65,15 @@ def model_struct(model: dict) -> tuple:
                                          for l in range(L) for p in PROJ_ORDER])
     norms = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data
                                           for l in range(L) for n in ("input_norm", "post_norm")])
+    qk = None
+    if "q_norm" in model["layers"][0]:
+        qk = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data
+                                           for l in range(L) for n in ("q_norm", "k_norm")])
     m = QoModel(cfg=c, embed=model["embed"].ctypes.data, final_norm=model["final_norm"].ctypes.data,
                 proj=ctypes.cast(proj, ctypes.POINTER(ctypes.c_void_p)),
-                norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)))
-    return m, (proj, norms)
+                norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)),
+                qk_norms=ctypes.cast(qk, ctypes.POINTER(ctypes.c_void_p)) if qk is not None else None)
+    return m, (proj, norms, qk)
 
 
 class Decoder:

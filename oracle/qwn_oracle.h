@@ -137,6 +137,8 @@ typedef struct {
     const float *final_norm;        /* [hidden] */
     const uint8_t *const *proj;     /* [layers * 7]: q k v o gate up down blocks */
     const float *const *norms;      /* [layers * 2]: input, post attention */
+    const float *const *qk_norms;   /* NULL, or [layers * 2]: per-head q and k norm weights
+                                       [head_dim] (Qwen3 self_attn.q_norm / k_norm) */
 } qo_model;
 
 typedef struct qo_decoder qo_decoder;

@@ -148,6 +148,15 @@ int qo_decoder_forward(qo_decoder *d, int token, float *logits_out) {
         if (matmul(d, w[0], d->xb, D, Q, d->q) || matmul(d, w[1], d->xb, D, KV, d->k) ||
             matmul(d, w[2], d->xb, D, KV, d->v))
             return -1;
+        if (d->m.qk_norms) {
+            /* head_rmsnorm (c/qwanto_decode.c:654-684, 1652-1655): per head, in place,
+             * the same arithmetic as rmsnorm */
+            for (int h = 0; h < H; h++)
+                qo_rmsnorm(d->q + (size_t)h * HD, d->q + (size_t)h * HD, d->m.qk_norms[2 * l], HD, c->rms_eps);
+            for (int h = 0; h < HK; h++)
+                qo_rmsnorm(d->k + (size_t)h * HD, d->k + (size_t)h * HD, d->m.qk_norms[2 * l + 1], HD,
+                           c->rms_eps);
+        }
         qo_rope_apply(d->q, H, HD, ct, st);
         qo_rope_apply(d->k, HK, HD, ct, st);
         qo_q8_quantize_vector(d->k, d->kcache[l] + (size_t)pos * KV, d->kscale[l] + (size_t)pos * groups, KV);

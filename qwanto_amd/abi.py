@@ -181,7 +181,7 @@ class DecoderDesc(_Versioned):
                [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
                 ("projections", ctypes.c_void_p), ("embedding", ctypes.c_void_p),
                 ("input_norms", ctypes.c_void_p), ("post_norms", ctypes.c_void_p),
-                ("final_norm", ctypes.c_void_p)]
+                ("final_norm", ctypes.c_void_p), ("q_norms", ctypes.c_void_p), ("k_norms", ctypes.c_void_p)]
 
 
 class DecoderStats(_Versioned):
@@ -607,12 +607,19 @@ class ResidentDecoder:
         self._norm_post = np.ascontiguousarray(np.stack([model["layers"][l]["post_norm"] for l in range(L)]),
                                                dtype=np.float32)
         self._final = np.ascontiguousarray(model["final_norm"], dtype=np.float32)
+        self._qn = self._kn = None
+        if "q_norm" in model["layers"][0]:
+            self._qn = np.ascontiguousarray(np.stack([model["layers"][l]["q_norm"] for l in range(L)]),
+                                            dtype=np.float32)
+            self._kn = np.ascontiguousarray(np.stack([model["layers"][l]["k_norm"] for l in range(L)]),
+                                            dtype=np.float32)
         desc = DecoderDesc(hidden=D, intermediate=I, layers=L, heads=cfg["heads"], kv_heads=cfg["kv_heads"],
                            head_dim=cfg["head_dim"], vocab=cfg["vocab"], max_ctx=cfg["max_ctx"],
                            rope_theta=cfg["rope_theta"], rms_eps=cfg["rms_eps"],
                            projections=ctypes.cast(self._proj_arr, ctypes.c_void_p).value,
                            embedding=ctypes.addressof(self._embed), input_norms=_p(self._norm_in),
-                           post_norms=_p(self._norm_post), final_norm=_p(self._final))
+                           post_norms=_p(self._norm_post), final_norm=_p(self._final),
+                           q_norms=_p(self._qn), k_norms=_p(self._kn))
         self.handle = Handle()
         lib = ctx.lib
         lib.check("decoder_create", lib.lib.qwn_hip_decoder_create(ctx._h, ctypes.byref(desc),

@@ -342,8 +342,10 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
                                                            const float *__restrict__ cos_tab,
                                                            const float *__restrict__ sin_tab,
                                                            const int32_t *__restrict__ pos_ptr, uint32_t q_stride,
-                                                           uint32_t kv_stride) {
+                                                           uint32_t kv_stride, const float *__restrict__ q_norm,
+                                                           const float *__restrict__ k_norm, float eps) {
     extern __shared__ float kr[];  // [channels] rotated key
+    __shared__ float inv_s[kMaxNormHeads];
     q += static_cast<size_t>(blockIdx.x) * q_stride;
     k += static_cast<size_t>(blockIdx.x) * kv_stride;
     v += static_cast<size_t>(blockIdx.x) * kv_stride;
@@ -352,16 +354,38 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
     const uint32_t row = pos < c.max_tokens ? pos : 0;
     const float *ct = cos_tab + static_cast<size_t>(row) * half;
     const float *st = sin_tab + static_cast<size_t>(row) * half;
+    // per-head q/k RMSNorm ahead of the rotation (c/qwanto_decode.c:654-684,
+    // 1652-1655): one wave per head for its 1/rms, applied as (x * inv) * w
+    const bool qk = q_norm != nullptr;
+    if (qk) {
+        const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, nwaves = blockDim.x / 64;
+        for (uint32_t hh = wave; hh < q_heads + c.kv_heads; hh += nwaves) {
+            const float *x = hh < q_heads ? q + static_cast<size_t>(hh) * D : k + static_cast<size_t>(hh - q_heads) * D;
+            float ss = 0.0f;
+            for (uint32_t d = lane; d < D; d += 64) ss = fmaf(x[d], x[d], ss);
+            ss = wave_sum_all(ss);
+            if (lane == 0) inv_s[hh] = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+        }
+        __syncthreads();
+    }
     for (uint32_t p = threadIdx.x; p < q_heads * half; p += blockDim.x) {
         const uint32_t h = p / half, i = p % half;
         float *r = q + static_cast<size_t>(h) * D;
-        const float a = r[i], b = r[i + half];
+        float a = r[i], b = r[i + half];
+        if (qk) {
+            a = (a * inv_s[h]) * q_norm[i];
+            b = (b * inv_s[h]) * q_norm[i + half];
+        }
         r[i] = fmaf(a, ct[i], -(b * st[i]));
         r[i + half] = fmaf(a, st[i], b * ct[i]);
     }
     for (uint32_t p = threadIdx.x; p < c.kv_heads * half; p += blockDim.x) {
         const uint32_t h = p / half, i = p % half;
-        const float a = k[h * D + i], b = k[h * D + i + half];
+        float a = k[h * D + i], b = k[h * D + i + half];
+        if (qk) {
+            a = (a * inv_s[q_heads + h]) * k_norm[i];
+            b = (b * inv_s[q_heads + h]) * k_norm[i + half];
+        }
         kr[h * D + i] = fmaf(a, ct[i], -(b * st[i]));
         kr[h * D + i + half] = fmaf(a, st[i], b * ct[i]);
     }
@@ -431,11 +455,22 @@ struct DecodeAttnArgs {
     uint32_t rope_row_only;
     uint32_t token_stride;   // floats between the query (and output) rows of a token block
     uint32_t count;          // query tokens (grid z)
+    const float *q_norm;     // decode mode, optional: per-head q/k RMSNorm weights [head_dim]
+    const float *k_norm;
+    float eps;
 };
 
 __device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *ct, const float *st) {
     const uint32_t i = d < half ? d : d - half;
     const float a = x[i], b = x[i + half];
+    return d < half ? fmaf(a, ct[i], -(b * st[i])) : fmaf(a, st[i], b * ct[i]);
+}
+
+// The same after a per-head RMSNorm, (x * inv) * w (c/qwanto_decode.c:654-684).
+__device__ __forceinline__ float rope_norm_at(const float *x, uint32_t d, uint32_t half, const float *ct,
+                                              const float *st, float inv, const float *w) {
+    const uint32_t i = d < half ? d : d - half;
+    const float a = (x[i] * inv) * w[i], b = (x[i + half] * inv) * w[i + half];
     return d < half ? fmaf(a, ct[i], -(b * st[i])) : fmaf(a, st[i], b * ct[i]);
 }
 
@@ -525,13 +560,30 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
     const float *ct = rope ? a.cos_tab + rope_off : nullptr;
     const float *st = rope ? a.sin_tab + rope_off : nullptr;
 
+    // 0. decode mode with q/k norms: 1/rms of each query head and of the
+    //    current key head, one wave each
+    __shared__ float inv_s[GMAX + 1];
+    const bool qk = rope && a.q_norm != nullptr;
+    if (qk) {
+        for (uint32_t hh = wave; hh < G + (cur ? 1u : 0u); hh += 4) {
+            const float *x = hh < G ? query + static_cast<size_t>(h0 + hh) * D : a.key + static_cast<size_t>(kvh) * D;
+            float ss = 0.0f;
+#pragma unroll
+            for (uint32_t d = lane; d < static_cast<uint32_t>(D); d += 64) ss = fmaf(x[d], x[d], ss);
+            ss = wave_sum_all(ss);
+            if (lane == 0) inv_s[hh < G ? hh : GMAX] = 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps);
+        }
+        __syncthreads();
+    }
+
     // 1. query heads of this KV head (rotated in decode mode) -> LDS
     for (uint32_t i = tid; i < GMAX * D; i += blockDim.x) {
         const uint32_t g = i / D, d = i % D;
         float v = 0.0f;
         if (g < G) {
             const float *qh = query + static_cast<size_t>(h0 + g) * D;
-            v = rope ? rope_at(qh, d, half, ct, st) : qh[d];
+            v = qk ? rope_norm_at(qh, d, half, ct, st, inv_s[g], a.q_norm)
+                   : rope ? rope_at(qh, d, half, ct, st) : qh[d];
         }
         q_s[i] = v;
     }
@@ -542,7 +594,9 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             const uint32_t grp = is_v ? gi - NG : gi;
             const uint32_t d = grp * 64 + lane;
             const float *src = (is_v ? a.value : a.key) + static_cast<size_t>(kvh) * D;
-            const float x = is_v ? src[d] : rope_at(src, d, half, ct, st);
+            const float x = is_v ? src[d]
+                                 : qk ? rope_norm_at(src, d, half, ct, st, inv_s[GMAX], a.k_norm)
+                                      : rope_at(src, d, half, ct, st);
             const float amax = wave_max_all(isfinite(x) ? fabsf(x) : 0.0f);
             const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
             const int8_t qv = q8_of(x, scale);
@@ -1171,10 +1225,14 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base) {
 
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
-                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count) {
-    if (c.head_dim % 2 || c.channels > 8192 || count == 0) return hipErrorInvalidValue;
+                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count, const float *q_norm,
+                              const float *k_norm, float eps) {
+    if (c.head_dim % 2 || c.channels > 8192 || count == 0 || (!q_norm) != (!k_norm) ||
+        (q_norm && query_heads + c.kv_heads > static_cast<uint32_t>(kMaxNormHeads)))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_append_kernel, dim3(count), dim3(1024), c.channels * sizeof(float), stream, c, query,
-                       query_heads, key, value, cos_tab, sin_tab, pos_ptr, query_heads * c.head_dim, c.channels);
+                       query_heads, key, value, cos_tab, sin_tab, pos_ptr, query_heads * c.head_dim, c.channels,
+                       q_norm, k_norm, eps);
     return hipGetLastError();
 }
 
@@ -1287,6 +1345,10 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.rope_row_only = l.rope_row_only ? 1u : 0u;
     args.count = l.count;
     args.token_stride = l.query_heads * c.head_dim;
+    if ((!l.q_norm) != (!l.k_norm) || (l.q_norm && !l.key)) return hipErrorInvalidValue;
+    args.q_norm = l.q_norm;
+    args.k_norm = l.k_norm;
+    args.eps = l.eps;
     return launch_decode_attention_args(args, l.output, stream);
 }
 

@@ -149,6 +149,7 @@ struct Decoder {
           *up = nullptr, *logits = nullptr, *partials = nullptr;
     float *norms_in = nullptr, *norms_post = nullptr, *final_norm = nullptr, *cos_tab = nullptr,
           *sin_tab = nullptr, *rope_row = nullptr;
+    float *q_norms = nullptr, *k_norms = nullptr;  // [layers][head_dim] or null
     uint64_t *argmax = nullptr;
     uint32_t argmax_n = 0;
     uint8_t *head_image = nullptr;  // fp32 image of the final-norm output
@@ -295,10 +296,12 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
         const DeviceTensor *const *w = d->proj.data() + static_cast<size_t>(l) * kProj;
         const float *nin = d->norms_in + static_cast<size_t>(l) * D;
         const float *npost = d->norms_post + static_cast<size_t>(l) * D;
+        const float *qn = d->q_norms ? d->q_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
+        const float *kn = d->k_norms ? d->k_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
         if ((e = project({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}, kInNorm, d->px, nullptr, nin, D,
                          false)) != hipSuccess ||
             (e = launch_rope_append(d->caches[l], d->pq, d->heads, d->pk, d->pv, d->cos_tab, d->sin_tab, d->ppos, s,
-                                    m)) != hipSuccess)
+                                    m, qn, kn, d->eps)) != hipSuccess)
             return e;
         if (d->fused_attention) {
             DecodeAttentionLaunch at;
@@ -342,6 +345,8 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
     int32_t *pos = d->state + 1;
     for (uint32_t l = 0; l < d->layers; ++l) {
         const DeviceTensor *const *w = d->proj.data() + static_cast<size_t>(l) * kProj;
+        const float *qn = d->q_norms ? d->q_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
+        const float *kn = d->k_norms ? d->k_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
         GemvGroupLaunch qkv = group({w[P_Q], w[P_K], w[P_V]}, {d->q, d->k, d->v});
         qkv.input_mode = kInNorm;
         qkv.x = d->x;
@@ -363,10 +368,13 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
             at.cos_tab = d->rope_row;
             at.sin_tab = d->rope_row + d->head_dim / 2;
             at.rope_row_only = true;
+            at.q_norm = qn;
+            at.k_norm = kn;
+            at.eps = d->eps;
             if ((e = launch_decode_attention(at, s)) != hipSuccess) return e;
         } else {
-            if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s)) !=
-                hipSuccess)
+            if ((e = launch_rope_append(d->caches[l], d->q, d->heads, d->k, d->v, d->cos_tab, d->sin_tab, pos, s, 1,
+                                        qn, kn, d->eps)) != hipSuccess)
                 return e;
             if ((e = launch_attention_at(d->caches[l], d->q, d->attn, d->heads, pos, d->attn_scale, d->partials,
                                          s)) != hipSuccess)
@@ -482,7 +490,8 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         !desc->embedding || !desc->input_norms || !desc->post_norms || !desc->final_norm || desc->hidden == 0 ||
         desc->layers == 0 || desc->heads == 0 || desc->kv_heads == 0 || desc->heads % desc->kv_heads ||
         desc->head_dim == 0 || desc->head_dim % 2 || desc->vocab == 0 || desc->max_ctx == 0 ||
-        desc->intermediate == 0) {
+        desc->intermediate == 0 || (!desc->q_norms) != (!desc->k_norms) ||
+        (desc->q_norms && desc->heads + desc->kv_heads > static_cast<uint32_t>(kMaxNormHeads))) {
         set_error("invalid decoder description");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
@@ -537,6 +546,10 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     part(reinterpret_cast<void **>(&d->norms_in), static_cast<size_t>(d->layers) * D * 4);
     part(reinterpret_cast<void **>(&d->norms_post), static_cast<size_t>(d->layers) * D * 4);
     part(reinterpret_cast<void **>(&d->final_norm), D * 4);
+    if (desc->q_norms) {
+        part(reinterpret_cast<void **>(&d->q_norms), static_cast<size_t>(d->layers) * d->head_dim * 4);
+        part(reinterpret_cast<void **>(&d->k_norms), static_cast<size_t>(d->layers) * d->head_dim * 4);
+    }
     const uint32_t half = d->head_dim / 2;
     part(reinterpret_cast<void **>(&d->cos_tab), static_cast<size_t>(d->max_ctx) * half * 4);
     part(reinterpret_cast<void **>(&d->sin_tab), static_cast<size_t>(d->max_ctx) * half * 4);
@@ -663,6 +676,12 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         e = hipMemcpyAsync(d->norms_post, desc->post_norms, static_cast<size_t>(d->layers) * D * 4,
                            hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->final_norm, desc->final_norm, D * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && desc->q_norms)
+        e = hipMemcpyAsync(d->q_norms, desc->q_norms, static_cast<size_t>(d->layers) * d->head_dim * 4,
+                           hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && desc->k_norms)
+        e = hipMemcpyAsync(d->k_norms, desc->k_norms, static_cast<size_t>(d->layers) * d->head_dim * 4,
+                           hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->feed, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, s);

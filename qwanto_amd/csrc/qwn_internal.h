@@ -237,9 +237,14 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base);
 // slot *pos_ptr (one workgroup per token; cos/sin tables
 // [max_tokens][head_dim/2]).  count > 1: a block of tokens, q/key/value
 // [count][...] back to back, token i at slot pos_ptr[i].
+// q_norm/k_norm (both or neither, [head_dim]): per-head RMSNorm with eps
+// before the rotation (Qwen3, c/qwanto_decode.c:654-684), at most
+// kMaxNormHeads query + KV heads.
+constexpr int kMaxNormHeads = 128;
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
-                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count = 1);
+                              const int32_t *pos_ptr, hipStream_t stream, uint32_t count = 1,
+                              const float *q_norm = nullptr, const float *k_norm = nullptr, float eps = 0.0f);
 
 // Quantize one token's fp32 K and V [channels] into slot `token`.
 hipError_t launch_kv_append(const KvCache &c, const float *key,
@@ -286,6 +291,9 @@ struct DecodeAttentionLaunch {
     uint32_t count = 1;               // > 1: a block of query tokens (no key/value): query and
                                       // output [count][query_heads][head_dim], positions
                                       // position_ptr[count], one split
+    const float *q_norm = nullptr;    // with key: per-head q/k RMSNorm weights [head_dim]
+    const float *k_norm = nullptr;    // before RoPE (both or neither)
+    float eps = 0.0f;
 };
 // int8 MFMA attention (no RoPE/append) over span tokens of the cache: the
 // position from position_ptr when non-null; partials of

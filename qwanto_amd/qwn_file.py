@@ -226,6 +226,9 @@ def write_decoder_model(path: str, model: dict) -> int:
         pre = f"model.layers.{l}."
         tensors.append((pre + "input_layernorm.weight", DT_F32, (D,), layer["input_norm"]))
         tensors.append((pre + "post_attention_layernorm.weight", DT_F32, (D,), layer["post_norm"]))
+        if "q_norm" in layer:  # Qwen3 per-head q/k norms (c/qwanto_decode.c:975-976)
+            tensors.append((pre + "self_attn.q_norm.weight", DT_F32, (cfg["head_dim"],), layer["q_norm"]))
+            tensors.append((pre + "self_attn.k_norm.weight", DT_F32, (cfg["head_dim"],), layer["k_norm"]))
         for p, suffix in _PROJ_NAMES.items():
             out, inp = model["shapes"][p]
             tensors.append((pre + suffix, qdt, (inp, out), layer[p]))
@@ -251,6 +254,9 @@ def read_decoder_model(path: str) -> dict:
         pre = f"model.layers.{l}."
         layer = {"input_norm": f.array(pre + "input_layernorm.weight"),
                  "post_norm": f.array(pre + "post_attention_layernorm.weight")}
+        if pre + "self_attn.q_norm.weight" in f.tensors:
+            layer["q_norm"] = f.array(pre + "self_attn.q_norm.weight")
+            layer["k_norm"] = f.array(pre + "self_attn.k_norm.weight")
         for p, suffix in _PROJ_NAMES.items():
             t = f.tensors[pre + suffix]
             dtype = "q4_0" if t["dtype"] == DT_Q4_0 else "hvsq2"

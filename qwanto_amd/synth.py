@@ -110,20 +110,22 @@ QWEN2_1P5B_CONFIG = {
     "hidden": 1536, "intermediate": 8960, "layers": 28, "heads": 12, "kv_heads": 2,
     "head_dim": 128, "vocab": 151936, "max_ctx": 512, "rope_theta": 1.0e6, "rms_eps": 1.0e-6,
 }
-# the Qwen3-4B layer shapes of the HyperVSQ-2 GEMV workload as a dense
-# decoder (no q/k norms: the resident decoder serves dense Qwen2-style
-# layers), tied F16 embedding
+# the Qwen3-4B layer shapes of the HyperVSQ-2 GEMV workload as a decoder
+# (per-head q/k norms with decoder_model(..., qk_norm=True)), tied F16
+# embedding
 QWEN3_4B_SHAPED_CONFIG = {
     "hidden": 2560, "intermediate": 9728, "layers": 36, "heads": 32, "kv_heads": 8,
     "head_dim": 128, "vocab": 151936, "max_ctx": 512, "rope_theta": 1.0e6, "rms_eps": 1.0e-6,
 }
 
 
-def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0") -> dict:
+def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_norm: bool = False) -> dict:
     """Random decoder weights with the layout of a .qwn dense model: per layer
     q, k, v, o, gate, up, down quantized matrices ([out][in] row-major
-    blocks), input/post norm vectors; a tied F16 embedding [vocab][hidden]
-    and the final norm."""
+    blocks), input/post norm vectors (and, with qk_norm, per-head q/k norm
+    weights [head_dim] as Qwen3's self_attn.q_norm / k_norm, drawn
+    1 + 0.2 N(0,1)); a tied F16 embedding [vocab][hidden] and the final
+    norm."""
     D, I = cfg["hidden"], cfg["intermediate"]
     Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
     shapes = {"q": (Q, D), "k": (KV, D), "v": (KV, D), "o": (D, Q),
@@ -133,6 +135,9 @@ def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0") -> d
         layer = {p: weights(dtype, rng, *shapes[p]) for p in PROJECTIONS}
         layer["input_norm"] = np.ones(D, dtype=np.float32)
         layer["post_norm"] = np.ones(D, dtype=np.float32)
+        if qk_norm:
+            for n in ("q_norm", "k_norm"):
+                layer[n] = (1.0 + 0.2 * rng.standard_normal(cfg["head_dim"])).astype(np.float32)
         layers.append(layer)
     embed = f16_weights(rng, cfg["vocab"], D)
     return {"cfg": dict(cfg), "dtype": dtype, "shapes": shapes, "layers": layers,

@@ -25,11 +25,14 @@ def ref_decoder_or_skip(path, ctx):
     return oracle.load_ref_decoder(path, ctx)
 
 
-@pytest.mark.parametrize("cfg,dtype,steps", [(SMALL, "q4_0", 12), (SMALL, "hvsq2", 8),
-                                             (QWEN2_LIKE, "q4_0", 10)])
-def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dtype, steps):
+@pytest.mark.parametrize("cfg,dtype,steps,qk", [(SMALL, "q4_0", 12, False), (SMALL, "hvsq2", 8, False),
+                                                (QWEN2_LIKE, "q4_0", 10, False), (SMALL, "hvsq2", 8, True),
+                                                (QWEN2_LIKE, "q4_0", 10, True)])
+def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dtype, steps, qk):
+    """qk: Qwen3-style per-head q/k RMSNorm weights in the file
+    (self_attn.q_norm / k_norm, c/qwanto_decode.c:975-976, 1652-1655)."""
     rng = np.random.default_rng(11)
-    model = synth.decoder_model(rng, cfg, dtype)
+    model = synth.decoder_model(rng, cfg, dtype, qk_norm=qk)
     path = str(tmp_path / "m.qwn")
     qwn_file.write_decoder_model(path, model)
     ref = ref_decoder_or_skip(path, cfg["max_ctx"])

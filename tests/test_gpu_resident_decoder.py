@@ -45,11 +45,17 @@ def with_norms(rng, model):
 LONG_CTX = dict(SMALL, max_ctx=1500)
 
 
-@pytest.mark.parametrize("cfg,dtype", [(SMALL, "q4_0"), (SMALL, "hvsq2"), (QWEN2_LIKE, "q4_0"),
-                                       (QWEN2_LIKE, "hvsq2"), (LONG_CTX, "q4_0")])
-def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype):
+@pytest.mark.parametrize("cfg,dtype,qk", [(SMALL, "q4_0", False), (SMALL, "hvsq2", False),
+                                          (QWEN2_LIKE, "q4_0", False), (QWEN2_LIKE, "hvsq2", False),
+                                          (LONG_CTX, "q4_0", False), (SMALL, "hvsq2", True),
+                                          (QWEN2_LIKE, "q4_0", True), (LONG_CTX, "hvsq2", True)])
+def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype, qk):
+    """qk: Qwen3-style per-head q/k RMSNorm before RoPE (the oracle's is
+    bit-identical to the reference decoder's, test_decoder_oracle.py); in
+    the fused decode attention kernel, and for LONG_CTX in the RoPE/append
+    kernel."""
     rng = np.random.default_rng(31)
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk))
     dec = abi.ResidentDecoder(gpu_ctx, model)
     ref = oracle_lib.decoder(model)
     try:
@@ -78,10 +84,12 @@ def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype):
 PREFILL_ORACLE_RTOL = 2e-2  # gross errors (positions, causal mask, cache layout) move logits by O(1)
 
 
-@pytest.mark.parametrize("cfg,dtype,P", [(SMALL, "q4_0", 21), (SMALL, "hvsq2", 16), (QWEN2_LIKE, "q4_0", 37),
-                                         (QWEN2_LIKE, "hvsq2", 37),
-                                         (QWEN2_LIKE, "hvsq2", 5), (LONG_CTX, "q4_0", 18), (SMALL, "q4_0", 1)])
-def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P):
+@pytest.mark.parametrize("cfg,dtype,P,qk", [(SMALL, "q4_0", 21, False), (SMALL, "hvsq2", 16, False),
+                                            (QWEN2_LIKE, "q4_0", 37, False), (QWEN2_LIKE, "hvsq2", 37, False),
+                                            (QWEN2_LIKE, "hvsq2", 5, False), (LONG_CTX, "q4_0", 18, False),
+                                            (SMALL, "q4_0", 1, False), (QWEN2_LIKE, "hvsq2", 20, True),
+                                            (LONG_CTX, "q4_0", 18, True)])
+def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk):
     """qwn_hip_decoder_prefill (prompt blocks of up to 16 tokens through the
     batched GEMV, block RoPE/append, causal attention per token; the
     split-attention path for LONG_CTX): the last prompt token's logits and
@@ -98,7 +106,7 @@ def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P)
     with or without prefill), so this bound only has to separate such flips
     from wrong positions, masks or cache slots."""
     rng = np.random.default_rng(77 + P)
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk))
     prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
     dec = abi.ResidentDecoder(gpu_ctx, model)
     ref = oracle_lib.decoder(model)
