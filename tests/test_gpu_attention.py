@@ -111,3 +111,35 @@ def test_append_contract(gpu_ctx):
     with pytest.raises(abi.AbiError):       # wrong channel count
         gpu_ctx.kv_append(h, np.zeros(9, np.float32), np.zeros(9, np.float32), 2)
     gpu_ctx.kv_destroy(h)
+
+
+def test_device_attention_reused_workspace(gpu_ctx, oracle_lib):
+    """qwn_hip_ext_kv_attention_device over many splits, several calls in a
+    row on one workspace (varying positions, so the number of splits and the
+    partials' layout vary too): each output against the oracle."""
+    import torch
+    rng = np.random.default_rng(21)
+    T, H, HK, D = 9000, 32, 8, 128
+    k = rng.standard_normal((T, HK * D), dtype=np.float32)
+    v = rng.standard_normal((T, HK * D), dtype=np.float32)
+    dev = torch.device("cuda:0")
+    h = gpu_ctx.kv_create(T, HK, D)
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        kd, vd = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+        gpu_ctx.kv_append_device(h, kd.data_ptr(), vd.data_ptr(), T, stream=s)
+        work = torch.zeros(gpu_ctx.attention_workspace_bytes(h, H, T - 1) // 4 + 1, device=dev)
+        kq, ks = oracle_lib.q8_quantize(k)
+        vq, vs = oracle_lib.q8_quantize(v)
+        for pos in (T - 1, 4095, 700, T - 1, 2500):
+            q = rng.standard_normal(H * D, dtype=np.float32)
+            qd = torch.from_numpy(q).to(dev)
+            out = torch.full((H * D,), float("nan"), device=dev)
+            gpu_ctx.kv_attention_device(h, qd.data_ptr(), out.data_ptr(), H, pos, float(D ** -0.5),
+                                        work.data_ptr(), stream=s)
+            torch.cuda.synchronize()
+            ref = oracle_lib.q8_attention(q, kq, vq, ks, vs, H, HK, D, pos, np.float32(D ** -0.5))
+            err = float(np.max(np.abs(out.cpu().numpy() - ref)))
+            assert err <= ATTN_ATOL, f"pos {pos}: max abs err {err:.3g}"
+    finally:
+        gpu_ctx.kv_destroy(h)
