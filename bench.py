@@ -280,11 +280,11 @@ def attention_bench(torch, ctx, steps=50):
 
 
 class MfmaSweep:
-    """Resident HyperVSQ-2 tensors of `layers` layers with MFMA images of M
-    tokens (8..16): int8-MFMA GEMM launches grouped as the decoder groups its
-    GEMVs (q/k/v, o, gate/up, down: four per layer)."""
+    """Resident HyperVSQ-2 or Q4_0 tensors of `layers` layers with MFMA
+    images of M tokens (8..16): int8-MFMA GEMM launches grouped as the
+    decoder groups its GEMVs (q/k/v, o, gate/up, down: four per layer)."""
 
-    def __init__(self, torch, ctx, shapes, layers, seed, batch):
+    def __init__(self, torch, ctx, shapes, layers, seed, batch, kind="hvsq2"):
         import numpy as np
 
         from qwanto_amd import synth
@@ -296,7 +296,7 @@ class MfmaSweep:
         self.items, self.handles = [], []
         self.weight_bytes = 0
         for _ in range(layers):
-            layer = {p: ctx.upload(synth.hvsq2_weights(rng, *shapes[p]), "hvsq2", *shapes[p])
+            layer = {p: ctx.upload(synth.weights(kind, rng, *shapes[p]), kind, *shapes[p])
                      for p in synth.PROJECTIONS}
             self.handles += list(layer.values())
             for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")),
@@ -311,7 +311,7 @@ class MfmaSweep:
                 ctx.mfma_image_device(h0, q8.data_ptr(), batch, q8.shape[1], img.data_ptr(), stream=s)
                 outs = [torch.zeros(batch, shapes[p][0], device=dev) for p in projs]
                 self.items.append(([layer[p] for p in projs], img, sc, outs))
-                self.weight_bytes += sum(synth.weight_bytes("hvsq2", *shapes[p]) for p in projs)
+                self.weight_bytes += sum(synth.weight_bytes(kind, *shapes[p]) for p in projs)
         torch.cuda.synchronize()
         self.flops = 2 * batch * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * layers
 
@@ -361,30 +361,39 @@ def upload_bench(ctx, layers=36, seed=3):
 
 
 def batch_sweep(torch, ctx, steps, warmup):
-    """HyperVSQ-2 GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers
-    of the Qwen3-4B shapes (weights read once per launch): dot8 grouped
-    launches below 8 tokens, grouped int8-MFMA launches from 8 up
-    (MFMA utilisation = useful int8 ops / dense int8 peak)."""
+    """GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers (weights
+    read once per launch): HyperVSQ-2 on the Qwen3-4B shapes (36 layers per
+    token in tokens_per_s), and under "q4_0" Q4_0 on the Qwen2-1.5B shapes
+    (28 layers); dot8 grouped launches below 8 tokens (Q4_0: 16), grouped
+    int8-MFMA launches from there (MFMA utilisation = useful int8 ops /
+    dense int8 peak)."""
     from qwanto_amd import synth
-    out = {}
-    for M in (1, 2, 4, 8, 16):
-        if M < 8:
-            sw = Sweep(torch, ctx, "hvsq2", synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
-            ms = time_graph(torch, sw.grouped, steps, warmup)
-            path = "dot8"
-            flops = 2 * M * sum(n * k for n, k in synth.QWEN3_4B_SHAPES.values()) * 4
-        else:
-            sw = MfmaSweep(torch, ctx, synth.QWEN3_4B_SHAPES, 4, seed=50 + M, batch=M)
-            ms = time_graph(torch, sw.run, steps, warmup)
-            path = "mfma-i8"
-            flops = sw.flops
-        tops = flops / (ms / 1e3) / 1e12
-        out[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
-                       "us_per_layer": round(ms * 1e3 / 4, 3),
-                       "tokens_per_s": round(M * 4 / (ms / 1e3) / 36, 1),
-                       "path": path, "int8_tops": round(tops, 2),
-                       "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5) if M >= 8 else None}
-        sw.close()
+
+    def sweep(kind, shapes, model_layers, seed0):
+        res = {}
+        for M in (1, 2, 4, 8, 16):
+            mfma = M >= (16 if kind == "q4_0" else 8)    # the library's own choice
+            if not mfma:
+                sw = Sweep(torch, ctx, kind, shapes, 4, seed=seed0 + M, batch=M)
+                ms = time_graph(torch, sw.grouped, steps, warmup)
+                path = "dot8"
+                flops = 2 * M * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * 4
+            else:
+                sw = MfmaSweep(torch, ctx, shapes, 4, seed=seed0 + M, batch=M, kind=kind)
+                ms = time_graph(torch, sw.run, steps, warmup)
+                path = "mfma-i8"
+                flops = sw.flops
+            tops = flops / (ms / 1e3) / 1e12
+            res[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
+                           "us_per_layer": round(ms * 1e3 / 4, 3),
+                           "tokens_per_s": round(M * 4 / (ms / 1e3) / model_layers, 1),
+                           "path": path, "int8_tops": round(tops, 2),
+                           "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5) if mfma else None}
+            sw.close()
+        return res
+
+    out = sweep("hvsq2", synth.QWEN3_4B_SHAPES, 36, 50)
+    out["q4_0"] = sweep("q4_0", synth.QWEN2_1P5B_SHAPES, 28, 70)
     return out
 
 

@@ -164,10 +164,8 @@ struct Decoder {
           *pup = nullptr, *pscales = nullptr;
     uint8_t *pimg = nullptr;
     uint32_t pimg_stride = 0;
-    // HyperVSQ-2 blocks of kMfmaMinTokens or more go through the int8 MFMA
-    // GEMM: int8 tokens [16][pq8_stride] and one MFMA image
-    int8_t *pq8 = nullptr;
-    uint32_t pq8_stride = 0;
+    // blocks that mfma_batch() sends through the int8 MFMA GEMM: the MFMA
+    // image of the widest input, written by the quantize step
     uint8_t *pmimg = nullptr;
     int32_t *ppos = nullptr;
     hipGraphExec_t prefill_exec[kPrefillTokens + 1][2] = {};
@@ -259,9 +257,9 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
     const uint32_t D = d->hidden, Q = d->heads * d->head_dim, I = d->inter;
     // one projection group of the block: its input prepared per token
     // (mode: fp32 / RMSNorm / SwiGLU of x), then the batched dot8 GEMV on
-    // activation images, or for HyperVSQ-2 from kMfmaMinTokens tokens the
-    // int8 MFMA GEMM on the MFMA image; add: residual stream
-    const bool mfma = d->pq8 && m >= kMfmaMinTokens;
+    // activation images, or where mfma_batch() says so the int8 MFMA GEMM
+    // on the MFMA image; add: residual stream
+    const bool mfma = d->pmimg && mfma_batch(d->proj[P_Q]->kind, m);
     auto project = [&](std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs,
                        uint32_t mode, const float *x, const float *x2, const float *norm, uint32_t x_stride,
                        bool add) {
@@ -269,8 +267,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
         hipError_t e2;
         if (mfma) {
             if ((e2 = launch_prepare_image(t0, mode, x, x2, norm, d->eps, m, x_stride, nullptr, 0, d->pscales,
-                                           d->pq8, d->pq8_stride, s)) != hipSuccess ||
-                (e2 = launch_mfma_image(t0, d->pq8, m, d->pq8_stride, d->pmimg, s)) != hipSuccess)
+                                           nullptr, 0, s, d->pmimg)) != hipSuccess)
                 return e2;
             const DeviceTensor *tv[kMaxGroup];
             float *ov[kMaxGroup];
@@ -570,20 +567,13 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         part(reinterpret_cast<void **>(&d->pscales), P * 4);
         part(reinterpret_cast<void **>(&d->ppos), P * 4);
         size_t stride = 0;
-        uint32_t units = 0;
-        for (int p : {P_Q, P_O, P_DOWN}) {
-            stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
-            units = std::max(units, d->proj[p]->units);
-        }
+        for (int p : {P_Q, P_O, P_DOWN}) stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
         d->pimg_stride = static_cast<uint32_t>((stride + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->pimg), P * d->pimg_stride);
-        if (kind == kHvsq2) {
-            d->pq8_stride = units * 256;
-            part(reinterpret_cast<void **>(&d->pq8), P * d->pq8_stride);
-            part(reinterpret_cast<void **>(&d->pmimg), mfma_image_bytes(*d->proj[P_DOWN]) +
-                                                           mfma_image_bytes(*d->proj[P_Q]) +
-                                                           mfma_image_bytes(*d->proj[P_O]));
-        }
+        if (kind == kHvsq2 || kind == kQ4_0)
+            part(reinterpret_cast<void **>(&d->pmimg),
+                 std::max({mfma_image_bytes(*d->proj[P_DOWN]), mfma_image_bytes(*d->proj[P_Q]),
+                           mfma_image_bytes(*d->proj[P_O])}));
     }
     // attention partials of the device-position kernels
     KvCache proto;

@@ -144,7 +144,12 @@ __host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHv
 // the fused one-token GEMV prologue for a block of tokens.  The values are
 // staged in LDS (dynamic, K floats) with coalesced loads where they fit
 // (`staged`), else recomputed from global memory; the image is written in
-// E-element sub-blocks by adjacent lanes, as the prologue does.
+// E-element sub-blocks by adjacent lanes, as the prologue does.  With
+// `mimg`, token t's columns of the int8-MFMA image of up to 16 tokens are
+// written instead of q8 (one sub-block is one 8- or 16-byte slot of that
+// image; the block sums are reduced over the adjacent lanes holding the
+// block); tokens >= M of the image are left as they are (the GEMM neither
+// mixes token columns nor stores those tokens).
 template <int KIND>
 __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
                                                               uint32_t x_stride, uint32_t units, uint8_t *image,
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
                                                               uint32_t q8_stride, uint32_t mode,
                                                               const float *__restrict__ x2,
                                                               const float *__restrict__ norm, float eps,
-                                                              uint32_t staged) {
+                                                              uint32_t staged, uint8_t *mimg) {
     extern __shared__ float vals[];  // [K] when staged
     __shared__ float wave_red[1024 / kWaveSize];
     constexpr uint32_t E = fused_sub_elems(KIND);
@@ -212,6 +217,46 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
             }
         }
         if (img) put_sub_block<KIND>(img, units, sb, nsub, w);
+        if (mimg) {
+            int s = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < E; ++i) s += static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
+            if constexpr (KIND == kQ4_0) {
+                // slot (block sb/4, group sb%4): elements {0,2,4,6} then {1,3,5,7}
+                s += __shfl_xor(s, 1);
+                s += __shfl_xor(s, 2);
+                const uint32_t nblk = (K + 31) / 32;
+                if (sb < nblk * 4) {
+                    const uint32_t lo = (w[0] & 0xffu) | ((w[0] >> 8) & 0xff00u) | ((w[1] & 0xffu) << 16) |
+                                        ((w[1] << 8) & 0xff000000u);
+                    const uint32_t hi = ((w[0] >> 8) & 0xffu) | ((w[0] >> 16) & 0xff00u) |
+                                        ((w[1] << 8) & 0xff0000u) | (w[1] & 0xff000000u);
+                    *reinterpret_cast<uint2 *>(mimg + (static_cast<size_t>(sb) * 16 + t) * 8) = make_uint2(lo, hi);
+                    if ((sb & 3u) == 0)
+                        reinterpret_cast<int32_t *>(mimg + static_cast<size_t>(nblk) * 512)[(sb >> 2) * 16 + t] = s;
+                }
+            } else {
+                // elements 16 sb .. 16 sb + 15 are slice sl = sb % 4 of group
+                // g = (sb / 4) % 4 of block sb / 16, image slot
+                // (block * 16 + sl * 4 + g); word k = byte k of w[0..3]
+                s += __shfl_xor(s, 1);
+                s += __shfl_xor(s, 2);
+                s += __shfl_xor(s, 4);
+                s += __shfl_xor(s, 8);
+                if (sb < nsub) {
+                    uint32_t o[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        o[k] = ((w[0] >> (8 * k)) & 0xffu) | (((w[1] >> (8 * k)) & 0xffu) << 8) |
+                               (((w[2] >> (8 * k)) & 0xffu) << 16) | (((w[3] >> (8 * k)) & 0xffu) << 24);
+                    const uint32_t slot = (sb & ~15u) | ((sb & 3u) << 2) | ((sb >> 2) & 3u);
+                    *reinterpret_cast<uint4 *>(mimg + (static_cast<size_t>(slot) * 16 + t) * 16) =
+                        make_uint4(o[0], o[1], o[2], o[3]);
+                    if ((sb & 15u) == 0)
+                        reinterpret_cast<int32_t *>(mimg + static_cast<size_t>(units) * 4096)[(sb >> 4) * 16 + t] = s;
+                }
+            }
+        }
         if (q8row && sb < nsub)
 #pragma unroll
             for (uint32_t i = 0; i < E; ++i)
@@ -806,6 +851,44 @@ __global__ __launch_bounds__(256) void mfma_image_kernel(const int8_t *__restric
     }
 }
 
+// Q4_0: one v_mfma_i32_16x16x32_i8 per 32-weight block.  A lane's A operand
+// is the 4 nibble bytes of weights 8g..8g+7 of its row (g = lane / 16) as
+// two words, low nibbles then high nibbles (the unsigned codes 0..15; the -8
+// is applied to the sum: sum (n-8)*a = sum n*a - 8*sum a), so each 8-byte
+// group of the image holds elements 8g + {0,2,4,6,1,3,5,7} of the block:
+//   image [block][g][token 0..15][8 B], then int32 sums [block][token 0..15].
+__host__ __device__ constexpr size_t mfma_q4_image_block_bytes() { return 4 * 16 * 8 + 16 * 4; }
+
+__global__ __launch_bounds__(256) void mfma_q4_image_kernel(const int8_t *__restrict__ q8, uint32_t q8_stride,
+                                                            uint32_t K, uint32_t M, uint32_t nblk, uint8_t *img) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < nblk * 64) {
+        const uint32_t m = idx % 16, g = (idx / 16) % 4, b = idx / 64;
+        uint32_t w[2] = {0, 0};
+        if (m < M) {
+            const int8_t *src = q8 + static_cast<size_t>(m) * q8_stride;
+            const uint32_t e0 = b * 32 + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t e = e0 + (i < 4 ? 2 * i : 2 * (i - 4) + 1);
+                const uint32_t v = e < K ? static_cast<uint8_t>(src[e]) : 0u;
+                w[i >> 2] |= v << (8 * (i & 3));
+            }
+        }
+        *reinterpret_cast<uint2 *>(img + static_cast<size_t>(idx) * 8) = make_uint2(w[0], w[1]);
+    }
+    if (idx < nblk * 16) {
+        const uint32_t b = idx / 16, m = idx % 16;
+        int sum = 0;
+        if (m < M) {
+            const int8_t *src = q8 + static_cast<size_t>(m) * q8_stride;
+            for (uint32_t i = 0; i < 32; ++i)
+                if (b * 32 + i < K) sum += src[b * 32 + i];
+        }
+        reinterpret_cast<int32_t *>(img + static_cast<size_t>(nblk) * 512)[idx] = sum;
+    }
+}
+
 typedef int mfma_v4i __attribute__((ext_vector_type(4)));
 
 // One launch over up to kMaxGroup HyperVSQ-2 tensors that share the image
@@ -824,6 +907,7 @@ struct MfmaArgs {
     size_t tile_payload_bytes;
     size_t tile_meta_bytes;
     uint32_t units, lanes_log2, rows_per_wave_log2;
+    uint32_t nblk;         // K blocks of a row (HyperVSQ-2: units; Q4_0: 32-weight blocks)
     uint32_t ks_log2;      // waves per workgroup (log2)
     uint32_t nb;           // K blocks per wave
     uint32_t stage_bytes;  // LDS bytes of the staged weight region (STAGE)
@@ -946,8 +1030,84 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
     }
 }
 
+// Position in LDS of 16-byte piece `piece` of a staged region of `npieces`
+// pieces: within every whole aligned group of 16 pieces the low four bits
+// are XORed with the group index (an involution, so the same map serves
+// the copy and the reads).  Q4_0 rows are n * 16 bytes apart in a tile;
+// this spreads the 4-byte A reads and 8-byte scale reads of a wave's 16
+// rows over distinct banks.
+__device__ __forceinline__ uint32_t lds_swizzle(uint32_t piece, uint32_t npieces) {
+    return (piece | 15u) < npieces ? piece ^ ((piece >> 4) & 15u) : piece;
+}
+
+// One chunk of up to NB Q4_0 blocks (32 weights each; unit u = b / 4 holds
+// blocks 4u .. 4u+3 as its four 16-byte payload chunks and their fp16
+// scales as its meta).  As mfma_chunk: every load of the chunk issued before
+// the first MFMA.  The tokens are the MFMA's A operand and the weight rows
+// its B operand, so lane (g, m) accumulates tokens 4g .. 4g+3 of weight row
+// m: the block scale it applies is the one it loaded itself, and the four
+// tokens' activation sums are one 16-byte load.
 template <int NB, int RT, bool STAGE>
-__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(MfmaArgs a) {
+__device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
+                                              const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
+                                              uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
+                                              uint32_t ppieces, uint32_t mpieces, float (&acc)[RT][4]) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.nblk) * 512);
+    uint32_t A[NB][RT];
+    uint2 Mt[NB][RT];
+    uint2 B[NB];
+    int4 SA[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t row = r0 + 16 * t + m;
+            const MfmaUnit u = mfma_unit(a, row < rows ? row : (STAGE ? r0 : 0u), STAGE ? t0 : 0u, b >> 2, b & 3);
+            if constexpr (STAGE) {
+                const uint32_t pa = 16 * lds_swizzle(static_cast<uint32_t>(u.payload) >> 4, ppieces);
+                const uint32_t ma = 16 * lds_swizzle(static_cast<uint32_t>(u.meta) >> 4, mpieces) +
+                                    (static_cast<uint32_t>(u.meta) & 8u);
+                A[i][t] = *reinterpret_cast<const uint32_t *>(lds + pa + 4 * g);
+                Mt[i][t] = *reinterpret_cast<const uint2 *>(lds + meta_lds + ma);
+            } else {
+                A[i][t] = *reinterpret_cast<const uint32_t *>(payload + u.payload + 4 * g);
+                Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
+            }
+        }
+        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+        SA[i] = *reinterpret_cast<const int4 *>(sums + b * 16 + 4 * g);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            if (r0 + 16 * t + m >= rows) Mt[i][t] = make_uint2(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (static_cast<uint32_t>(i) >= nblk) break;
+        const uint32_t q = (b0 + i) & 3;
+        const int corr[4] = {8 * SA[i].x, 8 * SA[i].y, 8 * SA[i].z, 8 * SA[i].w};
+        const long xv = static_cast<long>((static_cast<uint64_t>(B[i].y) << 32) | B[i].x);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t lo = A[i][t] & 0x0f0f0f0fu, hi = (A[i][t] >> 4) & 0x0f0f0f0fu;
+            const long wv = static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+            mfma_v4i ci = {0, 0, 0, 0};
+            // C[token][row]: element r is token 4g + r of row m
+            ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(xv, wv, ci, 0, 0, 0);
+            const uint32_t word = q < 2 ? Mt[i][t].x : Mt[i][t].y;
+            const float d = half_to_float((word >> (16 * (q & 1))) & 0xffffu);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(static_cast<float>(ci[r] - corr[r]), d, acc[t][r]);
+        }
+    }
+}
+
+template <int KIND, int NB, int RT, bool STAGE>
+__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(MfmaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -968,13 +1128,13 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const uint32_t r0 = (blockIdx.x - first) * (16 * RT);
     const uint32_t kb0 = ks * a.nb;
-    const uint32_t kb1 = min(a.units, kb0 + a.nb);
+    const uint32_t kb1 = min(a.nblk, kb0 + a.nb);
 
     // STAGE: the row group's wave tiles (16*RT rows = a whole number of
     // tiles) are contiguous in HBM; copy payload and meta into LDS with
     // direct 16-byte loads, every load instruction one contiguous 1 KB span
     const uint32_t t0 = r0 >> a.rows_per_wave_log2;
-    uint32_t meta_lds = 0;
+    uint32_t meta_lds = 0, ppieces = 0, mpieces = 0;
     if constexpr (STAGE) {
         const uint32_t ntile = min((16u * RT) >> a.rows_per_wave_log2, tiles - t0);
         const uint32_t pbytes = ntile * static_cast<uint32_t>(a.tile_payload_bytes);
@@ -982,13 +1142,20 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
         meta_lds = ((16u * RT) >> a.rows_per_wave_log2) * static_cast<uint32_t>(a.tile_payload_bytes);
         const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
         const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
+        // Q4_0: LDS position p holds piece lds_swizzle(p) (lane order fixes
+        // the destination, so the source address is permuted)
+        ppieces = (pbytes + 15) / 16;
+        mpieces = (mbytes + 15) / 16;
         for (uint32_t c0 = wave * kWaveSize * 16; c0 < pbytes; c0 += blockDim.x * 16)
-            if (c0 + lane * 16 < pbytes)
-                __builtin_amdgcn_global_load_lds(psrc + c0 + lane * 16, (lds_void *)(smem + c0), 16, 0, 0);
+            if (c0 + lane * 16 < pbytes) {
+                const uint32_t src = KIND == kQ4_0 ? 16 * lds_swizzle((c0 >> 4) + lane, ppieces) : c0 + lane * 16;
+                __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0), 16, 0, 0);
+            }
         for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
-            if (c0 + lane * 16 < mbytes)
-                __builtin_amdgcn_global_load_lds(msrc + c0 + lane * 16, (lds_void *)(smem + meta_lds + c0), 16, 0,
-                                                 0);
+            if (c0 + lane * 16 < mbytes) {
+                const uint32_t src = KIND == kQ4_0 ? 16 * lds_swizzle((c0 >> 4) + lane, mpieces) : c0 + lane * 16;
+                __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0), 16, 0, 0);
+            }
         wait_vmcnt<0>();               // this wave's copies landed
         __builtin_amdgcn_s_barrier();  // ... and every wave's
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -999,9 +1166,14 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
     for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
-    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB)
-        mfma_chunk<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
-                                  min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
+    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
+        if constexpr (KIND == kHvsq2)
+            mfma_chunk<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+                                      min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
+        else
+            mfma_chunk_q4<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+                                         min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces, acc);
+    }
 
     // the K-split partials, summed in wave order (LDS after the staged tiles)
     if (KS > 1) {
@@ -1028,6 +1200,27 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_hvsq2_kernel(M
     // accumulate: out += the rounded product (the residual stream), in two
     // roundings as the dot8 epilogue
     const uint32_t g = lane >> 4, m = lane & 15;
+    if constexpr (KIND == kQ4_0) {
+        // lane (g, m) holds tokens 4g .. 4g+3 of row m of each tile: rows
+        // are contiguous per token, so 16 lanes store one 64-byte span
+        if (ks == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = 4 * g + r;
+                if (tok >= a.ntok) continue;
+                const float xs = a.scales[tok];
+#pragma unroll
+                for (int t = 0; t < RT; ++t) {
+                    const uint32_t row = r0 + 16 * t + m;
+                    if (row >= rows) continue;
+                    float *dst = output + static_cast<size_t>(tok) * stride + row;
+                    const float v = mul_rounded(acc[t][r], xs);
+                    *dst = a.accumulate ? add_rounded(*dst, v) : v;
+                }
+            }
+        }
+        return;
+    }
     if (ks == 0 && m < a.ntok) {
         const float xs = a.scales[m];
         const bool vec = (a.vec_out >> job) & 1u;
@@ -1378,18 +1571,20 @@ hipError_t launch_quantize_image(const DeviceTensor &t, const float *x, uint32_t
 hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const float *x, const float *x2,
                                 const float *norm, float eps, uint32_t batch, uint32_t x_stride, uint8_t *image,
                                 uint32_t image_stride, float *scales, int8_t *q8, uint32_t q8_stride,
-                                hipStream_t stream) {
+                                hipStream_t stream, uint8_t *mfma_image) {
     if (batch == 0 || mode > kInSwiglu || mode == kInImage || (mode == kInNorm && !norm) ||
-        (mode == kInSwiglu && !x2))
+        (mode == kInSwiglu && !x2) || (mfma_image && batch > static_cast<uint32_t>(kMfmaTokens)))
         return hipErrorInvalidValue;
     const uint32_t staged = static_cast<size_t>(t.cols) * sizeof(float) <= kGemvLdsLimit ? 1u : 0u;
     const size_t lds = staged ? static_cast<size_t>(t.cols) * sizeof(float) : 0;
     if (t.kind == kHvsq2)
         hipLaunchKernelGGL(quantize_image_kernel<kHvsq2>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged);
+                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
+                           mfma_image);
     else if (t.kind == kQ4_0)
         hipLaunchKernelGGL(quantize_image_kernel<kQ4_0>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged);
+                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
+                           mfma_image);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1536,13 +1731,24 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
     return hipSuccess;
 }
 
+// K steps of one MFMA block: HyperVSQ-2 256-weight blocks, Q4_0 32-weight blocks.
+uint32_t mfma_steps(const DeviceTensor &t) { return t.kind == kQ4_0 ? (t.cols + 31) / 32 : t.units; }
+
 size_t mfma_image_bytes(const DeviceTensor &t) {
-    return static_cast<size_t>(t.units) * mfma_image_block_bytes();
+    if (t.kind == kQ4_0) return static_cast<size_t>(mfma_steps(t)) * mfma_q4_image_block_bytes();
+    return t.kind == kHvsq2 ? static_cast<size_t>(t.units) * mfma_image_block_bytes() : 0;
 }
 
 hipError_t launch_mfma_image(const DeviceTensor &t, const int8_t *q8, uint32_t batch, uint32_t q8_stride,
                              uint8_t *image, hipStream_t stream) {
-    if (t.kind != kHvsq2 || batch == 0 || batch > static_cast<uint32_t>(kMfmaTokens)) return hipErrorInvalidValue;
+    if ((t.kind != kHvsq2 && t.kind != kQ4_0) || batch == 0 || batch > static_cast<uint32_t>(kMfmaTokens))
+        return hipErrorInvalidValue;
+    if (t.kind == kQ4_0) {
+        const uint32_t n = mfma_steps(t) * 64;
+        hipLaunchKernelGGL(mfma_q4_image_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, q8, q8_stride, t.cols,
+                           batch, mfma_steps(t), image);
+        return hipGetLastError();
+    }
     const uint32_t n = t.units * 256;
     hipLaunchKernelGGL(mfma_image_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, q8, q8_stride, t.cols, batch,
                        t.units, image);
@@ -1567,39 +1773,49 @@ struct MfmaPlan {
 
 MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     MfmaPlan p;
-    const uint32_t units = t.units;
+    // K steps, and the unrolled chunk: 5 HyperVSQ-2 blocks (four MFMAs
+    // each), 8 Q4_0 blocks (one MFMA each)
+    const uint32_t units = mfma_steps(t);
+    const uint32_t chunk = t.kind == kQ4_0 ? 8 : 5;
     const uint64_t groups = (total_rows + 16 * p.rt - 1) / (16 * p.rt);
     auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
-    while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
-    while (p.ks_log2 < 3 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+    if (t.kind == kQ4_0) {
+        // as many K-split waves as keep the whole launch within one round of
+        // resident waves (256 CUs x 32)
+        while (p.ks_log2 < 3 && (groups << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+    } else {
+        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > chunk) ++p.ks_log2;
+        while (p.ks_log2 < 3 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+    }
     p.nb = per_wave(p.ks_log2);
-    p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
+    p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : (p.nb <= 5 || chunk == 5) ? 5 : 8;
     p.waves = 1u << p.ks_log2;
     const uint32_t part = (p.waves - 1) * kWaveSize * 4 * p.rt * 4;
     const uint32_t rows_grp = 16u * p.rt;
-    const uint64_t stage = rows_grp % t.rows_per_wave == 0
-                               ? static_cast<uint64_t>(rows_grp / t.rows_per_wave) *
-                                     (t.tile_payload_bytes + t.tile_meta_bytes)
-                               : ~0ull;
-    p.stage = stage + part <= 65536;
+    // staging needs whole tiles in the row group (tiles of 32 or 64 rows
+    // are never staged)
+    const bool whole = rows_grp % t.rows_per_wave == 0;
+    const uint64_t stage =
+        whole ? static_cast<uint64_t>(rows_grp / t.rows_per_wave) * (t.tile_payload_bytes + t.tile_meta_bytes) : 0;
+    p.stage = whole && stage + part <= 65536;
     p.stage_bytes = p.stage ? static_cast<uint32_t>(stage) : 0;
     p.lds_bytes = p.stage_bytes + part;
     return p;
 }
 
-template <int NB, int RT>
+template <int KIND, int NB, int RT>
 hipError_t launch_mfma_rt(bool stage, uint32_t grid, uint32_t threads, size_t lds, const MfmaArgs &a,
                           hipStream_t stream) {
     if (stage)
-        hipLaunchKernelGGL((mfma_hvsq2_kernel<NB, RT, true>), dim3(grid), dim3(threads), lds, stream, a);
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true>), dim3(grid), dim3(threads), lds, stream, a);
     else
-        hipLaunchKernelGGL((mfma_hvsq2_kernel<NB, RT, false>), dim3(grid), dim3(threads), lds, stream, a);
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false>), dim3(grid), dim3(threads), lds, stream, a);
     return hipGetLastError();
 }
 
-template <int NB>
+template <int KIND, int NB>
 hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, hipStream_t stream) {
-    return launch_mfma_rt<NB, 1>(p.stage, grid, p.waves * kWaveSize, p.lds_bytes, a, stream);
+    return launch_mfma_rt<KIND, NB, 1>(p.stage, grid, p.waves * kWaveSize, p.lds_bytes, a, stream);
 }
 
 }  // namespace
@@ -1614,7 +1830,8 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     uint64_t total_rows = 0;
     for (uint32_t i = 0; i < count; ++i) {
         const DeviceTensor &t = *tensors[i];
-        if (t.kind != kHvsq2 || t.cols != t0.cols || t.units != t0.units || t.lanes != t0.lanes ||
+        if ((t.kind != kHvsq2 && t.kind != kQ4_0) || t.kind != t0.kind || t.cols != t0.cols ||
+            t.units != t0.units || t.lanes != t0.lanes ||
             t.rows_per_wave != t0.rows_per_wave || t.tile_payload_bytes != t0.tile_payload_bytes ||
             t.tile_meta_bytes != t0.tile_meta_bytes || !outputs[i])
             return hipErrorInvalidValue;
@@ -1642,6 +1859,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.tile_payload_bytes = t0.tile_payload_bytes;
     a.tile_meta_bytes = t0.tile_meta_bytes;
     a.units = t0.units;
+    a.nblk = mfma_steps(t0);
     a.lanes_log2 = static_cast<uint32_t>(__builtin_ctz(t0.lanes));
     a.rows_per_wave_log2 = static_cast<uint32_t>(__builtin_ctz(t0.rows_per_wave));
     a.ks_log2 = p.ks_log2;
@@ -1651,10 +1869,18 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.scales = scales;
     a.ntok = batch;
     a.accumulate = accumulate ? 1u : 0u;
+    if (t0.kind == kQ4_0) {
+        switch (p.nbt) {
+        case 2: return launch_mfma_nb<kQ4_0, 2>(p, grid, a, stream);
+        case 3: return launch_mfma_nb<kQ4_0, 3>(p, grid, a, stream);
+        case 5: return launch_mfma_nb<kQ4_0, 5>(p, grid, a, stream);
+        default: return launch_mfma_nb<kQ4_0, 8>(p, grid, a, stream);
+        }
+    }
     switch (p.nbt) {
-    case 2: return launch_mfma_nb<2>(p, grid, a, stream);
-    case 3: return launch_mfma_nb<3>(p, grid, a, stream);
-    default: return launch_mfma_nb<5>(p, grid, a, stream);
+    case 2: return launch_mfma_nb<kHvsq2, 2>(p, grid, a, stream);
+    case 3: return launch_mfma_nb<kHvsq2, 3>(p, grid, a, stream);
+    default: return launch_mfma_nb<kHvsq2, 5>(p, grid, a, stream);
     }
 }
 

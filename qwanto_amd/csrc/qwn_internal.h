@@ -181,11 +181,12 @@ uint32_t gemv_group_grid(const GemvGroupLaunch &g);
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream);
 // Images of a block of fp32 tokens after the input transform of `mode`
 // (kInF32, kInNorm with `norm` and eps, kInSwiglu with x2 at the same
-// stride), quantized per token as launch_quantize_image.
+// stride), quantized per token as launch_quantize_image; with mfma_image
+// (batch <= 16) the tokens' columns of the MFMA image are written as well.
 hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const float *x, const float *x2,
                                 const float *norm, float eps, uint32_t batch, uint32_t x_stride, uint8_t *image,
                                 uint32_t image_stride, float *scales, int8_t *q8, uint32_t q8_stride,
-                                hipStream_t stream);
+                                hipStream_t stream, uint8_t *mfma_image = nullptr);
 // int8 MFMA batch GEMM of a HyperVSQ-2 tensor for 1..16 tokens (used from 8
 // tokens up): the activation layout its tiles read (the "MFMA image"), built
 // from int8 tokens [batch][q8_stride] (values past cols ignored), and the
@@ -202,6 +203,12 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate = false);
 constexpr uint32_t kMfmaMinTokens = 8;
+// Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV:
+// HyperVSQ-2 from 8 tokens; Q4_0 (one 16x16x32 MFMA per 32-weight block,
+// the same time at 8 tokens as at 16) from a full 16-token tile.
+inline bool mfma_batch(uint32_t kind, uint32_t batch) {
+    return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= 16);
+}
 
 // RMSNorm of one fp32 token into the fp32 image of an F16 tensor.
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,

@@ -169,8 +169,8 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     g.output = static_cast<float *>(ctx->dev_out.ptr);
     g.batch = r->batch;
     g.output_stride = r->rows;
-    // HyperVSQ-2 from 8 tokens: int8 MFMA tiles of 16 tokens
-    const bool mfma = t.kind == qwn::kHvsq2 && r->batch >= qwn::kMfmaMinTokens;
+    // int8 MFMA tiles of 16 tokens (HyperVSQ-2 from 8 tokens, Q4_0 from 16)
+    const bool mfma = qwn::mfma_batch(t.kind, r->batch);
     const size_t mfma_img = qwn::mfma_image_bytes(t);
     if (mfma && ((e = ctx->dev_work.ensure(mfma_img + (quantize ? in_bytes / 4 : 0))) != hipSuccess))
         return hip_fail("MFMA workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
@@ -1087,7 +1087,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *handle, con
 QWN_CUDA_ABI_API uint64_t qwn_hip_ext_mfma_image_bytes(const QwnCudaTensorHandle *h) {
     if (!h || !header_ok(*h) || !h->opaque) return 0;
     const DeviceTensor &t = static_cast<const ResidentTensor *>(h->opaque)->t;
-    return t.kind == qwn::kHvsq2 ? qwn::mfma_image_bytes(t) : 0;
+    return qwn::mfma_image_bytes(t);
 }
 
 QWN_CUDA_ABI_API int qwn_hip_ext_mfma_image_device(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
@@ -1100,8 +1100,9 @@ QWN_CUDA_ABI_API int qwn_hip_ext_mfma_image_device(QwnCudaContextHandle *handle,
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
     ResidentTensor *rt = ext_tensor(ctx, th);
-    if (!rt || rt->t.kind != qwn::kHvsq2 || q8_stride < rt->t.cols || (reinterpret_cast<uintptr_t>(image) & 15u)) {
-        set_error("MFMA image request does not fit the tensor (HyperVSQ-2 only)");
+    if (!rt || (rt->t.kind != qwn::kHvsq2 && rt->t.kind != qwn::kQ4_0) || q8_stride < rt->t.cols ||
+        (reinterpret_cast<uintptr_t>(image) & 15u)) {
+        set_error("MFMA image request does not fit the tensor (HyperVSQ-2 or Q4_0)");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
@@ -1119,8 +1120,9 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *handle, 
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
     ResidentTensor *rt = ext_tensor(ctx, th);
-    if (!rt || rt->t.kind != qwn::kHvsq2 || (output_stride && output_stride < rt->t.rows)) {
-        set_error("MFMA GEMM request does not fit the tensor (HyperVSQ-2 only)");
+    if (!rt || (rt->t.kind != qwn::kHvsq2 && rt->t.kind != qwn::kQ4_0) ||
+        (output_stride && output_stride < rt->t.rows)) {
+        set_error("MFMA GEMM request does not fit the tensor (HyperVSQ-2 or Q4_0)");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
@@ -1150,9 +1152,11 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_group_device(QwnCudaContextHandle *ha
     uint32_t strides[qwn::kMaxGroup] = {};
     for (uint32_t i = 0; i < count; ++i) {
         ResidentTensor *rt = ext_tensor(ctx, &tensors[i]);
-        if (!rt || rt->t.kind != qwn::kHvsq2 || !outputs[i] || (output_stride && output_stride < rt->t.rows) ||
-            (i > 0 && rt->t.cols != ts[0]->cols)) {
-            set_error("MFMA group GEMM tensor %u does not fit (HyperVSQ-2, equal columns, output stride)", i);
+        if (!rt || (rt->t.kind != qwn::kHvsq2 && rt->t.kind != qwn::kQ4_0) || !outputs[i] ||
+            (output_stride && output_stride < rt->t.rows) ||
+            (i > 0 && (rt->t.cols != ts[0]->cols || rt->t.kind != ts[0]->kind))) {
+            set_error("MFMA group GEMM tensor %u does not fit (HyperVSQ-2 or Q4_0, one kind, equal columns, "
+                      "output stride)", i);
             return QWN_CUDA_STATUS_INVALID_ARGUMENT;
         }
         ts[i] = &rt->t;

@@ -97,6 +97,51 @@ def test_q4_0_qwen2_1p5b_shapes(gpu_ctx, oracle_lib, N, K):
     check_q4_0(gpu_ctx, oracle_lib, N, K, seed=N * 7 + K)
 
 
+def oracle_product(oracle_lib, kind, w, q8, sums, xs, K, N):
+    if kind == "hvsq2":
+        return oracle_lib.gemv_hvsq2(w, q8, sums, float(xs), K, N)
+    return oracle_lib.gemv_q4_0_q8(w, q8, float(xs), K, N)
+
+
+def run_mfma_group(ctx, oracle_lib, kind, Ns, K, M, seed, accumulate=False):
+    """One qwn_hip_ext_mfma_image_device + gemm_mfma_group_device pass over
+    tensors of one kind and equal columns; every token of every tensor
+    against the oracle (with accumulate: the oracle product added to the
+    outputs' prior contents)."""
+    import torch
+    rng = np.random.default_rng(seed)
+    make = synth.hvsq2_weights if kind == "hvsq2" else synth.q4_0_weights
+    ws = [make(rng, N, K) for N in Ns]
+    x = synth.activations(rng, M, K)
+    q8, xs, sums = oracle_lib.quantize(x)
+    hs = [ctx.upload(w, kind, N, K) for w, N in zip(ws, Ns)]
+    try:
+        dev = torch.device("cuda:0")
+        q8d = torch.from_numpy(q8).to(dev)
+        xsd = torch.from_numpy(xs).to(dev)
+        img = torch.zeros(ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
+        if accumulate:
+            init = [rng.standard_normal((M, N)).astype(np.float32) for N in Ns]
+            ys = [torch.from_numpy(i.copy()).to(dev) for i in init]
+        else:
+            init = [np.zeros((M, N), np.float32) for N in Ns]
+            ys = [torch.full((M, N), float("nan"), dtype=torch.float32, device=dev) for N in Ns]
+        s = torch.cuda.current_stream().cuda_stream
+        ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
+        ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
+                                   stream=s, accumulate=accumulate)
+        torch.cuda.synchronize()
+        for w, N, y, i0 in zip(ws, Ns, ys, init):
+            yh = y.cpu().numpy()
+            for t in range(M):
+                ref = oracle_product(oracle_lib, kind, w, q8[t], sums[t], xs[t], K, N)
+                ok, worst = gemv_close(yh[t] - i0[t], ref)
+                assert ok, f"{kind} tensor {N}x{K} token {t}: worst {worst:.3g}"
+    finally:
+        for h in hs:
+            ctx.release(h)
+
+
 @pytest.mark.parametrize("Ns,K,M", [((4096, 1024, 1024), 2560, 16), ((9728, 9728), 2560, 16),
                                     ((8200, 77), 777, 9), ((16390, 5), 520, 11), ((300,), 16384, 8),
                                     ((2560,), 9728, 12)])
@@ -106,65 +151,29 @@ def test_hvsq2_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
     64-row-group launches with ragged rows, unaligned row counts and partial
     blocks, K beyond one chunk of blocks per wave), every token of every
     tensor against the oracle."""
-    import torch
-    rng = np.random.default_rng(sum(Ns) + K + M)
-    ws = [synth.hvsq2_weights(rng, N, K) for N in Ns]
-    x = synth.activations(rng, M, K)
-    q8, xs, sums = oracle_lib.quantize(x)
-    hs = [gpu_ctx.upload(w, "hvsq2", N, K) for w, N in zip(ws, Ns)]
-    try:
-        dev = torch.device("cuda:0")
-        q8d = torch.from_numpy(q8).to(dev)
-        xsd = torch.from_numpy(xs).to(dev)
-        img = torch.zeros(gpu_ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
-        ys = [torch.full((M, N), float("nan"), dtype=torch.float32, device=dev) for N in Ns]
-        s = torch.cuda.current_stream().cuda_stream
-        gpu_ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
-        gpu_ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
-                                       stream=s)
-        torch.cuda.synchronize()
-        for w, N, y in zip(ws, Ns, ys):
-            yh = y.cpu().numpy()
-            for t in range(M):
-                ref = oracle_lib.gemv_hvsq2(w, q8[t], sums[t], float(xs[t]), K, N)
-                ok, worst = gemv_close(yh[t], ref)
-                assert ok, f"tensor {N}x{K} token {t}: worst {worst:.3g}"
-    finally:
-        for h in hs:
-            gpu_ctx.release(h)
+    run_mfma_group(gpu_ctx, oracle_lib, "hvsq2", Ns, K, M, seed=sum(Ns) + K + M)
 
 
 @pytest.mark.parametrize("Ns,K,M", [((2560,), 4096, 16), ((77, 1030), 9728, 9)])
 def test_hvsq2_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
-    """accumulate = 1: outputs += the product (the decoder's residual adds),
-    against the oracle product added to the prior contents."""
-    import torch
-    rng = np.random.default_rng(sum(Ns) + K + M + 1)
-    ws = [synth.hvsq2_weights(rng, N, K) for N in Ns]
-    x = synth.activations(rng, M, K)
-    q8, xs, sums = oracle_lib.quantize(x)
-    hs = [gpu_ctx.upload(w, "hvsq2", N, K) for w, N in zip(ws, Ns)]
-    try:
-        dev = torch.device("cuda:0")
-        q8d = torch.from_numpy(q8).to(dev)
-        xsd = torch.from_numpy(xs).to(dev)
-        img = torch.zeros(gpu_ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
-        init = [rng.standard_normal((M, N)).astype(np.float32) for N in Ns]
-        ys = [torch.from_numpy(i.copy()).to(dev) for i in init]
-        s = torch.cuda.current_stream().cuda_stream
-        gpu_ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
-        gpu_ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
-                                       stream=s, accumulate=True)
-        torch.cuda.synchronize()
-        for w, N, y, i0 in zip(ws, Ns, ys, init):
-            yh = y.cpu().numpy()
-            for t in range(M):
-                ref = oracle_lib.gemv_hvsq2(w, q8[t], sums[t], float(xs[t]), K, N)
-                ok, worst = gemv_close(yh[t] - i0[t], ref)
-                assert ok, f"tensor {N}x{K} token {t}: worst {worst:.3g}"
-    finally:
-        for h in hs:
-            gpu_ctx.release(h)
+    """accumulate = 1: outputs += the product (the decoder's residual adds)."""
+    run_mfma_group(gpu_ctx, oracle_lib, "hvsq2", Ns, K, M, seed=sum(Ns) + K + M + 1, accumulate=True)
+
+
+@pytest.mark.parametrize("Ns,K,M", [((1536, 256, 256), 1536, 16), ((8960, 8960), 1536, 16),
+                                    ((1536,), 8960, 16), ((8200, 77), 777, 9), ((16390, 5), 520, 11),
+                                    ((3,), 31, 8), ((65, 130), 33, 12), ((300,), 16384, 10), ((64,), 224, 13)])
+def test_q4_0_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
+    """Q4_0 on the int8 MFMA GEMM (one 16x16x32 MFMA per 32-weight block):
+    the Qwen2-1.5B q/k/v, gate/up and down shapes, ragged rows, K not a
+    multiple of 32 (the last block partial) or of 128 (the last 4-block unit
+    partial), K-splits of 1..8 waves, partial token tiles."""
+    run_mfma_group(gpu_ctx, oracle_lib, "q4_0", Ns, K, M, seed=sum(Ns) + K + M + 2)
+
+
+@pytest.mark.parametrize("Ns,K,M", [((1536,), 8960, 16), ((77, 1030), 1536, 9)])
+def test_q4_0_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
+    run_mfma_group(gpu_ctx, oracle_lib, "q4_0", Ns, K, M, seed=sum(Ns) + K + M + 3, accumulate=True)
 
 
 @pytest.mark.parametrize("N,K", [(1, 1), (3, 31), (5, 32), (7, 100), (65, 129), (130, 520),
@@ -179,8 +188,10 @@ def test_hvsq2_batched(gpu_ctx, oracle_lib, M):
     check_hvsq2(gpu_ctx, oracle_lib, 4096, 2560, seed=100 + M, M=M)
 
 
-@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("M", [2, 5, 8, 16, 17])
 def test_q4_0_batched(gpu_ctx, oracle_lib, M):
+    """Through qwn_cuda_abi_gemm: the dot8 GEMV below 16 tokens, the MFMA
+    GEMM in 16-token tiles from 16 (17: a full tile and a 1-token tile)."""
     check_q4_0(gpu_ctx, oracle_lib, 1536, 8960, seed=200 + M, M=M)
 
 
@@ -384,7 +395,8 @@ def test_device_image_f16(gpu_ctx, oracle_lib):
 
 
 @pytest.mark.parametrize("kind,N,K,M", [("hvsq2", 1024, 2560, 1), ("hvsq2", 77, 700, 3),
-                                        ("q4_0", 1536, 1536, 1), ("q4_0", 40, 8960, 2)])
+                                        ("q4_0", 1536, 1536, 1), ("q4_0", 40, 8960, 2), ("q4_0", 300, 1000, 16),
+                                        ("hvsq2", 300, 1000, 12)])
 def test_abi_fp32_input_quantized_on_device(gpu_ctx, oracle_lib, kind, N, K, M):
     """INPUT_F32 with a quantized tensor: the library quantizes per token on
     the device (c/qwanto_kernels.c:354-433) -- the whole CPU matmul
