@@ -136,14 +136,15 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemv_group_device(QwnCudaContextHandle *context
 QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *context, const uint64_t *partials,
                                                uint32_t count, int32_t *index, void *stream);
 
-/* int8 MFMA batch GEMM of a HyperVSQ-2 tensor, 1..16 tokens per call (the
- * ABI's hypervsq2_gemm uses it from 8 tokens up): each 256-weight block is
- * one exact int8 dot product with the octant multipliers folded into the
- * weights, on v_mfma_i32_16x16x64_i8 tiles of 16 rows x 16 tokens.  The
- * activations are read from an "MFMA image" of the int8 tokens
- * (qwn_hip_ext_mfma_image_bytes() bytes, 16-byte aligned), built by
- * qwn_hip_ext_mfma_image_device from q8 [batch][q8_stride].
- * output [batch][output_stride] = W x_t * scales[t]. */
+/* int8 MFMA batch GEMM of a HyperVSQ-2 or Q4_0 tensor, 1..16 tokens per
+ * call (the ABI's GEMM uses it by itself from 8 HyperVSQ-2 / 16 Q4_0
+ * tokens): HyperVSQ-2 blocks are exact int8 dot products with the octant
+ * multipliers folded into the weights (v_mfma_i32_16x16x64_i8), Q4_0 blocks
+ * one v_mfma_i32_16x16x32_i8 each on the unsigned codes, on tiles of 16
+ * rows x 16 tokens.  The activations are read from an "MFMA image" of the
+ * int8 tokens (qwn_hip_ext_mfma_image_bytes() bytes, 16-byte aligned;
+ * 0 for F16 tensors), built by qwn_hip_ext_mfma_image_device from q8
+ * [batch][q8_stride].  output [batch][output_stride] = W x_t * scales[t]. */
 QWN_CUDA_ABI_API uint64_t qwn_hip_ext_mfma_image_bytes(const QwnCudaTensorHandle *tensor);
 QWN_CUDA_ABI_API int qwn_hip_ext_mfma_image_device(QwnCudaContextHandle *context,
                                                    const QwnCudaTensorHandle *tensor, const int8_t *q8,
@@ -153,7 +154,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_gemm_mfma_device(QwnCudaContextHandle *context,
                                                   const QwnCudaTensorHandle *tensor, const void *image,
                                                   const float *scales, float *output, uint32_t batch,
                                                   uint32_t output_stride, void *stream);
-/* The same GEMM over `count` (1..4) HyperVSQ-2 tensors with the same
+/* The same GEMM over `count` (1..4) tensors of one kind with the same
  * column count that share one MFMA image (q/k/v, gate/up), in one launch:
  * outputs[i] [batch][output_stride or the tensor's rows]; accumulate != 0
  * adds the product to the outputs (a residual stream) instead. */
