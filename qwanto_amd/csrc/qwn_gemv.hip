@@ -814,6 +814,7 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 // waves that split one row group's K combine their partial tiles through
 // LDS in wave order.
 constexpr int kMfmaTokens = 16;
+constexpr uint64_t kMfmaLdsLimit = 160 * 1024;  // LDS per workgroup on gfx950
 
 __host__ __device__ constexpr size_t mfma_image_block_bytes() { return 16 * 256 + 16 * 4; }
 
@@ -1793,11 +1794,11 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     const uint32_t part = (p.waves - 1) * kWaveSize * 4 * p.rt * 4;
     const uint32_t rows_grp = 16u * p.rt;
     // staging needs whole tiles in the row group (tiles of 32 or 64 rows
-    // are never staged)
+    // are never staged) and fits gfx950's 160 KB of LDS per workgroup
     const bool whole = rows_grp % t.rows_per_wave == 0;
     const uint64_t stage =
         whole ? static_cast<uint64_t>(rows_grp / t.rows_per_wave) * (t.tile_payload_bytes + t.tile_meta_bytes) : 0;
-    p.stage = whole && stage + part <= 65536;
+    p.stage = whole && stage + part <= kMfmaLdsLimit;
     p.stage_bytes = p.stage ? static_cast<uint32_t>(stage) : 0;
     p.lds_bytes = p.stage_bytes + part;
     return p;
