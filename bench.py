@@ -12,11 +12,12 @@ device from N(0,1) fp32) already resident in HBM.
 value = algorithmic weight bytes per step / step time (GB/s).  roofline is
 the dominant kernel of that step (the gate/up launch, 2 x 9728x2560,
 14,397,440 B) from HIP events on the launch stream; cpu_baseline times the
-reference's CPU GEMV (oracle/_ref, or the oracle port) on this host.
+oracle's restatement of the reference's CPU GEMV on this host's cores.
 
 Also reported: the same sweep with one launch per tensor, the Qwen2-1.5B
-Q4_0 sweep, the Q4_0 greedy decode (tok/s, with the reference CPU decoder
-on a bounded sample beside it), the same decode at the Qwen3-4B layer
+Q4_0 sweep with its per-launch GB/s, the Q4_0 greedy decode (tok/s, with
+the oracle CPU decoder on a bounded sample beside it, and the same decode
+through the synchronous host-pointer ABI), the same decode at the Qwen3-4B layer
 shapes in HyperVSQ-2, Q8-KV decode attention at the Qwen3-4B shape for 4096
 and 32768 cached tokens, the weight upload rate, and the HyperVSQ-2 batch
 sweep M = 1..16 (weights read once per launch).
@@ -211,33 +212,109 @@ def decode_bench(ctx, model, prompt, new_tokens=128, workload=DECODE_1P5B):
     }
 
 
-def cpu_decode_baseline(model, prompt, steps=6, threads=None):
-    """The reference decoder (c/qwanto_decode.c built in place, CPU backend,
-    Q8 KV) on the same model from a .qwn file: the first 4 prompt tokens,
-    then `steps` greedy steps, timed; tok/s over the greedy steps."""
+def cpu_decode_baseline(model, prompt, steps=16, threads=None):
+    """The oracle decoder (oracle/qwn_oracle_decoder.c, the C restatement of
+    c/qwanto_decode.c's CPU step, bit-identical to it) on the same model: the
+    prompt, then `steps` greedy steps, timed; tok/s over the greedy steps
+    (c/qwanto_decode.c:2121-2122).  The oracle splits the tied F16 LM head
+    over the threads where the reference runs it on one thread, so this is
+    a faster CPU baseline than qwnrun's own."""
     import numpy as np
 
     import oracle
-    from qwanto_amd import qwn_file, synth
-    if not os.path.exists(oracle.REF_DECODER_SO):
-        return None
     threads = threads or len(os.sched_getaffinity(0))
-    V = synth.QWEN2_1P5B_CONFIG["vocab"]
-    with tempfile.TemporaryDirectory() as tmp:
-        path = os.path.join(tmp, "m.qwn")
-        qwn_file.write_decoder_model(path, model)
-        ref = oracle.load_ref_decoder(path, synth.QWEN2_1P5B_CONFIG["max_ctx"], threads)
+    dec = oracle.load().decoder(model, threads=threads)
+    try:
+        for t in prompt:
+            logits = dec.forward(int(t))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = dec.forward(int(np.argmax(logits)))
+        dt = time.perf_counter() - t0
+    finally:
+        dec.close()
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle CPU decoder (C restatement of the reference step), {len(prompt)} prompt tokens "
+                      f"then {steps} greedy steps of the same model, {threads} OpenMP threads",
+            **cpu_host_info()}
+
+
+def host_decode_bench(model, prompt, new_tokens=128):
+    """The drop-in path: the host decoder (qwanto_amd/host, the reference
+    host step in C) driving every projection, the LM head and the Q8 KV
+    cache through the synchronous host-pointer ABI, as an unmodified qwnrun
+    does; tok/s = generated / decode wall time."""
+    from qwanto_amd.host_decoder import HostDecoder
+    dec = HostDecoder(model)
+    try:
+        # the weights upload on first use, inside the prompt steps (not timed)
+        dec.generate(prompt, new_tokens)
+        m = dec.metrics()
+    finally:
+        dec.close()
+    calls = m.abi_calls / max(1, m.prompt_tokens + m.generated_tokens)
+    return {"tok_s": round(m.generated_tokens / (m.decode_wall_ms / 1e3), 1),
+            "ms_per_token": round(m.decode_wall_ms / m.generated_tokens, 3),
+            "abi_calls_per_token": round(calls, 1),
+            "us_per_abi_call": round(m.decode_wall_ms * 1e3 / max(1, m.generated_tokens) / calls, 2),
+            "gpu_matmul_count": int(m.gpu_matmul_count), "cpu_fallback_count": int(m.cpu_fallback_count),
+            "backend_reason": m.backend_reason.decode(),
+            "workload": "host decoder over the qwn_cuda ABI (synchronous, host pointers), same model and "
+                        "prompt, greedy"}
+
+
+def cpu_host_info() -> dict:
+    """CPU model and the GPU-local NUMA node's physical cores on this host."""
+    info = {"cpu_model": None, "numa_node": None, "node_physical_cores": None}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cpus = gpu_local_cpus()
+    if cpus is not None:
+        node, cpus = cpus
+        info["numa_node"] = node
+        info["node_physical_cores"] = len(physical_cores(cpus))
+    return info
+
+
+def gpu_local_cpus():
+    """(NUMA node of GPU 0, the CPUs of that node this process may use), or
+    None where the node is unknown."""
+    try:
+        import torch
+        p = torch.cuda.get_device_properties(0)
+        bus = "%04x:%02x:%02x.0" % (getattr(p, "pci_domain_id", 0), p.pci_bus_id, p.pci_device_id)
+        node = int(open(f"/sys/bus/pci/devices/{bus}/numa_node").read())
+        if node < 0:
+            return None
+        allowed = os.sched_getaffinity(0)
+        cpus = set()
+        for part in open(f"/sys/devices/system/node/node{node}/cpulist").read().strip().split(","):
+            a, _, b = part.partition("-")
+            cpus.update(range(int(a), int(b or a) + 1))
+        cpus &= allowed
+        return (node, sorted(cpus)) if cpus else None
+    except Exception:
+        return None
+
+
+def physical_cores(cpus) -> list:
+    """One CPU per physical core among `cpus` (SMT siblings dropped)."""
+    seen, out = set(), []
+    for c in cpus:
         try:
-            for t in prompt[:4]:
-                logits = ref.forward(int(t), V)
-            t0 = time.perf_counter()
-            for _ in range(steps):
-                logits = ref.forward(int(np.argmax(logits)), V)
-            dt = time.perf_counter() - t0
-        finally:
-            ref.close()
-    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"reference CPU decoder, 4 prompt tokens then {steps} greedy steps of the same model"}
+            key = (open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip(),
+                   open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip())
+        except OSError:
+            key = ("?", str(c))
+        if key not in seen:
+            seen.add(key)
+            out.append(c)
+    return out
 
 
 def attention_bench(torch, ctx, steps=50):
@@ -397,21 +474,14 @@ def batch_sweep(torch, ctx, steps, warmup):
     return out
 
 
-def cpu_baseline(seconds: float):
-    """Time the reference's own CPU GEMV (oracle/_ref, built from c/qwanto_kernels.c)
-    -- or the oracle port when that build is absent -- over a bounded sample:
-    one Qwen3-4B layer's seven HyperVSQ-2 projections from N(0,1) fp32
-    activations (quantization included, as qwn_matmul_hypervsq2_f32 does),
-    rotating through four distinct layer copies (117 MB, beyond the LLC)."""
-    import ctypes
-
+def cpu_gemv_child(threads: int, seconds: float) -> dict:
+    """One thread count of the CPU GEMV baseline (run in a child process so
+    its OpenMP pool is pinned to the CPUs it was started on)."""
     import numpy as np
 
     import oracle
     from qwanto_amd import synth
-    ref = oracle.load_ref()
     ora = oracle.load()
-    kind = "reference" if ref is not None else "port"
     rng = np.random.default_rng(99)
     layers = []
     for _ in range(4):
@@ -421,35 +491,56 @@ def cpu_baseline(seconds: float):
             layer.append((synth.hvsq2_weights(rng, N, K), synth.activations(rng, 1, K), N))
         layers.append(layer)
     layer_bytes = sum(synth.weight_bytes("hvsq2", N, x.shape[1]) for _, x, N in layers[0])
-    gomp = None
-    try:
-        gomp = ctypes.CDLL("libgomp.so.1")
-    except OSError:
-        pass
-    ncpu = len(os.sched_getaffinity(0))
-    results = {}
-    for threads in sorted({8, ncpu}):
-        if gomp is not None:
-            gomp.omp_set_num_threads(threads)
-        done = 0
-        t0 = time.perf_counter()
-        while True:
-            for w, x, N in layers[done % 4]:
-                if ref is not None:
-                    ref.matmul_hvsq2(w, x, N)
-                else:
-                    ora.matmul_hvsq2(w, x, N, threads=threads)
-            done += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
-        dt = time.perf_counter() - t0
-        results[threads] = layer_bytes * done / dt / 1e9
+    for w, x, N in layers[0]:
+        ora.matmul_hvsq2(w, x, N, threads=threads)  # warm-up: thread pool, page faults
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        for w, x, N in layers[done % 4]:
+            ora.matmul_hvsq2(w, x, N, threads=threads)
+        done += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"gbps": layer_bytes * done / dt / 1e9, "kernel": ora.variant_name(ora.best_variant())}
+
+
+def cpu_baseline(seconds: float):
+    """The reference's production CPU GEMV (qwn_matmul_hypervsq2_f32 with the
+    vnni-delayed kernel, c/qwanto_kernels.c:841-918, 998-1176) as restated by
+    the oracle, over a bounded sample: one Qwen3-4B layer's seven HyperVSQ-2
+    projections from N(0,1) fp32 activations (quantization included),
+    rotating through four distinct layer copies (117 MB, beyond the LLC).
+    Twice: at 8 OpenMP threads (the reference's published evidence) and on
+    every physical core of the GPU-local NUMA node this process may use
+    (OMP_PLACES=cores, OMP_PROC_BIND=close), each in a child process pinned
+    to those CPUs."""
+    import subprocess
+
+    local = gpu_local_cpus()
+    allowed = sorted(os.sched_getaffinity(0))
+    node_cores = physical_cores(local[1] if local else allowed)
+    runs = {}
+    for label, cpus in (("8", physical_cores(allowed)[:8] or allowed[:8]), ("node", node_cores)):
+        threads = len(cpus)
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PLACES="cores", OMP_PROC_BIND="close",
+                   GOMP_CPU_AFFINITY=" ".join(map(str, cpus)))
+        code = ("import json, os, sys; os.sched_setaffinity(0, %r); sys.path.insert(0, %r); import bench; "
+                "print(json.dumps(bench.cpu_gemv_child(%d, %r)))" % (cpus, ROOT, threads, seconds))
+        res = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+        if res.returncode != 0:
+            raise RuntimeError("CPU baseline child failed: " + res.stderr[-2000:])
+        runs[label] = dict(json.loads(res.stdout.strip().splitlines()[-1]), threads=threads)
+    best = runs["node"]
     return {
-        "value": round(results[ncpu], 3), "unit": "GB/s", "cores": ncpu, "kind": kind,
-        "kernel": (ref.cpu_kernel_name() if ref is not None else ora.variant_name(ora.best_variant())),
+        "value": round(best["gbps"], 3), "unit": "GB/s", "cores": best["threads"], "kind": "port",
+        "kernel": best["kernel"],
         "sample": f"Qwen3-4B layer, 7 HyperVSQ-2 projections x 4 distinct copies (117 MB), batch 1, "
-                  f"fp32 N(0,1) input quantized per call, ~{seconds:.0f}s per thread count",
-        "gbps_by_threads": {str(k): round(v, 3) for k, v in results.items()},
+                  f"fp32 N(0,1) input quantized per call, ~{seconds:.0f}s per thread count; the oracle's "
+                  f"restatement of the reference's vnni-delayed GEMV",
+        "gbps_by_threads": {str(r["threads"]): round(r["gbps"], 3) for r in runs.values()},
+        "numa_local": local is not None,
+        **cpu_host_info(),
     }
 
 
@@ -535,13 +626,21 @@ def main():
     if not args.no_extras:
         q4 = Sweep(torch, ctx, "q4_0", synth.QWEN2_1P5B_SHAPES, 28, seed=2)
         ms_q4 = time_graph(torch, q4.grouped, args.steps, args.warmup)
+        # per-layer GEMV rate of the decode workload's projections (graph of
+        # the 28 launches of one kind / 28)
+        q4_launch = {}
+        for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")), ("down", ("down",))):
+            ms = time_graph(torch, lambda st, k=key: q4.grouped(st, only=k), args.steps, args.warmup) / 28
+            b = q4.bytes_of(projs)
+            q4_launch[key] = {"us": round(ms * 1e3, 3), "bytes": b, "gbps": round(b / (ms / 1e3) / 1e9, 1)}
         extra["q4_0_sweep_qwen2_1p5b"] = {
             "gbps": round(q4.weight_bytes / (ms_q4 / 1e3) / 1e9, 1), "ms_per_step": round(ms_q4, 4),
-            "weight_bytes": q4.weight_bytes, "launches_per_step": 4 * 28}
+            "weight_bytes": q4.weight_bytes, "launches_per_step": 4 * 28, "per_layer_launch": q4_launch}
         q4.close()
         if not args.no_decode:
             model, prompt = decode_model(prompt_len=args.decode_prompt)
             dec = decode_bench(ctx, model, prompt, args.decode_new)
+            dec["drop_in_abi"] = host_decode_bench(model, prompt, args.decode_new)
             if not args.no_cpu:
                 dec["cpu_baseline"] = cpu_decode_baseline(model, prompt)
             extra["decode_qwen2_1p5b_q4_0"] = dec

@@ -20,8 +20,7 @@
  * (HyperVSQ-2 or Q4_0, one dtype per decoder) and the F16 embedding, which
  * is also the tied LM head.  Norm weights are copied from the host at
  * creation, and so are the optional per-head q/k norm weights of Qwen3
- * layers.  Biases are not supported (the configurations this decoder
- * serves have none).
+ * layers and the optional q/k/v/o projection biases.
  */
 
 #include "qwn_cuda_abi.h"
@@ -51,6 +50,14 @@ typedef struct {
     const float *k_norms;                   /* NULL, or host [layers][head_dim]: Qwen3 per-head k norm
                                                (self_attn.q_norm / k_norm, c/qwanto_decode.c:975-976,
                                                1652-1655; both or neither) */
+    /* Optional projection biases (self_attn.{q,k,v,o}_proj.bias; Qwen2
+     * checkpoints carry q/k/v biases), each NULL or host [layers][rows of
+     * that projection]: added to the projection's output as the reference's
+     * add_bias (c/qwanto_decode.c:926-929, 1649-1651, 1722). */
+    const float *q_biases;                  /* [layers][heads * head_dim] */
+    const float *k_biases;                  /* [layers][kv_heads * head_dim] */
+    const float *v_biases;                  /* [layers][kv_heads * head_dim] */
+    const float *o_biases;                  /* [layers][hidden] */
 } QwnHipDecoderDesc;
 
 typedef struct {
@@ -90,6 +97,22 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *context, QwnH
 QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
                                              const int32_t *tokens, uint32_t count, float *logits,
                                              int32_t *next_token);
+/* Speculative-decoding verification: `count` (1..16) draft tokens at the
+ * current position as one block (as qwn_hip_decoder_prefill), with the tied
+ * LM head run on EVERY token of the block in one batched F16 GEMV:
+ * logits [count][vocab] (host, may be NULL) are the logits after each
+ * token, next_tokens[count] (may be NULL) the greedy choice after each --
+ * the [nodes x vocab] scores a draft-tree verifier consumes
+ * (c/qwanto_jetspec.c:160-205), where the reference steps its target model
+ * token by token (c/qwn_speculative.c:389-433).  The cache then holds all
+ * `count` tokens; qwn_hip_decoder_truncate drops the rejected ones. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_verify(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                            const int32_t *tokens, uint32_t count, float *logits,
+                                            int32_t *next_tokens);
+/* Keep the first `position` cached tokens (position <= the current one):
+ * the next step writes at `position`. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_truncate(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                              uint32_t position);
 /* Greedy generation as c/qwanto_decode.c:2085-2125: the prompt (in prefill
  * blocks, as qwn_hip_decoder_prefill), then max_new times: tokens[s] =
  * argmax of the last logits, one step on it.  Synchronises once after the
@@ -97,6 +120,14 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *context, QwnH
 QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
                                               const int32_t *prompt, uint32_t prompt_count, uint32_t max_new,
                                               int32_t *tokens, QwnHipDecoderStats *stats);
+
+/* Debug: cached tokens [first, first + count) of layer `layer`'s Q8 KV cache
+ * in the CPU cache's token-major layout (c/qwanto_turboquant.h:78-94):
+ * keys/values [count][kv_heads*head_dim] int8, scales [count][groups] fp32
+ * (host pointers, synchronous). */
+QWN_CUDA_ABI_API int qwn_hip_decoder_debug_kv_read(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                                   uint32_t layer, uint32_t first, uint32_t count, int8_t *keys,
+                                                   int8_t *values, float *key_scales, float *value_scales);
 
 #ifdef __cplusplus
 }

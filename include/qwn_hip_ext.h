@@ -244,6 +244,26 @@ QWN_CUDA_ABI_API int qwn_hip_ext_debug_int_sums(QwnCudaContextHandle *context,
                                                 int32_t *host_out,
                                                 uint64_t out_capacity);
 
+/* Debug: the exact int32 block dot products of the int8 MFMA GEMM
+ * (qwn_hip_ext_gemm_mfma_device's kernel, the same plan and operand code)
+ * for batch (1..16) int8 tokens host_q8 [batch][cols] (host pointers,
+ * synchronous).  out[token][row][block]: HyperVSQ-2 per 256-weight block
+ * sum over octants of multiplier * sum (code-1)*a; Q4_0 per 32-weight block
+ * sum (nibble-8)*a.  out_capacity counts int32 elements. */
+QWN_CUDA_ABI_API int qwn_hip_ext_debug_mfma_int_sums(QwnCudaContextHandle *context,
+                                                     const QwnCudaTensorHandle *tensor,
+                                                     const int8_t *host_q8, uint32_t batch,
+                                                     int32_t *host_out, uint64_t out_capacity);
+
+/* Debug: cached tokens [first, first + count) of a Q8 KV cache in the CPU
+ * cache's token-major layout (c/qwanto_turboquant.h:78-94): keys/values
+ * [count][kv_heads*head_dim] int8, scales [count][ceil(channels/64)] fp32
+ * (host pointers, synchronous). */
+QWN_CUDA_ABI_API int qwn_hip_ext_debug_kv_read(QwnCudaContextHandle *context,
+                                               const QwnCudaKvCacheHandle *cache, uint32_t first,
+                                               uint32_t count, int8_t *host_keys, int8_t *host_values,
+                                               float *host_key_scales, float *host_value_scales);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,12 @@ typedef struct {
     const float *final_norm;    /* [hidden] */
     const uint8_t *const *proj; /* [layers * 7]: q k v o gate up down */
     const float *const *norms;  /* [layers * 2]: input, post-attention */
+    const float *const *qk_norms; /* NULL, or [layers * 2]: per-head q and k RMSNorm weights
+                                     [head_dim] (self_attn.q_norm / k_norm,
+                                     c/qwanto_decode.c:654-684, 1652-1655) */
+    const float *const *biases;   /* NULL, or [layers * 4]: q, k, v, o projection biases
+                                     (self_attn.*_proj.bias), each NULL or [rows]
+                                     (c/qwanto_decode.c:926-929, 1649-1651, 1722) */
 } QhdModel;
 
 typedef struct {
@@ -55,14 +61,28 @@ typedef struct {
     double prefill_ms, decode_wall_ms;
     int prompt_tokens, generated_tokens;
     char kernel_type[32];
+    /* why the ABI library was accepted or refused: the reference loader's
+     * cuda_backend_reason strings (c/qwanto_decode.c:323-461), e.g.
+     * "qwn_cuda_dll_absent_from_runtime_directory",
+     * "qwn_cuda_dll_missing_versioned_abi_1",
+     * "abi_capability_or_hypervsq2_layout_rejected",
+     * "cuda_q8_kv_capability_unavailable", "cuda_capability_query_failed",
+     * "cuda_device_index_<n>_not_enumerated",
+     * "cuda_context_creation_failed_device_<n>",
+     * "versioned_abi_1_loaded_device_<n>"; plus this decoder's own
+     * "qwn_hip_q4_0_f16_capability_unavailable" (it routes Q4_0 and F16
+     * tensors through the ABI) */
+    char backend_reason[96];
 } QhdMetrics;
 
 typedef struct QhdDecoder QhdDecoder;
 
 /* abi_path: the ABI library to load; NULL = "qwn_cuda.so" in the directory
- * of this library (the reference loader's rule). */
+ * of this library (the reference loader's rule).  On failure returns NULL
+ * with the message in `error` and, when `reason` is not NULL, the
+ * backend_reason string in `reason` (96 bytes). */
 QhdDecoder *qhd_open(const QhdModel *model, const char *abi_path, int device, char *error,
-                     int error_len);
+                     int error_len, char *reason);
 void qhd_close(QhdDecoder *d);
 /* One forward step; logits_out (vocab floats) may be NULL. */
 int qhd_forward(QhdDecoder *d, int token, float *logits_out);

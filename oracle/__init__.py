@@ -46,7 +46,10 @@ class QoModelConfig(ctypes.Structure):
 class QoModel(ctypes.Structure):
     _fields_ = [("cfg", QoModelConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
                 ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p)),
-                ("qk_norms", ctypes.POINTER(ctypes.c_void_p))]
+                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p))]
+
+
+BIAS_ORDER = ("q_bias", "k_bias", "v_bias", "o_bias")
 
 
 PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
@@ -69,11 +72,16 @@ def model_struct(model: dict) -> tuple:
     if "q_norm" in model["layers"][0]:
         qk = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data
                                            for l in range(L) for n in ("q_norm", "k_norm")])
+    bias = None
+    if any(b in layer for layer in model["layers"] for b in BIAS_ORDER):
+        bias = (ctypes.c_void_p * (4 * L))(*[model["layers"][l][b].ctypes.data if b in model["layers"][l] else None
+                                             for l in range(L) for b in BIAS_ORDER])
     m = QoModel(cfg=c, embed=model["embed"].ctypes.data, final_norm=model["final_norm"].ctypes.data,
                 proj=ctypes.cast(proj, ctypes.POINTER(ctypes.c_void_p)),
                 norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)),
-                qk_norms=ctypes.cast(qk, ctypes.POINTER(ctypes.c_void_p)) if qk is not None else None)
-    return m, (proj, norms, qk)
+                qk_norms=ctypes.cast(qk, ctypes.POINTER(ctypes.c_void_p)) if qk is not None else None,
+                biases=ctypes.cast(bias, ctypes.POINTER(ctypes.c_void_p)) if bias is not None else None)
+    return m, (proj, norms, qk, bias)
 
 
 class Decoder:
@@ -94,6 +102,11 @@ class Decoder:
 
     def __del__(self):
         self.close()
+
+    def perturb(self, seed: int) -> None:
+        """Calibration mode: rounding-sized moves of half of every stage's
+        outputs (seed 0: off, the reference's arithmetic)."""
+        self.o.lib.qo_decoder_set_perturbation(self.h, seed)
 
     def forward(self, token: int) -> np.ndarray:
         logits = np.empty(self.vocab, dtype=np.float32)
@@ -146,6 +159,7 @@ class Oracle:
         lib.qo_q8_attention.argtypes = [_c_f32p, _c_i8p, _c_i8p, _c_f32p, _c_f32p,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_float, _c_f32p, ctypes.c_int]
+        lib.qo_q8_attention_abi.argtypes = lib.qo_q8_attention.argtypes[:-1]
         lib.qo_rmsnorm.argtypes = [_c_f32p, _c_f32p, _c_f32p, ctypes.c_int, ctypes.c_float]
         lib.qo_rope_table.argtypes = [_c_f32p, _c_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float]
         lib.qo_rope_apply.argtypes = [_c_f32p, ctypes.c_int, ctypes.c_int, _c_f32p, _c_f32p]
@@ -154,6 +168,7 @@ class Oracle:
         lib.qo_decoder_create.restype = ctypes.c_void_p
         lib.qo_decoder_free.argtypes = [ctypes.c_void_p]
         lib.qo_decoder_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, _c_f32p]
+        lib.qo_decoder_set_perturbation.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
         lib.qo_decoder_generate.argtypes = [ctypes.c_void_p, _c_i32p, ctypes.c_int, ctypes.c_int,
                                             _c_i32p, _c_f32p]
 
@@ -298,6 +313,17 @@ class Oracle:
                                  ptr(vq, ctypes.c_int8), ptr(ks, ctypes.c_float),
                                  ptr(vs, ctypes.c_float), query_heads, kv_heads, head_dim, pos,
                                  scale, ptr(out, ctypes.c_float), threads)
+        return out
+
+    def q8_attention_abi(self, query, kq, vq, ks, vs, query_heads, kv_heads, head_dim, pos,
+                         scale) -> np.ndarray:
+        """Attention with the GPU ABI's head mapping kv = h * HK // H (any ratio)."""
+        out = np.zeros(query_heads * head_dim, dtype=np.float32)
+        query = np.ascontiguousarray(query, dtype=np.float32)
+        self.lib.qo_q8_attention_abi(ptr(query, ctypes.c_float), ptr(kq, ctypes.c_int8),
+                                     ptr(vq, ctypes.c_int8), ptr(ks, ctypes.c_float),
+                                     ptr(vs, ctypes.c_float), query_heads, kv_heads, head_dim,
+                                     pos, scale, ptr(out, ctypes.c_float))
         return out
 
 

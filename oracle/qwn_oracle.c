@@ -683,3 +683,22 @@ void qo_q8_attention(const float *query, const int8_t *keys,
         free(scores);
     }
 }
+
+/* The GPU ABI's head mapping, kv_head = head * kv_heads / query_heads for
+ * any ratio (c/cuda/qwn_hypervsq2_cuda_abi.cu:184); for query heads that
+ * are a multiple of the KV heads it equals the decoder's mapping above. */
+void qo_q8_attention_abi(const float *query, const int8_t *keys,
+                         const int8_t *values, const float *key_scales,
+                         const float *value_scales, int query_heads, int kv_heads,
+                         int head_dim, int pos, float scale, float *out) {
+    const int n_channels = kv_heads * head_dim;
+    float *scores = (float *)malloc((size_t)(pos + 1) * sizeof(float));
+    if (!scores) return;
+    for (int h = 0; h < query_heads; h++) {
+        const int kh = (int)(((long long)h * kv_heads) / query_heads);
+        qo_q8_attention_head(query + (size_t)h * head_dim, keys, values,
+                             key_scales, value_scales, n_channels, head_dim,
+                             kh, pos, scale, scores, out + (size_t)h * head_dim);
+    }
+    free(scores);
+}

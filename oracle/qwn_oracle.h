@@ -120,6 +120,13 @@ void qo_q8_attention(const float *query, const int8_t *keys,
                      int head_dim, int pos, float scale, float *out,
                      int threads);
 
+/* The same over the GPU ABI's mapping kv = h * HK / H, any head ratio
+ * (c/cuda/qwn_hypervsq2_cuda_abi.cu:184); one thread. */
+void qo_q8_attention_abi(const float *query, const int8_t *keys,
+                         const int8_t *values, const float *key_scales,
+                         const float *value_scales, int query_heads, int kv_heads,
+                         int head_dim, int pos, float scale, float *out);
+
 /* ---- dense decoder (qwn_oracle_decoder.c) ------------------------------ */
 
 #define QO_PROJ_HVSQ2 1
@@ -139,6 +146,9 @@ typedef struct {
     const float *const *norms;      /* [layers * 2]: input, post attention */
     const float *const *qk_norms;   /* NULL, or [layers * 2]: per-head q and k norm weights
                                        [head_dim] (Qwen3 self_attn.q_norm / k_norm) */
+    const float *const *biases;     /* NULL, or [layers * 4]: q, k, v, o projection biases
+                                       (self_attn.{q,k,v,o}_proj.bias), each NULL or
+                                       [that projection's rows] */
 } qo_model;
 
 typedef struct qo_decoder qo_decoder;
@@ -157,6 +167,12 @@ void qo_decoder_free(qo_decoder *d);
 int qo_decoder_position(const qo_decoder *d);
 /* One forward step (c/qwanto_decode.c:1566-2032); logits_out may be NULL. */
 int qo_decoder_forward(qo_decoder *d, int token, float *logits_out);
+/* Calibration mode (seed 0 = off, the default): after every RMSNorm,
+ * attention and SwiGLU a pseudo-random half of the outputs moves by one ulp,
+ * after every projection and the LM head by 2^-23 of the largest output.
+ * Not the reference's arithmetic: it measures how far rounding-sized
+ * differences travel through the model's layers. */
+void qo_decoder_set_perturbation(qo_decoder *d, uint32_t seed);
 /* Greedy generate (c/qwanto_decode.c:2085-2125). */
 int qo_decoder_generate(qo_decoder *d, const int *prompt, int prompt_count, int max_new, int *tokens,
                         float *margins);

@@ -2,8 +2,10 @@
  * CPU oracle of the dense decoder step — TEST INFRASTRUCTURE ONLY.
  *
  * Restates qwn_decoder_forward / qwn_decoder_generate
- * (c/qwanto_decode.c:1566-2032, 2085-2125) for a dense Qwen2-style model
- * without biases or q/k norms, with `--kv-cache q8` and greedy sampling,
+ * (c/qwanto_decode.c:1566-2032, 2085-2125) for a dense Qwen2/Qwen3-style
+ * model -- optional q/k/v/o projection biases (add_bias, :926-929, applied
+ * at :1649-1651 and :1722) and per-head q/k RMSNorm (:1652-1655) -- with
+ * `--kv-cache q8` and greedy sampling,
  * using the oracle's kernels for every matmul (qo_matmul_q4_0 /
  * qo_matmul_hvsq2 = qwn_matmul_*_f32, qo_matmul_f16 = the F16 path of
  * qwn_matmul_f32) and the Q8 KV cache (qo_q8_*).  The element-wise steps
@@ -22,6 +24,8 @@ struct qo_decoder {
     qo_model m;
     int threads;
     int position;
+    uint32_t perturb;                  /* 0, or the seed of the rounding perturbation */
+    uint32_t calls;                    /* matmul calls (perturbation stream) */
     float *x, *xb, *q, *k, *v, *ctx, *gate, *up, *hidden, *logits;
     float *rope_cos, *rope_sin;        /* [max_ctx][head_dim/2] */
     int8_t **kcache, **vcache;         /* per layer [max_ctx][kv_channels] */
@@ -74,9 +78,65 @@ int qo_argmax(const float *logits, int n) {
     return best;
 }
 
-static int matmul(const qo_decoder *d, const uint8_t *w, const float *x, int in, int out, float *y) {
-    if (d->m.cfg.proj_dtype == QO_PROJ_Q4_0) return qo_matmul_q4_0(w, x, 1, in, out, y, d->threads);
-    return qo_matmul_hvsq2(w, x, 1, in, out, y, d->threads, -1);
+/* add_bias (c/qwanto_decode.c:926-929): x[i] += b[i]; b may be NULL */
+static void add_bias(float *x, const float *b, int n) {
+    if (!b) return;
+    for (int i = 0; i < n; i++) x[i] += b[i];
+}
+
+static const float *bias_of(const qo_decoder *d, int layer, int which) {
+    return d->m.biases ? d->m.biases[4 * layer + which] : NULL;
+}
+
+/* Calibration only (qo_decoder_set_perturbation): rounding-sized changes
+ * at every stage where a GPU step rounds differently, on a pseudo-random
+ * half of each vector's elements.  Element-wise stages (the RMSNorm,
+ * attention and SwiGLU outputs): one ulp of the element.  Sums (the
+ * projection outputs and the logits): 2^-23 of the vector's largest
+ * magnitude, the size of the differences another fp32 order of the same
+ * exact integer dot products gives (the error of a sum scales with its
+ * largest terms, not with the result).  Running the oracle with and
+ * without it measures how far such differences -- and the int8 rounding
+ * flips they cause -- travel through the layers. */
+static uint32_t perturb_hash(const qo_decoder *d, uint32_t call, int i) {
+    uint32_t h = d->perturb * 0x9E3779B1u ^ call * 0x85EBCA77u ^ (uint32_t)i * 0xC2B2AE3Du;
+    h ^= h >> 15;
+    h *= 0x2C1B3C6Du;
+    h ^= h >> 12;
+    return h;
+}
+
+static void perturb_outputs(qo_decoder *d, float *y, int n) {
+    if (!d->perturb) return;
+    const uint32_t call = d->calls++;
+    for (int i = 0; i < n; i++) {
+        const uint32_t h = perturb_hash(d, call, i);
+        if (h & 1u) y[i] = nextafterf(y[i], (h & 2u) ? INFINITY : -INFINITY);
+    }
+}
+
+static void perturb_sums(qo_decoder *d, float *y, int n) {
+    if (!d->perturb) return;
+    const uint32_t call = d->calls++;
+    float m = 0.0f;
+    for (int i = 0; i < n; i++) m = fmaxf(m, fabsf(y[i]));
+    const float delta = ldexpf(m, -23);
+    for (int i = 0; i < n; i++) {
+        const uint32_t h = perturb_hash(d, call, i);
+        if (h & 1u) y[i] += (h & 2u) ? delta : -delta;
+    }
+}
+
+static int matmul(qo_decoder *d, const uint8_t *w, const float *x, int in, int out, float *y) {
+    const int rc = d->m.cfg.proj_dtype == QO_PROJ_Q4_0 ? qo_matmul_q4_0(w, x, 1, in, out, y, d->threads)
+                                                       : qo_matmul_hvsq2(w, x, 1, in, out, y, d->threads, -1);
+    if (rc == 0) perturb_sums(d, y, out);
+    return rc;
+}
+
+void qo_decoder_set_perturbation(qo_decoder *d, uint32_t seed) {
+    d->perturb = seed;
+    d->calls = 0;
 }
 
 void qo_decoder_free(qo_decoder *d) {
@@ -145,9 +205,13 @@ int qo_decoder_forward(qo_decoder *d, int token, float *logits_out) {
     for (int l = 0; l < c->layers; l++) {
         const uint8_t *const *w = d->m.proj + (size_t)l * 7;
         qo_rmsnorm(d->xb, d->x, d->m.norms[2 * l], D, c->rms_eps);
+        perturb_outputs(d, d->xb, D);
         if (matmul(d, w[0], d->xb, D, Q, d->q) || matmul(d, w[1], d->xb, D, KV, d->k) ||
             matmul(d, w[2], d->xb, D, KV, d->v))
             return -1;
+        add_bias(d->q, bias_of(d, l, 0), Q);
+        add_bias(d->k, bias_of(d, l, 1), KV);
+        add_bias(d->v, bias_of(d, l, 2), KV);
         if (d->m.qk_norms) {
             /* head_rmsnorm (c/qwanto_decode.c:654-684, 1652-1655): per head, in place,
              * the same arithmetic as rmsnorm */
@@ -163,19 +227,25 @@ int qo_decoder_forward(qo_decoder *d, int token, float *logits_out) {
         qo_q8_quantize_vector(d->v, d->vcache[l] + (size_t)pos * KV, d->vscale[l] + (size_t)pos * groups, KV);
         qo_q8_attention(d->q, d->kcache[l], d->vcache[l], d->kscale[l], d->vscale[l], H, HK, HD, pos,
                         1.0f / sqrtf((float)HD), d->ctx, d->threads);
+        perturb_outputs(d, d->ctx, Q);
         if (matmul(d, w[3], d->ctx, Q, D, d->xb)) return -1;
+        add_bias(d->xb, bias_of(d, l, 3), D);
         for (int i = 0; i < D; i++) d->x[i] += d->xb[i];
         qo_rmsnorm(d->xb, d->x, d->m.norms[2 * l + 1], D, c->rms_eps);
+        perturb_outputs(d, d->xb, D);
         if (matmul(d, w[4], d->xb, D, I, d->gate) || matmul(d, w[5], d->xb, D, I, d->up)) return -1;
         for (int i = 0; i < I; i++) {
             const float g = d->gate[i];
             d->hidden[i] = (g / (1.0f + expf(-g))) * d->up[i];
         }
+        perturb_outputs(d, d->hidden, I);
         if (matmul(d, w[6], d->hidden, I, D, d->xb)) return -1;
         for (int i = 0; i < D; i++) d->x[i] += d->xb[i];
     }
     qo_rmsnorm(d->xb, d->x, d->m.final_norm, D, c->rms_eps);
+    perturb_outputs(d, d->xb, D);
     qo_matmul_f16(d->m.embed, d->xb, 1, D, c->vocab, d->logits, d->threads);
+    perturb_sums(d, d->logits, c->vocab);
     d->position++;
     if (logits_out) memcpy(logits_out, d->logits, (size_t)c->vocab * 4);
     return 0;

@@ -55,10 +55,12 @@ EXT_EXPORTS = (
     "qwn_hip_ext_gemv_group_partials", "qwn_hip_ext_gemv_group_device", "qwn_hip_ext_argmax_device",
     "qwn_hip_ext_mfma_image_bytes", "qwn_hip_ext_mfma_image_device", "qwn_hip_ext_gemm_mfma_device",
     "qwn_hip_ext_gemm_mfma_group_device", "qwn_hip_ext_upload_batch", "qwn_hip_ext_plan_residency",
+    "qwn_hip_ext_debug_mfma_int_sums", "qwn_hip_ext_debug_kv_read",
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
     "qwn_hip_decoder_forward", "qwn_hip_decoder_generate", "qwn_hip_decoder_prefill",
+    "qwn_hip_decoder_debug_kv_read", "qwn_hip_decoder_verify", "qwn_hip_decoder_truncate",
 )
 
 GEMV_INPUT = {"image": 0, "f32": 1, "rmsnorm": 2, "swiglu": 3}
@@ -181,7 +183,9 @@ class DecoderDesc(_Versioned):
                [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
                 ("projections", ctypes.c_void_p), ("embedding", ctypes.c_void_p),
                 ("input_norms", ctypes.c_void_p), ("post_norms", ctypes.c_void_p),
-                ("final_norm", ctypes.c_void_p), ("q_norms", ctypes.c_void_p), ("k_norms", ctypes.c_void_p)]
+                ("final_norm", ctypes.c_void_p), ("q_norms", ctypes.c_void_p), ("k_norms", ctypes.c_void_p),
+                ("q_biases", ctypes.c_void_p), ("k_biases", ctypes.c_void_p), ("v_biases", ctypes.c_void_p),
+                ("o_biases", ctypes.c_void_p)]
 
 
 class DecoderStats(_Versioned):
@@ -300,6 +304,8 @@ class Library:
                                                         ctypes.c_void_p, ctypes.c_void_p]
         lib.qwn_hip_ext_debug_int_sums.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
                                                    ctypes.c_void_p, ctypes.c_uint64]
+        lib.qwn_hip_ext_debug_mfma_int_sums.argtypes = [P(Handle), P(Handle), V, U32, V, ctypes.c_uint64]
+        lib.qwn_hip_ext_debug_kv_read.argtypes = [P(Handle), P(Handle), U32, U32, V, V, V, V]
         lib.qwn_hip_ext_gemv_group_partials.argtypes = [P(Handle), P(GemvGroupRequest)]
         lib.qwn_hip_ext_gemv_group_partials.restype = ctypes.c_uint32
         lib.qwn_hip_ext_gemv_group_device.argtypes = [P(Handle), P(GemvGroupRequest), V]
@@ -317,6 +323,9 @@ class Library:
         lib.qwn_hip_decoder_forward.argtypes = [P(Handle), P(Handle), ctypes.c_int32, V, V]
         lib.qwn_hip_decoder_generate.argtypes = [P(Handle), P(Handle), V, U32, U32, V, P(DecoderStats)]
         lib.qwn_hip_decoder_prefill.argtypes = [P(Handle), P(Handle), V, U32, V, V]
+        lib.qwn_hip_decoder_debug_kv_read.argtypes = [P(Handle), P(Handle), U32, U32, U32, V, V, V, V]
+        lib.qwn_hip_decoder_verify.argtypes = [P(Handle), P(Handle), V, U32, V, V]
+        lib.qwn_hip_decoder_truncate.argtypes = [P(Handle), P(Handle), U32]
 
     def last_error(self) -> str:
         buf = ctypes.create_string_buffer(512)
@@ -428,6 +437,27 @@ class Context:
         self.lib.check("debug_int_sums", self.lib.lib.qwn_hip_ext_debug_int_sums(
             self._h, ctypes.byref(h), _p(q8), _p(out), count))
         return out
+
+    def debug_mfma_sums(self, h: Handle, q8: np.ndarray, rows: int, nblk: int) -> np.ndarray:
+        """Exact int32 block dots of the MFMA GEMM: [batch][rows][nblk]."""
+        q8 = np.ascontiguousarray(q8, dtype=np.int8)
+        batch = q8.shape[0]
+        out = np.zeros((batch, rows, nblk), dtype=np.int32)
+        self.lib.check("debug_mfma_int_sums", self.lib.lib.qwn_hip_ext_debug_mfma_int_sums(
+            self._h, ctypes.byref(h), _p(q8), batch, _p(out), out.size))
+        return out
+
+    def kv_read(self, h: Handle, first: int, count: int, channels: int):
+        """Cached tokens [first, first+count) token-major: (keys, values,
+        key_scales, value_scales)."""
+        groups = (channels + 63) // 64
+        k = np.zeros((count, channels), dtype=np.int8)
+        v = np.zeros((count, channels), dtype=np.int8)
+        ks = np.zeros((count, groups), dtype=np.float32)
+        vs = np.zeros((count, groups), dtype=np.float32)
+        self.lib.check("debug_kv_read", self.lib.lib.qwn_hip_ext_debug_kv_read(
+            self._h, ctypes.byref(h), first, count, _p(k), _p(v), _p(ks), _p(vs)))
+        return k, v, ks, vs
 
     def image_bytes(self, h: Handle) -> int:
         """Bytes of one token's activation image for tensor h."""
@@ -613,17 +643,57 @@ class ResidentDecoder:
                                             dtype=np.float32)
             self._kn = np.ascontiguousarray(np.stack([model["layers"][l]["k_norm"] for l in range(L)]),
                                             dtype=np.float32)
+        # optional q/k/v/o biases, [layers][rows] per projection
+        self._bias = {}
+        for p in "qkvo":
+            if all(p + "_bias" in model["layers"][l] for l in range(L)):
+                self._bias[p] = np.ascontiguousarray(np.stack([model["layers"][l][p + "_bias"] for l in range(L)]),
+                                                     dtype=np.float32)
+            elif any(p + "_bias" in model["layers"][l] for l in range(L)):
+                raise ValueError(f"{p}_proj.bias must be present in every layer or in none")
         desc = DecoderDesc(hidden=D, intermediate=I, layers=L, heads=cfg["heads"], kv_heads=cfg["kv_heads"],
                            head_dim=cfg["head_dim"], vocab=cfg["vocab"], max_ctx=cfg["max_ctx"],
                            rope_theta=cfg["rope_theta"], rms_eps=cfg["rms_eps"],
                            projections=ctypes.cast(self._proj_arr, ctypes.c_void_p).value,
                            embedding=ctypes.addressof(self._embed), input_norms=_p(self._norm_in),
                            post_norms=_p(self._norm_post), final_norm=_p(self._final),
-                           q_norms=_p(self._qn), k_norms=_p(self._kn))
+                           q_norms=_p(self._qn), k_norms=_p(self._kn),
+                           **{p + "_biases": _p(self._bias.get(p)) for p in "qkvo"})
         self.handle = Handle()
         lib = ctx.lib
         lib.check("decoder_create", lib.lib.qwn_hip_decoder_create(ctx._h, ctypes.byref(desc),
                                                                    ctypes.byref(self.handle)))
+
+    def verify(self, tokens, logits: bool = True):
+        """One verify block: (logits [count][vocab] or None, greedy id after
+        each token [count])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = tokens.size
+        out = np.zeros((n, self.cfg["vocab"]), dtype=np.float32) if logits else None
+        ids = np.zeros(n, dtype=np.int32)
+        lib = self.ctx.lib
+        lib.check("decoder_verify", lib.lib.qwn_hip_decoder_verify(
+            self.ctx._h, ctypes.byref(self.handle), _p(tokens), n, _p(out), _p(ids)))
+        return out, ids
+
+    def truncate(self, position: int) -> None:
+        lib = self.ctx.lib
+        lib.check("decoder_truncate", lib.lib.qwn_hip_decoder_truncate(self.ctx._h, ctypes.byref(self.handle),
+                                                                       position))
+
+    def kv_read(self, layer: int, first: int, count: int):
+        """Layer `layer`'s cached tokens [first, first+count), token-major:
+        (keys, values, key_scales, value_scales)."""
+        C = self.cfg["kv_heads"] * self.cfg["head_dim"]
+        groups = (C + 63) // 64
+        k = np.zeros((count, C), dtype=np.int8)
+        v = np.zeros((count, C), dtype=np.int8)
+        ks = np.zeros((count, groups), dtype=np.float32)
+        vs = np.zeros((count, groups), dtype=np.float32)
+        lib = self.ctx.lib
+        lib.check("decoder_debug_kv_read", lib.lib.qwn_hip_decoder_debug_kv_read(
+            self.ctx._h, ctypes.byref(self.handle), layer, first, count, _p(k), _p(v), _p(ks), _p(vs)))
+        return k, v, ks, vs
 
     def forward(self, token: int, logits: bool = True):
         """One step; returns (logits or None, greedy next token)."""

@@ -61,16 +61,18 @@ __device__ __forceinline__ size_t scale_index(const KvCache &c, uint32_t token, 
     return (static_cast<size_t>(token / kKvPageTokens) * c.groups + group) * kKvPageTokens + token % kKvPageTokens;
 }
 
-// grid (groups, 2): y = 0 quantizes K, y = 1 quantizes V.  64 threads, one
-// per channel of the group.
+// grid (groups, 2, tokens): y = 0 quantizes K, y = 1 quantizes V; z is the
+// token of a block of consecutive tokens (key/value [z][channels], slot
+// token + z).  64 threads, one per channel of the group.
 __global__ __launch_bounds__(64) void kv_append_kernel(KvCache c, const float *__restrict__ key,
                                                        const float *__restrict__ value, uint32_t token,
                                                        const int32_t *__restrict__ token_ptr) {
     if (token_ptr) token = static_cast<uint32_t>(*token_ptr);
+    token += blockIdx.z;
     if (token >= c.max_tokens) return;
     const uint32_t g = blockIdx.x;
     const bool is_v = blockIdx.y == 1;
-    const float *src = is_v ? value : key;
+    const float *src = (is_v ? value : key) + static_cast<size_t>(blockIdx.z) * c.channels;
     const uint32_t ch = g * 64 + threadIdx.x;
     const bool valid = ch < c.channels;
     const float v = valid ? src[ch] : 0.0f;
@@ -88,6 +90,28 @@ __global__ __launch_bounds__(64) void kv_append_kernel(KvCache c, const float *_
     }
 }
 
+// Token-major copy of tokens [first, first + count): keys/values
+// [count][channels] int8 and scales [count][groups] fp32, the CPU cache's
+// layout (c/qwanto_turboquant.h:78-94), read through the same index
+// functions the attention kernels use.
+__global__ __launch_bounds__(256) void kv_gather_kernel(KvCache c, uint32_t first, uint32_t count,
+                                                        int8_t *__restrict__ keys, int8_t *__restrict__ values,
+                                                        float *__restrict__ key_scales,
+                                                        float *__restrict__ value_scales) {
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx < static_cast<uint64_t>(count) * c.channels) {
+        const uint32_t t = static_cast<uint32_t>(idx / c.channels), ch = static_cast<uint32_t>(idx % c.channels);
+        const uint32_t head = ch / c.head_dim, dim = ch % c.head_dim;
+        keys[idx] = c.keys[k_index(c, first + t, head, dim)];
+        values[idx] = c.values[v_offset(c, first + t, head, dim)];
+    }
+    if (idx < static_cast<uint64_t>(count) * c.groups) {
+        const uint32_t t = static_cast<uint32_t>(idx / c.groups), g = static_cast<uint32_t>(idx % c.groups);
+        key_scales[idx] = c.key_scales[scale_index(c, first + t, g)];
+        value_scales[idx] = c.value_scales[scale_index(c, first + t, g)];
+    }
+}
+
 struct AttnArgs {
     KvCache c;
     const float *query;
@@ -99,6 +123,8 @@ struct AttnArgs {
     uint32_t nsplit;
     float scale;
     const int32_t *position_ptr;  // non-null: tokens = *position_ptr + 1 (fixed split grid)
+    uint32_t head_mapped;         // 1: blockIdx.y is a query head (group 1), its KV head
+                                  // head * kv_heads / query_heads (any head ratio)
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -122,16 +148,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     extern __shared__ __align__(16) float sm[];
     const KvCache &c = a.c;
     const uint32_t D = c.head_dim;
-    const uint32_t kvh = blockIdx.y;
+    // query heads hbase .. hbase + G - 1 read KV head kvh
+    const uint32_t kvh = a.head_mapped ? blockIdx.y * c.kv_heads / a.query_heads : blockIdx.y;
+    const uint32_t G = a.group;
+    const uint32_t hbase = a.head_mapped ? blockIdx.y : blockIdx.y * G;
     const uint32_t split = blockIdx.x;
     const uint32_t t0 = split * a.split;
     const uint32_t tokens = a.position_ptr ? static_cast<uint32_t>(*a.position_ptr) + 1u : a.tokens;
-    const uint32_t G = a.group;
     if (t0 >= tokens) {
         // a split past the current position (fixed grid): an empty partial
         for (uint32_t i = threadIdx.x; i < G * D; i += blockDim.x) {
             const uint32_t g = i / D, d = i % D;
-            float *dst = a.partials + (static_cast<size_t>(kvh * G + g) * a.nsplit + split) * (D + 2);
+            float *dst = a.partials + (static_cast<size_t>(hbase + g) * a.nsplit + split) * (D + 2);
             dst[2 + d] = 0.0f;
             if (d == 0) {
                 dst[0] = -INFINITY;
@@ -148,7 +176,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 
     for (uint32_t i = threadIdx.x; i < GMAX * D; i += blockDim.x) {
         const uint32_t g = i / D, d = i % D;
-        q[i] = g < G ? a.query[(static_cast<size_t>(kvh) * G + g) * D + d] : 0.0f;
+        q[i] = g < G ? a.query[(static_cast<size_t>(hbase) + g) * D + d] : 0.0f;
     }
     __syncthreads();
 
@@ -266,7 +294,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
         const uint32_t g = i / D, d = i % D;
         float o = 0.0f;
         for (uint32_t ph = 0; ph < phases; ++ph) o += pv[(ph * GMAX + g) * D + d];
-        const uint32_t head = kvh * G + g;
+        const uint32_t head = hbase + g;
         float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
         dst[2 + d] = o;
         if (d == 0) {
@@ -311,7 +339,8 @@ hipError_t launch_split(const AttnArgs &args, hipStream_t stream) {
     const size_t lds = (static_cast<size_t>(GMAX) * D + kMaxSplitTokens * GMAX + 4 * GMAX +
                         static_cast<size_t>(phases) * GMAX * D) * sizeof(float);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attention_split_kernel<GMAX, FAST>), dim3(args.nsplit, args.c.kv_heads),
+    const uint32_t rows = args.head_mapped ? args.query_heads : args.c.kv_heads;
+    hipLaunchKernelGGL((attention_split_kernel<GMAX, FAST>), dim3(args.nsplit, rows),
                        dim3(kAttnThreads), lds, stream, args);
     return hipGetLastError();
 }
@@ -914,13 +943,10 @@ __device__ __forceinline__ void lds_wave_sync() {
 
 constexpr uint32_t kMfmaMaxSplits = 512;
 
-// waves per workgroup (four: eight, two per SIMD, measured slower at 4K and
-// 32K-token contexts on MI355X)
-__host__ __device__ constexpr int mfma_attention_waves(int, int) { return 4; }
-
-template <int D, int RT>
-__global__ __launch_bounds__(64 * mfma_attention_waves(D, RT)) void mfma_attention_kernel(MfmaAttnArgs a) {
-    constexpr int NW = mfma_attention_waves(D, RT);
+// NW waves per workgroup (mfma_attn_plan; eight, two per SIMD, measured
+// slower at 4K and 32K-token contexts)
+template <int D, int RT, int NW>
+__global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a) {
     constexpr int NG = D / 64;   // scale groups per head = MFMA k-steps
     constexpr int NT = 4;        // pages (16-token tiles) per 64-token block
     constexpr int HR = 4 * RT;   // query-head rows
@@ -1158,18 +1184,23 @@ __global__ __launch_bounds__(64 * mfma_attention_waves(D, RT)) void mfma_attenti
     }
 }
 
-template <int D, int RT>
+template <int D, int RT, int NW>
 hipError_t launch_mfma_attention_kernel(const MfmaAttnArgs &args, hipStream_t stream) {
-    hipLaunchKernelGGL((mfma_attention_kernel<D, RT>), dim3(args.nsplit, args.c.kv_heads),
-                       dim3(64 * mfma_attention_waves(D, RT)), 0, stream,
-                       args);
+    hipLaunchKernelGGL((mfma_attention_kernel<D, RT, NW>), dim3(args.nsplit, args.c.kv_heads), dim3(64 * NW), 0,
+                       stream, args);
     return hipGetLastError();
 }
 
+template <int D, int RT>
+hipError_t launch_mfma_attention_nw(const MfmaAttnArgs &args, uint32_t waves, hipStream_t stream) {
+    if (waves != 4) return hipErrorInvalidValue;
+    return launch_mfma_attention_kernel<D, RT, 4>(args, stream);
+}
+
 template <int D>
-hipError_t launch_mfma_attention_rt(const MfmaAttnArgs &args, hipStream_t stream) {
-    return args.group <= 4 ? launch_mfma_attention_kernel<D, 1>(args, stream)
-                           : launch_mfma_attention_kernel<D, 2>(args, stream);
+hipError_t launch_mfma_attention_rt(const MfmaAttnArgs &args, uint32_t waves, hipStream_t stream) {
+    return args.group <= 4 ? launch_mfma_attention_nw<D, 1>(args, waves, stream)
+                           : launch_mfma_attention_nw<D, 2>(args, waves, stream);
 }
 
 template <int D, int GMAX>
@@ -1261,30 +1292,34 @@ bool mfma_attention_supported(const KvCache &c, uint32_t query_heads) {
            query_heads % c.kv_heads == 0 && query_heads / c.kv_heads <= 8;
 }
 
-// Tokens per workgroup: one 64-token block per wave, doubled while the grid
-// would exceed 256 workgroups (one per CU, every workgroup resident in one
-// round, each wave streaming its blocks with the next block's loads in
-// flight, and few partials to merge); so at most kMfmaMaxSplits splits per
-// KV head.
-uint32_t mfma_split_tokens(const KvCache &c, uint32_t span, uint32_t waves) {
-    uint32_t s = 64 * waves;
-    while (static_cast<uint64_t>((span + s - 1) / s) * c.kv_heads > 256) s *= 2;
-    return s;
+// Launch plan over `span` tokens: four waves per workgroup, each streaming
+// 64-token blocks with the next block's loads in flight; tokens per
+// workgroup one block per wave, doubled while the grid would exceed 256
+// workgroups (one per CU, every workgroup resident in one round) or a KV
+// head kMfmaMaxSplits splits.  Measured on MI355X at 32 query / 8 KV heads:
+// one or two waves per workgroup and grids of up to 1024 workgroups (one
+// block per wave, no prefetch) ran slower at 4096 and at 32768 tokens.
+struct MfmaAttnPlan {
+    uint32_t waves, split, nsplit;
+};
+
+MfmaAttnPlan mfma_attn_plan(const KvCache &c, uint32_t span) {
+    MfmaAttnPlan p;
+    p.waves = 4;
+    uint64_t s = 64u * p.waves;
+    // stops at one split (s >= span) whatever the KV head count
+    while (s < span && ((span + s - 1) / s * c.kv_heads > 256 || (span + s - 1) / s > kMfmaMaxSplits)) s *= 2;
+    p.split = static_cast<uint32_t>(std::min<uint64_t>(s, 0x80000000u));
+    p.nsplit = static_cast<uint32_t>((static_cast<uint64_t>(span) + p.split - 1) / p.split);
+    return p;
 }
 
-uint32_t mfma_waves(const KvCache &c, uint32_t query_heads) {
-    const int rt = query_heads / c.kv_heads <= 4 ? 1 : 2;
-    return static_cast<uint32_t>(mfma_attention_waves(static_cast<int>(c.head_dim), rt));
-}
-
-uint32_t mfma_attention_launches(const KvCache &c, uint32_t query_heads, uint32_t span) {
-    const uint32_t s = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
-    return (span + s - 1) / s > 1 ? 2 : 1;
+uint32_t mfma_attention_launches(const KvCache &c, uint32_t, uint32_t span) {
+    return mfma_attn_plan(c, span).nsplit > 1 ? 2 : 1;
 }
 
 size_t mfma_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t span) {
-    const uint32_t s = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
-    const uint32_t nsplit = (span + s - 1) / s;
+    const uint32_t nsplit = mfma_attn_plan(c, span).nsplit;
     return nsplit > 1 ? static_cast<size_t>(query_heads) * nsplit * (c.head_dim + 2) : 0;
 }
 
@@ -1298,17 +1333,18 @@ hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *ou
     args.output = output;
     args.partials = partials;
     args.group = query_heads / c.kv_heads;
-    args.split = mfma_split_tokens(c, span, mfma_waves(c, query_heads));
-    args.nsplit = (span + args.split - 1) / args.split;
+    const MfmaAttnPlan plan = mfma_attn_plan(c, span);
+    args.split = plan.split;
+    args.nsplit = plan.nsplit;
     if ((args.nsplit > 1 && !partials) || args.nsplit > kMfmaMaxSplits) return hipErrorInvalidValue;
     args.scale = scale;
     args.position = position;
     args.position_ptr = position_ptr;
     hipError_t e;
     switch (c.head_dim) {
-    case 64: e = launch_mfma_attention_rt<64>(args, stream); break;
-    case 128: e = launch_mfma_attention_rt<128>(args, stream); break;
-    default: e = launch_mfma_attention_rt<256>(args, stream); break;
+    case 64: e = launch_mfma_attention_rt<64>(args, plan.waves, stream); break;
+    case 128: e = launch_mfma_attention_rt<128>(args, plan.waves, stream); break;
+    default: e = launch_mfma_attention_rt<256>(args, plan.waves, stream); break;
     }
     if (e != hipSuccess || args.nsplit == 1) return e;
     hipLaunchKernelGGL(decode_merge_kernel, dim3(query_heads), dim3(256), 0, stream, partials, output, args.nsplit,
@@ -1353,10 +1389,26 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
 }
 
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
-                            hipStream_t stream) {
-    if (token >= c.max_tokens) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2), dim3(64), 0, stream, c, key, value, token,
-                       static_cast<const int32_t *>(nullptr));
+                            hipStream_t stream, uint32_t count) {
+    if (count == 0 || token >= c.max_tokens || count > c.max_tokens - token) return hipErrorInvalidValue;
+    for (uint32_t done = 0; done < count;) {
+        const uint32_t n = std::min<uint32_t>(count - done, 32768u);
+        hipLaunchKernelGGL(kv_append_kernel, dim3(c.groups, 2, n), dim3(64), 0, stream, c,
+                           key + static_cast<size_t>(done) * c.channels, value + static_cast<size_t>(done) * c.channels,
+                           token + done, static_cast<const int32_t *>(nullptr));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        done += n;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_kv_gather(const KvCache &c, uint32_t first, uint32_t count, int8_t *keys, int8_t *values,
+                            float *key_scales, float *value_scales, hipStream_t stream) {
+    if (count == 0 || first > c.tokens || count > c.tokens - first) return hipErrorInvalidValue;
+    const uint64_t n = static_cast<uint64_t>(count) * c.channels;  // channels >= groups
+    hipLaunchKernelGGL(kv_gather_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, c, first,
+                       count, keys, values, key_scales, value_scales);
     return hipGetLastError();
 }
 
@@ -1375,9 +1427,21 @@ size_t attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32
 }
 
 namespace {
+// Query heads share a workgroup per KV head when they divide evenly into
+// groups of at most 8; any other ratio (query heads not a multiple of the
+// KV heads, fewer query than KV heads, or more than 8 per KV head) takes one
+// workgroup per query head with the reference's mapping
+// kv_head = head * kv_heads / query_heads (c/cuda/qwn_hypervsq2_cuda_abi.cu:184).
+void set_head_plan(AttnArgs &args, const KvCache &c, uint32_t query_heads) {
+    args.query_heads = query_heads;
+    const bool grouped = query_heads >= c.kv_heads && query_heads % c.kv_heads == 0 && query_heads / c.kv_heads <= 8;
+    args.head_mapped = grouped ? 0u : 1u;
+    args.group = grouped ? query_heads / c.kv_heads : 1u;
+}
+
 hipError_t launch_split_and_merge(AttnArgs &args, float *output, hipStream_t stream) {
     hipError_t e;
-    if (args.group <= 1) e = launch_fast_or_not<1>(args, stream);
+    if (args.head_mapped || args.group <= 1) e = launch_fast_or_not<1>(args, stream);
     else if (args.group <= 2) e = launch_fast_or_not<2>(args, stream);
     else if (args.group <= 4) e = launch_fast_or_not<4>(args, stream);
     else if (args.group <= 8) e = launch_fast_or_not<8>(args, stream);
@@ -1398,7 +1462,7 @@ size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads) {
 
 hipError_t launch_attention_at(const KvCache &c, const float *query, float *output, uint32_t query_heads,
                                const int32_t *position_ptr, float scale, float *partials, hipStream_t stream) {
-    if (query_heads % c.kv_heads != 0 || c.head_dim > 1024) return hipErrorInvalidValue;
+    if (query_heads == 0 || c.head_dim > 1024) return hipErrorInvalidValue;
     if (mfma_attention_supported(c, query_heads))
         return launch_mfma_attention(c, query, output, partials, query_heads, 0, position_ptr, c.max_tokens, scale,
                                      stream);
@@ -1406,8 +1470,7 @@ hipError_t launch_attention_at(const KvCache &c, const float *query, float *outp
     args.c = c;
     args.query = query;
     args.partials = partials;
-    args.query_heads = query_heads;
-    args.group = query_heads / c.kv_heads;
+    set_head_plan(args, c, query_heads);
     args.split = kDevicePositionSplit;
     args.nsplit = (c.max_tokens + kDevicePositionSplit - 1) / kDevicePositionSplit;
     args.scale = scale;
@@ -1417,8 +1480,7 @@ hipError_t launch_attention_at(const KvCache &c, const float *query, float *outp
 
 hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
     const KvCache &c = *a.cache;
-    if (a.position >= c.tokens || a.query_heads % c.kv_heads != 0 || c.head_dim > 1024)
-        return hipErrorInvalidValue;
+    if (a.position >= c.tokens || a.query_heads == 0 || c.head_dim > 1024) return hipErrorInvalidValue;
     if (mfma_attention_supported(c, a.query_heads))
         return launch_mfma_attention(c, a.query, a.output, a.partials, a.query_heads, a.position, nullptr,
                                      a.position + 1, a.scale, stream);
@@ -1426,8 +1488,7 @@ hipError_t launch_attention(const AttentionLaunch &a, hipStream_t stream) {
     args.c = c;
     args.query = a.query;
     args.partials = a.partials;
-    args.query_heads = a.query_heads;
-    args.group = a.query_heads / c.kv_heads;
+    set_head_plan(args, c, a.query_heads);
     args.tokens = a.position + 1;
     args.split = split_tokens(c, args.tokens);
     args.nsplit = (args.tokens + args.split - 1) / args.split;

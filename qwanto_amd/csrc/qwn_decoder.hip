@@ -150,6 +150,7 @@ struct Decoder {
     float *norms_in = nullptr, *norms_post = nullptr, *final_norm = nullptr, *cos_tab = nullptr,
           *sin_tab = nullptr, *rope_row = nullptr;
     float *q_norms = nullptr, *k_norms = nullptr;  // [layers][head_dim] or null
+    float *bias[4] = {};                           // q, k, v, o: [layers][rows] or null
     uint64_t *argmax = nullptr;
     uint32_t argmax_n = 0;
     uint8_t *head_image = nullptr;  // fp32 image of the final-norm output
@@ -168,8 +169,14 @@ struct Decoder {
     // image of the widest input, written by the quantize step
     uint8_t *pmimg = nullptr;
     int32_t *ppos = nullptr;
-    hipGraphExec_t prefill_exec[kPrefillTokens + 1][2] = {};
-    bool prefill_tried[kPrefillTokens + 1][2] = {};
+    // verify blocks: the LM head on every token of the block
+    float *vlogits = nullptr;       // [kPrefillTokens][vocab]
+    int32_t *vids = nullptr;        // [kPrefillTokens] greedy id after each token
+    uint8_t *vimg = nullptr;        // [kPrefillTokens][vimg_stride] fp32 LM-head images
+    uint32_t vimg_stride = 0;
+    // one graph per (block size, block kind: inner / ends the prompt / verify)
+    hipGraphExec_t prefill_exec[kPrefillTokens + 1][3] = {};
+    bool prefill_tried[kPrefillTokens + 1][3] = {};
     uint32_t position = 0;
     uint32_t launches = 0;
     uint32_t layer_launches = 0;  // kernels per layer
@@ -193,6 +200,13 @@ Decoder *decoder_of(Context *ctx, const QwnHipDecoderHandle *h) {
     if (!h || !header_ok(*h) || !h->opaque) return nullptr;
     auto *d = static_cast<Decoder *>(h->opaque);
     return std::find(ctx->decoders.begin(), ctx->decoders.end(), d) != ctx->decoders.end() ? d : nullptr;
+}
+
+// Bias of projection p (P_Q .. P_O) in layer l, or null.
+const float *layer_bias(const Decoder *d, uint32_t l, int p) {
+    if (!d->bias[p]) return nullptr;
+    const uint32_t rows = p == P_O ? d->hidden : (p == P_Q ? d->heads : d->kv_heads) * d->head_dim;
+    return d->bias[p] + static_cast<size_t>(l) * rows;
 }
 
 GemvGroupLaunch group(std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs) {
@@ -241,14 +255,22 @@ hipError_t enqueue_head(Decoder *d, const float *x, hipStream_t s) {
     return hipGetLastError();
 }
 
+// What follows the layers of a prefill block.
+enum BlockKind : uint32_t { kBlockInner = 0, kBlockLast = 1, kBlockVerify = 2 };
+
 // One prefill block of `m` prompt tokens at the device position (their ids
 // in feed): per layer the projections of all m tokens in one batched GEMV
 // each (weights read once per launch), RoPE and the Q8 append of the m
 // keys/values, causal attention of every token over the cache up to its
-// own position, residual adds in the GEMV epilogues.  `last`: the block
+// own position, residual adds in the GEMV epilogues.  kBlockLast: the block
 // ends the prompt, so the LM head runs on its last token and the greedy
-// token is recorded as a decode step would.
-hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
+// token is recorded as a decode step would.  kBlockVerify: the LM head runs
+// on every token of the block (one batched F16 GEMV, the head's weights
+// read once), logits [m][vocab] and each token's greedy successor; the
+// device position moves past the block and the last token's greedy id is
+// recorded as the step's.
+hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s) {
+    const bool last = kind == kBlockLast;
     hipError_t e;
     const EmbedArgs ea = embed_args(d);
     hipLaunchKernelGGL(prefill_embed_kernel, dim3((ea.units * 4 + 255) / 256, m), dim3(256), 0, s, ea, m, d->px,
@@ -262,7 +284,12 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
     const bool mfma = d->pmimg && mfma_batch(d->proj[P_Q]->kind, m);
     auto project = [&](std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs,
                        uint32_t mode, const float *x, const float *x2, const float *norm, uint32_t x_stride,
-                       bool add) {
+                       bool add, std::initializer_list<const float *> biases) {
+        const float *bv[kMaxGroup] = {};
+        {
+            uint32_t n = 0;
+            for (const float *b : biases) bv[n++] = b;
+        }
         const DeviceTensor &t0 = **ts.begin();
         hipError_t e2;
         if (mfma) {
@@ -275,7 +302,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
             for (const DeviceTensor *t : ts) tv[n++] = t;
             n = 0;
             for (float *o : outs) ov[n++] = o;
-            return launch_gemm_mfma_group(tv, ov, n, d->pmimg, d->pscales, m, nullptr, s, add);
+            return launch_gemm_mfma_group(tv, ov, n, d->pmimg, d->pscales, m, nullptr, s, add, nullptr, bv);
         }
         if ((e2 = launch_prepare_image(t0, mode, x, x2, norm, d->eps, m, x_stride, d->pimg, d->pimg_stride,
                                        d->pscales, nullptr, 0, s)) != hipSuccess)
@@ -287,6 +314,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
         g.image_stride = d->pimg_stride;
         g.scales = d->pscales;
         g.batch = m;
+        for (int i = 0; i < kMaxGroup; ++i) g.bias[i] = bv[i];
         return launch_gemv_group(g, s);
     };
     for (uint32_t l = 0; l < d->layers; ++l) {
@@ -295,8 +323,8 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
         const float *npost = d->norms_post + static_cast<size_t>(l) * D;
         const float *qn = d->q_norms ? d->q_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
         const float *kn = d->k_norms ? d->k_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
-        if ((e = project({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}, kInNorm, d->px, nullptr, nin, D,
-                         false)) != hipSuccess ||
+        if ((e = project({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}, kInNorm, d->px, nullptr, nin, D, false,
+                         {layer_bias(d, l, P_Q), layer_bias(d, l, P_K), layer_bias(d, l, P_V)})) != hipSuccess ||
             (e = launch_rope_append(d->caches[l], d->pq, d->heads, d->pk, d->pv, d->cos_tab, d->sin_tab, d->ppos, s,
                                     m, qn, kn, d->eps)) != hipSuccess)
             return e;
@@ -319,15 +347,28 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, bool last, hipStream_t s) {
                                              d->attn_scale, d->partials, s)) != hipSuccess)
                     return e;
         }
-        if ((e = project({w[P_O]}, {d->px}, kInF32, d->pattn, nullptr, nullptr, Q, true)) != hipSuccess ||
-            (e = project({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}, kInNorm, d->px, nullptr, npost, D, false)) !=
+        if ((e = project({w[P_O]}, {d->px}, kInF32, d->pattn, nullptr, nullptr, Q, true,
+                         {layer_bias(d, l, P_O)})) != hipSuccess ||
+            (e = project({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}, kInNorm, d->px, nullptr, npost, D, false, {})) !=
                 hipSuccess ||
-            (e = project({w[P_DOWN]}, {d->px}, kInSwiglu, d->pgate, d->pup, nullptr, I, true)) != hipSuccess)
+            (e = project({w[P_DOWN]}, {d->px}, kInSwiglu, d->pgate, d->pup, nullptr, I, true, {})) != hipSuccess)
             return e;
     }
     hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(64), 0, s, d->state, d->ppos, m, last ? 1u : 0u);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (last) return enqueue_head(d, d->px + static_cast<size_t>(m - 1) * D, s);
+    if (kind == kBlockVerify) {
+        if ((e = launch_norm_image(*d->embed, d->px, d->final_norm, d->eps, d->vimg, s, m, D, d->vimg_stride)) !=
+            hipSuccess)
+            return e;
+        GemvGroupLaunch head = group({d->embed}, {d->vlogits});
+        head.image = d->vimg;
+        head.image_stride = d->vimg_stride;
+        head.batch = m;
+        head.output_stride[0] = d->vocab;
+        if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
+        return launch_rows_argmax(d->vlogits, m, d->vocab, d->vocab, d->vids, d->state, s);
+    }
     return hipSuccess;
 }
 
@@ -346,6 +387,7 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         const float *kn = d->k_norms ? d->k_norms + static_cast<size_t>(l) * d->head_dim : nullptr;
         GemvGroupLaunch qkv = group({w[P_Q], w[P_K], w[P_V]}, {d->q, d->k, d->v});
         qkv.input_mode = kInNorm;
+        for (int p = P_Q; p <= P_V; ++p) qkv.bias[p] = layer_bias(d, l, p);
         qkv.x = d->x;
         qkv.norm = d->norms_in + static_cast<size_t>(l) * d->hidden;
         qkv.eps = d->eps;
@@ -380,6 +422,7 @@ hipError_t enqueue_step(Decoder *d, hipStream_t s, uint32_t *count) {
         GemvGroupLaunch o = group({w[P_O]}, {d->x});
         o.input_mode = kInF32;
         o.output_mode = kOutAdd;
+        o.bias[0] = layer_bias(d, l, P_O);
         o.x = d->attn;
         if ((e = launch_gemv_group(o, s)) != hipSuccess) return e;
         // gate and up rows paired in each workgroup: the epilogue writes
@@ -433,12 +476,19 @@ hipError_t run_prefill(Decoder *d, uint32_t count) {
     hipStream_t s = d->ctx->stream;
     for (uint32_t i = 0; i < count; i += kPrefillTokens) {
         const uint32_t m = std::min(kPrefillTokens, count - i);
-        const bool last = i + m == count;
-        const hipError_t e = run_captured(s, &d->prefill_exec[m][last], &d->prefill_tried[m][last],
-                                          [&] { return enqueue_prefill(d, m, last, s); });
+        const uint32_t kind = i + m == count ? kBlockLast : kBlockInner;
+        const hipError_t e = run_captured(s, &d->prefill_exec[m][kind], &d->prefill_tried[m][kind],
+                                          [&] { return enqueue_prefill(d, m, kind, s); });
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// One verify block of m <= kPrefillTokens tokens, already in feed.
+hipError_t run_verify(Decoder *d, uint32_t m) {
+    hipStream_t s = d->ctx->stream;
+    return run_captured(s, &d->prefill_exec[m][kBlockVerify], &d->prefill_tried[m][kBlockVerify],
+                        [&] { return enqueue_prefill(d, m, kBlockVerify, s); });
 }
 
 // Runs one step: the captured graph when capture worked, else the kernels.
@@ -547,6 +597,10 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         part(reinterpret_cast<void **>(&d->q_norms), static_cast<size_t>(d->layers) * d->head_dim * 4);
         part(reinterpret_cast<void **>(&d->k_norms), static_cast<size_t>(d->layers) * d->head_dim * 4);
     }
+    const float *const host_bias[4] = {desc->q_biases, desc->k_biases, desc->v_biases, desc->o_biases};
+    const uint32_t bias_rows[4] = {Q, KV, KV, D};
+    for (int p = 0; p < 4; ++p)
+        if (host_bias[p]) part(reinterpret_cast<void **>(&d->bias[p]), static_cast<size_t>(d->layers) * bias_rows[p] * 4);
     const uint32_t half = d->head_dim / 2;
     part(reinterpret_cast<void **>(&d->cos_tab), static_cast<size_t>(d->max_ctx) * half * 4);
     part(reinterpret_cast<void **>(&d->sin_tab), static_cast<size_t>(d->max_ctx) * half * 4);
@@ -574,6 +628,10 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
             part(reinterpret_cast<void **>(&d->pmimg),
                  std::max({mfma_image_bytes(*d->proj[P_DOWN]), mfma_image_bytes(*d->proj[P_Q]),
                            mfma_image_bytes(*d->proj[P_O])}));
+        d->vimg_stride = static_cast<uint32_t>((image_bytes(kF16, d->embed->units) + 15) & ~static_cast<size_t>(15));
+        part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
+        part(reinterpret_cast<void **>(&d->vlogits), P * d->vocab * 4);
+        part(reinterpret_cast<void **>(&d->vids), P * 4);
     }
     // attention partials of the device-position kernels
     KvCache proto;
@@ -672,6 +730,10 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     if (e == hipSuccess && desc->k_norms)
         e = hipMemcpyAsync(d->k_norms, desc->k_norms, static_cast<size_t>(d->layers) * d->head_dim * 4,
                            hipMemcpyHostToDevice, s);
+    for (int p = 0; p < 4; ++p)
+        if (e == hipSuccess && host_bias[p])
+            e = hipMemcpyAsync(d->bias[p], host_bias[p], static_cast<size_t>(d->layers) * bias_rows[p] * 4,
+                               hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->cos_tab, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->sin_tab, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipMemcpyAsync(d->feed, feed.data(), feed.size() * 4, hipMemcpyHostToDevice, s);
@@ -740,6 +802,41 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_reset(QwnCudaContextHandle *handle, QwnHipD
     return QWN_CUDA_STATUS_OK;
 }
 
+QWN_CUDA_ABI_API int qwn_hip_decoder_debug_kv_read(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                                   uint32_t layer, uint32_t first, uint32_t count, int8_t *keys,
+                                                   int8_t *values, float *key_scales, float *value_scales) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !keys || !values || !key_scales || !value_scales || count == 0) {
+        set_error("invalid decoder KV read");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || layer >= d->layers || first > d->position || count > d->position - first) {
+        set_error("decoder KV read beyond the decoder's layers or position");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    KvCache c = d->caches[layer];
+    c.tokens = d->position;
+    const size_t vb = static_cast<size_t>(count) * c.channels, sb = static_cast<size_t>(count) * c.groups * 4;
+    hipError_t e = hipSetDevice(ctx->device);
+    void *buf = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&buf, 2 * vb + 2 * sb + 256);
+    uint8_t *b = static_cast<uint8_t *>(buf);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess)
+        e = launch_kv_gather(c, first, count, reinterpret_cast<int8_t *>(b), reinterpret_cast<int8_t *>(b + vb),
+                             reinterpret_cast<float *>(b + 2 * vb), reinterpret_cast<float *>(b + 2 * vb + sb),
+                             ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(keys, b, vb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(values, b + vb, vb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(key_scales, b + 2 * vb, sb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(value_scales, b + 2 * vb + sb, sb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (buf) (void)hipFree(buf);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("decoder KV read", e);
+}
+
 QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h, int32_t token,
                                              float *logits, int32_t *next_token) {
     Context *ctx = context_of(handle);
@@ -804,6 +901,65 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *handle, QwnHi
     if (next_token) *next_token = st[0];
     const uint64_t blocks = (count + kPrefillTokens - 1) / kPrefillTokens;
     ctx->telemetry.gpu_matmul_count += blocks * 4ull * d->layers + 1;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_verify(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                            const int32_t *tokens, uint32_t count, float *logits,
+                                            int32_t *next_tokens) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !tokens || count == 0 || count > kPrefillTokens) {
+        set_error("invalid verify request (1..%u tokens)", kPrefillTokens);
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || static_cast<uint64_t>(d->position) + count > d->max_ctx) {
+        set_error("verify block does not fit the decoder's context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < count; ++i)
+        if (tokens[i] < 0 || static_cast<uint32_t>(tokens[i]) >= d->vocab) {
+            set_error("verify token %u out of range", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+    hipStream_t s = ctx->stream;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->feed + d->position, tokens, static_cast<size_t>(count) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = run_verify(d, count);
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, d->vlogits, static_cast<size_t>(count) * d->vocab * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && next_tokens)
+        e = hipMemcpyAsync(next_tokens, d->vids, static_cast<size_t>(count) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail("decoder verify", e);
+    d->position += count;
+    ctx->telemetry.gpu_matmul_count += 4ull * d->layers + 1;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_truncate(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                              uint32_t position) {
+    Context *ctx = context_of(handle);
+    if (!ctx) {
+        set_error("invalid context handle");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || position > d->position) {
+        set_error("truncate position beyond the decoder's tokens");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    // the cache slots past `position` are overwritten by the next tokens;
+    // only the device position and the host mirror move
+    const int32_t pos = static_cast<int32_t>(position);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->state + 1, &pos, 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail("decoder truncate", e);
+    d->position = position;
     return QWN_CUDA_STATUS_OK;
 }
 

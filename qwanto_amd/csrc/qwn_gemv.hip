@@ -111,12 +111,16 @@ __global__ __launch_bounds__(256) void image_from_f32_kernel(const float *__rest
     dst[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// RMSNorm of one token into an F16 tensor's fp32 image (the tied LM head
+// RMSNorm of a token into an F16 tensor's fp32 image (the tied LM head
 // input): y = (x * 1/sqrt(mean(x^2) + eps)) * w (c/qwanto_decode.c:627-652).
-// One workgroup of 1024 threads.
+// One workgroup of 1024 threads per token: token blockIdx.x reads
+// x + blockIdx.x * x_stride and writes image + blockIdx.x * image_stride.
 __global__ __launch_bounds__(1024) void norm_image_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                          uint32_t K, uint32_t units, float eps, uint8_t *image) {
+                                                          uint32_t K, uint32_t units, float eps, uint8_t *image,
+                                                          uint32_t x_stride, uint32_t image_stride) {
     __shared__ float red[1024 / kWaveSize];
+    x += static_cast<size_t>(blockIdx.x) * x_stride;
+    image += static_cast<size_t>(blockIdx.x) * image_stride;
     float ss = 0.0f;
     for (uint32_t k = threadIdx.x; k < K; k += blockDim.x) ss = fmaf(x[k], x[k], ss);
     ss = wave_sum_all(ss);
@@ -359,6 +363,7 @@ struct GemvArgs {
     // output
     uint32_t output_stride[kMaxGroup];  // elements between tokens, per job
     uint64_t *argmax_partials;
+    const float *bias[kMaxGroup];       // per job: null, or [rows] added to the product
 };
 
 // Separately rounded product and sum (never contracted into an fma).
@@ -566,6 +571,9 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     }
     float resid = 0.0f;
     if (a.output_mode == kOutAdd && writer) resid = output[row];
+    const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
+    float bias_v = 0.0f;
+    if (bias && writer) bias_v = bias[row];
 
     // 2. The LDS image.  Fused: this thread's block after the norm/SwiGLU,
     //    quantized with the workgroup-wide scale (c/qwanto_kernels.c:354-433)
@@ -768,6 +776,9 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             // projection before vec_add(x, y) (c/qwanto_decode.c:1925, 1955), so no
             // contraction into one fused multiply-add here
             if (KIND != kF16) s = mul_rounded(s, tok_scale[t]);
+            // the projection's bias, added to the stored product as the CPU's
+            // add_bias (c/qwanto_decode.c:926-929, 1649-1651, 1722)
+            if (bias) s = add_rounded(s, bias_v);
             if (a.output_mode == kOutAdd)
                 s = add_rounded(t == 0 ? resid : output[static_cast<size_t>(t) * out_stride + row], s);
             if (t == 0) first_out = s;
@@ -814,7 +825,6 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 // waves that split one row group's K combine their partial tiles through
 // LDS in wave order.
 constexpr int kMfmaTokens = 16;
-constexpr uint64_t kMfmaLdsLimit = 160 * 1024;  // LDS per workgroup on gfx950
 
 __host__ __device__ constexpr size_t mfma_image_block_bytes() { return 16 * 256 + 16 * 4; }
 
@@ -917,6 +927,8 @@ struct MfmaArgs {
     uint32_t ntok;
     uint32_t vec_out;      // bit i: job i's rows may be stored 4 at a time (16-byte aligned)
     uint32_t accumulate;   // out += W x (residual add) instead of out = W x
+    int32_t *dump;         // DUMP kernels: exact int32 block dots [token][row][nblk] of job 0
+    const float *bias[kMaxGroup];  // per job: null, or [rows] added to each token's product
 };
 
 constexpr int kMfmaMaxWaves = 8;
@@ -945,7 +957,7 @@ __device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, u
 // weight loads) of the whole chunk are issued before the first MFMA.
 // STAGE: the row group's weight tiles were copied to LDS (payload at 0, meta
 // at `meta_lds`) and the A operands are read from there.
-template <int NB, int RT, bool STAGE>
+template <int NB, int RT, bool STAGE, bool DUMP>
 __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
                                            const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
                                            uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
@@ -1018,6 +1030,15 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
                 av.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
                 ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, B[i][sl], ci, 0, 0, 0);
             }
+            if constexpr (DUMP) {
+                // sum over the block's octants of multiplier * sum (code-1)*a
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = r0 + 16 * t + 4 * g + r;
+                    if (row < rows && m < a.ntok)
+                        a.dump[(static_cast<size_t>(m) * rows + row) * a.nblk + b0 + i] = ci[r];
+                }
+            }
             // C element r of this lane is row 4g + r of the tile: its
             // d_base / m_base were loaded by lane 4g + r
 #pragma unroll
@@ -1048,7 +1069,7 @@ __device__ __forceinline__ uint32_t lds_swizzle(uint32_t piece, uint32_t npieces
 // its B operand, so lane (g, m) accumulates tokens 4g .. 4g+3 of weight row
 // m: the block scale it applies is the one it loaded itself, and the four
 // tokens' activation sums are one 16-byte load.
-template <int NB, int RT, bool STAGE>
+template <int NB, int RT, bool STAGE, bool DUMP>
 __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
                                               const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
                                               uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
@@ -1099,6 +1120,15 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
             mfma_v4i ci = {0, 0, 0, 0};
             // C[token][row]: element r is token 4g + r of row m
             ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(xv, wv, ci, 0, 0, 0);
+            if constexpr (DUMP) {
+                // sum (nibble-8)*a of the block for token 4g + r, row m
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = r0 + 16 * t + m, tok = 4 * g + r;
+                    if (row < rows && tok < a.ntok)
+                        a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r] - corr[r];
+                }
+            }
             const uint32_t word = q < 2 ? Mt[i][t].x : Mt[i][t].y;
             const float d = half_to_float((word >> (16 * (q & 1))) & 0xffffu);
 #pragma unroll
@@ -1107,7 +1137,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
     }
 }
 
-template <int KIND, int NB, int RT, bool STAGE>
+template <int KIND, int NB, int RT, bool STAGE, bool DUMP>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(MfmaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
@@ -1127,6 +1157,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                             : job == 2 ? a.output_stride[2]
                                        : a.output_stride[3];
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
+    const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
     const uint32_t r0 = (blockIdx.x - first) * (16 * RT);
     const uint32_t kb0 = ks * a.nb;
     const uint32_t kb1 = min(a.nblk, kb0 + a.nb);
@@ -1169,10 +1200,10 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
     for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
         if constexpr (KIND == kHvsq2)
-            mfma_chunk<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+            mfma_chunk<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
                                       min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
         else
-            mfma_chunk_q4<NB, RT, STAGE>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
                                          min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces, acc);
     }
 
@@ -1215,7 +1246,8 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                     const uint32_t row = r0 + 16 * t + m;
                     if (row >= rows) continue;
                     float *dst = output + static_cast<size_t>(tok) * stride + row;
-                    const float v = mul_rounded(acc[t][r], xs);
+                    float v = mul_rounded(acc[t][r], xs);
+                    if (bias) v = add_rounded(v, bias[row]);
                     *dst = a.accumulate ? add_rounded(*dst, v) : v;
                 }
             }
@@ -1232,6 +1264,11 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             if (vec && n0 + 4 <= rows) {
                 float4 v = make_float4(mul_rounded(acc[t][0], xs), mul_rounded(acc[t][1], xs),
                                        mul_rounded(acc[t][2], xs), mul_rounded(acc[t][3], xs));
+                if (bias) {
+                    const float4 bv = *reinterpret_cast<const float4 *>(bias + n0);
+                    v = make_float4(add_rounded(v.x, bv.x), add_rounded(v.y, bv.y), add_rounded(v.z, bv.z),
+                                    add_rounded(v.w, bv.w));
+                }
                 if (a.accumulate) {
                     const float4 o = *reinterpret_cast<const float4 *>(dst);
                     v = make_float4(add_rounded(o.x, v.x), add_rounded(o.y, v.y), add_rounded(o.z, v.z),
@@ -1242,7 +1279,8 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     if (n0 + r < rows) {
-                        const float v = mul_rounded(acc[t][r], xs);
+                        float v = mul_rounded(acc[t][r], xs);
+                        if (bias) v = add_rounded(v, bias[n0 + r]);
                         dst[r] = a.accumulate ? add_rounded(dst[r], v) : v;
                     }
             }
@@ -1658,6 +1696,9 @@ bool group_valid(const GemvGroupLaunch &g) {
         return false;
     }
     if (g.output_mode == kOutArgmax && (g.batch != 1 || !g.argmax_partials || g.njobs != 1)) return false;
+    if (g.output_mode == kOutArgmax || g.output_mode == kOutSwiglu)
+        for (int i = 0; i < g.njobs; ++i)
+            if (g.bias[i]) return false;
     if (g.output_mode == kOutSwiglu &&
         (g.batch != 1 || g.njobs != 2 || g.tensors[0]->rows != g.tensors[1]->rows))
         return false;
@@ -1692,6 +1733,7 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         args.output[i] = g.outputs[i];
         args.rows[i] = ti.rows;
         args.output_stride[i] = g.output_stride[i] ? g.output_stride[i] : ti.rows;
+        args.bias[i] = g.bias[i];
         args.job_block[i] = blk;
         blk += ti.tiles / w;
     }
@@ -1765,7 +1807,7 @@ namespace {
 // within the unrolled chunk of 5, then more (up to 8) while the launch has
 // fewer than 4096 waves and every wave keeps two blocks or more.  STAGE
 // where the row group is a whole number of wave tiles and they fit in LDS
-// (64 KB with the partial tiles).
+// (kMfmaLdsLimit with the partial tiles).
 struct MfmaPlan {
     int nbt = 0, rt = 1;
     bool stage = false;
@@ -1807,10 +1849,17 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
 template <int KIND, int NB, int RT>
 hipError_t launch_mfma_rt(bool stage, uint32_t grid, uint32_t threads, size_t lds, const MfmaArgs &a,
                           hipStream_t stream) {
-    if (stage)
-        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true>), dim3(grid), dim3(threads), lds, stream, a);
-    else
-        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false>), dim3(grid), dim3(threads), lds, stream, a);
+    if (a.dump) {
+        if (stage)
+            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, true>), dim3(grid), dim3(threads), lds, stream, a);
+        else
+            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, true>), dim3(grid), dim3(threads), lds, stream,
+                               a);
+    } else if (stage) {
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, false>), dim3(grid), dim3(threads), lds, stream, a);
+    } else {
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, false>), dim3(grid), dim3(threads), lds, stream, a);
+    }
     return hipGetLastError();
 }
 
@@ -1823,8 +1872,9 @@ hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, h
 
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
-                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate) {
-    if (count == 0 || count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
+                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate,
+                                  int32_t *dump, const float *const *biases) {
+    if ((dump && count != 1) || count == 0 || count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
         batch > static_cast<uint32_t>(kMfmaTokens))
         return hipErrorInvalidValue;
     const DeviceTensor &t0 = *tensors[0];
@@ -1851,7 +1901,9 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             a.rows[i] = t.rows;
             a.tiles[i] = t.tiles;
             a.output_stride[i] = output_strides && output_strides[i] ? output_strides[i] : t.rows;
-            if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0)
+            a.bias[i] = biases ? biases[i] : nullptr;
+            if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0 &&
+                (reinterpret_cast<uintptr_t>(a.bias[i]) & 15u) == 0)
                 a.vec_out |= 1u << i;
             grid += (t.rows + 16 * p.rt - 1) / (16 * p.rt);
         }
@@ -1870,6 +1922,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.scales = scales;
     a.ntok = batch;
     a.accumulate = accumulate ? 1u : 0u;
+    a.dump = dump;
     if (t0.kind == kQ4_0) {
         switch (p.nbt) {
         case 2: return launch_mfma_nb<kQ4_0, 2>(p, grid, a, stream);
@@ -1894,9 +1947,43 @@ hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const f
 }
 
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,
-                             hipStream_t stream) {
-    if (t.kind != kF16) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(norm_image_kernel, dim3(1), dim3(1024), 0, stream, x, norm, t.cols, t.units, eps, image);
+                             hipStream_t stream, uint32_t count, uint32_t x_stride, uint32_t image_stride) {
+    if (t.kind != kF16 || count == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(norm_image_kernel, dim3(count), dim3(1024), 0, stream, x, norm, t.cols, t.units, eps, image,
+                       x_stride, image_stride);
+    return hipGetLastError();
+}
+
+// First index of the largest value of each row of [rows][cols] fp32
+// (c/qwanto_decode.c:2048-2065; NaN never wins): one workgroup per row.
+__global__ __launch_bounds__(1024) void rows_argmax_kernel(const float *__restrict__ v, uint32_t cols, uint32_t stride,
+                                                           int32_t *__restrict__ ids, int32_t *last_out) {
+    __shared__ uint64_t red[1024 / kWaveSize];
+    const float *row = v + static_cast<size_t>(blockIdx.x) * stride;
+    uint64_t key = 0;
+    for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
+        const uint64_t k = argmax_key(row[i], i);
+        key = k > key ? k : key;
+    }
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) {
+        const uint64_t o = shfl_xor_u64(key, off);
+        key = o > key ? o : key;
+    }
+    if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t best = red[0];
+        for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) best = red[w] > best ? red[w] : best;
+        const int32_t id = best ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+        ids[blockIdx.x] = id;
+        if (last_out && blockIdx.x == gridDim.x - 1) *last_out = id;
+    }
+}
+
+hipError_t launch_rows_argmax(const float *v, uint32_t rows, uint32_t cols, uint32_t stride, int32_t *ids,
+                              int32_t *last_out, hipStream_t stream) {
+    if (rows == 0 || cols == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rows_argmax_kernel, dim3(rows), dim3(1024), 0, stream, v, cols, stride, ids, last_out);
     return hipGetLastError();
 }
 

@@ -174,6 +174,8 @@ struct GemvGroupLaunch {
     uint64_t *argmax_partials = nullptr;  // kOutArgmax: [grid] packed keys
     uint32_t output_stride[kMaxGroup] = {};  // elements between tokens per job (0: its rows)
     int waves = 0;                        // workgroup size in waves (0: chosen here)
+    const float *bias[kMaxGroup] = {};    // per job: null, or [rows] added to the stored product
+                                          // (STORE / ADD: before the residual add)
 };
 
 // Workgroups a grouped launch uses (the argmax partial count).
@@ -201,8 +203,12 @@ hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const f
 // accumulate: outputs += W x_t * scales[t] (the residual stream).
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
-                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate = false);
+                                  const uint32_t *output_strides, hipStream_t stream, bool accumulate = false,
+                                  int32_t *dump = nullptr, const float *const *biases = nullptr);
 constexpr uint32_t kMfmaMinTokens = 8;
+// LDS per workgroup the MFMA GEMM plans its staging against: gfx950's
+// 160 KB (context creation refuses a device that reports less).
+constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
 // Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV:
 // HyperVSQ-2 from 8 tokens; Q4_0 (one 16x16x32 MFMA per 32-weight block,
 // the same time at 8 tokens as at 16) from a full 16-token tile.
@@ -210,9 +216,15 @@ inline bool mfma_batch(uint32_t kind, uint32_t batch) {
     return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= 16);
 }
 
-// RMSNorm of one fp32 token into the fp32 image of an F16 tensor.
+// RMSNorm of `count` fp32 tokens ([count][x_stride]) into fp32 images of an
+// F16 tensor ([count][image_stride]).
 hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float *norm, float eps, uint8_t *image,
-                             hipStream_t stream);
+                             hipStream_t stream, uint32_t count = 1, uint32_t x_stride = 0,
+                             uint32_t image_stride = 0);
+// First index of the largest value of every row of [rows][cols] fp32 into
+// ids[rows]; the last row's also into *last_out when given.
+hipError_t launch_rows_argmax(const float *v, uint32_t rows, uint32_t cols, uint32_t stride, int32_t *ids,
+                              int32_t *last_out, hipStream_t stream);
 // Reduce argmax partials [n] to the winning row index (first index on ties).
 hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream);
 
@@ -253,10 +265,16 @@ hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_hea
                               const int32_t *pos_ptr, hipStream_t stream, uint32_t count = 1,
                               const float *q_norm = nullptr, const float *k_norm = nullptr, float eps = 0.0f);
 
-// Quantize one token's fp32 K and V [channels] into slot `token`.
+// Quantize `count` consecutive tokens' fp32 K and V ([count][channels])
+// into slots token .. token + count - 1 (one launch per 32768 tokens).
 hipError_t launch_kv_append(const KvCache &c, const float *key,
                             const float *value, uint32_t token,
-                            hipStream_t stream);
+                            hipStream_t stream, uint32_t count = 1);
+
+// Token-major copy of cached tokens [first, first + count) (debug readback):
+// keys/values [count][channels], scales [count][groups].
+hipError_t launch_kv_gather(const KvCache &c, uint32_t first, uint32_t count, int8_t *keys, int8_t *values,
+                            float *key_scales, float *value_scales, hipStream_t stream);
 
 struct AttentionLaunch {
     const KvCache *cache;

@@ -154,23 +154,35 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     }
     float *hscales = reinterpret_cast<float *>(hin + in_bytes);
     for (uint32_t b = 0; b < r->batch; ++b) hscales[b] = r->input_scales ? r->input_scales[b] : r->input_scale;
-    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, in_bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
-        (!quantize && (e = hipMemcpyAsync(ctx->dev_scales.ptr, hscales, scale_bytes, hipMemcpyHostToDevice,
-                                          ctx->stream)) != hipSuccess))
+    // int8 MFMA tiles of 16 tokens (HyperVSQ-2 from 8 tokens, Q4_0 from 16)
+    const bool mfma = qwn::mfma_batch(t.kind, r->batch);
+    // Small requests skip the copy engines: the image kernel reads the
+    // activations (and the GEMV its scales) straight from the pinned staging
+    // buffer, and the GEMV epilogue stores into the pinned output buffer, so a
+    // call is two kernels and one synchronisation instead of three DMA
+    // transfers around them.  Outputs of 64K+ rows (the LM head) and the MFMA
+    // path keep the device buffers and DMA.
+    const bool zero_copy = !mfma && r->rows < 65536;
+    if (!zero_copy &&
+        ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, in_bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+         (!quantize && (e = hipMemcpyAsync(ctx->dev_scales.ptr, hscales, scale_bytes, hipMemcpyHostToDevice,
+                                           ctx->stream)) != hipSuccess)))
         return hip_fail("activation upload", e);
+    const void *act = zero_copy ? static_cast<const void *>(hin) : ctx->dev_in.ptr;
+    float *scales_dev = zero_copy ? (quantize ? static_cast<float *>(ctx->dev_scales.ptr) : hscales)
+                                  : static_cast<float *>(ctx->dev_scales.ptr);
+    float *out_dev = zero_copy ? static_cast<float *>(ctx->host_out.ptr) : static_cast<float *>(ctx->dev_out.ptr);
     const double transfer_ms = ms_since(t_transfer);
 
     qwn::GemvLaunch g{};
     g.tensor = &t;
     g.image = ctx->dev_img.ptr;
     g.image_stride = img_stride;
-    g.scales = static_cast<const float *>(ctx->dev_scales.ptr);
+    g.scales = scales_dev;
     g.scale = r->input_scale;
-    g.output = static_cast<float *>(ctx->dev_out.ptr);
+    g.output = out_dev;
     g.batch = r->batch;
     g.output_stride = r->rows;
-    // int8 MFMA tiles of 16 tokens (HyperVSQ-2 from 8 tokens, Q4_0 from 16)
-    const bool mfma = qwn::mfma_batch(t.kind, r->batch);
     const size_t mfma_img = qwn::mfma_image_bytes(t);
     if (mfma && ((e = ctx->dev_work.ensure(mfma_img + (quantize ? in_bytes / 4 : 0))) != hipSuccess))
         return hip_fail("MFMA workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
@@ -198,18 +210,18 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
         }
     } else {
         if (quantize)
-            e = qwn::launch_quantize_image(t, static_cast<const float *>(ctx->dev_in.ptr), r->batch, dev_stride,
+            e = qwn::launch_quantize_image(t, static_cast<const float *>(act), r->batch, dev_stride,
                                            static_cast<uint8_t *>(ctx->dev_img.ptr), img_stride,
                                            static_cast<float *>(ctx->dev_scales.ptr), nullptr, 0, ctx->stream);
         else
-            e = qwn::launch_image(t, ctx->dev_in.ptr, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr),
-                                  img_stride, ctx->stream);
+            e = qwn::launch_image(t, act, r->batch, dev_stride, static_cast<uint8_t *>(ctx->dev_img.ptr), img_stride,
+                                  ctx->stream);
         if (e != hipSuccess) return hip_fail("activation image launch", e);
         if ((e = qwn::launch_gemv(g, ctx->stream)) != hipSuccess) return hip_fail("GEMV launch", e);
     }
     (void)hipEventRecord(ctx->ev_end, ctx->stream);
-    if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,
-                            ctx->stream)) != hipSuccess)
+    if (!zero_copy && (e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, out_bytes, hipMemcpyDeviceToHost,
+                                          ctx->stream)) != hipSuccess)
         return hip_fail("result download", e);
     const auto t_sync = std::chrono::steady_clock::now();
     if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail("GEMV synchronize", e);
@@ -330,6 +342,17 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *op
     if (hipGetDeviceCount(&n) != hipSuccess || options->device_id >= n) {
         set_error("device %d is not available", options->device_id);
         return QWN_CUDA_STATUS_UNAVAILABLE;
+    }
+    {
+        // the kernels are gfx950 code objects and the MFMA GEMM stages up to
+        // kMfmaLdsLimit bytes of LDS per workgroup
+        hipDeviceProp_t dp{};
+        if (hipGetDeviceProperties(&dp, options->device_id) != hipSuccess ||
+            std::strncmp(dp.gcnArchName, "gfx950", 6) != 0 || dp.sharedMemPerBlock < qwn::kMfmaLdsLimit) {
+            set_error("device %d (%s) is not a gfx950 device with %llu bytes of LDS per workgroup", options->device_id,
+                      dp.gcnArchName, static_cast<unsigned long long>(qwn::kMfmaLdsLimit));
+            return QWN_CUDA_STATUS_UNSUPPORTED;
+        }
     }
     auto *ctx = new (std::nothrow) Context();
     if (!ctx) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
@@ -716,16 +739,15 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_append(QwnCudaContextHandle *handle,
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return hip_fail("hipSetDevice", e);
     const size_t bytes = static_cast<size_t>(c.channels) * sizeof(float);
-    if ((e = ctx->host_in.ensure(2 * bytes)) != hipSuccess || (e = ctx->dev_in.ensure(2 * bytes)) != hipSuccess)
+    if ((e = ctx->host_in.ensure(2 * bytes)) != hipSuccess)
         return hip_fail("KV workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
     const auto t0 = std::chrono::steady_clock::now();
+    // the quantize kernel reads K and V straight from the pinned staging buffer
     uint8_t *hin = static_cast<uint8_t *>(ctx->host_in.ptr);
     std::memcpy(hin, r->host_key, bytes);
     std::memcpy(hin + bytes, r->host_value, bytes);
-    const float *dk = static_cast<const float *>(ctx->dev_in.ptr);
-    const float *dv = reinterpret_cast<const float *>(static_cast<uint8_t *>(ctx->dev_in.ptr) + bytes);
-    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, hin, 2 * bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
-        return hip_fail("Q8 KV upload", e);
+    const float *dk = reinterpret_cast<const float *>(hin);
+    const float *dv = reinterpret_cast<const float *>(hin + bytes);
     (void)hipEventRecord(ctx->ev_start, ctx->stream);
     if ((e = qwn::launch_kv_append(c, dk, dv, c.tokens, ctx->stream)) != hipSuccess)
         return hip_fail("Q8 KV quantize launch", e);
@@ -754,8 +776,9 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *handl
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
     ResidentKv *rk = cache_of(ctx, r->cache);
-    if (!rk || r->kv_heads != rk->c.kv_heads || r->head_dim != rk->c.head_dim || r->position >= rk->c.tokens ||
-        r->query_heads % r->kv_heads != 0) {
+    // any query/KV head ratio: query head h reads KV head h * kv_heads / query_heads
+    // (c/cuda/qwn_hypervsq2_cuda_abi.cu:184)
+    if (!rk || r->kv_heads != rk->c.kv_heads || r->head_dim != rk->c.head_dim || r->position >= rk->c.tokens) {
         set_error("invalid Q8 KV-cache attention request");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
@@ -765,18 +788,16 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *handl
     const size_t qbytes = static_cast<size_t>(r->query_heads) * c.head_dim * sizeof(float);
     const size_t work = qwn::attention_workspace_floats(c, r->query_heads, r->position) * sizeof(float);
     if ((e = ctx->host_in.ensure(qbytes)) != hipSuccess || (e = ctx->host_out.ensure(qbytes)) != hipSuccess ||
-        (e = ctx->dev_in.ensure(qbytes)) != hipSuccess || (e = ctx->dev_out.ensure(qbytes)) != hipSuccess ||
         (e = ctx->dev_work.ensure(work)) != hipSuccess)
         return hip_fail("attention workspace allocation", e, QWN_CUDA_STATUS_OUT_OF_MEMORY);
     const auto t0 = std::chrono::steady_clock::now();
+    // the kernels read the query from and write the output to the pinned
+    // staging buffers directly (no copy-engine transfers around them)
     std::memcpy(ctx->host_in.ptr, r->host_query, qbytes);
-    if ((e = hipMemcpyAsync(ctx->dev_in.ptr, ctx->host_in.ptr, qbytes, hipMemcpyHostToDevice, ctx->stream)) !=
-        hipSuccess)
-        return hip_fail("Q8 KV query upload", e);
     qwn::AttentionLaunch a{};
     a.cache = &c;
-    a.query = static_cast<const float *>(ctx->dev_in.ptr);
-    a.output = static_cast<float *>(ctx->dev_out.ptr);
+    a.query = static_cast<const float *>(ctx->host_in.ptr);
+    a.output = static_cast<float *>(ctx->host_out.ptr);
     a.query_heads = r->query_heads;
     a.position = r->position;
     a.scale = r->scale;
@@ -784,10 +805,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *handl
     (void)hipEventRecord(ctx->ev_start, ctx->stream);
     if ((e = qwn::launch_attention(a, ctx->stream)) != hipSuccess) return hip_fail("Q8 KV attention launch", e);
     (void)hipEventRecord(ctx->ev_end, ctx->stream);
-    if ((e = hipMemcpyAsync(ctx->host_out.ptr, ctx->dev_out.ptr, qbytes, hipMemcpyDeviceToHost, ctx->stream)) !=
-            hipSuccess ||
-        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess)
-        return hip_fail("Q8 KV attention", e);
+    if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail("Q8 KV attention", e);
     std::memcpy(r->host_output, ctx->host_out.ptr, qbytes);
     float kms = 0.0f;
     if (hipEventElapsedTime(&kms, ctx->ev_start, ctx->ev_end) != hipSuccess) kms = 0.0f;
@@ -1293,13 +1311,10 @@ QWN_CUDA_ABI_API int qwn_hip_ext_kv_append_device(QwnCudaContextHandle *handle, 
     }
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
     KvCache &c = rk->c;
-    for (uint32_t i = 0; i < count; ++i) {
-        hipError_t e = qwn::launch_kv_append(c, keys + static_cast<size_t>(i) * c.channels,
-                                             values + static_cast<size_t>(i) * c.channels, c.tokens, s);
-        if (e != hipSuccess) return hip_fail("device KV append launch", e);
-        c.tokens++;
-        ctx->telemetry.kv_cache_kernel_count += 2;
-    }
+    hipError_t e = qwn::launch_kv_append(c, keys, values, c.tokens, s, count);
+    if (e != hipSuccess) return hip_fail("device KV append launch", e);
+    c.tokens += count;
+    ctx->telemetry.kv_cache_kernel_count += 2ull * count;
     return QWN_CUDA_STATUS_OK;
 }
 
@@ -1321,7 +1336,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device(QwnCudaContextHandle *handl
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
     ResidentKv *rk = cache_of(ctx, *h);
-    if (!rk || position >= rk->c.tokens || query_heads % rk->c.kv_heads != 0) {
+    if (!rk || position >= rk->c.tokens) {
         set_error("invalid device attention request");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
@@ -1388,6 +1403,94 @@ QWN_CUDA_ABI_API int qwn_hip_ext_debug_int_sums(QwnCudaContextHandle *handle, co
     if (dimg) (void)hipFree(dimg);
     if (dout) (void)hipFree(dout);
     return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("debug integer sums", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_debug_mfma_int_sums(QwnCudaContextHandle *handle, const QwnCudaTensorHandle *th,
+                                                     const int8_t *host_q8, uint32_t batch, int32_t *host_out,
+                                                     uint64_t out_capacity) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !th || !host_q8 || !host_out || batch == 0 || batch > 16) {
+        set_error("invalid MFMA debug request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentTensor *rt = tensor_of(ctx, *th);
+    if (!rt || rt->t.kind == qwn::kF16) {
+        set_error("MFMA debug sums need a resident HyperVSQ-2 or Q4_0 tensor");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const DeviceTensor &t = rt->t;
+    const uint64_t nblk = t.kind == qwn::kHvsq2 ? t.units : (t.cols + 31ull) / 32ull;
+    const uint64_t n = static_cast<uint64_t>(batch) * t.rows * nblk;
+    if (out_capacity < n) {
+        set_error("MFMA debug output needs %llu int32 values", static_cast<unsigned long long>(n));
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    hipError_t e = hipSetDevice(ctx->device);
+    const uint32_t stride = (t.cols + 255u) & ~255u;
+    const size_t img = qwn::mfma_image_bytes(t);
+    void *dx = nullptr, *dimg = nullptr, *dout = nullptr, *dy = nullptr, *dsc = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&dx, static_cast<size_t>(stride) * batch);
+    if (e == hipSuccess) e = hipMalloc(&dimg, img);
+    if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&dy, static_cast<size_t>(batch) * t.rows * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&dsc, 16 * sizeof(float));
+    if (e == hipSuccess) e = hipMemsetAsync(dx, 0, static_cast<size_t>(stride) * batch, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(dsc, 0, 16 * sizeof(float), ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(dx, stride, host_q8, t.cols, t.cols, batch, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = qwn::launch_mfma_image(t, static_cast<const int8_t *>(dx), batch, stride, static_cast<uint8_t *>(dimg),
+                                   ctx->stream);
+    if (e == hipSuccess) {
+        const DeviceTensor *ts[1] = {&t};
+        float *outs[1] = {static_cast<float *>(dy)};
+        e = qwn::launch_gemm_mfma_group(ts, outs, 1, static_cast<const uint8_t *>(dimg),
+                                        static_cast<const float *>(dsc), batch, nullptr, ctx->stream, false,
+                                        static_cast<int32_t *>(dout));
+    }
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(host_out, dout, n * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    for (void *p : {dx, dimg, dout, dy, dsc})
+        if (p) (void)hipFree(p);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("MFMA debug integer sums", e);
+}
+
+QWN_CUDA_ABI_API int qwn_hip_ext_debug_kv_read(QwnCudaContextHandle *handle, const QwnCudaKvCacheHandle *h,
+                                               uint32_t first, uint32_t count, int8_t *host_keys,
+                                               int8_t *host_values, float *host_key_scales,
+                                               float *host_value_scales) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !h || !host_keys || !host_values || !host_key_scales || !host_value_scales || count == 0) {
+        set_error("invalid KV debug read");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    ResidentKv *rk = cache_of(ctx, *h);
+    if (!rk || first > rk->c.tokens || count > rk->c.tokens - first) {
+        set_error("KV debug read beyond the appended tokens");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    const KvCache &c = rk->c;
+    const size_t vb = static_cast<size_t>(count) * c.channels, sb = static_cast<size_t>(count) * c.groups * 4;
+    hipError_t e = hipSetDevice(ctx->device);
+    void *dk = nullptr, *dv = nullptr, *dks = nullptr, *dvs = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&dk, vb);
+    if (e == hipSuccess) e = hipMalloc(&dv, vb);
+    if (e == hipSuccess) e = hipMalloc(&dks, sb);
+    if (e == hipSuccess) e = hipMalloc(&dvs, sb);
+    if (e == hipSuccess)
+        e = qwn::launch_kv_gather(c, first, count, static_cast<int8_t *>(dk), static_cast<int8_t *>(dv),
+                                  static_cast<float *>(dks), static_cast<float *>(dvs), ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(host_keys, dk, vb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(host_values, dv, vb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(host_key_scales, dks, sb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(host_value_scales, dvs, sb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    for (void *p : {dk, dv, dks, dvs})
+        if (p) (void)hipFree(p);
+    return e == hipSuccess ? QWN_CUDA_STATUS_OK : hip_fail("KV debug read", e);
 }
 
 }  // extern "C"

@@ -122,6 +122,28 @@ static float half_to_float(uint16_t h) {
 
 /* ---- ABI bring-up (c/qwanto_decode.c:267-462) ---------------------------- */
 
+static void set_reason(QhdDecoder *d, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(d->metrics.backend_reason, sizeof(d->metrics.backend_reason), fmt, ap);
+    va_end(ap);
+}
+
+/* A capability block the host accepts (c/qwanto_decode.c:365-370, 408-413). */
+static int caps_ok(const QwnCudaAbiInfo *c) {
+    return c->header.abi_version == QWN_CUDA_ABI_VERSION && c->header.struct_size >= sizeof(QwnCudaAbiInfo) &&
+           (c->capability_bits & QWN_CUDA_CAP_HYPERVSQ2_GEMV) &&
+           c->hypervsq2_block_bytes == QWN_CUDA_HYPERVSQ2_BLOCK_BYTES &&
+           c->hypervsq2_block_elements == QWN_CUDA_HYPERVSQ2_BLOCK_ELEMENTS;
+}
+
+/* The reference loader's checks in its order, each refusal with its
+ * reason string: library present; the twelve versioned exports; query()
+ * (ABI version, struct size, HyperVSQ-2 74-byte layout); Q8 KV capability
+ * and the five KV exports (this decoder always uses the Q8 cache, the
+ * reference's --kv-cache q8); get_capabilities() with the same checks; the
+ * device enumerated; context creation.  Then this decoder's own need: the
+ * Q4_0 / F16 capabilities it routes through the ABI. */
 static int load_abi(QhdDecoder *d, const char *path, int device) {
     char candidate[PATH_MAX];
     if (!path) {
@@ -129,6 +151,7 @@ static int load_abi(QhdDecoder *d, const char *path, int device) {
         memset(&info, 0, sizeof(info));
         if (!dladdr((void *)&load_abi, &info) || !info.dli_fname) {
             fail(d, "cannot locate the decoder library's directory");
+            set_reason(d, "qwn_cuda_dll_absent_from_runtime_directory");
             return -1;
         }
         snprintf(candidate, sizeof(candidate), "%s", info.dli_fname);
@@ -144,16 +167,10 @@ static int load_abi(QhdDecoder *d, const char *path, int device) {
     a->handle = dlopen(path, RTLD_NOW | RTLD_LOCAL);
     if (!a->handle) {
         fail(d, "cannot load %s: %s", path, dlerror());
+        set_reason(d, "qwn_cuda_dll_absent_from_runtime_directory");
         return -1;
     }
-#define RESOLVE(field, name)                                         \
-    do {                                                             \
-        *(void **)&a->field = dlsym(a->handle, name);                \
-        if (!a->field) {                                             \
-            fail(d, "%s does not export %s", path, name);            \
-            return -1;                                               \
-        }                                                            \
-    } while (0)
+#define RESOLVE(field, name) (*(void **)&a->field = dlsym(a->handle, name))
     RESOLVE(query, "qwn_cuda_abi_query");
     RESOLVE(get_capabilities, "qwn_cuda_abi_get_capabilities");
     RESOLVE(enumerate_devices, "qwn_cuda_abi_enumerate_devices");
@@ -172,19 +189,39 @@ static int load_abi(QhdDecoder *d, const char *path, int device) {
     RESOLVE(get_telemetry, "qwn_cuda_abi_get_telemetry");
     RESOLVE(last_error, "qwn_cuda_abi_last_error");
 #undef RESOLVE
-    qwn_cuda_abi_header_init(&a->caps.header, sizeof(a->caps));
-    if (a->get_capabilities(&a->caps) != QWN_CUDA_STATUS_OK || a->caps.header.abi_version != QWN_CUDA_ABI_VERSION ||
-        a->caps.header.struct_size < sizeof(a->caps) || !(a->caps.capability_bits & QWN_CUDA_CAP_HYPERVSQ2_GEMV) ||
-        a->caps.hypervsq2_block_bytes != QWN_CUDA_HYPERVSQ2_BLOCK_BYTES ||
-        a->caps.hypervsq2_block_elements != QWN_CUDA_HYPERVSQ2_BLOCK_ELEMENTS) {
-        fail(d, "ABI version or capabilities mismatch");
+    if (!a->query || !a->get_capabilities || !a->enumerate_devices || !a->context_create || !a->context_destroy ||
+        !a->upload_tensor || !a->release_tensor || !a->gemv || !a->gemm || !a->synchronize || !a->get_telemetry ||
+        !a->last_error) {
+        a->last_error = NULL;
+        fail(d, "%s lacks the versioned qwnrun ABI", path);
+        set_reason(d, "qwn_cuda_dll_missing_versioned_abi_%u", QWN_CUDA_ABI_VERSION);
         return -1;
     }
-    const uint64_t need = QWN_CUDA_CAP_Q8_KV | QWN_CUDA_CAP_F16_GEMV |
-                          (d->m.cfg.proj_dtype == QHD_PROJ_Q4_0 ? QWN_CUDA_CAP_Q4_0_GEMV : 0);
-    if ((a->caps.capability_bits & need) != need) {
-        fail(d, "the ABI library lacks Q8 KV / F16 / Q4_0 support (capabilities 0x%llx)",
-             (unsigned long long)a->caps.capability_bits);
+    qwn_cuda_abi_header_init(&a->caps.header, sizeof(a->caps));
+    if (a->query(&a->caps) != QWN_CUDA_STATUS_OK || !caps_ok(&a->caps)) {
+        fail(d, "ABI or HyperVSQ-2 74-byte capability check failed");
+        set_reason(d, "abi_capability_or_hypervsq2_layout_rejected");
+        return -1;
+    }
+    if (!(a->caps.capability_bits & QWN_CUDA_CAP_Q8_KV) || !a->kv_cache_create || !a->kv_cache_destroy ||
+        !a->kv_cache_append || !a->kv_cache_attention || !a->kv_cache_reset) {
+        fail(d, "Q8 KV-cache capability is unavailable");
+        set_reason(d, "cuda_q8_kv_capability_unavailable");
+        return -1;
+    }
+    qwn_cuda_abi_header_init(&a->caps.header, sizeof(a->caps));
+    if (a->get_capabilities(&a->caps) != QWN_CUDA_STATUS_OK || !caps_ok(&a->caps)) {
+        fail(d, "capability query failed");
+        set_reason(d, "cuda_capability_query_failed");
+        return -1;
+    }
+    QwnCudaDeviceInfo devices[16];
+    memset(devices, 0, sizeof(devices));
+    uint32_t device_count = 0;
+    if (a->enumerate_devices(devices, 16, &device_count) != QWN_CUDA_STATUS_OK || device_count == 0 ||
+        device < 0 || (uint32_t)device >= device_count || device >= 16) {
+        fail(d, "device %d is unavailable", device);
+        set_reason(d, "cuda_device_index_%d_not_enumerated", device);
         return -1;
     }
     QwnCudaContextOptions opts;
@@ -194,9 +231,19 @@ static int load_abi(QhdDecoder *d, const char *path, int device) {
     opts.context_size = (uint64_t)d->m.cfg.max_ctx;
     qwn_cuda_abi_header_init(&a->context.header, sizeof(a->context));
     if (a->context_create(&opts, &a->context) != QWN_CUDA_STATUS_OK) {
+        a->context.opaque = NULL;
         fail(d, "context creation failed");
+        set_reason(d, "cuda_context_creation_failed_device_%d", device);
         return -1;
     }
+    const uint64_t need = QWN_CUDA_CAP_F16_GEMV | (d->m.cfg.proj_dtype == QHD_PROJ_Q4_0 ? QWN_CUDA_CAP_Q4_0_GEMV : 0);
+    if ((a->caps.capability_bits & need) != need) {
+        fail(d, "the ABI library lacks F16 / Q4_0 support (capabilities 0x%llx)",
+             (unsigned long long)a->caps.capability_bits);
+        set_reason(d, "qwn_hip_q4_0_f16_capability_unavailable");
+        return -1;
+    }
+    set_reason(d, "versioned_abi_%u_loaded_device_%d", QWN_CUDA_ABI_VERSION, device);
     return 0;
 }
 
@@ -230,6 +277,16 @@ static void rmsnorm(float *out, const float *x, const float *w, int n, float eps
     for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
     const float inv = 1.0f / sqrtf((float)(ss / n) + eps);
     for (int i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* add_bias (c/qwanto_decode.c:926-929): x[i] += b[i]; b may be NULL */
+static void add_bias(float *x, const float *b, int n) {
+    if (!b) return;
+    for (int i = 0; i < n; i++) x[i] += b[i];
+}
+
+static const float *bias_of(const QhdDecoder *d, int layer, int which) {
+    return d->m.biases ? d->m.biases[4 * layer + which] : NULL;
 }
 
 static void rope(float *v, int heads, int dim, const float *ct, const float *st) {
@@ -344,7 +401,7 @@ static int lm_head(QhdDecoder *d, const float *x, float *logits) {
 void qhd_close(QhdDecoder *d) {
     if (!d) return;
     Abi *a = &d->abi;
-    if (a->handle && a->context.opaque) {
+    if (a->handle && a->context.opaque && a->context_destroy) {
         for (int i = 0; i < d->resident_count; i++) a->release_tensor(&a->context, &d->resident[i].tensor);
         if (d->kv)
             for (int l = 0; l < d->m.cfg.layers; l++)
@@ -358,7 +415,8 @@ void qhd_close(QhdDecoder *d) {
     free(d);
 }
 
-QhdDecoder *qhd_open(const QhdModel *model, const char *abi_path, int device, char *error, int error_len) {
+QhdDecoder *qhd_open(const QhdModel *model, const char *abi_path, int device, char *error, int error_len,
+                     char *reason) {
     QhdDecoder *d = (QhdDecoder *)calloc(1, sizeof(*d));
     if (!d) return NULL;
     d->m = *model;
@@ -410,6 +468,7 @@ QhdDecoder *qhd_open(const QhdModel *model, const char *abi_path, int device, ch
     return d;
 out_fail:
     if (error && error_len > 0) snprintf(error, (size_t)error_len, "%s", d->error);
+    if (reason) snprintf(reason, sizeof(d->metrics.backend_reason), "%s", d->metrics.backend_reason);
     qhd_close(d);
     return NULL;
 }
@@ -479,10 +538,21 @@ int qhd_forward(QhdDecoder *d, int token, float *logits_out) {
         if (matmul(d, w[PROJ_Q], d->xb, D, Q, d->q) || matmul(d, w[PROJ_K], d->xb, D, KV, d->k) ||
             matmul(d, w[PROJ_V], d->xb, D, KV, d->v))
             return -1;
+        add_bias(d->q, bias_of(d, l, PROJ_Q), Q);
+        add_bias(d->k, bias_of(d, l, PROJ_K), KV);
+        add_bias(d->v, bias_of(d, l, PROJ_V), KV);
+        if (d->m.qk_norms) {
+            /* head_rmsnorm (c/qwanto_decode.c:654-684): each head in place */
+            for (int h = 0; h < c->heads; h++)
+                rmsnorm(d->q + (size_t)h * HD, d->q + (size_t)h * HD, d->m.qk_norms[2 * l], HD, c->rms_eps);
+            for (int h = 0; h < c->kv_heads; h++)
+                rmsnorm(d->k + (size_t)h * HD, d->k + (size_t)h * HD, d->m.qk_norms[2 * l + 1], HD, c->rms_eps);
+        }
         rope(d->q, c->heads, HD, ct, st);
         rope(d->k, c->kv_heads, HD, ct, st);
         if (kv_step(d, l, pos)) return -1;
         if (matmul(d, w[PROJ_O], d->ctx, Q, D, d->xb)) return -1;
+        add_bias(d->xb, bias_of(d, l, PROJ_O), D);
         for (int i = 0; i < D; i++) d->x[i] += d->xb[i];
         rmsnorm(d->xb, d->x, d->m.norms[2 * l + 1], D, c->rms_eps);
         if (matmul(d, w[PROJ_GATE], d->xb, D, I, d->gate) || matmul(d, w[PROJ_UP], d->xb, D, I, d->up)) return -1;

@@ -22,7 +22,8 @@ class QhdConfig(ctypes.Structure):
 
 class QhdModel(ctypes.Structure):
     _fields_ = [("cfg", QhdConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
-                ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p))]
+                ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p)),
+                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p))]
 
 
 class QhdMetrics(ctypes.Structure):
@@ -32,7 +33,15 @@ class QhdMetrics(ctypes.Structure):
                [(n, ctypes.c_double) for n in ("gpu_kernel_ms", "gpu_transfer_ms", "gpu_sync_ms", "prefill_ms",
                                                "decode_wall_ms")] + \
                [("prompt_tokens", ctypes.c_int), ("generated_tokens", ctypes.c_int),
-                ("kernel_type", ctypes.c_char * 32)]
+                ("kernel_type", ctypes.c_char * 32), ("backend_reason", ctypes.c_char * 96)]
+
+
+class OpenError(RuntimeError):
+    """qhd_open refused: `reason` is the loader's backend_reason string."""
+
+    def __init__(self, message: str, reason: str):
+        super().__init__(f"host decoder open failed: {message} [{reason}]")
+        self.reason = reason
 
 
 def model_struct(model: dict):
@@ -47,23 +56,35 @@ def model_struct(model: dict):
     proj = (ctypes.c_void_p * (7 * L))(*[model["layers"][l][p].ctypes.data for l in range(L) for p in PROJ_ORDER])
     norms = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data for l in range(L)
                                           for n in ("input_norm", "post_norm")])
+    qk = None
+    if "q_norm" in model["layers"][0]:
+        qk = (ctypes.c_void_p * (2 * L))(*[model["layers"][l][n].ctypes.data for l in range(L)
+                                           for n in ("q_norm", "k_norm")])
+    bias = None
+    names = ("q_bias", "k_bias", "v_bias", "o_bias")
+    if any(b in layer for layer in model["layers"] for b in names):
+        bias = (ctypes.c_void_p * (4 * L))(*[model["layers"][l][b].ctypes.data if b in model["layers"][l] else None
+                                             for l in range(L) for b in names])
+    P = ctypes.POINTER(ctypes.c_void_p)
     m = QhdModel(cfg=c, embed=model["embed"].ctypes.data, final_norm=model["final_norm"].ctypes.data,
-                 proj=ctypes.cast(proj, ctypes.POINTER(ctypes.c_void_p)),
-                 norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)))
-    return m, (proj, norms)
+                 proj=ctypes.cast(proj, P), norms=ctypes.cast(norms, P),
+                 qk_norms=ctypes.cast(qk, P) if qk is not None else None,
+                 biases=ctypes.cast(bias, P) if bias is not None else None)
+    return m, (proj, norms, qk, bias)
 
 
 class HostDecoder:
     def __init__(self, model: dict, abi_path: str | None = None, device: int = 0):
         if not os.path.exists(LIB_PATH):
             raise FileNotFoundError(f"{LIB_PATH} is not built (python qwanto_amd/build.py)")
-        try:
-            import torch  # noqa: F401  (one HIP runtime per process, see qwanto_amd.abi.load)
-        except ImportError:
-            pass
+        if abi_path is None:
+            try:
+                import torch  # noqa: F401  (one HIP runtime per process, see qwanto_amd.abi.load)
+            except ImportError:
+                pass
         lib = ctypes.CDLL(LIB_PATH)
         lib.qhd_open.argtypes = [ctypes.POINTER(QhdModel), ctypes.c_char_p, ctypes.c_int, ctypes.c_char_p,
-                                 ctypes.c_int]
+                                 ctypes.c_int, ctypes.c_char_p]
         lib.qhd_open.restype = ctypes.c_void_p
         lib.qhd_close.argtypes = [ctypes.c_void_p]
         lib.qhd_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
@@ -75,9 +96,11 @@ class HostDecoder:
         self.lib, self.model = lib, model
         self.struct, self._keep = model_struct(model)
         err = ctypes.create_string_buffer(256)
-        self.h = lib.qhd_open(ctypes.byref(self.struct), abi_path.encode() if abi_path else None, device, err, 256)
+        reason = ctypes.create_string_buffer(96)
+        self.h = lib.qhd_open(ctypes.byref(self.struct), abi_path.encode() if abi_path else None, device, err, 256,
+                              reason)
         if not self.h:
-            raise RuntimeError(f"host decoder open failed: {err.value.decode()}")
+            raise OpenError(err.value.decode(), reason.value.decode())
         self.vocab = model["cfg"]["vocab"]
 
     def _check(self, rc):

@@ -232,6 +232,10 @@ def write_decoder_model(path: str, model: dict) -> int:
         for p, suffix in _PROJ_NAMES.items():
             out, inp = model["shapes"][p]
             tensors.append((pre + suffix, qdt, (inp, out), layer[p]))
+        for p in ("q", "k", "v", "o"):  # optional biases (c/qwanto_decode.c:970-973)
+            if p + "_bias" in layer:
+                tensors.append((pre + f"self_attn.{p}_proj.bias", DT_F32, (model["shapes"][p][0],),
+                                layer[p + "_bias"]))
     tensors.append(("model.norm.weight", DT_F32, (D,), model["final_norm"]))
     dims = (D, cfg["intermediate"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["layers"], V,
             cfg["max_ctx"])
@@ -257,6 +261,9 @@ def read_decoder_model(path: str) -> dict:
         if pre + "self_attn.q_norm.weight" in f.tensors:
             layer["q_norm"] = f.array(pre + "self_attn.q_norm.weight")
             layer["k_norm"] = f.array(pre + "self_attn.k_norm.weight")
+        for p in ("q", "k", "v", "o"):
+            if pre + f"self_attn.{p}_proj.bias" in f.tensors:
+                layer[p + "_bias"] = f.array(pre + f"self_attn.{p}_proj.bias")
         for p, suffix in _PROJ_NAMES.items():
             t = f.tensors[pre + suffix]
             dtype = "q4_0" if t["dtype"] == DT_Q4_0 else "hvsq2"

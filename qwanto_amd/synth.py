@@ -50,21 +50,29 @@ def _half_bytes(values: np.ndarray) -> np.ndarray:
     return values.astype(np.float16).view(np.uint8).reshape(values.shape + (2,))
 
 
-def q4_0_weights(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
-    """Row-major Q4_0 matrix as a flat uint8 array."""
+def q4_0_weights(rng: np.random.Generator, rows: int, cols: int, std: float = 0.02,
+                 zero_mean: bool = False) -> np.ndarray:
+    """Row-major Q4_0 matrix as a flat uint8 array (block scales |N(0, std)|;
+    codes uniform over 0..15, or over 1..15 with zero_mean: weights (code-8)
+    with mean 0 instead of -scale/2)."""
     blocks = rows * ((cols + 31) // 32)
     out = np.empty((blocks, Q4_0_BLOCK_BYTES), dtype=np.uint8)
-    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, 0.02, blocks)).astype(np.float32))
-    out[:, 2:] = rng.integers(0, 256, (blocks, 16), dtype=np.uint8)
+    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, std, blocks)).astype(np.float32))
+    if zero_mean:
+        nib = rng.integers(1, 16, (blocks, 32), dtype=np.uint8)
+        out[:, 2:] = nib[:, :16] | (nib[:, 16:] << 4)
+    else:
+        out[:, 2:] = rng.integers(0, 256, (blocks, 16), dtype=np.uint8)
     return out.reshape(-1)
 
 
-def hvsq2_weights(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
-    """Row-major HyperVSQ-2 matrix as a flat uint8 array."""
+def hvsq2_weights(rng: np.random.Generator, rows: int, cols: int, std: float = 0.02) -> np.ndarray:
+    """Row-major HyperVSQ-2 matrix as a flat uint8 array (d_base |N(0, std)|,
+    m_base N(0, std))."""
     blocks = rows * ((cols + 255) // 256)
     out = np.empty((blocks, HVSQ2_BLOCK_BYTES), dtype=np.uint8)
-    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, 0.02, blocks)).astype(np.float32))
-    out[:, 2:4] = _half_bytes(rng.normal(0.0, 0.02, blocks).astype(np.float32))
+    out[:, 0:2] = _half_bytes(np.abs(rng.normal(0.0, std, blocks)).astype(np.float32))
+    out[:, 2:4] = _half_bytes(rng.normal(0.0, std, blocks).astype(np.float32))
     sub = rng.integers(1, 9, (blocks, 8), dtype=np.uint8)
     out[:, 4:8] = sub[:, 0::2] | (sub[:, 1::2] << 4)
     out[:, 8:10] = rng.integers(0, 256, (blocks, 2), dtype=np.uint8)
@@ -81,13 +89,14 @@ def activations(rng: np.random.Generator, batch: int, cols: int) -> np.ndarray:
     return rng.standard_normal((batch, cols), dtype=np.float32)
 
 
-def weights(dtype: str, rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+def weights(dtype: str, rng: np.random.Generator, rows: int, cols: int, std: float = 0.02,
+            zero_mean: bool = False) -> np.ndarray:
     if dtype == "q4_0":
-        return q4_0_weights(rng, rows, cols)
+        return q4_0_weights(rng, rows, cols, std, zero_mean)
     if dtype == "hvsq2":
-        return hvsq2_weights(rng, rows, cols)
+        return hvsq2_weights(rng, rows, cols, std)
     if dtype == "f16":
-        return f16_weights(rng, rows, cols)
+        return f16_weights(rng, rows, cols, std)
     raise ValueError(f"unknown weight dtype {dtype!r}")
 
 
@@ -119,27 +128,37 @@ QWEN3_4B_SHAPED_CONFIG = {
 }
 
 
-def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_norm: bool = False) -> dict:
+def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_norm: bool = False,
+                  weight_std: float = 0.02, embed_std: float = 0.02, zero_mean: bool = False,
+                  biases: str = "") -> dict:
     """Random decoder weights with the layout of a .qwn dense model: per layer
     q, k, v, o, gate, up, down quantized matrices ([out][in] row-major
     blocks), input/post norm vectors (and, with qk_norm, per-head q/k norm
     weights [head_dim] as Qwen3's self_attn.q_norm / k_norm, drawn
     1 + 0.2 N(0,1)); a tied F16 embedding [vocab][hidden] and the final
-    norm."""
+    norm.  weight_std / embed_std: the scale distributions' sigma (0.02 is
+    the benchmark models' draw); zero_mean: Q4_0 codes drawn from 1..15 so
+    the weights carry no common offset (with codes 0..15 every row's mean
+    weight is -scale/2, which drives the residual stream of a random model
+    toward one direction and its greedy output toward one token).  biases:
+    the projections among "qkvo" that get an F32 bias drawn 0.5 N(0,1)
+    (Qwen2 checkpoints carry q/k/v biases), as self_attn.*_proj.bias."""
     D, I = cfg["hidden"], cfg["intermediate"]
     Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
     shapes = {"q": (Q, D), "k": (KV, D), "v": (KV, D), "o": (D, Q),
               "gate": (I, D), "up": (I, D), "down": (D, I)}
     layers = []
     for _ in range(cfg["layers"]):
-        layer = {p: weights(dtype, rng, *shapes[p]) for p in PROJECTIONS}
+        layer = {p: weights(dtype, rng, *shapes[p], std=weight_std, zero_mean=zero_mean) for p in PROJECTIONS}
         layer["input_norm"] = np.ones(D, dtype=np.float32)
         layer["post_norm"] = np.ones(D, dtype=np.float32)
+        for p in biases:
+            layer[p + "_bias"] = (0.5 * rng.standard_normal(shapes[p][0])).astype(np.float32)
         if qk_norm:
             for n in ("q_norm", "k_norm"):
                 layer[n] = (1.0 + 0.2 * rng.standard_normal(cfg["head_dim"])).astype(np.float32)
         layers.append(layer)
-    embed = f16_weights(rng, cfg["vocab"], D)
+    embed = f16_weights(rng, cfg["vocab"], D, embed_std)
     return {"cfg": dict(cfg), "dtype": dtype, "shapes": shapes, "layers": layers,
             "embed": embed, "final_norm": np.ones(D, dtype=np.float32)}
 

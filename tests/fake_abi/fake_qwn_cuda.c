@@ -1,0 +1,213 @@
+/*
+ * A CPU-only stand-in for qwn_cuda.so -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Exports the versioned qwn_cuda_abi_* set (include/qwn_cuda_abi.h) with no
+ * device behind it, so the host decoder's loader (the reference's
+ * qwn_cuda_load, c/qwanto_decode.c:267-462) can be driven through each of
+ * its refusal branches on a machine without a GPU.  One compile-time switch
+ * per branch (tests/test_loader_branches.py builds every variant):
+ *
+ *   FAKE_OMIT_GEMM        no qwn_cuda_abi_hypervsq2_gemm export (a legacy library)
+ *   FAKE_ABI_VERSION=n    query() reports ABI version n
+ *   FAKE_INFO_SIZE=n      query() reports struct_size n
+ *   FAKE_BLOCK_BYTES=n    query() reports n-byte HyperVSQ-2 blocks
+ *   FAKE_NO_Q8_CAP        no Q8 KV capability bit
+ *   FAKE_OMIT_KV_RESET    no qwn_cuda_abi_kv_cache_reset export
+ *   FAKE_CAPS_FAIL        get_capabilities() fails while query() succeeds
+ *   FAKE_DEVICES=n        enumerate_devices() reports n devices
+ *   FAKE_CONTEXT_FAIL     context_create() fails
+ *   FAKE_NO_Q4_CAP        no Q4_0 capability bit (the build's extension)
+ *   FAKE_GEMV_ZERO_COUNT  gemv returns OK without counting a matmul
+ *
+ * Every accepted call returns OK and does nothing else; gemv refuses
+ * (UNSUPPORTED) unless FAKE_GEMV_ZERO_COUNT.
+ */
+#include <stdio.h>
+#include <string.h>
+
+#include "qwn_cuda_abi.h"
+
+#ifndef FAKE_ABI_VERSION
+#define FAKE_ABI_VERSION QWN_CUDA_ABI_VERSION
+#endif
+#ifndef FAKE_INFO_SIZE
+#define FAKE_INFO_SIZE sizeof(QwnCudaAbiInfo)
+#endif
+#ifndef FAKE_BLOCK_BYTES
+#define FAKE_BLOCK_BYTES QWN_CUDA_HYPERVSQ2_BLOCK_BYTES
+#endif
+#ifndef FAKE_DEVICES
+#define FAKE_DEVICES 1
+#endif
+
+static char g_error[128] = "";
+static QwnCudaTelemetry g_telemetry;
+static int g_context_token, g_tensor_token, g_cache_token;
+
+static void fill_info(QwnCudaAbiInfo *info, uint32_t version) {
+    memset(info, 0, sizeof(*info));
+    info->header.struct_size = (uint32_t)(FAKE_INFO_SIZE);
+    info->header.abi_version = version;
+    uint64_t caps = QWN_CUDA_CAP_HYPERVSQ2_GEMV | QWN_CUDA_CAP_HYPERVSQ2_GEMM | QWN_CUDA_CAP_RESIDENT_WEIGHTS |
+                    QWN_CUDA_CAP_TELEMETRY | QWN_CUDA_CAP_DEVICE_ENUMERATION | QWN_CUDA_CAP_Q8_KV |
+                    QWN_CUDA_CAP_Q4_0_GEMV | QWN_CUDA_CAP_F16_GEMV;
+#ifdef FAKE_NO_Q8_CAP
+    caps &= ~(uint64_t)QWN_CUDA_CAP_Q8_KV;
+#endif
+#ifdef FAKE_NO_Q4_CAP
+    caps &= ~(uint64_t)QWN_CUDA_CAP_Q4_0_GEMV;
+#endif
+    info->capability_bits = caps;
+    info->max_devices = 1;
+    info->max_resident_tensors = 1024;
+    info->hypervsq2_block_bytes = FAKE_BLOCK_BYTES;
+    info->hypervsq2_block_elements = QWN_CUDA_HYPERVSQ2_BLOCK_ELEMENTS;
+    snprintf(info->abi_name, sizeof(info->abi_name), "fake-cpu-abi");
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_query(QwnCudaAbiInfo *info) {
+    if (!info) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    fill_info(info, FAKE_ABI_VERSION);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_get_capabilities(QwnCudaAbiInfo *info) {
+    if (!info) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+#ifdef FAKE_CAPS_FAIL
+    snprintf(g_error, sizeof(g_error), "fake: capability query refused");
+    return QWN_CUDA_STATUS_UNAVAILABLE;
+#else
+    fill_info(info, FAKE_ABI_VERSION);
+    return QWN_CUDA_STATUS_OK;
+#endif
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_enumerate_devices(QwnCudaDeviceInfo *devices, uint32_t capacity,
+                                                     uint32_t *count) {
+    if (!count) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    *count = FAKE_DEVICES;
+    for (uint32_t i = 0; devices && i < capacity && i < (uint32_t)FAKE_DEVICES; i++) {
+        memset(&devices[i], 0, sizeof(devices[i]));
+        devices[i].header.struct_size = sizeof(devices[i]);
+        devices[i].header.abi_version = QWN_CUDA_ABI_VERSION;
+        devices[i].device_id = (int32_t)i;
+        snprintf(devices[i].name, sizeof(devices[i].name), "fake device %u", i);
+    }
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *options,
+                                                 QwnCudaContextHandle *context) {
+    if (!options || !context) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+#ifdef FAKE_CONTEXT_FAIL
+    snprintf(g_error, sizeof(g_error), "fake: no context on device %d", options->device_id);
+    return QWN_CUDA_STATUS_UNAVAILABLE;
+#else
+    context->opaque = &g_context_token;
+    memset(&g_telemetry, 0, sizeof(g_telemetry));
+    g_telemetry.header.struct_size = sizeof(g_telemetry);
+    g_telemetry.header.abi_version = QWN_CUDA_ABI_VERSION;
+    return QWN_CUDA_STATUS_OK;
+#endif
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *context) {
+    if (context) context->opaque = NULL;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *context, const QwnCudaTensorUpload *upload,
+                                                QwnCudaTensorHandle *tensor) {
+    if (!context || !upload || !tensor) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    tensor->opaque = &g_tensor_token;
+    g_telemetry.gpu_upload_count++;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *context, QwnCudaTensorHandle *tensor) {
+    (void)context;
+    if (tensor) tensor->opaque = NULL;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_create(QwnCudaContextHandle *context, const QwnCudaKvCacheOptions *options,
+                                                  QwnCudaKvCacheHandle *cache) {
+    if (!context || !options || !cache) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    cache->opaque = &g_cache_token;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_destroy(QwnCudaContextHandle *context, QwnCudaKvCacheHandle *cache) {
+    (void)context;
+    if (cache) cache->opaque = NULL;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_append(QwnCudaContextHandle *context,
+                                                  const QwnCudaKvAppendRequest *request,
+                                                  QwnCudaTelemetry *telemetry) {
+    (void)context;
+    (void)request;
+    if (telemetry) *telemetry = g_telemetry;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *context,
+                                                     const QwnCudaKvAttentionRequest *request,
+                                                     QwnCudaTelemetry *telemetry) {
+    (void)context;
+    (void)request;
+    if (telemetry) *telemetry = g_telemetry;
+    return QWN_CUDA_STATUS_OK;
+}
+
+#ifndef FAKE_OMIT_KV_RESET
+QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_reset(QwnCudaContextHandle *context, QwnCudaKvCacheHandle *cache) {
+    (void)context;
+    (void)cache;
+    return QWN_CUDA_STATUS_OK;
+}
+#endif
+
+static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *telemetry) {
+    (void)request;
+#ifdef FAKE_GEMV_ZERO_COUNT
+    if (telemetry) *telemetry = g_telemetry; /* OK, but no matmul counted */
+    return QWN_CUDA_STATUS_OK;
+#else
+    if (telemetry) *telemetry = g_telemetry;
+    snprintf(g_error, sizeof(g_error), "fake: no device to run a projection on");
+    return QWN_CUDA_STATUS_UNSUPPORTED;
+#endif
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_hypervsq2_gemv(QwnCudaContextHandle *context, const QwnCudaGemmRequest *request,
+                                                 QwnCudaTelemetry *telemetry) {
+    (void)context;
+    return fake_matmul(request, telemetry);
+}
+
+#ifndef FAKE_OMIT_GEMM
+QWN_CUDA_ABI_API int qwn_cuda_abi_hypervsq2_gemm(QwnCudaContextHandle *context, const QwnCudaGemmRequest *request,
+                                                 QwnCudaTelemetry *telemetry) {
+    (void)context;
+    return fake_matmul(request, telemetry);
+}
+#endif
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_synchronize(QwnCudaContextHandle *context) {
+    (void)context;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_get_telemetry(QwnCudaContextHandle *context, QwnCudaTelemetry *telemetry) {
+    (void)context;
+    if (telemetry) *telemetry = g_telemetry;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_cuda_abi_last_error(char *buffer, uint32_t buffer_size) {
+    if (!buffer || buffer_size == 0) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    snprintf(buffer, buffer_size, "%s", g_error);
+    return QWN_CUDA_STATUS_OK;
+}

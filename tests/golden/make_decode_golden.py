@@ -1,13 +1,25 @@
-"""Golden greedy decode of the Qwen2-1.5B shaped synthetic Q4_0 model.
+"""Golden greedy decodes of the Qwen2-1.5B shaped synthetic Q4_0 model.
 
-Builds the model from the seeded generator (qwanto_amd.synth), runs the
-oracle decoder (oracle/qwn_oracle_decoder.c) over a 32-token prompt and 128
-greedy steps, and -- where the reference decoder is built in place
-(oracle/_ref/libqwn_ref_decoder.so, from c/qwanto_decode.c) -- replays the
-same prompt and generated ids through it from a .qwn file and requires the
-same ids and bit-identical logits.  Writes decode_qwen2_1p5b_q4_0.json:
-seed, prompt, generated ids, logit margins, and the logit vector of the
-first generated step (as a checksum source).
+Two models, each from the seeded generator (qwanto_amd.synth):
+  decode_qwen2_1p5b_q4_0.json         the benchmark draw (block scales and
+      the F16 embedding N(0, 0.02), codes uniform over 0..15); its greedy
+      output settles on one token, as random models with biased weights do
+  decode_qwen2_1p5b_q4_0_varied.json  zero-mean codes (1..15), block scales
+      |N(0, 0.01)|, embedding N(0, 0.05): a greedy sequence that keeps
+      changing token
+For each: the oracle decoder (oracle/qwn_oracle_decoder.c) runs a 32-token
+prompt and 128 greedy steps; every step's logits are summarised (the 16
+largest with their ids, the largest magnitude, the top-two margin, a
+SHA-256 of the whole vector).  The sensitivity envelope: the same run
+teacher-forced on those ids with the oracle's calibration perturbation
+(rounding-sized moves of half the outputs of every RMSNorm, projection,
+attention and SwiGLU, four seeds),
+each step's distance from the exact logits measured as the GPU tests
+measure theirs (tests/decode_golden.step_error) -- how far rounding-sized
+differences travel through 28 layers of this model.  Where the reference decoder is built in
+place (oracle/_ref/libqwn_ref_decoder.so, from c/qwanto_decode.c) the same
+prompt and ids are replayed through it from a .qwn file, requiring
+bit-identical logits at every step.
 
     python tests/golden/make_decode_golden.py [--steps 128] [--threads 8]
 """
@@ -27,67 +39,119 @@ sys.path.insert(0, ROOT)
 import oracle  # noqa: E402
 from qwanto_amd import qwn_file, synth  # noqa: E402
 
-SEED = 2026
-OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "decode_qwen2_1p5b_q4_0.json")
+HERE = os.path.dirname(os.path.abspath(__file__))
+VARIANTS = {
+    "decode_qwen2_1p5b_q4_0.json": dict(seed=2026, weight_std=0.02, embed_std=0.02, zero_mean=False),
+    "decode_qwen2_1p5b_q4_0_varied.json": dict(seed=2028, weight_std=0.01, embed_std=0.05, zero_mean=True),
+}
+TOP = 16
+ENVELOPE_SEEDS = (1, 2, 3, 4)
 
 
-def build_model():
-    rng = np.random.default_rng(SEED)
-    model = synth.decoder_model(rng, synth.QWEN2_1P5B_CONFIG, "q4_0")
+def build_model(spec: dict):
+    """The model and prompt a golden file describes (tests rebuild them from
+    the same fields)."""
+    rng = np.random.default_rng(spec["seed"])
+    model = synth.decoder_model(rng, synth.QWEN2_1P5B_CONFIG, "q4_0", weight_std=spec["weight_std"],
+                                embed_std=spec["embed_std"], zero_mean=spec["zero_mean"])
     prompt = synth.prompt_tokens(rng, synth.QWEN2_1P5B_CONFIG["vocab"], 32)
     return model, prompt
+
+
+def summarise(logits: np.ndarray) -> dict:
+    # 16 largest, ordered by value then index (the first-maximum rule)
+    ids = np.lexsort((np.arange(logits.size), -logits.astype(np.float64)))[:TOP]
+    srt = np.partition(logits, -2)[-2:]
+    return {"ids": [int(i) for i in ids], "logits": [float(logits[i]) for i in ids],
+            "max_abs": float(np.max(np.abs(logits))), "margin": float(srt[1] - srt[0]),
+            "sha256": hashlib.sha256(logits.tobytes()).hexdigest()}
+
+
+def envelope(name, model, prompt, tokens, summaries, threads) -> dict:
+    """The perturbed oracle's per-step distances from the golden steps."""
+    sys.path.insert(0, os.path.dirname(HERE))
+    import decode_golden
+    o = oracle.load()
+    env = []
+    for seed in ENVELOPE_SEEDS:
+        d = o.decoder(model, threads=threads)
+        d.perturb(seed)
+        for tok in prompt:
+            logits = d.forward(int(tok))
+        errs = [decode_golden.step_error(logits, summaries[0])]
+        for s in range(len(tokens) - 1):
+            errs.append(decode_golden.step_error(d.forward(tokens[s]), summaries[s + 1]))
+        d.close()
+        env.append(errs)
+    env = np.array(env)
+    print(f"{name}: envelope median {np.median(env, axis=1).max():.3g}, max {env.max():.3g}", flush=True)
+    return {"seeds": list(ENVELOPE_SEEDS), "median": float(np.median(env, axis=1).max()), "max": float(env.max()),
+            "per_step": [float(v) for v in env.max(axis=0)]}
+
+
+def refresh_envelope(name: str, threads: int):
+    """Recompute only the envelope of an existing golden file."""
+    path = os.path.join(HERE, name)
+    g = json.load(open(path))
+    model, prompt = build_model({k: g[k] for k in ("seed", "weight_std", "embed_std", "zero_mean")})
+    g["envelope"] = envelope(name, model, prompt, g["tokens"], g["steps"], threads)
+    with open(path, "w") as f:
+        json.dump(g, f)
+
+
+def run(name: str, spec: dict, steps: int, threads: int):
+    t0 = time.time()
+    model, prompt = build_model(spec)
+    o = oracle.load()
+    dec = o.decoder(model, threads=threads)
+    for tok in prompt:
+        logits = dec.forward(int(tok))
+    tokens, summaries = [], []
+    for _ in range(steps):
+        summaries.append(summarise(logits))
+        tokens.append(summaries[-1]["ids"][0])
+        logits = dec.forward(tokens[-1])
+    dec.close()
+    print(f"{name}: oracle {steps} steps in {time.time() - t0:.1f}s, {len(set(tokens))} distinct ids", flush=True)
+    checked = False
+    if os.path.exists(oracle.REF_DECODER_SO):
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "m.qwn")
+            qwn_file.write_decoder_model(path, model)
+            ref = oracle.load_ref_decoder(path, synth.QWEN2_1P5B_CONFIG["max_ctx"], threads)
+            V = synth.QWEN2_1P5B_CONFIG["vocab"]
+            for tok in prompt:
+                rl = ref.forward(int(tok), V)
+            for s in range(steps):
+                assert hashlib.sha256(rl.tobytes()).hexdigest() == summaries[s]["sha256"], f"step {s}: logits differ"
+                rl = ref.forward(tokens[s], V)
+            ref.close()
+        print(f"{name}: reference decoder agrees bit for bit", flush=True)
+        checked = True
+    out = {"config": synth.QWEN2_1P5B_CONFIG, "dtype": "q4_0", **spec,
+           "prompt": [int(t) for t in prompt], "tokens": tokens,
+           "margins": [s["margin"] for s in summaries], "steps": summaries,
+           "envelope": envelope(name, model, prompt, tokens, summaries, threads),
+           "checked_against_reference_decoder": checked}
+    with open(os.path.join(HERE, name), "w") as f:
+        json.dump(out, f)
+    print(f"wrote {name}; min margin {min(out['margins']):.4g}", flush=True)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--threads", type=int, default=8)
+    ap.add_argument("--only", default=None, help="one output file name")
+    ap.add_argument("--envelope-only", action="store_true",
+                    help="recompute only the sensitivity envelope of the existing files")
     args = ap.parse_args()
-    t0 = time.time()
-    model, prompt = build_model()
-    print(f"model built in {time.time() - t0:.1f}s", flush=True)
-    o = oracle.load()
-    dec = o.decoder(model, threads=args.threads)
-    logits_steps = []
-    for tok in prompt:
-        logits = dec.forward(int(tok))
-    tokens, margins = [], []
-    first_logits = None
-    t1 = time.time()
-    for s in range(args.steps):
-        t = int(np.argmax(logits))
-        srt = np.partition(logits, -2)[-2:]
-        tokens.append(t)
-        margins.append(float(logits[t] - srt[0] if srt[1] == logits[t] else logits[t] - srt[1]))
-        if first_logits is None:
-            first_logits = logits.copy()
-        logits_steps.append(hashlib.sha256(logits.tobytes()).hexdigest())
-        logits = dec.forward(t)
-    print(f"oracle decode {args.steps} steps in {time.time() - t1:.1f}s", flush=True)
-    checked = False
-    if os.path.exists(oracle.REF_DECODER_SO):
-        with tempfile.TemporaryDirectory() as tmp:
-            path = os.path.join(tmp, "m.qwn")
-            qwn_file.write_decoder_model(path, model)
-            ref = oracle.load_ref_decoder(path, synth.QWEN2_1P5B_CONFIG["max_ctx"], args.threads)
-            V = synth.QWEN2_1P5B_CONFIG["vocab"]
-            t2 = time.time()
-            for tok in prompt:
-                rl = ref.forward(int(tok), V)
-            for s in range(args.steps):
-                assert hashlib.sha256(rl.tobytes()).hexdigest() == logits_steps[s], f"step {s}: logits differ"
-                assert int(np.argmax(rl)) == tokens[s]
-                rl = ref.forward(tokens[s], V)
-            ref.close()
-            print(f"reference decoder agrees bit for bit ({time.time() - t2:.1f}s)", flush=True)
-            checked = True
-    out = {"config": synth.QWEN2_1P5B_CONFIG, "dtype": "q4_0", "seed": SEED,
-           "prompt": [int(t) for t in prompt], "tokens": tokens, "margins": margins,
-           "first_step_logits_sha256": logits_steps[0],
-           "checked_against_reference_decoder": checked}
-    with open(OUT, "w") as f:
-        json.dump(out, f)
-    print(f"wrote {OUT}; min margin {min(margins):.4g}")
+    for name, spec in VARIANTS.items():
+        if args.only in (None, name):
+            if args.envelope_only:
+                refresh_envelope(name, args.threads)
+            else:
+                run(name, spec, args.steps, args.threads)
 
 
 if __name__ == "__main__":

@@ -25,14 +25,17 @@ def ref_decoder_or_skip(path, ctx):
     return oracle.load_ref_decoder(path, ctx)
 
 
-@pytest.mark.parametrize("cfg,dtype,steps,qk", [(SMALL, "q4_0", 12, False), (SMALL, "hvsq2", 8, False),
-                                                (QWEN2_LIKE, "q4_0", 10, False), (SMALL, "hvsq2", 8, True),
-                                                (QWEN2_LIKE, "q4_0", 10, True)])
-def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dtype, steps, qk):
+@pytest.mark.parametrize("cfg,dtype,steps,qk,bias", [
+    (SMALL, "q4_0", 12, False, ""), (SMALL, "hvsq2", 8, False, ""), (QWEN2_LIKE, "q4_0", 10, False, ""),
+    (SMALL, "hvsq2", 8, True, ""), (QWEN2_LIKE, "q4_0", 10, True, ""),
+    (QWEN2_LIKE, "q4_0", 10, False, "qkv"), (SMALL, "hvsq2", 8, True, "qkvo"), (SMALL, "q4_0", 8, False, "o")])
+def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dtype, steps, qk, bias):
     """qk: Qwen3-style per-head q/k RMSNorm weights in the file
-    (self_attn.q_norm / k_norm, c/qwanto_decode.c:975-976, 1652-1655)."""
+    (self_attn.q_norm / k_norm, c/qwanto_decode.c:975-976, 1652-1655).
+    bias: the projections carrying self_attn.*_proj.bias (q/k/v as Qwen2,
+    c/qwanto_decode.c:1649-1651; o, :1722)."""
     rng = np.random.default_rng(11)
-    model = synth.decoder_model(rng, cfg, dtype, qk_norm=qk)
+    model = synth.decoder_model(rng, cfg, dtype, qk_norm=qk, biases=bias)
     path = str(tmp_path / "m.qwn")
     qwn_file.write_decoder_model(path, model)
     ref = ref_decoder_or_skip(path, cfg["max_ctx"])
@@ -46,6 +49,26 @@ def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dty
         token = int(np.argmax(a))
     ref.close()
     dec.close()
+    if bias:
+        # the biases matter: the same model without them gives other logits
+        plain = {**model, "layers": [{k: v for k, v in layer.items() if not k.endswith("_bias")}
+                                     for layer in model["layers"]]}
+        d2, d3 = oracle_lib.decoder(plain), oracle_lib.decoder(model)
+        assert not np.array_equal(d2.forward(3), d3.forward(3))
+        d2.close()
+        d3.close()
+
+
+def test_qwn_roundtrip_biases(tmp_path):
+    rng = np.random.default_rng(4)
+    model = synth.decoder_model(rng, SMALL, "q4_0", biases="qkvo")
+    path = str(tmp_path / "b.qwn")
+    qwn_file.write_decoder_model(path, model)
+    back = qwn_file.read_decoder_model(path)
+    for l in range(SMALL["layers"]):
+        for p in "qkvo":
+            assert np.array_equal(back["layers"][l][p + "_bias"], model["layers"][l][p + "_bias"])
+    back["file"].close()
 
 
 def test_qwn_roundtrip(tmp_path):

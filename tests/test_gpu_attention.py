@@ -143,3 +143,107 @@ def test_device_attention_reused_workspace(gpu_ctx, oracle_lib):
             assert err <= ATTN_ATOL, f"pos {pos}: max abs err {err:.3g}"
     finally:
         gpu_ctx.kv_destroy(h)
+
+
+def test_kv_readback_bit_exact(gpu_ctx, oracle_lib):
+    """The cache's int8 keys/values and fp32 scales, read back token-major,
+    equal the oracle's Q8 quantization bit for bit: tokens appended through
+    the ABI (with NaN/Inf and an all-zero token) and through the device
+    block append, at a head_dim whose groups span heads."""
+    import torch
+    rng = np.random.default_rng(31)
+    for HK, D in ((2, 65), (8, 128)):
+        C = HK * D
+        T1, T2 = 21, 300
+        k = rng.standard_normal((T1 + T2, C), dtype=np.float32) * 3
+        v = rng.standard_normal((T1 + T2, C), dtype=np.float32)
+        k[3, :5] = [np.nan, np.inf, -np.inf, 0.5, -0.5]
+        v[4, 1], v[6, :] = np.nan, 0.0
+        h = gpu_ctx.kv_create(T1 + T2, HK, D)
+        try:
+            for t in range(T1):
+                gpu_ctx.kv_append(h, k[t], v[t], t)
+            kd = torch.from_numpy(k[T1:].copy()).to("cuda:0")
+            vd = torch.from_numpy(v[T1:].copy()).to("cuda:0")
+            gpu_ctx.kv_append_device(h, kd.data_ptr(), vd.data_ptr(), T2,
+                                     stream=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            gk, gv, gks, gvs = gpu_ctx.kv_read(h, 0, T1 + T2, C)
+            kq, ks = oracle_lib.q8_quantize(k)
+            vq, vs = oracle_lib.q8_quantize(v)
+            assert np.array_equal(gk, kq) and np.array_equal(gv, vq)
+            assert np.array_equal(gks.view(np.uint32), ks.view(np.uint32))
+            assert np.array_equal(gvs.view(np.uint32), vs.view(np.uint32))
+            # a window in the middle reads the same slots
+            wk, _, wks, _ = gpu_ctx.kv_read(h, 17, 40, C)
+            assert np.array_equal(wk, kq[17:57]) and np.array_equal(wks, ks[17:57])
+        finally:
+            gpu_ctx.kv_destroy(h)
+
+
+@pytest.mark.parametrize("T,H,HK,D", [
+    (37, 16, 1, 128), (300, 64, 4, 128), (65, 32, 1, 64),   # 16, 16 and 32 query heads per KV head
+    (50, 12, 8, 128), (40, 3, 2, 64), (20, 2, 4, 128),      # uneven ratios, fewer query than KV heads
+    (1100, 6, 4, 128), (90, 10, 4, 65),
+])
+def test_head_ratios(gpu_ctx, oracle_lib, T, H, HK, D):
+    """Any query/KV head ratio, with the reference ABI's mapping
+    kv_head = head * kv_heads / query_heads (c/cuda/qwn_hypervsq2_cuda_abi.cu:184)."""
+    rng = np.random.default_rng(T * 3 + H)
+    C = HK * D
+    k = rng.standard_normal((T, C), dtype=np.float32)
+    v = rng.standard_normal((T, C), dtype=np.float32)
+    q = rng.standard_normal(H * D, dtype=np.float32)
+    scale = np.float32(1.0 / np.sqrt(D))
+    h = gpu_ctx.kv_create(T, HK, D)
+    try:
+        for t in range(T):
+            gpu_ctx.kv_append(h, k[t], v[t], t)
+        kq, ks = oracle_lib.q8_quantize(k)
+        vq, vs = oracle_lib.q8_quantize(v)
+        for pos in (T - 1, T // 2):
+            out = gpu_ctx.kv_attention(h, q, H, HK, D, pos, float(scale))
+            ref = oracle_lib.q8_attention_abi(q, kq, vq, ks, vs, H, HK, D, pos, scale)
+            err = float(np.max(np.abs(out - ref)))
+            assert err <= ATTN_ATOL, f"T={T} H={H} HK={HK} D={D} pos={pos}: max abs err {err:.3g}"
+    finally:
+        gpu_ctx.kv_destroy(h)
+
+
+def test_config3_32k_tokens(gpu_ctx, oracle_lib):
+    """The long-context case at full size: 32 query / 8 KV heads, head_dim
+    128, 32768 cached tokens (32 splits of the MFMA attention plus the merge),
+    through the ABI (host query) and the device entry point, at the last
+    position and at one inside the last split."""
+    import torch
+    T, H, HK, D = 32768, 32, 8, 128
+    rng = np.random.default_rng(3276)
+    k = rng.standard_normal((T, HK * D), dtype=np.float32)
+    v = rng.standard_normal((T, HK * D), dtype=np.float32)
+    scale = np.float32(1.0 / np.sqrt(D))
+    dev = torch.device("cuda:0")
+    h = gpu_ctx.kv_create(T, HK, D)
+    try:
+        s = torch.cuda.current_stream().cuda_stream
+        kd, vd = torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev)
+        gpu_ctx.kv_append_device(h, kd.data_ptr(), vd.data_ptr(), T, stream=s)
+        torch.cuda.synchronize()
+        del kd, vd
+        kq, ks = oracle_lib.q8_quantize(k)
+        vq, vs = oracle_lib.q8_quantize(v)
+        work = torch.zeros(gpu_ctx.attention_workspace_bytes(h, H, T - 1) // 4 + 1, device=dev)
+        for pos in (T - 1, T - 700):
+            q = rng.standard_normal(H * D, dtype=np.float32)
+            ref = oracle_lib.q8_attention(q, kq, vq, ks, vs, H, HK, D, pos, scale)
+            out = gpu_ctx.kv_attention(h, q, H, HK, D, pos, float(scale))
+            err = float(np.max(np.abs(out - ref)))
+            assert err <= ATTN_ATOL, f"ABI pos {pos}: max abs err {err:.3g}"
+            qd = torch.from_numpy(q).to(dev)
+            od = torch.full((H * D,), float("nan"), device=dev)
+            gpu_ctx.kv_attention_device(h, qd.data_ptr(), od.data_ptr(), H, pos, float(scale), work.data_ptr(),
+                                        stream=s)
+            torch.cuda.synchronize()
+            err = float(np.max(np.abs(od.cpu().numpy() - ref)))
+            assert err <= ATTN_ATOL, f"device pos {pos}: max abs err {err:.3g}"
+    finally:
+        gpu_ctx.kv_destroy(h)

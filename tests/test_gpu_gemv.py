@@ -413,3 +413,38 @@ def test_abi_fp32_input_quantized_on_device(gpu_ctx, oracle_lib, kind, N, K, M):
             assert ok, f"{kind} {N}x{K} token {t}: worst {worst:.3g}"
     finally:
         gpu_ctx.release(h)
+
+
+def hvsq2_block_products(w, sum_q, N, K):
+    """Per 256-weight block: sum over octants of multiplier * sum (code-1)*a,
+    the exact integer the MFMA path forms (multipliers: 4 bytes at offset 4
+    of each 74-byte block, low nibble = even octant)."""
+    nb = (K + 255) // 256
+    blocks = w.reshape(N, nb, 74)
+    sub = np.stack([(blocks[:, :, 4 + o // 2] >> (4 * (o % 2))) & 15 for o in range(8)], axis=-1)
+    return (sub.astype(np.int64) * sum_q.reshape(N, nb, 8).astype(np.int64)).sum(axis=-1)
+
+
+@pytest.mark.parametrize("kind,N,K,M", [("hvsq2", 300, 2560, 16), ("hvsq2", 77, 4096, 9), ("hvsq2", 40, 700, 12),
+                                        ("q4_0", 200, 1536, 16), ("q4_0", 1536, 8960, 16), ("q4_0", 33, 100, 11)])
+def test_mfma_int32_block_dots(gpu_ctx, oracle_lib, kind, N, K, M):
+    """The MFMA GEMM's per-block int32 dots, dumped by the same kernel (same
+    plan, staging and operand code), bit-exact against the oracle's integer
+    sums for every token."""
+    rng = np.random.default_rng(N + K + M)
+    w = synth.weights(kind, rng, N, K)
+    q8, xs, sums = quantize(oracle_lib, synth.activations(rng, M, K))
+    h = gpu_ctx.upload(w, kind, N, K)
+    try:
+        nblk = (K + 255) // 256 if kind == "hvsq2" else (K + 31) // 32
+        got = gpu_ctx.debug_mfma_sums(h, q8[:, :K], N, nblk)
+        for t in range(M):
+            if kind == "hvsq2":
+                sq, _ = oracle_lib.hvsq2_octant_sums(w, q8[t], K, N)
+                ref = hvsq2_block_products(w, sq, N, K)
+            else:
+                ref = oracle_lib.q4_0_block_sums(w, q8[t], K, N)
+            bad = np.argwhere(got[t] != ref)
+            assert bad.size == 0, f"{kind} N={N} K={K} token {t}: block dots differ at {bad[:5]}"
+    finally:
+        gpu_ctx.release(h)

@@ -1,34 +1,35 @@
 """The resident decoder (include/qwn_hip_decoder.h: the whole step on the
 device, one HIP graph per token) against the oracle decoder, which is
 bit-identical to the reference decoder (test_decoder_oracle.py), and
-against the golden greedy ids of the Qwen2-1.5B-shaped Q4_0 model.
+against the golden greedy decodes of the Qwen2-1.5B-shaped Q4_0 model.
 
 On the device the RMSNorm sums, the SwiGLU exp and the GEMV combination run
-in a different fp32 order than the CPU's, so logits agree to ~1e-6 of their
-scale at most steps.  Where an activation lands within that rounding of an
-int8 boundary its quantized value moves by one and the step's logits move
-by up to a few 1e-3 of their scale (the ABI-driven host decoder shows the
-same steps, as both use the same GEMV kernels).  So: every step within
-5e-3, the median step within 1e-5 (no systematic error), greedy ids equal
-except where the best two logits are closer than the step's error.
+in another fp32 order than the CPU's.  Where an activation lands within that
+rounding of an int8 boundary its quantized value moves by one; the
+difference travels through the later layers and stays in the KV cache.
+The logits are therefore held to the oracle's own sensitivity to
+rounding-sized differences, measured on the same model and tokens
+(parity.oracle_envelope / parity.within_envelope): the GPU's median and
+worst step within ENV_K times the perturbed oracle's.  The caches written
+by a prefill block and by token-by-token steps are compared entry by
+entry: the first layer's may differ only by one int8 step where such a
+flip happened.
 """
-import json
-import os
-
 import numpy as np
 import pytest
 
+import decode_golden
+from parity import ENV_K, oracle_envelope, step_errors, within_envelope
 from qwanto_amd import abi, synth
 
 pytestmark = pytest.mark.gpu
 
-GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "decode_qwen2_1p5b_q4_0.json")
 SMALL = dict(hidden=256, intermediate=512, layers=2, heads=4, kv_heads=2, head_dim=64, vocab=1000,
              max_ctx=64, rope_theta=1e6, rms_eps=1e-6)
 QWEN2_LIKE = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, head_dim=128, vocab=4096,
                   max_ctx=80, rope_theta=1e6, rms_eps=1e-6)
-STEP_RTOL = 5e-3     # any step, of the logit vector's max magnitude
-MEDIAN_RTOL = 1e-5   # the median step
+# a context of more than one split: RoPE/append kernel + MFMA split attention
+LONG_CTX = dict(SMALL, max_ctx=1500)
 
 
 def with_norms(rng, model):
@@ -41,116 +42,142 @@ def with_norms(rng, model):
     return model
 
 
-# a context of more than one split: RoPE/append kernel + MFMA split attention
-LONG_CTX = dict(SMALL, max_ctx=1500)
-
-
-@pytest.mark.parametrize("cfg,dtype,qk", [(SMALL, "q4_0", False), (SMALL, "hvsq2", False),
-                                          (QWEN2_LIKE, "q4_0", False), (QWEN2_LIKE, "hvsq2", False),
-                                          (LONG_CTX, "q4_0", False), (SMALL, "hvsq2", True),
-                                          (QWEN2_LIKE, "q4_0", True), (LONG_CTX, "hvsq2", True)])
-def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype, qk):
-    """qk: Qwen3-style per-head q/k RMSNorm before RoPE (the oracle's is
-    bit-identical to the reference decoder's, test_decoder_oracle.py); in
-    the fused decode attention kernel, and for LONG_CTX in the RoPE/append
-    kernel."""
+@pytest.mark.parametrize("cfg,dtype,qk,bias", [(SMALL, "q4_0", False, ""), (SMALL, "hvsq2", False, ""),
+                                               (QWEN2_LIKE, "q4_0", False, ""), (QWEN2_LIKE, "hvsq2", False, ""),
+                                               (LONG_CTX, "q4_0", False, ""), (SMALL, "hvsq2", True, ""),
+                                               (QWEN2_LIKE, "q4_0", True, ""), (LONG_CTX, "hvsq2", True, ""),
+                                               (QWEN2_LIKE, "q4_0", False, "qkv"), (SMALL, "hvsq2", False, "qkvo"),
+                                               (LONG_CTX, "q4_0", False, "qkvo")])
+def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype, qk, bias):
+    """24 steps, each fed the oracle's greedy token.  qk: Qwen3-style
+    per-head q/k RMSNorm before RoPE (in the fused decode attention kernel,
+    and for LONG_CTX in the RoPE/append kernel).  bias: q/k/v(/o) projection
+    biases, added in the GEMV epilogues (c/qwanto_decode.c:1649-1651, 1722)."""
     rng = np.random.default_rng(31)
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk, biases=bias))
     dec = abi.ResidentDecoder(gpu_ctx, model)
     ref = oracle_lib.decoder(model)
     try:
-        token = 11
-        errs = []
+        token, inputs, gpu_steps, ref_steps = 11, [], [], []
         for step in range(24):
             a, greedy = dec.forward(token)
             b = ref.forward(token)
-            scale = float(np.max(np.abs(b)))
-            err = float(np.max(np.abs(a - b))) / scale
-            errs.append(err)
-            assert err <= STEP_RTOL, f"step {step}: logits differ by {err:.3g} of their scale"
             assert greedy == int(np.argmax(a)), "device argmax is not the first maximum of its logits"
+            inputs.append(token)
+            gpu_steps.append(a)
+            ref_steps.append(b)
+            err = step_errors([a], [b])[0]
             tb = int(np.argmax(b))
             if greedy != tb:
                 top2 = np.sort(b)[-2:]
-                assert top2[1] - top2[0] <= 2 * err * scale, \
+                assert top2[1] - top2[0] <= 2 * err * np.max(np.abs(b)), \
                     f"step {step}: greedy ids differ with margin {top2[1] - top2[0]:.3g}"
             token = tb
-        assert float(np.median(errs)) <= MEDIAN_RTOL, f"median step error {np.median(errs):.3g}"
     finally:
         dec.close()
         ref.close()
+    errs = step_errors(gpu_steps, ref_steps)
+    ok, msg = within_envelope(errs, oracle_envelope(oracle_lib, model, inputs, ref_steps))
+    assert ok, msg
 
 
-PREFILL_ORACLE_RTOL = 2e-2  # gross errors (positions, causal mask, cache layout) move logits by O(1)
-# Models with per-head q/k RMSNorm: unit-RMS keys and queries make the
-# attention logits large, and one int8 step of a Q8 key or activation moves
-# the output logits by up to 2e-2 of their scale.  Measured on the oracle
-# itself: its GEMM outputs moved by 1..8 ulps (the size of the difference
-# between the MFMA GEMM of a 16-token block and the dot8 GEMV of one token,
-# at most 7e-8 of the output scale) move the logits of the LONG_CTX q4_0
-# models of 18..20 prompt tokens by 3.6e-3..1.9e-2 with the greedy tokens
-# held fixed.  Prefill and token-by-token are then compared with this bound
-# and no median.
-QK_FLIP_RTOL = 5e-2
+def read_caches(dec, layers, count):
+    return [dec.kv_read(l, 0, count) for l in range(layers)]
 
 
-@pytest.mark.parametrize("cfg,dtype,P,qk", [(SMALL, "q4_0", 21, False), (SMALL, "hvsq2", 16, False),
-                                            (QWEN2_LIKE, "q4_0", 37, False), (QWEN2_LIKE, "hvsq2", 37, False),
-                                            (QWEN2_LIKE, "hvsq2", 5, False), (LONG_CTX, "q4_0", 18, False),
-                                            (SMALL, "q4_0", 1, False), (QWEN2_LIKE, "hvsq2", 20, True),
-                                            (LONG_CTX, "q4_0", 18, True), (LONG_CTX, "q4_0", 24, True)])
-def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk):
+@pytest.mark.parametrize("cfg,dtype,P,qk,bias", [
+    (SMALL, "q4_0", 21, False, ""), (SMALL, "hvsq2", 16, False, ""), (QWEN2_LIKE, "q4_0", 37, False, ""),
+    (QWEN2_LIKE, "hvsq2", 37, False, ""), (QWEN2_LIKE, "hvsq2", 5, False, ""), (LONG_CTX, "q4_0", 18, False, ""),
+    (SMALL, "q4_0", 1, False, ""), (QWEN2_LIKE, "hvsq2", 20, True, ""), (LONG_CTX, "q4_0", 18, True, ""),
+    (LONG_CTX, "q4_0", 24, True, ""),
+    # biases through the MFMA GEMM epilogue (16-token Q4_0 and 8+-token HyperVSQ-2 blocks) and the dot8 GEMV
+    (QWEN2_LIKE, "q4_0", 37, False, "qkv"), (QWEN2_LIKE, "hvsq2", 20, False, "qkvo"),
+    (SMALL, "q4_0", 5, False, "qkvo")])
+def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
     """qwn_hip_decoder_prefill (prompt blocks of up to 16 tokens through the
-    batched GEMV, block RoPE/append, causal attention per token; the
-    split-attention path for LONG_CTX): the last prompt token's logits and
-    eight forward() steps that read the cache the prefill wrote.
+    batched GEMV / int8 MFMA GEMM, block RoPE/append, causal attention per
+    token; the split-attention path for LONG_CTX): the last prompt token's
+    logits and eight forward() steps that read the cache the prefill wrote.
 
-    Against the same decoder stepping the prompt token by token: the two
-    differ in the fp32 order of the RMSNorm sums (one kernel per token
-    block here, the fused GEMV prologue there) and, for blocks of 8+
-    tokens, of the GEMM sums (int8 MFMA here, dot8 there), so the median
-    step agrees within 1e-5 of the logit scale, any step within STEP_RTOL
-    (q/k-norm models: QK_FLIP_RTOL).
-    Against the oracle stepping the prompt: every step within
-    PREFILL_ORACLE_RTOL.  The token-by-token path's own distance to the
-    oracle is STEP_RTOL-sized per flip, and a flip written into the cache
-    stays in every later step (measured: 6.5e-3 at QWEN2_LIKE, 37 tokens,
-    with or without prefill), so this bound only has to separate such flips
-    from wrong positions, masks or cache slots."""
+    Against the oracle (prompt and the oracle's greedy ids): within the
+    oracle's envelope.  Against the same decoder stepping the prompt token
+    by token: the two differ in the fp32 order of the RMSNorm sums and, for
+    blocks on the MFMA GEMM, of the GEMM sums, so within twice the envelope.
+    Their Q8 caches: layer 0, whose input is the embedding itself, holds the
+    same int8 values except where a value sits at a rounding boundary (one
+    int8 step, at most 2% of the entries); deeper layers carry those flips'
+    effects forward, so at most 5% of their entries may differ."""
     rng = np.random.default_rng(77 + P)
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk, biases=bias))
     prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
     dec = abi.ResidentDecoder(gpu_ctx, model)
     ref = oracle_lib.decoder(model)
     try:
-        for t in prompt:
-            b = ref.forward(int(t))
-        oracle_steps, tokens = [b], []
+        ref_all = [ref.forward(int(t)) for t in prompt]
+        oracle_steps, tokens = [ref_all[-1]], []
         for _ in range(8):
             tokens.append(int(np.argmax(oracle_steps[-1])))
             oracle_steps.append(ref.forward(tokens[-1]))
+        ref_all += oracle_steps[1:]
         a, greedy = dec.prefill(prompt)
         assert greedy == int(np.argmax(a)), "device argmax is not the first maximum of its logits"
+        prefill_caches = read_caches(dec, cfg["layers"], P)
         prefill_steps = [a] + [dec.forward(t)[0] for t in tokens]
         dec.reset()
         for t in prompt:
             a, _ = dec.forward(int(t))
+        step_caches = read_caches(dec, cfg["layers"], P)
         step_steps = [a] + [dec.forward(t)[0] for t in tokens]
-        vs_step, vs_oracle = [], []
-        for pa, sa, ob in zip(prefill_steps, step_steps, oracle_steps):
-            scale = float(np.max(np.abs(ob)))
-            vs_step.append(float(np.max(np.abs(pa - sa))) / scale)
-            vs_oracle.append(float(np.max(np.abs(pa - ob))) / scale)
-        if qk:
-            assert max(vs_step) <= QK_FLIP_RTOL, f"prefill vs token-by-token: {vs_step}"
-            assert max(vs_oracle) <= QK_FLIP_RTOL, f"prefill vs oracle: {vs_oracle}"
-            return
-        assert max(vs_step) <= STEP_RTOL, f"prefill vs token-by-token: {vs_step}"
-        assert float(np.median(vs_step)) <= MEDIAN_RTOL, f"prefill vs token-by-token: {vs_step}"
-        assert max(vs_oracle) <= PREFILL_ORACLE_RTOL, f"prefill vs oracle: {vs_oracle}"
     finally:
         dec.close()
         ref.close()
+    env_all = oracle_envelope(oracle_lib, model, list(prompt) + tokens, ref_all)
+    env = env_all[:, P - 1:]   # the steps compared: the last prompt token and the eight after it
+    ok, msg = within_envelope(step_errors(prefill_steps, oracle_steps), env)
+    assert ok, "prefill vs oracle: " + msg
+    ok, msg = within_envelope(step_errors(prefill_steps, step_steps), env, k=2 * ENV_K)
+    assert ok, "prefill vs token-by-token: " + msg
+    for l, (pc, sc) in enumerate(zip(prefill_caches, step_caches)):
+        for name, x, y in (("keys", pc[0], sc[0]), ("values", pc[1], sc[1])):
+            d = np.abs(x.astype(np.int32) - y.astype(np.int32))
+            frac = float(np.mean(d > 0))
+            print(f"layer {l} {name}: {frac:.3%} of entries differ, by at most {d.max()}")
+            if l == 0:
+                assert d.max() <= 1 and frac <= 0.02, f"layer 0 {name}: {frac:.3%} differ, by up to {d.max()}"
+            else:
+                assert frac <= 0.05, f"layer {l} {name}: {frac:.3%} of entries differ (by up to {d.max()})"
+        for name, x, y in (("key scales", pc[2], sc[2]), ("value scales", pc[3], sc[3])):
+            rel = np.abs(x.astype(np.float64) - y) / np.abs(y)
+            bound = 1.0 / 127 if l == 0 else 0.1
+            assert rel.max() <= bound, f"layer {l} {name}: relative difference {rel.max():.3g}"
+
+
+def test_decoder_cache_matches_oracle_quantization(gpu_ctx, oracle_lib):
+    """The resident decoder's layer-0 cache after its first token: the Q8
+    quantization (c/qwanto_turboquant.c:555-600) of the k and v projections
+    of the normalized embedding row (RoPE is the identity at position 0),
+    recomputed with the oracle: int8 entries equal except where the GEMV's
+    fp32 combination moved a value across a rounding boundary (one step, a
+    handful of entries), scales within an ulp or so."""
+    rng = np.random.default_rng(12)
+    cfg = SMALL
+    model = with_norms(rng, synth.decoder_model(rng, cfg, "q4_0"))
+    dec = abi.ResidentDecoder(gpu_ctx, model)
+    try:
+        dec.forward(7)
+        k, v, ks, vs = dec.kv_read(0, 0, 1)
+    finally:
+        dec.close()
+    KV = cfg["kv_heads"] * cfg["head_dim"]
+    x = model["embed"][7].astype(np.float32)
+    xn = oracle_lib.rmsnorm(x, model["layers"][0]["input_norm"], cfg["rms_eps"])
+    kf = oracle_lib.matmul_q4_0(model["layers"][0]["k"], xn[None, :], KV)[0]
+    vf = oracle_lib.matmul_q4_0(model["layers"][0]["v"], xn[None, :], KV)[0]
+    kq, kss = oracle_lib.q8_quantize(kf)
+    vq, vss = oracle_lib.q8_quantize(vf)
+    assert np.abs(k[0].astype(int) - kq).max() <= 1 and np.mean(k[0] != kq) <= 0.02
+    assert np.abs(v[0].astype(int) - vq).max() <= 1 and np.mean(v[0] != vq) <= 0.02
+    assert np.allclose(ks[0], kss, rtol=1e-6, atol=0) and np.allclose(vs[0], vss, rtol=1e-6, atol=0)
 
 
 def test_generate_equals_stepwise(gpu_ctx):
@@ -178,27 +205,75 @@ def test_generate_equals_stepwise(gpu_ctx):
         dec.close()
 
 
-def test_resident_decoder_qwen2_1p5b_greedy_128(gpu_ctx):
+@pytest.mark.parametrize("name", decode_golden.NAMES)
+def test_resident_decoder_qwen2_1p5b_golden(gpu_ctx, name):
     """Config-2 shape: 28 Q4_0 layers, tied F16 LM head (151936 x 1536), Q8
-    KV; 32-token prompt, 128 greedy ids against the golden ids that the
-    oracle and the reference decoder produced."""
-    if not os.path.exists(GOLDEN):
+    KV; 32-token prompt, 128 greedy steps of the golden decode (the oracle's,
+    bit-identical to the reference decoder's).
+
+    Teacher-forced: the prompt as two 16-token prefill blocks, then the
+    golden ids one forward() at a time; every step's logits against the
+    golden step (decode_golden.step_error: the top-16 logits, nothing else
+    above them), within the golden's stored envelope.  Free-running:
+    generate() gives the golden ids, except past a step whose golden top-two
+    margin is within that step's measured error."""
+    loaded = decode_golden.load(name)
+    if loaded is None:
         pytest.skip("golden decode fixture absent")
-    g = json.load(open(GOLDEN))
-    rng = np.random.default_rng(g["seed"])
-    model = synth.decoder_model(rng, g["config"], g["dtype"])
-    prompt = synth.prompt_tokens(rng, g["config"]["vocab"], len(g["prompt"]))
-    assert prompt.tolist() == g["prompt"]
+    g, model, prompt = loaded
     dec = abi.ResidentDecoder(gpu_ctx, model)
     try:
+        a, greedy = dec.prefill(prompt)
+        errs = [decode_golden.step_error(a, g["steps"][0])]
+        for s, tok in enumerate(g["tokens"][:-1]):
+            a, greedy = dec.forward(tok)
+            errs.append(decode_golden.step_error(a, g["steps"][s + 1]))
+        dec.reset()
         toks, st = dec.generate(prompt, len(g["tokens"]))
     finally:
         dec.close()
-    first_diff = next((i for i, (a, b) in enumerate(zip(toks.tolist(), g["tokens"])) if a != b), None)
-    print(f"resident decoder: {st.generated_tokens} tokens in {st.decode_ms:.1f} ms "
-          f"({st.generated_tokens / (st.decode_ms / 1e3):.1f} tok/s), prefill {st.prefill_ms:.1f} ms, "
-          f"{st.launches_per_step} kernels/step, graph {st.graph}, first divergence {first_diff}")
+    ok, msg = within_envelope(errs, g["envelope"])
+    first_diff = next((i for i, (x, y) in enumerate(zip(toks.tolist(), g["tokens"])) if x != y), None)
+    print(f"{name}: {len(set(g['tokens']))} distinct golden ids, {msg}, "
+          f"{st.generated_tokens / (st.decode_ms / 1e3):.1f} tok/s, first divergence {first_diff}")
+    assert ok, msg
     if first_diff is not None:
-        assert g["margins"][first_diff] < 1e-2, \
+        assert g["margins"][first_diff] <= 2 * errs[first_diff] * g["steps"][first_diff]["max_abs"], \
             f"greedy ids diverge at step {first_diff} with golden margin {g['margins'][first_diff]:.4g}"
     assert st.graph == 1
+
+
+@pytest.mark.parametrize("cfg,dtype,P,M", [(QWEN2_LIKE, "q4_0", 20, 16), (SMALL, "hvsq2", 5, 8),
+                                           (SMALL, "q4_0", 3, 4), (QWEN2_LIKE, "hvsq2", 1, 1),
+                                           (LONG_CTX, "q4_0", 30, 16)])
+def test_verify_block_matches_oracle_steps(gpu_ctx, oracle_lib, cfg, dtype, P, M):
+    """qwn_hip_decoder_verify: M draft tokens after a P-token prompt as one
+    block, logits for every token (the [nodes x vocab] a draft verifier
+    scores, c/qwanto_jetspec.c:160-205), against the oracle stepping the
+    same tokens one at a time; each token's greedy id is the first maximum
+    of its logits.  Then truncate() to keep two of the drafts and step the
+    third token again: its logits agree with the verify block's."""
+    rng = np.random.default_rng(900 + P + M)
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
+    prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
+    draft = synth.prompt_tokens(rng, cfg["vocab"], M)
+    dec = abi.ResidentDecoder(gpu_ctx, model)
+    ref = oracle_lib.decoder(model)
+    try:
+        ref_all = [ref.forward(int(t)) for t in list(prompt) + list(draft)]
+        dec.prefill(prompt, logits=False)
+        logits, ids = dec.verify(draft)
+        assert ids.tolist() == [int(np.argmax(row)) for row in logits]
+        again = None
+        if M >= 3:
+            dec.truncate(P + 2)
+            again, _ = dec.forward(int(draft[2]))
+    finally:
+        dec.close()
+        ref.close()
+    env = oracle_envelope(oracle_lib, model, list(prompt) + list(draft), ref_all)[:, P:]
+    ok, msg = within_envelope(step_errors(list(logits), ref_all[P:]), env)
+    assert ok, "verify vs oracle: " + msg
+    if again is not None:
+        ok, msg = within_envelope(step_errors([again], [logits[2]]), env[:, 2:3], k=2 * ENV_K)
+        assert ok, "step after truncate vs verify: " + msg
