@@ -234,6 +234,21 @@ QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device(QwnCudaContextHandle *conte
                                                      uint32_t position, float scale,
                                                      void *workspace, void *stream);
 
+/* The same attention with no workspace argument and no allocation: the
+ * split partials live in a file-scope device array of 4 MiB per GPU (its
+ * address looked up once per device at context creation).  No counterpart
+ * in the reference; for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid hipMalloc).  A request whose partials
+ * exceed the array (qwn_hip_ext_attention_workspace_bytes() > 4 MiB) is
+ * refused with QWN_CUDA_STATUS_INVALID_ARGUMENT.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on a GPU (other streams,
+ * other contexts on the same device) race. */
+QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device_noalloc(QwnCudaContextHandle *context,
+                                                             QwnCudaKvCacheHandle *cache,
+                                                             const float *query, float *output,
+                                                             uint32_t query_heads, uint32_t position,
+                                                             float scale, void *stream);
+
 /* Debug: the integer sums of the GEMV for one token, computed by the same
  * device code as the GEMV (host pointers, synchronous).  HyperVSQ-2:
  * out[row][block*8 + octant] = sum (code-1)*a; Q4_0: out[row][block] =

@@ -56,6 +56,7 @@ EXT_EXPORTS = (
     "qwn_hip_ext_mfma_image_bytes", "qwn_hip_ext_mfma_image_device", "qwn_hip_ext_gemm_mfma_device",
     "qwn_hip_ext_gemm_mfma_group_device", "qwn_hip_ext_upload_batch", "qwn_hip_ext_plan_residency",
     "qwn_hip_ext_debug_mfma_int_sums", "qwn_hip_ext_debug_kv_read",
+    "qwn_hip_ext_kv_attention_device_noalloc",
 )
 DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
@@ -302,6 +303,10 @@ class Library:
                                                         ctypes.c_void_p, ctypes.c_uint32,
                                                         ctypes.c_uint32, ctypes.c_float,
                                                         ctypes.c_void_p, ctypes.c_void_p]
+        lib.qwn_hip_ext_kv_attention_device_noalloc.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
+                                                                ctypes.c_void_p, ctypes.c_uint32,
+                                                                ctypes.c_uint32, ctypes.c_float,
+                                                                ctypes.c_void_p]
         lib.qwn_hip_ext_debug_int_sums.argtypes = [P(Handle), P(Handle), ctypes.c_void_p,
                                                    ctypes.c_void_p, ctypes.c_uint64]
         lib.qwn_hip_ext_debug_mfma_int_sums.argtypes = [P(Handle), P(Handle), V, U32, V, ctypes.c_uint64]

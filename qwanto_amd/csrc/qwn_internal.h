@@ -271,6 +271,11 @@ hipError_t launch_kv_append(const KvCache &c, const float *key,
                             const float *value, uint32_t token,
                             hipStream_t stream, uint32_t count = 1);
 
+// Looks up, once per device (which must be current), the device address of
+// the allocation-free attention's file-scope partials array
+// (qwn_noalloc.hip).
+hipError_t noalloc_init_device(int device);
+
 // Token-major copy of cached tokens [first, first + count) (debug readback):
 // keys/values [count][channels], scales [count][groups].
 hipError_t launch_kv_gather(const KvCache &c, uint32_t first, uint32_t count, int8_t *keys, int8_t *values,

@@ -359,6 +359,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *op
     ctx->device = options->device_id;
     ctx->budget = options->memory_budget_bytes;
     hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = qwn::noalloc_init_device(ctx->device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_end);
