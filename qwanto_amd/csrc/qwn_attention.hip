@@ -30,24 +30,26 @@ namespace {
 constexpr int kAttnThreads = 256;
 constexpr int kMaxSplitTokens = 256;
 
+// Each KV head's pages are contiguous, so a workgroup streaming one head's
+// span of the context reads one contiguous run of keys and one of values.
 // key byte of (token, head, channel); channels 16q .. 16q + 15 of a token
 // are the 16 bytes at k_index(token, head, 16q)
 __device__ __forceinline__ size_t k_index(const KvCache &c, uint32_t token, uint32_t head, uint32_t dim) {
     const uint32_t page = token / kKvPageTokens, slot = token % kKvPageTokens;
     const uint32_t chunks = (c.head_dim + 15) / 16;
-    return (((static_cast<size_t>(page) * c.kv_heads + head) * chunks + dim / 16) * kKvPageTokens + slot) * 16 +
+    return (((static_cast<size_t>(head) * c.pages + page) * chunks + dim / 16) * kKvPageTokens + slot) * 16 +
            dim % 16;
 }
 
 // value byte of (token, head, channel)
 __device__ __forceinline__ size_t v_offset(const KvCache &c, uint32_t token, uint32_t head, uint32_t dim) {
     const uint32_t page = token / kKvPageTokens, slot = token % kKvPageTokens;
-    return ((static_cast<size_t>(page) * c.kv_heads + head) * c.head_dim + dim) * kKvPageTokens + slot;
+    return ((static_cast<size_t>(head) * c.pages + page) * c.head_dim + dim) * kKvPageTokens + slot;
 }
 
 // the 16 value bytes of (page, head, channel)
 __device__ __forceinline__ size_t v_page_offset(const KvCache &c, uint32_t page, uint32_t head, uint32_t dim) {
-    return ((static_cast<size_t>(page) * c.kv_heads + head) * c.head_dim + dim) * kKvPageTokens;
+    return ((static_cast<size_t>(head) * c.pages + page) * c.head_dim + dim) * kKvPageTokens;
 }
 
 __device__ __forceinline__ void store_q8(const KvCache &c, bool is_v, uint32_t token, uint32_t head, uint32_t dim,
@@ -56,9 +58,12 @@ __device__ __forceinline__ void store_q8(const KvCache &c, bool is_v, uint32_t t
     else c.keys[k_index(c, token, head, dim)] = q;
 }
 
-// scale of (token, group)
+// scale of (token, group): [group][64-token quad][slot 0..15][page of the
+// quad 0..3], so the four floats at scale_index(64q + slot, g) are the
+// scales of tokens slot, 16 + slot, 32 + slot, 48 + slot of quad q
 __device__ __forceinline__ size_t scale_index(const KvCache &c, uint32_t token, uint32_t group) {
-    return (static_cast<size_t>(token / kKvPageTokens) * c.groups + group) * kKvPageTokens + token % kKvPageTokens;
+    return ((static_cast<size_t>(group) * c.quads + token / (4 * kKvPageTokens)) * kKvPageTokens +
+            token % kKvPageTokens) * 4 + (token / kKvPageTokens) % 4;
 }
 
 // grid (groups, 2, tokens): y = 0 quantizes K, y = 1 quantizes V; z is the
@@ -935,6 +940,27 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + dpp_rot<0x121>(v);
 }
 
+// DPP quad permutations: quad_perm<ctrl> moves within each 4-lane quad
+// (0xb1: lane ^ 1, 0x4e: lane ^ 2); quad_bcast_u32(v, q) gives every lane of
+// the quad lane q's v.
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t quad_bcast_u32(uint32_t v, int q) {
+    const int x = static_cast<int>(v);
+    switch (q) {
+    case 0: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x00, 0xf, 0xf, false));
+    case 1: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x55, 0xf, 0xf, false));
+    case 2: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xaa, 0xf, 0xf, false));
+    default: return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xff, 0xf, 0xf, false));
+    }
+}
+
+__device__ __forceinline__ float f4_at(const float4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 __device__ __forceinline__ void lds_wave_sync() {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -978,45 +1004,123 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
     const uint32_t col = lane % 16, kq = lane / 16;   // MFMA column / k-quarter of this lane
 
     // 1. query pieces (A of the scores), this lane: head (col / 4) of row
-    //    tile rt, piece col % 4, channels 64g + 16kq .. +15
+    //    tile rt, piece col % 4, channels 64g + 16kq .. +15.  Where the
+    //    registers allow (kEarly), the query loads are issued first, then the
+    //    first block's keys and values, and the pieces are computed while
+    //    those are in flight (loads retire in order, so a query load issued
+    //    after them would wait for them).
+    constexpr bool kEarly = D <= 128 && RT * NG <= 4;
     att_v4i qa[RT][NG];
     float qs1[RT][NG];   // s1 of head kq (+ 4rt): the C-layout head of this lane
+    float4 xq[kEarly ? RT : 1][kEarly ? NG : 1];
+    // The four lanes of a quad (piece col % 4) share a head and 16
+    // channels: lane p loads and splits channels 4p .. 4p + 3, and the
+    // quad exchanges the pieces.  Rows past the group load head 0's
+    // channels (no branch around the loads, so the waits that follow can
+    // count them exactly) and are zeroed where the pieces are made.
+    auto load_query = [&](int rt, int g) -> float4 {
+        const uint32_t hl = rt * 4 + col / 4;
+        return *reinterpret_cast<const float4 *>(a.query + static_cast<size_t>(kvh * G + (hl < G ? hl : 0u)) * D +
+                                                 64 * g + 16 * kq + 4 * (col % 4));
+    };
+    auto make_pieces = [&](int rt, int g, float4 xin) {
+        const uint32_t piece = col % 4;
+        const bool row_ok = rt * 4 + col / 4 < G;
+        const float x[4] = {row_ok ? xin.x : 0.0f, row_ok ? xin.y : 0.0f, row_ok ? xin.z : 0.0f,
+                            row_ok ? xin.w : 0.0f};
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax = fmaxf(amax, quad_perm<0xb1>(amax));   // lanes p ^ 1
+        amax = fmaxf(amax, quad_perm<0x4e>(amax));   // lanes p ^ 2
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const float s1 = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
+        const float inv1 = amax > 0.0f ? 127.0f / amax : 1.0f;
+        // mine[j]: piece j of my four channels, one byte each
+        uint32_t mine[3] = {0, 0, 0};
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t pc = three_pieces(x[e], s1, inv1);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) mine[j] |= ((pc >> (8 * j)) & 0xffu) << (8 * e);
+        }
+        // word q of my operand: piece `piece` of lane q's channels
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t b0 = quad_bcast_u32(mine[0], q), b1 = quad_bcast_u32(mine[1], q);
+            const uint32_t b2 = quad_bcast_u32(mine[2], q);
+            w[q] = piece == 0 ? b0 : piece == 1 ? b1 : piece == 2 ? b2 : 0u;
+        }
+        qa[rt][g] = att_v4i{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
+                            static_cast<int>(w[3])};
+        // head h's scale sits in lane 4h (kq 0, piece 0)
+        qs1[rt][g] = __shfl(s1, 4 * kq);
+    };
+    if constexpr (kEarly) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) xq[rt][g] = load_query(rt, g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. loads of a block: keys (B of the scores) for token b0 + 16i + col
+    //    and its scales; value words (B of P.V) of page b0/16 + kq, channel
+    //    64g + 16n + col.  Tokens past t1 read a valid token (t0) and are
+    //    masked.  The next block's loads are issued before this block's
+    //    arithmetic.
+    struct BlockLoads {
+        att_v4i kb[NG][NT], vb[NG][4];
+        float4 ks[NG], vs[NG];   // .x .. .w: scales of tokens b0 + col, + 16, + 32, + 48
+    };
+    auto load_block = [&](uint32_t b0, BlockLoads &L) {
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const uint32_t t = b0 + 16 * i + col;
+            const uint32_t tl = t < t1 ? t : t0;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                L.kb[g][i] = *reinterpret_cast<const att_v4i *>(c.keys + k_index(c, tl, kvh, 64 * g + 16 * kq));
+        }
+        // b0 starts a 64-token quad: one 16-byte load per scale group gives
+        // this lane's token in each of the four pages (masked tokens read
+        // slots of the same quad, which hold finite values)
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const uint32_t hl = rt * 4 + col / 4, piece = col % 4;
-            float x[16];
-            if (hl < G) {
-                const float4 *src = reinterpret_cast<const float4 *>(
-                    a.query + static_cast<size_t>(kvh * G + hl) * D + 64 * g + 16 * kq);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float4 v = src[i];
-                    x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) x[i] = 0.0f;
-            }
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 16));
-            amax = fmaxf(amax, __shfl_xor(amax, 32));
-            const float s1 = amax > 0.0f ? amax * (1.0f / 127.0f) : 1.0f;
-            const float inv1 = amax > 0.0f ? 127.0f / amax : 1.0f;
-            uint32_t w[4] = {0, 0, 0, 0};
-            if (piece < 3) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    w[i / 4] |= ((three_pieces(x[i], s1, inv1) >> (8 * piece)) & 0xffu) << (8 * (i % 4));
-            }
-            qa[rt][g] = att_v4i{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
-                                static_cast<int>(w[3])};
-            // head h's scale sits in lane 4h (kq 0, piece 0)
-            qs1[rt][g] = __shfl(s1, 4 * kq);
+            L.ks[g] = *reinterpret_cast<const float4 *>(c.key_scales + scale_index(c, b0 + col, kvh * NG + g));
+            L.vs[g] = *reinterpret_cast<const float4 *>(c.value_scales + scale_index(c, b0 + col, kvh * NG + g));
         }
+        const uint32_t pt = b0 + 16 * kq;
+        const uint32_t pg = (pt < t1 ? pt : t0) / kKvPageTokens;
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+                L.vb[g][n] = *reinterpret_cast<const att_v4i *>(c.values + v_page_offset(c, pg, kvh, 64 * g + 16 * n + col));
+    };
+    // blocks of this wave: b0, b0 + step, ... below t1 (wave-uniform)
+    const uint32_t step = 64 * NW;
+    uint32_t b0 = t0 + 64 * wave;
+    const uint32_t nblk = b0 < t1 ? (t1 - b0 + step - 1) / step : 0u;
+    const uint32_t last = b0 + (nblk ? nblk - 1 : 0u) * step;
+    BlockLoads buf0;
+    if constexpr (kEarly) {
+        // unconditional (a wave without blocks loads the split's first
+        // block and never uses it): no branch for the waits to merge over
+        load_block(nblk ? b0 : t0, buf0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) make_pieces(rt, g, xq[rt][g]);
+    } else {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) make_pieces(rt, g, load_query(rt, g));
+        __builtin_amdgcn_sched_barrier(0);
+        if (D <= 128 && nblk) load_block(b0, buf0);
+    }
 
     float m_run[RT], l_run[RT], o_acc[RT][NG][4];
 #pragma unroll
@@ -1029,46 +1133,11 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
             for (int n = 0; n < 4; ++n) o_acc[rt][g][n] = 0.0f;
     }
 
-    // 2. loads of a block: keys (B of the scores) for token b0 + 16i + col
-    //    and its scales; value words (B of P.V) of page b0/16 + kq, channel
-    //    64g + 16n + col.  Tokens past t1 read a valid token (t0) and are
-    //    masked.  The next block's loads are issued before this block's
-    //    arithmetic.
-    struct BlockLoads {
-        att_v4i kb[NG][NT], vb[NG][4];
-        float ks[NG][NT], vs[NG][NT];
-    };
-    auto load_block = [&](uint32_t b0, BlockLoads &L) {
-#pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const uint32_t t = b0 + 16 * i + col;
-            const uint32_t tl = t < t1 ? t : t0;
-#pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                L.kb[g][i] = *reinterpret_cast<const att_v4i *>(c.keys + k_index(c, tl, kvh, 64 * g + 16 * kq));
-                L.ks[g][i] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
-                L.vs[g][i] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
-            }
-        }
-        const uint32_t pt = b0 + 16 * kq;
-        const uint32_t pg = (pt < t1 ? pt : t0) / kKvPageTokens;
-#pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-            for (int n = 0; n < 4; ++n)
-                L.vb[g][n] = *reinterpret_cast<const att_v4i *>(c.values + v_page_offset(c, pg, kvh, 64 * g + 16 * n + col));
-    };
-    // (at head_dim 256 two blocks of loads do not fit the registers: no prefetch)
-    constexpr bool kPrefetch = D <= 128;
-    BlockLoads cur, nxt;
-    if (kPrefetch && t0 + 64 * wave < t1) load_block(t0 + 64 * wave, cur);
-    for (uint32_t b0 = t0 + 64 * wave; b0 < t1; b0 += 64 * NW) {
-        if (!kPrefetch) load_block(b0, cur);
-        else if (b0 + 64 * NW < t1) load_block(b0 + 64 * NW, nxt);
+    auto process_block = [&](const BlockLoads &cur, uint32_t b0) {
         const att_v4i (&kb)[NG][NT] = cur.kb;
         const att_v4i (&vb)[NG][4] = cur.vb;
-        const float (&ks)[NG][NT] = cur.ks;
-        const float (&vs)[NG][NT] = cur.vs;
+        const float4 (&ks)[NG] = cur.ks;
+        const float4 (&vs)[NG] = cur.vs;
         bool valid[NT];
 #pragma unroll
         for (int i = 0; i < NT; ++i) valid[i] = b0 + 16 * i + col < t1;
@@ -1084,7 +1153,7 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
                 for (int g = 0; g < NG; ++g) {
                     const att_v4i cacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[rt][g], kb[g][i],
                                                                                att_v4i{0, 0, 0, 0}, 0, 0, 0);
-                    dot = fmaf(pieces_dot(cacc, qs1[rt][g]), ks[g][i], dot);
+                    dot = fmaf(pieces_dot(cacc, qs1[rt][g]), f4_at(ks[g], i), dot);
                 }
                 sc[i] = valid[i] ? dot * a.scale : -INFINITY;
             }
@@ -1108,7 +1177,7 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
                 float pv[NT], am = 0.0f;
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
-                    pv[i] = p[i] * vs[g][i];
+                    pv[i] = p[i] * f4_at(vs[g], i);
                     am = fmaxf(am, pv[i]);
                 }
                 am = row16_max(am);
@@ -1140,7 +1209,27 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
             }
             lds_wave_sync();
         }
-        if (kPrefetch) cur = nxt;
+    };
+    // Two load buffers used in turn (no register copy between them, so the
+    // wait before a block covers that block's loads only and the next
+    // block's stay in flight).  The last prefetch of a wave re-reads its
+    // current block (an L2 hit) so every load is unconditional.  At head_dim
+    // 256 two buffers do not fit the registers: load, then compute.
+    if constexpr (D <= 128) {
+        BlockLoads buf1;
+        for (uint32_t k = 1; k < nblk; k += 2) {
+            load_block(b0 + step, buf1);
+            process_block(buf0, b0);
+            load_block(min(b0 + 2 * step, last), buf0);
+            process_block(buf1, b0 + step);
+            b0 += 2 * step;
+        }
+        if (nblk % 2) process_block(buf0, b0);
+    } else {
+        for (; b0 < t1; b0 += step) {
+            load_block(b0, buf0);
+            process_block(buf0, b0);
+        }
     }
 
     // 7. merge the four waves: lane (kq, col) holds head kq (+4rt), channel
@@ -1240,11 +1329,13 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base) {
     c.channels = c.kv_heads * c.head_dim;
     c.groups = (c.channels + 63u) / 64u;
     c.pages = (c.max_tokens + kKvPageTokens - 1) / kKvPageTokens;
+    c.quads = (c.pages + 3) / 4;
     const size_t slots = static_cast<size_t>(c.pages) * kKvPageTokens;
     const size_t padded_dim = (c.head_dim + 15u) / 16u * 16u;
     const size_t key_bytes = (slots * c.kv_heads * padded_dim + 255) & ~static_cast<size_t>(255);
     const size_t value_bytes = (slots * c.channels + 255) & ~static_cast<size_t>(255);
-    const size_t scale_bytes = (slots * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
+    const size_t scale_bytes =
+        (static_cast<size_t>(c.quads) * 4 * kKvPageTokens * c.groups * sizeof(float) + 255) & ~static_cast<size_t>(255);
     if (base) {
         c.keys = reinterpret_cast<int8_t *>(base);
         c.values = reinterpret_cast<int8_t *>(base + key_bytes);
@@ -1296,19 +1387,24 @@ bool mfma_attention_supported(const KvCache &c, uint32_t query_heads) {
 // 64-token blocks with the next block's loads in flight; tokens per
 // workgroup one block per wave, doubled while the grid would exceed 256
 // workgroups (one per CU, every workgroup resident in one round) or a KV
-// head kMfmaMaxSplits splits.  Measured on MI355X at 32 query / 8 KV heads:
-// one or two waves per workgroup and grids of up to 1024 workgroups (one
-// block per wave, no prefetch) ran slower at 4096 and at 32768 tokens.
+// head kMfmaMaxSplits splits.  Measured on MI355X at 32 query / 8 KV heads,
+// 4096 and 32768 tokens: one, two or eight waves per workgroup and grids of
+// 512 or 1024 workgroups all ran slower (at 32768 tokens the 256-workgroup
+// kernel already streams the cache at about 5 TB/s).
 struct MfmaAttnPlan {
     uint32_t waves, split, nsplit;
 };
 
+constexpr uint32_t kMfmaAttnWaves = 4;
+constexpr uint32_t kMfmaAttnMaxWgs = 256;
+
 MfmaAttnPlan mfma_attn_plan(const KvCache &c, uint32_t span) {
     MfmaAttnPlan p;
-    p.waves = 4;
+    p.waves = kMfmaAttnWaves;
     uint64_t s = 64u * p.waves;
     // stops at one split (s >= span) whatever the KV head count
-    while (s < span && ((span + s - 1) / s * c.kv_heads > 256 || (span + s - 1) / s > kMfmaMaxSplits)) s *= 2;
+    while (s < span && ((span + s - 1) / s * c.kv_heads > kMfmaAttnMaxWgs || (span + s - 1) / s > kMfmaMaxSplits))
+        s *= 2;
     p.split = static_cast<uint32_t>(std::min<uint64_t>(s, 0x80000000u));
     p.nsplit = static_cast<uint32_t>((static_cast<uint64_t>(span) + p.split - 1) / p.split);
     return p;

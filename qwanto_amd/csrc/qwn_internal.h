@@ -236,10 +236,11 @@ struct KvCache {
     uint32_t channels = 0;
     uint32_t groups = 0;       // ceil(channels / 64) scale groups per token
     uint32_t pages = 0;        // ceil(max_tokens / 16)
+    uint32_t quads = 0;        // ceil(pages / 4): 64-token groups of pages
     uint32_t tokens = 0;
-    int8_t *keys = nullptr;    // [pages][kv_heads][head_dim/16][16 tokens][16 channels]
-    int8_t *values = nullptr;  // [pages][kv_heads][head_dim][16 tokens]
-    float *key_scales = nullptr;    // [pages][groups][16 tokens]
+    int8_t *keys = nullptr;    // [kv_heads][pages][head_dim/16][16 tokens][16 channels]
+    int8_t *values = nullptr;  // [kv_heads][pages][head_dim][16 tokens]
+    float *key_scales = nullptr;    // [groups][quads][16 slots][4 pages]
     float *value_scales = nullptr;
     uint64_t bytes = 0;
 };
