@@ -441,7 +441,7 @@ def batch_sweep(torch, ctx, steps, warmup):
     """GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers (weights
     read once per launch): HyperVSQ-2 on the Qwen3-4B shapes (36 layers per
     token in tokens_per_s), and under "q4_0" Q4_0 on the Qwen2-1.5B shapes
-    (28 layers); dot8 grouped launches below 8 tokens (Q4_0: 16), grouped
+    (28 layers); dot8 grouped launches below 3 tokens (Q4_0: 16), grouped
     int8-MFMA launches from there (MFMA utilisation = useful int8 ops /
     dense int8 peak)."""
     from qwanto_amd import synth
@@ -449,7 +449,7 @@ def batch_sweep(torch, ctx, steps, warmup):
     def sweep(kind, shapes, model_layers, seed0):
         res = {}
         for M in (1, 2, 4, 8, 16):
-            mfma = M >= (16 if kind == "q4_0" else 8)    # the library's own choice
+            mfma = M >= (16 if kind == "q4_0" else 3)    # the library's own choice (mfma_batch)
             if not mfma:
                 sw = Sweep(torch, ctx, kind, shapes, 4, seed=seed0 + M, batch=M)
                 ms = time_graph(torch, sw.grouped, steps, warmup)

@@ -205,13 +205,16 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate = false,
                                   int32_t *dump = nullptr, const float *const *biases = nullptr);
-constexpr uint32_t kMfmaMinTokens = 8;
+constexpr uint32_t kMfmaMinTokens = 3;
 // LDS per workgroup the MFMA GEMM plans its staging against: gfx950's
 // 160 KB (context creation refuses a device that reports less).
 constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
 // Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV:
-// HyperVSQ-2 from 8 tokens; Q4_0 (one 16x16x32 MFMA per 32-weight block,
-// the same time at 8 tokens as at 16) from a full 16-token tile.
+// HyperVSQ-2 from 3 tokens (measured on Qwen3-4B layers: the MFMA GEMM takes
+// about 25 us per layer whatever the token count up to 16, the dot8 GEMV
+// 17.9 us at 1 token, 22.8 at 2 and 33.4 at 4, which is how 3 tokens run);
+// Q4_0 (one 16x16x32 MFMA per 32-weight block, the same time at 8 tokens as
+// at 16, slower than the dot8 GEMV below 16) from a full 16-token tile.
 inline bool mfma_batch(uint32_t kind, uint32_t batch) {
     return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= 16);
 }

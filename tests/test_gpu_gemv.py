@@ -144,7 +144,8 @@ def run_mfma_group(ctx, oracle_lib, kind, Ns, K, M, seed, accumulate=False):
 
 @pytest.mark.parametrize("Ns,K,M", [((4096, 1024, 1024), 2560, 16), ((9728, 9728), 2560, 16),
                                     ((8200, 77), 777, 9), ((16390, 5), 520, 11), ((300,), 16384, 8),
-                                    ((2560,), 9728, 12)])
+                                    ((2560,), 9728, 12), ((4096, 1024, 1024), 2560, 3),
+                                    ((9728, 9728), 2560, 4), ((2560,), 9728, 5)])
 def test_hvsq2_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
     """qwn_hip_ext_gemm_mfma_group_device: one MFMA launch over tensors of
     equal columns sharing one image (q/k/v and gate/up shapes, 32- and
@@ -196,9 +197,9 @@ def test_q4_0_batched(gpu_ctx, oracle_lib, M):
 
 
 @pytest.mark.parametrize("N,K,M", [(77, 700, 8), (130, 513, 9), (1, 256, 8), (64, 256, 16), (300, 7936, 12),
-                                   (2560, 4096, 16)])
+                                   (2560, 4096, 16), (77, 700, 3), (130, 513, 4), (300, 7936, 7)])
 def test_hvsq2_mfma_ragged(gpu_ctx, oracle_lib, N, K, M):
-    """HyperVSQ-2 from 8 tokens runs on int8 MFMA tiles (16 rows x 16
+    """HyperVSQ-2 from 3 tokens runs on int8 MFMA tiles (16 rows x 16
     tokens): ragged rows, partial blocks, partial token tiles."""
     check_hvsq2(gpu_ctx, oracle_lib, N, K, seed=N + K + M, M=M)
 
@@ -426,6 +427,7 @@ def hvsq2_block_products(w, sum_q, N, K):
 
 
 @pytest.mark.parametrize("kind,N,K,M", [("hvsq2", 300, 2560, 16), ("hvsq2", 77, 4096, 9), ("hvsq2", 40, 700, 12),
+                                        ("hvsq2", 300, 2560, 3), ("hvsq2", 77, 9728, 4),
                                         ("q4_0", 200, 1536, 16), ("q4_0", 1536, 8960, 16), ("q4_0", 33, 100, 11)])
 def test_mfma_int32_block_dots(gpu_ctx, oracle_lib, kind, N, K, M):
     """The MFMA GEMM's per-block int32 dots, dumped by the same kernel (same
