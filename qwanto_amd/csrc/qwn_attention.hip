@@ -449,36 +449,32 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
 
 // ---- decode attention -------------------------------------------------------
 //
-// One workgroup per query head, 256 threads, for contexts up to 1024 tokens
-// (latency-bound: the K/V rows are re-read per query head from L2; longer
-// contexts use the MFMA kernel below).  The kernel also handles splits with
-// all G query heads of a KV head per workgroup (heads_per_wg), which the
-// launcher does not use.  Online softmax over chunks of 256 tokens; one
-// split writes the output.  Each chunk is one memory round
-// trip: a thread loads one token's whole key row (scores) and, at the same
-// time, the value bytes it needs later; nothing waits on a cross-lane
-// reduction per token.
-//   scores: thread = token, s_g = sum over 64-channel groups of
-//           k_scale * sum q_g,c * k_c (the group scale factored out)
+// One workgroup of 256 x TPT threads per query head, the whole context (up
+// to 1024 tokens) in one split: the short-context decode step, bound by
+// memory latency, the rate one CU pulls a chunk in (~70 KB for 256 tokens)
+// and the per-token arithmetic, not by bytes (a KV head's query heads read
+// its rows from L2).  Online softmax over chunks of 256 tokens; every load
+// of a chunk is one round trip, the first chunk's issued with the query's
+// before anything waits.
+//   scores: TPT adjacent lanes per token, each D/TPT channels of its key
+//           row, scaled per 64-channel group, summed by lane swaps
 //   P.V:    thread = (channel, phase of 4-token groups); the chunk's value
-//           words (16 tokens of one channel) are staged in LDS in the
-//           cache's own channel-major page order; phases summed through
-//           LDS at the end
+//           words (16 tokens of one channel) staged in LDS in the cache's
+//           own channel-major page order; phases summed through LDS at the
+//           end
 //
-// Decode mode (key != null): the workgroup also applies RoPE to its query
-// heads (c/qwanto_decode.c:686-729) and, for the split holding the current
-// position, rotates and Q8-quantizes the current key and value
-// (c/qwanto_turboquant.c:555-600), stores them in the cache for later steps
-// and attends to them from LDS.
+// Decode mode (key != null): RoPE on the query head (c/qwanto_decode.c:
+// 686-729), optionally after a per-head RMSNorm of query and key (654-684),
+// and the current key (rotated) and value Q8-quantized (c/qwanto_turboquant.c:
+// 555-600), stored in the cache for later steps and attended to from LDS.
+// Prefill mode (key == null): grid z is the query token of a block, its
+// query already rotated and its key/value already in the cache.
 struct DecodeAttnArgs {
     KvCache c;
     const float *query;      // [H][D]
-    float *output;           // [H][D] (nsplit == 1)
-    float *partials;         // [H][nsplit][D + 2] (nsplit > 1)
+    float *output;           // [H][D]
     uint32_t group;          // query heads per KV head
-    uint32_t heads_per_wg;   // query heads one workgroup handles (divides group)
-    uint32_t split;
-    uint32_t nsplit;
+    uint32_t span;           // attends to tokens [0, min(position + 1, span))
     float scale;
     uint32_t position;
     const int32_t *position_ptr;
@@ -494,20 +490,6 @@ struct DecodeAttnArgs {
     float eps;
 };
 
-__device__ __forceinline__ float rope_at(const float *x, uint32_t d, uint32_t half, const float *ct, const float *st) {
-    const uint32_t i = d < half ? d : d - half;
-    const float a = x[i], b = x[i + half];
-    return d < half ? fmaf(a, ct[i], -(b * st[i])) : fmaf(a, st[i], b * ct[i]);
-}
-
-// The same after a per-head RMSNorm, (x * inv) * w (c/qwanto_decode.c:654-684).
-__device__ __forceinline__ float rope_norm_at(const float *x, uint32_t d, uint32_t half, const float *ct,
-                                              const float *st, float inv, const float *w) {
-    const uint32_t i = d < half ? d : d - half;
-    const float a = (x[i] * inv) * w[i], b = (x[i + half] * inv) * w[i + half];
-    return d < half ? fmaf(a, ct[i], -(b * st[i])) : fmaf(a, st[i], b * ct[i]);
-}
-
 __device__ __forceinline__ int8_t q8_of(float x, float scale) {
     if (!isfinite(x)) return 0;
     const float s = x / scale;  // IEEE division, like the CPU path
@@ -518,165 +500,211 @@ __device__ __forceinline__ float i8f(uint32_t w, int i) {
     return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xffu));
 }
 
-template <int D, int GMAX>
-__global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a) {
+template <int D, int TPT>
+__global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnArgs a) {
+    constexpr int NT = 256 * TPT, NW = NT / 64;
     constexpr int NG = D / 64;                 // Q8 scale groups per head
-    constexpr int KW = D / 16;                 // uint4 words of one key row
-    constexpr int CH = D <= 128 ? 256 : 128;   // tokens per chunk (V staged in LDS)
-    constexpr int VW = CH * D / 16 / 256;      // value words (16 tokens x 1 channel) per thread
-    constexpr int PH = 256 / D;                // P.V: phases of 4-token groups
-    __shared__ __align__(16) float q_s[GMAX * D];
-    __shared__ __align__(16) float s_s[GMAX * CH];
-    __shared__ float red[2][4][GMAX];
-    __shared__ __align__(16) float pv_s[PH * GMAX * D];
+    constexpr int CH = 256;                    // tokens per chunk, TPT lanes each in the scores
+    constexpr int CPT = D / TPT;               // key channels per lane
+    constexpr int KWT = CPT / 16;              // uint4 key words per lane
+    constexpr int KGL = CPT >= 64 ? CPT / 64 : 1;    // key scale groups per lane
+    constexpr int WPG = KWT / KGL;                   // key words per lane and group
+    constexpr int VGL = (NG + TPT - 1) / TPT;        // value scale groups per lane
+    constexpr int VW = CH * D / 16 / NT;       // value words (16 tokens x 1 channel) per thread
+    constexpr int PH = NT / D;                 // P.V: phases of 4-token groups
+    constexpr uint32_t half = D / 2;
+    static_assert(NT / TPT == CH && (CPT >= 64 ? CPT % 64 == 0 : 64 % CPT == 0) && VW >= 1 && PH >= 1,
+                  "decode attention geometry");
+    __shared__ __align__(16) float q_s[D];
+    __shared__ __align__(16) float s_s[CH];
+    __shared__ float red[2][NW];
+    __shared__ __align__(16) float pv_s[PH * D];
     __shared__ __align__(16) uint4 v_s[CH / 16 * D];   // the chunk's values [page][channel][16 tokens]
     __shared__ float vsc_s[CH * NG];                   // and their scales
     __shared__ __align__(16) int8_t kcur[D];
     __shared__ __align__(16) int8_t vcur[D];
     __shared__ float kcur_s[NG], vcur_s[NG];
+    __shared__ float nrm_s[8];
     const KvCache &c = a.c;
-    // this workgroup: KV head kvh, its query heads h0 .. h0 + G - 1
-    const uint32_t G = a.heads_per_wg, wgs_per_kv = a.group / G;
-    const uint32_t kvh = blockIdx.y / wgs_per_kv, split = blockIdx.x;
-    const uint32_t h0 = kvh * a.group + (blockIdx.y % wgs_per_kv) * G;
-    const bool writer = blockIdx.y % wgs_per_kv == 0;  // appends the current token
-    const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-    const uint32_t t0 = split * a.split;
-    // One round trip per chunk: thread tid takes token c0 + tid -- its key
-    // row and scales -- and VW value words (page, channel) of the chunk;
-    // threads past the chunk's n tokens, and pages without one, read the
-    // split's first token or page again (cache hits), and are masked.  The
-    // current token's slot is being written by this launch: its key, value
-    // bytes and scales come from LDS.
-    uint4 kr[KW], vr[VW];
-    float ks[NG], vsc[NG];
-    auto load_chunk = [&](uint32_t c0, uint32_t n) {
-        const uint32_t tl = tid < n ? c0 + tid : t0;
+    const uint32_t head = blockIdx.y, kvh = head / a.group;
+    const bool writer = head % a.group == 0;  // appends the current token
+    const uint32_t tid = threadIdx.x, lane = tid % 64;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const uint32_t slot = tid / TPT, part = tid % TPT;
+    const uint32_t kgrp = part * CPT / 64;     // first scale group of this lane's key channels
+    // One round trip per chunk: the lanes of slot take token c0 + slot --
+    // its key row's D/4-channel parts and scales -- and each thread VW
+    // value words (page, channel) of the chunk; slots past the last
+    // readable token `lim`, and pages past its page, read that token or
+    // page instead, and are masked later.  The current token's slot is being
+    // written by this launch: its key, value bytes and scales come from LDS.
+    uint4 kr[KWT], vr[VW];
+    float ks[KGL], vsc[VGL];
+    auto load_chunk = [&](uint32_t c0, uint32_t lim) {
+        const uint32_t tl = min(c0 + slot, lim);
 #pragma unroll
-        for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, 16 * w));
+        for (int w = 0; w < KWT; ++w)
+            kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, part * CPT + 16 * w));
 #pragma unroll
         for (int w = 0; w < VW; ++w) {
-            const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
-            const uint32_t pg = pl * kKvPageTokens < n ? c0 / kKvPageTokens + pl : t0 / kKvPageTokens;
+            const uint32_t i = tid + NT * w, pl = i / D, ch = i % D;
+            const uint32_t pg = min(c0 / kKvPageTokens + pl, lim / kKvPageTokens);
             vr[w] = *reinterpret_cast<const uint4 *>(c.values + v_page_offset(c, pg, kvh, ch));
         }
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + g)];
-            vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + g)];
-        }
-    };
-    // grid z: the query token of a block (token_stride floats apart, its
-    // position position_ptr[z]); one split only
-    const float *query = a.query + static_cast<size_t>(blockIdx.z) * a.token_stride;
-    float *out = a.output + static_cast<size_t>(blockIdx.z) * a.token_stride;
-    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(a.position_ptr[blockIdx.z]) : a.position;
-    if (pos >= c.max_tokens) return;
-    const uint32_t tokens = pos + 1;
-    if (t0 >= tokens) {
-        // a split past the position (fixed grid): an empty partial
-        for (uint32_t i = tid; i < G * D; i += blockDim.x) {
-            const uint32_t g = i / D, d = i % D;
-            float *dst = a.partials + (static_cast<size_t>(h0 + g) * a.nsplit + split) * (D + 2);
-            dst[2 + d] = 0.0f;
-            if (d == 0) {
-                dst[0] = -INFINITY;
-                dst[1] = 0.0f;
-            }
-        }
-        return;
-    }
-    const uint32_t t1 = min(tokens, t0 + a.split);
-    const bool rope = a.key != nullptr;
-    const bool cur = rope && pos >= t0 && pos < t1;
-    constexpr uint32_t half = D / 2;
-    const size_t rope_off = a.rope_row_only ? 0 : static_cast<size_t>(pos) * half;
-    const float *ct = rope ? a.cos_tab + rope_off : nullptr;
-    const float *st = rope ? a.sin_tab + rope_off : nullptr;
-
-    // 0. decode mode with q/k norms: 1/rms of each query head and of the
-    //    current key head, one wave each
-    __shared__ float inv_s[GMAX + 1];
-    const bool qk = rope && a.q_norm != nullptr;
-    if (qk) {
-        for (uint32_t hh = wave; hh < G + (cur ? 1u : 0u); hh += 4) {
-            const float *x = hh < G ? query + static_cast<size_t>(h0 + hh) * D : a.key + static_cast<size_t>(kvh) * D;
-            float ss = 0.0f;
+        for (int g = 0; g < KGL; ++g) ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + kgrp + g)];
 #pragma unroll
-            for (uint32_t d = lane; d < static_cast<uint32_t>(D); d += 64) ss = fmaf(x[d], x[d], ss);
-            ss = wave_sum_all(ss);
-            if (lane == 0) inv_s[hh < G ? hh : GMAX] = 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps);
+        for (int g = 0; g < VGL; ++g)
+            vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + min(part * VGL + g, NG - 1u))];
+    };
+    const float *query = a.query + static_cast<size_t>(blockIdx.z) * a.token_stride + static_cast<size_t>(head) * D;
+    float *out = a.output + static_cast<size_t>(blockIdx.z) * a.token_stride + static_cast<size_t>(head) * D;
+    const bool rope = a.key != nullptr;
+    const bool qk = rope && a.q_norm != nullptr;
+    const bool row_only = rope && a.rope_row_only;
+
+    // 0. Every load the prologue needs, issued before anything waits (an
+    //    address is selected, never a load predicated: a load under a
+    //    per-lane condition makes the compiler drain the loads in flight
+    //    first): the first chunk (it does not depend on the position: its
+    //    tokens past the position are masked), the query element of thread
+    //    d < D with its RoPE partner, norm weights and cos/sin, and wave
+    //    gi < 2*NG's current key (gi < NG) or value 64-channel group.  Only
+    //    a RoPE table indexed by the position waits for the position.
+    load_chunk(0, c.max_tokens - 1);
+    const uint32_t qd = tid % D, qi = qd < half ? qd : qd - half;
+    const float qa = query[rope ? qi : qd], qb = query[qi + half];
+    float qwa = 0.0f, qwb = 0.0f, qcs = 0.0f, qsn = 0.0f;
+    const float *ct = a.cos_tab, *st = a.sin_tab;
+    if (row_only) {
+        qcs = ct[qi];
+        qsn = st[qi];
+    }
+    if (qk) {
+        qwa = a.q_norm[qi];
+        qwb = a.q_norm[qi + half];
+    }
+    const uint32_t gi = min(wave, 2u * NG - 1u);
+    const bool cv = gi >= NG;
+    const uint32_t cd = (cv ? gi - NG : gi) * 64 + lane, ci = cd < half ? cd : cd - half;
+    float ca = 0.0f, cb = 0.0f, cwa = 0.0f, cwb = 0.0f, ccs = 0.0f, csn = 0.0f;
+    if (rope) {
+        const float *kh = a.key + static_cast<size_t>(kvh) * D;
+        ca = *(cv ? a.value + static_cast<size_t>(kvh) * D + cd : kh + ci);
+        cb = kh[ci + half];
+        if (row_only) {
+            ccs = ct[ci];
+            csn = st[ci];
         }
+        if (qk) {
+            cwa = a.k_norm[ci];
+            cwb = a.k_norm[ci + half];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(a.position_ptr[blockIdx.z]) : a.position;
+    if (rope && !row_only) {
+        // a full RoPE table: the position's row
+        ct += static_cast<size_t>(pos) * half;
+        st += static_cast<size_t>(pos) * half;
+        qcs = ct[qi];
+        qsn = st[qi];
+        ccs = ct[ci];
+        csn = st[ci];
+    }
+    if (pos >= c.max_tokens) return;
+    const uint32_t t1 = min(pos + 1, a.span);
+    const bool cur = rope && pos < t1;
+
+    // 1. q/k norms: 1/rms of the query head and of the current key head
+    //    from wave sums of squares (waves < D/64 hold the query, waves
+    //    < NG the key groups)
+    float qinv = 1.0f, kinv = 1.0f;
+    if (qk) {
+        const float qown = qd < half ? qa : qb;
+        const float qs2 = wave_sum_all(qown * qown);
+        const float kown = cd < half ? ca : cb;
+        const float ks2 = wave_sum_all(kown * kown);
+        if (lane == 0 && wave < static_cast<uint32_t>(D / 64)) nrm_s[wave] = qs2;
+        if (lane == 0 && wave < static_cast<uint32_t>(NG)) nrm_s[4 + wave] = ks2;
         __syncthreads();
+        float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+        for (int w = 0; w < D / 64; ++w) sq += nrm_s[w];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) sk += nrm_s[4 + g];
+        qinv = 1.0f / sqrtf(sq / static_cast<float>(D) + a.eps);
+        kinv = 1.0f / sqrtf(sk / static_cast<float>(D) + a.eps);
     }
 
-    // 1. query heads of this KV head (rotated in decode mode) -> LDS
-    for (uint32_t i = tid; i < GMAX * D; i += blockDim.x) {
-        const uint32_t g = i / D, d = i % D;
-        float v = 0.0f;
-        if (g < G) {
-            const float *qh = query + static_cast<size_t>(h0 + g) * D;
-            v = qk ? rope_norm_at(qh, d, half, ct, st, inv_s[g], a.q_norm)
-                   : rope ? rope_at(qh, d, half, ct, st) : qh[d];
-        }
-        q_s[i] = v;
-    }
-    // the current token's key (rotated) and value: one wave per 64-channel group
-    if (cur) {
-        for (uint32_t gi = wave; gi < 2 * NG; gi += 4) {
-            const bool is_v = gi >= NG;
-            const uint32_t grp = is_v ? gi - NG : gi;
-            const uint32_t d = grp * 64 + lane;
-            const float *src = (is_v ? a.value : a.key) + static_cast<size_t>(kvh) * D;
-            const float x = is_v ? src[d]
-                                 : qk ? rope_norm_at(src, d, half, ct, st, inv_s[GMAX], a.k_norm)
-                                      : rope_at(src, d, half, ct, st);
-            const float amax = wave_max_all(isfinite(x) ? fabsf(x) : 0.0f);
-            const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-            const int8_t qv = q8_of(x, scale);
-            (is_v ? vcur : kcur)[d] = qv;
-            if (writer) store_q8(c, is_v, pos, kvh, d, qv);
-            if (lane == 0) {
-                (is_v ? vcur_s : kcur_s)[grp] = scale;
-                if (writer) (is_v ? c.value_scales : c.key_scales)[scale_index(c, pos, kvh * NG + grp)] = scale;
+    // 2. the query head (normed and rotated in decode mode) -> LDS
+    if (tid < static_cast<uint32_t>(D)) {
+        float v = qa;
+        if (rope) {
+            float x0 = qa, x1 = qb;
+            if (qk) {
+                x0 = (x0 * qinv) * qwa;
+                x1 = (x1 * qinv) * qwb;
             }
+            v = qd < half ? fmaf(x0, qcs, -(x1 * qsn)) : fmaf(x0, qsn, x1 * qcs);
+        }
+        q_s[qd] = v;
+    }
+    // the current token's key (normed, rotated) and value: one wave per
+    // 64-channel group, Q8-quantized
+    if (cur && wave < 2u * NG) {
+        float x = ca;
+        if (!cv) {
+            float x0 = ca, x1 = cb;
+            if (qk) {
+                x0 = (x0 * kinv) * cwa;
+                x1 = (x1 * kinv) * cwb;
+            }
+            x = cd < half ? fmaf(x0, ccs, -(x1 * csn)) : fmaf(x0, csn, x1 * ccs);
+        }
+        const uint32_t grp = cv ? gi - NG : gi;
+        const float amax = wave_max_all(isfinite(x) ? fabsf(x) : 0.0f);
+        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        const int8_t qv = q8_of(x, scale);
+        (cv ? vcur : kcur)[cd] = qv;
+        if (writer) store_q8(c, cv, pos, kvh, cd, qv);
+        if (lane == 0) {
+            (cv ? vcur_s : kcur_s)[grp] = scale;
+            if (writer) (cv ? c.value_scales : c.key_scales)[scale_index(c, pos, kvh * NG + grp)] = scale;
         }
     }
     __syncthreads();
 
     const uint32_t vch = tid % D, ph = tid / D;   // P.V channel and phase
     const uint32_t vgrp = vch / 64;
-    float m_run[GMAX], l_run[GMAX], acc[GMAX];
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
-        m_run[g] = -INFINITY;
-        l_run[g] = 0.0f;
-        acc[g] = 0.0f;
-    }
-
-    for (uint32_t c0 = t0; c0 < t1; c0 += CH) {
+    float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < t1; c0 += CH) {
         const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
-        // 2. the chunk's loads
-        load_chunk(c0, n);
-        const bool has = tid < n;
-        const bool is_cur = cur && has && c0 + tid == pos;
+        // 3. the chunk's loads (the first chunk's were issued at the start)
+        if (c0 != 0) load_chunk(c0, t1 - 1);
+        const bool has = slot < n;
         if (cur) {
+            // the current token's key part, scales and value byte
+            const bool is_cur = has && c0 + slot == pos;
 #pragma unroll
-            for (int w = 0; w < KW; ++w) {
+            for (int w = 0; w < KWT; ++w) {
                 // component selects (a select of the uint4 struct goes through scratch)
-                const uint4 kc = reinterpret_cast<const uint4 *>(kcur)[w];
+                const uint4 kc = reinterpret_cast<const uint4 *>(kcur)[part * KWT + w];
                 kr[w].x = is_cur ? kc.x : kr[w].x;
                 kr[w].y = is_cur ? kc.y : kr[w].y;
                 kr[w].z = is_cur ? kc.z : kr[w].z;
                 kr[w].w = is_cur ? kc.w : kr[w].w;
             }
-            // the current token's byte in the value words of its page
+#pragma unroll
+            for (int g = 0; g < KGL; ++g) ks[g] = is_cur ? kcur_s[kgrp + g] : ks[g];
+#pragma unroll
+            for (int g = 0; g < VGL; ++g) vsc[g] = is_cur ? vcur_s[min(part * VGL + g, NG - 1u)] : vsc[g];
             const uint32_t cur_page = pos / kKvPageTokens - c0 / kKvPageTokens;
             const uint32_t cw = (pos % kKvPageTokens) / 4, shift = 8 * (pos % 4);
 #pragma unroll
             for (int w = 0; w < VW; ++w) {
-                const uint32_t i = tid + 256 * w, pl = i / D, ch = i % D;
-                const bool hit = pl == cur_page;
+                const uint32_t i = tid + NT * w, pl = i / D, ch = i % D;
+                const bool hit = pos >= c0 && pl == cur_page;
                 const uint32_t b = static_cast<uint32_t>(static_cast<uint8_t>(vcur[ch])) << shift;
                 const uint32_t keep = ~(0xffu << shift);
                 vr[w].x = hit && cw == 0 ? (vr[w].x & keep) | b : vr[w].x;
@@ -684,75 +712,63 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
                 vr[w].z = hit && cw == 2 ? (vr[w].z & keep) | b : vr[w].z;
                 vr[w].w = hit && cw == 3 ? (vr[w].w & keep) | b : vr[w].w;
             }
-#pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                ks[g] = is_cur ? kcur_s[g] : ks[g];
-                vsc[g] = is_cur ? vcur_s[g] : vsc[g];
-            }
         }
-        // the value words and the token's scales -> LDS for the P.V phase
+        // the value words and the tokens' scales -> LDS for the P.V phase
 #pragma unroll
-        for (int w = 0; w < VW; ++w) v_s[tid + 256 * w] = vr[w];
+        for (int w = 0; w < VW; ++w) v_s[tid + NT * w] = vr[w];
 #pragma unroll
-        for (int g = 0; g < NG; ++g) vsc_s[tid % CH * NG + g] = has ? vsc[g] : 0.0f;
-        // 3. scores of this thread's token
-        float sc[GMAX];
+        for (int g = 0; g < VGL; ++g)
+            if (part * VGL + g < static_cast<uint32_t>(NG)) vsc_s[slot * NG + part * VGL + g] = has ? vsc[g] : 0.0f;
+        // 4. the score of this lane's token: its channels, scaled by their
+        //    group's key scale, summed over the token's four lanes
+        float sc = 0.0f;
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) sc[g] = 0.0f;
+        for (int g = 0; g < KGL; ++g) {
+            float pg = 0.0f;
 #pragma unroll
-        for (int grp = 0; grp < NG; ++grp) {
-            float part[GMAX];
-#pragma unroll
-            for (int g = 0; g < GMAX; ++g) part[g] = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint4 kw = kr[grp * 4 + w];
+            for (int w = g * WPG; w < (g + 1) * WPG; ++w) {
+                const uint4 kw = kr[w];
                 const uint32_t k4[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float k0 = i8f(k4[e], 0), k1 = i8f(k4[e], 1), k2 = i8f(k4[e], 2), k3 = i8f(k4[e], 3);
-                    const uint32_t d0 = grp * 64 + w * 16 + e * 4;
-#pragma unroll
-                    for (int g = 0; g < GMAX; ++g) {
-                        if (static_cast<uint32_t>(g) >= G) break;
-                        const float4 qq = *reinterpret_cast<const float4 *>(q_s + g * D + d0);
-                        part[g] = fmaf(qq.x, k0, part[g]);
-                        part[g] = fmaf(qq.y, k1, part[g]);
-                        part[g] = fmaf(qq.z, k2, part[g]);
-                        part[g] = fmaf(qq.w, k3, part[g]);
-                    }
+                    const uint32_t d0 = part * CPT + w * 16 + e * 4;
+                    const float4 qq = *reinterpret_cast<const float4 *>(q_s + d0);
+                    pg = fmaf(qq.x, i8f(k4[e], 0), pg);
+                    pg = fmaf(qq.y, i8f(k4[e], 1), pg);
+                    pg = fmaf(qq.z, i8f(k4[e], 2), pg);
+                    pg = fmaf(qq.w, i8f(k4[e], 3), pg);
                 }
             }
-#pragma unroll
-            for (int g = 0; g < GMAX; ++g) sc[g] = fmaf(part[g], ks[grp], sc[g]);
+            sc = fmaf(pg, ks[g], sc);
         }
-        // 4. chunk softmax, running max and sum
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            sc[g] = (has && static_cast<uint32_t>(g) < G) ? sc[g] * a.scale : -INFINITY;
-            const float m = wave_max_all(sc[g]);
-            if (lane == 0) red[0][wave][g] = m;
-        }
-        __syncthreads();
-        float alpha[GMAX];
-#pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            const float mc = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
-            const float mn = fmaxf(m_run[g], mc);
-            alpha[g] = m_run[g] == -INFINITY ? 0.0f : expf(m_run[g] - mn);
-            m_run[g] = mn;
-            const float p = (has && static_cast<uint32_t>(g) < G) ? expf(sc[g] - mn) : 0.0f;
-            if (tid < CH) s_s[g * CH + tid] = p;
-            const float ps = wave_sum_all(p);
-            if (lane == 0) red[1][wave][g] = ps;
+        for (int off = 1; off < TPT; off <<= 1) sc += __shfl_xor(sc, off);
+        // 5. chunk softmax, running max and sum
+        sc = has ? sc * a.scale : -INFINITY;
+        {
+            const float m = wave_max_all(sc);
+            if (lane == 0) red[0][wave] = m;
         }
         __syncthreads();
+        float mc = red[0][0];
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            l_run[g] = l_run[g] * alpha[g] + ((red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]));
-            acc[g] *= alpha[g];
+        for (int w = 1; w < NW; ++w) mc = fmaxf(mc, red[0][w]);
+        const float mn = fmaxf(m_run, mc);
+        const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - mn);
+        m_run = mn;
+        const float p = has ? expf(sc - mn) : 0.0f;
+        if (part == 0) s_s[slot] = p;
+        {
+            const float ps = wave_sum_all(part == 0 ? p : 0.0f);
+            if (lane == 0) red[1][wave] = ps;
         }
-        // 5. P.V of this thread's channel over its 4-token groups (from LDS)
+        __syncthreads();
+        float lc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) lc += red[1][w];
+        l_run = l_run * alpha + lc;
+        acc *= alpha;
+        // 6. P.V of this thread's channel over its 4-token groups (from LDS)
         const uint32_t *v_u32 = reinterpret_cast<const uint32_t *>(v_s);
         for (uint32_t tl = 4 * ph; tl < n; tl += 4 * PH) {
             const uint32_t vw = v_u32[((tl / kKvPageTokens) * D + vch) * 4 + (tl % kKvPageTokens) / 4];
@@ -760,40 +776,23 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(DecodeAttnArgs a)
             const float v1 = i8f(vw, 1) * vsc_s[(tl + 1) * NG + vgrp];
             const float v2 = i8f(vw, 2) * vsc_s[(tl + 2) * NG + vgrp];
             const float v3 = i8f(vw, 3) * vsc_s[(tl + 3) * NG + vgrp];
-#pragma unroll
-            for (int g = 0; g < GMAX; ++g) {
-                if (static_cast<uint32_t>(g) >= G) break;
-                const float4 p = *reinterpret_cast<const float4 *>(s_s + g * CH + tl);
-                acc[g] = fmaf(p.x, v0, acc[g]);
-                acc[g] = fmaf(p.y, v1, acc[g]);
-                acc[g] = fmaf(p.z, v2, acc[g]);
-                acc[g] = fmaf(p.w, v3, acc[g]);
-            }
+            const float4 pp = *reinterpret_cast<const float4 *>(s_s + tl);
+            acc = fmaf(pp.x, v0, acc);
+            acc = fmaf(pp.y, v1, acc);
+            acc = fmaf(pp.z, v2, acc);
+            acc = fmaf(pp.w, v3, acc);
         }
         __syncthreads();
     }
 
-    // 6. sum the token phases; output or partial
-#pragma unroll
-    for (int g = 0; g < GMAX; ++g)
-        if (static_cast<uint32_t>(g) < G) pv_s[(ph * GMAX + g) * D + vch] = acc[g];
+    // 7. sum the token phases; the output
+    pv_s[ph * D + vch] = acc;
     __syncthreads();
-    for (uint32_t i = tid; i < G * D; i += blockDim.x) {
-        const uint32_t g = i / D, d = i % D;
+    if (tid < static_cast<uint32_t>(D)) {
         float o = 0.0f;
 #pragma unroll
-        for (int p = 0; p < PH; ++p) o += pv_s[(p * GMAX + g) * D + d];
-        const uint32_t head = h0 + g;
-        if (a.nsplit == 1) {
-            out[static_cast<size_t>(head) * D + d] = o / l_run[g];
-        } else {
-            float *dst = a.partials + (static_cast<size_t>(head) * a.nsplit + split) * (D + 2);
-            dst[2 + d] = o;
-            if (d == 0) {
-                dst[0] = m_run[g];
-                dst[1] = l_run[g];
-            }
-        }
+        for (int p = 0; p < PH; ++p) o += pv_s[p * D + tid];
+        out[tid] = o / l_run;
     }
 }
 
@@ -1292,34 +1291,18 @@ hipError_t launch_mfma_attention_rt(const MfmaAttnArgs &args, uint32_t waves, hi
                            : launch_mfma_attention_nw<D, 2>(args, waves, stream);
 }
 
-template <int D, int GMAX>
-hipError_t launch_decode_kernel(const DecodeAttnArgs &args, hipStream_t stream) {
-    const uint32_t wgs_per_kv = args.group / args.heads_per_wg;
-    hipLaunchKernelGGL((decode_attention_kernel<D, GMAX>),
-                       dim3(args.nsplit, args.c.kv_heads * wgs_per_kv, std::max(args.count, 1u)), dim3(256), 0,
-                       stream, args);
-    return hipGetLastError();
-}
+// Two lanes per token (512 threads): measured on MI355X at 12 query / 2 KV
+// heads, position 100, graph of back-to-back launches: 5.5 us per launch
+// against 6.2 with four lanes (16 waves: the softmax's wave reductions and
+// barriers cost more than the shorter scores save) and 6.1 with one (the
+// per-token chains get longer)
+constexpr int kDecodeTpt = 2;
 
-// One query head per workgroup (the split attention of longer contexts is
-// the MFMA kernel).
 template <int D>
-hipError_t launch_decode_g(const DecodeAttnArgs &args, hipStream_t stream) {
-    if (args.heads_per_wg != 1) return hipErrorInvalidValue;
-    return launch_decode_kernel<D, 1>(args, stream);
-}
-
-hipError_t launch_decode_attention_args(const DecodeAttnArgs &args, float *output, hipStream_t stream) {
-    hipError_t e;
-    switch (args.c.head_dim) {
-    case 64: e = launch_decode_g<64>(args, stream); break;
-    case 128: e = launch_decode_g<128>(args, stream); break;
-    case 256: e = launch_decode_g<256>(args, stream); break;
-    default: return hipErrorInvalidValue;
-    }
-    if (e != hipSuccess || args.nsplit == 1) return e;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(args.c.kv_heads * args.group), dim3(256), 0, stream, args.partials,
-                       output, args.nsplit, args.c.head_dim);
+hipError_t launch_decode_kernel(const DecodeAttnArgs &args, hipStream_t stream) {
+    hipLaunchKernelGGL((decode_attention_kernel<D, kDecodeTpt>),
+                       dim3(1, args.c.kv_heads * args.group, std::max(args.count, 1u)), dim3(256 * kDecodeTpt), 0,
+                       stream, args);
     return hipGetLastError();
 }
 
@@ -1454,19 +1437,17 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
                                                                     !l.sin_tab)) ||
         l.count == 0 || (l.count > 1 && (l.key || !l.position_ptr)))
         return hipErrorInvalidValue;
+    // the whole context in one split (K/V rows are re-read per query head
+    // from L2: the latency case); longer contexts take the RoPE/append
+    // kernel and the MFMA attention
+    if (l.span_tokens == 0 || decode_split_tokens(c, l.span_tokens) < l.span_tokens) return hipErrorInvalidValue;
+    if ((!l.q_norm) != (!l.k_norm) || (l.q_norm && !l.key)) return hipErrorInvalidValue;
     DecodeAttnArgs args{};
     args.c = c;
     args.query = l.query;
     args.output = l.output;
-    args.partials = l.partials;
     args.group = l.query_heads / c.kv_heads;
-    args.split = decode_split_tokens(c, l.span_tokens);
-    args.nsplit = (l.span_tokens + args.split - 1) / args.split;
-    // one query head per workgroup, the whole context in one split (K/V are
-    // re-read per head from L2: the latency case); longer contexts take the
-    // RoPE/append kernel and the MFMA attention
-    if (args.nsplit != 1) return hipErrorInvalidValue;
-    args.heads_per_wg = 1;
+    args.span = l.span_tokens;
     args.scale = l.scale;
     args.position = l.position;
     args.position_ptr = l.position_ptr;
@@ -1477,11 +1458,14 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.rope_row_only = l.rope_row_only ? 1u : 0u;
     args.count = l.count;
     args.token_stride = l.query_heads * c.head_dim;
-    if ((!l.q_norm) != (!l.k_norm) || (l.q_norm && !l.key)) return hipErrorInvalidValue;
     args.q_norm = l.q_norm;
     args.k_norm = l.k_norm;
     args.eps = l.eps;
-    return launch_decode_attention_args(args, l.output, stream);
+    switch (c.head_dim) {
+    case 64: return launch_decode_kernel<64>(args, stream);
+    case 128: return launch_decode_kernel<128>(args, stream);
+    default: return launch_decode_kernel<256>(args, stream);
+    }
 }
 
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
