@@ -1076,8 +1076,9 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
                                               uint32_t ppieces, uint32_t mpieces, float (&acc)[RT][4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
     const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.nblk) * 512);
-    uint32_t A[NB][RT];
-    uint2 Mt[NB][RT];
+    // the four fp16 block scales of a unit as two plain words (a select of
+    // a uint2's fields by the block's position went through scratch memory)
+    uint32_t A[NB][RT], Ml[NB][RT], Mh[NB][RT];
     uint2 B[NB];
     int4 SA[NB];
 #pragma unroll
@@ -1092,20 +1093,19 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
                 const uint32_t ma = 16 * lds_swizzle(static_cast<uint32_t>(u.meta) >> 4, mpieces) +
                                     (static_cast<uint32_t>(u.meta) & 8u);
                 A[i][t] = *reinterpret_cast<const uint32_t *>(lds + pa + 4 * g);
-                Mt[i][t] = *reinterpret_cast<const uint2 *>(lds + meta_lds + ma);
+                const uint2 mt = *reinterpret_cast<const uint2 *>(lds + meta_lds + ma);
+                Ml[i][t] = mt.x;
+                Mh[i][t] = mt.y;
             } else {
                 A[i][t] = *reinterpret_cast<const uint32_t *>(payload + u.payload + 4 * g);
-                Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
+                const uint2 mt = *reinterpret_cast<const uint2 *>(meta + u.meta);
+                Ml[i][t] = mt.x;
+                Mh[i][t] = mt.y;
             }
         }
         B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
         SA[i] = *reinterpret_cast<const int4 *>(sums + b * 16 + 4 * g);
     }
-#pragma unroll
-    for (int i = 0; i < NB; ++i)
-#pragma unroll
-        for (int t = 0; t < RT; ++t)
-            if (r0 + 16 * t + m >= rows) Mt[i][t] = make_uint2(0, 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1129,8 +1129,10 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
                         a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r] - corr[r];
                 }
             }
-            const uint32_t word = q < 2 ? Mt[i][t].x : Mt[i][t].y;
-            const float d = half_to_float((word >> (16 * (q & 1))) & 0xffffu);
+            // rows past the tensor contribute nothing (scale 0)
+            const uint64_t w64 = (static_cast<uint64_t>(Mh[i][t]) << 32) | Ml[i][t];
+            const uint32_t h = r0 + 16 * t + m < rows ? static_cast<uint32_t>(w64 >> (16 * q)) & 0xffffu : 0u;
+            const float d = half_to_float(h);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(static_cast<float>(ci[r] - corr[r]), d, acc[t][r]);
         }
