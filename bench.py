@@ -359,7 +359,8 @@ def attention_bench(torch, ctx, steps=50):
 class MfmaSweep:
     """Resident HyperVSQ-2 or Q4_0 tensors of `layers` layers with MFMA
     images of M tokens (8..16): int8-MFMA GEMM launches grouped as the
-    decoder groups its GEMVs (q/k/v, o, gate/up, down: four per layer)."""
+    decoder groups its GEMVs (q/k/v, o, gate/up, down: four per layer; o and
+    down accumulate into their outputs, the residual adds)."""
 
     def __init__(self, torch, ctx, shapes, layers, seed, batch, kind="hvsq2"):
         import numpy as np
@@ -387,15 +388,16 @@ class MfmaSweep:
                 img = torch.zeros(ctx.mfma_image_bytes(h0), dtype=torch.uint8, device=dev)
                 ctx.mfma_image_device(h0, q8.data_ptr(), batch, q8.shape[1], img.data_ptr(), stream=s)
                 outs = [torch.zeros(batch, shapes[p][0], device=dev) for p in projs]
-                self.items.append(([layer[p] for p in projs], img, sc, outs))
+                # o and down add into the residual stream, as the decoder runs them
+                self.items.append(([layer[p] for p in projs], img, sc, outs, key in ("o", "down")))
                 self.weight_bytes += sum(synth.weight_bytes(kind, *shapes[p]) for p in projs)
         torch.cuda.synchronize()
         self.flops = 2 * batch * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * layers
 
     def run(self, stream):
-        for hs, img, sc, outs in self.items:
+        for hs, img, sc, outs, acc in self.items:
             self.ctx.gemm_mfma_group_device(hs, img.data_ptr(), sc.data_ptr(), [o.data_ptr() for o in outs],
-                                            self.batch, stream=stream)
+                                            self.batch, stream=stream, accumulate=acc)
 
     def close(self):
         for h in self.handles:
@@ -441,7 +443,7 @@ def batch_sweep(torch, ctx, steps, warmup):
     """GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers (weights
     read once per launch): HyperVSQ-2 on the Qwen3-4B shapes (36 layers per
     token in tokens_per_s), and under "q4_0" Q4_0 on the Qwen2-1.5B shapes
-    (28 layers); dot8 grouped launches below 3 tokens (Q4_0: 16), grouped
+    (28 layers); dot8 grouped launches below 3 tokens (Q4_0: 6), grouped
     int8-MFMA launches from there (MFMA utilisation = useful int8 ops /
     dense int8 peak)."""
     from qwanto_amd import synth
@@ -449,7 +451,7 @@ def batch_sweep(torch, ctx, steps, warmup):
     def sweep(kind, shapes, model_layers, seed0):
         res = {}
         for M in (1, 2, 4, 8, 16):
-            mfma = M >= (16 if kind == "q4_0" else 3)    # the library's own choice (mfma_batch)
+            mfma = M >= (6 if kind == "q4_0" else 3)     # the library's own choice (mfma_batch)
             if not mfma:
                 sw = Sweep(torch, ctx, kind, shapes, 4, seed=seed0 + M, batch=M)
                 ms = time_graph(torch, sw.grouped, steps, warmup)

@@ -151,8 +151,8 @@ __host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHv
 // E-element sub-blocks by adjacent lanes, as the prologue does.  With
 // `mimg`, token t's columns of the int8-MFMA image of up to 16 tokens are
 // written instead of q8 (one sub-block is one 8- or 16-byte slot of that
-// image; the block sums are reduced over the adjacent lanes holding the
-// block); tokens >= M of the image are left as they are (the GEMM neither
+// image; HyperVSQ-2's block sums are reduced over the adjacent lanes
+// holding the block); tokens >= M of the image are left as they are (the GEMM neither
 // mixes token columns nor stores those tokens).
 template <int KIND>
 __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
@@ -222,13 +222,8 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
         }
         if (img) put_sub_block<KIND>(img, units, sb, nsub, w);
         if (mimg) {
-            int s = 0;
-#pragma unroll
-            for (uint32_t i = 0; i < E; ++i) s += static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
             if constexpr (KIND == kQ4_0) {
                 // slot (block sb/4, group sb%4): elements {0,2,4,6} then {1,3,5,7}
-                s += __shfl_xor(s, 1);
-                s += __shfl_xor(s, 2);
                 const uint32_t nblk = (K + 31) / 32;
                 if (sb < nblk * 4) {
                     const uint32_t lo = (w[0] & 0xffu) | ((w[0] >> 8) & 0xff00u) | ((w[1] & 0xffu) << 16) |
@@ -236,13 +231,14 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
                     const uint32_t hi = ((w[0] >> 8) & 0xffu) | ((w[0] >> 16) & 0xff00u) |
                                         ((w[1] << 8) & 0xff0000u) | (w[1] & 0xff000000u);
                     *reinterpret_cast<uint2 *>(mimg + (static_cast<size_t>(sb) * 16 + t) * 8) = make_uint2(lo, hi);
-                    if ((sb & 3u) == 0)
-                        reinterpret_cast<int32_t *>(mimg + static_cast<size_t>(nblk) * 512)[(sb >> 2) * 16 + t] = s;
                 }
             } else {
                 // elements 16 sb .. 16 sb + 15 are slice sl = sb % 4 of group
                 // g = (sb / 4) % 4 of block sb / 16, image slot
                 // (block * 16 + sl * 4 + g); word k = byte k of w[0..3]
+                int s = 0;
+#pragma unroll
+                for (uint32_t i = 0; i < E; ++i) s += static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
                 s += __shfl_xor(s, 1);
                 s += __shfl_xor(s, 2);
                 s += __shfl_xor(s, 4);
@@ -862,13 +858,14 @@ __global__ __launch_bounds__(256) void mfma_image_kernel(const int8_t *__restric
     }
 }
 
-// Q4_0: one v_mfma_i32_16x16x32_i8 per 32-weight block.  A lane's A operand
-// is the 4 nibble bytes of weights 8g..8g+7 of its row (g = lane / 16) as
-// two words, low nibbles then high nibbles (the unsigned codes 0..15; the -8
-// is applied to the sum: sum (n-8)*a = sum n*a - 8*sum a), so each 8-byte
-// group of the image holds elements 8g + {0,2,4,6,1,3,5,7} of the block:
-//   image [block][g][token 0..15][8 B], then int32 sums [block][token 0..15].
-__host__ __device__ constexpr size_t mfma_q4_image_block_bytes() { return 4 * 16 * 8 + 16 * 4; }
+// Q4_0: one v_mfma_i32_16x16x32_i8 per 32-weight block.  A lane's weight
+// operand is the 4 nibble bytes of weights 8g..8g+7 of its row (g = lane /
+// 16) as two words, low nibbles then high nibbles (turned into the signed
+// weights n - 8), so each 8-byte group of the image holds elements
+// 8g + {0,2,4,6,1,3,5,7} of the block:
+//   image [block][g][token 0..15][8 B]  (no activation sums: the signed
+//   weights need no correction).
+__host__ __device__ constexpr size_t mfma_q4_image_block_bytes() { return 4 * 16 * 8; }
 
 __global__ __launch_bounds__(256) void mfma_q4_image_kernel(const int8_t *__restrict__ q8, uint32_t q8_stride,
                                                             uint32_t K, uint32_t M, uint32_t nblk, uint8_t *img) {
@@ -887,16 +884,6 @@ __global__ __launch_bounds__(256) void mfma_q4_image_kernel(const int8_t *__rest
             }
         }
         *reinterpret_cast<uint2 *>(img + static_cast<size_t>(idx) * 8) = make_uint2(w[0], w[1]);
-    }
-    if (idx < nblk * 16) {
-        const uint32_t b = idx / 16, m = idx % 16;
-        int sum = 0;
-        if (m < M) {
-            const int8_t *src = q8 + static_cast<size_t>(m) * q8_stride;
-            for (uint32_t i = 0; i < 32; ++i)
-                if (b * 32 + i < K) sum += src[b * 32 + i];
-        }
-        reinterpret_cast<int32_t *>(img + static_cast<size_t>(nblk) * 512)[idx] = sum;
     }
 }
 
@@ -931,7 +918,7 @@ struct MfmaArgs {
     const float *bias[kMaxGroup];  // per job: null, or [rows] added to each token's product
 };
 
-constexpr int kMfmaMaxWaves = 8;
+constexpr int kMfmaMaxWaves = 16;
 
 // Byte offsets of (row, unit, chunk g) in the wave-tile layout, relative to
 // the first tile `t0`:
@@ -1062,25 +1049,45 @@ __device__ __forceinline__ uint32_t lds_swizzle(uint32_t piece, uint32_t npieces
     return (piece | 15u) < npieces ? piece ^ ((piece >> 4) & 15u) : piece;
 }
 
+// Q4_0 codes n of four bytes, low or high nibbles, as the signed int8
+// weights n - 8: per byte (0x80 | n) - 8 stays within the byte (no borrow),
+// and flipping its top bit gives n - 8 in two's complement.
+__device__ __forceinline__ uint32_t q4_signed(uint32_t nibbles) {
+    return ((nibbles | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+}
+
+// The image words of up to NB Q4_0 blocks from b0 (each lane's 8 bytes of
+// a block: tokens m, elements 8g .. 8g+7); blocks past kb1 are not loaded.
+template <int NB>
+__device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, uint32_t b0, uint32_t kb1, uint32_t lane,
+                                               uint2 (&B)[NB]) {
+    if (b0 >= kb1) return;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + i < kb1 ? b0 + i : b0;
+        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+    }
+}
+
 // One chunk of up to NB Q4_0 blocks (32 weights each; unit u = b / 4 holds
 // blocks 4u .. 4u+3 as its four 16-byte payload chunks and their fp16
-// scales as its meta).  As mfma_chunk: every load of the chunk issued before
-// the first MFMA.  The tokens are the MFMA's A operand and the weight rows
-// its B operand, so lane (g, m) accumulates tokens 4g .. 4g+3 of weight row
-// m: the block scale it applies is the one it loaded itself, and the four
-// tokens' activation sums are one 16-byte load.
+// scales as its meta), one v_mfma_i32_16x16x32_i8 per block on the signed
+// weights n - 8 (so a block's product is its exact integer dot, no
+// correction).  The tokens are the MFMA's A operand and the weight rows its
+// B operand, so lane (g, m) accumulates tokens 4g .. 4g+3 of weight row m
+// and applies the block scale it loaded itself.  `B` holds the chunk's
+// image words, loaded by the caller ahead of time (STAGE: one chunk ahead,
+// so the next chunk's image loads are in flight while this one computes).
 template <int NB, int RT, bool STAGE, bool DUMP>
 __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
                                               const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
                                               uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
-                                              uint32_t ppieces, uint32_t mpieces, float (&acc)[RT][4]) {
+                                              uint32_t ppieces, uint32_t mpieces, const uint2 (&B)[NB],
+                                              float (&acc)[RT][4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
-    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.nblk) * 512);
     // the four fp16 block scales of a unit as two plain words (a select of
     // a uint2's fields by the block's position went through scratch memory)
     uint32_t A[NB][RT], Ml[NB][RT], Mh[NB][RT];
-    uint2 B[NB];
-    int4 SA[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
@@ -1103,19 +1110,16 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
                 Mh[i][t] = mt.y;
             }
         }
-        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
-        SA[i] = *reinterpret_cast<const int4 *>(sums + b * 16 + 4 * g);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (static_cast<uint32_t>(i) >= nblk) break;
         const uint32_t q = (b0 + i) & 3;
-        const int corr[4] = {8 * SA[i].x, 8 * SA[i].y, 8 * SA[i].z, 8 * SA[i].w};
         const long xv = static_cast<long>((static_cast<uint64_t>(B[i].y) << 32) | B[i].x);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            const uint32_t lo = A[i][t] & 0x0f0f0f0fu, hi = (A[i][t] >> 4) & 0x0f0f0f0fu;
+            const uint32_t lo = q4_signed(A[i][t] & 0x0f0f0f0fu), hi = q4_signed((A[i][t] >> 4) & 0x0f0f0f0fu);
             const long wv = static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
             mfma_v4i ci = {0, 0, 0, 0};
             // C[token][row]: element r is token 4g + r of row m
@@ -1126,7 +1130,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = r0 + 16 * t + m, tok = 4 * g + r;
                     if (row < rows && tok < a.ntok)
-                        a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r] - corr[r];
+                        a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
                 }
             }
             // rows past the tensor contribute nothing (scale 0)
@@ -1134,7 +1138,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
             const uint32_t h = r0 + 16 * t + m < rows ? static_cast<uint32_t>(w64 >> (16 * q)) & 0xffffu : 0u;
             const float d = half_to_float(h);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(static_cast<float>(ci[r] - corr[r]), d, acc[t][r]);
+            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(static_cast<float>(ci[r]), d, acc[t][r]);
         }
     }
 }
@@ -1200,13 +1204,36 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
-    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
-        if constexpr (KIND == kHvsq2)
+    if constexpr (KIND == kHvsq2) {
+        for (uint32_t b0 = kb0; b0 < kb1; b0 += NB)
             mfma_chunk<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
-                                      min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
-        else
+                                            min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
+    } else if constexpr (STAGE) {
+        // the weights are in LDS: each chunk's image words are loaded one
+        // chunk ahead (two register sets used in turn), so a chunk's
+        // products run while the next chunk's image is on its way
+        uint2 Bx[NB], By[NB];
+        q4_image_loads<NB>(a, kb0, kb1, lane, Bx);
+        for (uint32_t b0 = kb0; b0 < kb1; b0 += 2 * NB) {
+            const uint32_t b1 = b0 + NB;
+            q4_image_loads<NB>(a, b1, kb1, lane, By);
             mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
-                                         min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces, acc);
+                                               min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
+                                               Bx, acc);
+            if (b1 >= kb1) break;
+            q4_image_loads<NB>(a, b1 + NB, kb1, lane, Bx);
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b1,
+                                               min(static_cast<uint32_t>(NB), kb1 - b1), lane, ppieces, mpieces,
+                                               By, acc);
+        }
+    } else {
+        uint2 Bx[NB];
+        for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
+            q4_image_loads<NB>(a, b0, kb1, lane, Bx);
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+                                               min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
+                                               Bx, acc);
+        }
     }
 
     // the K-split partials, summed in wave order (LDS after the staged tiles)
@@ -1286,6 +1313,155 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                         dst[r] = a.accumulate ? add_rounded(dst[r], v) : v;
                     }
             }
+        }
+    }
+}
+
+// Q4_0 launches of few row groups in accumulate mode (the residual adds of
+// the o and down projections: 96-160 row groups leave most of the 256 CUs
+// idle, and a CU's vector ALU bounds the per-block work): each row group is
+// split four ways along K by a block's position in its unit (split s takes
+// blocks 4u + s, i.e. chunk s of every unit, which in the wave-tile layout
+// is one contiguous span per tile and slot), so a split stages a quarter of
+// the row group's payload (and its whole meta), its waves divide the units,
+// and the four partial products are added to the output with float atomics
+// (their order is not fixed: the last bits of the residual can differ from
+// run to run).
+struct Q4Split {
+    uint32_t qs, t0, tpieces, ppieces, mpieces, meta_lds;
+};
+
+template <int NB>
+__device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t *lds, const Q4Split &sp,
+                                               uint32_t rows, uint32_t r0, uint32_t v0, uint32_t nv, uint32_t lane,
+                                               float (&acc)[4]) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+    const uint32_t row = r0 + m;
+    const uint32_t rr = row < rows ? row : r0;
+    const uint32_t tile = (rr >> a.rows_per_wave_log2) - sp.t0, grp = rr & (R - 1);
+    uint32_t A[NB], Ml[NB], Mh[NB];
+    uint2 B[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t v = v0 + (static_cast<uint32_t>(i) < nv ? i : 0);
+        const uint32_t slot = v >> a.lanes_log2, jj = v & (L - 1);
+        const uint32_t n = min(L, a.units - slot * L);
+        const uint32_t piece = tile * sp.tpieces + R * L * slot + grp * n + jj;
+        A[i] = *reinterpret_cast<const uint32_t *>(lds + 16 * lds_swizzle(piece, sp.ppieces) + 4 * g);
+        const uint32_t mo = static_cast<uint32_t>(tile * a.tile_meta_bytes) + 8 * R * L * slot + (grp * n + jj) * 8;
+        const uint2 mt =
+            *reinterpret_cast<const uint2 *>(lds + sp.meta_lds + 16 * lds_swizzle(mo >> 4, sp.mpieces) + (mo & 8u));
+        Ml[i] = mt.x;
+        Mh[i] = mt.y;
+        const uint32_t b = min(4 * v + sp.qs, a.nblk - 1);
+        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const bool live = row < rows;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (static_cast<uint32_t>(i) >= nv) break;
+        const bool has = live && 4 * (v0 + i) + sp.qs < a.nblk;
+        const long xv = static_cast<long>((static_cast<uint64_t>(B[i].y) << 32) | B[i].x);
+        const uint32_t lo = q4_signed(A[i] & 0x0f0f0f0fu), hi = q4_signed((A[i] >> 4) & 0x0f0f0f0fu);
+        const long wv = static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+        mfma_v4i ci = {0, 0, 0, 0};
+        ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(xv, wv, ci, 0, 0, 0);
+        const uint64_t w64 = (static_cast<uint64_t>(Mh[i]) << 32) | Ml[i];
+        const uint32_t h = has ? static_cast<uint32_t>(w64 >> (16 * sp.qs)) & 0xffffu : 0u;
+        const float d = half_to_float(h);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), d, acc[r]);
+    }
+}
+
+template <int NB>
+__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_split_kernel(MfmaArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lane = threadIdx.x % kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+    const uint32_t KS = 1u << a.ks_log2;
+    const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
+    uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
+    job = __builtin_amdgcn_readfirstlane(job);
+    const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
+    const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
+    float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
+    const uint32_t rows = job == 0 ? a.rows[0] : job == 1 ? a.rows[1] : job == 2 ? a.rows[2] : a.rows[3];
+    const uint32_t tiles = job == 0 ? a.tiles[0] : job == 1 ? a.tiles[1] : job == 2 ? a.tiles[2] : a.tiles[3];
+    const uint32_t stride = job == 0   ? a.output_stride[0]
+                            : job == 1 ? a.output_stride[1]
+                            : job == 2 ? a.output_stride[2]
+                                       : a.output_stride[3];
+    const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
+    const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
+    const uint32_t local = blockIdx.x - first;
+    const uint32_t R = 1u << a.rows_per_wave_log2, L = 1u << a.lanes_log2;
+    Q4Split sp;
+    sp.qs = local & 3u;
+    const uint32_t r0 = (local >> 2) * 16;
+    sp.t0 = r0 >> a.rows_per_wave_log2;
+    // the row group's tiles: chunk qs of each slot, then the whole meta
+    const uint32_t ntile = min(16u >> a.rows_per_wave_log2, tiles - sp.t0);
+    sp.tpieces = R * a.units;
+    sp.ppieces = ntile * sp.tpieces;
+    sp.meta_lds = (16u >> a.rows_per_wave_log2) * sp.tpieces * 16;
+    const uint32_t mbytes = ntile * static_cast<uint32_t>(a.tile_meta_bytes);
+    sp.mpieces = (mbytes + 15) / 16;
+    const uint8_t *msrc = meta + static_cast<size_t>(sp.t0) * a.tile_meta_bytes;
+    for (uint32_t c0 = wave * kWaveSize; c0 < sp.ppieces; c0 += blockDim.x)
+        if (c0 + lane < sp.ppieces) {
+            // LDS position p holds piece lds_swizzle(p): the source is permuted
+            const uint32_t pc = lds_swizzle(c0 + lane, sp.ppieces);
+            const uint32_t tile = pc / sp.tpieces, rem = pc - tile * sp.tpieces;
+            const uint32_t slot = rem / (R * L), r2 = rem - slot * R * L;
+            const uint32_t n = min(L, a.units - slot * L);
+            const size_t src = static_cast<size_t>(sp.t0 + tile) * a.tile_payload_bytes +
+                               static_cast<size_t>(64) * R * L * slot + 16 * (sp.qs * R * n + r2);
+            __builtin_amdgcn_global_load_lds(payload + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
+        }
+    for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
+        if (c0 + lane * 16 < mbytes) {
+            const uint32_t src = 16 * lds_swizzle((c0 >> 4) + lane, sp.mpieces);
+            __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + sp.meta_lds + c0), 16, 0, 0);
+        }
+    wait_vmcnt<0>();               // this wave's copies landed
+    __builtin_amdgcn_s_barrier();  // ... and every wave's
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t v0 = wave * a.nb, v1 = min(a.units, v0 + a.nb);
+    for (uint32_t v = v0; v < v1; v += NB)
+        mfma_chunk_q4s<NB>(a, smem, sp, rows, r0, v, min(static_cast<uint32_t>(NB), v1 - v), lane, acc);
+
+    // the waves' partials, summed in wave order (LDS after the staged tiles)
+    if (KS > 1) {
+        float *part_s = reinterpret_cast<float *>(smem + a.stage_bytes);
+        if (wave > 0) {
+            float *dst = part_s + ((wave - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r] = acc[r];
+        }
+        __syncthreads();
+        if (wave == 0)
+            for (uint32_t k = 1; k < KS; ++k) {
+                const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] += src[r];
+            }
+    }
+    // lane (g, m) holds tokens 4g .. 4g+3 of row m: the split's rounded
+    // partial product (and, split 0, the bias) added to the output
+    const uint32_t g = lane >> 4, m = lane & 15, row = r0 + m;
+    if (wave == 0 && row < rows) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = 4 * g + r;
+            if (tok >= a.ntok) continue;
+            float v = mul_rounded(acc[r], a.scales[tok]);
+            if (bias && sp.qs == 0) v = add_rounded(v, bias[row]);
+            unsafeAtomicAdd(output + static_cast<size_t>(tok) * stride + row, v);
         }
     }
 }
@@ -1806,8 +1982,9 @@ namespace {
 // a workgroup per 16-row group (one row tile per wave measured faster than
 // two or four sharing the image loads: more waves, shorter chains), its
 // waves splitting the K blocks -- the fewest that keep a wave's blocks
-// within the unrolled chunk of 5, then more (up to 8) while the launch has
-// fewer than 4096 waves and every wave keeps two blocks or more.  STAGE
+// within the unrolled chunk of 5, then more (up to 16) while the launch has
+// fewer than 4096 waves (Q4_0: 8192) and every wave keeps two blocks or
+// more.  STAGE
 // where the row group is a whole number of wave tiles and they fit in LDS
 // (kMfmaLdsLimit with the partial tiles).
 struct MfmaPlan {
@@ -1824,13 +2001,16 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     const uint32_t chunk = t.kind == kQ4_0 ? 8 : 5;
     const uint64_t groups = (total_rows + 16 * p.rt - 1) / (16 * p.rt);
     auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
+    // up to 16 K-split waves per workgroup: a launch of few row groups (the
+    // 1536- to 2560-row o/down/q/k/v projections) otherwise leaves most
+    // SIMDs with one wave or none, each walking a long K range
     if (t.kind == kQ4_0) {
         // as many K-split waves as keep the whole launch within one round of
         // resident waves (256 CUs x 32)
-        while (p.ks_log2 < 3 && (groups << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+        while (p.ks_log2 < 4 && (groups << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
     } else {
-        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > chunk) ++p.ks_log2;
-        while (p.ks_log2 < 3 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+        while (p.ks_log2 < 4 && per_wave(p.ks_log2) > chunk) ++p.ks_log2;
+        while (p.ks_log2 < 4 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
     }
     p.nb = per_wave(p.ks_log2);
     p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : (p.nb <= 5 || chunk == 5) ? 5 : 8;
@@ -1890,7 +2070,24 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             return hipErrorInvalidValue;
         total_rows += t.rows;
     }
-    const MfmaPlan p = mfma_plan(t0, total_rows);
+    MfmaPlan p = mfma_plan(t0, total_rows);
+    // Q4_0 residual adds over few row groups: the four-way K split
+    const uint64_t groups = (total_rows + 15) / 16;
+    const bool split = t0.kind == kQ4_0 && accumulate && !dump && p.stage && groups < 256;
+    if (split) {
+        const uint32_t units = t0.units;
+        auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
+        p.ks_log2 = 0;
+        while (p.ks_log2 < 4 && ((4 * groups) << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2)
+            ++p.ks_log2;
+        p.nb = per_wave(p.ks_log2);
+        p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : p.nb <= 5 ? 5 : 8;
+        p.waves = 1u << p.ks_log2;
+        const uint32_t tiles_grp = 16u / t0.rows_per_wave;
+        p.stage_bytes = tiles_grp * (t0.rows_per_wave * units * 16 + static_cast<uint32_t>(t0.tile_meta_bytes));
+        p.lds_bytes = p.stage_bytes + (p.waves - 1) * kWaveSize * 16;
+        if (p.lds_bytes > kMfmaLdsLimit) return hipErrorInvalidValue;
+    }
     MfmaArgs a{};
     uint32_t grid = 0;
     for (uint32_t i = 0; i < static_cast<uint32_t>(kMaxGroup); ++i) {
@@ -1907,7 +2104,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0 &&
                 (reinterpret_cast<uintptr_t>(a.bias[i]) & 15u) == 0)
                 a.vec_out |= 1u << i;
-            grid += (t.rows + 16 * p.rt - 1) / (16 * p.rt);
+            grid += split ? 4 * ((t.rows + 15) / 16) : (t.rows + 16 * p.rt - 1) / (16 * p.rt);
         }
     }
     a.job_block[kMaxGroup] = grid;
@@ -1925,6 +2122,16 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.ntok = batch;
     a.accumulate = accumulate ? 1u : 0u;
     a.dump = dump;
+    if (split) {
+        const uint32_t threads = p.waves * kWaveSize;
+        switch (p.nbt) {
+        case 2: hipLaunchKernelGGL(mfma_q4_split_kernel<2>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
+        case 3: hipLaunchKernelGGL(mfma_q4_split_kernel<3>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
+        case 5: hipLaunchKernelGGL(mfma_q4_split_kernel<5>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
+        default: hipLaunchKernelGGL(mfma_q4_split_kernel<8>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
+        }
+        return hipGetLastError();
+    }
     if (t0.kind == kQ4_0) {
         switch (p.nbt) {
         case 2: return launch_mfma_nb<kQ4_0, 2>(p, grid, a, stream);

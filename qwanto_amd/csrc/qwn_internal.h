@@ -206,6 +206,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate = false,
                                   int32_t *dump = nullptr, const float *const *biases = nullptr);
 constexpr uint32_t kMfmaMinTokens = 3;
+constexpr uint32_t kMfmaMinTokensQ4 = 6;
 // LDS per workgroup the MFMA GEMM plans its staging against: gfx950's
 // 160 KB (context creation refuses a device that reports less).
 constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
@@ -213,10 +214,11 @@ constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
 // HyperVSQ-2 from 3 tokens (measured on Qwen3-4B layers: the MFMA GEMM takes
 // about 25 us per layer whatever the token count up to 16, the dot8 GEMV
 // 17.9 us at 1 token, 22.8 at 2 and 33.4 at 4, which is how 3 tokens run);
-// Q4_0 (one 16x16x32 MFMA per 32-weight block, the same time at 8 tokens as
-// at 16, slower than the dot8 GEMV below 16) from a full 16-token tile.
+// Q4_0 (one 16x16x32 MFMA per 32-weight block) from 6 tokens (Qwen2-1.5B
+// layers: the MFMA GEMM about 31 us whatever the token count, the dot8
+// GEMV 24.7 us at 4 tokens and 39.0 at 8).
 inline bool mfma_batch(uint32_t kind, uint32_t batch) {
-    return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= 16);
+    return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= kMfmaMinTokensQ4);
 }
 
 // RMSNorm of `count` fp32 tokens ([count][x_stride]) into fp32 images of an

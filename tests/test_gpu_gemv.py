@@ -172,8 +172,14 @@ def test_q4_0_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
     run_mfma_group(gpu_ctx, oracle_lib, "q4_0", Ns, K, M, seed=sum(Ns) + K + M + 2)
 
 
-@pytest.mark.parametrize("Ns,K,M", [((1536,), 8960, 16), ((77, 1030), 1536, 9)])
+@pytest.mark.parametrize("Ns,K,M", [((1536,), 8960, 16), ((77, 1030), 1536, 9), ((1536,), 1536, 16),
+                                    ((2560,), 9728, 16), ((65, 130), 33, 12), ((3,), 31, 8),
+                                    ((1000, 40), 777, 5), ((300,), 16384, 10), ((4100,), 1536, 16)])
 def test_q4_0_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
+    """accumulate = 1 (the residual adds): launches of fewer than 256 row
+    groups take the four-way K split (each split's partial added with float
+    atomics), the rest the single-pass kernel; ragged rows, K not a multiple
+    of 32 or 128, partial token tiles."""
     run_mfma_group(gpu_ctx, oracle_lib, "q4_0", Ns, K, M, seed=sum(Ns) + K + M + 3, accumulate=True)
 
 

@@ -90,7 +90,7 @@ def read_caches(dec, layers, count):
     (QWEN2_LIKE, "hvsq2", 37, False, ""), (QWEN2_LIKE, "hvsq2", 5, False, ""), (LONG_CTX, "q4_0", 18, False, ""),
     (SMALL, "q4_0", 1, False, ""), (QWEN2_LIKE, "hvsq2", 20, True, ""), (LONG_CTX, "q4_0", 18, True, ""),
     (LONG_CTX, "q4_0", 24, True, ""),
-    # biases through the MFMA GEMM epilogue (16-token Q4_0 and 3+-token HyperVSQ-2 blocks) and the dot8 GEMV
+    # biases through the MFMA GEMM epilogue (6+-token Q4_0 and 3+-token HyperVSQ-2 blocks) and the dot8 GEMV
     (QWEN2_LIKE, "q4_0", 37, False, "qkv"), (QWEN2_LIKE, "hvsq2", 20, False, "qkvo"),
     (SMALL, "q4_0", 5, False, "qkvo")])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
