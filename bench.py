@@ -53,7 +53,8 @@ def parse():
     p.add_argument("--no-decode", action="store_true", help="skip the decode workload")
     p.add_argument("--decode-new", type=int, default=128, help="greedy tokens of the decode workload")
     p.add_argument("--decode-prompt", type=int, default=32, help="prompt tokens of the decode workload")
-    p.add_argument("--profile", choices=("gate-up", "decode", "decode-4b", "attention", "batch", "upload", "copy"),
+    p.add_argument("--profile", choices=("gate-up", "decode", "decode-4b", "drop-in", "attention", "batch", "upload",
+                                        "copy"),
                    help="profiling mode: run only one workload (for rocprofv3)")
     return p.parse_args()
 
@@ -572,6 +573,11 @@ def main():
     if args.profile == "decode":
         model, prompt = decode_model(prompt_len=args.decode_prompt)
         print(json.dumps({"profile_mode": "decode", **decode_bench(ctx, model, prompt, args.decode_new)}),
+              flush=True)
+        return
+    if args.profile == "drop-in":
+        model, prompt = decode_model(prompt_len=args.decode_prompt)
+        print(json.dumps({"profile_mode": "drop-in", **host_decode_bench(model, prompt, args.decode_new)}),
               flush=True)
         return
     if args.profile == "decode-4b":
