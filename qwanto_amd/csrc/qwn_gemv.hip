@@ -918,7 +918,8 @@ struct MfmaArgs {
     const float *bias[kMaxGroup];  // per job: null, or [rows] added to each token's product
 };
 
-constexpr int kMfmaMaxWaves = 16;
+constexpr int kMfmaMaxWaves = 8;
+constexpr int kMfmaSplitMaxWaves = 16;  // the Q4_0 K-split kernel
 
 // Byte offsets of (row, unit, chunk g) in the wave-tile layout, relative to
 // the first tile `t0`:
@@ -1377,7 +1378,7 @@ __device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t 
 }
 
 template <int NB>
-__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_split_kernel(MfmaArgs a) {
+__global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_kernel(MfmaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -1982,9 +1983,9 @@ namespace {
 // a workgroup per 16-row group (one row tile per wave measured faster than
 // two or four sharing the image loads: more waves, shorter chains), its
 // waves splitting the K blocks -- the fewest that keep a wave's blocks
-// within the unrolled chunk of 5, then more (up to 16) while the launch has
+// within the unrolled chunk of 5, then more (up to 8) while the launch has
 // fewer than 4096 waves (Q4_0: 8192) and every wave keeps two blocks or
-// more.  STAGE
+// more (the four-way K-split kernel of Q4_0 residual adds, up to 16).  STAGE
 // where the row group is a whole number of wave tiles and they fit in LDS
 // (kMfmaLdsLimit with the partial tiles).
 struct MfmaPlan {
@@ -2001,16 +2002,13 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     const uint32_t chunk = t.kind == kQ4_0 ? 8 : 5;
     const uint64_t groups = (total_rows + 16 * p.rt - 1) / (16 * p.rt);
     auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
-    // up to 16 K-split waves per workgroup: a launch of few row groups (the
-    // 1536- to 2560-row o/down/q/k/v projections) otherwise leaves most
-    // SIMDs with one wave or none, each walking a long K range
     if (t.kind == kQ4_0) {
         // as many K-split waves as keep the whole launch within one round of
         // resident waves (256 CUs x 32)
-        while (p.ks_log2 < 4 && (groups << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+        while (p.ks_log2 < 3 && (groups << (p.ks_log2 + 1)) <= 8192 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
     } else {
-        while (p.ks_log2 < 4 && per_wave(p.ks_log2) > chunk) ++p.ks_log2;
-        while (p.ks_log2 < 4 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
+        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > chunk) ++p.ks_log2;
+        while (p.ks_log2 < 3 && (groups << p.ks_log2) < 4096 && per_wave(p.ks_log2 + 1) >= 2) ++p.ks_log2;
     }
     p.nb = per_wave(p.ks_log2);
     p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : (p.nb <= 5 || chunk == 5) ? 5 : 8;
