@@ -1050,6 +1050,19 @@ __device__ __forceinline__ uint32_t lds_swizzle(uint32_t piece, uint32_t npieces
     return (piece | 15u) < npieces ? piece ^ ((piece >> 4) & 15u) : piece;
 }
 
+// Staged Q4_0 row groups are laid out row-major in LDS: payload
+// [16 rows][q4_pay_stride(units) 16-byte pieces] (piece b of a row = chunk
+// b % 4 of unit b / 4, i.e. 32-weight block b), then meta [16 rows]
+// [q4_meta_stride(units) dwords] (unit u's four fp16 scales at dwords 2u,
+// 2u + 1).  The odd piece stride (and odd pair stride of the meta) spreads
+// a wave's 16 rows over the LDS banks, and a block's address is a per-lane
+// base plus the block index, with no per-block layout arithmetic.
+__host__ __device__ constexpr uint32_t q4_pay_stride(uint32_t units) { return 4 * units + 1; }
+__host__ __device__ constexpr uint32_t q4_meta_stride(uint32_t units) { return 2 * (units | 1u); }
+__host__ __device__ constexpr uint32_t q4_stage_bytes(uint32_t units) {
+    return 16 * 16 * q4_pay_stride(units) + 16 * 4 * q4_meta_stride(units);
+}
+
 // Q4_0 codes n of four bytes, low or high nibbles, as the signed int8
 // weights n - 8: per byte (0x80 | n) - 8 stays within the byte (no borrow),
 // and flipping its top bit gives n - 8 in two's complement.
@@ -1079,6 +1092,8 @@ __device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, uint32_t b0, u
 // and applies the block scale it loaded itself.  `B` holds the chunk's
 // image words, loaded by the caller ahead of time (STAGE: one chunk ahead,
 // so the next chunk's image loads are in flight while this one computes).
+// STAGE: the row group is in LDS in the row-major layout, `ppieces` and
+// `mpieces` its payload and meta strides.
 template <int NB, int RT, bool STAGE, bool DUMP>
 __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
                                               const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
@@ -1095,13 +1110,13 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const uint32_t row = r0 + 16 * t + m;
-            const MfmaUnit u = mfma_unit(a, row < rows ? row : (STAGE ? r0 : 0u), STAGE ? t0 : 0u, b >> 2, b & 3);
+            const MfmaUnit u = STAGE ? MfmaUnit{} : mfma_unit(a, row < rows ? row : 0u, 0u, b >> 2, b & 3);
             if constexpr (STAGE) {
-                const uint32_t pa = 16 * lds_swizzle(static_cast<uint32_t>(u.payload) >> 4, ppieces);
-                const uint32_t ma = 16 * lds_swizzle(static_cast<uint32_t>(u.meta) >> 4, mpieces) +
-                                    (static_cast<uint32_t>(u.meta) & 8u);
-                A[i][t] = *reinterpret_cast<const uint32_t *>(lds + pa + 4 * g);
-                const uint2 mt = *reinterpret_cast<const uint2 *>(lds + meta_lds + ma);
+                // row 16t + m of the staged group (rows past the tensor read
+                // the group's row 0 and get scale 0)
+                const uint32_t rr = row < rows ? 16 * t + m : 0u;
+                A[i][t] = *reinterpret_cast<const uint32_t *>(lds + 16 * (rr * ppieces + b) + 4 * g);
+                const uint2 mt = *reinterpret_cast<const uint2 *>(lds + meta_lds + 4 * (rr * mpieces + 2 * (b >> 2)));
                 Ml[i][t] = mt.x;
                 Mh[i][t] = mt.y;
             } else {
@@ -1181,20 +1196,59 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         meta_lds = ((16u * RT) >> a.rows_per_wave_log2) * static_cast<uint32_t>(a.tile_payload_bytes);
         const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
         const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
-        // Q4_0: LDS position p holds piece lds_swizzle(p) (lane order fixes
-        // the destination, so the source address is permuted)
-        ppieces = (pbytes + 15) / 16;
-        mpieces = (mbytes + 15) / 16;
-        for (uint32_t c0 = wave * kWaveSize * 16; c0 < pbytes; c0 += blockDim.x * 16)
-            if (c0 + lane * 16 < pbytes) {
-                const uint32_t src = KIND == kQ4_0 ? 16 * lds_swizzle((c0 >> 4) + lane, ppieces) : c0 + lane * 16;
-                __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0), 16, 0, 0);
+        if constexpr (KIND == kQ4_0) {
+            // row-major layout (q4_pay_stride): LDS piece p of the copy is
+            // (row p / stride, block p % stride); the lane order fixes the
+            // destination, so each lane computes its piece's source in the
+            // wave-tile layout.  Padding pieces and rows past the tensor's
+            // tiles copy the tile start (never read, or read with scale 0).
+            const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+            ppieces = q4_pay_stride(a.units);
+            mpieces = q4_meta_stride(a.units);
+            meta_lds = 16 * 16 * ppieces;
+            auto unit_at = [&](uint32_t rr, uint32_t u, uint32_t &tile_off, uint32_t &slot, uint32_t &n,
+                               uint32_t &pos) {
+                const uint32_t tl = rr >> a.rows_per_wave_log2, grp = rr & (R - 1);
+                slot = u >> a.lanes_log2;
+                n = min(L, a.units - slot * L);
+                tile_off = tl;
+                pos = grp * n + (u & (L - 1));
+            };
+            for (uint32_t c0 = wave * kWaveSize; c0 < 16 * ppieces; c0 += blockDim.x) {
+                const uint32_t pc = c0 + lane, rr = pc / ppieces, b = pc - rr * ppieces;
+                size_t src = 0;
+                if (rr < 16 && b < 4 * a.units) {
+                    uint32_t tl, slot, n, pos;
+                    unit_at(rr, b >> 2, tl, slot, n, pos);
+                    if (tl < ntile)
+                        src = static_cast<size_t>(tl) * a.tile_payload_bytes + static_cast<size_t>(64) * R * L * slot +
+                              16 * ((b & 3) * R * n + pos);
+                }
+                if (pc < 16 * ppieces)
+                    __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
             }
-        for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
-            if (c0 + lane * 16 < mbytes) {
-                const uint32_t src = KIND == kQ4_0 ? 16 * lds_swizzle((c0 >> 4) + lane, mpieces) : c0 + lane * 16;
-                __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0), 16, 0, 0);
+            for (uint32_t c0 = wave * kWaveSize; c0 < 16 * mpieces; c0 += blockDim.x) {
+                const uint32_t dw = c0 + lane, rr = dw / mpieces, w = dw - rr * mpieces;
+                size_t src = 0;
+                if (rr < 16 && (w >> 1) < a.units) {
+                    uint32_t tl, slot, n, pos;
+                    unit_at(rr, w >> 1, tl, slot, n, pos);
+                    if (tl < ntile)
+                        src = static_cast<size_t>(tl) * a.tile_meta_bytes + static_cast<size_t>(8) * R * L * slot +
+                              8 * pos + 4 * (w & 1);
+                }
+                if (dw < 16 * mpieces)
+                    __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0 * 4), 4, 0, 0);
             }
+        } else {
+            for (uint32_t c0 = wave * kWaveSize * 16; c0 < pbytes; c0 += blockDim.x * 16)
+                if (c0 + lane * 16 < pbytes)
+                    __builtin_amdgcn_global_load_lds(psrc + c0 + lane * 16, (lds_void *)(smem + c0), 16, 0, 0);
+            for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
+                if (c0 + lane * 16 < mbytes)
+                    __builtin_amdgcn_global_load_lds(msrc + c0 + lane * 16, (lds_void *)(smem + meta_lds + c0), 16,
+                                                     0, 0);
+        }
         wait_vmcnt<0>();               // this wave's copies landed
         __builtin_amdgcn_s_barrier();  // ... and every wave's
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -2019,7 +2073,10 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     // are never staged) and fits gfx950's 160 KB of LDS per workgroup
     const bool whole = rows_grp % t.rows_per_wave == 0;
     const uint64_t stage =
-        whole ? static_cast<uint64_t>(rows_grp / t.rows_per_wave) * (t.tile_payload_bytes + t.tile_meta_bytes) : 0;
+        !whole ? 0
+               : t.kind == kQ4_0 ? q4_stage_bytes(t.units)
+                                 : static_cast<uint64_t>(rows_grp / t.rows_per_wave) *
+                                       (t.tile_payload_bytes + t.tile_meta_bytes);
     p.stage = whole && stage + part <= kMfmaLdsLimit;
     p.stage_bytes = p.stage ? static_cast<uint32_t>(stage) : 0;
     p.lds_bytes = p.stage_bytes + part;
