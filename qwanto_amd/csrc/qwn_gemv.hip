@@ -1040,16 +1040,6 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
     }
 }
 
-// Position in LDS of 16-byte piece `piece` of a staged region of `npieces`
-// pieces: within every whole aligned group of 16 pieces the low four bits
-// are XORed with the group index (an involution, so the same map serves
-// the copy and the reads).  Q4_0 rows are n * 16 bytes apart in a tile;
-// this spreads the 4-byte A reads and 8-byte scale reads of a wave's 16
-// rows over distinct banks.
-__device__ __forceinline__ uint32_t lds_swizzle(uint32_t piece, uint32_t npieces) {
-    return (piece | 15u) < npieces ? piece ^ ((piece >> 4) & 15u) : piece;
-}
-
 // Staged Q4_0 row groups are laid out row-major in LDS: payload
 // [16 rows][q4_pay_stride(units) 16-byte pieces] (piece b of a row = chunk
 // b % 4 of unit b / 4, i.e. 32-weight block b), then meta [16 rows]
@@ -1383,30 +1373,26 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 // (their order is not fixed: the last bits of the residual can differ from
 // run to run).
 struct Q4Split {
-    uint32_t qs, t0, tpieces, ppieces, mpieces, meta_lds;
+    uint32_t qs, pst, mst, meta_lds;
 };
 
+// One chunk of the split's units v0 .. v0 + nv - 1 (block 4v + qs of each),
+// operands read from the split's row-major staging: payload [16 rows][pst
+// pieces] (piece v = chunk qs of unit v), meta [16 rows][mst dwords].
 template <int NB>
 __device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t *lds, const Q4Split &sp,
                                                uint32_t rows, uint32_t r0, uint32_t v0, uint32_t nv, uint32_t lane,
                                                float (&acc)[4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
-    const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
     const uint32_t row = r0 + m;
-    const uint32_t rr = row < rows ? row : r0;
-    const uint32_t tile = (rr >> a.rows_per_wave_log2) - sp.t0, grp = rr & (R - 1);
+    const uint32_t rr = row < rows ? m : 0u;
     uint32_t A[NB], Ml[NB], Mh[NB];
     uint2 B[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const uint32_t v = v0 + (static_cast<uint32_t>(i) < nv ? i : 0);
-        const uint32_t slot = v >> a.lanes_log2, jj = v & (L - 1);
-        const uint32_t n = min(L, a.units - slot * L);
-        const uint32_t piece = tile * sp.tpieces + R * L * slot + grp * n + jj;
-        A[i] = *reinterpret_cast<const uint32_t *>(lds + 16 * lds_swizzle(piece, sp.ppieces) + 4 * g);
-        const uint32_t mo = static_cast<uint32_t>(tile * a.tile_meta_bytes) + 8 * R * L * slot + (grp * n + jj) * 8;
-        const uint2 mt =
-            *reinterpret_cast<const uint2 *>(lds + sp.meta_lds + 16 * lds_swizzle(mo >> 4, sp.mpieces) + (mo & 8u));
+        A[i] = *reinterpret_cast<const uint32_t *>(lds + 16 * (rr * sp.pst + v) + 4 * g);
+        const uint2 mt = *reinterpret_cast<const uint2 *>(lds + sp.meta_lds + 4 * (rr * sp.mst + 2 * v));
         Ml[i] = mt.x;
         Mh[i] = mt.y;
         const uint32_t b = min(4 * v + sp.qs, a.nblk - 1);
@@ -1456,31 +1442,40 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
     Q4Split sp;
     sp.qs = local & 3u;
     const uint32_t r0 = (local >> 2) * 16;
-    sp.t0 = r0 >> a.rows_per_wave_log2;
-    // the row group's tiles: chunk qs of each slot, then the whole meta
-    const uint32_t ntile = min(16u >> a.rows_per_wave_log2, tiles - sp.t0);
-    sp.tpieces = R * a.units;
-    sp.ppieces = ntile * sp.tpieces;
-    sp.meta_lds = (16u >> a.rows_per_wave_log2) * sp.tpieces * 16;
-    const uint32_t mbytes = ntile * static_cast<uint32_t>(a.tile_meta_bytes);
-    sp.mpieces = (mbytes + 15) / 16;
-    const uint8_t *msrc = meta + static_cast<size_t>(sp.t0) * a.tile_meta_bytes;
-    for (uint32_t c0 = wave * kWaveSize; c0 < sp.ppieces; c0 += blockDim.x)
-        if (c0 + lane < sp.ppieces) {
-            // LDS position p holds piece lds_swizzle(p): the source is permuted
-            const uint32_t pc = lds_swizzle(c0 + lane, sp.ppieces);
-            const uint32_t tile = pc / sp.tpieces, rem = pc - tile * sp.tpieces;
-            const uint32_t slot = rem / (R * L), r2 = rem - slot * R * L;
-            const uint32_t n = min(L, a.units - slot * L);
-            const size_t src = static_cast<size_t>(sp.t0 + tile) * a.tile_payload_bytes +
-                               static_cast<size_t>(64) * R * L * slot + 16 * (sp.qs * R * n + r2);
-            __builtin_amdgcn_global_load_lds(payload + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
+    const uint32_t t0 = r0 >> a.rows_per_wave_log2;
+    // the row group's chunk qs of every unit, row-major, then its meta; the
+    // lane order fixes the LDS destination, so each lane computes its
+    // piece's source (padding pieces and rows past the tensor's tiles copy
+    // the tile start: never read, or read with scale 0)
+    const uint32_t ntile = min(16u >> a.rows_per_wave_log2, tiles - t0);
+    sp.pst = a.units | 1u;
+    sp.mst = q4_meta_stride(a.units);
+    sp.meta_lds = 16 * 16 * sp.pst;
+    const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
+    const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
+    for (uint32_t c0 = wave * kWaveSize; c0 < 16 * sp.pst; c0 += blockDim.x) {
+        const uint32_t pc = c0 + lane, rr = pc / sp.pst, v = pc - rr * sp.pst;
+        const uint32_t tl = rr >> a.rows_per_wave_log2, grp = rr & (R - 1);
+        size_t src = 0;
+        if (rr < 16 && v < a.units && tl < ntile) {
+            const uint32_t slot = v >> a.lanes_log2, n = min(L, a.units - slot * L);
+            src = static_cast<size_t>(tl) * a.tile_payload_bytes + static_cast<size_t>(64) * R * L * slot +
+                  16 * (sp.qs * R * n + grp * n + (v & (L - 1)));
         }
-    for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
-        if (c0 + lane * 16 < mbytes) {
-            const uint32_t src = 16 * lds_swizzle((c0 >> 4) + lane, sp.mpieces);
-            __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + sp.meta_lds + c0), 16, 0, 0);
+        if (pc < 16 * sp.pst) __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
+    }
+    for (uint32_t c0 = wave * kWaveSize; c0 < 16 * sp.mst; c0 += blockDim.x) {
+        const uint32_t dw = c0 + lane, rr = dw / sp.mst, w = dw - rr * sp.mst;
+        const uint32_t tl = rr >> a.rows_per_wave_log2, grp = rr & (R - 1), v = w >> 1;
+        size_t src = 0;
+        if (rr < 16 && v < a.units && tl < ntile) {
+            const uint32_t slot = v >> a.lanes_log2, n = min(L, a.units - slot * L);
+            src = static_cast<size_t>(tl) * a.tile_meta_bytes + static_cast<size_t>(8) * R * L * slot +
+                  8 * (grp * n + (v & (L - 1))) + 4 * (w & 1);
         }
+        if (dw < 16 * sp.mst)
+            __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + sp.meta_lds + c0 * 4), 4, 0, 0);
+    }
     wait_vmcnt<0>();               // this wave's copies landed
     __builtin_amdgcn_s_barrier();  // ... and every wave's
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -2138,8 +2133,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         p.nb = per_wave(p.ks_log2);
         p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : p.nb <= 5 ? 5 : 8;
         p.waves = 1u << p.ks_log2;
-        const uint32_t tiles_grp = 16u / t0.rows_per_wave;
-        p.stage_bytes = tiles_grp * (t0.rows_per_wave * units * 16 + static_cast<uint32_t>(t0.tile_meta_bytes));
+        p.stage_bytes = 16 * 16 * (units | 1u) + 16 * 4 * q4_meta_stride(units);
         p.lds_bytes = p.stage_bytes + (p.waves - 1) * kWaveSize * 16;
         if (p.lds_bytes > kMfmaLdsLimit) return hipErrorInvalidValue;
     }
