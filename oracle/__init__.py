@@ -17,7 +17,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "liboracle.so")
+# QWN_ORACLE_LIB names another build of the same sources (the sanitizer run)
+ORACLE_SO = os.environ.get("QWN_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libqwn_ref.so")
 
 _c_i8p = ctypes.POINTER(ctypes.c_int8)

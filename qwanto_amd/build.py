@@ -67,16 +67,21 @@ def build(verbose: bool = True) -> str:
 HOST_DECODER = os.path.join(LIBDIR, "libqwn_host_decoder.so")
 
 
-def build_host_decoder() -> str:
+SANITIZE_FLAGS = ("-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+                  "-fno-sanitize-recover=all")
+
+
+def build_host_decoder(out: str = HOST_DECODER, sanitize: bool = False) -> str:
     """The host-side decoder (plain C, above the ABI): gcc, no contraction so
-    its explicit fused multiply-adds are the only ones."""
-    tmp = HOST_DECODER + ".tmp"
+    its explicit fused multiply-adds are the only ones.  ``sanitize`` builds
+    it with AddressSanitizer and UndefinedBehaviorSanitizer into ``out``."""
+    tmp = out + ".tmp"
     cmd = [os.environ.get("CC", "gcc"), "-O2", "-std=gnu11", "-fPIC", "-shared", "-ffp-contract=off",
-           "-Wall", "-Wextra", "-I" + os.path.join(ROOT, "include"),
+           "-Wall", "-Wextra", *(SANITIZE_FLAGS if sanitize else ()), "-I" + os.path.join(ROOT, "include"),
            os.path.join(PKG, "host", "qwn_host_decoder.c"), "-o", tmp, "-ldl", "-lm"]
     subprocess.run(cmd, check=True)
-    os.replace(tmp, HOST_DECODER)
-    return HOST_DECODER
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

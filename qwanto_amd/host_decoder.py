@@ -10,7 +10,8 @@ import numpy as np
 
 from . import build
 
-LIB_PATH = build.HOST_DECODER
+# QWN_HOST_DECODER_LIB names another build of the same source (the sanitizer run)
+LIB_PATH = os.environ.get("QWN_HOST_DECODER_LIB") or build.HOST_DECODER
 PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
 
 

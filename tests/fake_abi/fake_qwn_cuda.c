@@ -18,14 +18,33 @@
  *   FAKE_CONTEXT_FAIL     context_create() fails
  *   FAKE_NO_Q4_CAP        no Q4_0 capability bit (the build's extension)
  *   FAKE_GEMV_ZERO_COUNT  gemv returns OK without counting a matmul
+ *   FAKE_COMPUTE          a working CPU library: uploads are copied, every
+ *                         projection and Q8 KV call is computed by the
+ *                         oracle (link with oracle/liboracle.so), so the host
+ *                         decoder runs end to end without a device
  *
- * Every accepted call returns OK and does nothing else; gemv refuses
- * (UNSUPPORTED) unless FAKE_GEMV_ZERO_COUNT.
+ * Without FAKE_COMPUTE every accepted call returns OK and does nothing else;
+ * gemv refuses (UNSUPPORTED) unless FAKE_GEMV_ZERO_COUNT.
  */
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "qwn_cuda_abi.h"
+#ifdef FAKE_COMPUTE
+#include "qwn_oracle.h"
+
+typedef struct {
+    uint8_t *data;
+    uint32_t dtype, rows, cols;
+} FakeTensor;
+
+typedef struct {
+    uint32_t max_tokens, channels, groups;
+    int8_t *keys, *values;
+    float *key_scales, *value_scales;
+} FakeCache;
+#endif
 
 #ifndef FAKE_ABI_VERSION
 #define FAKE_ABI_VERSION QWN_CUDA_ABI_VERSION
@@ -42,7 +61,10 @@
 
 static char g_error[128] = "";
 static QwnCudaTelemetry g_telemetry;
-static int g_context_token, g_tensor_token, g_cache_token;
+static int g_context_token;
+#ifndef FAKE_COMPUTE
+static int g_tensor_token, g_cache_token;
+#endif
 
 static void fill_info(QwnCudaAbiInfo *info, uint32_t version) {
     memset(info, 0, sizeof(*info));
@@ -119,13 +141,32 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_destroy(QwnCudaContextHandle *context)
 QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *context, const QwnCudaTensorUpload *upload,
                                                 QwnCudaTensorHandle *tensor) {
     if (!context || !upload || !tensor) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+#ifdef FAKE_COMPUTE
+    FakeTensor *t = (FakeTensor *)calloc(1, sizeof(FakeTensor));
+    if (!t || !(t->data = (uint8_t *)malloc(upload->data_bytes))) {
+        free(t);
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+    memcpy(t->data, upload->host_data, upload->data_bytes);
+    t->dtype = upload->dtype;
+    t->rows = upload->rows;
+    t->cols = upload->cols;
+    tensor->opaque = t;
+#else
     tensor->opaque = &g_tensor_token;
+#endif
     g_telemetry.gpu_upload_count++;
     return QWN_CUDA_STATUS_OK;
 }
 
 QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *context, QwnCudaTensorHandle *tensor) {
     (void)context;
+#ifdef FAKE_COMPUTE
+    if (tensor && tensor->opaque) {
+        free(((FakeTensor *)tensor->opaque)->data);
+        free(tensor->opaque);
+    }
+#endif
     if (tensor) tensor->opaque = NULL;
     return QWN_CUDA_STATUS_OK;
 }
@@ -133,12 +174,40 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *context, 
 QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_create(QwnCudaContextHandle *context, const QwnCudaKvCacheOptions *options,
                                                   QwnCudaKvCacheHandle *cache) {
     if (!context || !options || !cache) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+#ifdef FAKE_COMPUTE
+    FakeCache *c = (FakeCache *)calloc(1, sizeof(FakeCache));
+    if (!c) return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    c->max_tokens = options->max_tokens;
+    c->channels = options->kv_heads * options->head_dim;
+    c->groups = (c->channels + 63) / 64;
+    const size_t n = (size_t)c->max_tokens * c->channels, g = (size_t)c->max_tokens * c->groups;
+    c->keys = (int8_t *)calloc(n, 1);
+    c->values = (int8_t *)calloc(n, 1);
+    c->key_scales = (float *)calloc(g, sizeof(float));
+    c->value_scales = (float *)calloc(g, sizeof(float));
+    cache->opaque = c;
+    if (!c->keys || !c->values || !c->key_scales || !c->value_scales) {
+        qwn_cuda_abi_kv_cache_destroy(context, cache);
+        return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+    }
+#else
     cache->opaque = &g_cache_token;
+#endif
     return QWN_CUDA_STATUS_OK;
 }
 
 QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_destroy(QwnCudaContextHandle *context, QwnCudaKvCacheHandle *cache) {
     (void)context;
+#ifdef FAKE_COMPUTE
+    if (cache && cache->opaque) {
+        FakeCache *c = (FakeCache *)cache->opaque;
+        free(c->keys);
+        free(c->values);
+        free(c->key_scales);
+        free(c->value_scales);
+        free(c);
+    }
+#endif
     if (cache) cache->opaque = NULL;
     return QWN_CUDA_STATUS_OK;
 }
@@ -147,7 +216,19 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_append(QwnCudaContextHandle *context,
                                                   const QwnCudaKvAppendRequest *request,
                                                   QwnCudaTelemetry *telemetry) {
     (void)context;
+#ifdef FAKE_COMPUTE
+    if (!request || !request->cache.opaque) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    FakeCache *c = (FakeCache *)request->cache.opaque;
+    if (request->token >= c->max_tokens || request->n_channels != c->channels) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    const size_t t = request->token;
+    qo_q8_quantize_vector(request->host_key, c->keys + t * c->channels, c->key_scales + t * c->groups,
+                          (int)c->channels);
+    qo_q8_quantize_vector(request->host_value, c->values + t * c->channels, c->value_scales + t * c->groups,
+                          (int)c->channels);
+    g_telemetry.kv_cache_kernel_count++;
+#else
     (void)request;
+#endif
     if (telemetry) *telemetry = g_telemetry;
     return QWN_CUDA_STATUS_OK;
 }
@@ -156,7 +237,18 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_attention(QwnCudaContextHandle *conte
                                                      const QwnCudaKvAttentionRequest *request,
                                                      QwnCudaTelemetry *telemetry) {
     (void)context;
+#ifdef FAKE_COMPUTE
+    if (!request || !request->cache.opaque) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    FakeCache *c = (FakeCache *)request->cache.opaque;
+    if (request->position >= c->max_tokens || request->kv_heads * request->head_dim != c->channels)
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    qo_q8_attention_abi(request->host_query, c->keys, c->values, c->key_scales, c->value_scales,
+                        (int)request->query_heads, (int)request->kv_heads, (int)request->head_dim,
+                        (int)request->position, request->scale, request->host_output);
+    g_telemetry.kv_cache_kernel_count++;
+#else
     (void)request;
+#endif
     if (telemetry) *telemetry = g_telemetry;
     return QWN_CUDA_STATUS_OK;
 }
@@ -169,6 +261,49 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_reset(QwnCudaContextHandle *context, 
 }
 #endif
 
+#ifdef FAKE_COMPUTE
+/* One token per request row, as the host decoder sends them: Q4_0 and
+ * HyperVSQ-2 take int8 tokens with one scale, F16 takes fp32. */
+static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *telemetry) {
+    if (!request || !request->tensor.opaque || !request->input_q8 || !request->output)
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    const FakeTensor *t = (const FakeTensor *)request->tensor.opaque;
+    const int K = (int)t->cols, N = (int)t->rows;
+    if (request->rows != t->rows || request->cols != t->cols) return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    for (uint32_t b = 0; b < request->batch; b++) {
+        float *y = request->output + (size_t)b * request->output_stride;
+        if (t->dtype == QWN_CUDA_TENSOR_F16 && request->input_mode == QWN_CUDA_INPUT_F32) {
+            const float *x = (const float *)request->input_q8 + (size_t)b * request->input_stride;
+            qo_matmul_f16((const uint16_t *)t->data, x, 1, K, N, y, 1);
+        } else if (request->input_mode == QWN_CUDA_INPUT_Q8 && t->dtype == QWN_CUDA_TENSOR_Q4_0_18) {
+            const int8_t *q = request->input_q8 + (size_t)b * request->input_stride;
+            const float s = request->input_scales ? request->input_scales[b] : request->input_scale;
+            qo_gemv_q4_0_q8(t->data, q, s, K, N, y, 1);
+        } else if (request->input_mode == QWN_CUDA_INPUT_Q8 && t->dtype == QWN_CUDA_TENSOR_HYPERVSQ2_74) {
+            const int padded = (K + 255) & ~255;
+            int8_t *q = (int8_t *)calloc((size_t)padded, 1);
+            int32_t *sums = (int32_t *)calloc((size_t)padded / 32, sizeof(int32_t));
+            if (!q || !sums) {
+                free(q);
+                free(sums);
+                return QWN_CUDA_STATUS_OUT_OF_MEMORY;
+            }
+            memcpy(q, request->input_q8 + (size_t)b * request->input_stride, (size_t)K);
+            for (int i = 0; i < padded; i++) sums[i / 32] += q[i];
+            const float s = request->input_scales ? request->input_scales[b] : request->input_scale;
+            qo_gemv_hvsq2_delayed(t->data, q, sums, s, K, N, (size_t)(K + 255) / 256 * 74, y, 0);
+            free(q);
+            free(sums);
+        } else {
+            snprintf(g_error, sizeof(g_error), "fake: dtype %u with input mode %u", t->dtype, request->input_mode);
+            return QWN_CUDA_STATUS_UNSUPPORTED;
+        }
+    }
+    g_telemetry.gpu_matmul_count++;
+    if (telemetry) *telemetry = g_telemetry;
+    return QWN_CUDA_STATUS_OK;
+}
+#else
 static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *telemetry) {
     (void)request;
 #ifdef FAKE_GEMV_ZERO_COUNT
@@ -180,6 +315,7 @@ static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *tele
     return QWN_CUDA_STATUS_UNSUPPORTED;
 #endif
 }
+#endif
 
 QWN_CUDA_ABI_API int qwn_cuda_abi_hypervsq2_gemv(QwnCudaContextHandle *context, const QwnCudaGemmRequest *request,
                                                  QwnCudaTelemetry *telemetry) {

@@ -28,10 +28,19 @@ def host_lib():
 
 
 def fake(tmp_path, *defines) -> str:
-    """Build one variant of the fake library; returns its path."""
+    """Build one variant of the fake library; returns its path.  FAKE_COMPUTE
+    links the oracle library named by QWN_ORACLE_LIB (the sanitizer run's
+    build) or oracle/liboracle.so.  QWN_FAKE_CFLAGS adds compiler flags."""
     out = str(tmp_path / ("fake_" + ("_".join(d.split("=")[0] for d in defines) or "ok") + ".so"))
+    link = []
+    if "FAKE_COMPUTE" in defines:
+        lib = os.environ.get("QWN_ORACLE_LIB") or os.path.join(ROOT, "oracle", "liboracle.so")
+        if not os.path.exists(lib):
+            subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "liboracle.so"], check=True)
+        link = ["-I" + os.path.join(ROOT, "oracle"), lib, "-Wl,-rpath," + os.path.dirname(lib)]
     cmd = [shutil.which("gcc") or "gcc", "-O1", "-shared", "-fPIC", "-std=gnu11", "-Wall",
-           "-I" + os.path.join(ROOT, "include"), *("-D" + d for d in defines), FAKE_SRC, "-o", out]
+           *os.environ.get("QWN_FAKE_CFLAGS", "").split(), "-I" + os.path.join(ROOT, "include"),
+           *("-D" + d for d in defines), FAKE_SRC, "-o", out, *link]
     subprocess.run(cmd, check=True)
     return out
 
@@ -92,3 +101,30 @@ def test_accepted_library_fails_closed(tmp_path, host_lib, defines):
     m = dec.metrics()
     assert m.cpu_fallback_count == 0 and m.gpu_matmul_count == 0
     dec.close()
+
+
+@pytest.mark.parametrize("dtype,extra", [("q4_0", {}), ("hvsq2", {}), ("q4_0", {"qk_norm": True, "biases": "qkvo"}),
+                                         ("hvsq2", {"qk_norm": True, "biases": "qkv"})])
+def test_host_decoder_end_to_end_on_cpu(tmp_path, host_lib, dtype, extra):
+    """A working CPU library (FAKE_COMPUTE: every projection and Q8 KV call
+    computed by the oracle's kernels) under the host decoder: its own step
+    arithmetic (RMSNorm, RoPE, q/k norms, biases, per-token quantize, SwiGLU,
+    residuals, the request fields it builds) must give the oracle decoder's
+    logits bit for bit, step after step, with no device in the loop."""
+    import oracle
+    cfg = dict(TINY, hidden=128, intermediate=256, layers=2, heads=4, kv_heads=2, vocab=300, max_ctx=24)
+    model = synth.decoder_model(np.random.default_rng(5), cfg, dtype, **extra)
+    dec = HostDecoder(model, abi_path=fake(tmp_path, "FAKE_COMPUTE"))
+    ref = oracle.load().decoder(model)
+    try:
+        token = 11
+        for step in range(20):
+            a, b = dec.forward(token), ref.forward(token)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+                f"step {step}: max |diff| {np.max(np.abs(a - b)):.3g}"
+            token = int(np.argmax(b))
+        m = dec.metrics()
+        assert m.cpu_fallback_count == 0 and m.gpu_matmul_count == 20 * (7 * cfg["layers"] + 1)
+    finally:
+        dec.close()
+        ref.close()
