@@ -253,7 +253,8 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
                     *reinterpret_cast<uint4 *>(mimg + (static_cast<size_t>(slot) * 16 + t) * 16) =
                         make_uint4(o[0], o[1], o[2], o[3]);
                     if ((sb & 15u) == 0)
-                        reinterpret_cast<int32_t *>(mimg + static_cast<size_t>(units) * 4096)[(sb >> 4) * 16 + t] = s;
+                        reinterpret_cast<float *>(mimg + static_cast<size_t>(units) * 4096)[(sb >> 4) * 16 + t] =
+                            static_cast<float>(s);
                 }
             }
         }
@@ -813,13 +814,14 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 // 4*byte + k, so the MFMA image stores each 16-element group of activations
 // in that transposed order:
 //   image [block][s][g][token 0..15][16 B] (byte 4k+b = element 16s+4b+k of
-//   the group 64g..64g+63), then int32 sums [block][token 0..15].
+//   the group 64g..64g+63), then the blocks' activation sums as floats
+//   [block][token 0..15] (|sum| <= 256 * 127: exact).
 // The weights stay in the GEMV wave-tile layout (one resident copy).  A
-// wave owns RT row tiles (16*RT rows, sharing each image load) and a range
-// of K blocks, and issues every load of up to five blocks before its first
-// MFMA, as the batch-1 GEMV issues its whole weight share at once; the
-// waves that split one row group's K combine their partial tiles through
-// LDS in wave order.
+// workgroup owns a 16-row group and its waves split the K blocks, combining
+// their partial tiles through LDS in wave order.  Where the group fits LDS
+// its tiles are copied there whole (mfma_chunk_hv: the weights are then the
+// B operand, so a lane applies its own row's scales); longer rows read the
+// weights straight from HBM (mfma_chunk: weights as the A operand).
 constexpr int kMfmaTokens = 16;
 
 __host__ __device__ constexpr size_t mfma_image_block_bytes() { return 16 * 256 + 16 * 4; }
@@ -854,7 +856,7 @@ __global__ __launch_bounds__(256) void mfma_image_kernel(const int8_t *__restric
                 if (e < K) sum += src[e];
             }
         }
-        reinterpret_cast<int32_t *>(img + static_cast<size_t>(units) * 4096)[idx] = sum;
+        reinterpret_cast<float *>(img + static_cast<size_t>(units) * 4096)[idx] = static_cast<float>(sum);
     }
 }
 
@@ -916,6 +918,7 @@ struct MfmaArgs {
     uint32_t accumulate;   // out += W x (residual add) instead of out = W x
     int32_t *dump;         // DUMP kernels: exact int32 block dots [token][row][nblk] of job 0
     const float *bias[kMaxGroup];  // per job: null, or [rows] added to each token's product
+    uint32_t pad_p, pad_m;         // HyperVSQ-2 staging gaps (hv_lds_pieces)
 };
 
 constexpr int kMfmaMaxWaves = 8;
@@ -941,32 +944,30 @@ __device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, u
     return u;
 }
 
-// One chunk of up to NB blocks.  The image loads (and, without STAGE, the
-// weight loads) of the whole chunk are issued before the first MFMA.
-// STAGE: the row group's weight tiles were copied to LDS (payload at 0, meta
-// at `meta_lds`) and the A operands are read from there.
-template <int NB, int RT, bool STAGE, bool DUMP>
+// One chunk of up to NB blocks of a row group read straight from the
+// wave-tile layout (rows too long to stage in LDS): the weight and image
+// loads of the whole chunk are issued before the first MFMA.  The weights
+// are the MFMA's A operand here, so lane (g, m) holds rows 4g .. 4g+3 of
+// token m and takes those rows' d and m from the lanes that loaded them.
+template <int NB, int RT, bool DUMP>
 __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
-                                           const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
-                                           uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
+                                           uint32_t rows, uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
                                            float (&acc)[RT][4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
-    const int32_t *sums = reinterpret_cast<const int32_t *>(a.image + static_cast<size_t>(a.units) * 4096);
+    const float *sums = reinterpret_cast<const float *>(a.image + static_cast<size_t>(a.units) * 4096);
     uint4 A[NB][RT];
     uint2 Mt[NB][RT];
     mfma_v4i B[NB][4];
-    int SA[NB];
-    if constexpr (!STAGE) {
+    float SA[NB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
 #pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const uint32_t row = r0 + 16 * t + m;
-                const MfmaUnit u = mfma_unit(a, row < rows ? row : 0, 0, b, g);
-                A[i][t] = *reinterpret_cast<const uint4 *>(payload + u.payload);
-                Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
-            }
+        for (int t = 0; t < RT; ++t) {
+            const uint32_t row = r0 + 16 * t + m;
+            const MfmaUnit u = mfma_unit(a, row < rows ? row : 0, 0, b, g);
+            A[i][t] = *reinterpret_cast<const uint4 *>(payload + u.payload);
+            Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
         }
     }
 #pragma unroll
@@ -977,19 +978,6 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
         for (int sl = 0; sl < 4; ++sl) B[i][sl] = *reinterpret_cast<const mfma_v4i *>(ib + sl * 1024);
         SA[i] = sums[b * 16 + m];
     }
-    if constexpr (STAGE) {
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
-#pragma unroll
-            for (int t = 0; t < RT; ++t) {
-                const uint32_t row = r0 + 16 * t + m;
-                const MfmaUnit u = mfma_unit(a, row < rows ? row : r0, t0, b, g);
-                A[i][t] = *reinterpret_cast<const uint4 *>(lds + u.payload);
-                Mt[i][t] = *reinterpret_cast<const uint2 *>(lds + meta_lds + u.meta);
-            }
-        }
-    }
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -999,7 +987,7 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (static_cast<uint32_t>(i) >= nblk) break;
-        const float sa = static_cast<float>(SA[i]);
+        const float sa = SA[i];
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const uint32_t subs = (Mt[i][t].y >> (8 * g)) & 0xffu;
@@ -1037,6 +1025,140 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
                 acc[t][r] = fmaf(static_cast<float>(ci[r]), dsc, fmaf(msc, sa, acc[t][r]));
             }
         }
+    }
+}
+
+// Staged HyperVSQ-2 row groups keep their tiles' wave-tile layout (copied
+// whole, every load instruction one contiguous 1 KB span), with a gap of
+// `pad` 16-byte pieces after every 64 pieces (each copy instruction's LDS
+// destination moves on by 64 + pad pieces): piece q of the copy sits at LDS
+// piece q + (q / 64) * pad.  The gaps (payload and meta separately, chosen
+// per tile shape at upload: hv_stage_pads) spread a wave's operand reads of
+// one block over the LDS banks, which the plain layout folds onto two of
+// sixteen 16-byte bank groups for the common shapes.
+__host__ __device__ constexpr uint32_t hv_lds_pieces(uint32_t pieces, uint32_t pad) {
+    return pieces + (pieces + 63) / 64 * pad;
+}
+__host__ __device__ constexpr uint32_t hv_stage_bytes(uint32_t units, uint32_t pad_p, uint32_t pad_m) {
+    return 16 * hv_lds_pieces(64 * units, pad_p) + 16 * hv_lds_pieces(8 * units, pad_m);
+}
+
+// Per-lane operand offsets of a staged group for lane (g, m): the payload
+// piece and meta byte of row m's unit 0 in a full slot and in the last
+// slot (whose width differs); a unit adds a wave-uniform slot and lane offset.
+struct HvLane {
+    uint32_t qf, ql, mf, ml, last_slot;
+};
+
+__device__ __forceinline__ HvLane hv_lane(const MfmaArgs &a, uint32_t lane) {
+    const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const uint32_t tl = m >> a.rows_per_wave_log2, grp = m & (R - 1);
+    HvLane h;
+    h.last_slot = (a.units - 1) >> a.lanes_log2;
+    const uint32_t nlast = a.units - h.last_slot * L;
+    const uint32_t tq = tl * static_cast<uint32_t>(a.tile_payload_bytes / 16);
+    const uint32_t tmb = tl * static_cast<uint32_t>(a.tile_meta_bytes);
+    h.qf = tq + (g * R + grp) * L;
+    h.ql = tq + (g * R + grp) * nlast;
+    h.mf = tmb + 8 * grp * L;
+    h.ml = tmb + 8 * grp * nlast;
+    return h;
+}
+
+// The image operands of up to NB HyperVSQ-2 blocks from b0 (nv of them real,
+// the rest repeat b0): per block four 16-byte MFMA operands (tokens m, chunk
+// g of each slice) and the activation sums of tokens 4g .. 4g+3.  Bounded
+// buffer loads: the columns of tokens past a.ntok read as zero with no
+// memory access (their products are never stored), so a 4-token batch moves
+// a quarter of the image.  Always 5 * NB loads, so a caller can wait for
+// older loads with vmcnt(5 * NB).
+template <int NB>
+struct HvImage {
+    mfma_v4i B[NB][4];
+    float4 SA[NB];
+};
+
+template <int NB>
+__device__ __forceinline__ void hv_image_loads(const MfmaArgs &a, uint32_t b0, uint32_t nv, uint32_t lane,
+                                               HvImage<NB> &im) {
+    const uint32_t bytes = a.units * static_cast<uint32_t>(mfma_image_block_bytes());
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.image), 0, static_cast<int>(bytes), 0x00020000);
+    const uint32_t m = lane & 15, g = lane >> 4;
+    const uint32_t skip = m < a.ntok ? 0u : 0x80000000u, sskip = 4 * g < a.ntok ? 0u : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + (static_cast<uint32_t>(i) < nv ? i : 0);
+        const uint32_t off = (b * 4096 + lane * 16) | skip;
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl)
+            im.B[i][sl] =
+                __builtin_bit_cast(mfma_v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off + sl * 1024, 0, 0));
+        im.SA[i] = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (a.units * 4096 + (b * 16 + 4 * g) * 4) | sskip, 0, 0));
+    }
+}
+
+// One chunk of up to NB HyperVSQ-2 blocks b0 .. b0 + nv - 1 of a staged
+// group (`im` their image operands, `meta_lds` the staged meta).  The tokens
+// are the MFMA's A operand and the weight rows its B operand, so lane (g, m)
+// accumulates tokens 4g .. 4g+3 of row m and applies the d and m of its own
+// row (no exchange between lanes).  `live`: row m exists (else its scales
+// count as 0).
+template <int NB, bool DUMP>
+__device__ __forceinline__ void mfma_chunk_hv(const MfmaArgs &a, const uint8_t *lds, uint32_t meta_lds,
+                                              const HvLane &hl, uint32_t b0, uint32_t nv, bool live, uint32_t rows,
+                                              uint32_t r0, uint32_t lane, const HvImage<NB> &im, float (&acc)[4]) {
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const uint32_t R = 1u << a.rows_per_wave_log2, L = 1u << a.lanes_log2;
+    uint4 A[NB];
+    uint2 Mt[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const uint32_t b = b0 + (static_cast<uint32_t>(i) < nv ? i : 0);
+        const uint32_t slot = b >> a.lanes_log2, jj = b & (L - 1);
+        const bool last = slot == hl.last_slot;
+        const uint32_t q = (last ? hl.ql : hl.qf) + 4 * R * L * slot + jj;
+        A[i] = *reinterpret_cast<const uint4 *>(lds + 16 * (q + (q >> 6) * a.pad_p));
+        const uint32_t mb = (last ? hl.ml : hl.mf) + 8 * R * L * slot + 8 * jj, mq = mb >> 4;
+        Mt[i] = *reinterpret_cast<const uint2 *>(lds + meta_lds + 16 * (mq + (mq >> 6) * a.pad_m) + (mb & 8u));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (static_cast<uint32_t>(i) >= nv) break;
+        const uint32_t subs = (Mt[i].y >> (8 * g)) & 0xffu;
+        const uint32_t cw[4] = {A[i].x, A[i].y, A[i].z, A[i].w};
+        mfma_v4i ci = {0, 0, 0, 0};
+#pragma unroll
+        for (int sl = 0; sl < 4; ++sl) {
+            const uint32_t sub = (subs >> (4 * (sl >> 1))) & 15u;
+            // table bytes: code 0 -> -s, 1 -> 0, 2 -> s, 3 -> 2s
+            const uint32_t lut = ((0u - sub) & 0xffu) | (sub << 16) | ((2u * sub) << 24);
+            const uint32_t c = cw[sl];
+            mfma_v4i wv;
+            wv.x = static_cast<int>(__builtin_amdgcn_perm(0u, lut, c & 0x03030303u));
+            wv.y = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 2) & 0x03030303u));
+            wv.z = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 4) & 0x03030303u));
+            wv.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
+            // C[token][row]: element r is token 4g + r of row m
+            ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(im.B[i][sl], wv, ci, 0, 0, 0);
+        }
+        if constexpr (DUMP) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = r0 + m, tok = 4 * g + r;
+                if (row < rows && tok < a.ntok)
+                    a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
+            }
+        }
+        const uint32_t dm = live ? Mt[i].x : 0u;
+        const float dsc = half_to_float(dm & 0xffffu) * 0.125f;
+        const float msc = half_to_float(dm >> 16);
+        const float sa[4] = {im.SA[i].x, im.SA[i].y, im.SA[i].z, im.SA[i].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), dsc, fmaf(msc, sa[r], acc[r]));
     }
 }
 
@@ -1173,20 +1295,35 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     const uint32_t r0 = (blockIdx.x - first) * (16 * RT);
     const uint32_t kb0 = ks * a.nb;
     const uint32_t kb1 = min(a.nblk, kb0 + a.nb);
+    // token-major epilogue (lane (g, m): tokens 4g .. 4g+3 of row m): its
+    // token scales and, adding into the output, the prior outputs, loaded
+    // now so the epilogue does not wait a memory round trip
+    float xs_pre[4], res_pre[RT][4];
+    if constexpr (KIND == kQ4_0 || STAGE) {
+        const uint32_t g = lane >> 4, m = lane & 15;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+        if (a.accumulate && ks == 0) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t tok = 4 * g + r, row = r0 + 16 * t + m;
+                    res_pre[t][r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+                }
+        }
+    }
 
     // STAGE: the row group's wave tiles (16*RT rows = a whole number of
-    // tiles) are contiguous in HBM; copy payload and meta into LDS with
-    // direct 16-byte loads, every load instruction one contiguous 1 KB span
+    // tiles) are copied into LDS row-major with direct loads
     const uint32_t t0 = r0 >> a.rows_per_wave_log2;
     uint32_t meta_lds = 0, ppieces = 0, mpieces = 0;
+    HvImage<NB> him;
     if constexpr (STAGE) {
         const uint32_t ntile = min((16u * RT) >> a.rows_per_wave_log2, tiles - t0);
-        const uint32_t pbytes = ntile * static_cast<uint32_t>(a.tile_payload_bytes);
-        const uint32_t mbytes = ntile * static_cast<uint32_t>(a.tile_meta_bytes);
-        meta_lds = ((16u * RT) >> a.rows_per_wave_log2) * static_cast<uint32_t>(a.tile_payload_bytes);
-        const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
-        const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
         if constexpr (KIND == kQ4_0) {
+            const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
+            const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
             // row-major layout (q4_pay_stride): LDS piece p of the copy is
             // (row p / stride, block p % stride); the lane order fixes the
             // destination, so each lane computes its piece's source in the
@@ -1231,15 +1368,29 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                     __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0 * 4), 4, 0, 0);
             }
         } else {
-            for (uint32_t c0 = wave * kWaveSize * 16; c0 < pbytes; c0 += blockDim.x * 16)
-                if (c0 + lane * 16 < pbytes)
-                    __builtin_amdgcn_global_load_lds(psrc + c0 + lane * 16, (lds_void *)(smem + c0), 16, 0, 0);
-            for (uint32_t c0 = wave * kWaveSize * 16; c0 < mbytes; c0 += blockDim.x * 16)
-                if (c0 + lane * 16 < mbytes)
-                    __builtin_amdgcn_global_load_lds(msrc + c0 + lane * 16, (lds_void *)(smem + meta_lds + c0), 16,
-                                                     0, 0);
+            static_assert(RT == 1, "the staged HyperVSQ-2 group is 16 rows");
+            const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
+            const uint8_t *msrc = meta + static_cast<size_t>(t0) * a.tile_meta_bytes;
+            const uint32_t np = ntile * static_cast<uint32_t>(a.tile_payload_bytes / 16);
+            const uint32_t nm = (ntile * static_cast<uint32_t>(a.tile_meta_bytes) + 15) / 16;
+            meta_lds = 16 * hv_lds_pieces(64 * a.units, a.pad_p);
+            for (uint32_t c0 = wave * kWaveSize; c0 < np; c0 += blockDim.x)
+                if (c0 + lane < np)
+                    __builtin_amdgcn_global_load_lds(psrc + 16 * static_cast<size_t>(c0 + lane),
+                                                     (lds_void *)(smem + 16 * (c0 + (c0 >> 6) * a.pad_p)), 16, 0, 0);
+            for (uint32_t c0 = wave * kWaveSize; c0 < nm; c0 += blockDim.x)
+                if (c0 + lane < nm)
+                    __builtin_amdgcn_global_load_lds(msrc + 16 * static_cast<size_t>(c0 + lane),
+                                                     (lds_void *)(smem + meta_lds + 16 * (c0 + (c0 >> 6) * a.pad_m)),
+                                                     16, 0, 0);
+            // the first chunk's image loads go out behind the copies
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kb0 < kb1) hv_image_loads<NB>(a, kb0, min(static_cast<uint32_t>(NB), kb1 - kb0), lane, him);
         }
-        wait_vmcnt<0>();               // this wave's copies landed
+        // this wave's copies landed (HyperVSQ-2: all but its image loads)
+        if (KIND == kHvsq2 && kb0 < kb1) wait_vmcnt<5 * NB>();
+        else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();  // ... and every wave's
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
@@ -1249,10 +1400,18 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     for (int t = 0; t < RT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
-    if constexpr (KIND == kHvsq2) {
+    if constexpr (KIND == kHvsq2 && STAGE) {
+        const bool live = r0 + (lane & 15) < rows;
+        const HvLane hl = hv_lane(a, lane);
+        for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
+            const uint32_t nv = min(static_cast<uint32_t>(NB), kb1 - b0);
+            if (b0 != kb0) hv_image_loads<NB>(a, b0, nv, lane, him);
+            mfma_chunk_hv<NB, DUMP>(a, smem, meta_lds, hl, b0, nv, live, rows, r0, lane, him, acc[0]);
+        }
+    } else if constexpr (KIND == kHvsq2) {
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB)
-            mfma_chunk<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
-                                            min(static_cast<uint32_t>(NB), kb1 - b0), lane, acc);
+            mfma_chunk<NB, RT, DUMP>(a, payload, meta, rows, r0, b0, min(static_cast<uint32_t>(NB), kb1 - b0), lane,
+                                     acc);
     } else if constexpr (STAGE) {
         // the weights are in LDS: each chunk's image words are loaded one
         // chunk ahead (two register sets used in turn), so a chunk's
@@ -1306,7 +1465,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     // accumulate: out += the rounded product (the residual stream), in two
     // roundings as the dot8 epilogue
     const uint32_t g = lane >> 4, m = lane & 15;
-    if constexpr (KIND == kQ4_0) {
+    if constexpr (KIND == kQ4_0 || STAGE) {
         // lane (g, m) holds tokens 4g .. 4g+3 of row m of each tile: rows
         // are contiguous per token, so 16 lanes store one 64-byte span
         if (ks == 0) {
@@ -1314,15 +1473,13 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             for (int r = 0; r < 4; ++r) {
                 const uint32_t tok = 4 * g + r;
                 if (tok >= a.ntok) continue;
-                const float xs = a.scales[tok];
 #pragma unroll
                 for (int t = 0; t < RT; ++t) {
                     const uint32_t row = r0 + 16 * t + m;
                     if (row >= rows) continue;
-                    float *dst = output + static_cast<size_t>(tok) * stride + row;
-                    float v = mul_rounded(acc[t][r], xs);
+                    float v = mul_rounded(acc[t][r], xs_pre[r]);
                     if (bias) v = add_rounded(v, bias[row]);
-                    *dst = a.accumulate ? add_rounded(*dst, v) : v;
+                    output[static_cast<size_t>(tok) * stride + row] = a.accumulate ? add_rounded(res_pre[t][r], v) : v;
                 }
             }
         }
@@ -1724,6 +1881,52 @@ bool set_units(DeviceTensor &t) {
 
 }  // namespace
 
+// The gaps of the staged HyperVSQ-2 layout (hv_lds_pieces) for a tile
+// shape, found by laying out a wave's operand reads of every unit of a row
+// group: the payload gap with the fewest 16-byte reads per 16-byte bank
+// group (ds_read_b128 over 64 lanes: 4 at best), summed over the units, and
+// the meta gap with the fewest distinct 8-byte words per 8-byte bank pair
+// (16 rows, the four lane groups reading the same words).
+static void hv_stage_pads(DeviceTensor &t) {
+    t.stage_pad_p = t.stage_pad_m = 0;
+    const uint32_t L = t.lanes, R = t.rows_per_wave, units = t.units;
+    if (t.kind != kHvsq2 || R == 0 || 16 % R != 0) return;
+    const uint32_t last = (units - 1) / L, nlast = units - last * L;
+    const uint32_t tq = static_cast<uint32_t>(t.tile_payload_bytes / 16), tmb = static_cast<uint32_t>(t.tile_meta_bytes);
+    uint64_t best_p = ~0ull, best_m = ~0ull;
+    for (uint32_t pad = 0; pad < 16; ++pad) {
+        uint64_t cost_p = 0, cost_m = 0;
+        for (uint32_t b = 0; b < units; ++b) {
+            const uint32_t slot = b / L, jj = b % L, n = slot == last ? nlast : L;
+            uint32_t cnt[16] = {};
+            uint32_t words[16], nwords = 0;
+            for (uint32_t lane = 0; lane < 64; ++lane) {
+                const uint32_t g = lane >> 4, m = lane & 15, tl = m / R, grp = m % R;
+                const uint32_t q = tl * tq + (g * R + grp) * n + 4 * R * L * slot + jj;
+                ++cnt[(q + (q >> 6) * pad) & 15u];
+                if (g == 0) {
+                    const uint32_t mb = tl * tmb + 8 * R * L * slot + 8 * (grp * n + jj), mq = mb >> 4;
+                    words[nwords++] = (16 * (mq + (mq >> 6) * pad) + (mb & 8u)) / 8;
+                }
+            }
+            uint32_t worst = 0;
+            for (uint32_t c : cnt) worst = std::max(worst, c);
+            cost_p += worst;
+            uint32_t per[32] = {};
+            for (uint32_t i = 0; i < nwords; ++i) {
+                bool seen = false;
+                for (uint32_t j = 0; j < i; ++j) seen |= words[j] == words[i];
+                if (!seen) ++per[words[i] & 31u];
+            }
+            uint32_t wm = 0;
+            for (uint32_t c : per) wm = std::max(wm, c);
+            cost_m += wm;
+        }
+        if (cost_p < best_p) best_p = cost_p, t.stage_pad_p = pad;
+        if (cost_m < best_m) best_m = cost_m, t.stage_pad_m = pad;
+    }
+}
+
 bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     if (!set_units(t)) return false;
     bool upl_ok = false;
@@ -1742,6 +1945,7 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     const size_t payload = t.tile_payload_bytes * t.tiles;
     const size_t meta = t.tile_meta_bytes * t.tiles;
     t.device_bytes = ((payload + 255) & ~static_cast<size_t>(255)) + meta;
+    hv_stage_pads(t);
     return true;
 }
 
@@ -2066,12 +2270,12 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     const uint32_t rows_grp = 16u * p.rt;
     // staging needs whole tiles in the row group (tiles of 32 or 64 rows
     // are never staged) and fits gfx950's 160 KB of LDS per workgroup
-    const bool whole = rows_grp % t.rows_per_wave == 0;
-    const uint64_t stage =
-        !whole ? 0
-               : t.kind == kQ4_0 ? q4_stage_bytes(t.units)
-                                 : static_cast<uint64_t>(rows_grp / t.rows_per_wave) *
-                                       (t.tile_payload_bytes + t.tile_meta_bytes);
+    // (HyperVSQ-2 meta copied in whole 16-byte pieces: an even number of
+    // 8-byte entries per tile)
+    const bool whole = rows_grp % t.rows_per_wave == 0 && (t.kind != kHvsq2 || t.tile_meta_bytes % 16 == 0);
+    const uint64_t stage = !whole                ? 0
+                           : t.kind == kQ4_0 ? q4_stage_bytes(t.units)
+                                             : hv_stage_bytes(t.units, t.stage_pad_p, t.stage_pad_m);
     p.stage = whole && stage + part <= kMfmaLdsLimit;
     p.stage_bytes = p.stage ? static_cast<uint32_t>(stage) : 0;
     p.lds_bytes = p.stage_bytes + part;
@@ -2121,7 +2325,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         total_rows += t.rows;
     }
     MfmaPlan p = mfma_plan(t0, total_rows);
-    // Q4_0 residual adds over few row groups: the four-way K split
+    // residual adds over few row groups: the four-way K split
     const uint64_t groups = (total_rows + 15) / 16;
     const bool split = t0.kind == kQ4_0 && accumulate && !dump && p.stage && groups < 256;
     if (split) {
@@ -2171,6 +2375,8 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.ntok = batch;
     a.accumulate = accumulate ? 1u : 0u;
     a.dump = dump;
+    a.pad_p = t0.stage_pad_p;
+    a.pad_m = t0.stage_pad_m;
     if (split) {
         const uint32_t threads = p.waves * kWaveSize;
         switch (p.nbt) {

@@ -73,6 +73,10 @@ struct DeviceTensor {
     uint8_t *meta = nullptr;     // null for F16
     uint64_t device_bytes = 0;   // bytes allocated on the device
     uint64_t logical_bytes = 0;  // algorithmic (on-disk) bytes
+    // HyperVSQ-2 MFMA staging: gaps (16-byte pieces after every 64) of the
+    // payload and meta copies in LDS, chosen for the tile shape
+    uint32_t stage_pad_p = 0;
+    uint32_t stage_pad_m = 0;
 };
 
 // Launch shape of one GEMV call.

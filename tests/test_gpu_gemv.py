@@ -145,19 +145,25 @@ def run_mfma_group(ctx, oracle_lib, kind, Ns, K, M, seed, accumulate=False):
 @pytest.mark.parametrize("Ns,K,M", [((4096, 1024, 1024), 2560, 16), ((9728, 9728), 2560, 16),
                                     ((8200, 77), 777, 9), ((16390, 5), 520, 11), ((300,), 16384, 8),
                                     ((2560,), 9728, 12), ((4096, 1024, 1024), 2560, 3),
-                                    ((9728, 9728), 2560, 4), ((2560,), 9728, 5)])
+                                    ((9728, 9728), 2560, 4), ((2560,), 9728, 5), ((40, 7), 16640, 5)])
 def test_hvsq2_mfma_group(gpu_ctx, oracle_lib, Ns, K, M):
     """qwn_hip_ext_gemm_mfma_group_device: one MFMA launch over tensors of
     equal columns sharing one image (q/k/v and gate/up shapes, 32- and
     64-row-group launches with ragged rows, unaligned row counts and partial
     blocks, K beyond one chunk of blocks per wave), every token of every
-    tensor against the oracle."""
+    tensor against the oracle; 65 units of one row per wave tile, whose odd
+    meta tiles are read straight from HBM instead of staged)."""
     run_mfma_group(gpu_ctx, oracle_lib, "hvsq2", Ns, K, M, seed=sum(Ns) + K + M)
 
 
-@pytest.mark.parametrize("Ns,K,M", [((2560,), 4096, 16), ((77, 1030), 9728, 9)])
+@pytest.mark.parametrize("Ns,K,M", [((2560,), 4096, 16), ((77, 1030), 9728, 9), ((2560,), 9728, 16),
+                                    ((2560,), 9728, 4), ((1000, 40), 2000, 5), ((65, 130), 700, 12),
+                                    ((300,), 16384, 10), ((4100,), 2560, 16), ((33,), 1800, 3)])
 def test_hvsq2_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
-    """accumulate = 1: outputs += the product (the decoder's residual adds)."""
+    """accumulate = 1: outputs += the product (the decoder's residual adds,
+    the prior outputs loaded ahead of the products): the o and down shapes
+    at 4 and 16 tokens, ragged rows and partial blocks, 3..16 tokens, and K
+    beyond what one workgroup stages in LDS."""
     run_mfma_group(gpu_ctx, oracle_lib, "hvsq2", Ns, K, M, seed=sum(Ns) + K + M + 1, accumulate=True)
 
 
@@ -433,7 +439,7 @@ def hvsq2_block_products(w, sum_q, N, K):
 
 
 @pytest.mark.parametrize("kind,N,K,M", [("hvsq2", 300, 2560, 16), ("hvsq2", 77, 4096, 9), ("hvsq2", 40, 700, 12),
-                                        ("hvsq2", 300, 2560, 3), ("hvsq2", 77, 9728, 4),
+                                        ("hvsq2", 300, 2560, 3), ("hvsq2", 77, 9728, 4), ("hvsq2", 40, 16640, 6),
                                         ("q4_0", 200, 1536, 16), ("q4_0", 1536, 8960, 16), ("q4_0", 33, 100, 11)])
 def test_mfma_int32_block_dots(gpu_ctx, oracle_lib, kind, N, K, M):
     """The MFMA GEMM's per-block int32 dots, dumped by the same kernel (same
