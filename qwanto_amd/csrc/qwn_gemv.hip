@@ -1319,6 +1319,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     const uint32_t t0 = r0 >> a.rows_per_wave_log2;
     uint32_t meta_lds = 0, ppieces = 0, mpieces = 0;
     HvImage<NB> him;
+    uint2 Bx[NB], By[NB];
     if constexpr (STAGE) {
         const uint32_t ntile = min((16u * RT) >> a.rows_per_wave_log2, tiles - t0);
         if constexpr (KIND == kQ4_0) {
@@ -1327,46 +1328,61 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             // row-major layout (q4_pay_stride): LDS piece p of the copy is
             // (row p / stride, block p % stride); the lane order fixes the
             // destination, so each lane computes its piece's source in the
-            // wave-tile layout.  Padding pieces and rows past the tensor's
-            // tiles copy the tile start (never read, or read with scale 0).
-            const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+            // wave-tile layout, in 32-bit arithmetic, its (row, block)
+            // advanced by the workgroup's width each step (one division up
+            // front).  A padding piece copies its row's last block again
+            // (same cache line); rows past the tensor's tiles copy the tile
+            // start (read with scale 0).
+            const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2, step = blockDim.x;
+            const uint32_t tp = static_cast<uint32_t>(a.tile_payload_bytes);
+            const uint32_t tm = static_cast<uint32_t>(a.tile_meta_bytes);
             ppieces = q4_pay_stride(a.units);
             mpieces = q4_meta_stride(a.units);
             meta_lds = 16 * 16 * ppieces;
-            auto unit_at = [&](uint32_t rr, uint32_t u, uint32_t &tile_off, uint32_t &slot, uint32_t &n,
-                               uint32_t &pos) {
-                const uint32_t tl = rr >> a.rows_per_wave_log2, grp = rr & (R - 1);
-                slot = u >> a.lanes_log2;
-                n = min(L, a.units - slot * L);
-                tile_off = tl;
-                pos = grp * n + (u & (L - 1));
-            };
-            for (uint32_t c0 = wave * kWaveSize; c0 < 16 * ppieces; c0 += blockDim.x) {
-                const uint32_t pc = c0 + lane, rr = pc / ppieces, b = pc - rr * ppieces;
-                size_t src = 0;
-                if (rr < 16 && b < 4 * a.units) {
-                    uint32_t tl, slot, n, pos;
-                    unit_at(rr, b >> 2, tl, slot, n, pos);
-                    if (tl < ntile)
-                        src = static_cast<size_t>(tl) * a.tile_payload_bytes + static_cast<size_t>(64) * R * L * slot +
-                              16 * ((b & 3) * R * n + pos);
+            {
+                const uint32_t dq = step / ppieces, dr = step - dq * ppieces;
+                uint32_t pc = wave * kWaveSize + lane, rr = pc / ppieces, b = pc - rr * ppieces;
+                for (uint32_t c0 = wave * kWaveSize; c0 < 16 * ppieces; c0 += step) {
+                    const uint32_t tl = rr >> a.rows_per_wave_log2, bb = min(b, 4 * a.units - 1);
+                    const uint32_t u = bb >> 2, slot = u >> a.lanes_log2, n = min(L, a.units - slot * L);
+                    const uint32_t src =
+                        tl < ntile ? tl * tp + 64 * R * L * slot + 16 * (((bb & 3) * R + (rr & (R - 1))) * n + (u & (L - 1)))
+                                   : 0u;
+                    if (pc < 16 * ppieces)
+                        __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
+                    pc += step;
+                    b += dr;
+                    rr += dq;
+                    if (b >= ppieces) {
+                        b -= ppieces;
+                        ++rr;
+                    }
                 }
-                if (pc < 16 * ppieces)
-                    __builtin_amdgcn_global_load_lds(psrc + src, (lds_void *)(smem + c0 * 16), 16, 0, 0);
             }
-            for (uint32_t c0 = wave * kWaveSize; c0 < 16 * mpieces; c0 += blockDim.x) {
-                const uint32_t dw = c0 + lane, rr = dw / mpieces, w = dw - rr * mpieces;
-                size_t src = 0;
-                if (rr < 16 && (w >> 1) < a.units) {
-                    uint32_t tl, slot, n, pos;
-                    unit_at(rr, w >> 1, tl, slot, n, pos);
-                    if (tl < ntile)
-                        src = static_cast<size_t>(tl) * a.tile_meta_bytes + static_cast<size_t>(8) * R * L * slot +
-                              8 * pos + 4 * (w & 1);
+            {
+                const uint32_t dq = step / mpieces, dr = step - dq * mpieces;
+                uint32_t dw = wave * kWaveSize + lane, rr = dw / mpieces, w = dw - rr * mpieces;
+                for (uint32_t c0 = wave * kWaveSize; c0 < 16 * mpieces; c0 += step) {
+                    const uint32_t tl = rr >> a.rows_per_wave_log2, u = min(w >> 1, a.units - 1);
+                    const uint32_t slot = u >> a.lanes_log2, n = min(L, a.units - slot * L);
+                    const uint32_t src =
+                        tl < ntile ? tl * tm + 8 * R * L * slot + 8 * ((rr & (R - 1)) * n + (u & (L - 1))) + 4 * (w & 1)
+                                   : 0u;
+                    if (dw < 16 * mpieces)
+                        __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0 * 4), 4, 0, 0);
+                    dw += step;
+                    w += dr;
+                    rr += dq;
+                    if (w >= mpieces) {
+                        w -= mpieces;
+                        ++rr;
+                    }
                 }
-                if (dw < 16 * mpieces)
-                    __builtin_amdgcn_global_load_lds(msrc + src, (lds_void *)(smem + meta_lds + c0 * 4), 4, 0, 0);
             }
+            // the first chunk's image words go out behind the copies
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_sched_barrier(0);
+            q4_image_loads<NB>(a, kb0, kb1, lane, Bx);
         } else {
             static_assert(RT == 1, "the staged HyperVSQ-2 group is 16 rows");
             const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
@@ -1388,8 +1404,9 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             __builtin_amdgcn_sched_barrier(0);
             if (kb0 < kb1) hv_image_loads<NB>(a, kb0, min(static_cast<uint32_t>(NB), kb1 - kb0), lane, him);
         }
-        // this wave's copies landed (HyperVSQ-2: all but its image loads)
-        if (KIND == kHvsq2 && kb0 < kb1) wait_vmcnt<5 * NB>();
+        // this wave's copies landed (all but its first image loads, which
+        // retire after them)
+        if (kb0 < kb1) wait_vmcnt<KIND == kHvsq2 ? 5 * NB : NB>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();  // ... and every wave's
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -1414,10 +1431,9 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                                      acc);
     } else if constexpr (STAGE) {
         // the weights are in LDS: each chunk's image words are loaded one
-        // chunk ahead (two register sets used in turn), so a chunk's
-        // products run while the next chunk's image is on its way
-        uint2 Bx[NB], By[NB];
-        q4_image_loads<NB>(a, kb0, kb1, lane, Bx);
+        // chunk ahead (two register sets used in turn, the first chunk's
+        // behind the staging copies), so a chunk's products run while the
+        // next chunk's image is on its way
         for (uint32_t b0 = kb0; b0 < kb1; b0 += 2 * NB) {
             const uint32_t b1 = b0 + NB;
             q4_image_loads<NB>(a, b1, kb1, lane, By);
@@ -1431,7 +1447,6 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                                                By, acc);
         }
     } else {
-        uint2 Bx[NB];
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
             q4_image_loads<NB>(a, b0, kb1, lane, Bx);
             mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
