@@ -56,6 +56,8 @@ def parse():
     p.add_argument("--profile", choices=("gate-up", "decode", "decode-4b", "drop-in", "attention", "batch", "upload",
                                         "copy"),
                    help="profiling mode: run only one workload (for rocprofv3)")
+    p.add_argument("--batch-m", default="1,2,4,8,16",
+                   help="token counts of the batch sweep (comma-separated, each 1..16)")
     return p.parse_args()
 
 
@@ -440,7 +442,7 @@ def upload_bench(ctx, layers=36, seed=3):
             "per_tensor_gbps": round(total / t_single / 1e9, 2), "per_tensor_s": round(t_single, 3)}
 
 
-def batch_sweep(torch, ctx, steps, warmup):
+def batch_sweep(torch, ctx, steps, warmup, ms_list=(1, 2, 4, 8, 16)):
     """GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers (weights
     read once per launch): HyperVSQ-2 on the Qwen3-4B shapes (36 layers per
     token in tokens_per_s), and under "q4_0" Q4_0 on the Qwen2-1.5B shapes
@@ -451,7 +453,7 @@ def batch_sweep(torch, ctx, steps, warmup):
 
     def sweep(kind, shapes, model_layers, seed0):
         res = {}
-        for M in (1, 2, 4, 8, 16):
+        for M in ms_list:
             mfma = M >= (6 if kind == "q4_0" else 3)     # the library's own choice (mfma_batch)
             if not mfma:
                 sw = Sweep(torch, ctx, kind, shapes, 4, seed=seed0 + M, batch=M)
@@ -593,7 +595,10 @@ def main():
         print(json.dumps({"profile_mode": "upload", **upload_bench(ctx)}), flush=True)
         return
     if args.profile == "batch":
-        print(json.dumps({"profile_mode": "batch", **batch_sweep(torch, ctx, args.steps, args.warmup)}),
+        ms_list = tuple(int(m) for m in args.batch_m.split(","))
+        if not ms_list or any(m < 1 or m > 16 for m in ms_list):
+            sys.exit("--batch-m: token counts between 1 and 16")
+        print(json.dumps({"profile_mode": "batch", **batch_sweep(torch, ctx, args.steps, args.warmup, ms_list)}),
               flush=True)
         return
     t_setup = time.perf_counter()
