@@ -268,13 +268,19 @@ def host_decode_bench(model, prompt, new_tokens=128):
 
 def cpu_host_info() -> dict:
     """CPU model and the GPU-local NUMA node's physical cores on this host."""
-    info = {"cpu_model": None, "numa_node": None, "node_physical_cores": None}
+    info = {"cpu_model": None, "cpu_family": None, "hypervisor": False, "numa_node": None,
+            "node_physical_cores": None}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                info["cpu_model"] = line.split(":", 1)[1].strip()
-                break
-    except OSError:
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and info["cpu_model"] is None:
+                info["cpu_model"] = val
+            elif key == "cpu family" and info["cpu_family"] is None:
+                info["cpu_family"] = int(val)
+            elif key == "flags" and not info["hypervisor"]:
+                info["hypervisor"] = "hypervisor" in val.split()
+    except (OSError, ValueError):
         pass
     cpus = gpu_local_cpus()
     if cpus is not None:
@@ -286,14 +292,18 @@ def cpu_host_info() -> dict:
 
 def gpu_local_cpus():
     """(NUMA node of GPU 0, the CPUs of that node this process may use), or
-    None where the node is unknown."""
+    None where the node is unknown.  A device that reports no node (-1, as
+    under a hypervisor) on a host with a single NUMA node is local to it."""
     try:
         import torch
         p = torch.cuda.get_device_properties(0)
         bus = "%04x:%02x:%02x.0" % (getattr(p, "pci_domain_id", 0), p.pci_bus_id, p.pci_device_id)
         node = int(open(f"/sys/bus/pci/devices/{bus}/numa_node").read())
         if node < 0:
-            return None
+            nodes = [n for n in os.listdir("/sys/devices/system/node") if n.startswith("node") and n[4:].isdigit()]
+            if len(nodes) != 1:
+                return None
+            node = int(nodes[0][4:])
         allowed = os.sched_getaffinity(0)
         cpus = set()
         for part in open(f"/sys/devices/system/node/node{node}/cpulist").read().strip().split(","):
