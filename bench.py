@@ -61,28 +61,35 @@ def parse():
     return p.parse_args()
 
 
+def upload_layers(ctx, dtype, shapes, layers, seed) -> list:
+    """`layers` layers of resident seeded tensors ({projection: handle})."""
+    import numpy as np
+
+    from qwanto_amd import synth
+    rng = np.random.default_rng(seed)
+    return [{p: ctx.upload(synth.weights(dtype, rng, *shapes[p]), dtype, *shapes[p]) for p in synth.PROJECTIONS}
+            for _ in range(layers)]
+
+
 class Sweep:
     """Resident weights, activation images and outputs of a GEMV sweep over
-    `layers` layers of one model shape."""
+    `layers` layers of one model shape (`weights`: layers uploaded by the
+    caller, who releases them)."""
 
-    def __init__(self, torch, ctx, dtype, shapes, layers, seed, batch=1):
-        import numpy as np
-
+    def __init__(self, torch, ctx, dtype, shapes, layers, seed, batch=1, weights=None):
         from qwanto_amd import synth
         self.torch, self.ctx, self.dtype, self.batch = torch, ctx, dtype, batch
-        rng = np.random.default_rng(seed)
         torch.manual_seed(seed)
         dev = torch.device("cuda:0")
+        self.owned = weights is None
+        if weights is None:
+            weights = upload_layers(ctx, dtype, shapes, layers, seed)
         self.layers = []
         self.weight_bytes = 0
         self.shapes = shapes
-        for _ in range(layers):
-            layer = {}
-            for proj in synth.PROJECTIONS:
-                N, K = shapes[proj]
-                w = synth.weights(dtype, rng, N, K)
-                layer[proj] = ctx.upload(w, dtype, N, K)
-                self.weight_bytes += synth.weight_bytes(dtype, N, K)
+        for handles in weights:
+            layer = dict(handles)
+            self.weight_bytes += sum(synth.weight_bytes(dtype, *shapes[p]) for p in synth.PROJECTIONS)
             # one image per distinct input: qkv (hidden), o (attention), gu (hidden), down (ffn)
             imgs = {}
             for key, proj in (("qkv", "q"), ("o", "o"), ("gu", "gate"), ("down", "down")):
@@ -135,11 +142,12 @@ class Sweep:
         return sum(synth.weight_bytes(self.dtype, *self.shapes[p]) for p in projs)
 
     def close(self):
-        """Release the resident tensors (the ABI holds at most 512)."""
+        """Release the resident tensors it uploaded (the ABI holds at most 512)."""
         from qwanto_amd import synth
-        for layer in self.layers:
-            for proj in synth.PROJECTIONS:
-                self.ctx.release(layer[proj])
+        if self.owned:
+            for layer in self.layers:
+                for proj in synth.PROJECTIONS:
+                    self.ctx.release(layer[proj])
         self.layers = []
         self._requests = []
 
@@ -375,21 +383,21 @@ class MfmaSweep:
     decoder groups its GEMVs (q/k/v, o, gate/up, down: four per layer; o and
     down accumulate into their outputs, the residual adds)."""
 
-    def __init__(self, torch, ctx, shapes, layers, seed, batch, kind="hvsq2"):
-        import numpy as np
-
+    def __init__(self, torch, ctx, shapes, layers, seed, batch, kind="hvsq2", weights=None):
         from qwanto_amd import synth
         self.ctx, self.batch, self.shapes = ctx, batch, shapes
-        rng = np.random.default_rng(seed)
         torch.manual_seed(seed)
         dev = torch.device("cuda:0")
         s = torch.cuda.current_stream().cuda_stream
         self.items, self.handles = [], []
         self.weight_bytes = 0
-        for _ in range(layers):
-            layer = {p: ctx.upload(synth.weights(kind, rng, *shapes[p]), kind, *shapes[p])
-                     for p in synth.PROJECTIONS}
-            self.handles += list(layer.values())
+        owned = weights is None
+        if weights is None:
+            weights = upload_layers(ctx, kind, shapes, layers, seed)
+        layers = len(weights)
+        for layer in weights:
+            if owned:
+                self.handles += list(layer.values())
             for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")),
                                ("down", ("down",))):
                 h0 = layer[projs[0]]
@@ -453,39 +461,50 @@ def upload_bench(ctx, layers=36, seed=3):
 
 
 def batch_sweep(torch, ctx, steps, warmup, ms_list=(1, 2, 4, 8, 16)):
-    """GEMM at M = 1, 2, 4, 8, 16 tokens per launch over 4 layers (weights
-    read once per launch): HyperVSQ-2 on the Qwen3-4B shapes (36 layers per
-    token in tokens_per_s), and under "q4_0" Q4_0 on the Qwen2-1.5B shapes
-    (28 layers); dot8 grouped launches below 3 tokens (Q4_0: 6), grouped
-    int8-MFMA launches from there (MFMA utilisation = useful int8 ops /
-    dense int8 peak)."""
+    """GEMM at M = 1, 2, 4, 8, 16 tokens per launch (weights read once per
+    launch), rotating through at least 1 GB of distinct layers so every
+    launch reads its weights from HBM (beyond the 256 MB infinity cache):
+    HyperVSQ-2 on 36 layers of the Qwen3-4B shapes (1.05 GB; 36 layers per
+    token in tokens_per_s), and under "q4_0" Q4_0 on 40 layers of the
+    Qwen2-1.5B shapes (1.05 GB; 28 layers per token); dot8 grouped launches
+    below 3 tokens (Q4_0: 6), grouped int8-MFMA launches from there (MFMA
+    utilisation = useful int8 ops / dense int8 peak).  One set of weights
+    per kind serves every M."""
     from qwanto_amd import synth
 
-    def sweep(kind, shapes, model_layers, seed0):
+    def sweep(kind, shapes, layers, model_layers, seed0):
         res = {}
-        for M in ms_list:
-            mfma = M >= (6 if kind == "q4_0" else 3)     # the library's own choice (mfma_batch)
-            if not mfma:
-                sw = Sweep(torch, ctx, kind, shapes, 4, seed=seed0 + M, batch=M)
-                ms = time_graph(torch, sw.grouped, steps, warmup)
-                path = "dot8"
-                flops = 2 * M * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * 4
-            else:
-                sw = MfmaSweep(torch, ctx, shapes, 4, seed=seed0 + M, batch=M, kind=kind)
-                ms = time_graph(torch, sw.run, steps, warmup)
-                path = "mfma-i8"
-                flops = sw.flops
-            tops = flops / (ms / 1e3) / 1e12
-            res[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
-                           "us_per_layer": round(ms * 1e3 / 4, 3),
-                           "tokens_per_s": round(M * 4 / (ms / 1e3) / model_layers, 1),
-                           "path": path, "int8_tops": round(tops, 2),
-                           "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5) if mfma else None}
-            sw.close()
+        weights = upload_layers(ctx, kind, shapes, layers, seed0)
+        try:
+            for M in ms_list:
+                mfma = M >= (6 if kind == "q4_0" else 3)     # the library's own choice (mfma_batch)
+                if not mfma:
+                    sw = Sweep(torch, ctx, kind, shapes, layers, seed=seed0 + M, batch=M, weights=weights)
+                    ms = time_graph(torch, sw.grouped, steps, warmup)
+                    path = "dot8"
+                    flops = 2 * M * sum(shapes[p][0] * shapes[p][1] for p in synth.PROJECTIONS) * layers
+                else:
+                    sw = MfmaSweep(torch, ctx, shapes, layers, seed=seed0 + M, batch=M, kind=kind,
+                                   weights=weights)
+                    ms = time_graph(torch, sw.run, steps, warmup)
+                    path = "mfma-i8"
+                    flops = sw.flops
+                tops = flops / (ms / 1e3) / 1e12
+                res[str(M)] = {"gbps": round(sw.weight_bytes / (ms / 1e3) / 1e9, 1),
+                               "us_per_layer": round(ms * 1e3 / layers, 3),
+                               "tokens_per_s": round(M * layers / (ms / 1e3) / model_layers, 1),
+                               "path": path, "int8_tops": round(tops, 2),
+                               "mfma_util": round(tops / INT8_MFMA_PEAK_TOPS, 5) if mfma else None}
+                sw.close()
+        finally:
+            for layer in weights:
+                for h in layer.values():
+                    ctx.release(h)
+        res["layers"] = layers
         return res
 
-    out = sweep("hvsq2", synth.QWEN3_4B_SHAPES, 36, 50)
-    out["q4_0"] = sweep("q4_0", synth.QWEN2_1P5B_SHAPES, 28, 70)
+    out = sweep("hvsq2", synth.QWEN3_4B_SHAPES, 36, 36, 50)
+    out["q4_0"] = sweep("q4_0", synth.QWEN2_1P5B_SHAPES, 40, 28, 70)
     return out
 
 
