@@ -666,18 +666,24 @@ def main():
     sweep.close()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     if not args.no_extras:
-        q4 = Sweep(torch, ctx, "q4_0", synth.QWEN2_1P5B_SHAPES, 28, seed=2)
+        # 40 distinct Qwen2-1.5B-shaped layers (1.05 GB) in decode order
+        q4_layers = 40
+        q4 = Sweep(torch, ctx, "q4_0", synth.QWEN2_1P5B_SHAPES, q4_layers, seed=2)
         ms_q4 = time_graph(torch, q4.grouped, args.steps, args.warmup)
         # per-layer GEMV rate of the decode workload's projections (graph of
-        # the 28 launches of one kind / 28)
+        # one kind's launches over every layer / layers); a kind's working
+        # set is recorded with it: the smaller kinds' weights (q/k/v, o) fit
+        # in the 256 MB infinity cache when replayed alone
         q4_launch = {}
         for key, projs in (("qkv", ("q", "k", "v")), ("o", ("o",)), ("gu", ("gate", "up")), ("down", ("down",))):
-            ms = time_graph(torch, lambda st, k=key: q4.grouped(st, only=k), args.steps, args.warmup) / 28
+            ms = time_graph(torch, lambda st, k=key: q4.grouped(st, only=k), args.steps, args.warmup) / q4_layers
             b = q4.bytes_of(projs)
-            q4_launch[key] = {"us": round(ms * 1e3, 3), "bytes": b, "gbps": round(b / (ms / 1e3) / 1e9, 1)}
+            q4_launch[key] = {"us": round(ms * 1e3, 3), "bytes": b, "gbps": round(b / (ms / 1e3) / 1e9, 1),
+                              "working_set_bytes": b * q4_layers}
         extra["q4_0_sweep_qwen2_1p5b"] = {
             "gbps": round(q4.weight_bytes / (ms_q4 / 1e3) / 1e9, 1), "ms_per_step": round(ms_q4, 4),
-            "weight_bytes": q4.weight_bytes, "launches_per_step": 4 * 28, "per_layer_launch": q4_launch}
+            "weight_bytes": q4.weight_bytes, "layers": q4_layers, "launches_per_step": 4 * q4_layers,
+            "per_layer_launch": q4_launch}
         q4.close()
         if not args.no_decode:
             model, prompt = decode_model(prompt_len=args.decode_prompt)
