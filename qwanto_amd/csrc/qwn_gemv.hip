@@ -924,19 +924,18 @@ struct MfmaArgs {
 constexpr int kMfmaMaxWaves = 8;
 constexpr int kMfmaSplitMaxWaves = 16;  // the Q4_0 K-split kernel
 
-// Byte offsets of (row, unit, chunk g) in the wave-tile layout, relative to
-// the first tile `t0`:
-//   payload (tile - t0) * tile_payload + 64*R*L*slot + (g*R*n + grp*n + jj) * 16
-//   meta    (tile - t0) * tile_meta    +  8*R*L*slot + (grp*n + jj) * 8
+// Byte offsets of (row, unit, chunk g) in the wave-tile layout:
+//   payload tile * tile_payload + 64*R*L*slot + (g*R*n + grp*n + jj) * 16
+//   meta    tile * tile_meta    +  8*R*L*slot + (grp*n + jj) * 8
 // with slot = unit / L, jj = unit % L, n = units in the slot.
 struct MfmaUnit {
     size_t payload, meta;
 };
-__device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, uint32_t t0, uint32_t b, uint32_t g) {
+__device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, uint32_t b, uint32_t g) {
     const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
     const uint32_t slot = b >> a.lanes_log2, jj = b & (L - 1);
     const uint32_t n = min(L, a.units - slot * L);
-    const uint32_t tile = (row >> a.rows_per_wave_log2) - t0, grp = row & (R - 1);
+    const uint32_t tile = row >> a.rows_per_wave_log2, grp = row & (R - 1);
     MfmaUnit u;
     u.payload = tile * a.tile_payload_bytes + static_cast<size_t>(64) * R * L * slot +
                 (static_cast<size_t>(g) * R * n + grp * n + jj) * 16;
@@ -965,7 +964,7 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const uint32_t row = r0 + 16 * t + m;
-            const MfmaUnit u = mfma_unit(a, row < rows ? row : 0, 0, b, g);
+            const MfmaUnit u = mfma_unit(a, row < rows ? row : 0, b, g);
             A[i][t] = *reinterpret_cast<const uint4 *>(payload + u.payload);
             Mt[i][t] = *reinterpret_cast<const uint2 *>(meta + u.meta);
         }
@@ -1208,7 +1207,7 @@ __device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, uint32_t b0, u
 // `mpieces` its payload and meta strides.
 template <int NB, int RT, bool STAGE, bool DUMP>
 __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
-                                              const uint8_t *lds, uint32_t meta_lds, uint32_t t0, uint32_t rows,
+                                              const uint8_t *lds, uint32_t meta_lds, uint32_t rows,
                                               uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
                                               uint32_t ppieces, uint32_t mpieces, const uint2 (&B)[NB],
                                               float (&acc)[RT][4]) {
@@ -1222,7 +1221,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
             const uint32_t row = r0 + 16 * t + m;
-            const MfmaUnit u = STAGE ? MfmaUnit{} : mfma_unit(a, row < rows ? row : 0u, 0u, b >> 2, b & 3);
+            const MfmaUnit u = STAGE ? MfmaUnit{} : mfma_unit(a, row < rows ? row : 0u, b >> 2, b & 3);
             if constexpr (STAGE) {
                 // row 16t + m of the staged group (rows past the tensor read
                 // the group's row 0 and get scale 0)
@@ -1437,19 +1436,19 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         for (uint32_t b0 = kb0; b0 < kb1; b0 += 2 * NB) {
             const uint32_t b1 = b0 + NB;
             q4_image_loads<NB>(a, b1, kb1, lane, By);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b0,
                                                min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
                                                Bx, acc);
             if (b1 >= kb1) break;
             q4_image_loads<NB>(a, b1 + NB, kb1, lane, Bx);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b1,
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b1,
                                                min(static_cast<uint32_t>(NB), kb1 - b1), lane, ppieces, mpieces,
                                                By, acc);
         }
     } else {
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
             q4_image_loads<NB>(a, b0, kb1, lane, Bx);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, t0, rows, r0, b0,
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b0,
                                                min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
                                                Bx, acc);
         }
