@@ -53,6 +53,7 @@ struct DeviceBuffer {
 struct ResidentTensor {
     DeviceTensor t;
     void *allocation = nullptr;
+    void *mfma_allocation = nullptr;  // the MFMA-order copy (HyperVSQ-2), if any
 };
 
 struct ResidentKv {

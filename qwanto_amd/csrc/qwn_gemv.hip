@@ -1533,6 +1533,170 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     }
 }
 
+// HyperVSQ-2 tensors with an MFMA-order copy: each wave loads its operands
+// straight from HBM (a unit's 16 rows x 4 chunks are one contiguous 1 KB,
+// lane (g, m) taking chunk g of row m; its meta one 128-byte span), so a
+// workgroup has no staging copy, no barrier before its products and no LDS
+// bank gaps; the products are mfma_chunk_hv's, the K-split sum and the
+// token-major epilogue mfma_gemm_kernel's.  payload[i] / meta[i] of the
+// arguments are the copies.
+template <int NB, bool DUMP>
+__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(MfmaArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lane = threadIdx.x % kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+    const uint32_t KS = 1u << a.ks_log2;
+    const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
+    uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
+    job = __builtin_amdgcn_readfirstlane(job);
+    const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
+    const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
+    float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
+    const uint32_t rows = job == 0 ? a.rows[0] : job == 1 ? a.rows[1] : job == 2 ? a.rows[2] : a.rows[3];
+    const uint32_t stride = job == 0   ? a.output_stride[0]
+                            : job == 1 ? a.output_stride[1]
+                            : job == 2 ? a.output_stride[2]
+                                       : a.output_stride[3];
+    const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
+    const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
+    const uint32_t rg = blockIdx.x - first, r0 = rg * 16;
+    const uint32_t g = lane >> 4, m = lane & 15;
+    const uint32_t kb0 = wave * a.nb, kb1 = min(a.nblk, kb0 + a.nb);
+    // the epilogue's token scales and prior outputs, loaded ahead
+    float xs_pre[4], res_pre[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+    if (a.accumulate && wave == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = 4 * g + r, row = r0 + m;
+            res_pre[r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+        }
+    }
+    const uint8_t *pbase = payload + (static_cast<size_t>(rg) * a.units) * 1024 + lane * 16;
+    const uint8_t *mbase = meta + (static_cast<size_t>(rg) * a.units) * 128 + m * 8;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    HvImage<NB> im;
+    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
+        const uint32_t nv = min(static_cast<uint32_t>(NB), kb1 - b0);
+        uint4 A[NB];
+        uint2 Mt[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t u = b0 + (static_cast<uint32_t>(i) < nv ? i : 0);
+            A[i] = *reinterpret_cast<const uint4 *>(pbase + static_cast<size_t>(u) * 1024);
+            Mt[i] = *reinterpret_cast<const uint2 *>(mbase + static_cast<size_t>(u) * 128);
+        }
+        hv_image_loads<NB>(a, b0, nv, lane, im);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (static_cast<uint32_t>(i) >= nv) break;
+            const uint32_t subs = (Mt[i].y >> (8 * g)) & 0xffu;
+            const uint32_t cw[4] = {A[i].x, A[i].y, A[i].z, A[i].w};
+            mfma_v4i ci = {0, 0, 0, 0};
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl) {
+                const uint32_t sub = (subs >> (4 * (sl >> 1))) & 15u;
+                // table bytes: code 0 -> -s, 1 -> 0, 2 -> s, 3 -> 2s
+                const uint32_t lut = ((0u - sub) & 0xffu) | (sub << 16) | ((2u * sub) << 24);
+                const uint32_t c = cw[sl];
+                mfma_v4i wv;
+                wv.x = static_cast<int>(__builtin_amdgcn_perm(0u, lut, c & 0x03030303u));
+                wv.y = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 2) & 0x03030303u));
+                wv.z = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 4) & 0x03030303u));
+                wv.w = static_cast<int>(__builtin_amdgcn_perm(0u, lut, (c >> 6) & 0x03030303u));
+                // C[token][row]: element r is token 4g + r of row m
+                ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(im.B[i][sl], wv, ci, 0, 0, 0);
+            }
+            if constexpr (DUMP) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t row = r0 + m, tok = 4 * g + r;
+                    if (row < rows && tok < a.ntok)
+                        a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
+                }
+            }
+            // rows past the matrix are zero in the copy: d = m = 0
+            const uint32_t dm = Mt[i].x;
+            const float dsc = half_to_float(dm & 0xffffu) * 0.125f;
+            const float msc = half_to_float(dm >> 16);
+            const float sa[4] = {im.SA[i].x, im.SA[i].y, im.SA[i].z, im.SA[i].w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), dsc, fmaf(msc, sa[r], acc[r]));
+        }
+    }
+    // the K-split partials, summed in wave order
+    if (KS > 1) {
+        float *part_s = reinterpret_cast<float *>(smem);
+        if (wave > 0) {
+            float *dst = part_s + ((wave - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r] = acc[r];
+        }
+        __syncthreads();
+        if (wave == 0)
+            for (uint32_t k = 1; k < KS; ++k) {
+                const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] += src[r];
+            }
+    }
+    // lane (g, m) holds tokens 4g .. 4g+3 of row m; accumulate: out += the
+    // rounded product, in two roundings as the dot8 epilogue
+    const uint32_t row = r0 + m;
+    if (wave == 0 && row < rows) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = 4 * g + r;
+            if (tok >= a.ntok) continue;
+            float v = mul_rounded(acc[r], xs_pre[r]);
+            if (bias) v = add_rounded(v, bias[row]);
+            output[static_cast<size_t>(tok) * stride + row] = a.accumulate ? add_rounded(res_pre[r], v) : v;
+        }
+    }
+}
+
+// The MFMA-order copy of a HyperVSQ-2 tensor from its wave-tile layout: one
+// thread per 16-byte payload piece and per 8-byte meta entry of the copy.
+struct MfmaCopyArgs {
+    const uint8_t *payload, *meta;
+    uint8_t *dst_payload, *dst_meta;
+    size_t tile_payload, tile_meta;
+    uint32_t units, lanes_log2, rows_per_wave_log2, tiles, groups;
+};
+
+__global__ __launch_bounds__(256) void mfma_copy_kernel(MfmaCopyArgs a) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
+    const size_t npay = static_cast<size_t>(a.groups) * a.units * 64;
+    if (idx < npay) {
+        const uint32_t piece = static_cast<uint32_t>(idx % 64), gu = static_cast<uint32_t>(idx / 64);
+        const uint32_t rg = gu / a.units, u = gu - rg * a.units, g = piece >> 4, row = rg * 16 + (piece & 15);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if ((row >> a.rows_per_wave_log2) < a.tiles) {
+            const uint32_t tile = row >> a.rows_per_wave_log2, grp = row & (R - 1);
+            const uint32_t slot = u >> a.lanes_log2, n = min(L, a.units - slot * L);
+            v = *reinterpret_cast<const uint4 *>(a.payload + tile * a.tile_payload + static_cast<size_t>(64) * R * L * slot +
+                                                 16 * (static_cast<size_t>(g) * R * n + grp * n + (u & (L - 1))));
+        }
+        reinterpret_cast<uint4 *>(a.dst_payload)[idx] = v;
+    }
+    const size_t nmeta = static_cast<size_t>(a.groups) * a.units * 16;
+    if (idx < nmeta) {
+        const uint32_t gu = static_cast<uint32_t>(idx / 16), rg = gu / a.units, u = gu - rg * a.units;
+        const uint32_t row = rg * 16 + static_cast<uint32_t>(idx % 16);
+        uint2 v = make_uint2(0, 0);
+        if ((row >> a.rows_per_wave_log2) < a.tiles) {
+            const uint32_t tile = row >> a.rows_per_wave_log2, grp = row & (R - 1);
+            const uint32_t slot = u >> a.lanes_log2, n = min(L, a.units - slot * L);
+            v = *reinterpret_cast<const uint2 *>(a.meta + tile * a.tile_meta + static_cast<size_t>(8) * R * L * slot +
+                                                 8 * (static_cast<size_t>(grp) * n + (u & (L - 1))));
+        }
+        reinterpret_cast<uint2 *>(a.dst_meta)[idx] = v;
+    }
+}
+
 // Q4_0 launches of few row groups in accumulate mode (the residual adds of
 // the o and down projections: 96-160 row groups leave most of the 256 CUs
 // idle, and a CU's vector ALU bounds the per-block work): each row group is
@@ -2320,6 +2484,31 @@ hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, h
 
 }  // namespace
 
+size_t mfma_copy_bytes(const DeviceTensor &t) {
+    if (t.kind != kHvsq2) return 0;
+    const size_t groups = (t.rows + 15) / 16;
+    return groups * t.units * 1024 + groups * t.units * 128;
+}
+
+hipError_t launch_mfma_copy(const DeviceTensor &t, hipStream_t stream) {
+    if (t.kind != kHvsq2 || !t.mfma_payload || !t.mfma_meta || !t.payload || !t.meta) return hipErrorInvalidValue;
+    MfmaCopyArgs c{};
+    c.payload = t.payload;
+    c.meta = t.meta;
+    c.dst_payload = t.mfma_payload;
+    c.dst_meta = t.mfma_meta;
+    c.tile_payload = t.tile_payload_bytes;
+    c.tile_meta = t.tile_meta_bytes;
+    c.units = t.units;
+    c.lanes_log2 = static_cast<uint32_t>(__builtin_ctz(t.lanes));
+    c.rows_per_wave_log2 = static_cast<uint32_t>(__builtin_ctz(t.rows_per_wave));
+    c.tiles = t.tiles;
+    c.groups = (t.rows + 15) / 16;
+    const size_t n = static_cast<size_t>(c.groups) * t.units * 64;
+    hipLaunchKernelGGL(mfma_copy_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, c);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate,
@@ -2339,6 +2528,9 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         total_rows += t.rows;
     }
     MfmaPlan p = mfma_plan(t0, total_rows);
+    // HyperVSQ-2 tensors that all carry the MFMA-order copy: direct loads
+    bool direct = t0.kind == kHvsq2;
+    for (uint32_t i = 0; i < count; ++i) direct = direct && tensors[i]->mfma_payload && tensors[i]->mfma_meta;
     // residual adds over few row groups: the four-way K split
     const uint64_t groups = (total_rows + 15) / 16;
     const bool split = t0.kind == kQ4_0 && accumulate && !dump && p.stage && groups < 256;
@@ -2361,8 +2553,8 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         a.job_block[i] = grid;
         if (i < count) {
             const DeviceTensor &t = *tensors[i];
-            a.payload[i] = t.payload;
-            a.meta[i] = t.meta;
+            a.payload[i] = direct ? t.mfma_payload : t.payload;
+            a.meta[i] = direct ? t.mfma_meta : t.meta;
             a.output[i] = outputs[i];
             a.rows[i] = t.rows;
             a.tiles[i] = t.tiles;
@@ -2371,7 +2563,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0 &&
                 (reinterpret_cast<uintptr_t>(a.bias[i]) & 15u) == 0)
                 a.vec_out |= 1u << i;
-            grid += split ? 4 * ((t.rows + 15) / 16) : (t.rows + 16 * p.rt - 1) / (16 * p.rt);
+            grid += split ? 4 * ((t.rows + 15) / 16) : direct ? (t.rows + 15) / 16 : (t.rows + 16 * p.rt - 1) / (16 * p.rt);
         }
     }
     a.job_block[kMaxGroup] = grid;
@@ -2391,6 +2583,34 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.dump = dump;
     a.pad_p = t0.stage_pad_p;
     a.pad_m = t0.stage_pad_m;
+    if (direct) {
+        // the fewest waves that keep a wave's units within one unrolled chunk
+        // of 5 (a wave's loads all in flight at once)
+        auto per_wave = [&](uint32_t ks) { return (t0.units + (1u << ks) - 1) >> ks; };
+        p.ks_log2 = 0;
+        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
+        p.nb = per_wave(p.ks_log2);
+        p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
+        p.waves = 1u << p.ks_log2;
+        a.ks_log2 = p.ks_log2;
+        a.nb = p.nb;
+        const uint32_t threads = p.waves * kWaveSize;
+        const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
+        if (dump) {
+            switch (p.nbt) {
+            case 2: hipLaunchKernelGGL((mfma_direct_kernel<2, true>), dim3(grid), dim3(threads), lds, stream, a); break;
+            case 3: hipLaunchKernelGGL((mfma_direct_kernel<3, true>), dim3(grid), dim3(threads), lds, stream, a); break;
+            default: hipLaunchKernelGGL((mfma_direct_kernel<5, true>), dim3(grid), dim3(threads), lds, stream, a); break;
+            }
+        } else {
+            switch (p.nbt) {
+            case 2: hipLaunchKernelGGL((mfma_direct_kernel<2, false>), dim3(grid), dim3(threads), lds, stream, a); break;
+            case 3: hipLaunchKernelGGL((mfma_direct_kernel<3, false>), dim3(grid), dim3(threads), lds, stream, a); break;
+            default: hipLaunchKernelGGL((mfma_direct_kernel<5, false>), dim3(grid), dim3(threads), lds, stream, a); break;
+            }
+        }
+        return hipGetLastError();
+    }
     if (split) {
         const uint32_t threads = p.waves * kWaveSize;
         switch (p.nbt) {

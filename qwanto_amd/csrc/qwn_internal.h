@@ -77,7 +77,18 @@ struct DeviceTensor {
     // payload and meta copies in LDS, chosen for the tile shape
     uint32_t stage_pad_p = 0;
     uint32_t stage_pad_m = 0;
+    // HyperVSQ-2: optional second copy in the MFMA GEMM's operand order,
+    // payload [16-row group][unit][chunk g][row m][16 B], meta [16-row
+    // group][unit][row m][8 B] (rows past the matrix zero); null if absent
+    uint8_t *mfma_payload = nullptr;
+    uint8_t *mfma_meta = nullptr;
 };
+
+// Bytes of a HyperVSQ-2 tensor's MFMA-order copy (0 for other kinds).
+size_t mfma_copy_bytes(const DeviceTensor &t);
+// Fills t.mfma_payload / t.mfma_meta (a block of mfma_copy_bytes at
+// mfma_payload) from the wave-tile layout, on `stream` after its upload.
+hipError_t launch_mfma_copy(const DeviceTensor &t, hipStream_t stream);
 
 // Launch shape of one GEMV call.
 struct GemvPlan {

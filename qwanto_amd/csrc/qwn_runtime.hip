@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -249,7 +250,29 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
 
 void free_tensor(ResidentTensor *rt) {
     if (rt->allocation) (void)hipFree(rt->allocation);
+    if (rt->mfma_allocation) (void)hipFree(rt->mfma_allocation);
     delete rt;
+}
+
+// The MFMA-order copy of a HyperVSQ-2 tensor (qwn::launch_mfma_copy), which
+// the batched GEMM reads directly instead of staging the wave tiles: made
+// where device memory has room for it with 1 GB to spare (it is not charged
+// to the context's budget, which counts the tensors' own bytes) and unless
+// QWN_HIP_MFMA_COPY=0; without it the GEMM stages the tiles.
+void attach_mfma_copy(ResidentTensor *rt) {
+    const size_t cb = qwn::mfma_copy_bytes(rt->t);
+    if (!cb) return;
+    const char *env = std::getenv("QWN_HIP_MFMA_COPY");
+    if (env && env[0] == '0') return;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess || free_b < cb + (1ull << 30)) return;
+    if (hipMalloc(&rt->mfma_allocation, cb) != hipSuccess) {
+        rt->mfma_allocation = nullptr;
+        return;
+    }
+    const size_t groups = (rt->t.rows + 15) / 16;
+    rt->t.mfma_payload = static_cast<uint8_t *>(rt->mfma_allocation);
+    rt->t.mfma_meta = rt->t.mfma_payload + groups * rt->t.units * 1024;
 }
 
 void free_cache(ResidentKv *rk) {
@@ -576,11 +599,17 @@ int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count,
         made.push_back(rt);
     }
     const auto t0 = std::chrono::steady_clock::now();
-    for (uint32_t i = 0; i < count; ++i)
+    for (uint32_t i = 0; i < count; ++i) {
         if ((e = enqueue_upload(ctx, made[i]->t, static_cast<const uint8_t *>(ups[i].host_data))) != hipSuccess) {
             (void)hip_fail("tensor upload", e);
             return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
         }
+        attach_mfma_copy(made[i]);
+        if (made[i]->t.mfma_payload && (e = qwn::launch_mfma_copy(made[i]->t, ctx->stream)) != hipSuccess) {
+            (void)hip_fail("MFMA-order copy", e);
+            return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
+        }
+    }
     if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
         (void)hip_fail("tensor upload", e);
         return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);

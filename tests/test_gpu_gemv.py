@@ -167,6 +167,75 @@ def test_hvsq2_mfma_group_accumulate(gpu_ctx, oracle_lib, Ns, K, M):
     run_mfma_group(gpu_ctx, oracle_lib, "hvsq2", Ns, K, M, seed=sum(Ns) + K + M + 1, accumulate=True)
 
 
+def mfma_group_outputs(ctx, kind, ws, Ns, K, q8, xs, accumulate, init):
+    """Outputs of one grouped MFMA launch over freshly uploaded tensors (so
+    the upload-time choice of the MFMA-order copy applies)."""
+    import torch
+    M = q8.shape[0]
+    hs = [ctx.upload(w, kind, N, K) for w, N in zip(ws, Ns)]
+    try:
+        dev = torch.device("cuda:0")
+        q8d = torch.from_numpy(q8).to(dev)
+        xsd = torch.from_numpy(xs).to(dev)
+        img = torch.zeros(ctx.mfma_image_bytes(hs[0]), dtype=torch.uint8, device=dev)
+        ys = [torch.from_numpy(i.copy()).to(dev) for i in init]
+        s = torch.cuda.current_stream().cuda_stream
+        ctx.mfma_image_device(hs[0], q8d.data_ptr(), M, q8.shape[1], img.data_ptr(), stream=s)
+        ctx.gemm_mfma_group_device(hs, img.data_ptr(), xsd.data_ptr(), [y.data_ptr() for y in ys], M,
+                                   stream=s, accumulate=accumulate)
+        torch.cuda.synchronize()
+        return [y.cpu().numpy() for y in ys]
+    finally:
+        for h in hs:
+            ctx.release(h)
+
+
+@pytest.mark.parametrize("Ns,K,M,accumulate", [((9728, 9728), 2560, 4, False), ((2560,), 9728, 16, True),
+                                               ((77, 1030), 700, 9, False), ((40, 7), 16640, 5, True),
+                                               ((4096, 1024, 1024), 2560, 3, False), ((33,), 256, 12, True)])
+def test_hvsq2_mfma_direct_matches_staged(gpu_ctx, oracle_lib, monkeypatch, Ns, K, M, accumulate):
+    """HyperVSQ-2 tensors uploaded with the MFMA-order copy (the GEMM reads
+    its operands straight from HBM) and without it (QWN_HIP_MFMA_COPY=0: the
+    GEMM stages the wave tiles in LDS, or for long rows reads them from the
+    wave-tile layout): both within the oracle's tolerance, and bit-identical
+    to each other (the same integer products summed in the same order)."""
+    rng = np.random.default_rng(sum(Ns) + K + M + 11)
+    ws = [synth.hvsq2_weights(rng, N, K) for N in Ns]
+    q8, xs, sums = oracle_lib.quantize(synth.activations(rng, M, K))
+    init = [rng.standard_normal((M, N)).astype(np.float32) if accumulate else np.zeros((M, N), np.float32)
+            for N in Ns]
+    direct = mfma_group_outputs(gpu_ctx, "hvsq2", ws, Ns, K, q8, xs, accumulate, init)
+    monkeypatch.setenv("QWN_HIP_MFMA_COPY", "0")
+    staged = mfma_group_outputs(gpu_ctx, "hvsq2", ws, Ns, K, q8, xs, accumulate, init)
+    for w, N, yd, ys, i0 in zip(ws, Ns, direct, staged, init):
+        assert np.array_equal(yd.view(np.uint32), ys.view(np.uint32)), \
+            f"{N}x{K} M={M}: direct and staged differ by up to {np.max(np.abs(yd - ys)):.3g}"
+        for t in range(M):
+            ref = oracle_product(oracle_lib, "hvsq2", w, q8[t], sums[t], xs[t], K, N)
+            ok, worst = gemv_close(yd[t] - i0[t], ref)
+            assert ok, f"{N}x{K} token {t}: worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("K,M", [(2560, 16), (16640, 6)])
+def test_hvsq2_mfma_staged_int32_block_dots(gpu_ctx, oracle_lib, monkeypatch, K, M):
+    """The staged (and, for 65-unit rows, the wave-tile) MFMA kernels' int32
+    block dots, with the MFMA-order copy turned off at upload."""
+    monkeypatch.setenv("QWN_HIP_MFMA_COPY", "0")
+    rng = np.random.default_rng(K + M + 5)
+    N = 77
+    w = synth.hvsq2_weights(rng, N, K)
+    q8, xs, sums = quantize(oracle_lib, synth.activations(rng, M, K))
+    h = gpu_ctx.upload(w, "hvsq2", N, K)
+    try:
+        nblk = (K + 255) // 256
+        got = gpu_ctx.debug_mfma_sums(h, q8[:, :K], N, nblk)
+        for t in range(M):
+            sq, _ = oracle_lib.hvsq2_octant_sums(w, q8[t], K, N)
+            assert np.array_equal(got[t], hvsq2_block_products(w, sq, N, K)), f"token {t}"
+    finally:
+        gpu_ctx.release(h)
+
+
 @pytest.mark.parametrize("Ns,K,M", [((1536, 256, 256), 1536, 16), ((8960, 8960), 1536, 16),
                                     ((1536,), 8960, 16), ((8200, 77), 777, 9), ((16390, 5), 520, 11),
                                     ((3,), 31, 8), ((65, 130), 33, 12), ((300,), 16384, 10), ((64,), 224, 13)])
