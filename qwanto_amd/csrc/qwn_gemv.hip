@@ -1663,7 +1663,7 @@ struct MfmaCopyArgs {
     const uint8_t *payload, *meta;
     uint8_t *dst_payload, *dst_meta;
     size_t tile_payload, tile_meta;
-    uint32_t units, lanes_log2, rows_per_wave_log2, tiles, groups;
+    uint32_t units, lanes_log2, rows_per_wave_log2, tiles, groups, q4;
 };
 
 __global__ __launch_bounds__(256) void mfma_copy_kernel(MfmaCopyArgs a) {
@@ -1677,8 +1677,19 @@ __global__ __launch_bounds__(256) void mfma_copy_kernel(MfmaCopyArgs a) {
         if ((row >> a.rows_per_wave_log2) < a.tiles) {
             const uint32_t tile = row >> a.rows_per_wave_log2, grp = row & (R - 1);
             const uint32_t slot = u >> a.lanes_log2, n = min(L, a.units - slot * L);
-            v = *reinterpret_cast<const uint4 *>(a.payload + tile * a.tile_payload + static_cast<size_t>(64) * R * L * slot +
-                                                 16 * (static_cast<size_t>(g) * R * n + grp * n + (u & (L - 1))));
+            const uint8_t *src = a.payload + tile * a.tile_payload + static_cast<size_t>(64) * R * L * slot;
+            if (a.q4) {
+                // Q4_0: word q of piece (g, m) is word g of block 4u + q
+                // (chunk q) of row m
+                uint32_t w[4];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q)
+                    w[q] = *reinterpret_cast<const uint32_t *>(
+                        src + 16 * (static_cast<size_t>(q) * R * n + grp * n + (u & (L - 1))) + 4 * g);
+                v = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+                v = *reinterpret_cast<const uint4 *>(src + 16 * (static_cast<size_t>(g) * R * n + grp * n + (u & (L - 1))));
+            }
         }
         reinterpret_cast<uint4 *>(a.dst_payload)[idx] = v;
     }
@@ -1847,6 +1858,138 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
             float v = mul_rounded(acc[r], a.scales[tok]);
             if (bias && sp.qs == 0) v = add_rounded(v, bias[row]);
             unsafeAtomicAdd(output + static_cast<size_t>(tok) * stride + row, v);
+        }
+    }
+}
+
+// Q4_0 tensors with an MFMA-order copy: a unit (four 32-weight blocks) of
+// 16 rows is one contiguous 1 KB, 16 bytes per lane (g, m): word q holds
+// lane g's four bytes of row m's block 4u + q (its eight K positions: low
+// nibbles 4g .. 4g+3, high 16+4g .. 16+4g+3), so one load feeds the unit's
+// four MFMAs; the row's four block scales are one 8-byte load.  Each wave
+// loads a chunk of units straight from HBM, then multiplies.  SPLIT: the
+// residual adds over few row groups, each row group split four ways by
+// unit range, the partials added with float atomics (in no fixed order);
+// otherwise mfma_gemm_kernel's single pass, the waves' partials summed in
+// wave order.  payload[i] / meta[i] of the arguments are the copies; a.nb
+// is units per wave.
+template <int NB, bool SPLIT, bool DUMP>
+__global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kernel(MfmaArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lane = threadIdx.x % kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+    const uint32_t KS = 1u << a.ks_log2;
+    const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
+    uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
+    job = __builtin_amdgcn_readfirstlane(job);
+    const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
+    const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
+    float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
+    const uint32_t rows = job == 0 ? a.rows[0] : job == 1 ? a.rows[1] : job == 2 ? a.rows[2] : a.rows[3];
+    const uint32_t stride = job == 0   ? a.output_stride[0]
+                            : job == 1 ? a.output_stride[1]
+                            : job == 2 ? a.output_stride[2]
+                                       : a.output_stride[3];
+    const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
+    const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
+    const uint32_t local = blockIdx.x - first;
+    const uint32_t qs = SPLIT ? (local & 3u) : 0u, rg = SPLIT ? (local >> 2) : local, r0 = rg * 16;
+    const uint32_t g = lane >> 4, m = lane & 15, row = r0 + m;
+    // this workgroup's units (SPLIT: quarter qs of the row's), then the wave's
+    const uint32_t per_split = SPLIT ? (a.units + 3) / 4 : a.units;
+    const uint32_t s0 = min(a.units, qs * per_split), s1 = min(a.units, s0 + per_split);
+    const uint32_t v0 = min(s1, s0 + wave * a.nb), v1 = min(s1, v0 + a.nb);
+    float xs_pre[4], res_pre[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+    if (!SPLIT && a.accumulate && wave == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = 4 * g + r;
+            res_pre[r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+        }
+    }
+    const uint8_t *pbase = payload + static_cast<size_t>(rg) * a.units * 1024 + lane * 16;
+    const uint8_t *mbase = meta + static_cast<size_t>(rg) * a.units * 128 + m * 8;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c0 = v0; c0 < v1; c0 += NB) {
+        const uint32_t nv = min(static_cast<uint32_t>(NB), v1 - c0);
+        uint4 A[NB];
+        uint2 Mt[NB], X[NB][4];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t u = c0 + (static_cast<uint32_t>(i) < nv ? i : 0);
+            A[i] = *reinterpret_cast<const uint4 *>(pbase + static_cast<size_t>(u) * 1024);
+            Mt[i] = *reinterpret_cast<const uint2 *>(mbase + static_cast<size_t>(u) * 128);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // blocks past K (the last unit's padding) read the last block
+                // and are skipped below
+                const uint32_t b = min(4 * u + q, a.nblk - 1);
+                X[i][q] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            if (static_cast<uint32_t>(i) >= nv) break;
+            const uint32_t u = c0 + i;
+            const uint32_t cw[4] = {A[i].x, A[i].y, A[i].z, A[i].w};
+            const uint32_t dw[2] = {Mt[i].x, Mt[i].y};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t b = 4 * u + q;
+                if (b >= a.nblk) break;
+                const long xv = static_cast<long>((static_cast<uint64_t>(X[i][q].y) << 32) | X[i][q].x);
+                const uint32_t lo = q4_signed(cw[q] & 0x0f0f0f0fu), hi = q4_signed((cw[q] >> 4) & 0x0f0f0f0fu);
+                const long wv = static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+                mfma_v4i ci = {0, 0, 0, 0};
+                // C[token][row]: element r is token 4g + r of row m
+                ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(xv, wv, ci, 0, 0, 0);
+                if constexpr (DUMP) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t tok = 4 * g + r;
+                        if (row < rows && tok < a.ntok) a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b] = ci[r];
+                    }
+                }
+                // rows past the matrix are zero in the copy: scale 0
+                const float d = half_to_float((dw[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), d, acc[r]);
+            }
+        }
+    }
+    // the K-split partials, summed in wave order
+    if (KS > 1) {
+        float *part_s = reinterpret_cast<float *>(smem);
+        if (wave > 0) {
+            float *dst = part_s + ((wave - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r] = acc[r];
+        }
+        __syncthreads();
+        if (wave == 0)
+            for (uint32_t k = 1; k < KS; ++k) {
+                const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] += src[r];
+            }
+    }
+    // lane (g, m) holds tokens 4g .. 4g+3 of row m
+    if (wave == 0 && row < rows) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t tok = 4 * g + r;
+            if (tok >= a.ntok) continue;
+            float v = mul_rounded(acc[r], xs_pre[r]);
+            if constexpr (SPLIT) {
+                if (bias && qs == 0) v = add_rounded(v, bias[row]);
+                unsafeAtomicAdd(output + static_cast<size_t>(tok) * stride + row, v);
+            } else {
+                if (bias) v = add_rounded(v, bias[row]);
+                output[static_cast<size_t>(tok) * stride + row] = a.accumulate ? add_rounded(res_pre[r], v) : v;
+            }
         }
     }
 }
@@ -2485,13 +2628,14 @@ hipError_t launch_mfma_nb(const MfmaPlan &p, uint32_t grid, const MfmaArgs &a, h
 }  // namespace
 
 size_t mfma_copy_bytes(const DeviceTensor &t) {
-    if (t.kind != kHvsq2) return 0;
+    if (t.kind != kHvsq2 && t.kind != kQ4_0) return 0;
     const size_t groups = (t.rows + 15) / 16;
     return groups * t.units * 1024 + groups * t.units * 128;
 }
 
 hipError_t launch_mfma_copy(const DeviceTensor &t, hipStream_t stream) {
-    if (t.kind != kHvsq2 || !t.mfma_payload || !t.mfma_meta || !t.payload || !t.meta) return hipErrorInvalidValue;
+    if ((t.kind != kHvsq2 && t.kind != kQ4_0) || !t.mfma_payload || !t.mfma_meta || !t.payload || !t.meta)
+        return hipErrorInvalidValue;
     MfmaCopyArgs c{};
     c.payload = t.payload;
     c.meta = t.meta;
@@ -2504,6 +2648,7 @@ hipError_t launch_mfma_copy(const DeviceTensor &t, hipStream_t stream) {
     c.rows_per_wave_log2 = static_cast<uint32_t>(__builtin_ctz(t.rows_per_wave));
     c.tiles = t.tiles;
     c.groups = (t.rows + 15) / 16;
+    c.q4 = t.kind == kQ4_0 ? 1u : 0u;
     const size_t n = static_cast<size_t>(c.groups) * t.units * 64;
     hipLaunchKernelGGL(mfma_copy_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, c);
     return hipGetLastError();
@@ -2528,13 +2673,13 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         total_rows += t.rows;
     }
     MfmaPlan p = mfma_plan(t0, total_rows);
-    // HyperVSQ-2 tensors that all carry the MFMA-order copy: direct loads
-    bool direct = t0.kind == kHvsq2;
+    // tensors that all carry the MFMA-order copy: direct loads
+    bool direct = true;
     for (uint32_t i = 0; i < count; ++i) direct = direct && tensors[i]->mfma_payload && tensors[i]->mfma_meta;
     // residual adds over few row groups: the four-way K split
     const uint64_t groups = (total_rows + 15) / 16;
-    const bool split = t0.kind == kQ4_0 && accumulate && !dump && p.stage && groups < 256;
-    if (split) {
+    const bool split = t0.kind == kQ4_0 && accumulate && !dump && (p.stage || direct) && groups < 256;
+    if (split && !direct) {
         const uint32_t units = t0.units;
         auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
         p.ks_log2 = 0;
@@ -2583,6 +2728,44 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.dump = dump;
     a.pad_p = t0.stage_pad_p;
     a.pad_m = t0.stage_pad_m;
+    if (direct && t0.kind == kQ4_0) {
+        // the fewest waves (up to 8) that keep a wave's units (of the row's,
+        // or of a split's quarter) within one unrolled chunk of 5
+        const uint32_t span = split ? (t0.units + 3) / 4 : t0.units;
+        auto per_wave = [&](uint32_t ks) { return (span + (1u << ks) - 1) >> ks; };
+        p.ks_log2 = 0;
+        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
+        p.nb = per_wave(p.ks_log2);
+        p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
+        p.waves = 1u << p.ks_log2;
+        a.ks_log2 = p.ks_log2;
+        a.nb = p.nb;
+        const uint32_t threads = p.waves * kWaveSize;
+        const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
+        if (p.waves > static_cast<uint32_t>(kMfmaMaxWaves)) return hipErrorInvalidValue;
+#define QWN_Q4D(NBV, SP, DU) hipLaunchKernelGGL((mfma_q4_direct_kernel<NBV, SP, DU>), dim3(grid), dim3(threads), lds, stream, a)
+        if (split) {
+            switch (p.nbt) {
+            case 2: QWN_Q4D(2, true, false); break;
+            case 3: QWN_Q4D(3, true, false); break;
+            default: QWN_Q4D(5, true, false); break;
+            }
+        } else if (dump) {
+            switch (p.nbt) {
+            case 2: QWN_Q4D(2, false, true); break;
+            case 3: QWN_Q4D(3, false, true); break;
+            default: QWN_Q4D(5, false, true); break;
+            }
+        } else {
+            switch (p.nbt) {
+            case 2: QWN_Q4D(2, false, false); break;
+            case 3: QWN_Q4D(3, false, false); break;
+            default: QWN_Q4D(5, false, false); break;
+            }
+        }
+#undef QWN_Q4D
+        return hipGetLastError();
+    }
     if (direct) {
         // the fewest waves that keep a wave's units within one unrolled chunk
         // of 5 (a wave's loads all in flight at once)

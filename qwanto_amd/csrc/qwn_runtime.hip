@@ -254,8 +254,8 @@ void free_tensor(ResidentTensor *rt) {
     delete rt;
 }
 
-// The MFMA-order copy of a HyperVSQ-2 tensor (qwn::launch_mfma_copy), which
-// the batched GEMM reads directly instead of staging the wave tiles: made
+// The MFMA-order copy of a HyperVSQ-2 or Q4_0 tensor (qwn::launch_mfma_copy),
+// which the batched GEMM reads directly instead of staging the wave tiles: made
 // where device memory has room for it with 1 GB to spare (it is not charged
 // to the context's budget, which counts the tensors' own bytes) and unless
 // QWN_HIP_MFMA_COPY=0; without it the GEMM stages the tiles.
