@@ -281,7 +281,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
     // (mode: fp32 / RMSNorm / SwiGLU of x), then the batched dot8 GEMV on
     // activation images, or where mfma_batch() says so the int8 MFMA GEMM
     // on the MFMA image; add: residual stream
-    const bool mfma = d->pmimg && mfma_batch(d->proj[P_Q]->kind, m);
+    const bool mfma = d->pmimg && mfma_batch(d->proj[P_Q]->kind, m, d->proj[P_Q]->mfma_payload != nullptr);
     auto project = [&](std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs,
                        uint32_t mode, const float *x, const float *x2, const float *norm, uint32_t x_stride,
                        bool add, std::initializer_list<const float *> biases) {

@@ -225,15 +225,17 @@ constexpr uint32_t kMfmaMinTokensQ4 = 6;
 // LDS per workgroup the MFMA GEMM plans its staging against: gfx950's
 // 160 KB (context creation refuses a device that reports less).
 constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
-// Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV:
-// HyperVSQ-2 from 3 tokens (measured on Qwen3-4B layers: the MFMA GEMM takes
-// about 25 us per layer whatever the token count up to 16, the dot8 GEMV
-// 17.9 us at 1 token, 22.8 at 2 and 33.4 at 4, which is how 3 tokens run);
-// Q4_0 (one 16x16x32 MFMA per 32-weight block) from 6 tokens (Qwen2-1.5B
-// layers: the MFMA GEMM about 31 us whatever the token count, the dot8
-// GEMV 24.7 us at 4 tokens and 39.0 at 8).
-inline bool mfma_batch(uint32_t kind, uint32_t batch) {
-    return (kind == kHvsq2 && batch >= kMfmaMinTokens) || (kind == kQ4_0 && batch >= kMfmaMinTokensQ4);
+// Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV
+// (per-layer times with the weights rotated through HBM): HyperVSQ-2 from 3
+// tokens (Qwen3-4B layers: the MFMA GEMM about 24-26 us whatever the token
+// count up to 16, the dot8 GEMV 23.3 us at 2 tokens and 33.2 at 3); Q4_0
+// (one 16x16x32 MFMA per 32-weight block) with the MFMA-order copy
+// (`copy`) from 3 tokens too (Qwen2-1.5B layers: the MFMA GEMM 21.7 us at 2
+// tokens, 22.3 at 3, 23.1 at 6; the dot8 GEMV 18.8, 24.6, 38.5), without
+// it, staged in LDS, from 6 (about 31 us whatever the token count).
+inline bool mfma_batch(uint32_t kind, uint32_t batch, bool copy) {
+    return (kind == kHvsq2 && batch >= kMfmaMinTokens) ||
+           (kind == kQ4_0 && batch >= (copy ? kMfmaMinTokens : kMfmaMinTokensQ4));
 }
 
 // RMSNorm of `count` fp32 tokens ([count][x_stride]) into fp32 images of an

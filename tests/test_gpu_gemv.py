@@ -309,11 +309,20 @@ def test_hvsq2_batched(gpu_ctx, oracle_lib, M):
     check_hvsq2(gpu_ctx, oracle_lib, 4096, 2560, seed=100 + M, M=M)
 
 
-@pytest.mark.parametrize("M", [2, 5, 8, 16, 17])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16, 17])
 def test_q4_0_batched(gpu_ctx, oracle_lib, M):
-    """Through qwn_cuda_abi_gemm: the dot8 GEMV below 16 tokens, the MFMA
-    GEMM in 16-token tiles from 16 (17: a full tile and a 1-token tile)."""
+    """Through qwn_cuda_abi_gemm: the dot8 GEMV at 2 tokens, the MFMA GEMM
+    on the MFMA-order copy from 3, in 16-token tiles (17: a full tile and a
+    1-token tile)."""
     check_q4_0(gpu_ctx, oracle_lib, 1536, 8960, seed=200 + M, M=M)
+
+
+@pytest.mark.parametrize("M", [4, 5, 6])
+def test_q4_0_batched_without_copy(gpu_ctx, oracle_lib, monkeypatch, M):
+    """Uploaded without the MFMA-order copy (QWN_HIP_MFMA_COPY=0): the dot8
+    GEMV up to 5 tokens, the staged MFMA GEMM from 6."""
+    monkeypatch.setenv("QWN_HIP_MFMA_COPY", "0")
+    check_q4_0(gpu_ctx, oracle_lib, 1536, 8960, seed=210 + M, M=M)
 
 
 @pytest.mark.parametrize("N,K,M", [(77, 700, 8), (130, 513, 9), (1, 256, 8), (64, 256, 16), (300, 7936, 12),
