@@ -1538,9 +1538,11 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 // lane (g, m) taking chunk g of row m; its meta one 128-byte span), so a
 // workgroup has no staging copy, no barrier before its products and no LDS
 // bank gaps; the products are mfma_chunk_hv's, the K-split sum and the
-// token-major epilogue mfma_gemm_kernel's.  payload[i] / meta[i] of the
-// arguments are the copies.
-template <int NB, bool DUMP>
+// token-major epilogue mfma_gemm_kernel's.  SPLIT: the residual adds over
+// few row groups, each row group split four ways by unit range, the
+// partials added with float atomics (in no fixed order).  payload[i] /
+// meta[i] of the arguments are the copies.
+template <int NB, bool SPLIT, bool DUMP>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(MfmaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
@@ -1559,14 +1561,18 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
                                        : a.output_stride[3];
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
-    const uint32_t rg = blockIdx.x - first, r0 = rg * 16;
+    const uint32_t local = blockIdx.x - first;
+    const uint32_t qs = SPLIT ? (local & 3u) : 0u, rg = SPLIT ? (local >> 2) : local, r0 = rg * 16;
     const uint32_t g = lane >> 4, m = lane & 15;
-    const uint32_t kb0 = wave * a.nb, kb1 = min(a.nblk, kb0 + a.nb);
+    // this workgroup's units (SPLIT: quarter qs of the row's), then the wave's
+    const uint32_t per_split = SPLIT ? (a.nblk + 3) / 4 : a.nblk;
+    const uint32_t s0 = min(a.nblk, qs * per_split), s1 = min(a.nblk, s0 + per_split);
+    const uint32_t kb0 = min(s1, s0 + wave * a.nb), kb1 = min(s1, kb0 + a.nb);
     // the epilogue's token scales and prior outputs, loaded ahead
     float xs_pre[4], res_pre[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
-    if (a.accumulate && wave == 0) {
+    if (!SPLIT && a.accumulate && wave == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r, row = r0 + m;
@@ -1651,14 +1657,20 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
             const uint32_t tok = 4 * g + r;
             if (tok >= a.ntok) continue;
             float v = mul_rounded(acc[r], xs_pre[r]);
-            if (bias) v = add_rounded(v, bias[row]);
-            output[static_cast<size_t>(tok) * stride + row] = a.accumulate ? add_rounded(res_pre[r], v) : v;
+            if constexpr (SPLIT) {
+                if (bias && qs == 0) v = add_rounded(v, bias[row]);
+                unsafeAtomicAdd(output + static_cast<size_t>(tok) * stride + row, v);
+            } else {
+                if (bias) v = add_rounded(v, bias[row]);
+                output[static_cast<size_t>(tok) * stride + row] = a.accumulate ? add_rounded(res_pre[r], v) : v;
+            }
         }
     }
 }
 
-// The MFMA-order copy of a HyperVSQ-2 tensor from its wave-tile layout: one
-// thread per 16-byte payload piece and per 8-byte meta entry of the copy.
+// The MFMA-order copy of a HyperVSQ-2 or Q4_0 tensor from its wave-tile
+// layout: one thread per 16-byte payload piece and per 8-byte meta entry of
+// the copy.
 struct MfmaCopyArgs {
     const uint8_t *payload, *meta;
     uint8_t *dst_payload, *dst_meta;
@@ -2678,7 +2690,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     for (uint32_t i = 0; i < count; ++i) direct = direct && tensors[i]->mfma_payload && tensors[i]->mfma_meta;
     // residual adds over few row groups: the four-way K split
     const uint64_t groups = (total_rows + 15) / 16;
-    const bool split = t0.kind == kQ4_0 && accumulate && !dump && (p.stage || direct) && groups < 256;
+    const bool split = accumulate && !dump && groups < 256 && (direct || (t0.kind == kQ4_0 && p.stage));
     if (split && !direct) {
         const uint32_t units = t0.units;
         auto per_wave = [&](uint32_t ks) { return (units + (1u << ks) - 1) >> ks; };
@@ -2767,9 +2779,11 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         return hipGetLastError();
     }
     if (direct) {
-        // the fewest waves that keep a wave's units within one unrolled chunk
-        // of 5 (a wave's loads all in flight at once)
-        auto per_wave = [&](uint32_t ks) { return (t0.units + (1u << ks) - 1) >> ks; };
+        // the fewest waves that keep a wave's units (of the row's, or of a
+        // split's quarter) within one unrolled chunk of 5 (a wave's loads all
+        // in flight at once)
+        const uint32_t span = split ? (t0.units + 3) / 4 : t0.units;
+        auto per_wave = [&](uint32_t ks) { return (span + (1u << ks) - 1) >> ks; };
         p.ks_log2 = 0;
         while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
         p.nb = per_wave(p.ks_log2);
@@ -2779,19 +2793,27 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         a.nb = p.nb;
         const uint32_t threads = p.waves * kWaveSize;
         const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
-        if (dump) {
+#define QWN_HVD(NBV, SP, DU) hipLaunchKernelGGL((mfma_direct_kernel<NBV, SP, DU>), dim3(grid), dim3(threads), lds, stream, a)
+        if (split) {
             switch (p.nbt) {
-            case 2: hipLaunchKernelGGL((mfma_direct_kernel<2, true>), dim3(grid), dim3(threads), lds, stream, a); break;
-            case 3: hipLaunchKernelGGL((mfma_direct_kernel<3, true>), dim3(grid), dim3(threads), lds, stream, a); break;
-            default: hipLaunchKernelGGL((mfma_direct_kernel<5, true>), dim3(grid), dim3(threads), lds, stream, a); break;
+            case 2: QWN_HVD(2, true, false); break;
+            case 3: QWN_HVD(3, true, false); break;
+            default: QWN_HVD(5, true, false); break;
+            }
+        } else if (dump) {
+            switch (p.nbt) {
+            case 2: QWN_HVD(2, false, true); break;
+            case 3: QWN_HVD(3, false, true); break;
+            default: QWN_HVD(5, false, true); break;
             }
         } else {
             switch (p.nbt) {
-            case 2: hipLaunchKernelGGL((mfma_direct_kernel<2, false>), dim3(grid), dim3(threads), lds, stream, a); break;
-            case 3: hipLaunchKernelGGL((mfma_direct_kernel<3, false>), dim3(grid), dim3(threads), lds, stream, a); break;
-            default: hipLaunchKernelGGL((mfma_direct_kernel<5, false>), dim3(grid), dim3(threads), lds, stream, a); break;
+            case 2: QWN_HVD(2, false, false); break;
+            case 3: QWN_HVD(3, false, false); break;
+            default: QWN_HVD(5, false, false); break;
             }
         }
+#undef QWN_HVD
         return hipGetLastError();
     }
     if (split) {
