@@ -256,17 +256,30 @@ void free_tensor(ResidentTensor *rt) {
 }
 
 // The MFMA-order copy of a HyperVSQ-2 or Q4_0 tensor (qwn::launch_mfma_copy),
-// which the batched GEMM reads directly instead of staging the wave tiles: made
-// where device memory has room for it with 1 GB to spare (it is not charged
-// to the context's budget, which counts the tensors' own bytes) and unless
-// QWN_HIP_MFMA_COPY=0; without it the GEMM stages the tiles.
-void attach_mfma_copy(ResidentTensor *rt) {
+// which the batched GEMM reads directly instead of staging the wave tiles.
+// It is not charged to the context's budget (which counts the tensors' own
+// bytes), so it is made only from memory nothing else is counting on: the
+// device keeps at least half its memory free after the copy, and, under a
+// budget, also the bytes the budget still allows tensors (beyond
+// `pending`, this upload's tensors, allocated but not yet charged) plus a
+// tenth of the device for caches and workspaces.  A model too large for
+// that gets copies for its first tensors only, or none; a group of tensors
+// that are not all copied runs the staged GEMM.  QWN_HIP_MFMA_COPY=0 turns
+// the copies off.
+void attach_mfma_copy(Context *ctx, ResidentTensor *rt, uint64_t pending) {
     const size_t cb = qwn::mfma_copy_bytes(rt->t);
     if (!cb) return;
     const char *env = std::getenv("QWN_HIP_MFMA_COPY");
     if (env && env[0] == '0') return;
     size_t free_b = 0, total_b = 0;
-    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess || free_b < cb + (1ull << 30)) return;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return;
+    uint64_t reserve = total_b / 2;
+    if (ctx->budget) {
+        const uint64_t charged = ctx->resident + pending;
+        const uint64_t headroom = ctx->budget > charged ? ctx->budget - charged : 0;
+        reserve = std::max<uint64_t>(reserve, headroom + total_b / 10);
+    }
+    if (free_b < cb + reserve) return;
     if (hipMalloc(&rt->mfma_allocation, cb) != hipSuccess) {
         rt->mfma_allocation = nullptr;
         return;
@@ -600,12 +613,14 @@ int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count,
         made.push_back(rt);
     }
     const auto t0 = std::chrono::steady_clock::now();
+    uint64_t pending = 0;
+    for (uint32_t i = 0; i < count; ++i) pending += made[i]->t.logical_bytes;
     for (uint32_t i = 0; i < count; ++i) {
         if ((e = enqueue_upload(ctx, made[i]->t, static_cast<const uint8_t *>(ups[i].host_data))) != hipSuccess) {
             (void)hip_fail("tensor upload", e);
             return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
         }
-        attach_mfma_copy(made[i]);
+        attach_mfma_copy(ctx, made[i], pending);
         if (made[i]->t.mfma_payload && (e = qwn::launch_mfma_copy(made[i]->t, ctx->stream)) != hipSuccess) {
             (void)hip_fail("MFMA-order copy", e);
             return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
