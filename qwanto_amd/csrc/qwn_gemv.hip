@@ -1583,17 +1583,33 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     const uint8_t *mbase = meta + (static_cast<size_t>(rg) * a.units) * 128 + m * 8;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     HvImage<NB> im;
-    for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
+    // the image as bounded buffer loads that skip absent tokens' columns
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(a.image), 0, static_cast<int>(a.units * static_cast<uint32_t>(mfma_image_block_bytes())),
+        0x00020000);
+    const uint32_t skip = m < a.ntok ? 0u : 0x80000000u, sskip = 4 * g < a.ntok ? 0u : 0x80000000u;
+    // one chunk of the wave's units from b0; the first is issued outside the
+    // loop, so the loop header's wait for every load in flight does not
+    // hold the first weight loads behind the epilogue's early loads
+    auto chunk = [&](uint32_t b0) {
         const uint32_t nv = min(static_cast<uint32_t>(NB), kb1 - b0);
         uint4 A[NB];
         uint2 Mt[NB];
+        // unit by unit (weights, meta, image), so a unit's products wait
+        // only for its own loads and the later units' arrive meanwhile
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const uint32_t u = b0 + (static_cast<uint32_t>(i) < nv ? i : 0);
             A[i] = *reinterpret_cast<const uint4 *>(pbase + static_cast<size_t>(u) * 1024);
             Mt[i] = *reinterpret_cast<const uint2 *>(mbase + static_cast<size_t>(u) * 128);
+            const uint32_t off = (u * 4096 + lane * 16) | skip;
+#pragma unroll
+            for (int sl = 0; sl < 4; ++sl)
+                im.B[i][sl] =
+                    __builtin_bit_cast(mfma_v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, off + sl * 1024, 0, 0));
+            im.SA[i] = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(rs, (a.units * 4096 + (u * 16 + 4 * g) * 4) | sskip, 0, 0));
         }
-        hv_image_loads<NB>(a, b0, nv, lane, im);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
@@ -1631,7 +1647,9 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), dsc, fmaf(msc, sa[r], acc[r]));
         }
-    }
+    };
+    if (kb0 < kb1) chunk(kb0);
+    for (uint32_t b0 = kb0 + NB; b0 < kb1; b0 += NB) chunk(b0);
     // the K-split partials, summed in wave order
     if (KS > 1) {
         float *part_s = reinterpret_cast<float *>(smem);
@@ -1924,7 +1942,10 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
     const uint8_t *pbase = payload + static_cast<size_t>(rg) * a.units * 1024 + lane * 16;
     const uint8_t *mbase = meta + static_cast<size_t>(rg) * a.units * 128 + m * 8;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t c0 = v0; c0 < v1; c0 += NB) {
+    // one chunk of the wave's units from c0; the first is issued outside the
+    // loop, so the loop header's wait for every load in flight does not
+    // hold the first weight loads behind the epilogue's early loads
+    auto chunk = [&](uint32_t c0) {
         const uint32_t nv = min(static_cast<uint32_t>(NB), v1 - c0);
         uint4 A[NB];
         uint2 Mt[NB], X[NB][4];
@@ -1971,7 +1992,9 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
                 for (int r = 0; r < 4; ++r) acc[r] = fmaf(static_cast<float>(ci[r]), d, acc[r]);
             }
         }
-    }
+    };
+    if (v0 < v1) chunk(v0);
+    for (uint32_t c0 = v0 + NB; c0 < v1; c0 += NB) chunk(c0);
     // the K-split partials, summed in wave order
     if (KS > 1) {
         float *part_s = reinterpret_cast<float *>(smem);
