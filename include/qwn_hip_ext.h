@@ -8,7 +8,8 @@
  * callers that keep activations on the device: a resident decode loop, a
  * benchmark that times kernels with inputs already in HBM, HIP graph
  * capture.  They take DEVICE pointers, enqueue on the caller's stream
- * (a hipStream_t passed as void*; NULL = the context's own stream), never
+ * (a hipStream_t passed as void*; NULL = the context's own stream, a
+ * blocking stream, so ordered with work on the null stream), never
  * synchronise and never allocate, so they are safe to record into a graph.
  * The library advertises them with QWN_CUDA_CAP_DEVICE_POINTERS.
  *

@@ -397,7 +397,11 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *op
     ctx->budget = options->memory_budget_bytes;
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess) e = qwn::noalloc_init_device(ctx->device);
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    // A blocking stream: work on it is ordered with work on the null stream
+    // (torch's default stream), which callers of the device-pointer entry
+    // points pass as NULL = this stream; a non-blocking stream let a null-stream
+    // fill of an output buffer land after the library's kernel had written it.
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamDefault);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_end);
     if (e != hipSuccess) {
