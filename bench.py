@@ -467,8 +467,8 @@ def batch_sweep(torch, ctx, steps, warmup, ms_list=(1, 2, 4, 8, 16)):
     HyperVSQ-2 on 36 layers of the Qwen3-4B shapes (1.05 GB; 36 layers per
     token in tokens_per_s), and under "q4_0" Q4_0 on 40 layers of the
     Qwen2-1.5B shapes (1.05 GB; 28 layers per token); dot8 grouped launches
-    below 3 tokens, grouped int8-MFMA launches from there (MFMA
-    utilisation = useful int8 ops / dense int8 peak).  One set of weights
+    below 2 (HyperVSQ-2) or 3 (Q4_0) tokens, grouped int8-MFMA launches from
+    there (MFMA utilisation = useful int8 ops / dense int8 peak).  One set of weights
     per kind serves every M."""
     from qwanto_amd import synth
 
@@ -477,7 +477,8 @@ def batch_sweep(torch, ctx, steps, warmup, ms_list=(1, 2, 4, 8, 16)):
         weights = upload_layers(ctx, kind, shapes, layers, seed0)
         try:
             for M in ms_list:
-                mfma = M >= 3     # the library's own choice (mfma_batch, weights with the MFMA-order copy)
+                # the library's own choice (mfma_batch, weights with the MFMA-order copy)
+                mfma = M >= (2 if kind == "hvsq2" else 3)
                 if not mfma:
                     sw = Sweep(torch, ctx, kind, shapes, layers, seed=seed0 + M, batch=M, weights=weights)
                     ms = time_graph(torch, sw.grouped, steps, warmup)

@@ -138,8 +138,8 @@ QWN_CUDA_ABI_API int qwn_hip_ext_argmax_device(QwnCudaContextHandle *context, co
                                                uint32_t count, int32_t *index, void *stream);
 
 /* int8 MFMA batch GEMM of a HyperVSQ-2 or Q4_0 tensor, 1..16 tokens per
- * call (the ABI's GEMM uses it by itself from 3 HyperVSQ-2 / 6 Q4_0
- * tokens): HyperVSQ-2 blocks are exact int8 dot products with the octant
+ * call (the ABI's GEMM uses it by itself from 2 HyperVSQ-2 / 3 Q4_0
+ * tokens on the MFMA-order copy, from 3 / 6 without it): HyperVSQ-2 blocks are exact int8 dot products with the octant
  * multipliers folded into the weights (v_mfma_i32_16x16x64_i8), Q4_0 blocks
  * one v_mfma_i32_16x16x32_i8 each on the signed codes n - 8, on tiles of 16
  * rows x 16 tokens.  The activations are read from an "MFMA image" of the

@@ -226,15 +226,15 @@ constexpr uint32_t kMfmaMinTokensQ4 = 6;
 // 160 KB (context creation refuses a device that reports less).
 constexpr uint64_t kMfmaLdsLimit = 160 * 1024;
 // Batches that take the int8 MFMA GEMM instead of the batched dot8 GEMV
-// (per-layer times with the weights rotated through HBM): HyperVSQ-2 from 3
-// tokens (Qwen3-4B layers: the MFMA GEMM about 24-26 us whatever the token
-// count up to 16, the dot8 GEMV 23.3 us at 2 tokens and 33.2 at 3); Q4_0
-// (one 16x16x32 MFMA per 32-weight block) with the MFMA-order copy
-// (`copy`) from 3 tokens too (Qwen2-1.5B layers: the MFMA GEMM 21.7 us at 2
-// tokens, 22.3 at 3, 23.1 at 6; the dot8 GEMV 18.8, 24.6, 38.5), without
-// it, staged in LDS, from 6 (about 31 us whatever the token count).
+// (per-layer times with the weights rotated through HBM).  With the
+// MFMA-order copy (`copy`): HyperVSQ-2 from 2 tokens (Qwen3-4B layers: the
+// MFMA GEMM 20.5 / 20.9 / 21.0 us at 1 / 2 / 3 tokens, the dot8 GEMV 18.1 /
+// 23.3 / 33.3), Q4_0 from 3 (Qwen2-1.5B layers: the MFMA GEMM 20.4 / 20.7 /
+// 21.6 us, the dot8 GEMV 16.3 / 18.8 / 24.5).  Without it, staged in LDS:
+// HyperVSQ-2 from 3 tokens (about 24-26 us whatever the token count),
+// Q4_0 from 6 (about 31 us).
 inline bool mfma_batch(uint32_t kind, uint32_t batch, bool copy) {
-    return (kind == kHvsq2 && batch >= kMfmaMinTokens) ||
+    return (kind == kHvsq2 && batch >= (copy ? 2u : kMfmaMinTokens)) ||
            (kind == kQ4_0 && batch >= (copy ? kMfmaMinTokens : kMfmaMinTokensQ4));
 }
 

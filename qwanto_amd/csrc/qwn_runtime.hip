@@ -155,8 +155,8 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     }
     float *hscales = reinterpret_cast<float *>(hin + in_bytes);
     for (uint32_t b = 0; b < r->batch; ++b) hscales[b] = r->input_scales ? r->input_scales[b] : r->input_scale;
-    // int8 MFMA tiles of 16 tokens (from 3 tokens; Q4_0 without the
-    // MFMA-order copy from 6)
+    // int8 MFMA tiles of 16 tokens (mfma_batch: from 2 HyperVSQ-2 / 3 Q4_0
+    // tokens on the MFMA-order copy, from 3 / 6 without it)
     const bool mfma = qwn::mfma_batch(t.kind, r->batch, t.mfma_payload != nullptr);
     // Small requests skip the copy engines: the image kernel reads the
     // activations (and the GEMV its scales) straight from the pinned staging

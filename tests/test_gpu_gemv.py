@@ -317,6 +317,15 @@ def test_q4_0_batched(gpu_ctx, oracle_lib, M):
     check_q4_0(gpu_ctx, oracle_lib, 1536, 8960, seed=200 + M, M=M)
 
 
+@pytest.mark.parametrize("M", [2, 3])
+def test_hvsq2_batched_without_copy(gpu_ctx, oracle_lib, monkeypatch, M):
+    """Uploaded without the MFMA-order copy (QWN_HIP_MFMA_COPY=0): the dot8
+    GEMV at 2 tokens, the staged MFMA GEMM from 3 (with the copy the MFMA
+    GEMM takes 2 tokens already: test_hvsq2_batched)."""
+    monkeypatch.setenv("QWN_HIP_MFMA_COPY", "0")
+    check_hvsq2(gpu_ctx, oracle_lib, 4096, 2560, seed=110 + M, M=M)
+
+
 @pytest.mark.parametrize("M", [4, 5, 6])
 def test_q4_0_batched_without_copy(gpu_ctx, oracle_lib, monkeypatch, M):
     """Uploaded without the MFMA-order copy (QWN_HIP_MFMA_COPY=0): the dot8
