@@ -509,6 +509,37 @@ def test_device_image_path(gpu_ctx, oracle_lib, kind, K, M):
             gpu_ctx.release(h)
 
 
+def test_null_stream_ordered_with_context_stream(gpu_ctx, oracle_lib):
+    """A device entry point given stream NULL runs on the context's stream,
+    which is ordered with the null stream (torch's default stream): an input
+    written on the null stream behind several milliseconds of other work is
+    read only once it is written (scales bit-exact against the oracle's)."""
+    import torch
+    assert torch.cuda.current_stream().cuda_stream == 0, "torch's default stream is the null stream"
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(4242)
+    K, N = 2560, 64
+    h = gpu_ctx.upload(synth.weights("hvsq2", rng, N, K), "hvsq2", N, K)
+    x = synth.activations(rng, 1, K)
+    _, xs_ref, _ = quantize(oracle_lib, x)
+    try:
+        src = torch.from_numpy(x).to(dev)
+        xd = torch.zeros(1, K, dtype=torch.float32, device=dev)
+        ib = gpu_ctx.image_bytes(h)
+        img = torch.zeros(1, ib, dtype=torch.uint8, device=dev)
+        sc = torch.zeros(1, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        a = torch.randn(4096, 4096, dtype=torch.float32, device=dev)
+        for _ in range(8):
+            a = (a @ a) * 1e-3   # fp32 products keep the null stream busy
+        xd.copy_(src)            # the input, written behind them
+        gpu_ctx.quantize_image_device(h, xd.data_ptr(), 1, K, img.data_ptr(), ib, sc.data_ptr())
+        torch.cuda.synchronize()
+        assert np.array_equal(sc.cpu().numpy(), xs_ref)
+    finally:
+        gpu_ctx.release(h)
+
+
 def test_device_image_f16(gpu_ctx, oracle_lib):
     import torch
     rng = np.random.default_rng(5)
