@@ -10,7 +10,7 @@
  * Every struct, enum value and exported symbol of ABI version 1 keeps the
  * reference's binary layout, because an unmodified qwnrun dlopen()s this
  * library and passes its own structs: the layout is the interface, so it
- * cannot be redesigned. tests/test_abi_layout.py checks every size and field
+ * cannot be redesigned. tests/test_abi.py checks every size and field
  * offset against a fixture generated from the reference header.
  *
  * Extensions (marked EXT below) only append enum values and capability bits;

@@ -36,6 +36,8 @@ typedef struct {
     uint32_t units_per_lane;
     uint32_t rows_per_wave;
     uint32_t grid;
+    uint64_t mfma_copy_bytes; /* the batched GEMM's MFMA-order copy (0: none), charged to the
+                                 context's budget and gpu_resident_bytes with logical_bytes */
 } QwnHipTensorInfo;
 
 /* Shape, byte counts and batch-1 launch plan of a resident tensor. */
@@ -242,8 +244,13 @@ QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device(QwnCudaContextHandle *conte
  * capture, serving loops that forbid hipMalloc).  A request whose partials
  * exceed the array (qwn_hip_ext_attention_workspace_bytes() > 4 MiB) is
  * refused with QWN_CUDA_STATUS_INVALID_ARGUMENT.  Every call on one GPU
- * shares that GPU's array: calls that overlap on a GPU (other streams,
- * other contexts on the same device) race. */
+ * shares that GPU's array, so calls must not run at the same time on one
+ * GPU: a call is refused with QWN_CUDA_STATUS_UNAVAILABLE while the
+ * previous call on that GPU, enqueued on a different stream (another
+ * stream of the caller, another context's stream), has not finished.
+ * Calls on one stream are ordered and always accepted.  Calls recorded
+ * into a HIP graph are not tracked: a graph that replays them on two
+ * streams at once races. */
 QWN_CUDA_ABI_API int qwn_hip_ext_kv_attention_device_noalloc(QwnCudaContextHandle *context,
                                                              QwnCudaKvCacheHandle *cache,
                                                              const float *query, float *output,

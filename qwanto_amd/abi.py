@@ -163,7 +163,8 @@ class TensorInfo(_Versioned):
                 ("cols", ctypes.c_uint32), ("units_per_row", ctypes.c_uint32),
                 ("logical_bytes", ctypes.c_uint64), ("device_bytes", ctypes.c_uint64),
                 ("lanes_per_row", ctypes.c_uint32), ("units_per_lane", ctypes.c_uint32),
-                ("rows_per_wave", ctypes.c_uint32), ("grid", ctypes.c_uint32)]
+                ("rows_per_wave", ctypes.c_uint32), ("grid", ctypes.c_uint32),
+                ("mfma_copy_bytes", ctypes.c_uint64)]
 
 
 class GemvGroupRequest(_Versioned):

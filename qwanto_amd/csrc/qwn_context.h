@@ -53,7 +53,8 @@ struct DeviceBuffer {
 struct ResidentTensor {
     DeviceTensor t;
     void *allocation = nullptr;
-    void *mfma_allocation = nullptr;  // the MFMA-order copy (HyperVSQ-2), if any
+    void *mfma_allocation = nullptr;  // the MFMA-order copy (HyperVSQ-2, Q4_0), if any
+    uint64_t copy_bytes = 0;          // its size, charged to the context like the tensor's own bytes
 };
 
 struct ResidentKv {
@@ -78,7 +79,8 @@ struct Context {
     std::mutex mutex;
     int device = -1;
     uint64_t budget = 0;
-    uint64_t resident = 0;  // logical bytes charged against the budget
+    uint64_t resident = 0;  // bytes charged against the budget: tensors' logical bytes, their
+                            // MFMA-order copies, Q8 KV caches (gpu_resident_bytes reports it)
     hipStream_t stream = nullptr;
     hipEvent_t ev_start = nullptr, ev_end = nullptr;
     PinnedBuffer host_in, host_out;

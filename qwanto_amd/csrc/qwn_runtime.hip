@@ -257,16 +257,21 @@ void free_tensor(ResidentTensor *rt) {
 
 // The MFMA-order copy of a HyperVSQ-2 or Q4_0 tensor (qwn::launch_mfma_copy),
 // which the batched GEMM reads directly instead of staging the wave tiles.
-// It is not charged to the context's budget (which counts the tensors' own
-// bytes), so it is made only from memory nothing else is counting on: the
-// device keeps at least half its memory free after the copy, and, under a
-// budget, also the bytes the budget still allows tensors (beyond
-// `pending`, this upload's tensors, allocated but not yet charged) plus a
-// tenth of the device for caches and workspaces.  A model too large for
-// that gets copies for its first tensors only, or none; a group of tensors
-// that are not all copied runs the staged GEMM.  QWN_HIP_MFMA_COPY=0 turns
-// the copies off.
-void attach_mfma_copy(Context *ctx, ResidentTensor *rt, uint64_t pending) {
+// Its bytes are charged to the context like the tensor's own (the budget
+// caps every device byte a tensor holds, c/cuda/qwn_hypervsq2_cuda_abi.cu:
+// 554-562) and reported in gpu_resident_bytes.  The copy is optional, so it
+// never takes room a tensor needs:
+//  - under a budget it is made only in a batch upload (`batch`), from the
+//    budget left after every tensor of the batch (`pending`: this upload's
+//    tensors, not yet charged) and the copies already made (`copies`), and
+//    only while a tenth of the device stays free; an upload of one tensor at
+//    a time (the reference host's lazy upload) gets no copy, since a later
+//    tensor would otherwise be refused for the room it took;
+//  - without a budget it is made while half the device stays free.
+// A model too large for that gets copies for its first tensors only, or
+// none; a group of tensors that are not all copied runs the staged GEMM.
+// QWN_HIP_MFMA_COPY=0 turns the copies off.
+void attach_mfma_copy(Context *ctx, ResidentTensor *rt, uint64_t pending, uint64_t copies, bool batch) {
     const size_t cb = qwn::mfma_copy_bytes(rt->t);
     if (!cb) return;
     const char *env = std::getenv("QWN_HIP_MFMA_COPY");
@@ -275,15 +280,16 @@ void attach_mfma_copy(Context *ctx, ResidentTensor *rt, uint64_t pending) {
     if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return;
     uint64_t reserve = total_b / 2;
     if (ctx->budget) {
-        const uint64_t charged = ctx->resident + pending;
-        const uint64_t headroom = ctx->budget > charged ? ctx->budget - charged : 0;
-        reserve = std::max<uint64_t>(reserve, headroom + total_b / 10);
+        const uint64_t charged = ctx->resident + pending + copies;
+        if (!batch || charged > ctx->budget || ctx->budget - charged < cb) return;
+        reserve = total_b / 10;
     }
     if (free_b < cb + reserve) return;
     if (hipMalloc(&rt->mfma_allocation, cb) != hipSuccess) {
         rt->mfma_allocation = nullptr;
         return;
     }
+    rt->copy_bytes = cb;
     const size_t groups = (rt->t.rows + 15) / 16;
     rt->t.mfma_payload = static_cast<uint8_t *>(rt->mfma_allocation);
     rt->t.mfma_meta = rt->t.mfma_payload + groups * rt->t.units * 1024;
@@ -575,7 +581,11 @@ hipError_t enqueue_upload(Context *ctx, const DeviceTensor &t, const uint8_t *ho
 
 // Uploads `count` tensors (context lock held): describe and allocate all,
 // pipeline all, one synchronisation; on failure none stays resident.
-int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count, QwnCudaTensorHandle *out) {
+// `batch`: the caller handed over its tensors together
+// (qwn_hip_ext_upload_batch), so under a budget MFMA-order copies may use
+// what the budget leaves after all of them.
+int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count, QwnCudaTensorHandle *out,
+                   bool batch) {
     std::vector<ResidentTensor *> made;
     uint64_t bytes = 0, device_bytes = 0;
     auto fail = [&](int status) {
@@ -617,14 +627,15 @@ int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count,
         made.push_back(rt);
     }
     const auto t0 = std::chrono::steady_clock::now();
-    uint64_t pending = 0;
+    uint64_t pending = 0, copies = 0;
     for (uint32_t i = 0; i < count; ++i) pending += made[i]->t.logical_bytes;
     for (uint32_t i = 0; i < count; ++i) {
         if ((e = enqueue_upload(ctx, made[i]->t, static_cast<const uint8_t *>(ups[i].host_data))) != hipSuccess) {
             (void)hip_fail("tensor upload", e);
             return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
         }
-        attach_mfma_copy(ctx, made[i], pending);
+        attach_mfma_copy(ctx, made[i], pending, copies, batch);
+        copies += made[i]->copy_bytes;
         if (made[i]->t.mfma_payload && (e = qwn::launch_mfma_copy(made[i]->t, ctx->stream)) != hipSuccess) {
             (void)hip_fail("MFMA-order copy", e);
             return fail(QWN_CUDA_STATUS_RUNTIME_ERROR);
@@ -638,7 +649,7 @@ int upload_tensors(Context *ctx, const QwnCudaTensorUpload *ups, uint32_t count,
     QwnCudaTelemetry &tm = ctx->telemetry;
     for (uint32_t i = 0; i < count; ++i) {
         ctx->tensors.push_back(made[i]);
-        ctx->resident += made[i]->t.logical_bytes;
+        ctx->resident += made[i]->t.logical_bytes + made[i]->copy_bytes;
         tm.gpu_upload_count++;
         tm.gpu_upload_bytes += made[i]->t.logical_bytes;
         std::memset(&out[i], 0, sizeof(out[i]));
@@ -661,7 +672,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_upload_tensor(QwnCudaContextHandle *handle,
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
-    return upload_tensors(ctx, up, 1, out);
+    return upload_tensors(ctx, up, 1, out, false);
 }
 
 QWN_CUDA_ABI_API int qwn_hip_ext_upload_batch(QwnCudaContextHandle *handle, const QwnCudaTensorUpload *uploads,
@@ -672,7 +683,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_upload_batch(QwnCudaContextHandle *handle, cons
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
     std::lock_guard<std::mutex> lock(ctx->mutex);
-    return upload_tensors(ctx, uploads, count, out);
+    return upload_tensors(ctx, uploads, count, out, true);
 }
 
 QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *handle, QwnCudaTensorHandle *h) {
@@ -689,7 +700,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_release_tensor(QwnCudaContextHandle *handle, Q
     }
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
-    ctx->resident -= std::min(ctx->resident, rt->t.logical_bytes);
+    ctx->resident -= std::min(ctx->resident, rt->t.logical_bytes + rt->copy_bytes);
     ctx->tensors.erase(std::find(ctx->tensors.begin(), ctx->tensors.end(), rt));
     free_tensor(rt);
     ctx->telemetry.gpu_resident_bytes = ctx->resident;
@@ -942,7 +953,8 @@ QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHi
         set_error("invalid tensor info request");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
-    const DeviceTensor &t = static_cast<const ResidentTensor *>(h->opaque)->t;
+    const ResidentTensor *rt = static_cast<const ResidentTensor *>(h->opaque);
+    const DeviceTensor &t = rt->t;
     std::memset(info, 0, sizeof(*info));
     qwn_cuda_abi_header_init(&info->header, sizeof(*info));
     info->dtype = t.kind == qwn::kHvsq2 ? QWN_CUDA_TENSOR_HYPERVSQ2_74
@@ -956,6 +968,7 @@ QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHi
     info->units_per_lane = t.upl;
     info->rows_per_wave = t.rows_per_wave;
     info->grid = static_cast<uint32_t>(qwn::plan_gemv(t, 1).grid);
+    info->mfma_copy_bytes = rt->copy_bytes;
     return QWN_CUDA_STATUS_OK;
 }
 
@@ -1364,7 +1377,9 @@ QWN_CUDA_ABI_API int qwn_hip_ext_kv_append_device(QwnCudaContextHandle *handle, 
     hipError_t e = qwn::launch_kv_append(c, keys, values, c.tokens, s, count);
     if (e != hipSuccess) return hip_fail("device KV append launch", e);
     c.tokens += count;
-    ctx->telemetry.kv_cache_kernel_count += 2ull * count;
+    // launches issued (one per 32768 tokens), counted twice as the ABI
+    // append counts its one fused K and V launch
+    ctx->telemetry.kv_cache_kernel_count += 2ull * ((count + 32767u) / 32768u);
     return QWN_CUDA_STATUS_OK;
 }
 

@@ -1,5 +1,5 @@
 """Compile a probe against a qwn_cuda_abi.h and report every struct's size
-and field offsets (used by tests/test_abi_layout.py and the fixture
+and field offsets (used by tests/test_abi.py and the fixture
 generator tests/golden/make_abi_layout.py)."""
 import json
 import os

@@ -75,7 +75,8 @@ def test_abi_known_answer(gpu_ctx, oracle_lib):
     assert np.max(np.abs(y - expect)) <= 1e-3
     assert tm.gpu_matmul_count > before.gpu_matmul_count and tm.gpu_kernel_launch_count > 0
     assert tm.gpu_upload_count == before.gpu_upload_count + 1
-    assert tm.gpu_resident_bytes == before.gpu_resident_bytes + w.size
+    # the tensor's bytes and its MFMA-order copy, if one was made
+    assert tm.gpu_resident_bytes == before.gpu_resident_bytes + w.size + gpu_ctx.tensor_info(h).mfma_copy_bytes
     assert tm.kernel_type.startswith(b"hvsq2-74")
     gpu_ctx.release(h)
     assert gpu_ctx.telemetry().gpu_resident_bytes == before.gpu_resident_bytes
@@ -442,6 +443,67 @@ def test_memory_budget(hip_lib):
             ctx.upload(w, "hvsq2", 16, 256)
         assert e.value.status == -4
         ctx.upload(synth.hvsq2_weights(rng, 8, 256), "hvsq2", 8, 256)  # 592 bytes fits
+
+
+def _free_bytes():
+    import torch
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info(0)[0]
+
+
+def test_mfma_copy_charged_to_budget(hip_lib):
+    """The batched GEMM's MFMA-order copy is charged like the tensor's own
+    bytes (c/cuda/qwn_hypervsq2_cuda_abi.cu:554-562 caps every device byte a
+    tensor holds): tensors plus copies never exceed the budget,
+    gpu_resident_bytes reports both and equals the device memory the upload
+    took (hipMemGetInfo) up to the device layout's padding and allocation
+    rounding, release gives both back, and an upload of one tensor at a time
+    under a budget gets no copy (a later tensor would lose room to it)."""
+    rng = np.random.default_rng(11)
+    shapes = [(9728, 2560, "hvsq2"), (9728, 2560, "hvsq2"), (8960, 1536, "q4_0"), (2560, 9728, "hvsq2")]
+    items = [(synth.weights(kind, rng, n, k), kind, n, k) for n, k, kind in shapes]
+    logical = [w.nbytes for w, _, _, _ in items]
+    granule = 2 << 20  # hipMalloc rounding per allocation, at most
+    # no budget: every tensor copied (half the device stays free)
+    with abi.Context(hip_lib, device=0) as ctx:
+        ctx.upload_batch(items[:1])  # the upload pipeline's staging buffers, allocated once
+        base = ctx.telemetry().gpu_resident_bytes
+        free0 = _free_bytes()
+        hs = ctx.upload_batch(items[1:])
+        took = free0 - _free_bytes()
+        infos = [ctx.tensor_info(h) for h in hs]
+        assert all(i.mfma_copy_bytes > 0 for i in infos)
+        reported = ctx.telemetry().gpu_resident_bytes - base
+        assert reported == sum(i.logical_bytes + i.mfma_copy_bytes for i in infos)
+        device = sum(i.device_bytes + i.mfma_copy_bytes for i in infos)
+        assert abs(took - device) <= 2 * len(infos) * granule, (took, device)
+        assert abs(device - reported) <= 0.03 * reported, (device, reported)
+        ctx.release(hs[0])
+        assert ctx.telemetry().gpu_resident_bytes == base + reported - infos[0].logical_bytes - infos[0].mfma_copy_bytes
+    # a budget with room for the tensors and some copies: copies only from what
+    # the batch's tensors leave, never past the budget
+    with abi.Context(hip_lib, device=0) as probe:
+        copy_sizes = [probe.tensor_info(h).mfma_copy_bytes for h in probe.upload_batch(items)]
+    for extra in (0, copy_sizes[0], copy_sizes[0] + copy_sizes[1] + 4096, sum(copy_sizes)):
+        budget = sum(logical) + extra
+        with abi.Context(hip_lib, device=0, budget=budget) as ctx:
+            hs = ctx.upload_batch(items)
+            infos = [ctx.tensor_info(h) for h in hs]
+            copies = sum(i.mfma_copy_bytes for i in infos)
+            assert ctx.telemetry().gpu_resident_bytes == sum(logical) + copies <= budget
+            assert copies <= extra and (extra - copies) < max(copy_sizes)  # none left out that fit
+            # a GEMM on a tensor with and without its copy gives the same rows
+            x = rng.integers(-127, 128, size=(4, 2560), dtype=np.int8)
+            y = ctx.gemm(hs[0], x, 9728, 2560, scales=np.full(4, 0.01, np.float32))
+            with abi.Context(hip_lib, device=0) as ref_ctx:
+                h = ref_ctx.upload(items[0][0], "hvsq2", 9728, 2560)
+                y_ref = ref_ctx.gemm(h, x, 9728, 2560, scales=np.full(4, 0.01, np.float32))
+            np.testing.assert_allclose(y, y_ref, rtol=1e-5, atol=1e-5)
+    # one tensor at a time under a budget: no copies, every tensor fits
+    with abi.Context(hip_lib, device=0, budget=sum(logical) + sum(copy_sizes)) as ctx:
+        hs = [ctx.upload(w, kind, n, k) for w, kind, n, k in items]
+        assert all(ctx.tensor_info(h).mfma_copy_bytes == 0 for h in hs)
+        assert ctx.telemetry().gpu_resident_bytes == sum(logical)
 
 
 def test_device_enumeration(hip_lib):

@@ -53,8 +53,10 @@ def test_upload_batch_mixed(gpu_ctx, oracle_lib):
     try:
         after = gpu_ctx.telemetry()
         assert after.gpu_upload_count - before.gpu_upload_count == len(shapes)
+        # the tensors' bytes plus the MFMA-order copies made for them
         assert after.gpu_resident_bytes - before.gpu_resident_bytes == sum(
-            synth.weight_bytes(d, N, K) for d, N, K in shapes)
+            synth.weight_bytes(d, N, K) for d, N, K in shapes) + sum(
+            gpu_ctx.tensor_info(h).mfma_copy_bytes for h in hs)
         for h, w, (d, N, K) in zip(hs, ws, shapes):
             check(gpu_ctx, oracle_lib, h, d, w, N, K, rng)
     finally:

@@ -3,7 +3,9 @@ split partials live in the library's file-scope device array, for callers
 that cannot allocate) against qwn_hip_ext_kv_attention_device with a
 workspace, through the C ABI: two calls in a row, the second smaller, each
 bit-identical to the workspace variant and within 1e-4 of the oracle
-(c/tests/test_cuda_q8_kv.cu:158); a request beyond the array is refused."""
+(c/tests/test_cuda_q8_kv.cu:158); a request beyond the array is refused, and
+so is a call that would run while another stream's call still uses the
+array."""
 import ctypes
 
 import numpy as np
@@ -76,4 +78,45 @@ def test_noalloc_attention_refuses_oversize(gpu_ctx):
         assert rc == -1  # QWN_CUDA_STATUS_INVALID_ARGUMENT
         assert "device array" in gpu_ctx.lib.last_error()
     finally:
+        gpu_ctx.kv_destroy(h)
+
+
+def test_noalloc_attention_refuses_overlap(gpu_ctx):
+    """The device array is shared by every call on the GPU, so a call is
+    refused (QWN_CUDA_STATUS_UNAVAILABLE) while the previous one, enqueued
+    on another stream, has not run: here it waits behind ~20 ms of fp32
+    products.  A call on that same stream is ordered behind it and
+    accepted; once that stream has finished, a call on the other stream is
+    accepted again, and every accepted call's output is the same."""
+    import torch
+    dev = torch.device("cuda:0")
+    T, HK, D, H = 256, 8, 128, 32
+    scale = float(D ** -0.5)
+    h = gpu_ctx.kv_create(T, HK, D)
+    try:
+        main = torch.cuda.current_stream()
+        kv = torch.randn(T, HK * D, device=dev)
+        gpu_ctx.kv_append_device(h, kv.data_ptr(), kv.data_ptr(), T, stream=main.cuda_stream)
+        q = torch.randn(H * D, device=dev)
+        outs = [torch.full((H * D,), float("nan"), device=dev) for _ in range(3)]
+        torch.cuda.synchronize()
+        busy = torch.cuda.Stream()
+        a = torch.randn(4096, 4096, device=dev)
+        with torch.cuda.stream(busy):
+            for _ in range(20):
+                a = (a @ a) / 64.0
+        assert noalloc(gpu_ctx, h, q.data_ptr(), outs[0].data_ptr(), H, T - 1, scale, busy.cuda_stream) == 0
+        rc = noalloc(gpu_ctx, h, q.data_ptr(), outs[1].data_ptr(), H, T - 1, scale, main.cuda_stream)
+        assert rc == -3, f"overlapping call accepted (rc {rc})"  # QWN_CUDA_STATUS_UNAVAILABLE
+        assert "in use" in gpu_ctx.lib.last_error()
+        assert noalloc(gpu_ctx, h, q.data_ptr(), outs[1].data_ptr(), H, T - 1, scale, busy.cuda_stream) == 0
+        busy.synchronize()
+        assert noalloc(gpu_ctx, h, q.data_ptr(), outs[2].data_ptr(), H, T - 1, scale, main.cuda_stream) == 0
+        torch.cuda.synchronize()
+        ref = outs[0].cpu().numpy()
+        assert not np.isnan(ref).any()
+        for o in outs[1:]:
+            assert np.array_equal(o.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    finally:
+        torch.cuda.synchronize()
         gpu_ctx.kv_destroy(h)
