@@ -79,7 +79,9 @@ enum {
     /* EXT: F16 row-major tensors with QWN_CUDA_INPUT_F32 activations. */
     QWN_CUDA_CAP_F16_GEMV = 1ull << 7,
     /* EXT: the qwn_hip_ext_* device-pointer entry points (qwn_hip_ext.h). */
-    QWN_CUDA_CAP_DEVICE_POINTERS = 1ull << 8
+    QWN_CUDA_CAP_DEVICE_POINTERS = 1ull << 8,
+    /* EXT: BF16 row-major tensors with QWN_CUDA_INPUT_F32 activations. */
+    QWN_CUDA_CAP_BF16_GEMV = 1ull << 9
 };
 
 typedef enum {
@@ -97,13 +99,15 @@ typedef enum {
     /* EXT */
     QWN_CUDA_TENSOR_Q4_0_18 = 2,
     /* EXT: IEEE binary16, rows x cols row-major (cols fastest). */
-    QWN_CUDA_TENSOR_F16 = 3
+    QWN_CUDA_TENSOR_F16 = 3,
+    /* EXT: bfloat16 (the high half of a binary32), rows x cols row-major. */
+    QWN_CUDA_TENSOR_BF16 = 4
 } QwnCudaTensorDType;
 
 typedef enum {
     QWN_CUDA_INPUT_Q8 = 1,
     /* EXT: input_q8 points at fp32 activations [batch x input_stride];
-     * F16 tensors take them as is, quantized tensors quantize them per
+     * F16 and BF16 tensors take them as is, quantized tensors quantize them per
      * token on the device (the reference's host-side arithmetic). */
     QWN_CUDA_INPUT_F32 = 2
 } QwnCudaInputMode;

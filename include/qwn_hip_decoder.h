@@ -17,8 +17,9 @@
  *
  * Weights are the tensors of qwn_cuda_abi.h, already uploaded to the same
  * context (qwn_cuda_abi_upload_tensor): seven projections per layer
- * (HyperVSQ-2 or Q4_0, one dtype per decoder) and the F16 embedding, which
- * is also the tied LM head.  Norm weights are copied from the host at
+ * (HyperVSQ-2 or Q4_0, one dtype per decoder), the F16 or BF16 embedding
+ * (c/qwanto_decode.c:561), which is also the LM head unless an untied
+ * lm_head tensor is given.  Norm weights are copied from the host at
  * creation, and so are the optional per-head q/k norm weights of Qwen3
  * layers and the optional q/k/v/o projection biases.
  */
@@ -42,7 +43,7 @@ typedef struct {
     float rope_theta;
     float rms_eps;
     const QwnCudaTensorHandle *projections; /* [layers * 7]: q, k, v, o, gate, up, down */
-    const QwnCudaTensorHandle *embedding;   /* F16 [vocab][hidden] */
+    const QwnCudaTensorHandle *embedding;   /* F16 or BF16 [vocab][hidden] */
     const float *input_norms;               /* host [layers][hidden] */
     const float *post_norms;                /* host [layers][hidden] */
     const float *final_norm;                /* host [hidden] */
@@ -58,6 +59,12 @@ typedef struct {
     const float *k_biases;                  /* [layers][kv_heads * head_dim] */
     const float *v_biases;                  /* [layers][kv_heads * head_dim] */
     const float *o_biases;                  /* [layers][hidden] */
+    /* Optional untied LM head (lm_head.weight / output.weight,
+     * c/qwanto_decode.c:1074-1076): NULL, the embedding is the head; else a
+     * [vocab][hidden] tensor in F16, BF16, Q4_0 or HyperVSQ-2 (the quantized
+     * kinds quantize the final-norm output per token, as every quantized
+     * projection does, c/qwanto_decode.c:2007). */
+    const QwnCudaTensorHandle *lm_head;
 } QwnHipDecoderDesc;
 
 typedef struct {

@@ -11,9 +11,10 @@
  * activation quantization, one synchronous ABI call per projection,
  * telemetry mirrored into metrics, fail-closed), the Q8 KV calls
  * (:1657-1724) and the forward / greedy generate semantics
- * (:1566-2032, :2085-2125) of a dense Qwen2-style model.  Q4_0 and F16
- * tensors are routed through the ABI too (the library's extra dtypes), so
- * every projection and the tied LM head run on the GPU.
+ * (:1566-2032, :2085-2125) of a dense Qwen2-style model.  Q4_0, F16 and
+ * BF16 tensors are routed through the ABI too (the library's extra dtypes),
+ * so every projection and the LM head (tied, or lm_head.weight in any of
+ * those dtypes) run on the GPU.
  *
  * There is no CPU fallback: if the ABI library is missing or refuses a
  * call, the call fails and last_error says why.
@@ -28,6 +29,12 @@ extern "C" {
 #define QHD_PROJ_HVSQ2 1 /* 74-byte HyperVSQ-2 blocks */
 #define QHD_PROJ_Q4_0 2  /* 18-byte Q4_0 blocks */
 
+/* dtypes of the embedding (F16, BF16) and of an untied LM head (any) */
+#define QHD_DT_F16 1
+#define QHD_DT_Q4_0 2
+#define QHD_DT_BF16 4
+#define QHD_DT_HVSQ2 9
+
 typedef struct {
     int hidden, intermediate, layers, heads, kv_heads, head_dim, vocab, max_ctx;
     float rope_theta, rms_eps;
@@ -37,7 +44,7 @@ typedef struct {
 /* Host weights (row-major [out][in] blocks; kept alive by the caller). */
 typedef struct {
     QhdConfig cfg;
-    const uint16_t *embed;      /* F16 [vocab][hidden], tied LM head */
+    const uint16_t *embed;      /* [vocab][hidden] in embed_dtype; the LM head when lm_head is NULL */
     const float *final_norm;    /* [hidden] */
     const uint8_t *const *proj; /* [layers * 7]: q k v o gate up down */
     const float *const *norms;  /* [layers * 2]: input, post-attention */
@@ -47,6 +54,10 @@ typedef struct {
     const float *const *biases;   /* NULL, or [layers * 4]: q, k, v, o projection biases
                                      (self_attn.*_proj.bias), each NULL or [rows]
                                      (c/qwanto_decode.c:926-929, 1649-1651, 1722) */
+    int embed_dtype;              /* QHD_DT_F16 (also 0) or QHD_DT_BF16 (c/qwanto_decode.c:561) */
+    const void *lm_head;          /* NULL (tied), or lm_head.weight [vocab][hidden] in lm_head_dtype
+                                     (c/qwanto_decode.c:1074-1076) */
+    int lm_head_dtype;            /* QHD_DT_F16 / QHD_DT_BF16 / QHD_DT_Q4_0 / QHD_DT_HVSQ2 */
 } QhdModel;
 
 typedef struct {

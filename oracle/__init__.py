@@ -47,7 +47,12 @@ class QoModelConfig(ctypes.Structure):
 class QoModel(ctypes.Structure):
     _fields_ = [("cfg", QoModelConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
                 ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p)),
-                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p))]
+                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p)),
+                ("embed_dtype", ctypes.c_int), ("lm_head", ctypes.c_void_p), ("lm_head_dtype", ctypes.c_int)]
+
+
+# qwn_oracle.h QO_DT_*: the embedding's and an untied LM head's dtype
+DT_CODES = {"f16": 1, "bf16": 4, "q4_0": 2, "hvsq2": 9}
 
 
 BIAS_ORDER = ("q_bias", "k_bias", "v_bias", "o_bias")
@@ -81,7 +86,10 @@ def model_struct(model: dict) -> tuple:
                 proj=ctypes.cast(proj, ctypes.POINTER(ctypes.c_void_p)),
                 norms=ctypes.cast(norms, ctypes.POINTER(ctypes.c_void_p)),
                 qk_norms=ctypes.cast(qk, ctypes.POINTER(ctypes.c_void_p)) if qk is not None else None,
-                biases=ctypes.cast(bias, ctypes.POINTER(ctypes.c_void_p)) if bias is not None else None)
+                biases=ctypes.cast(bias, ctypes.POINTER(ctypes.c_void_p)) if bias is not None else None,
+                embed_dtype=DT_CODES[model.get("embed_dtype", "f16")],
+                lm_head=model["lm_head"].ctypes.data if "lm_head" in model else None,
+                lm_head_dtype=DT_CODES[model["lm_head_dtype"]] if "lm_head" in model else 0)
     return m, (proj, norms, qk, bias)
 
 
@@ -156,6 +164,9 @@ class Oracle:
         lib.qo_variant_name.restype = ctypes.c_char_p
         lib.qo_matmul_f16.argtypes = [_c_u16p, _c_f32p, ctypes.c_int, ctypes.c_int,
                                       ctypes.c_int, _c_f32p, ctypes.c_int]
+        lib.qo_matmul_bf16.argtypes = lib.qo_matmul_f16.argtypes
+        lib.qo_bf16_to_float.argtypes = [ctypes.c_uint16]
+        lib.qo_bf16_to_float.restype = ctypes.c_float
         lib.qo_q8_quantize_vector.argtypes = [_c_f32p, _c_i8p, _c_f32p, ctypes.c_int]
         lib.qo_q8_attention.argtypes = [_c_f32p, _c_i8p, _c_i8p, _c_f32p, _c_f32p,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -293,6 +304,19 @@ class Oracle:
                                M, K, N, ptr(y, ctypes.c_float), threads)
         return y
 
+    def matmul_bf16(self, w: np.ndarray, x: np.ndarray, threads: int = 1) -> np.ndarray:
+        """w: [N][K] bfloat16 bit patterns (uint16)."""
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        N, K = w.shape
+        M = x.shape[0]
+        y = np.zeros((M, N), dtype=np.float32)
+        self.lib.qo_matmul_bf16(w.ctypes.data_as(_c_u16p), ptr(x, ctypes.c_float), M, K, N,
+                                ptr(y, ctypes.c_float), threads)
+        return y
+
     # -- Q8 KV -----------------------------------------------------------------
     def q8_quantize(self, v: np.ndarray):
         v = np.ascontiguousarray(v, dtype=np.float32)
@@ -334,7 +358,7 @@ class Reference:
     def __init__(self, path: str = REF_SO):
         lib = ctypes.CDLL(path)
         self.lib = lib
-        for name in ("ref_matmul_q4_0", "ref_matmul_hvsq2", "ref_matmul_f16"):
+        for name in ("ref_matmul_q4_0", "ref_matmul_hvsq2", "ref_matmul_f16", "ref_matmul_bf16"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, _c_f32p, ctypes.c_int, ctypes.c_int,
                            ctypes.c_int, _c_f32p]
@@ -389,6 +413,11 @@ class Reference:
     def matmul_f16(self, w, x):
         w = np.ascontiguousarray(w, dtype=np.float16)
         return self._matmul(self.lib.ref_matmul_f16, w, x, w.shape[0])
+
+    def matmul_bf16(self, w, x):
+        """w: [N][K] bfloat16 bit patterns (uint16)."""
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        return self._matmul(self.lib.ref_matmul_bf16, w, x, w.shape[0])
 
     def quantize_token(self, x: np.ndarray):
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -561,8 +561,29 @@ void qo_hvsq2_octant_sums(const uint8_t *w, const int8_t *q8, int K, int N,
 /* a6: F16 generic matmul                                              */
 /* ------------------------------------------------------------------ */
 
+float qo_bf16_to_float(uint16_t h) {
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, sizeof(f));
+    return f;
+}
+
+static void matmul_half(const uint16_t *w, int bf16, const float *x, int M, int K, int N, float *y,
+                        int threads);
+
 void qo_matmul_f16(const uint16_t *w, const float *x, int M, int K, int N,
                    float *y, int threads) {
+    matmul_half(w, 0, x, M, K, N, y, threads);
+}
+
+void qo_matmul_bf16(const uint16_t *w, const float *x, int M, int K, int N,
+                    float *y, int threads) {
+    matmul_half(w, 1, x, M, K, N, y, threads);
+}
+
+/* Both 16-bit row formats: the row decoded to fp32, then the one loop. */
+static void matmul_half(const uint16_t *w, int bf16, const float *x, int M, int K, int N, float *y,
+                        int threads) {
 #if defined(_OPENMP)
     #pragma omp parallel num_threads(effective_threads(threads))
 #endif
@@ -574,7 +595,7 @@ void qo_matmul_f16(const uint16_t *w, const float *x, int M, int K, int N,
         for (int n = 0; n < N; n++) {
             if (!row) continue;
             const uint16_t *src = w + (size_t)n * K;
-            for (int k = 0; k < K; k++) row[k] = qo_half_to_float(src[k]);
+            for (int k = 0; k < K; k++) row[k] = bf16 ? qo_bf16_to_float(src[k]) : qo_half_to_float(src[k]);
             for (int t = 0; t < M; t++) {
                 const float *xr = x + (size_t)t * K;
                 /* GCC vectorises the products (eight, then one four-wide

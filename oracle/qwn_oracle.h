@@ -95,6 +95,16 @@ const char *qo_variant_name(int variant);
 void qo_matmul_f16(const uint16_t *w, const float *x, int M, int K, int N,
                    float *y, int threads);
 
+/* Exact bfloat16 -> binary32: the 16 bits become the high half
+ * (c/qwanto_kernels.c:287-290). */
+float qo_bf16_to_float(uint16_t h);
+
+/* The BF16 case of the same matmul: qwn_row_f32 decodes a BF16 row
+ * (c/qwanto_kernels.c:1508-1527), then the same loop as F16
+ * (:1605-1614). */
+void qo_matmul_bf16(const uint16_t *w, const float *x, int M, int K, int N,
+                    float *y, int threads);
+
 /* ---- Q8 KV cache --------------------------------------------------- */
 
 /* qwn_q8_quantize_vector (c/qwanto_turboquant.c:555-586): per 64-channel
@@ -138,9 +148,16 @@ typedef struct {
     int proj_dtype; /* QO_PROJ_* */
 } qo_model_config;
 
+/* dtypes of the embedding and of an untied LM head */
+#define QO_DT_F16 1
+#define QO_DT_BF16 4
+#define QO_DT_Q4_0 2
+#define QO_DT_HVSQ2 9
+
 typedef struct {
     qo_model_config cfg;
-    const uint16_t *embed;          /* F16 [vocab][hidden], tied LM head */
+    const uint16_t *embed;          /* [vocab][hidden], F16 or BF16 (embed_dtype); the LM head when
+                                       lm_head is NULL (tied) */
     const float *final_norm;        /* [hidden] */
     const uint8_t *const *proj;     /* [layers * 7]: q k v o gate up down blocks */
     const float *const *norms;      /* [layers * 2]: input, post attention */
@@ -149,6 +166,10 @@ typedef struct {
     const float *const *biases;     /* NULL, or [layers * 4]: q, k, v, o projection biases
                                        (self_attn.{q,k,v,o}_proj.bias), each NULL or
                                        [that projection's rows] */
+    int embed_dtype;                /* QO_DT_F16 or QO_DT_BF16 (0 = F16) */
+    const void *lm_head;            /* NULL (tied), or lm_head.weight [vocab][hidden] in lm_head_dtype
+                                       (c/qwanto_decode.c:1074-1076) */
+    int lm_head_dtype;              /* QO_DT_F16 / QO_DT_BF16 / QO_DT_Q4_0 / QO_DT_HVSQ2 */
 } qo_model;
 
 typedef struct qo_decoder qo_decoder;

@@ -13,6 +13,8 @@
  *   rmsnorm      c/qwanto_decode.c:627-652 (n % 8 == 0: eight fma lanes)
  *   RoPE table   :601-625 (glibc powf/cosf/sinf), rotation :686-729 (fma)
  *   SwiGLU       :1946-1949, residual vec_add, greedy argmax :2043-2065
+ * The embedding is F16 or BF16 (:561); the LM head is lm_head.weight when
+ * present (F16, BF16, Q4_0 or HyperVSQ-2), else the embedding (:1074-1076).
  */
 #include <math.h>
 #include <stdlib.h>
@@ -134,6 +136,24 @@ static int matmul(qo_decoder *d, const uint8_t *w, const float *x, int in, int o
     return rc;
 }
 
+/* The LM head (c/qwanto_decode.c:2007): lm_head.weight when the model has
+ * one, else the embedding (:1074-1076), through the matmul of its dtype
+ * (qwn_matmul_f32, c/qwanto_kernels.c:1531-1616: Q4_0 and HyperVSQ-2
+ * quantize the activation per call, F16 and BF16 decode rows). */
+static int lm_head(qo_decoder *d, const float *x, float *logits) {
+    const qo_model_config *c = &d->m.cfg;
+    const void *w = d->m.lm_head ? d->m.lm_head : (const void *)d->m.embed;
+    const int dt = d->m.lm_head ? d->m.lm_head_dtype : (d->m.embed_dtype ? d->m.embed_dtype : QO_DT_F16);
+    switch (dt) {
+    case QO_DT_F16: qo_matmul_f16((const uint16_t *)w, x, 1, c->hidden, c->vocab, logits, d->threads); return 0;
+    case QO_DT_BF16: qo_matmul_bf16((const uint16_t *)w, x, 1, c->hidden, c->vocab, logits, d->threads); return 0;
+    case QO_DT_Q4_0: return qo_matmul_q4_0((const uint8_t *)w, x, 1, c->hidden, c->vocab, logits, d->threads);
+    case QO_DT_HVSQ2:
+        return qo_matmul_hvsq2((const uint8_t *)w, x, 1, c->hidden, c->vocab, logits, d->threads, -1);
+    default: return -1;
+    }
+}
+
 void qo_decoder_set_perturbation(qo_decoder *d, uint32_t seed) {
     d->perturb = seed;
     d->calls = 0;
@@ -199,8 +219,12 @@ int qo_decoder_forward(qo_decoder *d, int token, float *logits_out) {
     const int Q = H * HD, KV = HK * HD, I = c->intermediate, groups = (KV + 63) / 64;
     const int pos = d->position, half = HD / 2;
     if (token < 0 || token >= c->vocab || pos >= c->max_ctx) return -1;
+    /* embedding row: F16 or BF16 (qwn_row_f32, c/qwanto_kernels.c:1508-1527) */
     const uint16_t *erow = d->m.embed + (size_t)token * D;
-    for (int i = 0; i < D; i++) d->x[i] = qo_half_to_float(erow[i]);
+    if (d->m.embed_dtype == QO_DT_BF16)
+        for (int i = 0; i < D; i++) d->x[i] = qo_bf16_to_float(erow[i]);
+    else
+        for (int i = 0; i < D; i++) d->x[i] = qo_half_to_float(erow[i]);
     const float *ct = d->rope_cos + (size_t)pos * half, *st = d->rope_sin + (size_t)pos * half;
     for (int l = 0; l < c->layers; l++) {
         const uint8_t *const *w = d->m.proj + (size_t)l * 7;
@@ -244,7 +268,7 @@ int qo_decoder_forward(qo_decoder *d, int token, float *logits_out) {
     }
     qo_rmsnorm(d->xb, d->x, d->m.final_norm, D, c->rms_eps);
     perturb_outputs(d, d->xb, D);
-    qo_matmul_f16(d->m.embed, d->xb, 1, D, c->vocab, d->logits, d->threads);
+    if (lm_head(d, d->xb, d->logits)) return -1;
     perturb_sums(d, d->logits, c->vocab);
     d->position++;
     if (logits_out) memcpy(logits_out, d->logits, (size_t)c->vocab * 4);

@@ -61,6 +61,11 @@ int ref_matmul_f16(const void *w, uint64_t bytes, const float *x, int M,
     return run_matmul(QWN_DT_F16, w, bytes, x, M, K, N, y);
 }
 
+int ref_matmul_bf16(const void *w, uint64_t bytes, const float *x, int M,
+                    int K, int N, float *y) {
+    return run_matmul(QWN_DT_BF16, w, bytes, x, M, K, N, y);
+}
+
 /* Quantize one token as the decoder does before a GPU call
  * (qwn_prepare_cuda_activation) and expose the block sums too. */
 int ref_quantize_token(const float *x, int K, int8_t *q8_out,

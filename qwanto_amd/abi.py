@@ -29,14 +29,17 @@ CAP_Q8_KV = 1 << 5
 CAP_Q4_0_GEMV = 1 << 6
 CAP_F16_GEMV = 1 << 7
 CAP_DEVICE_POINTERS = 1 << 8
+CAP_BF16_GEMV = 1 << 9
 
 TENSOR_HYPERVSQ2_74 = 1
 TENSOR_Q4_0_18 = 2
 TENSOR_F16 = 3
+TENSOR_BF16 = 4
 INPUT_Q8 = 1
 INPUT_F32 = 2
 
-DTYPES = {"hvsq2": (TENSOR_HYPERVSQ2_74, 74), "q4_0": (TENSOR_Q4_0_18, 18), "f16": (TENSOR_F16, 2)}
+DTYPES = {"hvsq2": (TENSOR_HYPERVSQ2_74, 74), "q4_0": (TENSOR_Q4_0_18, 18), "f16": (TENSOR_F16, 2),
+          "bf16": (TENSOR_BF16, 2)}
 
 EXPORTS = (
     "qwn_cuda_abi_query", "qwn_cuda_abi_get_capabilities", "qwn_cuda_abi_enumerate_devices",
@@ -187,7 +190,7 @@ class DecoderDesc(_Versioned):
                 ("input_norms", ctypes.c_void_p), ("post_norms", ctypes.c_void_p),
                 ("final_norm", ctypes.c_void_p), ("q_norms", ctypes.c_void_p), ("k_norms", ctypes.c_void_p),
                 ("q_biases", ctypes.c_void_p), ("k_biases", ctypes.c_void_p), ("v_biases", ctypes.c_void_p),
-                ("o_biases", ctypes.c_void_p)]
+                ("o_biases", ctypes.c_void_p), ("lm_head", ctypes.c_void_p)]
 
 
 class DecoderStats(_Versioned):
@@ -617,7 +620,8 @@ class Context:
 class ResidentDecoder:
     """The library's resident greedy decoder (include/qwn_hip_decoder.h) over a
     synth.decoder_model / qwn_file model dict: uploads the seven projections
-    per layer and the F16 embedding to `ctx`, then creates the decoder."""
+    per layer, the F16 or BF16 embedding and an untied LM head if the model
+    has one to `ctx`, then creates the decoder."""
 
     PROJ_ORDER = ("q", "k", "v", "o", "gate", "up", "down")
 
@@ -636,7 +640,10 @@ class ResidentDecoder:
             for p in self.PROJ_ORDER:
                 rows, cols = shapes[p]
                 self._tensors.append(ctx.upload(model["layers"][l][p], dtype, rows, cols))
-        self._embed = ctx.upload(model["embed"], "f16", cfg["vocab"], D)
+        self._embed = ctx.upload(model["embed"], model.get("embed_dtype", "f16"), cfg["vocab"], D)
+        self._head = None
+        if "lm_head" in model:
+            self._head = ctx.upload(model["lm_head"], model["lm_head_dtype"], cfg["vocab"], D)
         self._proj_arr = (Handle * len(self._tensors))(*self._tensors)
         self._norm_in = np.ascontiguousarray(np.stack([model["layers"][l]["input_norm"] for l in range(L)]),
                                              dtype=np.float32)
@@ -664,7 +671,8 @@ class ResidentDecoder:
                            embedding=ctypes.addressof(self._embed), input_norms=_p(self._norm_in),
                            post_norms=_p(self._norm_post), final_norm=_p(self._final),
                            q_norms=_p(self._qn), k_norms=_p(self._kn),
-                           **{p + "_biases": _p(self._bias.get(p)) for p in "qkvo"})
+                           **{p + "_biases": _p(self._bias.get(p)) for p in "qkvo"},
+                           lm_head=ctypes.addressof(self._head) if self._head is not None else None)
         self.handle = Handle()
         lib = ctx.lib
         lib.check("decoder_create", lib.lib.qwn_hip_decoder_create(ctx._h, ctypes.byref(desc),
@@ -736,9 +744,10 @@ class ResidentDecoder:
         if self.handle.opaque:
             self.ctx.lib.check("decoder_destroy", self.ctx.lib.lib.qwn_hip_decoder_destroy(
                 self.ctx._h, ctypes.byref(self.handle)))
-        for t in self._tensors + [self._embed]:
-            self.ctx.release(t)
-        self._tensors = []
+        for t in self._tensors + [self._embed, self._head]:
+            if t is not None:
+                self.ctx.release(t)
+        self._tensors, self._embed, self._head = [], None, None
 
 
 _LIB: Library | None = None

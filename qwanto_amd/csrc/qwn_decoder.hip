@@ -39,12 +39,13 @@ constexpr uint32_t kPrefillTokens = 16;  // prompt tokens per prefill block (the
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN };
 
 // x = embedding row of the step's token (feed[pos] when the host supplied
-// one, else the previous step's greedy choice): F16 -> fp32 straight from
-// the LM head's wave-tile layout.  One thread per 8 halves.
+// one, else the previous step's greedy choice): F16 or BF16 -> fp32 straight
+// from the embedding's wave-tile layout.  One thread per 8 values.
 struct EmbedArgs {
     const uint8_t *payload;
     size_t tile_payload;
     uint32_t lanes, rows_per_wave, units, hidden, vocab, max_ctx;
+    uint32_t bf16;  // BF16 rows (c/qwanto_decode.c:561): the 16 bits are the high half
     const int32_t *feed;
     const int32_t *state;  // [0] = last greedy token, [1] = position
     float *x;
@@ -55,6 +56,10 @@ struct EmbedArgs {
     uint32_t half;
     float *rope_row;
 };
+
+__device__ __forceinline__ float embed_value(uint32_t raw, uint32_t bf16) {
+    return bf16 ? __builtin_bit_cast(float, raw << 16) : half_to_float(raw);
+}
 
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -76,7 +81,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     const uint32_t k0 = u * 32 + q * 8;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-        if (k0 + e < a.hidden) a.x[k0 + e] = half_to_float((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        if (k0 + e < a.hidden) a.x[k0 + e] = embed_value((w[e >> 1] >> (16 * (e & 1))) & 0xffffu, a.bf16);
 }
 
 // Prefill block: x[i] = embedding row of feed[p0 + i] for the block's
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256) void prefill_embed_kernel(EmbedArgs a, uint32_
     float *xi = x + static_cast<size_t>(i) * a.hidden;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-        if (k0 + e < a.hidden) xi[k0 + e] = half_to_float((w[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+        if (k0 + e < a.hidden) xi[k0 + e] = embed_value((w[e >> 1] >> (16 * (e & 1))) & 0xffffu, a.bf16);
 }
 
 // End of a prefill block: the device position moves past the block, or, in
@@ -144,6 +149,7 @@ struct Decoder {
     float eps = 0.0f, attn_scale = 0.0f;
     std::vector<const DeviceTensor *> proj;
     const DeviceTensor *embed = nullptr;
+    const DeviceTensor *head = nullptr;  // the LM head: an untied lm_head tensor, or embed
     void *allocation = nullptr;
     float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gate = nullptr,
           *up = nullptr, *logits = nullptr, *partials = nullptr;
@@ -234,22 +240,40 @@ EmbedArgs embed_args(const Decoder *d) {
     ea.sin_tab = d->sin_tab;
     ea.half = d->head_dim / 2;
     ea.rope_row = d->rope_row;
+    ea.bf16 = d->embed->bf16 ? 1u : 0u;
     return ea;
 }
 
-// The LM head on the fp32 residual x: final RMSNorm into the F16 image,
-// the image-mode GEMV with per-workgroup argmax partials (fewer registers
-// than the fused prologue: more waves per CU in flight), and the step end
-// that records the greedy token at the device position and advances it.
-hipError_t enqueue_head(Decoder *d, const float *x, hipStream_t s) {
-    hipError_t e;
-    if ((e = launch_norm_image(*d->embed, x, d->final_norm, d->eps, d->head_image, s)) != hipSuccess) return e;
-    GemvGroupLaunch head = group({d->embed}, {d->logits});
-    head.image = d->head_image;
-    head.image_stride = static_cast<uint32_t>(image_bytes(kF16, d->embed->units));
+// The LM head launch of one token, with per-workgroup argmax partials.  An
+// F16 or BF16 head reads an fp32 image of the final RMSNorm output (built by
+// the norm kernel: the image-mode GEMV takes fewer registers than the fused
+// prologue, so more waves per CU are in flight); a Q4_0 or HyperVSQ-2 head
+// normalizes and quantizes x in its own prologue, as the projections do.
+GemvGroupLaunch head_launch(const Decoder *d, const float *x) {
+    GemvGroupLaunch head = group({d->head}, {d->logits});
+    if (d->head->kind == kF16) {
+        head.image = d->head_image;
+        head.image_stride = static_cast<uint32_t>(image_bytes(kF16, d->head->units));
+    } else {
+        head.input_mode = kInNorm;
+        head.x = x;
+        head.norm = d->final_norm;
+        head.eps = d->eps;
+    }
     head.output_mode = kOutArgmax;
     head.argmax_partials = d->argmax;
-    if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
+    return head;
+}
+
+// The LM head on the fp32 residual x (c/qwanto_decode.c:2000-2007) and the
+// step end that records the greedy token at the device position and
+// advances it.
+hipError_t enqueue_head(Decoder *d, const float *x, hipStream_t s) {
+    hipError_t e;
+    if (d->head->kind == kF16 &&
+        (e = launch_norm_image(*d->head, x, d->final_norm, d->eps, d->head_image, s)) != hipSuccess)
+        return e;
+    if ((e = launch_gemv_group(head_launch(d, x), s)) != hipSuccess) return e;
     hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(1024), 0, s, d->argmax, d->argmax_n, d->state,
                        d->out_tokens, d->max_ctx);
     return hipGetLastError();
@@ -358,12 +382,18 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (last) return enqueue_head(d, d->px + static_cast<size_t>(m - 1) * D, s);
     if (kind == kBlockVerify) {
-        if ((e = launch_norm_image(*d->embed, d->px, d->final_norm, d->eps, d->vimg, s, m, D, d->vimg_stride)) !=
-            hipSuccess)
-            return e;
-        GemvGroupLaunch head = group({d->embed}, {d->vlogits});
+        // the head on every token: fp32 images (F16/BF16) or per-token int8
+        // images of the normalized tokens (Q4_0/HyperVSQ-2), one batched GEMV
+        if (d->head->kind == kF16)
+            e = launch_norm_image(*d->head, d->px, d->final_norm, d->eps, d->vimg, s, m, D, d->vimg_stride);
+        else
+            e = launch_prepare_image(*d->head, kInNorm, d->px, nullptr, d->final_norm, d->eps, m, D, d->vimg,
+                                     d->vimg_stride, d->pscales, nullptr, 0, s);
+        if (e != hipSuccess) return e;
+        GemvGroupLaunch head = group({d->head}, {d->vlogits});
         head.image = d->vimg;
         head.image_stride = d->vimg_stride;
+        if (d->head->kind != kF16) head.scales = d->pscales;
         head.batch = m;
         head.output_stride[0] = d->vocab;
         if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
@@ -571,13 +601,19 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
             if (t) d->weight_bytes += logical_bytes(*t);
         }
     d->embed = ok ? check_shape(ctx, *desc->embedding, kF16, d->vocab, D) : nullptr;
-    if (!ok || !d->embed) {
+    d->head = d->embed;
+    if (ok && desc->lm_head) {
+        ResidentTensor *rh = tensor_of(ctx, *desc->lm_head);
+        d->head = rh && rh->t.rows == d->vocab && rh->t.cols == D ? &rh->t : nullptr;
+    }
+    if (!ok || !d->embed || !d->head) {
         delete d;
         set_error("decoder weights do not match the configuration (one quantized dtype for all projections, "
-                  "F16 [vocab][hidden] embedding)");
+                  "F16/BF16 [vocab][hidden] embedding, lm_head [vocab][hidden] if given)");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
-    d->weight_bytes += d->embed->logical_bytes;
+    // per step the LM head is read whole; the embedding only one row
+    d->weight_bytes += d->head->logical_bytes;
 
     // device memory: activations, tables, caches, state
     std::vector<std::pair<void **, size_t>> parts;
@@ -628,7 +664,8 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
             part(reinterpret_cast<void **>(&d->pmimg),
                  std::max({mfma_image_bytes(*d->proj[P_DOWN]), mfma_image_bytes(*d->proj[P_Q]),
                            mfma_image_bytes(*d->proj[P_O])}));
-        d->vimg_stride = static_cast<uint32_t>((image_bytes(kF16, d->embed->units) + 15) & ~static_cast<size_t>(15));
+        d->vimg_stride =
+            static_cast<uint32_t>((image_bytes(d->head->kind, d->head->units) + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
         part(reinterpret_cast<void **>(&d->vlogits), P * d->vocab * 4);
         part(reinterpret_cast<void **>(&d->vids), P * 4);
@@ -648,14 +685,18 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
          std::max<size_t>(d->fused_attention ? decode_attention_workspace_floats(proto, d->heads, d->max_ctx)
                                              : attention_at_workspace_floats(proto, d->heads),
                           1) * 4);
-    GemvGroupLaunch head = group({d->embed}, {nullptr});
-    head.outputs[0] = reinterpret_cast<float *>(16);  // validity only: a non-null placeholder
-    head.image = reinterpret_cast<const void *>(16);
-    head.output_mode = kOutArgmax;
-    head.argmax_partials = reinterpret_cast<uint64_t *>(16);
-    d->argmax_n = gemv_group_grid(head);
+    {
+        // the head launch's shape; its buffers are not placed yet, so
+        // non-null placeholders stand in for them (validity only)
+        GemvGroupLaunch head = head_launch(d, reinterpret_cast<const float *>(16));
+        head.outputs[0] = reinterpret_cast<float *>(16);
+        head.argmax_partials = reinterpret_cast<uint64_t *>(16);
+        if (head.input_mode == kInImage) head.image = reinterpret_cast<const void *>(16);
+        else head.norm = reinterpret_cast<const float *>(16);
+        d->argmax_n = gemv_group_grid(head);
+    }
     part(reinterpret_cast<void **>(&d->argmax), static_cast<size_t>(d->argmax_n) * 8);
-    part(reinterpret_cast<void **>(&d->head_image), image_bytes(kF16, d->embed->units));
+    part(reinterpret_cast<void **>(&d->head_image), image_bytes(kF16, d->head->units));
     // every grouped launch of the step must accept its fused input
     bool fits = d->argmax_n > 0;
     {
@@ -750,7 +791,8 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
                            : 1 + (mfma_attention_supported(proto, d->heads) ? mfma_attention_launches(proto, d->heads, d->max_ctx)
                                                                            : 2);
     d->layer_launches = 4 + attention_launches;
-    d->launches = d->layer_launches * d->layers + 4;  // + embed, norm image, LM head, step end
+    // + embed, the norm image (F16/BF16 heads), LM head, step end
+    d->launches = d->layer_launches * d->layers + (d->head->kind == kF16 ? 4 : 3);
     ctx->decoders.push_back(d);
     std::memset(out, 0, sizeof(*out));
     qwn_cuda_abi_header_init(&out->header, sizeof(*out));

@@ -361,6 +361,7 @@ struct GemvArgs {
     uint32_t output_stride[kMaxGroup];  // elements between tokens, per job
     uint64_t *argmax_partials;
     const float *bias[kMaxGroup];       // per job: null, or [rows] added to the product
+    uint32_t bf16;                      // kF16 layout holding bfloat16 weights
 };
 
 // Separately rounded product and sum (never contracted into an fma).
@@ -730,10 +731,19 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             for (int q = 0; q < 4; ++q) {
                 const uint32_t h[4] = {pay[i][q].x, pay[i][q].y, pay[i][q].z, pay[i][q].w};
                 float wf[8];
+                if (a.bf16) {
+                    // bfloat16: the 16 bits are the high half of the fp32 value
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    wf[2 * k] = half_to_float(h[k] & 0xffffu);
-                    wf[2 * k + 1] = half_to_float(h[k] >> 16);
+                    for (int k = 0; k < 4; ++k) {
+                        wf[2 * k] = __builtin_bit_cast(float, h[k] << 16);
+                        wf[2 * k + 1] = __builtin_bit_cast(float, h[k] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        wf[2 * k] = half_to_float(h[k] & 0xffffu);
+                        wf[2 * k + 1] = half_to_float(h[k] >> 16);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
@@ -2221,6 +2231,7 @@ GemvArgs args_of(const DeviceTensor &t) {
     a.image_bytes = static_cast<uint32_t>(image_bytes(t.kind, t.units));
     a.cols = t.cols;
     a.scale = 1.0f;
+    a.bf16 = t.bf16 ? 1u : 0u;
     return a;
 }
 
@@ -2468,8 +2479,9 @@ bool group_valid(const GemvGroupLaunch &g) {
     if (g.njobs < 1 || g.njobs > kMaxGroup) return false;
     const DeviceTensor &t0 = *g.tensors[0];
     for (int i = 0; i < g.njobs; ++i) {
+        if (!g.tensors[i] || !g.outputs[i]) return false;
         const DeviceTensor &t = *g.tensors[i];
-        if (!g.tensors[i] || !g.outputs[i] || t.kind != t0.kind || t.cols != t0.cols || t.units != t0.units ||
+        if (t.kind != t0.kind || t.bf16 != t0.bf16 || t.cols != t0.cols || t.units != t0.units ||
             t.lanes != t0.lanes || t.upl != t0.upl || t.rows_per_wave != t0.rows_per_wave)
             return false;
     }

@@ -23,7 +23,8 @@
 //               reference kernels never read them either)
 //   Q4_0:       chunk q = the 16 nibble bytes of block 4u+q; meta = the
 //               four fp16 block scales (zero for padding blocks)
-//   F16:        chunk q = halves 8q..8q+7 of the unit, no meta
+//   F16:        chunk q = halves 8q..8q+7 of the unit, no meta (BF16
+//               tensors use the same layout, flagged DeviceTensor::bf16)
 // Rows past the matrix end (the last tile) are stored as zeros.
 #pragma once
 
@@ -71,6 +72,7 @@ struct DeviceTensor {
     size_t tile_meta_bytes = 0;
     uint8_t *payload = nullptr;
     uint8_t *meta = nullptr;     // null for F16
+    bool bf16 = false;           // kF16 layout holding bfloat16 weights (the high halves of fp32)
     uint64_t device_bytes = 0;   // bytes allocated on the device
     uint64_t logical_bytes = 0;  // algorithmic (on-disk) bytes
     // HyperVSQ-2 MFMA staging: gaps (16-byte pieces after every 64) of the

@@ -78,11 +78,11 @@ void copy_telemetry(const Context *ctx, QwnCudaTelemetry *out) {
     if (out) *out = ctx->telemetry;
 }
 
-const char *kernel_name(int kind) {
-    switch (kind) {
+const char *kernel_name(const qwn::DeviceTensor &t) {
+    switch (t.kind) {
     case qwn::kHvsq2: return "hvsq2-74-q8-gfx950";
     case qwn::kQ4_0: return "q4_0-18-q8-gfx950";
-    case qwn::kF16: return "f16-f32-gfx950";
+    case qwn::kF16: return t.bf16 ? "bf16-f32-gfx950" : "f16-f32-gfx950";
     default: return "none";
     }
 }
@@ -244,7 +244,7 @@ int execute_gemm(Context *ctx, const QwnCudaGemmRequest *r, QwnCudaTelemetry *te
     tm.gpu_sync_ms += sync_ms;
     tm.gpu_resident_bytes = ctx->resident;
     tm.device_id = ctx->device;
-    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", kernel_name(t.kind));
+    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", kernel_name(t));
     copy_telemetry(ctx, telemetry);
     return QWN_CUDA_STATUS_OK;
 }
@@ -322,7 +322,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_query(QwnCudaAbiInfo *info) {
                             QWN_CUDA_CAP_RESIDENT_WEIGHTS | QWN_CUDA_CAP_TELEMETRY |
                             QWN_CUDA_CAP_DEVICE_ENUMERATION | QWN_CUDA_CAP_Q8_KV |
                             QWN_CUDA_CAP_Q4_0_GEMV | QWN_CUDA_CAP_F16_GEMV |
-                            QWN_CUDA_CAP_DEVICE_POINTERS;
+                            QWN_CUDA_CAP_DEVICE_POINTERS | QWN_CUDA_CAP_BF16_GEMV;
     info->max_devices = 16;
     info->max_resident_tensors = QWN_CUDA_MAX_RESIDENT_TENSORS;
     info->hypervsq2_block_bytes = QWN_CUDA_HYPERVSQ2_BLOCK_BYTES;
@@ -422,7 +422,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_context_create(const QwnCudaContextOptions *op
     hipDeviceProp_t p{};
     if (hipGetDeviceProperties(&p, ctx->device) == hipSuccess)
         std::snprintf(tm.device_name, sizeof(tm.device_name), "%s (%s)", p.name, p.gcnArchName);
-    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", kernel_name(qwn::kHvsq2));
+    std::snprintf(tm.kernel_type, sizeof(tm.kernel_type), "%s", "hvsq2-74-q8-gfx950");
     std::snprintf(tm.kv_cache_kernel_type, sizeof(tm.kv_cache_kernel_type), "Unavailable");
     std::memset(handle, 0, sizeof(*handle));
     qwn_cuda_abi_header_init(&handle->header, sizeof(*handle));
@@ -490,8 +490,10 @@ int describe_upload(const QwnCudaTensorUpload *up, DeviceTensor &t) {
         t.logical_bytes = static_cast<uint64_t>(up->rows) * ((up->cols + 31u) / 32u) * 18u;
         break;
     case QWN_CUDA_TENSOR_F16:
+    case QWN_CUDA_TENSOR_BF16:
         if (up->block_bytes != 2) break;
         t.kind = qwn::kF16;
+        t.bf16 = up->dtype == QWN_CUDA_TENSOR_BF16;
         t.logical_bytes = static_cast<uint64_t>(up->rows) * up->cols * 2u;
         break;
     default:
@@ -958,7 +960,9 @@ QWN_CUDA_ABI_API int qwn_hip_ext_tensor_info(const QwnCudaTensorHandle *h, QwnHi
     std::memset(info, 0, sizeof(*info));
     qwn_cuda_abi_header_init(&info->header, sizeof(*info));
     info->dtype = t.kind == qwn::kHvsq2 ? QWN_CUDA_TENSOR_HYPERVSQ2_74
-                                        : (t.kind == qwn::kQ4_0 ? QWN_CUDA_TENSOR_Q4_0_18 : QWN_CUDA_TENSOR_F16);
+                  : t.kind == qwn::kQ4_0 ? QWN_CUDA_TENSOR_Q4_0_18
+                  : t.bf16               ? QWN_CUDA_TENSOR_BF16
+                                         : QWN_CUDA_TENSOR_F16;
     info->rows = t.rows;
     info->cols = t.cols;
     info->units_per_row = t.units;

@@ -236,9 +236,12 @@ static int load_abi(QhdDecoder *d, const char *path, int device) {
         set_reason(d, "cuda_context_creation_failed_device_%d", device);
         return -1;
     }
-    const uint64_t need = QWN_CUDA_CAP_F16_GEMV | (d->m.cfg.proj_dtype == QHD_PROJ_Q4_0 ? QWN_CUDA_CAP_Q4_0_GEMV : 0);
+    const int head_dt = d->m.lm_head ? d->m.lm_head_dtype : (d->m.embed_dtype ? d->m.embed_dtype : QHD_DT_F16);
+    const uint64_t need = (head_dt == QHD_DT_F16 ? QWN_CUDA_CAP_F16_GEMV : 0) |
+                          (head_dt == QHD_DT_BF16 ? QWN_CUDA_CAP_BF16_GEMV : 0) |
+                          (d->m.cfg.proj_dtype == QHD_PROJ_Q4_0 || head_dt == QHD_DT_Q4_0 ? QWN_CUDA_CAP_Q4_0_GEMV : 0);
     if ((a->caps.capability_bits & need) != need) {
-        fail(d, "the ABI library lacks F16 / Q4_0 support (capabilities 0x%llx)",
+        fail(d, "the ABI library lacks F16 / BF16 / Q4_0 support (capabilities 0x%llx)",
              (unsigned long long)a->caps.capability_bits);
         set_reason(d, "qwn_hip_q4_0_f16_capability_unavailable");
         return -1;
@@ -378,8 +381,9 @@ static int gemv(QhdDecoder *d, int slot, const void *input, float scale, uint32_
     return 0;
 }
 
-static int matmul(QhdDecoder *d, const uint8_t *w, const float *x, int in, int out, float *y) {
-    const int q4 = d->m.cfg.proj_dtype == QHD_PROJ_Q4_0;
+/* A quantized matmul (Q4_0 or HyperVSQ-2 blocks): the activation quantized
+ * on the host, one GEMV call (c/qwanto_decode.c:776-924). */
+static int matmul_q(QhdDecoder *d, const uint8_t *w, int q4, const float *x, int in, int out, float *y) {
     const uint64_t row_bytes = q4 ? (uint64_t)(in + 31) / 32 * 18 : (uint64_t)(in + 255) / 256 * 74;
     const int slot = resident_slot(d, w, q4 ? QWN_CUDA_TENSOR_Q4_0_18 : QWN_CUDA_TENSOR_HYPERVSQ2_74,
                                    q4 ? 18 : 74, row_bytes * (uint64_t)out, out, in);
@@ -388,10 +392,21 @@ static int matmul(QhdDecoder *d, const uint8_t *w, const float *x, int in, int o
     return gemv(d, slot, d->q8, scale, QWN_CUDA_INPUT_Q8, in, out, y);
 }
 
+static int matmul(QhdDecoder *d, const uint8_t *w, const float *x, int in, int out, float *y) {
+    return matmul_q(d, w, d->m.cfg.proj_dtype == QHD_PROJ_Q4_0, x, in, out, y);
+}
+
+/* The LM head (c/qwanto_decode.c:2007): lm_head.weight when the model has
+ * one, else the embedding (:1074-1076).  F16 / BF16 rows take the fp32
+ * activation; Q4_0 / HyperVSQ-2 blocks quantize it as every projection. */
 static int lm_head(QhdDecoder *d, const float *x, float *logits) {
     const QhdConfig *c = &d->m.cfg;
-    const int slot = resident_slot(d, d->m.embed, QWN_CUDA_TENSOR_F16, 2, (uint64_t)c->vocab * c->hidden * 2,
-                                   c->vocab, c->hidden);
+    const void *w = d->m.lm_head ? d->m.lm_head : (const void *)d->m.embed;
+    const int dt = d->m.lm_head ? d->m.lm_head_dtype : (d->m.embed_dtype ? d->m.embed_dtype : QHD_DT_F16);
+    if (dt == QHD_DT_Q4_0 || dt == QHD_DT_HVSQ2)
+        return matmul_q(d, (const uint8_t *)w, dt == QHD_DT_Q4_0, x, c->hidden, c->vocab, logits);
+    const int slot = resident_slot(d, w, dt == QHD_DT_BF16 ? QWN_CUDA_TENSOR_BF16 : QWN_CUDA_TENSOR_F16, 2,
+                                   (uint64_t)c->vocab * c->hidden * 2, c->vocab, c->hidden);
     if (slot < 0) return -1;
     return gemv(d, slot, x, 0.0f, QWN_CUDA_INPUT_F32, c->hidden, c->vocab, logits);
 }
@@ -529,8 +544,16 @@ int qhd_forward(QhdDecoder *d, int token, float *logits_out) {
         fail(d, "token %d or position %d out of range", token, pos);
         return -1;
     }
+    /* embedding row: F16 or BF16 (qwn_row_f32, c/qwanto_kernels.c:1508-1527) */
     const uint16_t *erow = d->m.embed + (size_t)token * D;
-    for (int i = 0; i < D; i++) d->x[i] = half_to_float(erow[i]);
+    if (d->m.embed_dtype == QHD_DT_BF16) {
+        for (int i = 0; i < D; i++) {
+            const uint32_t bits = (uint32_t)erow[i] << 16;
+            memcpy(&d->x[i], &bits, sizeof(float));
+        }
+    } else {
+        for (int i = 0; i < D; i++) d->x[i] = half_to_float(erow[i]);
+    }
     const float *ct = d->rope_cos + (size_t)pos * half, *st = d->rope_sin + (size_t)pos * half;
     for (int l = 0; l < c->layers; l++) {
         const uint8_t *const *w = d->m.proj + (size_t)l * PROJ_COUNT;

@@ -24,7 +24,12 @@ class QhdConfig(ctypes.Structure):
 class QhdModel(ctypes.Structure):
     _fields_ = [("cfg", QhdConfig), ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
                 ("proj", ctypes.POINTER(ctypes.c_void_p)), ("norms", ctypes.POINTER(ctypes.c_void_p)),
-                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p))]
+                ("qk_norms", ctypes.POINTER(ctypes.c_void_p)), ("biases", ctypes.POINTER(ctypes.c_void_p)),
+                ("embed_dtype", ctypes.c_int), ("lm_head", ctypes.c_void_p), ("lm_head_dtype", ctypes.c_int)]
+
+
+# include/qwn_host_decoder.h QHD_DT_*
+DT_CODES = {"f16": 1, "q4_0": 2, "bf16": 4, "hvsq2": 9}
 
 
 class QhdMetrics(ctypes.Structure):
@@ -70,7 +75,10 @@ def model_struct(model: dict):
     m = QhdModel(cfg=c, embed=model["embed"].ctypes.data, final_norm=model["final_norm"].ctypes.data,
                  proj=ctypes.cast(proj, P), norms=ctypes.cast(norms, P),
                  qk_norms=ctypes.cast(qk, P) if qk is not None else None,
-                 biases=ctypes.cast(bias, P) if bias is not None else None)
+                 biases=ctypes.cast(bias, P) if bias is not None else None,
+                 embed_dtype=DT_CODES[model.get("embed_dtype", "f16")],
+                 lm_head=model["lm_head"].ctypes.data if "lm_head" in model else None,
+                 lm_head_dtype=DT_CODES[model["lm_head_dtype"]] if "lm_head" in model else 0)
     return m, (proj, norms, qk, bias)
 
 

@@ -189,6 +189,8 @@ class QwnFile:
             return raw.view(np.float32).reshape(t["shape"][::-1])
         if t["dtype"] == DT_F16:
             return raw.view(np.float16).reshape(t["shape"][::-1])
+        if t["dtype"] == DT_BF16:  # bit patterns
+            return raw.view(np.uint16).reshape(t["shape"][::-1])
         return raw
 
     def json(self, name: str):
@@ -197,6 +199,7 @@ class QwnFile:
 
 # ---- decoder models -------------------------------------------------------------
 
+_HEAD_DT = {"f16": DT_F16, "bf16": DT_BF16, "q4_0": DT_Q4_0, "hvsq2": DT_HYPER_VSQ2}
 _PROJ_NAMES = {"q": "self_attn.q_proj.weight", "k": "self_attn.k_proj.weight",
                "v": "self_attn.v_proj.weight", "o": "self_attn.o_proj.weight",
                "gate": "mlp.gate_proj.weight", "up": "mlp.up_proj.weight",
@@ -206,8 +209,9 @@ _PROJ_NAMES = {"q": "self_attn.q_proj.weight", "k": "self_attn.k_proj.weight",
 def write_decoder_model(path: str, model: dict) -> int:
     """Write a synthetic dense decoder (qwanto_amd.synth.decoder_model) as a
     .qwn file the reference decoder opens: __qwn.config (HF-style JSON),
-    a minimal __qwn.tokenizer, tied F16 embedding, F32 norms, and the
-    quantized projections."""
+    a minimal __qwn.tokenizer, the F16 or BF16 embedding, F32 norms, the
+    quantized projections and, for an untied model, lm_head.weight
+    (c/qwanto_decode.c:1074-1076)."""
     cfg = model["cfg"]
     D, V = cfg["hidden"], cfg["vocab"]
     qdt = DT_Q4_0 if model["dtype"] == "q4_0" else DT_HYPER_VSQ2
@@ -216,12 +220,13 @@ def write_decoder_model(path: str, model: dict) -> int:
           "num_key_value_heads": cfg["kv_heads"], "head_dim": cfg["head_dim"], "vocab_size": V,
           "max_position_embeddings": cfg["max_ctx"], "rms_norm_eps": cfg["rms_eps"],
           "rope_theta": cfg["rope_theta"], "bos_token_id": -1, "eos_token_id": -1,
-          "tie_word_embeddings": True}
+          "tie_word_embeddings": "lm_head" not in model}
     tok = {"model": {"type": "BPE", "vocab": {f"t{i}": i for i in range(V)}, "merges": []},
            "added_tokens": []}
     cj, tj = json.dumps(hf).encode(), json.dumps(tok).encode()
     tensors = [("__qwn.config", DT_BYTES, (len(cj),), cj), ("__qwn.tokenizer", DT_BYTES, (len(tj),), tj),
-               ("model.embed_tokens.weight", DT_F16, (D, V), model["embed"])]
+               ("model.embed_tokens.weight", DT_BF16 if model.get("embed_dtype") == "bf16" else DT_F16, (D, V),
+                model["embed"])]
     for l, layer in enumerate(model["layers"]):
         pre = f"model.layers.{l}."
         tensors.append((pre + "input_layernorm.weight", DT_F32, (D,), layer["input_norm"]))
@@ -237,6 +242,8 @@ def write_decoder_model(path: str, model: dict) -> int:
                 tensors.append((pre + f"self_attn.{p}_proj.bias", DT_F32, (model["shapes"][p][0],),
                                 layer[p + "_bias"]))
     tensors.append(("model.norm.weight", DT_F32, (D,), model["final_norm"]))
+    if "lm_head" in model:
+        tensors.append(("lm_head.weight", _HEAD_DT[model["lm_head_dtype"]], (D, V), model["lm_head"]))
     dims = (D, cfg["intermediate"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["layers"], V,
             cfg["max_ctx"])
     return write_qwn(path, tensors, arch_dims=dims,
@@ -270,6 +277,12 @@ def read_decoder_model(path: str) -> dict:
             shapes[p] = (t["shape"][1], t["shape"][0])
             layer[p] = f.raw(pre + suffix)
         layers.append(layer)
-    return {"cfg": cfg, "dtype": dtype, "shapes": shapes, "layers": layers,
-            "embed": f.array("model.embed_tokens.weight"), "final_norm": f.array("model.norm.weight"),
-            "file": f}
+    model = {"cfg": cfg, "dtype": dtype, "shapes": shapes, "layers": layers,
+             "embed": f.array("model.embed_tokens.weight"),
+             "embed_dtype": "bf16" if f.tensors["model.embed_tokens.weight"]["dtype"] == DT_BF16 else "f16",
+             "final_norm": f.array("model.norm.weight"), "file": f}
+    if "lm_head.weight" in f.tensors:
+        dt = {v: k for k, v in _HEAD_DT.items()}[f.tensors["lm_head.weight"]["dtype"]]
+        model["lm_head"] = f.array("lm_head.weight") if dt in ("f16", "bf16") else f.raw("lm_head.weight")
+        model["lm_head_dtype"] = dt
+    return model

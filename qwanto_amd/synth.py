@@ -85,6 +85,21 @@ def f16_weights(rng: np.random.Generator, rows: int, cols: int,
     return rng.normal(0.0, std, (rows, cols)).astype(np.float16)
 
 
+def to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    """fp32 -> bfloat16 bit patterns (uint16), rounded to nearest even."""
+    b = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint32) << 16).view(np.float32)
+
+
+def bf16_weights(rng: np.random.Generator, rows: int, cols: int, std: float = 0.02) -> np.ndarray:
+    """[rows][cols] bfloat16 bit patterns (uint16) of N(0, std) draws."""
+    return to_bf16_bits(rng.normal(0.0, std, (rows, cols)).astype(np.float32))
+
+
 def activations(rng: np.random.Generator, batch: int, cols: int) -> np.ndarray:
     return rng.standard_normal((batch, cols), dtype=np.float32)
 
@@ -97,6 +112,8 @@ def weights(dtype: str, rng: np.random.Generator, rows: int, cols: int, std: flo
         return hvsq2_weights(rng, rows, cols, std)
     if dtype == "f16":
         return f16_weights(rng, rows, cols, std)
+    if dtype == "bf16":
+        return bf16_weights(rng, rows, cols, std)
     raise ValueError(f"unknown weight dtype {dtype!r}")
 
 
@@ -106,7 +123,7 @@ def weight_bytes(dtype: str, rows: int, cols: int) -> int:
         return rows * q4_0_row_bytes(cols)
     if dtype == "hvsq2":
         return rows * hvsq2_row_bytes(cols)
-    if dtype == "f16":
+    if dtype in ("f16", "bf16"):
         return rows * cols * 2
     raise ValueError(dtype)
 
@@ -130,7 +147,8 @@ QWEN3_4B_SHAPED_CONFIG = {
 
 def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_norm: bool = False,
                   weight_std: float = 0.02, embed_std: float = 0.02, zero_mean: bool = False,
-                  biases: str = "") -> dict:
+                  biases: str = "", embed_dtype: str = "f16", lm_head: str | None = None,
+                  head_std: float = 0.02) -> dict:
     """Random decoder weights with the layout of a .qwn dense model: per layer
     q, k, v, o, gate, up, down quantized matrices ([out][in] row-major
     blocks), input/post norm vectors (and, with qk_norm, per-head q/k norm
@@ -142,7 +160,11 @@ def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_n
     weight is -scale/2, which drives the residual stream of a random model
     toward one direction and its greedy output toward one token).  biases:
     the projections among "qkvo" that get an F32 bias drawn 0.5 N(0,1)
-    (Qwen2 checkpoints carry q/k/v biases), as self_attn.*_proj.bias."""
+    (Qwen2 checkpoints carry q/k/v biases), as self_attn.*_proj.bias.
+    embed_dtype: "f16" (the benchmark models) or "bf16" (bit patterns as
+    uint16).  lm_head: None (the embedding is the LM head), or the dtype of a
+    separate lm_head.weight [vocab][hidden] ("f16", "bf16", "q4_0",
+    "hvsq2"), drawn after everything else with scale sigma head_std."""
     D, I = cfg["hidden"], cfg["intermediate"]
     Q, KV = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
     shapes = {"q": (Q, D), "k": (KV, D), "v": (KV, D), "o": (D, Q),
@@ -158,9 +180,13 @@ def decoder_model(rng: np.random.Generator, cfg: dict, dtype: str = "q4_0", qk_n
             for n in ("q_norm", "k_norm"):
                 layer[n] = (1.0 + 0.2 * rng.standard_normal(cfg["head_dim"])).astype(np.float32)
         layers.append(layer)
-    embed = f16_weights(rng, cfg["vocab"], D, embed_std)
-    return {"cfg": dict(cfg), "dtype": dtype, "shapes": shapes, "layers": layers,
-            "embed": embed, "final_norm": np.ones(D, dtype=np.float32)}
+    embed = (f16_weights if embed_dtype == "f16" else bf16_weights)(rng, cfg["vocab"], D, embed_std)
+    model = {"cfg": dict(cfg), "dtype": dtype, "shapes": shapes, "layers": layers,
+             "embed": embed, "embed_dtype": embed_dtype, "final_norm": np.ones(D, dtype=np.float32)}
+    if lm_head is not None:
+        model["lm_head"] = weights(lm_head, rng, cfg["vocab"], D, std=head_std)
+        model["lm_head_dtype"] = lm_head
+    return model
 
 
 def prompt_tokens(rng: np.random.Generator, vocab: int, count: int = 32) -> np.ndarray:

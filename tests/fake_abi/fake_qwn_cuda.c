@@ -72,7 +72,7 @@ static void fill_info(QwnCudaAbiInfo *info, uint32_t version) {
     info->header.abi_version = version;
     uint64_t caps = QWN_CUDA_CAP_HYPERVSQ2_GEMV | QWN_CUDA_CAP_HYPERVSQ2_GEMM | QWN_CUDA_CAP_RESIDENT_WEIGHTS |
                     QWN_CUDA_CAP_TELEMETRY | QWN_CUDA_CAP_DEVICE_ENUMERATION | QWN_CUDA_CAP_Q8_KV |
-                    QWN_CUDA_CAP_Q4_0_GEMV | QWN_CUDA_CAP_F16_GEMV;
+                    QWN_CUDA_CAP_Q4_0_GEMV | QWN_CUDA_CAP_F16_GEMV | QWN_CUDA_CAP_BF16_GEMV;
 #ifdef FAKE_NO_Q8_CAP
     caps &= ~(uint64_t)QWN_CUDA_CAP_Q8_KV;
 #endif
@@ -263,7 +263,7 @@ QWN_CUDA_ABI_API int qwn_cuda_abi_kv_cache_reset(QwnCudaContextHandle *context, 
 
 #ifdef FAKE_COMPUTE
 /* One token per request row, as the host decoder sends them: Q4_0 and
- * HyperVSQ-2 take int8 tokens with one scale, F16 takes fp32. */
+ * HyperVSQ-2 take int8 tokens with one scale, F16 and BF16 take fp32. */
 static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *telemetry) {
     if (!request || !request->tensor.opaque || !request->input_q8 || !request->output)
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
@@ -275,6 +275,9 @@ static int fake_matmul(const QwnCudaGemmRequest *request, QwnCudaTelemetry *tele
         if (t->dtype == QWN_CUDA_TENSOR_F16 && request->input_mode == QWN_CUDA_INPUT_F32) {
             const float *x = (const float *)request->input_q8 + (size_t)b * request->input_stride;
             qo_matmul_f16((const uint16_t *)t->data, x, 1, K, N, y, 1);
+        } else if (t->dtype == QWN_CUDA_TENSOR_BF16 && request->input_mode == QWN_CUDA_INPUT_F32) {
+            const float *x = (const float *)request->input_q8 + (size_t)b * request->input_stride;
+            qo_matmul_bf16((const uint16_t *)t->data, x, 1, K, N, y, 1);
         } else if (request->input_mode == QWN_CUDA_INPUT_Q8 && t->dtype == QWN_CUDA_TENSOR_Q4_0_18) {
             const int8_t *q = request->input_q8 + (size_t)b * request->input_stride;
             const float s = request->input_scales ? request->input_scales[b] : request->input_scale;

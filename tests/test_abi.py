@@ -53,7 +53,7 @@ def test_extension_struct_layouts():
     import subprocess
     import tempfile
     fields = {"QwnHipGemvGroupRequest": abi.GemvGroupRequest, "QwnHipDecoderDesc": abi.DecoderDesc,
-              "QwnHipDecoderStats": abi.DecoderStats}
+              "QwnHipDecoderStats": abi.DecoderStats, "QwnHipTensorInfo": abi.TensorInfo}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "qwn_hip_ext.h"',
              '#include "qwn_hip_decoder.h"', 'int main(void) {']
     for cname, cls in fields.items():
@@ -83,7 +83,8 @@ def test_query_contract(hip_lib):
     assert info.header.abi_version == 1
     assert info.header.struct_size >= ctypes.sizeof(abi.AbiInfo)
     assert info.hypervsq2_block_bytes == 74 and info.hypervsq2_block_elements == 256
-    need = abi.CAP_HYPERVSQ2_GEMV | abi.CAP_HYPERVSQ2_GEMM | abi.CAP_Q8_KV | abi.CAP_Q4_0_GEMV
+    need = (abi.CAP_HYPERVSQ2_GEMV | abi.CAP_HYPERVSQ2_GEMM | abi.CAP_Q8_KV | abi.CAP_Q4_0_GEMV |
+            abi.CAP_F16_GEMV | abi.CAP_BF16_GEMV | abi.CAP_DEVICE_POINTERS)
     assert info.capability_bits & need == need
     assert info.abi_name == b"qwn_cuda_hypervsq2"
     assert info.max_resident_tensors == 512

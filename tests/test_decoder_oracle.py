@@ -59,6 +59,47 @@ def test_oracle_decoder_matches_reference_decoder(tmp_path, oracle_lib, cfg, dty
         d3.close()
 
 
+@pytest.mark.parametrize("embed,head,cfg_name,dtype", [
+    ("bf16", None, "SMALL", "q4_0"), ("f16", "f16", "SMALL", "hvsq2"), ("f16", "bf16", "SMALL", "q4_0"),
+    ("bf16", "q4_0", "SMALL", "q4_0"), ("f16", "hvsq2", "SMALL", "hvsq2"), ("bf16", "bf16", "QWEN2_LIKE", "q4_0"),
+    ("f16", "q4_0", "QWEN2_LIKE", "q4_0")])
+def test_untied_head_and_bf16_embedding_match_reference(tmp_path, oracle_lib, embed, head, cfg_name, dtype):
+    """A BF16 embedding (c/qwanto_decode.c:561; qwn_row_f32,
+    c/qwanto_kernels.c:1508-1527) and an untied lm_head.weight in each dtype
+    the LM head matmul takes (c/qwanto_decode.c:1074-1076, 2007; F16/BF16 rows
+    and the Q4_0 / HyperVSQ-2 quantized matmuls): the oracle's logits are the
+    reference decoder's bit for bit, and the head is really used (the same
+    model with the head dropped, i.e. tied, gives other logits)."""
+    cfg = {"SMALL": SMALL, "QWEN2_LIKE": QWEN2_LIKE}[cfg_name]
+    rng = np.random.default_rng(21)
+    model = synth.decoder_model(rng, cfg, dtype, embed_dtype=embed, lm_head=head)
+    path = str(tmp_path / "m.qwn")
+    qwn_file.write_decoder_model(path, model)
+    back = qwn_file.read_decoder_model(path)
+    assert back["embed_dtype"] == embed and back.get("lm_head_dtype") == head
+    assert np.array_equal(np.asarray(back["embed"]).view(np.uint16), model["embed"].view(np.uint16))
+    if head is not None:
+        assert np.array_equal(np.asarray(back["lm_head"]).view(np.uint8).ravel(), model["lm_head"].view(np.uint8).ravel())
+    back["file"].close()
+    ref = ref_decoder_or_skip(path, cfg["max_ctx"])
+    dec = oracle_lib.decoder(model)
+    token = 5
+    for step in range(6):
+        a = ref.forward(token, cfg["vocab"])
+        b = dec.forward(token)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), \
+            f"step {step}: logits differ by up to {np.abs(a - b).max()}"
+        token = int(np.argmax(a))
+    ref.close()
+    dec.close()
+    if head is not None:
+        tied = {k: v for k, v in model.items() if k not in ("lm_head", "lm_head_dtype")}
+        d1, d2 = oracle_lib.decoder(tied), oracle_lib.decoder(model)
+        assert not np.array_equal(d1.forward(5), d2.forward(5))
+        d1.close()
+        d2.close()
+
+
 def test_qwn_roundtrip_biases(tmp_path):
     rng = np.random.default_rng(4)
     model = synth.decoder_model(rng, SMALL, "q4_0", biases="qkvo")

@@ -75,6 +75,20 @@ def test_host_decoder_norms_and_biases(oracle_lib, cfg, dtype, qk, bias):
     run_against_oracle(oracle_lib, model, steps=16, token=5)
 
 
+@pytest.mark.parametrize("cfg,dtype,embed,head", [(SMALL, "q4_0", "bf16", None), (SMALL, "hvsq2", "f16", "bf16"),
+                                                  (QWEN2_LIKE, "q4_0", "bf16", "q4_0"),
+                                                  (SMALL, "hvsq2", "f16", "hvsq2"), (QWEN2_LIKE, "q4_0", "f16", "f16")])
+def test_host_decoder_untied_head_and_bf16_embedding(oracle_lib, cfg, dtype, embed, head):
+    """A BF16 embedding (c/qwanto_decode.c:561) and an untied lm_head.weight in
+    each dtype (:1074-1076, 2007) through the ABI: the BF16 GEMV with fp32
+    input, or the head's activation quantized on the host as every
+    projection's."""
+    rng = np.random.default_rng(43)
+    model = synth.decoder_model(rng, cfg, dtype, embed_dtype=embed, lm_head=head)
+    m = run_against_oracle(oracle_lib, model, steps=12, token=9)
+    assert m.cpu_fallback_count == 0 and m.gpu_matmul_count == 12 * (7 * cfg["layers"] + 1)
+
+
 @pytest.mark.parametrize("name", decode_golden.NAMES)
 def test_host_decoder_qwen2_1p5b_golden(name):
     """Config-2 shape through the ABI as qwnrun drives it (one synchronous

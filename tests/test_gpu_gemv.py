@@ -408,6 +408,33 @@ def test_f16_gemv(gpu_ctx, oracle_lib, N, K, M):
     gpu_ctx.release(h)
 
 
+@pytest.mark.parametrize("N,K,M", [(1000, 1536, 1), (77, 70, 2), (4096, 2560, 1), (33, 4096, 4), (300, 8960, 16)])
+def test_bf16_gemv(gpu_ctx, oracle_lib, N, K, M):
+    """BF16 rows (c/qwanto_kernels.c:287-290, 1508-1527) through the ABI with
+    fp32 activations, against the oracle's restatement of qwn_matmul_f32 on
+    BF16 (pinned to the reference build); subnormal and negative-zero
+    weights included."""
+    rng = np.random.default_rng(N * 3 + K + M)
+    w = synth.bf16_weights(rng, N, K)
+    w[0, :3] = (0x0001, 0x8000, 0x807F)
+    x = synth.activations(rng, M, K)
+    h = gpu_ctx.upload(w, "bf16", N, K)
+    try:
+        info = gpu_ctx.tensor_info(h)
+        assert info.dtype == abi.TENSOR_BF16 and info.logical_bytes == N * K * 2
+        tm = abi.Telemetry()
+        y = gpu_ctx.gemm(h, x, N, K, telemetry=tm)
+        assert tm.kernel_type.startswith(b"bf16")
+        ref = oracle_lib.matmul_bf16(w, x, threads=0)
+        for t in range(M):
+            ok, worst = gemv_close(y[t], ref[t])
+            assert ok, f"token {t}: worst {worst:.3g} of tolerance"
+        # the same bits read as F16 give other products: the conversion is the BF16 one
+        assert not np.allclose(y, oracle_lib.matmul_f16(w.view(np.float16), x, threads=0), rtol=1e-2)
+    finally:
+        gpu_ctx.release(h)
+
+
 def test_request_validation(gpu_ctx, hip_lib):
     rng = np.random.default_rng(1)
     w = synth.hvsq2_weights(rng, 8, 256)

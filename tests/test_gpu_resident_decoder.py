@@ -81,6 +81,56 @@ def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype, qk, bi
     assert ok, msg
 
 
+@pytest.mark.parametrize("cfg,dtype,embed,head", [
+    (SMALL, "q4_0", "bf16", None), (SMALL, "hvsq2", "f16", "f16"), (QWEN2_LIKE, "q4_0", "bf16", "bf16"),
+    (QWEN2_LIKE, "q4_0", "f16", "q4_0"), (SMALL, "hvsq2", "bf16", "hvsq2"), (LONG_CTX, "q4_0", "f16", "hvsq2")])
+def test_untied_head_and_bf16_embedding(gpu_ctx, oracle_lib, cfg, dtype, embed, head):
+    """A BF16 embedding (c/qwanto_decode.c:561) and an untied lm_head.weight
+    (c/qwanto_decode.c:1074-1076, 2007) in each dtype: F16/BF16 through the
+    norm image and the F16-layout GEMV, Q4_0/HyperVSQ-2 normalized and
+    quantized in the head GEMV's own prologue.  Stepping (the device argmax
+    epilogue on the head), a prefill block and a verify block (the batched
+    head on every token) against the oracle, which is bit-identical to the
+    reference decoder on the same model (test_decoder_oracle.py)."""
+    rng = np.random.default_rng(47)
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, embed_dtype=embed, lm_head=head))
+    prompt = synth.prompt_tokens(rng, cfg["vocab"], 6)
+    draft = synth.prompt_tokens(rng, cfg["vocab"], 5)
+    dec = abi.ResidentDecoder(gpu_ctx, model)
+    ref = oracle_lib.decoder(model)
+    try:
+        token, inputs, gpu_steps, ref_steps = 11, [], [], []
+        for step in range(12):
+            a, greedy = dec.forward(token)
+            b = ref.forward(token)
+            assert greedy == int(np.argmax(a)), "device argmax is not the first maximum of its logits"
+            inputs.append(token)
+            gpu_steps.append(a)
+            ref_steps.append(b)
+            token = int(np.argmax(b))
+        # a prefill block, then a verify block, continuing the same context
+        a, greedy = dec.prefill(prompt)
+        assert greedy == int(np.argmax(a))
+        inputs += [int(t) for t in prompt]
+        ref_prompt = [ref.forward(int(t)) for t in prompt]
+        gpu_steps.append(a)
+        ref_steps += ref_prompt
+        vl, ids = dec.verify(draft)
+        assert ids.tolist() == [int(np.argmax(r)) for r in vl]
+        inputs += [int(t) for t in draft]
+        ref_steps += [ref.forward(int(t)) for t in draft]
+        gpu_steps += list(vl)
+    finally:
+        dec.close()
+        ref.close()
+    env = oracle_envelope(oracle_lib, model, inputs, ref_steps)
+    # the compared steps: the 12 forwards, the prefill's last token, the 5 verify rows
+    keep = list(range(12)) + [12 + len(prompt) - 1] + list(range(12 + len(prompt), len(inputs)))
+    ref_kept = [ref_steps[i] for i in keep]
+    ok, msg = within_envelope(step_errors(gpu_steps, ref_kept), env[:, keep])
+    assert ok, msg
+
+
 def read_caches(dec, layers, count):
     return [dec.kv_read(l, 0, count) for l in range(layers)]
 

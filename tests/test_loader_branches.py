@@ -104,7 +104,12 @@ def test_accepted_library_fails_closed(tmp_path, host_lib, defines):
 
 
 @pytest.mark.parametrize("dtype,extra", [("q4_0", {}), ("hvsq2", {}), ("q4_0", {"qk_norm": True, "biases": "qkvo"}),
-                                         ("hvsq2", {"qk_norm": True, "biases": "qkv"})])
+                                         ("hvsq2", {"qk_norm": True, "biases": "qkv"}),
+                                         # BF16 embedding, untied heads in each dtype
+                                         ("q4_0", {"embed_dtype": "bf16"}),
+                                         ("q4_0", {"embed_dtype": "bf16", "lm_head": "bf16"}),
+                                         ("hvsq2", {"lm_head": "f16"}), ("q4_0", {"lm_head": "q4_0"}),
+                                         ("hvsq2", {"embed_dtype": "bf16", "lm_head": "hvsq2"})])
 def test_host_decoder_end_to_end_on_cpu(tmp_path, host_lib, dtype, extra):
     """A working CPU library (FAKE_COMPUTE: every projection and Q8 KV call
     computed by the oracle's kernels) under the host decoder: its own step

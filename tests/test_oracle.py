@@ -279,6 +279,37 @@ def test_f16_closed_form_and_reference(oracle_lib, ref_lib):
         assert np.array_equal(bits(y), bits(ref_lib.matmul_f16(w, x)))
 
 
+def test_bf16_conversion_all_patterns(oracle_lib):
+    """bfloat16 -> fp32 is the 16 bits placed high (c/qwanto_kernels.c:287-290):
+    every one of the 65536 patterns, NaN payloads and subnormals included,
+    against the same bits built by integer arithmetic."""
+    pats = np.arange(65536, dtype=np.uint32)
+    want = (pats << 16).astype(np.uint32)
+    got = np.array([oracle_lib.lib.qo_bf16_to_float(int(p)) for p in pats[::257]], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want[::257])
+    # the conversion the synthetic generator uses rounds to nearest even
+    assert synth.to_bf16_bits(np.array([1.0 + 2.0 ** -8], np.float32))[0] == 0x3F80  # tie -> even
+    assert synth.to_bf16_bits(np.array([1.0 + 3 * 2.0 ** -9], np.float32))[0] == 0x3F81
+
+
+def test_bf16_closed_form_and_reference(oracle_lib, ref_lib):
+    """qwn_matmul_f32 on BF16 rows (c/qwanto_kernels.c:1508-1527, 1605-1614):
+    within fp32 rounding of the fp64 product of the decoded weights, and
+    bit-identical to the reference build."""
+    rng = np.random.default_rng(15)
+    for K in (1, 7, 12, 70, 1536):
+        w = synth.bf16_weights(rng, 9, K)
+        w[0, 0] = 0x0001  # subnormal weight
+        x = synth.activations(rng, 2, K)
+        y = oracle_lib.matmul_bf16(w, x)
+        wf = synth.bf16_to_f32(w).astype(np.float64)
+        exact = x.astype(np.float64) @ wf.T
+        assert np.all(np.abs(y - exact) <= 1e-5 * (np.abs(x) @ np.abs(wf).T) + 1e-12)
+        assert np.array_equal(bits(y), bits(ref_lib.matmul_bf16(w, x)))
+        # a dropped conversion (the raw bits read as F16) would differ
+        assert not np.array_equal(bits(y), bits(oracle_lib.matmul_f16(w.view(np.float16), x)))
+
+
 # ---------------------------------------------------------------------------
 # Q8 KV cache
 # ---------------------------------------------------------------------------
