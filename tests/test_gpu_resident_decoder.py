@@ -257,16 +257,18 @@ def test_generate_equals_stepwise(gpu_ctx):
 
 @pytest.mark.parametrize("name", decode_golden.NAMES)
 def test_resident_decoder_qwen2_1p5b_golden(gpu_ctx, name):
-    """Config-2 shape: 28 Q4_0 layers, tied F16 LM head (151936 x 1536), Q8
-    KV; 32-token prompt, 128 greedy steps of the golden decode (the oracle's,
+    """Config-2 shape: 28 Q4_0 layers, F16 LM head (151936 x 1536; tied, or
+    the successor golden's untied head), Q8 KV; 32-token prompt, 128 greedy steps of the golden decode (the oracle's,
     bit-identical to the reference decoder's).
 
     Teacher-forced: the prompt as two 16-token prefill blocks, then the
     golden ids one forward() at a time; every step's logits against the
     golden step (decode_golden.step_error: the top-16 logits, nothing else
     above them), within the golden's stored envelope.  Free-running:
-    generate() gives the golden ids, except past a step whose golden top-two
-    margin is within that step's measured error."""
+    generate() gives the golden ids (decode_golden.check_greedy_ids): all
+    128 on the successor golden (128 distinct ids, every margin far above
+    the error); on the others none may differ before a step whose golden
+    top-two margin is within twice that step's measured error."""
     loaded = decode_golden.load(name)
     if loaded is None:
         pytest.skip("golden decode fixture absent")
@@ -283,13 +285,9 @@ def test_resident_decoder_qwen2_1p5b_golden(gpu_ctx, name):
     finally:
         dec.close()
     ok, msg = within_envelope(errs, g["envelope"])
-    first_diff = next((i for i, (x, y) in enumerate(zip(toks.tolist(), g["tokens"])) if x != y), None)
-    print(f"{name}: {len(set(g['tokens']))} distinct golden ids, {msg}, "
-          f"{st.generated_tokens / (st.decode_ms / 1e3):.1f} tok/s, first divergence {first_diff}")
+    print(f"{name}: {msg}, {st.generated_tokens / (st.decode_ms / 1e3):.1f} tok/s")
     assert ok, msg
-    if first_diff is not None:
-        assert g["margins"][first_diff] <= 2 * errs[first_diff] * g["steps"][first_diff]["max_abs"], \
-            f"greedy ids diverge at step {first_diff} with golden margin {g['margins'][first_diff]:.4g}"
+    print(decode_golden.check_greedy_ids(name, g, toks.tolist(), errs))
     assert st.graph == 1
 
 
