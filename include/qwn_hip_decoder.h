@@ -116,6 +116,31 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *context, QwnH
 QWN_CUDA_ABI_API int qwn_hip_decoder_verify(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
                                             const int32_t *tokens, uint32_t count, float *logits,
                                             int32_t *next_tokens);
+/* Speculative verification of a draft TREE (c/qwanto_jetspec.h:17-33):
+ * `count` (1..64) nodes after the cached prefix of P tokens, node i =
+ * (tokens[i], parents[i]) with parents[i] an earlier node or -1 (a root,
+ * attached to the prefix).  One forward over the nodes in index order, in
+ * blocks of 16: node i is rotated for position P + depth(i), its K/V held
+ * at cache slot P + i, and it attends to the prefix, its ancestors and
+ * itself (the ancestor mask of qwn_jetspec_build_tree_mask,
+ * c/qwanto_jetspec.c:33-49).  logits [count][vocab] (host, may be NULL) are
+ * the target's logits after each node -- the prediction for its children --
+ * and next_tokens[count] (may be NULL) their first maxima.  The rows
+ * qwn_jetspec_verify_tree reads (c/qwanto_jetspec.c:160-205: row i is the
+ * target's prediction FOR node i) are the logits of node i's parent, or,
+ * for a root, the logits after the prefix's last token.  The position stays
+ * at P: qwn_hip_decoder_commit_path keeps an accepted path, and any other
+ * call drops the tree. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_verify_tree(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                                 const int32_t *tokens, const int32_t *parents, uint32_t count,
+                                                 float *logits, int32_t *next_tokens);
+/* After qwn_hip_decoder_verify_tree: keeps the root-to-node path
+ * nodes[0..length) (nodes[0] a root, nodes[k] a child of nodes[k-1]) --
+ * their K/V, as the tree forward computed them, move to cache slots
+ * P .. P + length - 1 -- drops the other nodes, and moves the position to
+ * P + length. */
+QWN_CUDA_ABI_API int qwn_hip_decoder_commit_path(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,
+                                                 const uint32_t *nodes, uint32_t length);
 /* Keep the first `position` cached tokens (position <= the current one):
  * the next step writes at `position`. */
 QWN_CUDA_ABI_API int qwn_hip_decoder_truncate(QwnCudaContextHandle *context, QwnHipDecoderHandle *decoder,

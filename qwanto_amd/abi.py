@@ -65,6 +65,7 @@ DECODER_EXPORTS = (
     "qwn_hip_decoder_create", "qwn_hip_decoder_destroy", "qwn_hip_decoder_reset",
     "qwn_hip_decoder_forward", "qwn_hip_decoder_generate", "qwn_hip_decoder_prefill",
     "qwn_hip_decoder_debug_kv_read", "qwn_hip_decoder_verify", "qwn_hip_decoder_truncate",
+    "qwn_hip_decoder_verify_tree", "qwn_hip_decoder_commit_path",
 )
 
 GEMV_INPUT = {"image": 0, "f32": 1, "rmsnorm": 2, "swiglu": 3}
@@ -335,6 +336,8 @@ class Library:
         lib.qwn_hip_decoder_debug_kv_read.argtypes = [P(Handle), P(Handle), U32, U32, U32, V, V, V, V]
         lib.qwn_hip_decoder_verify.argtypes = [P(Handle), P(Handle), V, U32, V, V]
         lib.qwn_hip_decoder_truncate.argtypes = [P(Handle), P(Handle), U32]
+        lib.qwn_hip_decoder_verify_tree.argtypes = [P(Handle), P(Handle), V, V, U32, V, V]
+        lib.qwn_hip_decoder_commit_path.argtypes = [P(Handle), P(Handle), V, U32]
 
     def last_error(self) -> str:
         buf = ctypes.create_string_buffer(512)
@@ -689,6 +692,27 @@ class ResidentDecoder:
         lib.check("decoder_verify", lib.lib.qwn_hip_decoder_verify(
             self.ctx._h, ctypes.byref(self.handle), _p(tokens), n, _p(out), _p(ids)))
         return out, ids
+
+    def verify_tree(self, tokens, parents, logits: bool = True):
+        """One draft tree (node i = tokens[i] under parents[i], -1 for a root)
+        after the cached prefix: (logits after each node [count][vocab] or
+        None, their first maxima [count])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        parents = np.ascontiguousarray(parents, dtype=np.int32)
+        n = tokens.size
+        out = np.zeros((n, self.cfg["vocab"]), dtype=np.float32) if logits else None
+        ids = np.zeros(n, dtype=np.int32)
+        lib = self.ctx.lib
+        lib.check("decoder_verify_tree", lib.lib.qwn_hip_decoder_verify_tree(
+            self.ctx._h, ctypes.byref(self.handle), _p(tokens), _p(parents), n, _p(out), _p(ids)))
+        return out, ids
+
+    def commit_path(self, nodes) -> None:
+        """Keep the root-to-node path `nodes` of the last verified tree."""
+        nodes = np.ascontiguousarray(nodes, dtype=np.uint32)
+        lib = self.ctx.lib
+        lib.check("decoder_commit_path", lib.lib.qwn_hip_decoder_commit_path(
+            self.ctx._h, ctypes.byref(self.handle), _p(nodes), nodes.size))
 
     def truncate(self, position: int) -> None:
         lib = self.ctx.lib

@@ -117,6 +117,34 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(KvCache c, uint32_t firs
     }
 }
 
+// A draft tree's accepted path into consecutive slots: thread i < channels
+// moves channel i's key and value bytes, thread i < groups the group's two
+// scales, for k = 0, 1, ... in order (slot base + path[k] -> base + k; the
+// path is strictly increasing with path[k] >= k, so no source slot is read
+// after this thread overwrote it, and no two threads touch one byte).
+__global__ __launch_bounds__(256) void kv_commit_path_kernel(KvCache c, const int32_t *__restrict__ base_ptr,
+                                                             const int32_t *__restrict__ path, uint32_t len) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t base = static_cast<uint32_t>(*base_ptr);
+    if (idx < c.channels) {
+        const uint32_t head = idx / c.head_dim, dim = idx % c.head_dim;
+        for (uint32_t k = 0; k < len; ++k) {
+            const uint32_t src = base + static_cast<uint32_t>(path[k]), dst = base + k;
+            if (src >= c.max_tokens) break;
+            c.keys[k_index(c, dst, head, dim)] = c.keys[k_index(c, src, head, dim)];
+            c.values[v_offset(c, dst, head, dim)] = c.values[v_offset(c, src, head, dim)];
+        }
+    }
+    if (idx < c.groups) {
+        for (uint32_t k = 0; k < len; ++k) {
+            const uint32_t src = base + static_cast<uint32_t>(path[k]), dst = base + k;
+            if (src >= c.max_tokens) break;
+            c.key_scales[scale_index(c, dst, idx)] = c.key_scales[scale_index(c, src, idx)];
+            c.value_scales[scale_index(c, dst, idx)] = c.value_scales[scale_index(c, src, idx)];
+        }
+    }
+}
+
 struct AttnArgs {
     KvCache c;
     const float *query;
@@ -369,7 +397,9 @@ namespace {
 // with a = x[i], b = x[i + half] and the cos/sin table row of the position;
 // the append quantizes per 64-channel group as kv_append_kernel.  grid (n):
 // workgroup i takes token i of a block -- q + i*q_stride, k/v + i*kv_stride,
-// position pos_ptr[i].
+// cache slot pos_ptr[i], rotated for position rope_pos_ptr[i] (the slot
+// when null; a draft tree's node sits at slot P + index but position
+// P + depth).
 __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__restrict__ q, uint32_t q_heads,
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
@@ -377,15 +407,17 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
                                                            const float *__restrict__ sin_tab,
                                                            const int32_t *__restrict__ pos_ptr, uint32_t q_stride,
                                                            uint32_t kv_stride, const float *__restrict__ q_norm,
-                                                           const float *__restrict__ k_norm, float eps) {
+                                                           const float *__restrict__ k_norm, float eps,
+                                                           const int32_t *__restrict__ rope_pos_ptr) {
     extern __shared__ float kr[];  // [channels] rotated key
     __shared__ float inv_s[kMaxNormHeads];
     q += static_cast<size_t>(blockIdx.x) * q_stride;
     k += static_cast<size_t>(blockIdx.x) * kv_stride;
     v += static_cast<size_t>(blockIdx.x) * kv_stride;
     const uint32_t pos = static_cast<uint32_t>(pos_ptr[blockIdx.x]);
+    const uint32_t rpos = rope_pos_ptr ? static_cast<uint32_t>(rope_pos_ptr[blockIdx.x]) : pos;
     const uint32_t D = c.head_dim, half = D / 2;
-    const uint32_t row = pos < c.max_tokens ? pos : 0;
+    const uint32_t row = rpos < c.max_tokens ? rpos : 0;
     const float *ct = cos_tab + static_cast<size_t>(row) * half;
     const float *st = sin_tab + static_cast<size_t>(row) * half;
     // per-head q/k RMSNorm ahead of the rotation (c/qwanto_decode.c:654-684,
@@ -488,7 +520,25 @@ struct DecodeAttnArgs {
     const float *q_norm;     // decode mode, optional: per-head q/k RMSNorm weights [head_dim]
     const float *k_norm;
     float eps;
+    // prefill mode, optional: a draft tree's ancestor masks, one per query
+    // token; slot *tree_base + a is attended only where bit a is set (slots
+    // below *tree_base, the prefix, always)
+    const uint64_t *tree_mask;
+    const int32_t *tree_base;
 };
+
+// Whether slot t is attended under a tree mask relative to slot `base`
+// (no tree: tree_bits() gives all ones).  The 64-bit test is a lookup of
+// the mask's two halves by the slot's offset, written without any shift by
+// a wrapped offset: an earlier form, t < base || (mask >> min(t - base,
+// 63)) & 1, was compiled into the shift alone (the t < base test dropped),
+// which masked every token.
+__device__ __forceinline__ bool tree_attends(uint32_t t, uint32_t base, uint64_t mask) {
+    const uint32_t off = t - base;  // the slot's tree index when t >= base
+    const uint32_t half = off < 32u ? static_cast<uint32_t>(mask) : static_cast<uint32_t>(mask >> 32);
+    const bool bit = ((half >> (off & 31u)) & 1u) != 0u;
+    return t < base || (off < 64u && bit);
+}
 
 __device__ __forceinline__ int8_t q8_of(float x, float scale) {
     if (!isfinite(x)) return 0;
@@ -615,6 +665,8 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
     if (pos >= c.max_tokens) return;
     const uint32_t t1 = min(pos + 1, a.span);
     const bool cur = rope && pos < t1;
+    const uint64_t tmask = a.tree_mask ? a.tree_mask[blockIdx.z] : 0ull;
+    const uint32_t tbase = a.tree_mask ? static_cast<uint32_t>(*a.tree_base) : 0xffffffffu;
 
     // 1. q/k norms: 1/rms of the query head and of the current key head
     //    from wave sums of squares (waves < D/64 hold the query, waves
@@ -682,7 +734,7 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
         const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
         // 3. the chunk's loads (the first chunk's were issued at the start)
         if (c0 != 0) load_chunk(c0, t1 - 1);
-        const bool has = slot < n;
+        const bool has = slot < n && tree_attends(c0 + slot, tbase, tmask);
         if (cur) {
             // the current token's key part, scales and value byte
             const bool is_cur = has && c0 + slot == pos;
@@ -933,6 +985,8 @@ struct MfmaAttnArgs {
     float scale;
     uint32_t position;
     const int32_t *position_ptr;
+    const uint64_t *tree_mask;  // optional: the query token's ancestor mask over slots *tree_base + a
+    const int32_t *tree_base;
 };
 
 __device__ __forceinline__ int piece_round(float v) {
@@ -1039,6 +1093,8 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
     }
     const uint32_t t1 = min(tokens, t0 + a.split);
     const uint32_t col = lane % 16, kq = lane / 16;   // MFMA column / k-quarter of this lane
+    const uint64_t tmask = a.tree_mask ? *a.tree_mask : 0ull;
+    const uint32_t tbase = a.tree_mask ? static_cast<uint32_t>(*a.tree_base) : 0xffffffffu;
 
     // 1. query pieces (A of the scores), this lane: head (col / 4) of row
     //    tile rt, piece col % 4, channels 64g + 16kq .. +15.  Where the
@@ -1177,7 +1233,10 @@ __global__ __launch_bounds__(64 * NW) void mfma_attention_kernel(MfmaAttnArgs a)
         const float4 (&vs)[NG] = cur.vs;
         bool valid[NT];
 #pragma unroll
-        for (int i = 0; i < NT; ++i) valid[i] = b0 + 16 * i + col < t1;
+        for (int i = 0; i < NT; ++i) {
+            const uint32_t t = b0 + 16 * i + col;
+            valid[i] = t < t1 && tree_attends(t, tbase, tmask);
+        }
 
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -1369,13 +1428,13 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base) {
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
                               const int32_t *pos_ptr, hipStream_t stream, uint32_t count, const float *q_norm,
-                              const float *k_norm, float eps) {
+                              const float *k_norm, float eps, const int32_t *rope_pos_ptr) {
     if (c.head_dim % 2 || c.channels > 8192 || count == 0 || (!q_norm) != (!k_norm) ||
         (q_norm && query_heads + c.kv_heads > static_cast<uint32_t>(kMaxNormHeads)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_append_kernel, dim3(count), dim3(1024), c.channels * sizeof(float), stream, c, query,
                        query_heads, key, value, cos_tab, sin_tab, pos_ptr, query_heads * c.head_dim, c.channels,
-                       q_norm, k_norm, eps);
+                       q_norm, k_norm, eps, rope_pos_ptr);
     return hipGetLastError();
 }
 
@@ -1442,9 +1501,14 @@ size_t mfma_attention_workspace_floats(const KvCache &c, uint32_t query_heads, u
 
 hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *output, float *partials,
                                  uint32_t query_heads, uint32_t position, const int32_t *position_ptr,
-                                 uint32_t span, float scale, hipStream_t stream) {
-    if (!mfma_attention_supported(c, query_heads) || span == 0 || span > c.max_tokens) return hipErrorInvalidValue;
+                                 uint32_t span, float scale, hipStream_t stream, const uint64_t *tree_mask,
+                                 const int32_t *tree_base) {
+    if (!mfma_attention_supported(c, query_heads) || span == 0 || span > c.max_tokens ||
+        (!tree_mask) != (!tree_base))
+        return hipErrorInvalidValue;
     MfmaAttnArgs args{};
+    args.tree_mask = tree_mask;
+    args.tree_base = tree_base;
     args.c = c;
     args.query = query;
     args.output = output;
@@ -1482,7 +1546,8 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     const KvCache &c = *l.cache;
     if (!decode_attention_supported(c, l.query_heads) || (l.key && (c.head_dim % 64 || !l.value || !l.cos_tab ||
                                                                     !l.sin_tab)) ||
-        l.count == 0 || (l.count > 1 && (l.key || !l.position_ptr)))
+        l.count == 0 || (l.count > 1 && (l.key || !l.position_ptr)) || (!l.tree_mask) != (!l.tree_base) ||
+        (l.tree_mask && (l.key || !l.position_ptr)))
         return hipErrorInvalidValue;
     // the whole context in one split (K/V rows are re-read per query head
     // from L2: the latency case); longer contexts take the RoPE/append
@@ -1508,11 +1573,21 @@ hipError_t launch_decode_attention(const DecodeAttentionLaunch &l, hipStream_t s
     args.q_norm = l.q_norm;
     args.k_norm = l.k_norm;
     args.eps = l.eps;
+    args.tree_mask = l.tree_mask;
+    args.tree_base = l.tree_base;
     switch (c.head_dim) {
     case 64: return launch_decode_kernel<64>(args, stream);
     case 128: return launch_decode_kernel<128>(args, stream);
     default: return launch_decode_kernel<256>(args, stream);
     }
+}
+
+hipError_t launch_kv_commit_path(const KvCache &c, const int32_t *base, const int32_t *path, uint32_t len,
+                                 hipStream_t stream) {
+    if (!base || !path || len == 0 || len > 64) return hipErrorInvalidValue;
+    const uint32_t n = std::max(c.channels, c.groups);
+    hipLaunchKernelGGL(kv_commit_path_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, c, base, path, len);
+    return hipGetLastError();
 }
 
 hipError_t launch_kv_append(const KvCache &c, const float *key, const float *value, uint32_t token,
@@ -1588,11 +1663,13 @@ size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads) {
 }
 
 hipError_t launch_attention_at(const KvCache &c, const float *query, float *output, uint32_t query_heads,
-                               const int32_t *position_ptr, float scale, float *partials, hipStream_t stream) {
+                               const int32_t *position_ptr, float scale, float *partials, hipStream_t stream,
+                               const uint64_t *tree_mask, const int32_t *tree_base) {
     if (query_heads == 0 || c.head_dim > 1024) return hipErrorInvalidValue;
     if (mfma_attention_supported(c, query_heads))
         return launch_mfma_attention(c, query, output, partials, query_heads, 0, position_ptr, c.max_tokens, scale,
-                                     stream);
+                                     stream, tree_mask, tree_base);
+    if (tree_mask) return hipErrorInvalidValue;  // tree masks: the MFMA and decode kernels only
     AttnArgs args{};
     args.c = c;
     args.query = query;

@@ -36,6 +36,8 @@ namespace {
 
 constexpr int kProj = 7;
 constexpr uint32_t kPrefillTokens = 16;  // prompt tokens per prefill block (the GEMV's widest launch)
+constexpr uint32_t kTreeNodes = 64;      // draft-tree nodes per verify (c/qwanto_jetspec.h:17)
+constexpr uint32_t kTreeBlocks = kTreeNodes / kPrefillTokens;
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN };
 
 // x = embedding row of the step's token (feed[pos] when the host supplied
@@ -176,13 +178,24 @@ struct Decoder {
     uint8_t *pmimg = nullptr;
     int32_t *ppos = nullptr;
     // verify blocks: the LM head on every token of the block
-    float *vlogits = nullptr;       // [kPrefillTokens][vocab]
-    int32_t *vids = nullptr;        // [kPrefillTokens] greedy id after each token
+    float *vlogits = nullptr;       // [kTreeNodes][vocab]
+    int32_t *vids = nullptr;        // [kTreeNodes] greedy id after each token
     uint8_t *vimg = nullptr;        // [kPrefillTokens][vimg_stride] fp32 LM-head images
     uint32_t vimg_stride = 0;
     // one graph per (block size, block kind: inner / ends the prompt / verify)
     hipGraphExec_t prefill_exec[kPrefillTokens + 1][3] = {};
     bool prefill_tried[kPrefillTokens + 1][3] = {};
+    // draft trees: per node its ancestor-or-self mask and rotation position
+    // (prefix length + depth), the prefix length, an accepted path; one
+    // graph per (16-node block of the tree, block size)
+    uint64_t *tree_mask = nullptr;  // [kTreeNodes]
+    int32_t *tree_pos = nullptr;    // [kTreeNodes]
+    int32_t *tree_base = nullptr;   // [1]
+    int32_t *tree_path = nullptr;   // [kTreeNodes]
+    hipGraphExec_t tree_exec[kTreeBlocks][kPrefillTokens + 1] = {};
+    bool tree_tried[kTreeBlocks][kPrefillTokens + 1] = {};
+    uint32_t tree_nodes = 0;        // nodes of the verified tree awaiting commit (0: none)
+    std::vector<int32_t> tree_parents, tree_tokens;
     uint32_t position = 0;
     uint32_t launches = 0;
     uint32_t layer_launches = 0;  // kernels per layer
@@ -194,6 +207,9 @@ void destroy_decoder(Decoder *d) {
     if (!d) return;
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     for (auto &row : d->prefill_exec)
+        for (hipGraphExec_t x : row)
+            if (x) (void)hipGraphExecDestroy(x);
+    for (auto &row : d->tree_exec)
         for (hipGraphExec_t x : row)
             if (x) (void)hipGraphExecDestroy(x);
     if (d->allocation) (void)hipFree(d->allocation);
@@ -279,8 +295,9 @@ hipError_t enqueue_head(Decoder *d, const float *x, hipStream_t s) {
     return hipGetLastError();
 }
 
-// What follows the layers of a prefill block.
-enum BlockKind : uint32_t { kBlockInner = 0, kBlockLast = 1, kBlockVerify = 2 };
+// What follows the layers of a prefill block.  kBlockTree: 16 nodes of a
+// draft tree (block `block` of it), the LM head on each as kBlockVerify.
+enum BlockKind : uint32_t { kBlockInner = 0, kBlockLast = 1, kBlockVerify = 2, kBlockTree = 3 };
 
 // One prefill block of `m` prompt tokens at the device position (their ids
 // in feed): per layer the projections of all m tokens in one batched GEMV
@@ -292,9 +309,16 @@ enum BlockKind : uint32_t { kBlockInner = 0, kBlockLast = 1, kBlockVerify = 2 };
 // on every token of the block (one batched F16 GEMV, the head's weights
 // read once), logits [m][vocab] and each token's greedy successor; the
 // device position moves past the block and the last token's greedy id is
-// recorded as the step's.
-hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s) {
+// recorded as the step's.  kBlockTree: nodes 16 * block + i of a draft tree
+// (their ids in feed at the device position, which is the tree's base slot
+// plus 16 * block): each rotated for its position (prefix length + depth,
+// tree_pos), appended at its slot, attending to the prefix and its
+// ancestor-or-self slots (tree_mask); the head as kBlockVerify, into rows
+// 16 * block + i of vlogits / vids; the device position moves past the block.
+hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s, uint32_t block = 0) {
     const bool last = kind == kBlockLast;
+    const bool tree = kind == kBlockTree;
+    const uint32_t row0 = tree ? block * kPrefillTokens : 0;
     hipError_t e;
     const EmbedArgs ea = embed_args(d);
     hipLaunchKernelGGL(prefill_embed_kernel, dim3((ea.units * 4 + 255) / 256, m), dim3(256), 0, s, ea, m, d->px,
@@ -350,7 +374,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
         if ((e = project({w[P_Q], w[P_K], w[P_V]}, {d->pq, d->pk, d->pv}, kInNorm, d->px, nullptr, nin, D, false,
                          {layer_bias(d, l, P_Q), layer_bias(d, l, P_K), layer_bias(d, l, P_V)})) != hipSuccess ||
             (e = launch_rope_append(d->caches[l], d->pq, d->heads, d->pk, d->pv, d->cos_tab, d->sin_tab, d->ppos, s,
-                                    m, qn, kn, d->eps)) != hipSuccess)
+                                    m, qn, kn, d->eps, tree ? d->tree_pos + row0 : nullptr)) != hipSuccess)
             return e;
         if (d->fused_attention) {
             DecodeAttentionLaunch at;
@@ -363,12 +387,17 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
             at.span_tokens = d->max_ctx;
             at.scale = d->attn_scale;
             at.count = m;
+            if (tree) {
+                at.tree_mask = d->tree_mask + row0;
+                at.tree_base = d->tree_base;
+            }
             if ((e = launch_decode_attention(at, s)) != hipSuccess) return e;
         } else {
             for (uint32_t i = 0; i < m; ++i)
                 if ((e = launch_attention_at(d->caches[l], d->pq + static_cast<size_t>(i) * Q,
                                              d->pattn + static_cast<size_t>(i) * Q, d->heads, d->ppos + i,
-                                             d->attn_scale, d->partials, s)) != hipSuccess)
+                                             d->attn_scale, d->partials, s, tree ? d->tree_mask + row0 + i : nullptr,
+                                             tree ? d->tree_base : nullptr)) != hipSuccess)
                     return e;
         }
         if ((e = project({w[P_O]}, {d->px}, kInF32, d->pattn, nullptr, nullptr, Q, true,
@@ -381,7 +410,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
     hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(64), 0, s, d->state, d->ppos, m, last ? 1u : 0u);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (last) return enqueue_head(d, d->px + static_cast<size_t>(m - 1) * D, s);
-    if (kind == kBlockVerify) {
+    if (kind == kBlockVerify || tree) {
         // the head on every token: fp32 images (F16/BF16) or per-token int8
         // images of the normalized tokens (Q4_0/HyperVSQ-2), one batched GEMV
         if (d->head->kind == kF16)
@@ -390,14 +419,15 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s)
             e = launch_prepare_image(*d->head, kInNorm, d->px, nullptr, d->final_norm, d->eps, m, D, d->vimg,
                                      d->vimg_stride, d->pscales, nullptr, 0, s);
         if (e != hipSuccess) return e;
-        GemvGroupLaunch head = group({d->head}, {d->vlogits});
+        GemvGroupLaunch head = group({d->head}, {d->vlogits + static_cast<size_t>(row0) * d->vocab});
         head.image = d->vimg;
         head.image_stride = d->vimg_stride;
         if (d->head->kind != kF16) head.scales = d->pscales;
         head.batch = m;
         head.output_stride[0] = d->vocab;
         if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
-        return launch_rows_argmax(d->vlogits, m, d->vocab, d->vocab, d->vids, d->state, s);
+        return launch_rows_argmax(d->vlogits + static_cast<size_t>(row0) * d->vocab, m, d->vocab, d->vocab,
+                                  d->vids + row0, d->state, s);
     }
     return hipSuccess;
 }
@@ -519,6 +549,20 @@ hipError_t run_verify(Decoder *d, uint32_t m) {
     hipStream_t s = d->ctx->stream;
     return run_captured(s, &d->prefill_exec[m][kBlockVerify], &d->prefill_tried[m][kBlockVerify],
                         [&] { return enqueue_prefill(d, m, kBlockVerify, s); });
+}
+
+// The nodes of a draft tree, already in feed at the device position (the
+// tree's base slot), in blocks of up to 16 nodes: a node's ancestors come
+// before it, so every block finds them in the cache.
+hipError_t run_tree(Decoder *d, uint32_t count) {
+    hipStream_t s = d->ctx->stream;
+    for (uint32_t b = 0; b * kPrefillTokens < count; ++b) {
+        const uint32_t m = std::min(kPrefillTokens, count - b * kPrefillTokens);
+        const hipError_t e = run_captured(s, &d->tree_exec[b][m], &d->tree_tried[b][m],
+                                          [&] { return enqueue_prefill(d, m, kBlockTree, s, b); });
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // Runs one step: the captured graph when capture worked, else the kernels.
@@ -667,8 +711,12 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         d->vimg_stride =
             static_cast<uint32_t>((image_bytes(d->head->kind, d->head->units) + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
-        part(reinterpret_cast<void **>(&d->vlogits), P * d->vocab * 4);
-        part(reinterpret_cast<void **>(&d->vids), P * 4);
+        part(reinterpret_cast<void **>(&d->vlogits), static_cast<size_t>(kTreeNodes) * d->vocab * 4);
+        part(reinterpret_cast<void **>(&d->vids), kTreeNodes * 4);
+        part(reinterpret_cast<void **>(&d->tree_mask), kTreeNodes * 8);
+        part(reinterpret_cast<void **>(&d->tree_pos), kTreeNodes * 4);
+        part(reinterpret_cast<void **>(&d->tree_base), 4);
+        part(reinterpret_cast<void **>(&d->tree_path), kTreeNodes * 4);
     }
     // attention partials of the device-position kernels
     KvCache proto;
@@ -832,6 +880,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_reset(QwnCudaContextHandle *handle, QwnHipD
         set_error("invalid decoder handle");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
+    d->tree_nodes = 0;
     const int32_t state0[2] = {0, 0};
     std::vector<int32_t> feed(d->max_ctx, -1);
     hipError_t e = hipSetDevice(ctx->device);
@@ -892,6 +941,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_forward(QwnCudaContextHandle *handle, QwnHi
         set_error("invalid decoder step (token out of range or context full)");
         return QWN_CUDA_STATUS_INVALID_ARGUMENT;
     }
+    d->tree_nodes = 0;
     hipStream_t s = ctx->stream;
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess) e = hipMemcpyAsync(d->feed + d->position, &token, 4, hipMemcpyHostToDevice, s);
@@ -928,6 +978,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *handle, QwnHi
             set_error("prefill token %u out of range", i);
             return QWN_CUDA_STATUS_INVALID_ARGUMENT;
         }
+    d->tree_nodes = 0;
     hipStream_t s = ctx->stream;
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess)
@@ -965,6 +1016,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_verify(QwnCudaContextHandle *handle, QwnHip
             set_error("verify token %u out of range", i);
             return QWN_CUDA_STATUS_INVALID_ARGUMENT;
         }
+    d->tree_nodes = 0;
     hipStream_t s = ctx->stream;
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess)
@@ -996,12 +1048,114 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_truncate(QwnCudaContextHandle *handle, QwnH
     }
     // the cache slots past `position` are overwritten by the next tokens;
     // only the device position and the host mirror move
+    d->tree_nodes = 0;
     const int32_t pos = static_cast<int32_t>(position);
     hipError_t e = hipSetDevice(ctx->device);
     if (e == hipSuccess) e = hipMemcpyAsync(d->state + 1, &pos, 4, hipMemcpyHostToDevice, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return hip_fail("decoder truncate", e);
     d->position = position;
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_verify_tree(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                                 const int32_t *tokens, const int32_t *parents, uint32_t count,
+                                                 float *logits, int32_t *next_tokens) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !tokens || !parents || count == 0 || count > kTreeNodes) {
+        set_error("invalid tree verify request (1..%u nodes)", kTreeNodes);
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || static_cast<uint64_t>(d->position) + count > d->max_ctx) {
+        set_error("draft tree does not fit the decoder's context");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    // depth and ancestor-or-self mask of every node (c/qwanto_jetspec.c:33-49)
+    std::vector<uint64_t> mask(count);
+    std::vector<int32_t> pos(count);
+    std::vector<uint32_t> depth(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        const int32_t p = parents[i];
+        if (tokens[i] < 0 || static_cast<uint32_t>(tokens[i]) >= d->vocab || p < -1 || p >= static_cast<int32_t>(i)) {
+            set_error("tree node %u: token out of range or parent not an earlier node (or -1)", i);
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+        depth[i] = p < 0 ? 0 : depth[p] + 1;
+        mask[i] = (p < 0 ? 0ull : mask[p]) | (1ull << i);
+        pos[i] = static_cast<int32_t>(d->position + depth[i]);
+    }
+    // the masked attention runs in the one-split decode kernel or the MFMA kernel
+    if (!d->fused_attention && !mfma_attention_supported(d->caches[0], d->heads)) {
+        set_error("tree verify needs the decode or MFMA attention for this head shape");
+        return QWN_CUDA_STATUS_UNSUPPORTED;
+    }
+    d->tree_nodes = 0;
+    hipStream_t s = ctx->stream;
+    const int32_t base = static_cast<int32_t>(d->position);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->feed + d->position, tokens, static_cast<size_t>(count) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->tree_mask, mask.data(), count * 8, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->tree_pos, pos.data(), count * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->tree_base, &base, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = run_tree(d, count);
+    // the nodes stay in slots base .. base + count - 1 until a path is
+    // committed; the position stays at the prefix
+    if (e == hipSuccess) e = hipMemcpyAsync(d->state + 1, &base, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, d->vlogits, static_cast<size_t>(count) * d->vocab * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && next_tokens)
+        e = hipMemcpyAsync(next_tokens, d->vids, static_cast<size_t>(count) * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail("decoder tree verify", e);
+    d->tree_nodes = count;
+    d->tree_parents.assign(parents, parents + count);
+    d->tree_tokens.assign(tokens, tokens + count);
+    const uint64_t blocks = (count + kPrefillTokens - 1) / kPrefillTokens;
+    ctx->telemetry.gpu_matmul_count += blocks * (4ull * d->layers + 1);
+    return QWN_CUDA_STATUS_OK;
+}
+
+QWN_CUDA_ABI_API int qwn_hip_decoder_commit_path(QwnCudaContextHandle *handle, QwnHipDecoderHandle *h,
+                                                 const uint32_t *nodes, uint32_t length) {
+    Context *ctx = context_of(handle);
+    if (!ctx || !nodes || length == 0) {
+        set_error("invalid path commit request");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(ctx->mutex);
+    Decoder *d = decoder_of(ctx, h);
+    if (!d || d->tree_nodes == 0 || length > d->tree_nodes) {
+        set_error("no verified draft tree to commit from (or the path is longer than the tree)");
+        return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+    }
+    std::vector<int32_t> path(length), toks(length);
+    for (uint32_t k = 0; k < length; ++k) {
+        const int32_t want = k == 0 ? -1 : static_cast<int32_t>(nodes[k - 1]);
+        if (nodes[k] >= d->tree_nodes || d->tree_parents[nodes[k]] != want) {
+            set_error("path node %u is not %s", k, k == 0 ? "a root of the tree" : "a child of the previous node");
+            return QWN_CUDA_STATUS_INVALID_ARGUMENT;
+        }
+        path[k] = static_cast<int32_t>(nodes[k]);
+        toks[k] = d->tree_tokens[nodes[k]];
+    }
+    hipStream_t s = ctx->stream;
+    const int32_t next = static_cast<int32_t>(d->position + length);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->tree_path, path.data(), length * 4, hipMemcpyHostToDevice, s);
+    for (uint32_t l = 0; e == hipSuccess && l < d->layers; ++l)
+        e = launch_kv_commit_path(d->caches[l], d->tree_base, d->tree_path, length, s);
+    // the accepted tokens as the cache's history, and the position past them
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->feed + d->position, toks.data(), length * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(d->state + 1, &next, 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail("decoder path commit", e);
+    d->position += length;
+    d->tree_nodes = 0;
+    ctx->telemetry.kv_cache_kernel_count += d->layers;
     return QWN_CUDA_STATUS_OK;
 }
 
@@ -1024,6 +1178,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnH
             set_error("prompt token %u out of range", i);
             return QWN_CUDA_STATUS_INVALID_ARGUMENT;
         }
+    d->tree_nodes = 0;
     hipStream_t s = ctx->stream;
     const uint32_t p0 = d->position;
     std::vector<int32_t> feed(d->max_ctx - p0, -1);

@@ -283,12 +283,15 @@ size_t kv_cache_layout(KvCache &c, uint8_t *base);
 // [count][...] back to back, token i at slot pos_ptr[i].
 // q_norm/k_norm (both or neither, [head_dim]): per-head RMSNorm with eps
 // before the rotation (Qwen3, c/qwanto_decode.c:654-684), at most
-// kMaxNormHeads query + KV heads.
+// kMaxNormHeads query + KV heads.  rope_pos_ptr (optional, [count]): the
+// positions the tokens are rotated for when they differ from their slots
+// (a draft tree's node at slot P + index has position P + depth).
 constexpr int kMaxNormHeads = 128;
 hipError_t launch_rope_append(const KvCache &c, float *query, uint32_t query_heads, const float *key,
                               const float *value, const float *cos_tab, const float *sin_tab,
                               const int32_t *pos_ptr, hipStream_t stream, uint32_t count = 1,
-                              const float *q_norm = nullptr, const float *k_norm = nullptr, float eps = 0.0f);
+                              const float *q_norm = nullptr, const float *k_norm = nullptr, float eps = 0.0f,
+                              const int32_t *rope_pos_ptr = nullptr);
 
 // Quantize `count` consecutive tokens' fp32 K and V ([count][channels])
 // into slots token .. token + count - 1 (one launch per 32768 tokens).
@@ -349,6 +352,11 @@ struct DecodeAttentionLaunch {
     const float *q_norm = nullptr;    // with key: per-head q/k RMSNorm weights [head_dim]
     const float *k_norm = nullptr;    // before RoPE (both or neither)
     float eps = 0.0f;
+    // a block of draft-tree nodes (no key/value, position_ptr their slots):
+    // tree_mask[count] ancestor-or-self bits over slots *tree_base + a;
+    // slots below *tree_base (the prefix) are always attended
+    const uint64_t *tree_mask = nullptr;
+    const int32_t *tree_base = nullptr;
 };
 // int8 MFMA attention (no RoPE/append) over span tokens of the cache: the
 // position from position_ptr when non-null; partials of
@@ -359,7 +367,8 @@ size_t mfma_attention_workspace_floats(const KvCache &c, uint32_t query_heads, u
 uint32_t mfma_attention_launches(const KvCache &c, uint32_t query_heads, uint32_t span);
 hipError_t launch_mfma_attention(const KvCache &c, const float *query, float *output, float *partials,
                                  uint32_t query_heads, uint32_t position, const int32_t *position_ptr,
-                                 uint32_t span, float scale, hipStream_t stream);
+                                 uint32_t span, float scale, hipStream_t stream,
+                                 const uint64_t *tree_mask = nullptr, const int32_t *tree_base = nullptr);
 bool decode_attention_supported(const KvCache &c, uint32_t query_heads);
 uint32_t decode_split_tokens(const KvCache &c, uint32_t tokens);
 size_t decode_attention_workspace_floats(const KvCache &c, uint32_t query_heads, uint32_t tokens);
@@ -373,8 +382,18 @@ constexpr uint32_t kDevicePositionSplit = 64;
 hipError_t launch_kv_append_at(const KvCache &c, const float *key, const float *value,
                                const int32_t *token_ptr, hipStream_t stream);
 size_t attention_at_workspace_floats(const KvCache &c, uint32_t query_heads);
+// tree_mask / tree_base: a draft-tree node's ancestor mask (as in
+// DecodeAttentionLaunch; needs the MFMA attention, mfma_attention_supported).
 hipError_t launch_attention_at(const KvCache &c, const float *query, float *output,
                                uint32_t query_heads, const int32_t *position_ptr, float scale,
-                               float *partials, hipStream_t stream);
+                               float *partials, hipStream_t stream, const uint64_t *tree_mask = nullptr,
+                               const int32_t *tree_base = nullptr);
+
+// Keeps a draft tree's accepted path: for k < len, the K/V and scales of
+// slot base + path[k] move to slot base + k (path strictly increasing from
+// a node at index >= 0, each path[k] >= k, so an in-order copy never reads
+// a slot it has already overwritten).  path: device [len], len <= 64.
+hipError_t launch_kv_commit_path(const KvCache &c, const int32_t *base, const int32_t *path, uint32_t len,
+                                 hipStream_t stream);
 
 }  // namespace qwn
