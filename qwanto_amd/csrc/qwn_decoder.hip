@@ -180,6 +180,7 @@ struct Decoder {
     // verify blocks: the LM head on every token of the block
     float *vlogits = nullptr;       // [kTreeNodes][vocab]
     int32_t *vids = nullptr;        // [kTreeNodes] greedy id after each token
+    uint64_t *row_keys = nullptr;   // [kPrefillTokens][rows_argmax_parts(vocab)] argmax workspace
     uint8_t *vimg = nullptr;        // [kPrefillTokens][vimg_stride] fp32 LM-head images
     uint32_t vimg_stride = 0;
     // one graph per (block size, block kind: inner / ends the prompt / verify)
@@ -427,7 +428,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
         head.output_stride[0] = d->vocab;
         if ((e = launch_gemv_group(head, s)) != hipSuccess) return e;
         return launch_rows_argmax(d->vlogits + static_cast<size_t>(row0) * d->vocab, m, d->vocab, d->vocab,
-                                  d->vids + row0, d->state, s);
+                                  d->vids + row0, d->state, d->row_keys, s);
     }
     return hipSuccess;
 }
@@ -713,6 +714,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
         part(reinterpret_cast<void **>(&d->vlogits), static_cast<size_t>(kTreeNodes) * d->vocab * 4);
         part(reinterpret_cast<void **>(&d->vids), kTreeNodes * 4);
+        part(reinterpret_cast<void **>(&d->row_keys), P * rows_argmax_parts(d->vocab) * 8);
         part(reinterpret_cast<void **>(&d->tree_mask), kTreeNodes * 8);
         part(reinterpret_cast<void **>(&d->tree_pos), kTreeNodes * 4);
         part(reinterpret_cast<void **>(&d->tree_base), 4);

@@ -2893,35 +2893,83 @@ hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float 
 }
 
 // First index of the largest value of each row of [rows][cols] fp32
-// (c/qwanto_decode.c:2048-2065; NaN never wins): one workgroup per row.
-__global__ __launch_bounds__(1024) void rows_argmax_kernel(const float *__restrict__ v, uint32_t cols, uint32_t stride,
-                                                           int32_t *__restrict__ ids, int32_t *last_out) {
-    __shared__ uint64_t red[1024 / kWaveSize];
-    const float *row = v + static_cast<size_t>(blockIdx.x) * stride;
+// (c/qwanto_decode.c:2048-2065; NaN never wins), in two launches: each row
+// split over `parts` workgroups of 256 threads, each reducing its slice to
+// one key (float4 loads, four in flight per thread where the row allows),
+// then one workgroup per row reducing the parts' keys.  A row of the
+// 151936-entry vocabulary was one workgroup's 37 dependent load rounds.
+__device__ __forceinline__ uint64_t max_key(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__global__ __launch_bounds__(256) void rows_argmax_part_kernel(const float *__restrict__ v, uint32_t cols,
+                                                               uint32_t stride, uint32_t parts,
+                                                               uint64_t *__restrict__ keys) {
+    __shared__ uint64_t red[256 / kWaveSize];
+    const uint32_t row = blockIdx.y, part = blockIdx.x;
+    const float *r = v + static_cast<size_t>(row) * stride;
+    const uint32_t span = (cols + parts - 1) / parts;
+    const uint32_t c0 = part * span, c1 = min(cols, c0 + span);
     uint64_t key = 0;
-    for (uint32_t i = threadIdx.x; i < cols; i += blockDim.x) {
-        const uint64_t k = argmax_key(row[i], i);
-        key = k > key ? k : key;
+    // vector loads only where the whole float4 lies in [c0, c1) and the row
+    // start keeps them 16-byte aligned; the rest element by element
+    const bool vec = (reinterpret_cast<uintptr_t>(r) & 15u) == 0;
+    const uint32_t a0 = vec ? min(c1, (c0 + 3u) & ~3u) : c1;
+    const uint32_t a1 = vec ? max(a0, c1 & ~3u) : c1;
+    for (uint32_t i = c0 + threadIdx.x; i < a0; i += blockDim.x) key = max_key(key, argmax_key(r[i], i));
+    for (uint32_t i = a1 + threadIdx.x; i < c1; i += blockDim.x) key = max_key(key, argmax_key(r[i], i));
+    const float4 *r4 = reinterpret_cast<const float4 *>(r);
+    const uint32_t q0 = a0 / 4, q1 = a1 / 4;
+    uint32_t q = q0 + threadIdx.x;
+    for (; q + 3 * blockDim.x < q1; q += 4 * blockDim.x) {
+        float4 f[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[k] = r4[q + k * blockDim.x];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t e = 4 * (q + k * blockDim.x);
+            key = max_key(key, max_key(max_key(argmax_key(f[k].x, e), argmax_key(f[k].y, e + 1)),
+                                       max_key(argmax_key(f[k].z, e + 2), argmax_key(f[k].w, e + 3))));
+        }
     }
-    for (int off = kWaveSize / 2; off > 0; off >>= 1) {
-        const uint64_t o = shfl_xor_u64(key, off);
-        key = o > key ? o : key;
+    for (; q < q1; q += blockDim.x) {
+        const float4 f = r4[q];
+        const uint32_t e = 4 * q;
+        key = max_key(key, max_key(max_key(argmax_key(f.x, e), argmax_key(f.y, e + 1)),
+                                   max_key(argmax_key(f.z, e + 2), argmax_key(f.w, e + 3))));
     }
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) key = max_key(key, shfl_xor_u64(key, off));
     if (threadIdx.x % kWaveSize == 0) red[threadIdx.x / kWaveSize] = key;
     __syncthreads();
     if (threadIdx.x == 0) {
         uint64_t best = red[0];
-        for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) best = red[w] > best ? red[w] : best;
-        const int32_t id = best ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
-        ids[blockIdx.x] = id;
-        if (last_out && blockIdx.x == gridDim.x - 1) *last_out = id;
+        for (uint32_t w = 1; w < blockDim.x / kWaveSize; ++w) best = max_key(best, red[w]);
+        keys[static_cast<size_t>(row) * parts + part] = best;
     }
 }
 
+__global__ __launch_bounds__(64) void rows_argmax_finish_kernel(const uint64_t *__restrict__ keys, uint32_t parts,
+                                                                int32_t *__restrict__ ids, int32_t *last_out) {
+    const uint32_t row = blockIdx.x;
+    uint64_t key = 0;
+    for (uint32_t i = threadIdx.x; i < parts; i += blockDim.x) key = max_key(key, keys[static_cast<size_t>(row) * parts + i]);
+    for (int off = kWaveSize / 2; off > 0; off >>= 1) key = max_key(key, shfl_xor_u64(key, off));
+    if (threadIdx.x == 0) {
+        const int32_t id = key ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(key)) : 0;
+        ids[row] = id;
+        if (last_out && row == gridDim.x - 1) *last_out = id;
+    }
+}
+
+uint32_t rows_argmax_parts(uint32_t cols) { return std::min<uint32_t>(kRowsArgmaxMaxParts, (cols + 4095) / 4096); }
+
 hipError_t launch_rows_argmax(const float *v, uint32_t rows, uint32_t cols, uint32_t stride, int32_t *ids,
-                              int32_t *last_out, hipStream_t stream) {
-    if (rows == 0 || cols == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rows_argmax_kernel, dim3(rows), dim3(1024), 0, stream, v, cols, stride, ids, last_out);
+                              int32_t *last_out, uint64_t *keys, hipStream_t stream) {
+    if (rows == 0 || cols == 0 || !keys) return hipErrorInvalidValue;
+    const uint32_t parts = rows_argmax_parts(cols);
+    hipLaunchKernelGGL(rows_argmax_part_kernel, dim3(parts, rows), dim3(256), 0, stream, v, cols, stride, parts,
+                       keys);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(rows_argmax_finish_kernel, dim3(rows), dim3(64), 0, stream, keys, parts, ids, last_out);
     return hipGetLastError();
 }
 

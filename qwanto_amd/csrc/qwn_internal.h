@@ -246,9 +246,13 @@ hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float 
                              hipStream_t stream, uint32_t count = 1, uint32_t x_stride = 0,
                              uint32_t image_stride = 0);
 // First index of the largest value of every row of [rows][cols] fp32 into
-// ids[rows]; the last row's also into *last_out when given.
+// ids[rows]; the last row's also into *last_out when given.  keys: device
+// workspace of rows * rows_argmax_parts(cols) u64 (each row is split over
+// that many workgroups, then reduced).
+constexpr uint32_t kRowsArgmaxMaxParts = 32;
+uint32_t rows_argmax_parts(uint32_t cols);
 hipError_t launch_rows_argmax(const float *v, uint32_t rows, uint32_t cols, uint32_t stride, int32_t *ids,
-                              int32_t *last_out, hipStream_t stream);
+                              int32_t *last_out, uint64_t *keys, hipStream_t stream);
 // Reduce argmax partials [n] to the winning row index (first index on ties).
 hipError_t launch_argmax_finish(const uint64_t *partials, uint32_t n, int32_t *index_out, hipStream_t stream);
 
