@@ -553,24 +553,33 @@ __device__ __forceinline__ float i8f(uint32_t w, int i) {
 template <int D, int TPT>
 __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnArgs a) {
     constexpr int NT = 256 * TPT, NW = NT / 64;
+    constexpr int LW = NW / 2;                 // loader waves: the upper half of the workgroup
     constexpr int NG = D / 64;                 // Q8 scale groups per head
     constexpr int CH = 256;                    // tokens per chunk, TPT lanes each in the scores
+    constexpr int KCH = D / 16;                // 16-channel key chunks per token
     constexpr int CPT = D / TPT;               // key channels per lane
-    constexpr int KWT = CPT / 16;              // uint4 key words per lane
+    constexpr int KWT = CPT / 16;              // 16-byte key words per lane
     constexpr int KGL = CPT >= 64 ? CPT / 64 : 1;    // key scale groups per lane
     constexpr int WPG = KWT / KGL;                   // key words per lane and group
     constexpr int VGL = (NG + TPT - 1) / TPT;        // value scale groups per lane
-    constexpr int VW = CH * D / 16 / NT;       // value words (16 tokens x 1 channel) per thread
     constexpr int PH = NT / D;                 // P.V: phases of 4-token groups
+    constexpr int TSTEP = 4 * PH;              // P.V: token stride of a thread
+    constexpr int NIT = CH / TSTEP;            // P.V: a thread's 4-token groups per chunk
+    constexpr int KBLK = CH * D / 1024;        // 1 KB blocks of the chunk's keys (and of its values)
     constexpr uint32_t half = D / 2;
-    static_assert(NT / TPT == CH && (CPT >= 64 ? CPT % 64 == 0 : 64 % CPT == 0) && VW >= 1 && PH >= 1,
+    static_assert(NT / TPT == CH && (CPT >= 64 ? CPT % 64 == 0 : 64 % CPT == 0) && PH >= 1 && NIT % 4 == 0 &&
+                      D % 64 == 0 && NG <= LW && KBLK % LW == 0,
                   "decode attention geometry");
-    __shared__ __align__(16) float q_s[D];
-    __shared__ __align__(16) float s_s[CH];
+    // the chunk as the cache holds it (16 pages from a page boundary)
+    __shared__ __align__(16) int8_t k_l[CH * D];       // keys [page][16-channel chunk][slot][16]
+    __shared__ __align__(16) int8_t v_l[CH * D];       // values [page][channel][slot]
+    __shared__ __align__(16) float ksc_l[NG][CH];      // scales per group [quad][slot][page of the quad]
+    __shared__ __align__(16) float vsc_l[NG][CH];
+    __shared__ __align__(16) int8_t qp_s[3][D];        // the query as three int8 pieces
+    __shared__ float qs_s[NG];                         // the first piece's scale per group
+    __shared__ __align__(16) float pw_s[NG][CH];       // softmax weight x value scale, per group and slot
     __shared__ float red[2][NW];
     __shared__ __align__(16) float pv_s[PH * D];
-    __shared__ __align__(16) uint4 v_s[CH / 16 * D];   // the chunk's values [page][channel][16 tokens]
-    __shared__ float vsc_s[CH * NG];                   // and their scales
     __shared__ __align__(16) int8_t kcur[D];
     __shared__ __align__(16) int8_t vcur[D];
     __shared__ float kcur_s[NG], vcur_s[NG];
@@ -580,228 +589,255 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
     const bool writer = head % a.group == 0;  // appends the current token
     const uint32_t tid = threadIdx.x, lane = tid % 64;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const uint32_t slot = tid / TPT, part = tid % TPT;
+    // a wave's 64 / TPT slots, each in lanes l, l + 64 / TPT, ...: the
+    // lanes of one part read consecutive 16-byte key words of LDS (no bank
+    // conflicts), the parts of a slot are combined with one lane swizzle
+    constexpr uint32_t SPW = 64 / TPT;        // slots per wave
+    const uint32_t slot = wave * SPW + lane % SPW, part = lane / SPW;
     const uint32_t kgrp = part * CPT / 64;     // first scale group of this lane's key channels
-    // One round trip per chunk: the lanes of slot take token c0 + slot --
-    // its key row's D/4-channel parts and scales -- and each thread VW
-    // value words (page, channel) of the chunk; slots past the last
-    // readable token `lim`, and pages past its page, read that token or
-    // page instead, and are masked later.  The current token's slot is being
-    // written by this launch: its key, value bytes and scales come from LDS.
-    uint4 kr[KWT], vr[VW];
-    float ks[KGL], vsc[VGL];
-    auto load_chunk = [&](uint32_t c0, uint32_t lim) {
-        const uint32_t tl = min(c0 + slot, lim);
-#pragma unroll
-        for (int w = 0; w < KWT; ++w)
-            kr[w] = *reinterpret_cast<const uint4 *>(c.keys + k_index(c, tl, kvh, part * CPT + 16 * w));
-#pragma unroll
-        for (int w = 0; w < VW; ++w) {
-            const uint32_t i = tid + NT * w, pl = i / D, ch = i % D;
-            const uint32_t pg = min(c0 / kKvPageTokens + pl, lim / kKvPageTokens);
-            vr[w] = *reinterpret_cast<const uint4 *>(c.values + v_page_offset(c, pg, kvh, ch));
-        }
-#pragma unroll
-        for (int g = 0; g < KGL; ++g) ks[g] = c.key_scales[scale_index(c, tl, kvh * NG + kgrp + g)];
-#pragma unroll
-        for (int g = 0; g < VGL; ++g)
-            vsc[g] = c.value_scales[scale_index(c, tl, kvh * NG + min(part * VGL + g, NG - 1u))];
-    };
     const float *query = a.query + static_cast<size_t>(blockIdx.z) * a.token_stride + static_cast<size_t>(head) * D;
     float *out = a.output + static_cast<size_t>(blockIdx.z) * a.token_stride + static_cast<size_t>(head) * D;
     const bool rope = a.key != nullptr;
     const bool qk = rope && a.q_norm != nullptr;
     const bool row_only = rope && a.rope_row_only;
+    // Pin the argument fields of every early load: one batch of scalar
+    // loads and one wait ahead of the vector loads (a field read first at
+    // its use puts a dependent scalar round trip in front of the loads).
+    {
+        const uint64_t pk = reinterpret_cast<uint64_t>(c.keys), pv = reinterpret_cast<uint64_t>(c.values);
+        const uint64_t pks = reinterpret_cast<uint64_t>(c.key_scales);
+        const uint64_t pvs = reinterpret_cast<uint64_t>(c.value_scales);
+        const uint64_t pq = reinterpret_cast<uint64_t>(a.query), pkey = reinterpret_cast<uint64_t>(a.key);
+        const uint64_t pval = reinterpret_cast<uint64_t>(a.value), pct = reinterpret_cast<uint64_t>(a.cos_tab);
+        const uint64_t pst = reinterpret_cast<uint64_t>(a.sin_tab), pqn = reinterpret_cast<uint64_t>(a.q_norm);
+        const uint64_t pkn = reinterpret_cast<uint64_t>(a.k_norm), ppos = reinterpret_cast<uint64_t>(a.position_ptr);
+        asm volatile("" ::"s"(pk), "s"(pv), "s"(pks), "s"(pvs), "s"(pq), "s"(pkey), "s"(pval), "s"(pct), "s"(pst),
+                     "s"(pqn), "s"(pkn), "s"(ppos), "s"(c.pages), "s"(c.quads), "s"(c.max_tokens), "s"(a.group),
+                     "s"(a.token_stride), "s"(a.rope_row_only));
+    }
 
-    // 0. Every load the prologue needs, issued before anything waits (an
-    //    address is selected, never a load predicated: a load under a
-    //    per-lane condition makes the compiler drain the loads in flight
-    //    first): the first chunk (it does not depend on the position: its
-    //    tokens past the position are masked), the query element of thread
-    //    d < D with its RoPE partner, norm weights and cos/sin, and wave
-    //    gi < 2*NG's current key (gi < NG) or value 64-channel group.  Only
-    //    a RoPE table indexed by the position waits for the position.
-    load_chunk(0, c.max_tokens - 1);
+    // The loader waves copy a chunk of 256 tokens (pages p0 .. p0 + 15,
+    // clamped to the cache's last page / quad) straight into LDS: one 1 KB
+    // block per wave instruction, keys and values each a contiguous run of
+    // the KV head's pages, then each group's key and value scales (four
+    // 64-token quads, 1 KB).  Tokens past the readable ones are masked later.
+    auto issue_chunk = [&](uint32_t c0) {
+        const uint32_t lw = wave - LW;
+        const uint32_t p0 = c0 / kKvPageTokens, pmax = c.pages - 1, qmax = c.quads - 1;
+#pragma unroll
+        for (int jj = 0; jj < KBLK / LW; ++jj) {
+            const uint32_t j = jj * LW + lw, off = j * 1024 + lane * 16;
+            const uint32_t pg = min(p0 + off / (D * 16), pmax);
+            const size_t src = (static_cast<size_t>(kvh) * c.pages + pg) * (D * 16) + off % (D * 16);
+            __builtin_amdgcn_global_load_lds(c.keys + src, (lds_void *)(k_l + j * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(c.values + src, (lds_void *)(v_l + j * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int bb = 0; bb < (2 * NG + LW - 1) / LW; ++bb) {
+            const uint32_t b = bb * LW + lw;
+            if (b < 2u * NG) {
+                const uint32_t g = b % NG;
+                const uint32_t q = min(c0 / (4 * kKvPageTokens) + lane / 16, qmax);
+                const size_t src = (static_cast<size_t>(kvh * NG + g) * c.quads + q) * 64 + (lane % 16) * 4;
+                if (b < static_cast<uint32_t>(NG))
+                    __builtin_amdgcn_global_load_lds(c.key_scales + src, (lds_void *)(&ksc_l[g][0]), 16, 0, 0);
+                else
+                    __builtin_amdgcn_global_load_lds(c.value_scales + src, (lds_void *)(&vsc_l[g][0]), 16, 0, 0);
+            }
+        }
+    };
+
+    // 0. The loads.  Loader waves: the first chunk (it does not depend on
+    //    the position: its tokens past the position are masked).  Waves
+    //    w < NG, the prologue's: channel d = tid of the query with its RoPE
+    //    partner, of the current key and value, the norm weights and
+    //    cos/sin (a wave's loads return in issue order, so the prologue
+    //    never waits behind the chunk).  Only a RoPE table indexed by the
+    //    position waits for the position.
+    const bool loader = wave >= static_cast<uint32_t>(LW);
+    const bool prep = wave < static_cast<uint32_t>(NG);
     const uint32_t qd = tid % D, qi = qd < half ? qd : qd - half;
-    const float qa = query[rope ? qi : qd], qb = query[qi + half];
-    float qwa = 0.0f, qwb = 0.0f, qcs = 0.0f, qsn = 0.0f;
+    float qa = 0.0f, qb = 0.0f, ka = 0.0f, kb = 0.0f, va = 0.0f;
+    float qwa = 0.0f, qwb = 0.0f, kwa = 0.0f, kwb = 0.0f, cs = 0.0f, sn = 0.0f;
     const float *ct = a.cos_tab, *st = a.sin_tab;
-    if (row_only) {
-        qcs = ct[qi];
-        qsn = st[qi];
-    }
-    if (qk) {
-        qwa = a.q_norm[qi];
-        qwb = a.q_norm[qi + half];
-    }
-    const uint32_t gi = min(wave, 2u * NG - 1u);
-    const bool cv = gi >= NG;
-    const uint32_t cd = (cv ? gi - NG : gi) * 64 + lane, ci = cd < half ? cd : cd - half;
-    float ca = 0.0f, cb = 0.0f, cwa = 0.0f, cwb = 0.0f, ccs = 0.0f, csn = 0.0f;
-    if (rope) {
-        const float *kh = a.key + static_cast<size_t>(kvh) * D;
-        ca = *(cv ? a.value + static_cast<size_t>(kvh) * D + cd : kh + ci);
-        cb = kh[ci + half];
-        if (row_only) {
-            ccs = ct[ci];
-            csn = st[ci];
-        }
-        if (qk) {
-            cwa = a.k_norm[ci];
-            cwb = a.k_norm[ci + half];
+    if (loader) {
+        issue_chunk(0);
+    } else if (prep) {
+        qa = query[rope ? qi : qd];
+        qb = query[qi + half];
+        if (rope) {
+            const float *kh = a.key + static_cast<size_t>(kvh) * D;
+            ka = kh[qi];
+            kb = kh[qi + half];
+            va = a.value[static_cast<size_t>(kvh) * D + qd];
+            if (row_only) {
+                cs = ct[qi];
+                sn = st[qi];
+            }
+            if (qk) {
+                qwa = a.q_norm[qi];
+                qwb = a.q_norm[qi + half];
+                kwa = a.k_norm[qi];
+                kwb = a.k_norm[qi + half];
+            }
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
     const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(a.position_ptr[blockIdx.z]) : a.position;
-    if (rope && !row_only) {
+    const bool ok = pos < c.max_tokens;   // else the workgroup writes nothing and ends
+    if (prep && rope && !row_only && ok) {
         // a full RoPE table: the position's row
-        ct += static_cast<size_t>(pos) * half;
-        st += static_cast<size_t>(pos) * half;
-        qcs = ct[qi];
-        qsn = st[qi];
-        ccs = ct[ci];
-        csn = st[ci];
+        cs = ct[static_cast<size_t>(pos) * half + qi];
+        sn = st[static_cast<size_t>(pos) * half + qi];
     }
-    if (pos >= c.max_tokens) return;
     const uint32_t t1 = min(pos + 1, a.span);
-    const bool cur = rope && pos < t1;
+    const bool cur = ok && rope && pos < t1;
     const uint64_t tmask = a.tree_mask ? a.tree_mask[blockIdx.z] : 0ull;
     const uint32_t tbase = a.tree_mask ? static_cast<uint32_t>(*a.tree_base) : 0xffffffffu;
 
     // 1. q/k norms: 1/rms of the query head and of the current key head
-    //    from wave sums of squares (waves < D/64 hold the query, waves
-    //    < NG the key groups)
+    //    from the prologue waves' sums of squares
     float qinv = 1.0f, kinv = 1.0f;
     if (qk) {
-        const float qown = qd < half ? qa : qb;
-        const float qs2 = wave_sum_all(qown * qown);
-        const float kown = cd < half ? ca : cb;
-        const float ks2 = wave_sum_all(kown * kown);
-        if (lane == 0 && wave < static_cast<uint32_t>(D / 64)) nrm_s[wave] = qs2;
-        if (lane == 0 && wave < static_cast<uint32_t>(NG)) nrm_s[4 + wave] = ks2;
-        __syncthreads();
+        if (prep) {
+            const float qs2 = wave_sum_all((qd < half ? qa : qb) * (qd < half ? qa : qb));
+            const float ks2 = wave_sum_all((qd < half ? ka : kb) * (qd < half ? ka : kb));
+            if (lane == 0) {
+                nrm_s[wave] = qs2;
+                nrm_s[4 + wave] = ks2;
+            }
+        }
+        lds_barrier();
         float sq = 0.0f, sk = 0.0f;
 #pragma unroll
-        for (int w = 0; w < D / 64; ++w) sq += nrm_s[w];
-#pragma unroll
-        for (int g = 0; g < NG; ++g) sk += nrm_s[4 + g];
+        for (int g = 0; g < NG; ++g) {
+            sq += nrm_s[g];
+            sk += nrm_s[4 + g];
+        }
         qinv = 1.0f / sqrtf(sq / static_cast<float>(D) + a.eps);
         kinv = 1.0f / sqrtf(sk / static_cast<float>(D) + a.eps);
     }
 
-    // 2. the query head (normed and rotated in decode mode) -> LDS
-    if (tid < static_cast<uint32_t>(D)) {
+    // 2. Wave w < NG: query group w (normed and rotated in decode mode) as
+    //    three int8 pieces, q = s (q1 + q2 / 128 + q3 / 16384) with
+    //    s = max|q| / 127, each piece the rounded remainder of the ones
+    //    before: the scores are exact integer dot products with the int8
+    //    keys and the representation error is at most s / 32768 per channel
+    //    (below the fp32 rounding of max|q|); a non-finite query makes s NaN,
+    //    and so its scores.  Then the current token's key (normed, rotated)
+    //    and value group w, Q8-quantized.
+    if (prep) {
         float v = qa;
+        float xk = 0.0f;
         if (rope) {
-            float x0 = qa, x1 = qb;
+            float x0 = qa, x1 = qb, y0 = ka, y1 = kb;
             if (qk) {
                 x0 = (x0 * qinv) * qwa;
                 x1 = (x1 * qinv) * qwb;
+                y0 = (y0 * kinv) * kwa;
+                y1 = (y1 * kinv) * kwb;
             }
-            v = qd < half ? fmaf(x0, qcs, -(x1 * qsn)) : fmaf(x0, qsn, x1 * qcs);
+            v = qd < half ? fmaf(x0, cs, -(x1 * sn)) : fmaf(x0, sn, x1 * cs);
+            xk = qd < half ? fmaf(y0, cs, -(y1 * sn)) : fmaf(y0, sn, y1 * cs);
         }
-        q_s[qd] = v;
-    }
-    // the current token's key (normed, rotated) and value: one wave per
-    // 64-channel group, Q8-quantized
-    if (cur && wave < 2u * NG) {
-        float x = ca;
-        if (!cv) {
-            float x0 = ca, x1 = cb;
-            if (qk) {
-                x0 = (x0 * kinv) * cwa;
-                x1 = (x1 * kinv) * cwb;
+        const bool fin = isfinite(v);
+        const float amax = wave_max_all(fin ? fabsf(v) : 0.0f);
+        const float bad = wave_max_all(fin ? 0.0f : 1.0f);
+        const float s1 = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float inv1 = amax > 0.0f ? 127.0f / amax : 0.0f;
+        const float x = fin ? v : 0.0f;
+        const float p1 = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(x * inv1)));
+        const float r1 = fmaf(-p1, s1, x);
+        const float p2 = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(r1 * (inv1 * 128.0f))));
+        const float r2 = fmaf(-p2, s1 * 0x1p-7f, r1);
+        const float p3 = fminf(127.0f, fmaxf(-127.0f, __builtin_rintf(r2 * (inv1 * 16384.0f))));
+        qp_s[0][qd] = static_cast<int8_t>(p1);
+        qp_s[1][qd] = static_cast<int8_t>(p2);
+        qp_s[2][qd] = static_cast<int8_t>(p3);
+        if (lane == 0) qs_s[wave] = bad > 0.0f ? __builtin_nanf("") : s1;
+        if (cur) {
+            const float kmax = wave_max_all(isfinite(xk) ? fabsf(xk) : 0.0f);
+            const float vmax = wave_max_all(isfinite(va) ? fabsf(va) : 0.0f);
+            const float ksc = kmax > 0.0f ? kmax / 127.0f : 1.0f;
+            const float vsc = vmax > 0.0f ? vmax / 127.0f : 1.0f;
+            const int8_t kq = q8_of(xk, ksc), vq = q8_of(va, vsc);
+            kcur[qd] = kq;
+            vcur[qd] = vq;
+            if (writer) {
+                store_q8(c, false, pos, kvh, qd, kq);
+                store_q8(c, true, pos, kvh, qd, vq);
             }
-            x = cd < half ? fmaf(x0, ccs, -(x1 * csn)) : fmaf(x0, csn, x1 * ccs);
-        }
-        const uint32_t grp = cv ? gi - NG : gi;
-        const float amax = wave_max_all(isfinite(x) ? fabsf(x) : 0.0f);
-        const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-        const int8_t qv = q8_of(x, scale);
-        (cv ? vcur : kcur)[cd] = qv;
-        if (writer) store_q8(c, cv, pos, kvh, cd, qv);
-        if (lane == 0) {
-            (cv ? vcur_s : kcur_s)[grp] = scale;
-            if (writer) (cv ? c.value_scales : c.key_scales)[scale_index(c, pos, kvh * NG + grp)] = scale;
+            if (lane == 0) {
+                kcur_s[wave] = ksc;
+                vcur_s[wave] = vsc;
+                if (writer) {
+                    c.key_scales[scale_index(c, pos, kvh * NG + wave)] = ksc;
+                    c.value_scales[scale_index(c, pos, kvh * NG + wave)] = vsc;
+                }
+            }
         }
     }
-    __syncthreads();
+    if (loader) wait_vmcnt<0>();   // the chunk is in LDS
+    lds_barrier();
+    if (!ok) return;
 
     const uint32_t vch = tid % D, ph = tid / D;   // P.V channel and phase
     const uint32_t vgrp = vch / 64;
+    const uint32_t pl = slot / kKvPageTokens, s16 = slot % kKvPageTokens;
+    const uint32_t sidx = ((slot / (4 * kKvPageTokens)) * kKvPageTokens + s16) * 4 + pl % 4;   // in ksc_l/vsc_l
     float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;
     for (uint32_t c0 = 0; c0 < t1; c0 += CH) {
         const uint32_t n = min(static_cast<uint32_t>(CH), t1 - c0);
-        // 3. the chunk's loads (the first chunk's were issued at the start)
-        if (c0 != 0) load_chunk(c0, t1 - 1);
-        const bool has = slot < n && tree_attends(c0 + slot, tbase, tmask);
-        if (cur) {
-            // the current token's key part, scales and value byte
-            const bool is_cur = has && c0 + slot == pos;
-#pragma unroll
-            for (int w = 0; w < KWT; ++w) {
-                // component selects (a select of the uint4 struct goes through scratch)
-                const uint4 kc = reinterpret_cast<const uint4 *>(kcur)[part * KWT + w];
-                kr[w].x = is_cur ? kc.x : kr[w].x;
-                kr[w].y = is_cur ? kc.y : kr[w].y;
-                kr[w].z = is_cur ? kc.z : kr[w].z;
-                kr[w].w = is_cur ? kc.w : kr[w].w;
+        // 3. a later chunk: the previous one is consumed (barrier at the
+        //    end of its pass), the loader waves copy this one
+        if (c0 != 0) {
+            if (loader) {
+                issue_chunk(c0);
+                wait_vmcnt<0>();
             }
-#pragma unroll
-            for (int g = 0; g < KGL; ++g) ks[g] = is_cur ? kcur_s[kgrp + g] : ks[g];
-#pragma unroll
-            for (int g = 0; g < VGL; ++g) vsc[g] = is_cur ? vcur_s[min(part * VGL + g, NG - 1u)] : vsc[g];
-            const uint32_t cur_page = pos / kKvPageTokens - c0 / kKvPageTokens;
-            const uint32_t cw = (pos % kKvPageTokens) / 4, shift = 8 * (pos % 4);
-#pragma unroll
-            for (int w = 0; w < VW; ++w) {
-                const uint32_t i = tid + NT * w, pl = i / D, ch = i % D;
-                const bool hit = pos >= c0 && pl == cur_page;
-                const uint32_t b = static_cast<uint32_t>(static_cast<uint8_t>(vcur[ch])) << shift;
-                const uint32_t keep = ~(0xffu << shift);
-                vr[w].x = hit && cw == 0 ? (vr[w].x & keep) | b : vr[w].x;
-                vr[w].y = hit && cw == 1 ? (vr[w].y & keep) | b : vr[w].y;
-                vr[w].z = hit && cw == 2 ? (vr[w].z & keep) | b : vr[w].z;
-                vr[w].w = hit && cw == 3 ? (vr[w].w & keep) | b : vr[w].w;
-            }
+            lds_barrier();
         }
-        // the value words and the tokens' scales -> LDS for the P.V phase
-#pragma unroll
-        for (int w = 0; w < VW; ++w) v_s[tid + NT * w] = vr[w];
-#pragma unroll
-        for (int g = 0; g < VGL; ++g)
-            if (part * VGL + g < static_cast<uint32_t>(NG)) vsc_s[slot * NG + part * VGL + g] = has ? vsc[g] : 0.0f;
-        // 4. the score of this lane's token: its channels, scaled by their
-        //    group's key scale, summed over the token's four lanes
+        const bool has = slot < n && tree_attends(c0 + slot, tbase, tmask);
+        // the current token's slot is being written by this launch: its key,
+        // scales and value byte come from kcur / vcur
+        const bool is_cur = cur && has && c0 + slot == pos;
+        // 4. the score of this lane's token: per scale group, the exact int8
+        //    dot products of its key channels with the three query pieces,
+        //    scaled by the key scale and the piece scale, summed over the
+        //    token's TPT lanes
         float sc = 0.0f;
 #pragma unroll
         for (int g = 0; g < KGL; ++g) {
-            float pg = 0.0f;
+            int d1 = 0, d2 = 0, d3 = 0;
 #pragma unroll
             for (int w = g * WPG; w < (g + 1) * WPG; ++w) {
-                const uint4 kw = kr[w];
-                const uint32_t k4[4] = {kw.x, kw.y, kw.z, kw.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t d0 = part * CPT + w * 16 + e * 4;
-                    const float4 qq = *reinterpret_cast<const float4 *>(q_s + d0);
-                    pg = fmaf(qq.x, i8f(k4[e], 0), pg);
-                    pg = fmaf(qq.y, i8f(k4[e], 1), pg);
-                    pg = fmaf(qq.z, i8f(k4[e], 2), pg);
-                    pg = fmaf(qq.w, i8f(k4[e], 3), pg);
-                }
+                const uint32_t kc = part * (CPT / 16) + w;   // 16-channel chunk of this word
+                const int8_t *kp = is_cur ? kcur + kc * 16 : k_l + ((pl * KCH + kc) * kKvPageTokens + s16) * 16;
+                const uint4 kw = *reinterpret_cast<const uint4 *>(kp);
+                const uint4 a1 = *reinterpret_cast<const uint4 *>(&qp_s[0][kc * 16]);
+                const uint4 a2 = *reinterpret_cast<const uint4 *>(&qp_s[1][kc * 16]);
+                const uint4 a3 = *reinterpret_cast<const uint4 *>(&qp_s[2][kc * 16]);
+                d1 = sdot4(kw.x, a1.x, d1); d1 = sdot4(kw.y, a1.y, d1);
+                d1 = sdot4(kw.z, a1.z, d1); d1 = sdot4(kw.w, a1.w, d1);
+                d2 = sdot4(kw.x, a2.x, d2); d2 = sdot4(kw.y, a2.y, d2);
+                d2 = sdot4(kw.z, a2.z, d2); d2 = sdot4(kw.w, a2.w, d2);
+                d3 = sdot4(kw.x, a3.x, d3); d3 = sdot4(kw.y, a3.y, d3);
+                d3 = sdot4(kw.z, a3.z, d3); d3 = sdot4(kw.w, a3.w, d3);
             }
-            sc = fmaf(pg, ks[g], sc);
+            const float f = fmaf(static_cast<float>(d3), 0x1p-14f,
+                                 fmaf(static_cast<float>(d2), 0x1p-7f, static_cast<float>(d1)));
+            const uint32_t gk = kgrp + g;
+            const float ks = is_cur ? kcur_s[gk] : ksc_l[gk][sidx];
+            sc = fmaf(ks * qs_s[gk], f, sc);
         }
 #pragma unroll
-        for (int off = 1; off < TPT; off <<= 1) sc += __shfl_xor(sc, off);
+        for (int off = SPW; off < 64; off <<= 1) sc += __shfl_xor(sc, off);
         // 5. chunk softmax, running max and sum
         sc = has ? sc * a.scale : -INFINITY;
         {
             const float m = wave_max_all(sc);
             if (lane == 0) red[0][wave] = m;
         }
-        __syncthreads();
+        lds_barrier();
         float mc = red[0][0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) mc = fmaxf(mc, red[0][w]);
@@ -809,37 +845,62 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
         const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - mn);
         m_run = mn;
         const float p = has ? expf(sc - mn) : 0.0f;
-        if (part == 0) s_s[slot] = p;
+        // the weight of each value group of the slot: p times the token's
+        // value scale (masked slots 0: their scales may be any bits)
+#pragma unroll
+        for (int g = 0; g < VGL; ++g) {
+            const uint32_t gg = part * VGL + g;
+            if (gg < static_cast<uint32_t>(NG)) {
+                const float vs = is_cur ? vcur_s[gg] : vsc_l[gg][sidx];
+                pw_s[gg][slot] = has ? p * vs : 0.0f;
+            }
+        }
         {
             const float ps = wave_sum_all(part == 0 ? p : 0.0f);
             if (lane == 0) red[1][wave] = ps;
         }
-        __syncthreads();
+        lds_barrier();
         float lc = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) lc += red[1][w];
         l_run = l_run * alpha + lc;
         acc *= alpha;
-        // 6. P.V of this thread's channel over its 4-token groups (from LDS)
-        const uint32_t *v_u32 = reinterpret_cast<const uint32_t *>(v_s);
-        for (uint32_t tl = 4 * ph; tl < n; tl += 4 * PH) {
-            const uint32_t vw = v_u32[((tl / kKvPageTokens) * D + vch) * 4 + (tl % kKvPageTokens) / 4];
-            const float v0 = i8f(vw, 0) * vsc_s[tl * NG + vgrp];
-            const float v1 = i8f(vw, 1) * vsc_s[(tl + 1) * NG + vgrp];
-            const float v2 = i8f(vw, 2) * vsc_s[(tl + 2) * NG + vgrp];
-            const float v3 = i8f(vw, 3) * vsc_s[(tl + 3) * NG + vgrp];
-            const float4 pp = *reinterpret_cast<const float4 *>(s_s + tl);
-            acc = fmaf(pp.x, v0, acc);
-            acc = fmaf(pp.y, v1, acc);
-            acc = fmaf(pp.z, v2, acc);
-            acc = fmaf(pp.w, v3, acc);
+        // 6. P.V of this thread's channel over its 4-token groups (from LDS),
+        //    four groups' loads at a time; the first token of a batch decides
+        //    (per wave) whether it runs, masked slots carry weight 0.  The
+        //    current token's byte replaces the cache's in its group.
+        const uint32_t ctl = cur && pos >= c0 && pos - c0 < static_cast<uint32_t>(CH) ? pos - c0 : 0xffffffffu;
+        const uint32_t cshift = 8 * (ctl % 4), cbyte = static_cast<uint32_t>(static_cast<uint8_t>(vcur[vch])) << cshift;
+        const uint32_t *v_u32 = reinterpret_cast<const uint32_t *>(v_l);
+        const float *pw = pw_s[vgrp];
+#pragma unroll
+        for (int q4 = 0; q4 < NIT / 4; ++q4) {
+            if (4 * ph + TSTEP * 4 * q4 >= n) break;
+            uint32_t vw[4];
+            float4 pp[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t tl = 4 * ph + TSTEP * (4 * q4 + i);
+                vw[i] = v_u32[((tl / kKvPageTokens) * D + vch) * 4 + (tl % kKvPageTokens) / 4];
+                pp[i] = *reinterpret_cast<const float4 *>(pw + tl);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t tl = 4 * ph + TSTEP * (4 * q4 + i);
+                const uint32_t w4 = tl == (ctl & ~3u) ? (vw[i] & ~(0xffu << cshift)) | cbyte : vw[i];
+                acc = fmaf(pp[i].x, i8f(w4, 0), acc);
+                acc = fmaf(pp[i].y, i8f(w4, 1), acc);
+                acc = fmaf(pp[i].z, i8f(w4, 2), acc);
+                acc = fmaf(pp[i].w, i8f(w4, 3), acc);
+            }
         }
-        __syncthreads();
+        // the next chunk overwrites the chunk and the weights
+        if (c0 + CH < t1) lds_barrier();
     }
 
     // 7. sum the token phases; the output
     pv_s[ph * D + vch] = acc;
-    __syncthreads();
+    lds_barrier();
     if (tid < static_cast<uint32_t>(D)) {
         float o = 0.0f;
 #pragma unroll

@@ -48,6 +48,28 @@ __device__ __forceinline__ float dpp_max_step(float v) {
     return fmaxf(v, __builtin_bit_cast(float, moved));
 }
 
+// LDS address space, for the direct global-to-LDS loads
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n) (n <= 63), expcnt and lgkmcnt left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    constexpr int n = N > 63 ? 63 : N;
+    __builtin_amdgcn_s_waitcnt((n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// Compiler-level fence plus the hardware barrier, without the vmcnt(0)
+// that __syncthreads() implies: LDS writes before it are visible after it,
+// global loads and stores in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Whole-wave sum / max, returned to every lane (row reductions by DPP, then
 // the four row totals read as scalars and combined in row order).
 __device__ __forceinline__ float wave_sum_all(float v) {

@@ -60,7 +60,6 @@ namespace {
 constexpr uint32_t kMask33 = 0x33333333u;
 constexpr uint32_t kFlip8 = 0x88888888u;
 
-typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot8(static_cast<int>(a), static_cast<int>(b), c, false);
@@ -286,12 +285,6 @@ __device__ __forceinline__ void issue_image_copy(const uint8_t *__restrict__ ima
     }
 }
 
-// s_waitcnt vmcnt(n) (n <= 63), expcnt and lgkmcnt left alone.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    constexpr int n = N > 63 ? 63 : N;
-    __builtin_amdgcn_s_waitcnt((n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
 
 // ---- per-unit integer cores (shared by the GEMV and the dump kernel) ----
 
@@ -372,17 +365,6 @@ __device__ __forceinline__ float mul_rounded(float a, float b) {
 __device__ __forceinline__ float add_rounded(float a, float b) {
 #pragma clang fp contract(off)
     return a + b;
-}
-
-// Compiler-level fence plus the hardware barrier, without the vmcnt(0)
-// that __syncthreads() implies (the weight stream stays in flight).
-__device__ __forceinline__ void lds_barrier() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Workgroup reductions for the fused prologue: every thread gets the same
