@@ -2304,9 +2304,20 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
 // decode-size GEMV fits in one residency round of the chip and more rows
 // share each workgroup's activation image; shorter rows take one unit per
 // lane.  Idle lanes cost VALU slots but no memory traffic (compact tiles).
+// Narrow quantized tensors (at most 2048 columns, fewer than 4x as many rows:
+// the attention projections of a small model) take one unit per lane too: a
+// wave's dot products are one serial chain of about 160 VALU instructions per
+// HyperVSQ-2 unit (60 per Q4_0 unit) that no other wave shares its SIMD
+// with at these grid sizes, so halving it shortens the launch (Qwen2-1.5B
+// Q4_0 q/k/v 2.96 -> 2.70 us, o 2.92 -> 2.65 from images, 4.09 -> 3.65 and
+// 3.69 -> 3.44 with the fused prologue); the FFN rows keep two (there the
+// doubled grid repeats the fused prologue in twice the workgroups: gate+up
+// 7.12 -> 8.24 us).  q, k and v share the columns and have at most the
+// hidden size of rows, so a grouped launch's tensors always agree.
 bool layout_tensor(DeviceTensor &t) {
     if (!set_units(t)) return false;
-    const uint32_t per_lane = t.kind == kF16 ? 4 : (t.units >= 8 ? 2 : 1);
+    const bool narrow = t.kind != kF16 && t.cols <= 2048 && t.rows < 4 * t.cols;
+    const uint32_t per_lane = t.kind == kF16 ? 4 : (t.units >= 8 && !narrow ? 2 : 1);
     const uint32_t target = (t.units + per_lane - 1) / per_lane;
     uint32_t L = 1;
     while (L < target && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
