@@ -654,8 +654,13 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
     //    cos/sin (a wave's loads return in issue order, so the prologue
     //    never waits behind the chunk).  Only a RoPE table indexed by the
     //    position waits for the position.
+    // the current value's quantization takes waves NG .. 2NG-1 where they
+    // are not loaders (head_dim <= 128), else it joins the query's waves
+    constexpr bool VSEP = 2 * NG <= LW;
     const bool loader = wave >= static_cast<uint32_t>(LW);
     const bool prep = wave < static_cast<uint32_t>(NG);
+    const bool vprep = VSEP ? (wave >= static_cast<uint32_t>(NG) && wave < 2u * NG) : prep;
+    const uint32_t vwave = VSEP ? wave - NG : wave;   // value group of a vprep wave
     const uint32_t qd = tid % D, qi = qd < half ? qd : qd - half;
     float qa = 0.0f, qb = 0.0f, ka = 0.0f, kb = 0.0f, va = 0.0f;
     float qwa = 0.0f, qwb = 0.0f, kwa = 0.0f, kwb = 0.0f, cs = 0.0f, sn = 0.0f;
@@ -669,7 +674,7 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
             const float *kh = a.key + static_cast<size_t>(kvh) * D;
             ka = kh[qi];
             kb = kh[qi + half];
-            va = a.value[static_cast<size_t>(kvh) * D + qd];
+            if (!VSEP) va = a.value[static_cast<size_t>(kvh) * D + qd];
             if (row_only) {
                 cs = ct[qi];
                 sn = st[qi];
@@ -681,6 +686,8 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
                 kwb = a.k_norm[qi + half];
             }
         }
+    } else if (VSEP && vprep && rope) {
+        va = a.value[static_cast<size_t>(kvh) * D + qd];
     }
     const uint32_t pos = a.position_ptr ? static_cast<uint32_t>(a.position_ptr[blockIdx.z]) : a.position;
     const bool ok = pos < c.max_tokens;   // else the workgroup writes nothing and ends
@@ -723,8 +730,8 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
     //    before: the scores are exact integer dot products with the int8
     //    keys and the representation error is at most s / 32768 per channel
     //    (below the fp32 rounding of max|q|); a non-finite query makes s NaN,
-    //    and so its scores.  Then the current token's key (normed, rotated)
-    //    and value group w, Q8-quantized.
+    //    and so its scores.  Then the current token's key group w (normed,
+    //    rotated), Q8-quantized; its value groups in the vprep waves.
     if (prep) {
         float v = qa;
         float xk = 0.0f;
@@ -756,24 +763,25 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
         if (lane == 0) qs_s[wave] = bad > 0.0f ? __builtin_nanf("") : s1;
         if (cur) {
             const float kmax = wave_max_all(isfinite(xk) ? fabsf(xk) : 0.0f);
-            const float vmax = wave_max_all(isfinite(va) ? fabsf(va) : 0.0f);
             const float ksc = kmax > 0.0f ? kmax / 127.0f : 1.0f;
-            const float vsc = vmax > 0.0f ? vmax / 127.0f : 1.0f;
-            const int8_t kq = q8_of(xk, ksc), vq = q8_of(va, vsc);
+            const int8_t kq = q8_of(xk, ksc);
             kcur[qd] = kq;
-            vcur[qd] = vq;
-            if (writer) {
-                store_q8(c, false, pos, kvh, qd, kq);
-                store_q8(c, true, pos, kvh, qd, vq);
-            }
+            if (writer) store_q8(c, false, pos, kvh, qd, kq);
             if (lane == 0) {
                 kcur_s[wave] = ksc;
-                vcur_s[wave] = vsc;
-                if (writer) {
-                    c.key_scales[scale_index(c, pos, kvh * NG + wave)] = ksc;
-                    c.value_scales[scale_index(c, pos, kvh * NG + wave)] = vsc;
-                }
+                if (writer) c.key_scales[scale_index(c, pos, kvh * NG + wave)] = ksc;
             }
+        }
+    }
+    if (vprep && cur) {
+        const float vmax = wave_max_all(isfinite(va) ? fabsf(va) : 0.0f);
+        const float vsc = vmax > 0.0f ? vmax / 127.0f : 1.0f;
+        const int8_t vq = q8_of(va, vsc);
+        vcur[qd] = vq;
+        if (writer) store_q8(c, true, pos, kvh, qd, vq);
+        if (lane == 0) {
+            vcur_s[vwave] = vsc;
+            if (writer) c.value_scales[scale_index(c, pos, kvh * NG + vwave)] = vsc;
         }
     }
     if (loader) wait_vmcnt<0>();   // the chunk is in LDS
