@@ -30,6 +30,12 @@ QWEN2_LIKE = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, 
                   max_ctx=80, rope_theta=1e6, rms_eps=1e-6)
 # a context of more than one split: RoPE/append kernel + MFMA split attention
 LONG_CTX = dict(SMALL, max_ctx=1500)
+# contexts of one split past the first 256-token chunk(s) of the fused
+# decode attention (head_dim 64, 128 and 256)
+MID_CTX = dict(SMALL, max_ctx=640)
+MID_QWEN2 = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, head_dim=128, vocab=4096,
+                 max_ctx=640, rope_theta=1e6, rms_eps=1e-6)
+MID_HD256 = dict(SMALL, heads=2, kv_heads=1, head_dim=256, max_ctx=640)
 
 
 def with_norms(rng, model):
@@ -142,7 +148,11 @@ def read_caches(dec, layers, count):
     (LONG_CTX, "q4_0", 24, True, ""),
     # biases through the MFMA GEMM epilogue (6+-token Q4_0 and 3+-token HyperVSQ-2 blocks) and the dot8 GEMV
     (QWEN2_LIKE, "q4_0", 37, False, "qkv"), (QWEN2_LIKE, "hvsq2", 20, False, "qkvo"),
-    (SMALL, "q4_0", 5, False, "qkvo")])
+    (SMALL, "q4_0", 5, False, "qkvo"),
+    # prompts past the fused decode attention's 256-token chunks: the block
+    # prefill and the token-by-token steps both cross chunk boundaries
+    (MID_CTX, "q4_0", 270, False, ""), (MID_CTX, "hvsq2", 520, True, ""), (MID_QWEN2, "q4_0", 300, False, ""),
+    (MID_HD256, "q4_0", 270, True, "")])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
     """qwn_hip_decoder_prefill (prompt blocks of up to 16 tokens through the
     batched GEMV / int8 MFMA GEMM, block RoPE/append, causal attention per
@@ -156,7 +166,10 @@ def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P,
     Their Q8 caches: layer 0, whose input is the embedding itself, holds the
     same int8 values except where a value sits at a rounding boundary (one
     int8 step, at most 2% of the entries); deeper layers carry those flips'
-    effects forward, so at most 5% of their entries may differ."""
+    effects forward, so at most 5% of their entries may differ -- 8% past
+    128 prompt tokens, where each position's attention mixes more flipped
+    entries (3 layers at head_dim 128 and 300 tokens: 5.3-5.6% in layer 2,
+    with this decode attention and with the one before it)."""
     rng = np.random.default_rng(77 + P)
     model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, qk_norm=qk, biases=bias))
     prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
@@ -195,7 +208,8 @@ def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P,
             if l == 0:
                 assert d.max() <= 1 and frac <= 0.02, f"layer 0 {name}: {frac:.3%} differ, by up to {d.max()}"
             else:
-                assert frac <= 0.05, f"layer {l} {name}: {frac:.3%} of entries differ (by up to {d.max()})"
+                deep = 0.05 if P < 128 else 0.08
+                assert frac <= deep, f"layer {l} {name}: {frac:.3%} of entries differ (by up to {d.max()})"
         for name, x, y in (("key scales", pc[2], sc[2]), ("value scales", pc[3], sc[3])):
             rel = np.abs(x.astype(np.float64) - y) / np.abs(y)
             bound = 1.0 / 127 if l == 0 else 0.1

@@ -27,6 +27,8 @@ QWEN2_LIKE = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, 
                   max_ctx=128, rope_theta=1e6, rms_eps=1e-6)
 # past one split: the MFMA split attention with the tree mask
 LONG_CTX = dict(SMALL, max_ctx=1500)
+# one split, past the fused decode attention's first 256-token chunks
+MID_CTX = dict(SMALL, max_ctx=640)
 ENV_SEEDS = tuple(range(1, 9))
 
 
@@ -66,7 +68,9 @@ def path_to(parents, i):
     (SMALL, "q4_0", 20, (3, 8, 14, 15)), (QWEN2_LIKE, "hvsq2", 12, (3, 8, 14, 15)),
     (QWEN2_LIKE, "q4_0", 7, (3, 8, 14, 15)), (LONG_CTX, "hvsq2", 300, (3, 8, 14, 15)),
     # 64 nodes (four 16-node blocks), depth 8: the reference's limits (c/qwanto_jetspec.h:17-18)
-    (SMALL, "hvsq2", 9, (2, 4, 6, 8, 10, 10, 12, 12)), (LONG_CTX, "q4_0", 600, (1, 3, 6, 10, 14, 14, 16))])
+    (SMALL, "hvsq2", 9, (2, 4, 6, 8, 10, 10, 12, 12)), (LONG_CTX, "q4_0", 600, (1, 3, 6, 10, 14, 14, 16)),
+    # nodes straddling the 256- and 512-token chunk boundaries
+    (MID_CTX, "q4_0", 240, (3, 8, 14, 15)), (MID_CTX, "hvsq2", 500, (2, 4, 6, 8, 10, 10, 12, 12))])
 def test_tree_verify_matches_oracle_paths(gpu_ctx, oracle_lib, cfg, dtype, P, levels):
     rng = np.random.default_rng(1300 + P + sum(levels))
     model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
