@@ -43,6 +43,7 @@
 #include "qwn_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace qwn {
 
@@ -152,8 +153,13 @@ __host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHv
 // written instead of q8 (one sub-block is one 8- or 16-byte slot of that
 // image; HyperVSQ-2's block sums are reduced over the adjacent lanes
 // holding the block); tokens >= M of the image are left as they are (the GEMM neither
-// mixes token columns nor stores those tokens).
-template <int KIND>
+// mixes token columns nor stores those tokens).  EPT > 0 (K <= 1024 EPT,
+// the row staged): thread t loads elements t + 1024 e of the input (and of
+// the norm weights or the SwiGLU up half) into registers in one batch of
+// loads before anything waits, and the two reductions meet at LDS-only
+// barriers; the sums and maxima are taken in the same order as the EPT = 0
+// loop, which re-reads the row from global memory.
+template <int KIND, int EPT>
 __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
                                                               uint32_t x_stride, uint32_t units, uint8_t *image,
                                                               uint32_t image_stride, float *scales, int8_t *q8,
@@ -162,23 +168,12 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
                                                               const float *__restrict__ norm, float eps,
                                                               uint32_t staged, uint8_t *mimg) {
     extern __shared__ float vals[];  // [K] when staged
-    __shared__ float wave_red[1024 / kWaveSize];
+    __shared__ float wave_red[2][1024 / kWaveSize];
     constexpr uint32_t E = fused_sub_elems(KIND);
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t W = blockDim.x / kWaveSize;
     const float *row = x + static_cast<size_t>(t) * x_stride;
     float inv_rms = 1.0f;
-    if (mode == kInNorm) {
-        float ss = 0.0f;
-        for (uint32_t k = tid; k < K; k += blockDim.x) ss = fmaf(row[k], row[k], ss);
-        ss = wave_sum_all(ss);
-        if (tid % kWaveSize == 0) wave_red[tid / kWaveSize] = ss;
-        __syncthreads();
-        float tot = wave_red[0];
-        for (uint32_t w = 1; w < W; ++w) tot += wave_red[w];
-        inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
-        __syncthreads();
-    }
     auto value = [&](uint32_t k) {
         const float v = row[k];
         if (mode == kInNorm) return (v * inv_rms) * norm[k];
@@ -186,16 +181,66 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
         return v;
     };
     float amax = 0.0f;
-    for (uint32_t k = tid; k < K; k += blockDim.x) {
-        const float v = value(k);
-        if (staged) vals[k] = v;
-        amax = fmaxf(amax, fabsf(v));
+    if constexpr (EPT > 0) {
+        const float *ysrc = mode == kInNorm ? norm : mode == kInSwiglu ? x2 + static_cast<size_t>(t) * x_stride : row;
+        float xv[EPT], yv[EPT];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            const uint32_t k = tid + 1024u * e, kk = k < K ? k : 0u;
+            xv[e] = row[kk];
+            yv[e] = ysrc[kk];
+        }
+        if (mode == kInNorm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e)
+                if (tid + 1024u * e < K) ss = fmaf(xv[e], xv[e], ss);
+            ss = wave_sum_all(ss);
+            if (tid % kWaveSize == 0) wave_red[0][tid / kWaveSize] = ss;
+            lds_barrier();
+            float tot = wave_red[0][0];
+            for (uint32_t w = 1; w < W; ++w) tot += wave_red[0][w];
+            inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+        }
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            const uint32_t k = tid + 1024u * e;
+            if (k < K) {
+                const float xe = xv[e];
+                const float v = mode == kInNorm     ? (xe * inv_rms) * yv[e]
+                                : mode == kInSwiglu ? (xe / (1.0f + expf(-xe))) * yv[e]
+                                                    : xe;
+                vals[k] = v;
+                amax = fmaxf(amax, fabsf(v));
+            }
+        }
+        amax = wave_max_all(amax);
+        if (tid % kWaveSize == 0) wave_red[1][tid / kWaveSize] = amax;
+        lds_barrier();
+        amax = wave_red[1][0];
+        for (uint32_t w = 1; w < W; ++w) amax = fmaxf(amax, wave_red[1][w]);
+    } else {
+        if (mode == kInNorm) {
+            float ss = 0.0f;
+            for (uint32_t k = tid; k < K; k += blockDim.x) ss = fmaf(row[k], row[k], ss);
+            ss = wave_sum_all(ss);
+            if (tid % kWaveSize == 0) wave_red[0][tid / kWaveSize] = ss;
+            __syncthreads();
+            float tot = wave_red[0][0];
+            for (uint32_t w = 1; w < W; ++w) tot += wave_red[0][w];
+            inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+        }
+        for (uint32_t k = tid; k < K; k += blockDim.x) {
+            const float v = value(k);
+            if (staged) vals[k] = v;
+            amax = fmaxf(amax, fabsf(v));
+        }
+        amax = wave_max_all(amax);
+        if (tid % kWaveSize == 0) wave_red[1][tid / kWaveSize] = amax;
+        __syncthreads();
+        amax = wave_red[1][0];
+        for (uint32_t w = 1; w < W; ++w) amax = fmaxf(amax, wave_red[1][w]);
     }
-    amax = wave_max_all(amax);
-    if (tid % kWaveSize == 0) wave_red[tid / kWaveSize] = amax;
-    __syncthreads();
-    amax = wave_red[0];
-    for (uint32_t w = 1; w < W; ++w) amax = fmaxf(amax, wave_red[w]);
     // IEEE division and reciprocal, as the CPU path (c/qwanto_kernels.c:385-386)
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / scale;
@@ -2408,16 +2453,24 @@ hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const floa
         return hipErrorInvalidValue;
     const uint32_t staged = static_cast<size_t>(t.cols) * sizeof(float) <= kGemvLdsLimit ? 1u : 0u;
     const size_t lds = staged ? static_cast<size_t>(t.cols) * sizeof(float) : 0;
-    if (t.kind == kHvsq2)
-        hipLaunchKernelGGL(quantize_image_kernel<kHvsq2>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
+    if (t.kind != kHvsq2 && t.kind != kQ4_0) return hipErrorInvalidValue;
+    const uint32_t per = (t.cols + 1023) / 1024;   // elements per thread (staged rows: at most 16)
+    auto go = [&](auto kind_c, auto ept_c) {
+        constexpr int KD = decltype(kind_c)::value, EP = decltype(ept_c)::value;
+        hipLaunchKernelGGL((quantize_image_kernel<KD, EP>), dim3(batch), dim3(1024), lds, stream, x, t.cols,
+                           x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
                            mfma_image);
-    else if (t.kind == kQ4_0)
-        hipLaunchKernelGGL(quantize_image_kernel<kQ4_0>, dim3(batch), dim3(1024), lds, stream, x, t.cols, x_stride,
-                           t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
-                           mfma_image);
-    else
-        return hipErrorInvalidValue;
+    };
+    auto by_ept = [&](auto kind_c) {
+        if (!staged) go(kind_c, std::integral_constant<int, 0>{});
+        else if (per <= 1) go(kind_c, std::integral_constant<int, 1>{});
+        else if (per <= 2) go(kind_c, std::integral_constant<int, 2>{});
+        else if (per <= 4) go(kind_c, std::integral_constant<int, 4>{});
+        else if (per <= 8) go(kind_c, std::integral_constant<int, 8>{});
+        else go(kind_c, std::integral_constant<int, 16>{});
+    };
+    if (t.kind == kHvsq2) by_ept(std::integral_constant<int, kHvsq2>{});
+    else by_ept(std::integral_constant<int, kQ4_0>{});
     return hipGetLastError();
 }
 
