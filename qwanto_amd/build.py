@@ -19,7 +19,8 @@ LIBDIR = os.path.join(PKG, "lib")
 OBJDIR = os.path.join(PKG, "_build")
 LIB = os.path.join(LIBDIR, "libqwn_hip.so")
 LOADER_NAME = os.path.join(LIBDIR, "qwn_cuda.so")
-SOURCES = ["qwn_runtime.hip", "qwn_gemv.hip", "qwn_attention.hip", "qwn_decoder.hip", "qwn_noalloc.hip"]
+SOURCES = ["qwn_runtime.hip", "qwn_gemv.hip", "qwn_attention.hip", "qwn_decoder.hip", "qwn_noalloc.hip",
+           "qwn_head.hip"]
 ARCH = os.environ.get("QWN_HIP_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

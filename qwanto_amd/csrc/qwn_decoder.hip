@@ -182,6 +182,8 @@ struct Decoder {
     int32_t *vids = nullptr;        // [kTreeNodes] greedy id after each token
     uint64_t *row_keys = nullptr;   // [kPrefillTokens][rows_argmax_parts(vocab)] argmax workspace
     uint8_t *vimg = nullptr;        // [kPrefillTokens][vimg_stride] fp32 LM-head images
+    uint8_t *hpieces = nullptr;     // F16/BF16 head on the matrix cores: the block's activation pieces
+    float *hunscale = nullptr;      // [kPrefillTokens] their per-token unscale factors
     uint32_t vimg_stride = 0;
     // one graph per (block size, block kind: inner / ends the prompt / verify)
     hipGraphExec_t prefill_exec[kPrefillTokens + 1][3] = {};
@@ -412,8 +414,18 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (last) return enqueue_head(d, d->px + static_cast<size_t>(m - 1) * D, s);
     if (kind == kBlockVerify || tree) {
-        // the head on every token: fp32 images (F16/BF16) or per-token int8
+        // the head on every token: F16/BF16 rows on the matrix cores (the
+        // normed tokens as narrow pieces, the head read once for the block)
+        // where the pieces fit, else fp32 images (F16/BF16) or per-token int8
         // images of the normalized tokens (Q4_0/HyperVSQ-2), one batched GEMV
+        float *vl = d->vlogits + static_cast<size_t>(row0) * d->vocab;
+        if (d->hpieces) {
+            if ((e = launch_head_pieces(*d->head, d->px, D, d->final_norm, d->eps, m, d->hpieces, d->hunscale, s)) !=
+                    hipSuccess ||
+                (e = launch_mfma_head(*d->head, d->hpieces, d->hunscale, m, vl, d->vocab, s)) != hipSuccess)
+                return e;
+            return launch_rows_argmax(vl, m, d->vocab, d->vocab, d->vids + row0, d->state, d->row_keys, s);
+        }
         if (d->head->kind == kF16)
             e = launch_norm_image(*d->head, d->px, d->final_norm, d->eps, d->vimg, s, m, D, d->vimg_stride);
         else
@@ -712,6 +724,10 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         d->vimg_stride =
             static_cast<uint32_t>((image_bytes(d->head->kind, d->head->units) + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
+        if (mfma_head_supported(*d->head)) {
+            part(reinterpret_cast<void **>(&d->hpieces), head_pieces_bytes(*d->head));
+            part(reinterpret_cast<void **>(&d->hunscale), P * 4);
+        }
         part(reinterpret_cast<void **>(&d->vlogits), static_cast<size_t>(kTreeNodes) * d->vocab * 4);
         part(reinterpret_cast<void **>(&d->vids), kTreeNodes * 4);
         part(reinterpret_cast<void **>(&d->row_keys), P * rows_argmax_parts(d->vocab) * 8);

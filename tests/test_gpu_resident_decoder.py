@@ -305,18 +305,24 @@ def test_resident_decoder_qwen2_1p5b_golden(gpu_ctx, name):
     assert st.graph == 1
 
 
-@pytest.mark.parametrize("cfg,dtype,P,M", [(QWEN2_LIKE, "q4_0", 20, 16), (SMALL, "hvsq2", 5, 8),
-                                           (SMALL, "q4_0", 3, 4), (QWEN2_LIKE, "hvsq2", 1, 1),
-                                           (LONG_CTX, "q4_0", 30, 16)])
-def test_verify_block_matches_oracle_steps(gpu_ctx, oracle_lib, cfg, dtype, P, M):
+@pytest.mark.parametrize("cfg,dtype,P,M,embed,head", [
+    (QWEN2_LIKE, "q4_0", 20, 16, "f16", None), (SMALL, "hvsq2", 5, 8, "f16", None),
+    (SMALL, "q4_0", 3, 4, "f16", None), (QWEN2_LIKE, "hvsq2", 1, 1, "f16", None),
+    (LONG_CTX, "q4_0", 30, 16, "f16", None),
+    # untied heads: BF16 and F16 rows on the matrix cores, a Q4_0 head on the batched GEMV
+    (QWEN2_LIKE, "q4_0", 20, 16, "bf16", "bf16"), (SMALL, "hvsq2", 5, 11, "f16", "f16"),
+    (QWEN2_LIKE, "hvsq2", 3, 16, "bf16", "q4_0")])
+def test_verify_block_matches_oracle_steps(gpu_ctx, oracle_lib, cfg, dtype, P, M, embed, head):
     """qwn_hip_decoder_verify: M draft tokens after a P-token prompt as one
     block, logits for every token (the [nodes x vocab] a draft verifier
     scores, c/qwanto_jetspec.c:160-205), against the oracle stepping the
     same tokens one at a time; each token's greedy id is the first maximum
     of its logits.  Then truncate() to keep two of the drafts and step the
-    third token again: its logits agree with the verify block's."""
+    third token again: its logits agree with the verify block's.  F16/BF16
+    heads (tied or untied) run as matrix-core products of the head with the
+    tokens' narrow activation pieces (qwn_head.hip)."""
     rng = np.random.default_rng(900 + P + M)
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, embed_dtype=embed, lm_head=head))
     prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
     draft = synth.prompt_tokens(rng, cfg["vocab"], M)
     dec = abi.ResidentDecoder(gpu_ctx, model)
