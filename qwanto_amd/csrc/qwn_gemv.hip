@@ -153,14 +153,14 @@ __host__ __device__ constexpr int fused_sub_elems(int kind) { return kind == kHv
 // written instead of q8 (one sub-block is one 8- or 16-byte slot of that
 // image; HyperVSQ-2's block sums are reduced over the adjacent lanes
 // holding the block); tokens >= M of the image are left as they are (the GEMM neither
-// mixes token columns nor stores those tokens).  EPT > 0 (K <= 1024 EPT,
-// the row staged): thread t loads elements t + 1024 e of the input (and of
-// the norm weights or the SwiGLU up half) into registers in one batch of
-// loads before anything waits, and the two reductions meet at LDS-only
-// barriers; the sums and maxima are taken in the same order as the EPT = 0
-// loop, which re-reads the row from global memory.
-template <int KIND, int EPT>
-__global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
+// mixes token columns nor stores those tokens).  NT threads per token;
+// EPT > 0 (K <= NT EPT, the row staged): thread t loads elements t + NT e of
+// the input (and of the norm weights or the SwiGLU up half) into registers
+// in one batch of loads before anything waits, and the two reductions meet
+// at LDS-only barriers.  EPT = 0 (NT 1024): a strided loop that re-reads the
+// row from global memory.
+template <int KIND, int EPT, int NT>
+__global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restrict__ x, uint32_t K,
                                                               uint32_t x_stride, uint32_t units, uint8_t *image,
                                                               uint32_t image_stride, float *scales, int8_t *q8,
                                                               uint32_t q8_stride, uint32_t mode,
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
         float xv[EPT], yv[EPT];
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-            const uint32_t k = tid + 1024u * e, kk = k < K ? k : 0u;
+            const uint32_t k = tid + static_cast<uint32_t>(NT) * e, kk = k < K ? k : 0u;
             xv[e] = row[kk];
             yv[e] = ysrc[kk];
         }
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < EPT; ++e)
-                if (tid + 1024u * e < K) ss = fmaf(xv[e], xv[e], ss);
+                if (tid + static_cast<uint32_t>(NT) * e < K) ss = fmaf(xv[e], xv[e], ss);
             ss = wave_sum_all(ss);
             if (tid % kWaveSize == 0) wave_red[0][tid / kWaveSize] = ss;
             lds_barrier();
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(1024) void quantize_image_kernel(const float *__res
         }
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
-            const uint32_t k = tid + 1024u * e;
+            const uint32_t k = tid + static_cast<uint32_t>(NT) * e;
             if (k < K) {
                 const float xe = xv[e];
                 const float v = mode == kInNorm     ? (xe * inv_rms) * yv[e]
@@ -2454,12 +2454,21 @@ hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const floa
     const uint32_t staged = static_cast<size_t>(t.cols) * sizeof(float) <= kGemvLdsLimit ? 1u : 0u;
     const size_t lds = staged ? static_cast<size_t>(t.cols) * sizeof(float) : 0;
     if (t.kind != kHvsq2 && t.kind != kQ4_0) return hipErrorInvalidValue;
-    const uint32_t per = (t.cols + 1023) / 1024;   // elements per thread (staged rows: at most 16)
+    // rows up to 4096 wide: 256 threads (the two reductions' barriers
+    // synchronise four waves), else 1024
+    const bool narrow = staged && t.cols <= 4096;
+    const uint32_t nt = narrow ? 256u : 1024u;
+    const uint32_t per = (t.cols + nt - 1) / nt;   // elements per thread (staged rows: at most 16)
     auto go = [&](auto kind_c, auto ept_c) {
         constexpr int KD = decltype(kind_c)::value, EP = decltype(ept_c)::value;
-        hipLaunchKernelGGL((quantize_image_kernel<KD, EP>), dim3(batch), dim3(1024), lds, stream, x, t.cols,
-                           x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps, staged,
-                           mfma_image);
+        if (narrow)
+            hipLaunchKernelGGL((quantize_image_kernel<KD, EP, 256>), dim3(batch), dim3(256), lds, stream, x, t.cols,
+                               x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps,
+                               staged, mfma_image);
+        else
+            hipLaunchKernelGGL((quantize_image_kernel<KD, EP, 1024>), dim3(batch), dim3(1024), lds, stream, x,
+                               t.cols, x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm,
+                               eps, staged, mfma_image);
     };
     auto by_ept = [&](auto kind_c) {
         if (!staged) go(kind_c, std::integral_constant<int, 0>{});
