@@ -420,6 +420,12 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
     const uint32_t row = rpos < c.max_tokens ? rpos : 0;
     const float *ct = cos_tab + static_cast<size_t>(row) * half;
     const float *st = sin_tab + static_cast<size_t>(row) * half;
+    // the value this thread quantizes first (group gi = wave of the quantize
+    // loop below), loaded with the rotation's inputs rather than after the
+    // barrier
+    const uint32_t gi0 = threadIdx.x / 64, ch0 = (gi0 - c.groups) * 64 + threadIdx.x % 64;
+    const bool v0 = gi0 >= c.groups && gi0 < 2 * c.groups && ch0 < c.channels;
+    const float vpre = v[v0 ? ch0 : 0];
     // per-head q/k RMSNorm ahead of the rotation (c/qwanto_decode.c:654-684,
     // 1652-1655): one wave per head for its 1/rms, applied as (x * inv) * w
     const bool qk = q_norm != nullptr;
@@ -432,7 +438,7 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
             ss = wave_sum_all(ss);
             if (lane == 0) inv_s[hh] = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
         }
-        __syncthreads();
+        lds_barrier();
     }
     for (uint32_t p = threadIdx.x; p < q_heads * half; p += blockDim.x) {
         const uint32_t h = p / half, i = p % half;
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
         kr[h * D + i] = fmaf(a, ct[i], -(b * st[i]));
         kr[h * D + i + half] = fmaf(a, st[i], b * ct[i]);
     }
-    __syncthreads();
+    lds_barrier();   // the rotated keys; the rotated queries go to memory, read by a later launch
     if (pos >= c.max_tokens) return;
     const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64, nwaves = blockDim.x / 64;
     for (uint32_t gi = wave; gi < 2 * c.groups; gi += nwaves) {
@@ -463,7 +469,7 @@ __global__ __launch_bounds__(1024) void rope_append_kernel(KvCache c, float *__r
         const uint32_t g = is_v ? gi - c.groups : gi;
         const uint32_t ch = g * 64 + lane;
         const bool valid = ch < c.channels;
-        const float x = valid ? (is_v ? v[ch] : kr[ch]) : 0.0f;
+        const float x = valid ? (is_v ? (gi == gi0 ? vpre : v[ch]) : kr[ch]) : 0.0f;
         float amax = (valid && isfinite(x)) ? fabsf(x) : 0.0f;
         for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
         const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
