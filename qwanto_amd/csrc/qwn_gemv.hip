@@ -454,9 +454,16 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
 __host__ __device__ constexpr int max_waves_for(int upl) { return upl <= 4 ? kGemvMaxWaves : kGemvWaves; }
 
 
-template <int KIND, int MT, int UPL, int FR>
+// PAIRED_TILES: the tensor is stored one unit per lane (lanes >= 2) and the
+// launch runs it two units per lane: a wave takes two adjacent tiles, half
+// the lanes per row (lane j of a row holds its units j and j + L/2) and
+// twice the rows, so each workgroup's prologue serves as many rows as on a
+// two-units-per-lane layout.  Fused one-token launches whose one-tile grid
+// would hold more workgroups than the chip has CUs use it.
+template <int KIND, int MT, int UPL, int FR, bool PAIRED_TILES = false>
 __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(GemvArgs a) {
     constexpr bool FUSED = FR != 0;
+    static_assert(!PAIRED_TILES || (UPL == 2 && MT == 1), "paired tiles: two units per lane, one token");
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red[2][kGemvMaxWaves];
     __shared__ uint64_t red_key[kGemvMaxWaves];
@@ -469,8 +476,8 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     const uint32_t W = blockDim.x / kWaveSize;
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-    const uint32_t L = a.lanes;
-    const uint32_t grp = lane >> a.lanes_log2;
+    const uint32_t L = PAIRED_TILES ? a.lanes >> 1 : a.lanes;  // lanes per row of this launch
+    const uint32_t grp = lane >> (PAIRED_TILES ? a.lanes_log2 - 1 : a.lanes_log2);
     const uint32_t j = lane & (L - 1);
 
     // Job of this workgroup.  Every job field is read unconditionally and
@@ -517,9 +524,10 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
                                 : job == 2 ? a.output_stride[2]
                                            : a.output_stride[3];
     const uint32_t first = paired ? 0u : (job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3);
-    const uint32_t tile = paired ? blockIdx.x * half_w + wave % half_w : (blockIdx.x - first) * W + wave;
+    const uint32_t tile = (PAIRED_TILES ? 2 : 1) *
+                          (paired ? blockIdx.x * half_w + wave % half_w : (blockIdx.x - first) * W + wave);
     const uint32_t row = tile * a.rows_per_wave + grp;
-    const bool active = grp < a.rows_per_wave && row < rows;
+    const bool active = grp < (PAIRED_TILES ? 2 : 1) * a.rows_per_wave && row < rows;
     const bool writer = active && j == L - 1;
     constexpr bool fused = FUSED && MT == 1;
 
@@ -559,29 +567,51 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     // 1. Every weight load of this lane, metadata before codes.  Lanes
     //    without a unit load from the tile start instead of branching, so
     //    the loads stay one unconditional burst.
-    const uint8_t *tile_p = payload + tile * a.tile_payload_bytes;
-    const uint8_t *tile_m = meta + tile * a.tile_meta_bytes;
-    // Unit slot i holds units i*L + j, n = min(L, units - i*L) of them,
-    // stored compactly (qwn_internal.h).
     const size_t R = a.rows_per_wave;
     uint2 met[UPL];
     uint4 pay[UPL][CH];
+    if constexpr (PAIRED_TILES) {
+        // row grp of the pair: tile tile + grp / R, row grp % R; the tile's
+        // one slot holds all n = units units of a row
+        const uint32_t n = a.units, g = grp & (a.rows_per_wave - 1);
+        const bool second = grp >= a.rows_per_wave;
+        const uint8_t *tile_p = payload + tile * a.tile_payload_bytes + (second ? a.tile_payload_bytes : 0);
+        const uint8_t *tile_m = meta + tile * a.tile_meta_bytes + (second ? a.tile_meta_bytes : 0);
 #pragma unroll
-    for (int i = 0; i < UPL; ++i) {
-        const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
-        const bool ok = active && j < n;
-        if (KIND != kF16)
-            met[i] = *reinterpret_cast<const uint2 *>(
-                ok ? tile_m + 8 * R * L * i + (grp * n + j) * 8 : tile_m);
-    }
+        for (int i = 0; i < UPL; ++i) {
+            const uint32_t u = j + i * L;
+            met[i] = *reinterpret_cast<const uint2 *>(active && u < n ? tile_m + (g * n + u) * 8 : tile_m);
+        }
 #pragma unroll
-    for (int i = 0; i < UPL; ++i) {
-        const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
-        const bool ok = active && j < n;
-        const uint8_t *base = tile_p + 64 * R * L * i + (grp * n + j) * 16;
+        for (int i = 0; i < UPL; ++i) {
+            const uint32_t u = j + i * L;
+            const uint8_t *base = tile_p + (g * n + u) * 16;
 #pragma unroll
-        for (int q = 0; q < CH; ++q)
-            pay[i][q] = *reinterpret_cast<const uint4 *>(ok ? base + q * R * n * 16 : tile_p);
+            for (int q = 0; q < CH; ++q)
+                pay[i][q] = *reinterpret_cast<const uint4 *>(active && u < n ? base + q * R * n * 16 : tile_p);
+        }
+    } else {
+        const uint8_t *tile_p = payload + tile * a.tile_payload_bytes;
+        const uint8_t *tile_m = meta + tile * a.tile_meta_bytes;
+        // Unit slot i holds units i*L + j, n = min(L, units - i*L) of them,
+        // stored compactly (qwn_internal.h).
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
+            const bool ok = active && j < n;
+            if (KIND != kF16)
+                met[i] = *reinterpret_cast<const uint2 *>(
+                    ok ? tile_m + 8 * R * L * i + (grp * n + j) * 8 : tile_m);
+        }
+#pragma unroll
+        for (int i = 0; i < UPL; ++i) {
+            const uint32_t n = min(L, a.units > i * L ? a.units - i * L : 0u);
+            const bool ok = active && j < n;
+            const uint8_t *base = tile_p + 64 * R * L * i + (grp * n + j) * 16;
+#pragma unroll
+            for (int q = 0; q < CH; ++q)
+                pay[i][q] = *reinterpret_cast<const uint4 *>(ok ? base + q * R * n * 16 : tile_p);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -706,13 +736,21 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
     // 3. Dot products.
     const uint32_t ib = a.image_bytes;
     const uint32_t act_bytes = a.units * unit_lds_bytes(KIND);
-    float acc[MT];
+    // Paired tiles keep one sum per unit slot: the row total is then the
+    // upper half's lane sum plus the lower half's, the order the one-unit
+    // launch's lane reduction adds them in, so both launches of a tensor
+    // round alike.
+    constexpr int NS = PAIRED_TILES ? UPL : 1;
+    float accs[NS][MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) accs[i][t] = 0.0f;
 #pragma unroll
     for (int i = 0; i < UPL; ++i) {
         const uint32_t u = j + i * L;
         if (!(active && u < a.units)) continue;
+        float(&acc)[MT] = accs[PAIRED_TILES ? i : 0];
         if (KIND == kHvsq2) {
             const uint32_t *cw = reinterpret_cast<const uint32_t *>(pay[i]);
             const float d = half_to_float(met[i].x & 0xffffu);
@@ -789,8 +827,12 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
 
     // 4. Combine the L partials of each row with DPP; the group's last lane
     //    holds the row total and writes it.
+    float acc[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = group_sum(acc[t], L);
+    for (int t = 0; t < MT; ++t) {
+        acc[t] = group_sum(accs[0][t], L);
+        if constexpr (PAIRED_TILES) acc[t] = group_sum(accs[1][t], L) + acc[t];
+    }
     float first_out = 0.0f;
     if (paired) {
         // up rows -> LDS; the gate lane of the same row forms the SwiGLU
@@ -2185,60 +2227,70 @@ __global__ void repack_kernel(RepackArgs r) {
     }
 }
 
+template <int KIND, int UPL, bool PT>
+hipError_t launch_fused(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, hipStream_t stream) {
+    // as few sub-blocks per thread as the workgroup allows
+    const uint32_t nsub = args.units * unit_elems(KIND) / fused_sub_elems(KIND);
+    const uint32_t per_thread = (nsub + threads - 1) / threads;
+    if (per_thread <= 1)
+        hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 1, PT>), dim3(grid), dim3(threads), lds, stream, args);
+    else if (per_thread <= 2)
+        hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 2, PT>), dim3(grid), dim3(threads), lds, stream, args);
+    else if constexpr (fused_sub_elems(KIND) == 8) {
+        if (per_thread <= 3)
+            hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 3, PT>), dim3(grid), dim3(threads), lds, stream, args);
+        else
+            hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 4, PT>), dim3(grid), dim3(threads), lds, stream, args);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int KIND, int MT, int UPL>
-hipError_t launch_one(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, hipStream_t stream) {
+hipError_t launch_one(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int tpw,
+                      hipStream_t stream) {
     if constexpr (MT == 1) {
         if (args.input_mode != kInImage) {
-            // as few sub-blocks per thread as the workgroup allows
-            const uint32_t nsub = args.units * unit_elems(KIND) / fused_sub_elems(KIND);
-            const uint32_t per_thread = (nsub + threads - 1) / threads;
-            if (per_thread <= 1)
-                hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 1>), dim3(grid), dim3(threads), lds, stream, args);
-            else if (per_thread <= 2)
-                hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 2>), dim3(grid), dim3(threads), lds, stream, args);
-            else if constexpr (fused_sub_elems(KIND) == 8) {
-                if (per_thread <= 3)
-                    hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 3>), dim3(grid), dim3(threads), lds, stream, args);
-                else
-                    hipLaunchKernelGGL((gemv_kernel<KIND, 1, UPL, 4>), dim3(grid), dim3(threads), lds, stream,
-                                       args);
-            } else {
-                return hipErrorInvalidValue;
-            }
-            return hipGetLastError();
+            // two tiles per wave: the one-unit layout run two units per lane
+            if constexpr (UPL == 1 && KIND != kF16)
+                if (tpw == 2) return launch_fused<KIND, 2, true>(grid, threads, lds, args, stream);
+            if (tpw != 1) return hipErrorInvalidValue;
+            return launch_fused<KIND, UPL, false>(grid, threads, lds, args, stream);
         }
     }
+    if (tpw != 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemv_kernel<KIND, MT, UPL, 0>), dim3(grid), dim3(threads), lds, stream, args);
     return hipGetLastError();
 }
 
 template <int KIND, int MT>
-hipError_t dispatch_upl(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int upl,
+hipError_t dispatch_upl(uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int upl, int tpw,
                         hipStream_t stream) {
     switch (upl) {
-    case 1: return launch_one<KIND, MT, 1>(grid, threads, lds, args, stream);
-    case 2: return launch_one<KIND, MT, 2>(grid, threads, lds, args, stream);
-    case 3: return launch_one<KIND, MT, 3>(grid, threads, lds, args, stream);
-    case 4: return launch_one<KIND, MT, 4>(grid, threads, lds, args, stream);
-    case 5: return launch_one<KIND, MT, 5>(grid, threads, lds, args, stream);
-    case 6: return launch_one<KIND, MT, 6>(grid, threads, lds, args, stream);
-    case 8: return launch_one<KIND, MT, 8>(grid, threads, lds, args, stream);
-    case 10: return launch_one<KIND, MT, 10>(grid, threads, lds, args, stream);
-    case 12: return launch_one<KIND, MT, 12>(grid, threads, lds, args, stream);
-    case 16: return launch_one<KIND, MT, 16>(grid, threads, lds, args, stream);
+    case 1: return launch_one<KIND, MT, 1>(grid, threads, lds, args, tpw, stream);
+    case 2: return launch_one<KIND, MT, 2>(grid, threads, lds, args, tpw, stream);
+    case 3: return launch_one<KIND, MT, 3>(grid, threads, lds, args, tpw, stream);
+    case 4: return launch_one<KIND, MT, 4>(grid, threads, lds, args, tpw, stream);
+    case 5: return launch_one<KIND, MT, 5>(grid, threads, lds, args, tpw, stream);
+    case 6: return launch_one<KIND, MT, 6>(grid, threads, lds, args, tpw, stream);
+    case 8: return launch_one<KIND, MT, 8>(grid, threads, lds, args, tpw, stream);
+    case 10: return launch_one<KIND, MT, 10>(grid, threads, lds, args, tpw, stream);
+    case 12: return launch_one<KIND, MT, 12>(grid, threads, lds, args, tpw, stream);
+    case 16: return launch_one<KIND, MT, 16>(grid, threads, lds, args, tpw, stream);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <int KIND>
 hipError_t dispatch_mt(int mt, uint32_t grid, uint32_t threads, size_t lds, const GemvArgs &args, int upl,
-                       hipStream_t stream) {
+                       hipStream_t stream, int tpw = 1) {
     switch (mt) {
-    case 1: return dispatch_upl<KIND, 1>(grid, threads, lds, args, upl, stream);
-    case 2: return dispatch_upl<KIND, 2>(grid, threads, lds, args, upl, stream);
-    case 4: return dispatch_upl<KIND, 4>(grid, threads, lds, args, upl, stream);
-    case 8: return dispatch_upl<KIND, 8>(grid, threads, lds, args, upl, stream);
-    case 16: return dispatch_upl<KIND, 16>(grid, threads, lds, args, upl, stream);
+    case 1: return dispatch_upl<KIND, 1>(grid, threads, lds, args, upl, tpw, stream);
+    case 2: return dispatch_upl<KIND, 2>(grid, threads, lds, args, upl, tpw, stream);
+    case 4: return dispatch_upl<KIND, 4>(grid, threads, lds, args, upl, tpw, stream);
+    case 8: return dispatch_upl<KIND, 8>(grid, threads, lds, args, upl, tpw, stream);
+    case 16: return dispatch_upl<KIND, 16>(grid, threads, lds, args, upl, tpw, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -2343,26 +2395,27 @@ bool layout_tensor_with(DeviceTensor &t, uint32_t lanes, uint32_t upl) {
     return true;
 }
 
-// Lane plan: L lanes per row (a power of two, at most 64) holding about two
-// units each once a row has 8 or more (F16 rows, the LM head: about four):
-// half the waves of one unit per lane for the same bytes in flight, so a
-// decode-size GEMV fits in one residency round of the chip and more rows
-// share each workgroup's activation image; shorter rows take one unit per
-// lane.  Idle lanes cost VALU slots but no memory traffic (compact tiles).
-// Narrow quantized tensors (at most 2048 columns, fewer than 4x as many rows:
-// the attention projections of a small model) take one unit per lane too: a
-// wave's dot products are one serial chain of about 160 VALU instructions per
-// HyperVSQ-2 unit (60 per Q4_0 unit) that no other wave shares its SIMD
-// with at these grid sizes, so halving it shortens the launch (Qwen2-1.5B
-// Q4_0 q/k/v 2.96 -> 2.70 us, o 2.92 -> 2.65 from images, 4.09 -> 3.65 and
-// 3.69 -> 3.44 with the fused prologue); the FFN rows keep two (there the
-// doubled grid repeats the fused prologue in twice the workgroups: gate+up
-// 7.12 -> 8.24 us).  q, k and v share the columns and have at most the
-// hidden size of rows, so a grouped launch's tensors always agree.
+// Lane plan: L lanes per row (a power of two, at most 64), one unit per
+// lane for the quantized kinds, two for the FFN's expanding projections
+// (gate and up: rows >= 3x columns, 8 units or more), about four for F16
+// rows (the LM head).  A wave's dot products are one serial chain of about
+// 160 VALU instructions per HyperVSQ-2 unit (60 per Q4_0 unit) that at
+// decode grid sizes no other wave shares its SIMD with, so one unit per lane
+// halves the chain of two: launches from a prebuilt image gain (Qwen3-4B
+// HyperVSQ-2 q/k/v 3.54 -> 3.48 us, o 3.37 -> 3.14, down 4.59 -> 4.13).
+// Fused one-token launches whose one-unit grid would exceed a workgroup per
+// CU run such a tensor two units per lane over two tiles (paired tiles:
+// q/k/v 4.81 -> 4.79 us, o at one unit 4.28 -> 3.99; down 6.81 -> 7.19, its
+// row segments no longer line up with the cache lines).  Gate and up keep
+// two units per lane: their paired-tile launches lost 0.12 (Qwen3-4B) and
+// 0.38 us (Qwen2-1.5B) against the compact two-unit tiles.  Idle lanes cost
+// VALU slots but no memory traffic (compact tiles).  q, k and v share the
+// columns and have fewer rows than 3x the columns, so a grouped launch's
+// tensors agree.
 bool layout_tensor(DeviceTensor &t) {
     if (!set_units(t)) return false;
-    const bool narrow = t.kind != kF16 && t.cols <= 2048 && t.rows < 4 * t.cols;
-    const uint32_t per_lane = t.kind == kF16 ? 4 : (t.units >= 8 && !narrow ? 2 : 1);
+    const bool expanding = t.rows >= 3 * t.cols;
+    const uint32_t per_lane = t.kind == kF16 ? 4 : (t.units >= 8 && expanding ? 2 : 1);
     const uint32_t target = (t.units + per_lane - 1) / per_lane;
     uint32_t L = 1;
     while (L < target && L < static_cast<uint32_t>(kWaveSize)) L *= 2;
@@ -2515,12 +2568,31 @@ hipError_t launch_gemv(const GemvLaunch &g, hipStream_t stream) {
 
 namespace {
 
+// Tiles per wave: 2 (paired tiles) for a one-token fused launch on a
+// one-unit-per-lane layout whose one-tile-per-wave grid would hold more
+// workgroups than the chip has CUs (each workgroup repeats the
+// RMSNorm/quantize prologue, so the extra workgroups cost more than the
+// shorter dot chain saves: Qwen3-4B q/k/v 5.24 us at one tile per wave,
+// 4.79 paired), else 1.
+int choose_tpw(const GemvGroupLaunch &g, uint32_t total_tiles) {
+    const DeviceTensor &t = *g.tensors[0];
+    if (g.waves || g.input_mode == kInImage || g.batch != 1 || t.upl != 1 || t.lanes < 2 || t.kind == kF16)
+        return 1;
+    const int wmax = max_waves_for(1);
+    const uint32_t nsub = t.units * unit_elems(t.kind) / fused_sub_elems(t.kind);
+    int w = kGemvWaves;
+    while (static_cast<uint32_t>(w) * kWaveSize < nsub && w < wmax) w *= 2;
+    while (w < wmax && total_tiles / (2 * w) >= 512) w *= 2;
+    return total_tiles / static_cast<uint32_t>(w) > kChipCus ? 2 : 1;
+}
+
 // Workgroup width: the fused prologue needs a thread per 32-block of the
 // input (and runs shortest with a thread per sub-block); otherwise wider
 // workgroups only when the grid stays >= 2 per CU.
 int choose_waves(const GemvGroupLaunch &g, uint32_t total_tiles) {
     const DeviceTensor &t = *g.tensors[0];
     if (g.waves) return g.waves;
+    total_tiles /= static_cast<uint32_t>(choose_tpw(g, total_tiles));
     const int wmax = max_waves_for(static_cast<int>(t.upl));
     const uint32_t nsub = t.units * unit_elems(t.kind) / fused_sub_elems(t.kind);
     int w = kGemvWaves;
@@ -2567,7 +2639,7 @@ uint32_t gemv_group_grid(const GemvGroupLaunch &g) {
     uint32_t tiles = 0;
     for (int i = 0; i < g.njobs; ++i) tiles += g.tensors[i]->tiles;
     const int w = choose_waves(g, tiles);
-    return tiles / w;  // paired jobs: tiles of one job / (w / 2), the same
+    return tiles / (w * choose_tpw(g, tiles));  // paired jobs: tiles of one job / (w / 2), the same
 }
 
 hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
@@ -2577,12 +2649,13 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
     uint32_t tiles = 0;
     for (int i = 0; i < g.njobs; ++i) tiles += g.tensors[i]->tiles;
     const int w = choose_waves(g, tiles);
-    if ((w != 4 && w != 8) || w > max_waves_for(static_cast<int>(t.upl))) return hipErrorInvalidValue;
+    const int tpw = choose_tpw(g, tiles);
+    if ((w != 4 && w != 8) || w > max_waves_for(static_cast<int>(t.upl) * tpw)) return hipErrorInvalidValue;
     args.njobs = static_cast<uint32_t>(g.njobs);
     uint32_t blk = 0;
     for (int i = 0; i < g.njobs; ++i) {
         const DeviceTensor &ti = *g.tensors[i];
-        if (ti.tiles % w) return hipErrorInvalidValue;
+        if (ti.tiles % (w * tpw)) return hipErrorInvalidValue;
         args.payload[i] = ti.payload;
         args.meta[i] = ti.meta;
         args.output[i] = g.outputs[i];
@@ -2590,7 +2663,7 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         args.output_stride[i] = g.output_stride[i] ? g.output_stride[i] : ti.rows;
         args.bias[i] = g.bias[i];
         args.job_block[i] = blk;
-        blk += ti.tiles / w;
+        blk += ti.tiles / (w * tpw);
     }
     for (int i = g.njobs; i <= kMaxGroup; ++i) args.job_block[i] = blk;
     const uint32_t grid = blk;
@@ -2607,9 +2680,9 @@ hipError_t launch_gemv_group(const GemvGroupLaunch &g, hipStream_t stream) {
         args.ntok = 1;
         const size_t lds = image_bytes(t.kind, t.units);
         if (lds > kGemvLdsLimit) return hipErrorInvalidValue;
-        if (t.kind == kHvsq2) return dispatch_mt<kHvsq2>(1, grid, threads, lds, args, t.upl, stream);
-        if (t.kind == kQ4_0) return dispatch_mt<kQ4_0>(1, grid, threads, lds, args, t.upl, stream);
-        return dispatch_mt<kF16>(1, grid, threads, lds, args, t.upl, stream);
+        if (t.kind == kHvsq2) return dispatch_mt<kHvsq2>(1, grid, threads, lds, args, t.upl, stream, tpw);
+        if (t.kind == kQ4_0) return dispatch_mt<kQ4_0>(1, grid, threads, lds, args, t.upl, stream, tpw);
+        return dispatch_mt<kF16>(1, grid, threads, lds, args, t.upl, stream, tpw);
     }
     const GemvPlan p = plan_gemv(t, static_cast<int>(g.batch));
     if (p.tokens == 0 || p.lds_bytes > kGemvLdsLimit) return hipErrorInvalidValue;

@@ -43,6 +43,7 @@ constexpr int kGemvThreads = kWaveSize * kGemvWaves;
 constexpr int kGemvMaxWaves = 8;                  // waves per workgroup (largest launch)
 constexpr int kGemvMaxThreads = kWaveSize * kGemvMaxWaves;
 constexpr int kTilePad = 16;                      // tiles are stored in multiples of this
+constexpr uint32_t kChipCus = 256;                // compute units of one MI355X
 constexpr int kMaxTokensPerLaunch = 16;
 constexpr size_t kGemvLdsLimit = 64 * 1024;
 constexpr int kMaxGroup = 4;                      // tensors sharing one input in one launch
