@@ -72,6 +72,11 @@ GROUPS = [
     ("q4_0", [(1536, 8960)]),                                # down
     ("hvsq2", [(77, 512), (3, 512), (130, 512), (64, 512)]), # four ragged jobs
     ("q4_0", [(5, 96)]),                                     # K not a multiple of 128
+    # paired tiles (a one-unit-per-lane layout run two units per lane over
+    # two tiles, for grids beyond one workgroup per CU), ragged row counts:
+    ("hvsq2", [(40001, 512)]),                               # one lane per row of the pair
+    ("q4_0", [(5001, 4096)]),                                # 16 lanes per row
+    ("hvsq2", [(12001, 1536)]),                              # second unit slot partly empty
 ]
 
 
@@ -173,7 +178,8 @@ def test_swiglu_input(gpu_ctx, oracle_lib, kind, N, K):
         gpu_ctx.release(h)
 
 
-@pytest.mark.parametrize("kind,N,K", [("hvsq2", 9728, 2560), ("q4_0", 8960, 1536), ("q4_0", 70, 512)])
+@pytest.mark.parametrize("kind,N,K", [("hvsq2", 9728, 2560), ("q4_0", 8960, 1536), ("q4_0", 70, 512),
+                                     ("hvsq2", 12001, 1536)])
 def test_swiglu_output_pairs_gate_and_up(gpu_ctx, oracle_lib, kind, N, K):
     """Gate and up in one launch, SwiGLU in the epilogue: outputs[0] =
     silu(g) * u of the two GEMV outputs (exp within an ulp of numpy's)."""
@@ -195,7 +201,7 @@ def test_swiglu_output_pairs_gate_and_up(gpu_ctx, oracle_lib, kind, N, K):
         gpu_ctx.release(hu)
 
 
-@pytest.mark.parametrize("kind,N,K", [("hvsq2", 2560, 4096), ("q4_0", 1536, 1536)])
+@pytest.mark.parametrize("kind,N,K", [("hvsq2", 2560, 4096), ("q4_0", 1536, 1536), ("q4_0", 5001, 4096)])
 def test_residual_add_output(gpu_ctx, oracle_lib, kind, N, K):
     rng = np.random.default_rng(N + 5 * K)
     w = synth.weights(kind, rng, N, K)
@@ -250,6 +256,46 @@ def test_f16_lm_head_argmax(gpu_ctx, oracle_lib, N, K, case):
         ref = oracle_lib.matmul_f16(w, oracle_lib.rmsnorm(x, np.ones(K, np.float32), 1e-6))[0]
         ok, worst = gemv_close(y, ref, rtol=2e-4)
         assert ok, f"worst {worst:.3g} of tolerance"
+    finally:
+        gpu_ctx.release(h)
+
+
+@pytest.mark.parametrize("kind,N,K", [("q4_0", 40001, 512), ("hvsq2", 40001, 512)])
+def test_quantized_head_argmax_paired_tiles(gpu_ctx, oracle_lib, kind, N, K):
+    """A quantized LM head (an untied Q4_0 / HyperVSQ-2 head) with the argmax
+    epilogue on paired tiles: the logits equal the int8 path's bit for bit
+    and the reduced index is their first maximum, with the best row copied
+    to earlier rows in both tiles of other pairs."""
+    import torch
+    rng = np.random.default_rng(N + 3 * K)
+    w = synth.weights(kind, rng, N, K).reshape(N, -1)
+    x = rng.standard_normal(K).astype(np.float32)
+    h = gpu_ctx.upload(w.reshape(-1), kind, N, K)
+    try:
+        y0, _ = abi_gemv(gpu_ctx, h, oracle_lib, x, N, K)
+    finally:
+        gpu_ctx.release(h)
+    best = int(np.argmax(y0))
+    for r in (best // 3, best // 2 + 1, N - 1):   # rows of other tiles and pairs
+        w[r] = w[best]
+    h = gpu_ctx.upload(w.reshape(-1), kind, N, K)
+    try:
+        xd = dev(x)
+        probe, _ = gpu_ctx.gemv_group_request([h], [16], "f32", "argmax", x_ptr=xd.data_ptr(), partials_ptr=16)
+        n = gpu_ctx.gemv_group_partials(probe)
+        assert n > 0
+        parts = torch.zeros(n, dtype=torch.int64, device="cuda:0")
+        idx = torch.full((1,), -1, dtype=torch.int32, device="cuda:0")
+        logits = zeros(N)
+        req, keep = gpu_ctx.gemv_group_request([h], [logits.data_ptr()], "f32", "argmax", x_ptr=xd.data_ptr(),
+                                               partials_ptr=parts.data_ptr())
+        gpu_ctx.gemv_group_device(req, stream=stream())
+        gpu_ctx.argmax_device(parts.data_ptr(), n, idx.data_ptr(), stream=stream())
+        sync()
+        y = logits.cpu().numpy()
+        y_abi, _ = abi_gemv(gpu_ctx, h, oracle_lib, x, N, K)
+        assert np.array_equal(y, y_abi), "argmax-epilogue logits differ from the int8 path"
+        assert int(idx.cpu().numpy()[0]) == int(np.argmax(y)) == best // 3
     finally:
         gpu_ctx.release(h)
 
