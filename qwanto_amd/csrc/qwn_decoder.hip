@@ -35,9 +35,10 @@ namespace qwn {
 namespace {
 
 constexpr int kProj = 7;
-constexpr uint32_t kPrefillTokens = 16;  // prompt tokens per prefill block (the GEMV's widest launch)
+constexpr uint32_t kPrefillTokens = 16;  // tokens of a chain verify block (the GEMV's widest launch)
+constexpr uint32_t kBlockTokens = 64;    // tokens of a prompt / draft-tree block (MFMA GEMMs of 16-token groups)
 constexpr uint32_t kTreeNodes = 64;      // draft-tree nodes per verify (c/qwanto_jetspec.h:17)
-constexpr uint32_t kTreeBlocks = kTreeNodes / kPrefillTokens;
+constexpr uint32_t kTreeBlocks = kTreeNodes / kPrefillTokens;  // blocks of the narrowest block size
 enum { P_Q, P_K, P_V, P_O, P_GATE, P_UP, P_DOWN };
 
 // x = embedding row of the step's token (feed[pos] when the host supplied
@@ -166,9 +167,9 @@ struct Decoder {
     std::vector<KvCache> caches;
     hipGraphExec_t exec = nullptr;
     bool graph_tried = false;
-    // prefill: blocks of up to kPrefillTokens prompt tokens through the
-    // batched GEMV ([token][...] buffers), one graph per (block size, ends
-    // the prompt)
+    // prefill: blocks of up to block_tokens prompt tokens (kBlockTokens on
+    // the MFMA path, else kPrefillTokens) through the GEMMs ([token][...]
+    // buffers), one graph per (block size, ends the prompt)
     float *px = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *pattn = nullptr, *pgate = nullptr,
           *pup = nullptr, *pscales = nullptr;
     uint8_t *pimg = nullptr;
@@ -180,23 +181,24 @@ struct Decoder {
     // verify blocks: the LM head on every token of the block
     float *vlogits = nullptr;       // [kTreeNodes][vocab]
     int32_t *vids = nullptr;        // [kTreeNodes] greedy id after each token
-    uint64_t *row_keys = nullptr;   // [kPrefillTokens][rows_argmax_parts(vocab)] argmax workspace
-    uint8_t *vimg = nullptr;        // [kPrefillTokens][vimg_stride] fp32 LM-head images
+    uint64_t *row_keys = nullptr;   // [kBlockTokens][rows_argmax_parts(vocab)] argmax workspace
+    uint8_t *vimg = nullptr;        // [kBlockTokens][vimg_stride] fp32 LM-head images
     uint8_t *hpieces = nullptr;     // F16/BF16 head on the matrix cores: the block's activation pieces
-    float *hunscale = nullptr;      // [kPrefillTokens] their per-token unscale factors
+    float *hunscale = nullptr;      // [kBlockTokens] their per-token unscale factors
     uint32_t vimg_stride = 0;
     // one graph per (block size, block kind: inner / ends the prompt / verify)
-    hipGraphExec_t prefill_exec[kPrefillTokens + 1][3] = {};
-    bool prefill_tried[kPrefillTokens + 1][3] = {};
+    uint32_t block_tokens = kPrefillTokens;
+    hipGraphExec_t prefill_exec[kBlockTokens + 1][3] = {};
+    bool prefill_tried[kBlockTokens + 1][3] = {};
     // draft trees: per node its ancestor-or-self mask and rotation position
     // (prefix length + depth), the prefix length, an accepted path; one
-    // graph per (16-node block of the tree, block size)
+    // graph per (block of the tree, block size)
     uint64_t *tree_mask = nullptr;  // [kTreeNodes]
     int32_t *tree_pos = nullptr;    // [kTreeNodes]
     int32_t *tree_base = nullptr;   // [1]
     int32_t *tree_path = nullptr;   // [kTreeNodes]
-    hipGraphExec_t tree_exec[kTreeBlocks][kPrefillTokens + 1] = {};
-    bool tree_tried[kTreeBlocks][kPrefillTokens + 1] = {};
+    hipGraphExec_t tree_exec[kTreeBlocks][kBlockTokens + 1] = {};
+    bool tree_tried[kTreeBlocks][kBlockTokens + 1] = {};
     uint32_t tree_nodes = 0;        // nodes of the verified tree awaiting commit (0: none)
     std::vector<int32_t> tree_parents, tree_tokens;
     uint32_t position = 0;
@@ -321,7 +323,7 @@ enum BlockKind : uint32_t { kBlockInner = 0, kBlockLast = 1, kBlockVerify = 2, k
 hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s, uint32_t block = 0) {
     const bool last = kind == kBlockLast;
     const bool tree = kind == kBlockTree;
-    const uint32_t row0 = tree ? block * kPrefillTokens : 0;
+    const uint32_t row0 = tree ? block * d->block_tokens : 0;
     hipError_t e;
     const EmbedArgs ea = embed_args(d);
     hipLaunchKernelGGL(prefill_embed_kernel, dim3((ea.units * 4 + 255) / 256, m), dim3(256), 0, s, ea, m, d->px,
@@ -420,10 +422,15 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
         // images of the normalized tokens (Q4_0/HyperVSQ-2), one batched GEMV
         float *vl = d->vlogits + static_cast<size_t>(row0) * d->vocab;
         if (d->hpieces) {
-            if ((e = launch_head_pieces(*d->head, d->px, D, d->final_norm, d->eps, m, d->hpieces, d->hunscale, s)) !=
-                    hipSuccess ||
-                (e = launch_mfma_head(*d->head, d->hpieces, d->hunscale, m, vl, d->vocab, s)) != hipSuccess)
-                return e;
+            // 16 tokens per head launch (the pieces image holds 16)
+            for (uint32_t t0 = 0; t0 < m; t0 += kPrefillTokens) {
+                const uint32_t mg = std::min(kPrefillTokens, m - t0);
+                if ((e = launch_head_pieces(*d->head, d->px + static_cast<size_t>(t0) * D, D, d->final_norm, d->eps,
+                                            mg, d->hpieces, d->hunscale + t0, s)) != hipSuccess ||
+                    (e = launch_mfma_head(*d->head, d->hpieces, d->hunscale + t0, mg,
+                                          vl + static_cast<size_t>(t0) * d->vocab, d->vocab, s)) != hipSuccess)
+                    return e;
+            }
             return launch_rows_argmax(vl, m, d->vocab, d->vocab, d->vids + row0, d->state, d->row_keys, s);
         }
         if (d->head->kind == kF16)
@@ -547,8 +554,8 @@ hipError_t run_captured(hipStream_t s, hipGraphExec_t *exec, bool *tried, F enqu
 // The prompt, already in feed at the device position, in prefill blocks.
 hipError_t run_prefill(Decoder *d, uint32_t count) {
     hipStream_t s = d->ctx->stream;
-    for (uint32_t i = 0; i < count; i += kPrefillTokens) {
-        const uint32_t m = std::min(kPrefillTokens, count - i);
+    for (uint32_t i = 0; i < count; i += d->block_tokens) {
+        const uint32_t m = std::min(d->block_tokens, count - i);
         const uint32_t kind = i + m == count ? kBlockLast : kBlockInner;
         const hipError_t e = run_captured(s, &d->prefill_exec[m][kind], &d->prefill_tried[m][kind],
                                           [&] { return enqueue_prefill(d, m, kind, s); });
@@ -565,12 +572,13 @@ hipError_t run_verify(Decoder *d, uint32_t m) {
 }
 
 // The nodes of a draft tree, already in feed at the device position (the
-// tree's base slot), in blocks of up to 16 nodes: a node's ancestors come
-// before it, so every block finds them in the cache.
+// tree's base slot), in blocks of up to block_tokens nodes (one block for a
+// tree of 64 on the MFMA path): a node's ancestors come before it, so every
+// block finds them in the cache.
 hipError_t run_tree(Decoder *d, uint32_t count) {
     hipStream_t s = d->ctx->stream;
-    for (uint32_t b = 0; b * kPrefillTokens < count; ++b) {
-        const uint32_t m = std::min(kPrefillTokens, count - b * kPrefillTokens);
+    for (uint32_t b = 0; b * d->block_tokens < count; ++b) {
+        const uint32_t m = std::min(d->block_tokens, count - b * d->block_tokens);
         const hipError_t e = run_captured(s, &d->tree_exec[b][m], &d->tree_tried[b][m],
                                           [&] { return enqueue_prefill(d, m, kBlockTree, s, b); });
         if (e != hipSuccess) return e;
@@ -703,7 +711,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
     part(reinterpret_cast<void **>(&d->out_tokens), static_cast<size_t>(d->max_ctx) * 4);
     // prefill blocks: [token][...] activations, images of the widest input
     {
-        const size_t P = kPrefillTokens;
+        const size_t P = kBlockTokens;
         part(reinterpret_cast<void **>(&d->px), P * D * 4);
         part(reinterpret_cast<void **>(&d->pq), P * Q * 4);
         part(reinterpret_cast<void **>(&d->pk), P * KV * 4);
@@ -716,11 +724,15 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
         size_t stride = 0;
         for (int p : {P_Q, P_O, P_DOWN}) stride = std::max(stride, image_bytes(kind, d->proj[p]->units));
         d->pimg_stride = static_cast<uint32_t>((stride + 15) & ~static_cast<size_t>(15));
-        part(reinterpret_cast<void **>(&d->pimg), P * d->pimg_stride);
-        if (kind == kHvsq2 || kind == kQ4_0)
+        // dot8 images: blocks of up to kPrefillTokens tokens take that path
+        part(reinterpret_cast<void **>(&d->pimg), kPrefillTokens * d->pimg_stride);
+        // MFMA images: one per 16-token group of a block
+        if (kind == kHvsq2 || kind == kQ4_0) {
             part(reinterpret_cast<void **>(&d->pmimg),
-                 std::max({mfma_image_bytes(*d->proj[P_DOWN]), mfma_image_bytes(*d->proj[P_Q]),
-                           mfma_image_bytes(*d->proj[P_O])}));
+                 (kBlockTokens / 16) * std::max({mfma_image_bytes(*d->proj[P_DOWN]), mfma_image_bytes(*d->proj[P_Q]),
+                                                 mfma_image_bytes(*d->proj[P_O])}));
+            d->block_tokens = kBlockTokens;
+        }
         d->vimg_stride =
             static_cast<uint32_t>((image_bytes(d->head->kind, d->head->units) + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
@@ -1010,7 +1022,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_prefill(QwnCudaContextHandle *handle, QwnHi
     if (e != hipSuccess) return hip_fail("decoder prefill", e);
     d->position += count;
     if (next_token) *next_token = st[0];
-    const uint64_t blocks = (count + kPrefillTokens - 1) / kPrefillTokens;
+    const uint64_t blocks = (count + d->block_tokens - 1) / d->block_tokens;
     ctx->telemetry.gpu_matmul_count += blocks * 4ull * d->layers + 1;
     return QWN_CUDA_STATUS_OK;
 }
@@ -1131,7 +1143,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_verify_tree(QwnCudaContextHandle *handle, Q
     d->tree_nodes = count;
     d->tree_parents.assign(parents, parents + count);
     d->tree_tokens.assign(tokens, tokens + count);
-    const uint64_t blocks = (count + kPrefillTokens - 1) / kPrefillTokens;
+    const uint64_t blocks = (count + d->block_tokens - 1) / d->block_tokens;
     ctx->telemetry.gpu_matmul_count += blocks * (4ull * d->layers + 1);
     return QWN_CUDA_STATUS_OK;
 }
@@ -1230,7 +1242,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_generate(QwnCudaContextHandle *handle, QwnH
         stats->decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
         stats->weight_bytes_per_step = d->weight_bytes;
         stats->graph = d->exec ? 1u : 0u;
-        stats->prefill_block_tokens = kPrefillTokens;
+        stats->prefill_block_tokens = d->block_tokens;
     }
     return QWN_CUDA_STATUS_OK;
 }

@@ -166,13 +166,16 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
                                                               uint32_t q8_stride, uint32_t mode,
                                                               const float *__restrict__ x2,
                                                               const float *__restrict__ norm, float eps,
-                                                              uint32_t staged, uint8_t *mimg) {
+                                                              uint32_t staged, uint8_t *mimg, size_t mimg_group) {
     extern __shared__ float vals[];  // [K] when staged
     __shared__ float wave_red[2][1024 / kWaveSize];
     constexpr uint32_t E = fused_sub_elems(KIND);
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t W = blockDim.x / kWaveSize;
     const float *row = x + static_cast<size_t>(t) * x_stride;
+    // the MFMA image of the token's 16-token group, its column tc there
+    const uint32_t tc = t % 16;
+    if (mimg) mimg += (t / 16) * mimg_group;
     float inv_rms = 1.0f;
     auto value = [&](uint32_t k) {
         const float v = row[k];
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
                                         ((w[1] << 8) & 0xff000000u);
                     const uint32_t hi = ((w[0] >> 8) & 0xffu) | ((w[0] >> 16) & 0xff00u) |
                                         ((w[1] << 8) & 0xff0000u) | (w[1] & 0xff000000u);
-                    *reinterpret_cast<uint2 *>(mimg + (static_cast<size_t>(sb) * 16 + t) * 8) = make_uint2(lo, hi);
+                    *reinterpret_cast<uint2 *>(mimg + (static_cast<size_t>(sb) * 16 + tc) * 8) = make_uint2(lo, hi);
                 }
             } else {
                 // elements 16 sb .. 16 sb + 15 are slice sl = sb % 4 of group
@@ -294,10 +297,10 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
                         o[k] = ((w[0] >> (8 * k)) & 0xffu) | (((w[1] >> (8 * k)) & 0xffu) << 8) |
                                (((w[2] >> (8 * k)) & 0xffu) << 16) | (((w[3] >> (8 * k)) & 0xffu) << 24);
                     const uint32_t slot = (sb & ~15u) | ((sb & 3u) << 2) | ((sb >> 2) & 3u);
-                    *reinterpret_cast<uint4 *>(mimg + (static_cast<size_t>(slot) * 16 + t) * 16) =
+                    *reinterpret_cast<uint4 *>(mimg + (static_cast<size_t>(slot) * 16 + tc) * 16) =
                         make_uint4(o[0], o[1], o[2], o[3]);
                     if ((sb & 15u) == 0)
-                        reinterpret_cast<float *>(mimg + static_cast<size_t>(units) * 4096)[(sb >> 4) * 16 + t] =
+                        reinterpret_cast<float *>(mimg + static_cast<size_t>(units) * 4096)[(sb >> 4) * 16 + tc] =
                             static_cast<float>(s);
                 }
             }
@@ -990,7 +993,8 @@ struct MfmaArgs {
     uint32_t ks_log2;      // waves per workgroup (log2)
     uint32_t nb;           // K blocks per wave
     uint32_t stage_bytes;  // LDS bytes of the staged weight region (STAGE)
-    const uint8_t *image;  // mfma image of up to 16 tokens
+    const uint8_t *image;  // mfma images of up to 64 tokens, one per 16-token group (blockIdx.y)
+    size_t group_image_bytes;
     const float *scales;   // [ntok]
     uint32_t ntok;
     uint32_t vec_out;      // bit i: job i's rows may be stored 4 at a time (16-byte aligned)
@@ -1007,6 +1011,23 @@ constexpr int kMfmaSplitMaxWaves = 16;  // the Q4_0 K-split kernel
 //   payload tile * tile_payload + 64*R*L*slot + (g*R*n + grp*n + jj) * 16
 //   meta    tile * tile_meta    +  8*R*L*slot + (grp*n + jj) * 8
 // with slot = unit / L, jj = unit % L, n = units in the slot.
+// The 16-token group of a launch over more tokens (blockIdx.y): its image
+// (groups of 16 tokens stored one after another), scales, token count and
+// first token.
+struct MfmaTok {
+    const uint8_t *image;
+    const float *scales;
+    uint32_t ntok, tok0;
+};
+__device__ __forceinline__ MfmaTok mfma_tok(const MfmaArgs &a) {
+    MfmaTok t;
+    t.tok0 = 16 * blockIdx.y;
+    t.image = a.image + blockIdx.y * a.group_image_bytes;
+    t.scales = a.scales + t.tok0;
+    t.ntok = min(16u, a.ntok - t.tok0);
+    return t;
+}
+
 struct MfmaUnit {
     size_t payload, meta;
 };
@@ -1028,11 +1049,11 @@ __device__ __forceinline__ MfmaUnit mfma_unit(const MfmaArgs &a, uint32_t row, u
 // are the MFMA's A operand here, so lane (g, m) holds rows 4g .. 4g+3 of
 // token m and takes those rows' d and m from the lanes that loaded them.
 template <int NB, int RT, bool DUMP>
-__device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
+__device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const MfmaTok &tk, const uint8_t *payload, const uint8_t *meta,
                                            uint32_t rows, uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
                                            float (&acc)[RT][4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
-    const float *sums = reinterpret_cast<const float *>(a.image + static_cast<size_t>(a.units) * 4096);
+    const float *sums = reinterpret_cast<const float *>(tk.image + static_cast<size_t>(a.units) * 4096);
     uint4 A[NB][RT];
     uint2 Mt[NB][RT];
     mfma_v4i B[NB][4];
@@ -1051,7 +1072,7 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const uint32_t b = b0 + (static_cast<uint32_t>(i) < nblk ? i : 0);
-        const uint8_t *ib = a.image + static_cast<size_t>(b) * 4096 + lane * 16;
+        const uint8_t *ib = tk.image + static_cast<size_t>(b) * 4096 + lane * 16;
 #pragma unroll
         for (int sl = 0; sl < 4; ++sl) B[i][sl] = *reinterpret_cast<const mfma_v4i *>(ib + sl * 1024);
         SA[i] = sums[b * 16 + m];
@@ -1089,7 +1110,7 @@ __device__ __forceinline__ void mfma_chunk(const MfmaArgs &a, const uint8_t *pay
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = r0 + 16 * t + 4 * g + r;
-                    if (row < rows && m < a.ntok)
+                    if (row < rows && m < tk.ntok)
                         a.dump[(static_cast<size_t>(m) * rows + row) * a.nblk + b0 + i] = ci[r];
                 }
             }
@@ -1128,7 +1149,7 @@ struct HvLane {
     uint32_t qf, ql, mf, ml, last_slot;
 };
 
-__device__ __forceinline__ HvLane hv_lane(const MfmaArgs &a, uint32_t lane) {
+__device__ __forceinline__ HvLane hv_lane(const MfmaArgs &a, const MfmaTok &tk, uint32_t lane) {
     const uint32_t L = 1u << a.lanes_log2, R = 1u << a.rows_per_wave_log2;
     const uint32_t g = lane >> 4, m = lane & 15;
     const uint32_t tl = m >> a.rows_per_wave_log2, grp = m & (R - 1);
@@ -1147,7 +1168,7 @@ __device__ __forceinline__ HvLane hv_lane(const MfmaArgs &a, uint32_t lane) {
 // The image operands of up to NB HyperVSQ-2 blocks from b0 (nv of them real,
 // the rest repeat b0): per block four 16-byte MFMA operands (tokens m, chunk
 // g of each slice) and the activation sums of tokens 4g .. 4g+3.  Bounded
-// buffer loads: the columns of tokens past a.ntok read as zero with no
+// buffer loads: the columns of tokens past tk.ntok read as zero with no
 // memory access (their products are never stored), so a 4-token batch moves
 // a quarter of the image.  Always 5 * NB loads, so a caller can wait for
 // older loads with vmcnt(5 * NB).
@@ -1158,13 +1179,13 @@ struct HvImage {
 };
 
 template <int NB>
-__device__ __forceinline__ void hv_image_loads(const MfmaArgs &a, uint32_t b0, uint32_t nv, uint32_t lane,
+__device__ __forceinline__ void hv_image_loads(const MfmaArgs &a, const MfmaTok &tk, uint32_t b0, uint32_t nv, uint32_t lane,
                                                HvImage<NB> &im) {
     const uint32_t bytes = a.units * static_cast<uint32_t>(mfma_image_block_bytes());
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.image), 0, static_cast<int>(bytes), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(tk.image), 0, static_cast<int>(bytes), 0x00020000);
     const uint32_t m = lane & 15, g = lane >> 4;
-    const uint32_t skip = m < a.ntok ? 0u : 0x80000000u, sskip = 4 * g < a.ntok ? 0u : 0x80000000u;
+    const uint32_t skip = m < tk.ntok ? 0u : 0x80000000u, sskip = 4 * g < tk.ntok ? 0u : 0x80000000u;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const uint32_t b = b0 + (static_cast<uint32_t>(i) < nv ? i : 0);
@@ -1185,7 +1206,7 @@ __device__ __forceinline__ void hv_image_loads(const MfmaArgs &a, uint32_t b0, u
 // row (no exchange between lanes).  `live`: row m exists (else its scales
 // count as 0).
 template <int NB, bool DUMP>
-__device__ __forceinline__ void mfma_chunk_hv(const MfmaArgs &a, const uint8_t *lds, uint32_t meta_lds,
+__device__ __forceinline__ void mfma_chunk_hv(const MfmaArgs &a, const MfmaTok &tk, const uint8_t *lds, uint32_t meta_lds,
                                               const HvLane &hl, uint32_t b0, uint32_t nv, bool live, uint32_t rows,
                                               uint32_t r0, uint32_t lane, const HvImage<NB> &im, float (&acc)[4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
@@ -1227,7 +1248,7 @@ __device__ __forceinline__ void mfma_chunk_hv(const MfmaArgs &a, const uint8_t *
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t row = r0 + m, tok = 4 * g + r;
-                if (row < rows && tok < a.ntok)
+                if (row < rows && tok < tk.ntok)
                     a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
             }
         }
@@ -1263,13 +1284,13 @@ __device__ __forceinline__ uint32_t q4_signed(uint32_t nibbles) {
 // The image words of up to NB Q4_0 blocks from b0 (each lane's 8 bytes of
 // a block: tokens m, elements 8g .. 8g+7); blocks past kb1 are not loaded.
 template <int NB>
-__device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, uint32_t b0, uint32_t kb1, uint32_t lane,
+__device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, const MfmaTok &tk, uint32_t b0, uint32_t kb1, uint32_t lane,
                                                uint2 (&B)[NB]) {
     if (b0 >= kb1) return;
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const uint32_t b = b0 + i < kb1 ? b0 + i : b0;
-        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+        B[i] = *reinterpret_cast<const uint2 *>(tk.image + static_cast<size_t>(b) * 512 + lane * 8);
     }
 }
 
@@ -1285,7 +1306,7 @@ __device__ __forceinline__ void q4_image_loads(const MfmaArgs &a, uint32_t b0, u
 // STAGE: the row group is in LDS in the row-major layout, `ppieces` and
 // `mpieces` its payload and meta strides.
 template <int NB, int RT, bool STAGE, bool DUMP>
-__device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *payload, const uint8_t *meta,
+__device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const MfmaTok &tk, const uint8_t *payload, const uint8_t *meta,
                                               const uint8_t *lds, uint32_t meta_lds, uint32_t rows,
                                               uint32_t r0, uint32_t b0, uint32_t nblk, uint32_t lane,
                                               uint32_t ppieces, uint32_t mpieces, const uint2 (&B)[NB],
@@ -1335,7 +1356,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = r0 + 16 * t + m, tok = 4 * g + r;
-                    if (row < rows && tok < a.ntok)
+                    if (row < rows && tok < tk.ntok)
                         a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
                 }
             }
@@ -1351,6 +1372,7 @@ __device__ __forceinline__ void mfma_chunk_q4(const MfmaArgs &a, const uint8_t *
 
 template <int KIND, int NB, int RT, bool STAGE, bool DUMP>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(MfmaArgs a) {
+    const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -1368,6 +1390,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
                             : job == 1 ? a.output_stride[1]
                             : job == 2 ? a.output_stride[2]
                                        : a.output_stride[3];
+    output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
     const uint32_t r0 = (blockIdx.x - first) * (16 * RT);
@@ -1380,14 +1403,14 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
     if constexpr (KIND == kQ4_0 || STAGE) {
         const uint32_t g = lane >> 4, m = lane & 15;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+        for (int r = 0; r < 4; ++r) xs_pre[r] = tk.scales[min(4 * g + r, tk.ntok - 1)];
         if (a.accumulate && ks == 0) {
 #pragma unroll
             for (int t = 0; t < RT; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t tok = 4 * g + r, row = r0 + 16 * t + m;
-                    res_pre[t][r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+                    res_pre[t][r] = tok < tk.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
                 }
         }
     }
@@ -1460,7 +1483,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             // the first chunk's image words go out behind the copies
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_sched_barrier(0);
-            q4_image_loads<NB>(a, kb0, kb1, lane, Bx);
+            q4_image_loads<NB>(a, tk, kb0, kb1, lane, Bx);
         } else {
             static_assert(RT == 1, "the staged HyperVSQ-2 group is 16 rows");
             const uint8_t *psrc = payload + static_cast<size_t>(t0) * a.tile_payload_bytes;
@@ -1480,7 +1503,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
             // the first chunk's image loads go out behind the copies
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_sched_barrier(0);
-            if (kb0 < kb1) hv_image_loads<NB>(a, kb0, min(static_cast<uint32_t>(NB), kb1 - kb0), lane, him);
+            if (kb0 < kb1) hv_image_loads<NB>(a, tk, kb0, min(static_cast<uint32_t>(NB), kb1 - kb0), lane, him);
         }
         // this wave's copies landed (all but its first image loads, which
         // retire after them)
@@ -1497,15 +1520,15 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
     if constexpr (KIND == kHvsq2 && STAGE) {
         const bool live = r0 + (lane & 15) < rows;
-        const HvLane hl = hv_lane(a, lane);
+        const HvLane hl = hv_lane(a, tk, lane);
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
             const uint32_t nv = min(static_cast<uint32_t>(NB), kb1 - b0);
-            if (b0 != kb0) hv_image_loads<NB>(a, b0, nv, lane, him);
-            mfma_chunk_hv<NB, DUMP>(a, smem, meta_lds, hl, b0, nv, live, rows, r0, lane, him, acc[0]);
+            if (b0 != kb0) hv_image_loads<NB>(a, tk, b0, nv, lane, him);
+            mfma_chunk_hv<NB, DUMP>(a, tk, smem, meta_lds, hl, b0, nv, live, rows, r0, lane, him, acc[0]);
         }
     } else if constexpr (KIND == kHvsq2) {
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB)
-            mfma_chunk<NB, RT, DUMP>(a, payload, meta, rows, r0, b0, min(static_cast<uint32_t>(NB), kb1 - b0), lane,
+            mfma_chunk<NB, RT, DUMP>(a, tk, payload, meta, rows, r0, b0, min(static_cast<uint32_t>(NB), kb1 - b0), lane,
                                      acc);
     } else if constexpr (STAGE) {
         // the weights are in LDS: each chunk's image words are loaded one
@@ -1514,20 +1537,20 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         // next chunk's image is on its way
         for (uint32_t b0 = kb0; b0 < kb1; b0 += 2 * NB) {
             const uint32_t b1 = b0 + NB;
-            q4_image_loads<NB>(a, b1, kb1, lane, By);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b0,
+            q4_image_loads<NB>(a, tk, b1, kb1, lane, By);
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, tk, payload, meta, smem, meta_lds, rows, r0, b0,
                                                min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
                                                Bx, acc);
             if (b1 >= kb1) break;
-            q4_image_loads<NB>(a, b1 + NB, kb1, lane, Bx);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b1,
+            q4_image_loads<NB>(a, tk, b1 + NB, kb1, lane, Bx);
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, tk, payload, meta, smem, meta_lds, rows, r0, b1,
                                                min(static_cast<uint32_t>(NB), kb1 - b1), lane, ppieces, mpieces,
                                                By, acc);
         }
     } else {
         for (uint32_t b0 = kb0; b0 < kb1; b0 += NB) {
-            q4_image_loads<NB>(a, b0, kb1, lane, Bx);
-            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, payload, meta, smem, meta_lds, rows, r0, b0,
+            q4_image_loads<NB>(a, tk, b0, kb1, lane, Bx);
+            mfma_chunk_q4<NB, RT, STAGE, DUMP>(a, tk, payload, meta, smem, meta_lds, rows, r0, b0,
                                                min(static_cast<uint32_t>(NB), kb1 - b0), lane, ppieces, mpieces,
                                                Bx, acc);
         }
@@ -1565,7 +1588,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t tok = 4 * g + r;
-                if (tok >= a.ntok) continue;
+                if (tok >= tk.ntok) continue;
 #pragma unroll
                 for (int t = 0; t < RT; ++t) {
                     const uint32_t row = r0 + 16 * t + m;
@@ -1578,8 +1601,8 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
         }
         return;
     }
-    if (ks == 0 && m < a.ntok) {
-        const float xs = a.scales[m];
+    if (ks == 0 && m < tk.ntok) {
+        const float xs = tk.scales[m];
         const bool vec = (a.vec_out >> job) & 1u;
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
@@ -1623,6 +1646,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 // meta[i] of the arguments are the copies.
 template <int NB, bool SPLIT, bool DUMP>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(MfmaArgs a) {
+    const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -1638,6 +1662,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
                             : job == 1 ? a.output_stride[1]
                             : job == 2 ? a.output_stride[2]
                                        : a.output_stride[3];
+    output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
     const uint32_t local = blockIdx.x - first;
@@ -1650,12 +1675,12 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     // the epilogue's token scales and prior outputs, loaded ahead
     float xs_pre[4], res_pre[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+    for (int r = 0; r < 4; ++r) xs_pre[r] = tk.scales[min(4 * g + r, tk.ntok - 1)];
     if (!SPLIT && a.accumulate && wave == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r, row = r0 + m;
-            res_pre[r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+            res_pre[r] = tok < tk.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
         }
     }
     const uint8_t *pbase = payload + (static_cast<size_t>(rg) * a.units) * 1024 + lane * 16;
@@ -1664,9 +1689,9 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     HvImage<NB> im;
     // the image as bounded buffer loads that skip absent tokens' columns
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(a.image), 0, static_cast<int>(a.units * static_cast<uint32_t>(mfma_image_block_bytes())),
+        const_cast<uint8_t *>(tk.image), 0, static_cast<int>(a.units * static_cast<uint32_t>(mfma_image_block_bytes())),
         0x00020000);
-    const uint32_t skip = m < a.ntok ? 0u : 0x80000000u, sskip = 4 * g < a.ntok ? 0u : 0x80000000u;
+    const uint32_t skip = m < tk.ntok ? 0u : 0x80000000u, sskip = 4 * g < tk.ntok ? 0u : 0x80000000u;
     // one chunk of the wave's units from b0; the first is issued outside the
     // loop, so the loop header's wait for every load in flight does not
     // hold the first weight loads behind the epilogue's early loads
@@ -1714,7 +1739,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t row = r0 + m, tok = 4 * g + r;
-                    if (row < rows && tok < a.ntok)
+                    if (row < rows && tok < tk.ntok)
                         a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b0 + i] = ci[r];
                 }
             }
@@ -1752,7 +1777,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r;
-            if (tok >= a.ntok) continue;
+            if (tok >= tk.ntok) continue;
             float v = mul_rounded(acc[r], xs_pre[r]);
             if constexpr (SPLIT) {
                 if (bias && qs == 0) v = add_rounded(v, bias[row]);
@@ -1835,7 +1860,7 @@ struct Q4Split {
 // operands read from the split's row-major staging: payload [16 rows][pst
 // pieces] (piece v = chunk qs of unit v), meta [16 rows][mst dwords].
 template <int NB>
-__device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t *lds, const Q4Split &sp,
+__device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const MfmaTok &tk, const uint8_t *lds, const Q4Split &sp,
                                                uint32_t rows, uint32_t r0, uint32_t v0, uint32_t nv, uint32_t lane,
                                                float (&acc)[4]) {
     const uint32_t g = lane >> 4, m = lane & 15;
@@ -1851,7 +1876,7 @@ __device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t 
         Ml[i] = mt.x;
         Mh[i] = mt.y;
         const uint32_t b = min(4 * v + sp.qs, a.nblk - 1);
-        B[i] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+        B[i] = *reinterpret_cast<const uint2 *>(tk.image + static_cast<size_t>(b) * 512 + lane * 8);
     }
     __builtin_amdgcn_sched_barrier(0);
     const bool live = row < rows;
@@ -1874,6 +1899,7 @@ __device__ __forceinline__ void mfma_chunk_q4s(const MfmaArgs &a, const uint8_t 
 
 template <int NB>
 __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_kernel(MfmaArgs a) {
+    const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -1890,6 +1916,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
                             : job == 1 ? a.output_stride[1]
                             : job == 2 ? a.output_stride[2]
                                        : a.output_stride[3];
+    output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
     const uint32_t local = blockIdx.x - first;
@@ -1938,7 +1965,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t v0 = wave * a.nb, v1 = min(a.units, v0 + a.nb);
     for (uint32_t v = v0; v < v1; v += NB)
-        mfma_chunk_q4s<NB>(a, smem, sp, rows, r0, v, min(static_cast<uint32_t>(NB), v1 - v), lane, acc);
+        mfma_chunk_q4s<NB>(a, tk, smem, sp, rows, r0, v, min(static_cast<uint32_t>(NB), v1 - v), lane, acc);
 
     // the waves' partials, summed in wave order (LDS after the staged tiles)
     if (KS > 1) {
@@ -1963,8 +1990,8 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r;
-            if (tok >= a.ntok) continue;
-            float v = mul_rounded(acc[r], a.scales[tok]);
+            if (tok >= tk.ntok) continue;
+            float v = mul_rounded(acc[r], tk.scales[tok]);
             if (bias && sp.qs == 0) v = add_rounded(v, bias[row]);
             unsafeAtomicAdd(output + static_cast<size_t>(tok) * stride + row, v);
         }
@@ -1984,6 +2011,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
 // is units per wave.
 template <int NB, bool SPLIT, bool DUMP>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kernel(MfmaArgs a) {
+    const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
@@ -1999,6 +2027,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
                             : job == 1 ? a.output_stride[1]
                             : job == 2 ? a.output_stride[2]
                                        : a.output_stride[3];
+    output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
     const uint32_t local = blockIdx.x - first;
@@ -2010,12 +2039,12 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
     const uint32_t v0 = min(s1, s0 + wave * a.nb), v1 = min(s1, v0 + a.nb);
     float xs_pre[4], res_pre[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) xs_pre[r] = a.scales[min(4 * g + r, a.ntok - 1)];
+    for (int r = 0; r < 4; ++r) xs_pre[r] = tk.scales[min(4 * g + r, tk.ntok - 1)];
     if (!SPLIT && a.accumulate && wave == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r;
-            res_pre[r] = tok < a.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
+            res_pre[r] = tok < tk.ntok && row < rows ? output[static_cast<size_t>(tok) * stride + row] : 0.0f;
         }
     }
     const uint8_t *pbase = payload + static_cast<size_t>(rg) * a.units * 1024 + lane * 16;
@@ -2038,7 +2067,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
                 // blocks past K (the last unit's padding) read the last block
                 // and are skipped below
                 const uint32_t b = min(4 * u + q, a.nblk - 1);
-                X[i][q] = *reinterpret_cast<const uint2 *>(a.image + static_cast<size_t>(b) * 512 + lane * 8);
+                X[i][q] = *reinterpret_cast<const uint2 *>(tk.image + static_cast<size_t>(b) * 512 + lane * 8);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -2062,7 +2091,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const uint32_t tok = 4 * g + r;
-                        if (row < rows && tok < a.ntok) a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b] = ci[r];
+                        if (row < rows && tok < tk.ntok) a.dump[(static_cast<size_t>(tok) * rows + row) * a.nblk + b] = ci[r];
                     }
                 }
                 // rows past the matrix are zero in the copy: scale 0
@@ -2095,7 +2124,7 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r;
-            if (tok >= a.ntok) continue;
+            if (tok >= tk.ntok) continue;
             float v = mul_rounded(acc[r], xs_pre[r]);
             if constexpr (SPLIT) {
                 if (bias && qs == 0) v = add_rounded(v, bias[row]);
@@ -2502,8 +2531,9 @@ hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const floa
                                 uint32_t image_stride, float *scales, int8_t *q8, uint32_t q8_stride,
                                 hipStream_t stream, uint8_t *mfma_image) {
     if (batch == 0 || mode > kInSwiglu || mode == kInImage || (mode == kInNorm && !norm) ||
-        (mode == kInSwiglu && !x2) || (mfma_image && batch > static_cast<uint32_t>(kMfmaTokens)))
+        (mode == kInSwiglu && !x2) || (mfma_image && batch > static_cast<uint32_t>(kMfmaMaxBatch)))
         return hipErrorInvalidValue;
+    const size_t mgroup = mfma_image ? mfma_image_bytes(t) : 0;
     const uint32_t staged = static_cast<size_t>(t.cols) * sizeof(float) <= kGemvLdsLimit ? 1u : 0u;
     const size_t lds = staged ? static_cast<size_t>(t.cols) * sizeof(float) : 0;
     if (t.kind != kHvsq2 && t.kind != kQ4_0) return hipErrorInvalidValue;
@@ -2517,11 +2547,11 @@ hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const floa
         if (narrow)
             hipLaunchKernelGGL((quantize_image_kernel<KD, EP, 256>), dim3(batch), dim3(256), lds, stream, x, t.cols,
                                x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm, eps,
-                               staged, mfma_image);
+                               staged, mfma_image, mgroup);
         else
             hipLaunchKernelGGL((quantize_image_kernel<KD, EP, 1024>), dim3(batch), dim3(1024), lds, stream, x,
                                t.cols, x_stride, t.units, image, image_stride, scales, q8, q8_stride, mode, x2, norm,
-                               eps, staged, mfma_image);
+                               eps, staged, mfma_image, mgroup);
     };
     auto by_ept = [&](auto kind_c) {
         if (!staged) go(kind_c, std::integral_constant<int, 0>{});
@@ -2778,19 +2808,22 @@ MfmaPlan mfma_plan(const DeviceTensor &t, uint64_t total_rows) {
     return p;
 }
 
+// 16-token groups of a launch (grid.y; each group its own MFMA image)
+uint32_t mfma_groups(const MfmaArgs &a) { return (a.ntok + 15) / 16; }
+
 template <int KIND, int NB, int RT>
 hipError_t launch_mfma_rt(bool stage, uint32_t grid, uint32_t threads, size_t lds, const MfmaArgs &a,
                           hipStream_t stream) {
     if (a.dump) {
         if (stage)
-            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, true>), dim3(grid), dim3(threads), lds, stream, a);
+            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, true>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a);
         else
-            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, true>), dim3(grid), dim3(threads), lds, stream,
+            hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, true>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream,
                                a);
     } else if (stage) {
-        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, false>), dim3(grid), dim3(threads), lds, stream, a);
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, true, false>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a);
     } else {
-        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, false>), dim3(grid), dim3(threads), lds, stream, a);
+        hipLaunchKernelGGL((mfma_gemm_kernel<KIND, NB, RT, false, false>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a);
     }
     return hipGetLastError();
 }
@@ -2833,8 +2866,9 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate,
                                   int32_t *dump, const float *const *biases) {
-    if ((dump && count != 1) || count == 0 || count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
-        batch > static_cast<uint32_t>(kMfmaTokens))
+    if ((dump && (count != 1 || batch > static_cast<uint32_t>(kMfmaTokens))) || count == 0 ||
+        count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
+        batch > static_cast<uint32_t>(kMfmaMaxBatch))
         return hipErrorInvalidValue;
     const DeviceTensor &t0 = *tensors[0];
     uint64_t total_rows = 0;
@@ -2897,6 +2931,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     a.nb = p.nb;
     a.stage_bytes = p.stage_bytes;
     a.image = image;
+    a.group_image_bytes = mfma_image_bytes(t0);
     a.scales = scales;
     a.ntok = batch;
     a.accumulate = accumulate ? 1u : 0u;
@@ -2918,7 +2953,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         const uint32_t threads = p.waves * kWaveSize;
         const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
         if (p.waves > static_cast<uint32_t>(kMfmaMaxWaves)) return hipErrorInvalidValue;
-#define QWN_Q4D(NBV, SP, DU) hipLaunchKernelGGL((mfma_q4_direct_kernel<NBV, SP, DU>), dim3(grid), dim3(threads), lds, stream, a)
+#define QWN_Q4D(NBV, SP, DU) hipLaunchKernelGGL((mfma_q4_direct_kernel<NBV, SP, DU>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
         if (split) {
             switch (p.nbt) {
             case 2: QWN_Q4D(2, true, false); break;
@@ -2956,7 +2991,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         a.nb = p.nb;
         const uint32_t threads = p.waves * kWaveSize;
         const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
-#define QWN_HVD(NBV, SP, DU) hipLaunchKernelGGL((mfma_direct_kernel<NBV, SP, DU>), dim3(grid), dim3(threads), lds, stream, a)
+#define QWN_HVD(NBV, SP, DU) hipLaunchKernelGGL((mfma_direct_kernel<NBV, SP, DU>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
         if (split) {
             switch (p.nbt) {
             case 2: QWN_HVD(2, true, false); break;
@@ -2982,10 +3017,10 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     if (split) {
         const uint32_t threads = p.waves * kWaveSize;
         switch (p.nbt) {
-        case 2: hipLaunchKernelGGL(mfma_q4_split_kernel<2>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
-        case 3: hipLaunchKernelGGL(mfma_q4_split_kernel<3>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
-        case 5: hipLaunchKernelGGL(mfma_q4_split_kernel<5>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
-        default: hipLaunchKernelGGL(mfma_q4_split_kernel<8>, dim3(grid), dim3(threads), p.lds_bytes, stream, a); break;
+        case 2: hipLaunchKernelGGL(mfma_q4_split_kernel<2>, dim3(grid, mfma_groups(a)), dim3(threads), p.lds_bytes, stream, a); break;
+        case 3: hipLaunchKernelGGL(mfma_q4_split_kernel<3>, dim3(grid, mfma_groups(a)), dim3(threads), p.lds_bytes, stream, a); break;
+        case 5: hipLaunchKernelGGL(mfma_q4_split_kernel<5>, dim3(grid, mfma_groups(a)), dim3(threads), p.lds_bytes, stream, a); break;
+        default: hipLaunchKernelGGL(mfma_q4_split_kernel<8>, dim3(grid, mfma_groups(a)), dim3(threads), p.lds_bytes, stream, a); break;
         }
         return hipGetLastError();
     }

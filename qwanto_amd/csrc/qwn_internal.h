@@ -45,6 +45,7 @@ constexpr int kGemvMaxThreads = kWaveSize * kGemvMaxWaves;
 constexpr int kTilePad = 16;                      // tiles are stored in multiples of this
 constexpr uint32_t kChipCus = 256;                // compute units of one MI355X
 constexpr int kMaxTokensPerLaunch = 16;
+constexpr int kMfmaMaxBatch = 64;                 // tokens of one MFMA GEMM launch (16-token groups)
 constexpr size_t kGemvLdsLimit = 64 * 1024;
 constexpr int kMaxGroup = 4;                      // tensors sharing one input in one launch
 
@@ -218,7 +219,9 @@ hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const f
                             uint32_t batch, uint32_t output_stride, hipStream_t stream);
 // The same over up to kMaxGroup tensors of equal K sharing one image (one
 // launch); output_strides may be null (0 entries: each tensor's rows);
-// accumulate: outputs += W x_t * scales[t] (the residual stream).
+// accumulate: outputs += W x_t * scales[t] (the residual stream).  Up to
+// kMfmaMaxBatch tokens: token group g (tokens 16g .. 16g+15) reads its own
+// MFMA image at image + g * mfma_image_bytes(t) (dump: at most 16 tokens).
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate = false,

@@ -154,9 +154,10 @@ def read_caches(dec, layers, count):
     (MID_CTX, "q4_0", 270, False, ""), (MID_CTX, "hvsq2", 520, True, ""), (MID_QWEN2, "q4_0", 300, False, ""),
     (MID_HD256, "q4_0", 270, True, "")])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
-    """qwn_hip_decoder_prefill (prompt blocks of up to 16 tokens through the
-    batched GEMV / int8 MFMA GEMM, block RoPE/append, causal attention per
-    token; the split-attention path for LONG_CTX): the last prompt token's
+    """qwn_hip_decoder_prefill (prompt blocks of up to 64 tokens: the int8
+    MFMA GEMM over 16-token groups from 3 (Q4_0) / 2 (HyperVSQ-2) tokens,
+    the batched GEMV below; block RoPE/append, causal attention per token;
+    the split-attention path for LONG_CTX): the last prompt token's
     logits and eight forward() steps that read the cache the prefill wrote.
 
     Against the oracle (prompt and the oracle's greedy ids): within the
@@ -255,7 +256,7 @@ def test_generate_equals_stepwise(gpu_ctx):
         prompt = synth.prompt_tokens(rng, SMALL["vocab"], 19)
         toks, st = dec.generate(prompt, 20)
         assert st.generated_tokens == 20 and st.position == 39 and st.graph == 1
-        assert st.prefill_block_tokens == 16
+        assert st.prefill_block_tokens == 64   # int8 MFMA GEMMs over 16-token groups
         dec.reset()
         _, nxt = dec.prefill(prompt, logits=False)
         step = []
@@ -275,7 +276,7 @@ def test_resident_decoder_qwen2_1p5b_golden(gpu_ctx, name):
     the successor golden's untied head), Q8 KV; 32-token prompt, 128 greedy steps of the golden decode (the oracle's,
     bit-identical to the reference decoder's).
 
-    Teacher-forced: the prompt as two 16-token prefill blocks, then the
+    Teacher-forced: the prompt as one 32-token prefill block, then the
     golden ids one forward() at a time; every step's logits against the
     golden step (decode_golden.step_error: the top-16 logits, nothing else
     above them), within the golden's stored envelope.  Free-running:

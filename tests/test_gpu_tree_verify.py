@@ -67,7 +67,7 @@ def path_to(parents, i):
 @pytest.mark.parametrize("cfg,dtype,P,levels", [
     (SMALL, "q4_0", 20, (3, 8, 14, 15)), (QWEN2_LIKE, "hvsq2", 12, (3, 8, 14, 15)),
     (QWEN2_LIKE, "q4_0", 7, (3, 8, 14, 15)), (LONG_CTX, "hvsq2", 300, (3, 8, 14, 15)),
-    # 64 nodes (four 16-node blocks), depth 8: the reference's limits (c/qwanto_jetspec.h:17-18)
+    # 64 nodes (one block of four 16-token MFMA groups), depth 8: the reference's limits (c/qwanto_jetspec.h:17-18)
     (SMALL, "hvsq2", 9, (2, 4, 6, 8, 10, 10, 12, 12)), (LONG_CTX, "q4_0", 600, (1, 3, 6, 10, 14, 14, 16)),
     # nodes straddling the 256- and 512-token chunk boundaries
     (MID_CTX, "q4_0", 240, (3, 8, 14, 15)), (MID_CTX, "hvsq2", 500, (2, 4, 6, 8, 10, 10, 12, 12))])
