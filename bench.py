@@ -452,8 +452,8 @@ def lm_head_bench(torch, ctx, steps=20):
 
 def tree_verify_bench(ctx, model, prompt, reps=10):
     """Speculative verification on the resident decoder after the prompt: a
-    64-node draft tree (qwn_hip_decoder_verify_tree: 3 roots, depth 8, four
-    16-node blocks, the LM head on every node) against a 16-token chain
+    64-node draft tree (qwn_hip_decoder_verify_tree: 3 roots, depth 8, one
+    64-node block, the LM head on every node) against a 16-token chain
     verify block (qwn_hip_decoder_verify); ms per call including the
     synchronisation, the per-node greedy ids copied back (not the logits)."""
     import numpy as np

@@ -119,8 +119,9 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_verify(QwnCudaContextHandle *context, QwnHi
 /* Speculative verification of a draft TREE (c/qwanto_jetspec.h:17-33):
  * `count` (1..64) nodes after the cached prefix of P tokens, node i =
  * (tokens[i], parents[i]) with parents[i] an earlier node or -1 (a root,
- * attached to the prefix).  One forward over the nodes in index order, in
- * blocks of 16: node i is rotated for position P + depth(i), its K/V held
+ * attached to the prefix).  One forward over the nodes in index order (one
+ * block of up to 64 on the int8-MFMA path, else blocks of 16): node i is
+ * rotated for position P + depth(i), its K/V held
  * at cache slot P + i, and it attends to the prefix, its ancestors and
  * itself (the ancestor mask of qwn_jetspec_build_tree_mask,
  * c/qwanto_jetspec.c:33-49).  logits [count][vocab] (host, may be NULL) are
