@@ -154,6 +154,20 @@ def read_caches(dec, layers, count):
     (MID_CTX, "q4_0", 270, False, ""), (MID_CTX, "hvsq2", 520, True, ""), (MID_QWEN2, "q4_0", 300, False, ""),
     (MID_HD256, "q4_0", 270, True, "")])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
+    check_prefill(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias)
+
+
+@pytest.mark.parametrize("cfg,dtype,P", [(QWEN2_LIKE, "q4_0", 70), (QWEN2_LIKE, "hvsq2", 70), (SMALL, "q4_0", 37)])
+def test_prefill_without_mfma_copy(gpu_ctx, oracle_lib, monkeypatch, cfg, dtype, P):
+    """The same checks with the weights uploaded without the MFMA-order copy
+    (QWN_HIP_MFMA_COPY=0): a block's GEMMs take the staged MFMA kernels
+    (weights read from the wave tiles), over 16-token groups in one launch
+    (a 64-token block and a 6-token one; a 37-token block)."""
+    monkeypatch.setenv("QWN_HIP_MFMA_COPY", "0")
+    check_prefill(gpu_ctx, oracle_lib, cfg, dtype, P, False, "")
+
+
+def check_prefill(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
     """qwn_hip_decoder_prefill (prompt blocks of up to 64 tokens: the int8
     MFMA GEMM over 16-token groups from 3 (Q4_0) / 2 (HyperVSQ-2) tokens,
     the batched GEMV below; block RoPE/append, causal attention per token;
