@@ -335,9 +335,10 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
     // activation images, or where mfma_batch() says so the int8 MFMA GEMM
     // on the MFMA image; add: residual stream
     const bool mfma = d->pmimg && mfma_batch(d->proj[P_Q]->kind, m, d->proj[P_Q]->mfma_payload != nullptr);
+    // swiglu (MFMA, gate/up with the MFMA-order copy): outs[0] = silu(gate) * up
     auto project = [&](std::initializer_list<const DeviceTensor *> ts, std::initializer_list<float *> outs,
                        uint32_t mode, const float *x, const float *x2, const float *norm, uint32_t x_stride,
-                       bool add, std::initializer_list<const float *> biases) {
+                       bool add, std::initializer_list<const float *> biases, bool swiglu = false) {
         const float *bv[kMaxGroup] = {};
         {
             uint32_t n = 0;
@@ -355,7 +356,7 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
             for (const DeviceTensor *t : ts) tv[n++] = t;
             n = 0;
             for (float *o : outs) ov[n++] = o;
-            return launch_gemm_mfma_group(tv, ov, n, d->pmimg, d->pscales, m, nullptr, s, add, nullptr, bv);
+            return launch_gemm_mfma_group(tv, ov, n, d->pmimg, d->pscales, m, nullptr, s, add, nullptr, bv, swiglu);
         }
         if ((e2 = launch_prepare_image(t0, mode, x, x2, norm, d->eps, m, x_stride, d->pimg, d->pimg_stride,
                                        d->pscales, nullptr, 0, s)) != hipSuccess)
@@ -405,11 +406,16 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
                                              tree ? d->tree_base : nullptr)) != hipSuccess)
                     return e;
         }
+        // on the MFMA path with the MFMA-order copy the gate/up launch stores
+        // silu(gate) * up itself, and the down input is quantized as is
+        const bool pair = mfma && w[P_GATE]->mfma_payload && w[P_GATE]->mfma_meta && w[P_UP]->mfma_payload &&
+                          w[P_UP]->mfma_meta;
         if ((e = project({w[P_O]}, {d->px}, kInF32, d->pattn, nullptr, nullptr, Q, true,
                          {layer_bias(d, l, P_O)})) != hipSuccess ||
-            (e = project({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}, kInNorm, d->px, nullptr, npost, D, false, {})) !=
-                hipSuccess ||
-            (e = project({w[P_DOWN]}, {d->px}, kInSwiglu, d->pgate, d->pup, nullptr, I, true, {})) != hipSuccess)
+            (e = project({w[P_GATE], w[P_UP]}, {d->pgate, d->pup}, kInNorm, d->px, nullptr, npost, D, false, {},
+                         pair)) != hipSuccess ||
+            (e = project({w[P_DOWN]}, {d->px}, pair ? kInF32 : kInSwiglu, d->pgate, pair ? nullptr : d->pup, nullptr,
+                         I, true, {})) != hipSuccess)
             return e;
     }
     hipLaunchKernelGGL(prefill_advance_kernel, dim3(1), dim3(64), 0, s, d->state, d->ppos, m, last ? 1u : 0u);

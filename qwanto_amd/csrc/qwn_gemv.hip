@@ -1644,16 +1644,22 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_gemm_kernel(Mf
 // few row groups, each row group split four ways by unit range, the
 // partials added with float atomics (in no fixed order).  payload[i] /
 // meta[i] of the arguments are the copies.
-template <int NB, bool SPLIT, bool DUMP>
+template <int NB, bool SPLIT, bool DUMP, bool PAIR = false>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(MfmaArgs a) {
     const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
     const uint32_t KS = 1u << a.ks_log2;
+    static_assert(!PAIR || (!SPLIT && !DUMP), "gate/up pairs: plain stores");
+    // PAIR (the SwiGLU of a gate/up pair): waves [0, KS) take the gate rows
+    // of the row group, waves [KS, 2 KS) the same up rows; wj is a wave's
+    // index within its job
+    const uint32_t wj = PAIR && wave >= KS ? wave - KS : wave;
     const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
     uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
     job = __builtin_amdgcn_readfirstlane(job);
+    if constexpr (PAIR) job = wave >= KS ? 1u : 0u;
     const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
     const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
     float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
@@ -1665,18 +1671,18 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
-    const uint32_t local = blockIdx.x - first;
+    const uint32_t local = PAIR ? blockIdx.x : blockIdx.x - first;
     const uint32_t qs = SPLIT ? (local & 3u) : 0u, rg = SPLIT ? (local >> 2) : local, r0 = rg * 16;
     const uint32_t g = lane >> 4, m = lane & 15;
     // this workgroup's units (SPLIT: quarter qs of the row's), then the wave's
     const uint32_t per_split = SPLIT ? (a.nblk + 3) / 4 : a.nblk;
     const uint32_t s0 = min(a.nblk, qs * per_split), s1 = min(a.nblk, s0 + per_split);
-    const uint32_t kb0 = min(s1, s0 + wave * a.nb), kb1 = min(s1, kb0 + a.nb);
+    const uint32_t kb0 = min(s1, s0 + wj * a.nb), kb1 = min(s1, kb0 + a.nb);
     // the epilogue's token scales and prior outputs, loaded ahead
     float xs_pre[4], res_pre[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) xs_pre[r] = tk.scales[min(4 * g + r, tk.ntok - 1)];
-    if (!SPLIT && a.accumulate && wave == 0) {
+    if (!SPLIT && a.accumulate && wj == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r, row = r0 + m;
@@ -1756,14 +1762,16 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     for (uint32_t b0 = kb0 + NB; b0 < kb1; b0 += NB) chunk(b0);
     // the K-split partials, summed in wave order
     if (KS > 1) {
-        float *part_s = reinterpret_cast<float *>(smem);
-        if (wave > 0) {
-            float *dst = part_s + ((wave - 1) * kWaveSize + lane) * 4;
+        // PAIR: each job's partials in its own region (a grouped launch's
+        // other jobs are other workgroups)
+        float *part_s = reinterpret_cast<float *>(smem) + (PAIR ? job : 0u) * (KS - 1) * kWaveSize * 4;
+        if (wj > 0) {
+            float *dst = part_s + ((wj - 1) * kWaveSize + lane) * 4;
 #pragma unroll
             for (int r = 0; r < 4; ++r) dst[r] = acc[r];
         }
         __syncthreads();
-        if (wave == 0)
+        if (wj == 0)
             for (uint32_t k = 1; k < KS; ++k) {
                 const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4;
 #pragma unroll
@@ -1772,6 +1780,26 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_direct_kernel(
     }
     // lane (g, m) holds tokens 4g .. 4g+3 of row m; accumulate: out += the
     // rounded product, in two roundings as the dot8 epilogue
+    if constexpr (PAIR) {
+        // the up wave hands its rounded products over; the gate wave stores
+        // silu(gate) * up, the arithmetic of the SwiGLU input transform
+        float *up_s = reinterpret_cast<float *>(smem) + 2 * (KS - 1) * kWaveSize * 4;
+        if (job == 1 && wj == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) up_s[lane * 4 + r] = mul_rounded(acc[r], xs_pre[r]);
+        }
+        __syncthreads();
+        if (job == 0 && wj == 0 && r0 + m < rows) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = 4 * g + r;
+                if (tok >= tk.ntok) continue;
+                const float gv = mul_rounded(acc[r], xs_pre[r]), uv = up_s[lane * 4 + r];
+                output[static_cast<size_t>(tok) * stride + r0 + m] = mul_rounded(gv / (1.0f + expf(-gv)), uv);
+            }
+        }
+        return;
+    }
     const uint32_t row = r0 + m;
     if (wave == 0 && row < rows) {
 #pragma unroll
@@ -2009,16 +2037,22 @@ __global__ __launch_bounds__(kWaveSize * kMfmaSplitMaxWaves) void mfma_q4_split_
 // otherwise mfma_gemm_kernel's single pass, the waves' partials summed in
 // wave order.  payload[i] / meta[i] of the arguments are the copies; a.nb
 // is units per wave.
-template <int NB, bool SPLIT, bool DUMP>
+template <int NB, bool SPLIT, bool DUMP, bool PAIR = false>
 __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kernel(MfmaArgs a) {
     const MfmaTok tk = mfma_tok(a);
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x % kWaveSize;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
     const uint32_t KS = 1u << a.ks_log2;
+    static_assert(!PAIR || (!SPLIT && !DUMP), "gate/up pairs: plain stores");
+    // PAIR (the SwiGLU of a gate/up pair): waves [0, KS) take the gate rows
+    // of the row group, waves [KS, 2 KS) the same up rows; wj is a wave's
+    // index within its job
+    const uint32_t wj = PAIR && wave >= KS ? wave - KS : wave;
     const uint32_t b1 = a.job_block[1], b2 = a.job_block[2], b3 = a.job_block[3];
     uint32_t job = (blockIdx.x >= b1 ? 1u : 0u) + (blockIdx.x >= b2 ? 1u : 0u) + (blockIdx.x >= b3 ? 1u : 0u);
     job = __builtin_amdgcn_readfirstlane(job);
+    if constexpr (PAIR) job = wave >= KS ? 1u : 0u;
     const uint8_t *payload = job == 0 ? a.payload[0] : job == 1 ? a.payload[1] : job == 2 ? a.payload[2] : a.payload[3];
     const uint8_t *meta = job == 0 ? a.meta[0] : job == 1 ? a.meta[1] : job == 2 ? a.meta[2] : a.meta[3];
     float *output = job == 0 ? a.output[0] : job == 1 ? a.output[1] : job == 2 ? a.output[2] : a.output[3];
@@ -2030,17 +2064,17 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
     output += static_cast<size_t>(tk.tok0) * stride;  // this launch's token group
     const uint32_t first = job == 0 ? 0u : job == 1 ? b1 : job == 2 ? b2 : b3;
     const float *bias = job == 0 ? a.bias[0] : job == 1 ? a.bias[1] : job == 2 ? a.bias[2] : a.bias[3];
-    const uint32_t local = blockIdx.x - first;
+    const uint32_t local = PAIR ? blockIdx.x : blockIdx.x - first;
     const uint32_t qs = SPLIT ? (local & 3u) : 0u, rg = SPLIT ? (local >> 2) : local, r0 = rg * 16;
     const uint32_t g = lane >> 4, m = lane & 15, row = r0 + m;
     // this workgroup's units (SPLIT: quarter qs of the row's), then the wave's
     const uint32_t per_split = SPLIT ? (a.units + 3) / 4 : a.units;
     const uint32_t s0 = min(a.units, qs * per_split), s1 = min(a.units, s0 + per_split);
-    const uint32_t v0 = min(s1, s0 + wave * a.nb), v1 = min(s1, v0 + a.nb);
+    const uint32_t v0 = min(s1, s0 + wj * a.nb), v1 = min(s1, v0 + a.nb);
     float xs_pre[4], res_pre[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) xs_pre[r] = tk.scales[min(4 * g + r, tk.ntok - 1)];
-    if (!SPLIT && a.accumulate && wave == 0) {
+    if (!SPLIT && a.accumulate && wj == 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t tok = 4 * g + r;
@@ -2105,19 +2139,41 @@ __global__ __launch_bounds__(kWaveSize * kMfmaMaxWaves) void mfma_q4_direct_kern
     for (uint32_t c0 = v0 + NB; c0 < v1; c0 += NB) chunk(c0);
     // the K-split partials, summed in wave order
     if (KS > 1) {
-        float *part_s = reinterpret_cast<float *>(smem);
-        if (wave > 0) {
-            float *dst = part_s + ((wave - 1) * kWaveSize + lane) * 4;
+        // PAIR: each job's partials in its own region (a grouped launch's
+        // other jobs are other workgroups)
+        float *part_s = reinterpret_cast<float *>(smem) + (PAIR ? job : 0u) * (KS - 1) * kWaveSize * 4;
+        if (wj > 0) {
+            float *dst = part_s + ((wj - 1) * kWaveSize + lane) * 4;
 #pragma unroll
             for (int r = 0; r < 4; ++r) dst[r] = acc[r];
         }
         __syncthreads();
-        if (wave == 0)
+        if (wj == 0)
             for (uint32_t k = 1; k < KS; ++k) {
                 const float *src = part_s + ((k - 1) * kWaveSize + lane) * 4;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[r] += src[r];
             }
+    }
+    if constexpr (PAIR) {
+        // the up wave hands its rounded products over; the gate wave stores
+        // silu(gate) * up, the arithmetic of the SwiGLU input transform
+        float *up_s = reinterpret_cast<float *>(smem) + 2 * (KS - 1) * kWaveSize * 4;
+        if (job == 1 && wj == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) up_s[lane * 4 + r] = mul_rounded(acc[r], xs_pre[r]);
+        }
+        __syncthreads();
+        if (job == 0 && wj == 0 && r0 + m < rows) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tok = 4 * g + r;
+                if (tok >= tk.ntok) continue;
+                const float gv = mul_rounded(acc[r], xs_pre[r]), uv = up_s[lane * 4 + r];
+                output[static_cast<size_t>(tok) * stride + r0 + m] = mul_rounded(gv / (1.0f + expf(-gv)), uv);
+            }
+        }
+        return;
     }
     // lane (g, m) holds tokens 4g .. 4g+3 of row m
     if (wave == 0 && row < rows) {
@@ -2865,7 +2921,7 @@ hipError_t launch_mfma_copy(const DeviceTensor &t, hipStream_t stream) {
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate,
-                                  int32_t *dump, const float *const *biases) {
+                                  int32_t *dump, const float *const *biases, bool swiglu) {
     if ((dump && (count != 1 || batch > static_cast<uint32_t>(kMfmaTokens))) || count == 0 ||
         count > static_cast<uint32_t>(kMaxGroup) || !image || !scales || batch == 0 ||
         batch > static_cast<uint32_t>(kMfmaMaxBatch))
@@ -2885,6 +2941,11 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
     // tensors that all carry the MFMA-order copy: direct loads
     bool direct = true;
     for (uint32_t i = 0; i < count; ++i) direct = direct && tensors[i]->mfma_payload && tensors[i]->mfma_meta;
+    // a gate/up pair stored as silu(gate) * up into outputs[0]: direct
+    // loads, plain stores, two tensors of equal rows
+    if (swiglu && (!direct || count != 2 || accumulate || dump || tensors[1]->rows != t0.rows ||
+                   (biases && (biases[0] || biases[1]))))
+        return hipErrorInvalidValue;
     // residual adds over few row groups: the four-way K split
     const uint64_t groups = (total_rows + 15) / 16;
     const bool split = accumulate && !dump && groups < 256 && (direct || (t0.kind == kQ4_0 && p.stage));
@@ -2917,7 +2978,8 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             if (a.output_stride[i] % 4 == 0 && (reinterpret_cast<uintptr_t>(outputs[i]) & 15u) == 0 &&
                 (reinterpret_cast<uintptr_t>(a.bias[i]) & 15u) == 0)
                 a.vec_out |= 1u << i;
-            grid += split ? 4 * ((t.rows + 15) / 16) : direct ? (t.rows + 15) / 16 : (t.rows + 16 * p.rt - 1) / (16 * p.rt);
+            if (!swiglu || i == 0)
+                grid += split ? 4 * ((t.rows + 15) / 16) : direct ? (t.rows + 15) / 16 : (t.rows + 16 * p.rt - 1) / (16 * p.rt);
         }
     }
     a.job_block[kMaxGroup] = grid;
@@ -2944,17 +3006,27 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         const uint32_t span = split ? (t0.units + 3) / 4 : t0.units;
         auto per_wave = [&](uint32_t ks) { return (span + (1u << ks) - 1) >> ks; };
         p.ks_log2 = 0;
-        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
+        // a pair runs both jobs' waves: at most 4 per job
+        const uint32_t ks_max = swiglu ? 2u : 3u;
+        while (p.ks_log2 < ks_max && per_wave(p.ks_log2) > 5) ++p.ks_log2;
         p.nb = per_wave(p.ks_log2);
         p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
         p.waves = 1u << p.ks_log2;
         a.ks_log2 = p.ks_log2;
         a.nb = p.nb;
-        const uint32_t threads = p.waves * kWaveSize;
-        const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
-        if (p.waves > static_cast<uint32_t>(kMfmaMaxWaves)) return hipErrorInvalidValue;
+        const uint32_t jobs = swiglu ? 2u : 1u;
+        const uint32_t threads = jobs * p.waves * kWaveSize;
+        const size_t lds = static_cast<size_t>(jobs * (p.waves - 1) + (swiglu ? 1 : 0)) * kWaveSize * 16;
+        if (jobs * p.waves > static_cast<uint32_t>(kMfmaMaxWaves)) return hipErrorInvalidValue;
 #define QWN_Q4D(NBV, SP, DU) hipLaunchKernelGGL((mfma_q4_direct_kernel<NBV, SP, DU>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
-        if (split) {
+#define QWN_Q4P(NBV) hipLaunchKernelGGL((mfma_q4_direct_kernel<NBV, false, false, true>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
+        if (swiglu) {
+            switch (p.nbt) {
+            case 2: QWN_Q4P(2); break;
+            case 3: QWN_Q4P(3); break;
+            default: QWN_Q4P(5); break;
+            }
+        } else if (split) {
             switch (p.nbt) {
             case 2: QWN_Q4D(2, true, false); break;
             case 3: QWN_Q4D(3, true, false); break;
@@ -2973,6 +3045,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             default: QWN_Q4D(5, false, false); break;
             }
         }
+#undef QWN_Q4P
 #undef QWN_Q4D
         return hipGetLastError();
     }
@@ -2983,16 +3056,27 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
         const uint32_t span = split ? (t0.units + 3) / 4 : t0.units;
         auto per_wave = [&](uint32_t ks) { return (span + (1u << ks) - 1) >> ks; };
         p.ks_log2 = 0;
-        while (p.ks_log2 < 3 && per_wave(p.ks_log2) > 5) ++p.ks_log2;
+        // a pair runs both jobs' waves: at most 4 per job
+        const uint32_t ks_max = swiglu ? 2u : 3u;
+        while (p.ks_log2 < ks_max && per_wave(p.ks_log2) > 5) ++p.ks_log2;
         p.nb = per_wave(p.ks_log2);
         p.nbt = p.nb <= 2 ? 2 : p.nb <= 3 ? 3 : 5;
         p.waves = 1u << p.ks_log2;
         a.ks_log2 = p.ks_log2;
         a.nb = p.nb;
-        const uint32_t threads = p.waves * kWaveSize;
-        const size_t lds = static_cast<size_t>(p.waves - 1) * kWaveSize * 16;
+        const uint32_t jobs = swiglu ? 2u : 1u;
+        const uint32_t threads = jobs * p.waves * kWaveSize;
+        const size_t lds = static_cast<size_t>(jobs * (p.waves - 1) + (swiglu ? 1 : 0)) * kWaveSize * 16;
+        if (jobs * p.waves > static_cast<uint32_t>(kMfmaMaxWaves)) return hipErrorInvalidValue;
 #define QWN_HVD(NBV, SP, DU) hipLaunchKernelGGL((mfma_direct_kernel<NBV, SP, DU>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
-        if (split) {
+#define QWN_HVP(NBV) hipLaunchKernelGGL((mfma_direct_kernel<NBV, false, false, true>), dim3(grid, mfma_groups(a)), dim3(threads), lds, stream, a)
+        if (swiglu) {
+            switch (p.nbt) {
+            case 2: QWN_HVP(2); break;
+            case 3: QWN_HVP(3); break;
+            default: QWN_HVP(5); break;
+            }
+        } else if (split) {
             switch (p.nbt) {
             case 2: QWN_HVD(2, true, false); break;
             case 3: QWN_HVD(3, true, false); break;
@@ -3011,6 +3095,7 @@ hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *con
             default: QWN_HVD(5, false, false); break;
             }
         }
+#undef QWN_HVP
 #undef QWN_HVD
         return hipGetLastError();
     }

@@ -222,10 +222,14 @@ hipError_t launch_gemm_mfma(const DeviceTensor &t, const uint8_t *image, const f
 // accumulate: outputs += W x_t * scales[t] (the residual stream).  Up to
 // kMfmaMaxBatch tokens: token group g (tokens 16g .. 16g+15) reads its own
 // MFMA image at image + g * mfma_image_bytes(t) (dump: at most 16 tokens).
+// swiglu: tensors[0] / [1] are a gate / up pair of equal rows, both with
+// the MFMA-order copy, no bias, no accumulate: outputs[0] = silu(gate) * up
+// per token (outputs[1] untouched).
 hipError_t launch_gemm_mfma_group(const DeviceTensor *const *tensors, float *const *outputs, uint32_t count,
                                   const uint8_t *image, const float *scales, uint32_t batch,
                                   const uint32_t *output_strides, hipStream_t stream, bool accumulate = false,
-                                  int32_t *dump = nullptr, const float *const *biases = nullptr);
+                                  int32_t *dump = nullptr, const float *const *biases = nullptr,
+                                  bool swiglu = false);
 constexpr uint32_t kMfmaMinTokens = 3;
 constexpr uint32_t kMfmaMinTokensQ4 = 6;
 // LDS per workgroup the MFMA GEMM plans its staging against: gfx950's
