@@ -36,6 +36,9 @@ MID_CTX = dict(SMALL, max_ctx=640)
 MID_QWEN2 = dict(hidden=768, intermediate=1024, layers=3, heads=6, kv_heads=1, head_dim=128, vocab=4096,
                  max_ctx=640, rope_theta=1e6, rms_eps=1e-6)
 MID_HD256 = dict(SMALL, heads=2, kv_heads=1, head_dim=256, max_ctx=640)
+# a hidden size whose block GEMMs split K over waves (HyperVSQ-2 and Q4_0
+# gate/up pairs with two or more K-split waves per job)
+WIDE = dict(QWEN2_LIKE, hidden=1536, intermediate=2048, layers=2)
 
 
 def with_norms(rng, model):
@@ -152,7 +155,8 @@ def read_caches(dec, layers, count):
     # prompts past the fused decode attention's 256-token chunks: the block
     # prefill and the token-by-token steps both cross chunk boundaries
     (MID_CTX, "q4_0", 270, False, ""), (MID_CTX, "hvsq2", 520, True, ""), (MID_QWEN2, "q4_0", 300, False, ""),
-    (MID_HD256, "q4_0", 270, True, "")])
+    (MID_HD256, "q4_0", 270, True, ""),
+    (WIDE, "hvsq2", 40, False, ""), (WIDE, "q4_0", 40, False, "")])
 def test_prefill_matches_stepwise_and_oracle(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias):
     check_prefill(gpu_ctx, oracle_lib, cfg, dtype, P, qk, bias)
 
