@@ -2614,7 +2614,9 @@ hipError_t launch_prepare_image(const DeviceTensor &t, uint32_t mode, const floa
         else if (per <= 1) go(kind_c, std::integral_constant<int, 1>{});
         else if (per <= 2) go(kind_c, std::integral_constant<int, 2>{});
         else if (per <= 4) go(kind_c, std::integral_constant<int, 4>{});
+        else if (per <= 6) go(kind_c, std::integral_constant<int, 6>{});
         else if (per <= 8) go(kind_c, std::integral_constant<int, 8>{});
+        else if (per <= 10) go(kind_c, std::integral_constant<int, 10>{});
         else go(kind_c, std::integral_constant<int, 16>{});
     };
     if (t.kind == kHvsq2) by_ept(std::integral_constant<int, kHvsq2>{});
