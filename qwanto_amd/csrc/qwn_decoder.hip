@@ -428,9 +428,9 @@ hipError_t enqueue_prefill(Decoder *d, uint32_t m, uint32_t kind, hipStream_t s,
         // images of the normalized tokens (Q4_0/HyperVSQ-2), one batched GEMV
         float *vl = d->vlogits + static_cast<size_t>(row0) * d->vocab;
         if (d->hpieces) {
-            // 16 tokens per head launch (the pieces image holds 16)
-            for (uint32_t t0 = 0; t0 < m; t0 += kPrefillTokens) {
-                const uint32_t mg = std::min(kPrefillTokens, m - t0);
+            // up to 32 tokens per head launch (the head read once per launch)
+            for (uint32_t t0 = 0; t0 < m; t0 += 2 * kPrefillTokens) {
+                const uint32_t mg = std::min(2 * kPrefillTokens, m - t0);
                 if ((e = launch_head_pieces(*d->head, d->px + static_cast<size_t>(t0) * D, D, d->final_norm, d->eps,
                                             mg, d->hpieces, d->hunscale + t0, s)) != hipSuccess ||
                     (e = launch_mfma_head(*d->head, d->hpieces, d->hunscale + t0, mg,
@@ -743,7 +743,7 @@ QWN_CUDA_ABI_API int qwn_hip_decoder_create(QwnCudaContextHandle *handle, const 
             static_cast<uint32_t>((image_bytes(d->head->kind, d->head->units) + 15) & ~static_cast<size_t>(15));
         part(reinterpret_cast<void **>(&d->vimg), P * d->vimg_stride);
         if (mfma_head_supported(*d->head)) {
-            part(reinterpret_cast<void **>(&d->hpieces), head_pieces_bytes(*d->head));
+            part(reinterpret_cast<void **>(&d->hpieces), head_pieces_bytes_32(*d->head));
             part(reinterpret_cast<void **>(&d->hunscale), P * 4);
         }
         part(reinterpret_cast<void **>(&d->vlogits), static_cast<size_t>(kTreeNodes) * d->vocab * 4);

@@ -46,7 +46,7 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __builtin_bit_
 // grid (tokens), 1024 threads: RMSNorm of the token (the fp32 arithmetic of
 // the head's norm image: x * (1 / sqrt(mean x^2 + eps)) * w, the sum in the
 // same per-thread order), then its pieces; unscale[t] = 2^-s (1 for BF16).
-template <bool BF16, int EPT>
+template <bool BF16, int EPT, int TS>
 __global__ __launch_bounds__(1024) void head_pieces_kernel(const float *__restrict__ x, uint32_t x_stride,
                                                            const float *__restrict__ norm, float eps, uint32_t K,
                                                            uint32_t units, uint16_t *__restrict__ pieces,
@@ -95,13 +95,13 @@ __global__ __launch_bounds__(1024) void head_pieces_kernel(const float *__restri
         }
     }
     if (tid == 0) unscale[t] = back;
-    const size_t plane = static_cast<size_t>(units) * 4 * kHeadTokens * 8;   // elements per piece
+    const size_t plane = static_cast<size_t>(units) * 4 * TS * 8;   // elements per piece
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const uint32_t k = tid + 1024u * e;
         if (k < units * 32) {
             const uint32_t u = k / 32, q = (k % 32) / 8, j = k % 8;
-            const size_t at = ((static_cast<size_t>(u) * 4 + q) * kHeadTokens + t) * 8 + j;
+            const size_t at = ((static_cast<size_t>(u) * 4 + q) * TS + t) * 8 + j;
             if (BF16) {
                 const float x0 = v[e];
                 const uint16_t h0 = bf16_rne(x0);
@@ -220,11 +220,120 @@ __global__ __launch_bounds__(64 * kHeadWaves) void mfma_head_kernel(HeadArgs a) 
     }
 }
 
+// 17 to 32 tokens (pieces written for 32: head_pieces_bytes_32): grid
+// (workgroups, 2), blockIdx.y the half of the units
+// this workgroup covers (its pieces of both 16-token groups, [piece][unit -
+// u0][quarter][token 0..31][16 B], the LDS of one 16-token launch over all
+// units), each weight chunk fed to both groups' products; the two halves'
+// partial logits are added into the cleared output (two adds onto zero: the
+// same sum in either order).  The head is read once per 32 tokens.
+template <bool BF16>
+__global__ __launch_bounds__(64 * kHeadWaves) void mfma_head2_kernel(HeadArgs a) {
+    constexpr int NP = BF16 ? 3 : 2;
+    constexpr int TS = 2 * kHeadTokens;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, lane = tid % kWaveSize;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWaveSize);
+    const uint32_t units = a.units, uh = (units + 1) / 2;
+    const uint32_t u0 = blockIdx.y * uh, u1 = min(units, u0 + uh), nu = u1 - u0;
+    {
+        // each piece plane's units [u0, u1) are one contiguous run
+        const uint32_t per_plane = nu * 4 * TS;   // 16-byte pieces (8 elements each), a multiple of 64
+        const uint32_t total = NP * per_plane;
+        for (uint32_t c0 = wave * kWaveSize; c0 < total; c0 += blockDim.x) {
+            const uint32_t c = c0 + lane, p = c / per_plane, r = c - p * per_plane;
+            const size_t src = (static_cast<size_t>(p) * units * 4 * TS + static_cast<size_t>(u0) * 4 * TS + r) * 16;
+            __builtin_amdgcn_global_load_lds(a.pieces + src, (lds_void *)(smem + static_cast<size_t>(c0) * 16), 16,
+                                             0, 0);
+        }
+        wait_vmcnt<0>();
+        lds_barrier();
+    }
+    if (nu == 0) return;   // a one-unit row: the second half is empty
+    const uint32_t col = lane % 16, kq = lane / 16;
+    const uint32_t L = a.lanes, R = a.rows_per_wave;
+    const uint32_t ntiles = (a.rows + 15) / 16;
+    const uint32_t nstage = (nu + kHeadStage - 1) / kHeadStage;
+    for (uint32_t rt = blockIdx.x * kHeadWaves + wave; rt < ntiles; rt += gridDim.x * kHeadWaves) {
+        const uint32_t row = min(rt * 16 + col, a.padded_rows - 1);
+        const uint32_t tile = row >> a.rpw_log2, grp = row & (R - 1);
+        const uint8_t *tbase = a.payload + static_cast<size_t>(tile) * a.tile_payload;
+        auto chunk_at = [&](uint32_t u) -> const uint4 * {
+            const uint32_t i = u >> a.lanes_log2, jj = u & (L - 1);
+            const uint32_t n = min(L, units - i * L);
+            return reinterpret_cast<const uint4 *>(tbase + static_cast<size_t>(64) * R * L * i +
+                                                   (static_cast<size_t>(kq) * R * n + grp * n + jj) * 16);
+        };
+        uint4 wa[kHeadStage], wb[kHeadStage];
+        auto load_stage = [&](uint4 (&w)[kHeadStage], uint32_t st) {
+#pragma unroll
+            for (int i = 0; i < kHeadStage; ++i) w[i] = *chunk_at(u0 + min(st * kHeadStage + i, nu - 1));
+        };
+        float4v acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto run_stage = [&](const uint4 (&w)[kHeadStage], uint32_t st) {
+#pragma unroll
+            for (int i = 0; i < kHeadStage; ++i) {
+                const uint32_t ul = st * kHeadStage + i;
+                if (ul < nu) {
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) {
+                        const uint8_t *bp = smem + (((static_cast<size_t>(p) * nu + ul) * 4 + kq) * TS + col) * 16;
+                        const uint4 b0 = *reinterpret_cast<const uint4 *>(bp);
+                        const uint4 b1 = *reinterpret_cast<const uint4 *>(bp + kHeadTokens * 16);
+                        if constexpr (BF16) {
+                            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168, w[i]),
+                                                                           __builtin_bit_cast(bf168, b0), acc0, 0, 0, 0);
+                            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168, w[i]),
+                                                                           __builtin_bit_cast(bf168, b1), acc1, 0, 0, 0);
+                        } else {
+                            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w[i]),
+                                                                          __builtin_bit_cast(half8, b0), acc0, 0, 0, 0);
+                            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, w[i]),
+                                                                          __builtin_bit_cast(half8, b1), acc1, 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        };
+        load_stage(wa, 0);
+        for (uint32_t st = 0; st < nstage; st += 2) {
+            if (st + 1 < nstage) load_stage(wb, st + 1);
+            run_stage(wa, st);
+            if (st + 1 < nstage) {
+                if (st + 2 < nstage) load_stage(wa, st + 2);
+                run_stage(wb, st + 1);
+            }
+        }
+        // rows 4 kq + i of the tile, tokens col and 16 + col
+        const uint32_t r = rt * 16 + 4 * kq;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t tok = g * kHeadTokens + col;
+            if (tok < a.ntok) {
+                const float back = a.unscale[tok];
+                float *dst = a.out + static_cast<size_t>(tok) * a.out_stride + r;
+                const float4v &acc = g == 0 ? acc0 : acc1;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (r + i < a.rows) unsafeAtomicAdd(dst + i, acc[i] * back);
+            }
+        }
+    }
+}
+
+// rows [0, n) x [0, cols) of a [n][stride] fp32 array set to zero
+__global__ __launch_bounds__(256) void clear_rows_kernel(float *__restrict__ out, uint32_t cols, uint32_t stride) {
+    float *row = out + static_cast<size_t>(blockIdx.y) * stride;
+    for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < cols; k += gridDim.x * blockDim.x) row[k] = 0.0f;
+}
+
 }  // namespace
 
 size_t head_pieces_bytes(const DeviceTensor &t) {
     return static_cast<size_t>(t.bf16 ? 3 : 2) * t.units * 1024;
 }
+
+size_t head_pieces_bytes_32(const DeviceTensor &t) { return 2 * head_pieces_bytes(t); }
 
 bool mfma_head_supported(const DeviceTensor &t) {
     return t.kind == kF16 && t.units > 0 && (t.lanes & (t.lanes - 1)) == 0 &&
@@ -234,12 +343,18 @@ bool mfma_head_supported(const DeviceTensor &t) {
 
 hipError_t launch_head_pieces(const DeviceTensor &t, const float *x, uint32_t x_stride, const float *norm, float eps,
                               uint32_t ntok, uint8_t *pieces, float *unscale, hipStream_t stream) {
-    if (!mfma_head_supported(t) || ntok == 0 || ntok > static_cast<uint32_t>(kHeadTokens)) return hipErrorInvalidValue;
+    if (!mfma_head_supported(t) || ntok == 0 || ntok > static_cast<uint32_t>(2 * kHeadTokens))
+        return hipErrorInvalidValue;
     const uint32_t per = (t.units * 32 + 1023) / 1024;
     auto go = [&](auto bf_c, auto ept_c) {
-        hipLaunchKernelGGL((head_pieces_kernel<decltype(bf_c)::value, decltype(ept_c)::value>), dim3(ntok), dim3(1024),
-                           0, stream, x, x_stride, norm, eps, t.cols, t.units, reinterpret_cast<uint16_t *>(pieces),
-                           unscale);
+        constexpr bool B = decltype(bf_c)::value;
+        constexpr int E = decltype(ept_c)::value;
+        if (ntok > static_cast<uint32_t>(kHeadTokens))
+            hipLaunchKernelGGL((head_pieces_kernel<B, E, 2 * kHeadTokens>), dim3(ntok), dim3(1024), 0, stream, x,
+                               x_stride, norm, eps, t.cols, t.units, reinterpret_cast<uint16_t *>(pieces), unscale);
+        else
+            hipLaunchKernelGGL((head_pieces_kernel<B, E, kHeadTokens>), dim3(ntok), dim3(1024), 0, stream, x,
+                               x_stride, norm, eps, t.cols, t.units, reinterpret_cast<uint16_t *>(pieces), unscale);
     };
     auto by_ept = [&](auto bf_c) {
         if (per <= 1) go(bf_c, std::integral_constant<int, 1>{});
@@ -255,7 +370,7 @@ hipError_t launch_head_pieces(const DeviceTensor &t, const float *x, uint32_t x_
 
 hipError_t launch_mfma_head(const DeviceTensor &t, const uint8_t *pieces, const float *unscale, uint32_t ntok,
                             float *out, uint32_t out_stride, hipStream_t stream) {
-    if (!mfma_head_supported(t) || ntok == 0 || ntok > static_cast<uint32_t>(kHeadTokens) || out_stride < t.rows)
+    if (!mfma_head_supported(t) || ntok == 0 || ntok > static_cast<uint32_t>(2 * kHeadTokens) || out_stride < t.rows)
         return hipErrorInvalidValue;
     HeadArgs a{};
     a.payload = t.payload;
@@ -275,6 +390,23 @@ hipError_t launch_mfma_head(const DeviceTensor &t, const uint8_t *pieces, const 
     const uint32_t ntiles = (t.rows + 15) / 16;
     const uint32_t grid = std::max(1u, std::min(256u, (ntiles + kHeadWaves - 1) / kHeadWaves));
     const size_t lds = head_pieces_bytes(t);
+    if (ntok > static_cast<uint32_t>(kHeadTokens)) {
+        // the two unit halves add into a cleared output; LDS: the pieces of
+        // the larger half for 32 tokens
+        const size_t lds2 = static_cast<size_t>(t.bf16 ? 3 : 2) * ((t.units + 1) / 2) * 2048;
+        hipLaunchKernelGGL(clear_rows_kernel, dim3((t.rows + 1023) / 1024, ntok), dim3(256), 0, stream, out, t.rows,
+                           out_stride);
+        if (t.bf16) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_head2_kernel<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
+            hipLaunchKernelGGL(mfma_head2_kernel<true>, dim3(grid, 2), dim3(64 * kHeadWaves), lds2, stream, a);
+        } else {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_head2_kernel<false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
+            hipLaunchKernelGGL(mfma_head2_kernel<false>, dim3(grid, 2), dim3(64 * kHeadWaves), lds2, stream, a);
+        }
+        return hipGetLastError();
+    }
     if (t.bf16) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_head_kernel<true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));

@@ -257,13 +257,16 @@ hipError_t launch_norm_image(const DeviceTensor &t, const float *x, const float 
 // ids[rows]; the last row's also into *last_out when given.  keys: device
 // workspace of rows * rows_argmax_parts(cols) u64 (each row is split over
 // that many workgroups, then reduced).
-// LM head of a block of up to 16 tokens on the matrix cores (F16 / BF16
+// LM head of a block of up to 32 tokens on the matrix cores (F16 / BF16
 // heads whose activation pieces fit the LDS limit): launch_head_pieces
 // RMSNorms each token of x [ntok][x_stride] with `norm` and writes its
-// narrow pieces (head_pieces_bytes) and per-token unscale factors [16];
-// launch_mfma_head writes out [ntok][out_stride] = the logits.
+// narrow pieces (head_pieces_bytes for up to 16 tokens, head_pieces_bytes_32
+// beyond) and per-token unscale factors [ntok]; launch_mfma_head writes out
+// [ntok][out_stride] = the logits (beyond 16 tokens: the rows cleared, then
+// the two halves of the K range added in).
 constexpr size_t kHeadLdsLimit = 144 * 1024;
 size_t head_pieces_bytes(const DeviceTensor &t);
+size_t head_pieces_bytes_32(const DeviceTensor &t);
 bool mfma_head_supported(const DeviceTensor &t);
 hipError_t launch_head_pieces(const DeviceTensor &t, const float *x, uint32_t x_stride, const float *norm, float eps,
                               uint32_t ntok, uint8_t *pieces, float *unscale, hipStream_t stream);

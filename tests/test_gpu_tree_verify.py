@@ -64,16 +64,19 @@ def path_to(parents, i):
     return p[::-1]
 
 
-@pytest.mark.parametrize("cfg,dtype,P,levels", [
-    (SMALL, "q4_0", 20, (3, 8, 14, 15)), (QWEN2_LIKE, "hvsq2", 12, (3, 8, 14, 15)),
-    (QWEN2_LIKE, "q4_0", 7, (3, 8, 14, 15)), (LONG_CTX, "hvsq2", 300, (3, 8, 14, 15)),
+@pytest.mark.parametrize("cfg,dtype,P,levels,head", [
+    (SMALL, "q4_0", 20, (3, 8, 14, 15), None), (QWEN2_LIKE, "hvsq2", 12, (3, 8, 14, 15), None),
+    (QWEN2_LIKE, "q4_0", 7, (3, 8, 14, 15), None), (LONG_CTX, "hvsq2", 300, (3, 8, 14, 15), None),
+    # an untied BF16 head (three pieces per token) through the 32-token head launches
+    (QWEN2_LIKE, "q4_0", 9, (2, 4, 6, 8, 10, 10, 12, 12), "bf16"),
     # 64 nodes (one block of four 16-token MFMA groups), depth 8: the reference's limits (c/qwanto_jetspec.h:17-18)
-    (SMALL, "hvsq2", 9, (2, 4, 6, 8, 10, 10, 12, 12)), (LONG_CTX, "q4_0", 600, (1, 3, 6, 10, 14, 14, 16)),
+    (SMALL, "hvsq2", 9, (2, 4, 6, 8, 10, 10, 12, 12), None),
+    (LONG_CTX, "q4_0", 600, (1, 3, 6, 10, 14, 14, 16), None),
     # nodes straddling the 256- and 512-token chunk boundaries
-    (MID_CTX, "q4_0", 240, (3, 8, 14, 15)), (MID_CTX, "hvsq2", 500, (2, 4, 6, 8, 10, 10, 12, 12))])
-def test_tree_verify_matches_oracle_paths(gpu_ctx, oracle_lib, cfg, dtype, P, levels):
+    (MID_CTX, "q4_0", 240, (3, 8, 14, 15), None), (MID_CTX, "hvsq2", 500, (2, 4, 6, 8, 10, 10, 12, 12), None)])
+def test_tree_verify_matches_oracle_paths(gpu_ctx, oracle_lib, cfg, dtype, P, levels, head):
     rng = np.random.default_rng(1300 + P + sum(levels))
-    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype))
+    model = with_norms(rng, synth.decoder_model(rng, cfg, dtype, lm_head=head))
     prompt = synth.prompt_tokens(rng, cfg["vocab"], P)
     tokens, parents = random_tree(rng, levels, cfg["vocab"])
     n = tokens.size
