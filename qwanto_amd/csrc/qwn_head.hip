@@ -392,18 +392,21 @@ hipError_t launch_mfma_head(const DeviceTensor &t, const uint8_t *pieces, const 
     const size_t lds = head_pieces_bytes(t);
     if (ntok > static_cast<uint32_t>(kHeadTokens)) {
         // the two unit halves add into a cleared output; LDS: the pieces of
-        // the larger half for 32 tokens
+        // the larger half for 32 tokens; half the workgroups per half (one
+        // round of the chip for both halves: 2.404 -> 2.385 ms per 64-node
+        // tree against the full grid per half)
         const size_t lds2 = static_cast<size_t>(t.bf16 ? 3 : 2) * ((t.units + 1) / 2) * 2048;
+        const uint32_t grid2 = std::max(1u, grid / 2);
         hipLaunchKernelGGL(clear_rows_kernel, dim3((t.rows + 1023) / 1024, ntok), dim3(256), 0, stream, out, t.rows,
                            out_stride);
         if (t.bf16) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_head2_kernel<true>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
-            hipLaunchKernelGGL(mfma_head2_kernel<true>, dim3(grid, 2), dim3(64 * kHeadWaves), lds2, stream, a);
+            hipLaunchKernelGGL(mfma_head2_kernel<true>, dim3(grid2, 2), dim3(64 * kHeadWaves), lds2, stream, a);
         } else {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&mfma_head2_kernel<false>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds2));
-            hipLaunchKernelGGL(mfma_head2_kernel<false>, dim3(grid, 2), dim3(64 * kHeadWaves), lds2, stream, a);
+            hipLaunchKernelGGL(mfma_head2_kernel<false>, dim3(grid2, 2), dim3(64 * kHeadWaves), lds2, stream, a);
         }
         return hipGetLastError();
     }
