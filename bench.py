@@ -697,7 +697,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "qwn_hip runs on one GPU; this benchmark measures one MI355X "
-                                   "(the multi-GPU sharding is described in DESIGN.md, not built)",
+                                   "(sharding across GPUs is a design only, not built)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
