@@ -95,9 +95,9 @@ def test_resident_decoder_matches_oracle(gpu_ctx, oracle_lib, cfg, dtype, qk, bi
     (QWEN2_LIKE, "q4_0", "f16", "q4_0"), (SMALL, "hvsq2", "bf16", "hvsq2"), (LONG_CTX, "q4_0", "f16", "hvsq2")])
 def test_untied_head_and_bf16_embedding(gpu_ctx, oracle_lib, cfg, dtype, embed, head):
     """A BF16 embedding (c/qwanto_decode.c:561) and an untied lm_head.weight
-    (c/qwanto_decode.c:1074-1076, 2007) in each dtype: F16/BF16 through the
-    norm image and the F16-layout GEMV, Q4_0/HyperVSQ-2 normalized and
-    quantized in the head GEMV's own prologue.  Stepping (the device argmax
+    (c/qwanto_decode.c:1074-1076, 2007) in each dtype, one token's head
+    normalizing x in its own GEMV prologue (F16/BF16 rows on fp32 values,
+    Q4_0/HyperVSQ-2 on the quantized image).  Stepping (the device argmax
     epilogue on the head), a prefill block and a verify block (the batched
     head on every token) against the oracle, which is bit-identical to the
     reference decoder on the same model (test_decoder_oracle.py)."""
