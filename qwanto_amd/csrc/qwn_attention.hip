@@ -819,8 +819,12 @@ __global__ __launch_bounds__(256 * TPT) void decode_attention_kernel(DecodeAttnA
         //    scaled by the key scale and the piece scale, summed over the
         //    token's TPT lanes
         float sc = 0.0f;
+        // waves whose slots all lie past the chunk's tokens skip the
+        // products (their LDS reads are most of the phase's traffic)
+        const bool wave_has = wave * SPW < n;
 #pragma unroll
         for (int g = 0; g < KGL; ++g) {
+            if (!wave_has) break;
             int d1 = 0, d2 = 0, d3 = 0;
 #pragma unroll
             for (int w = g * WPG; w < (g + 1) * WPG; ++w) {
