@@ -61,6 +61,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Compiler-level fence plus the hardware barrier, without the vmcnt(0)
 // that __syncthreads() implies: LDS writes before it are visible after it,
 // global loads and stores in flight stay in flight.
+// The int8 of c, |c| <= 127, rounded half to even, in the low byte of the
+// result: c + 1.5 * 2^23 lies where the fp32 spacing is 1, so the add
+// rounds c to the nearest even integer n and leaves 0x4b400000 + n as the
+// bits (one add where rintf and a float-to-int conversion take two).
+__device__ __forceinline__ uint32_t q8_low_byte(float c) { return __builtin_bit_cast(uint32_t, c + 12582912.0f); }
+
+// The low bytes of a, b, c, d as bytes 0..3 of one word (three byte
+// permutes: v_perm_b32 selects bytes 0-3 from its second operand and 4-7
+// from its first, 0x0c gives zero).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
 __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_sched_barrier(0);
@@ -97,30 +112,38 @@ __device__ __forceinline__ float wave_max_all(float v) {
 
 // Nibble-pack 8 int8 values (two dwords, element order) into the high
 // (signed, a >> 4) and low (a & 15) nibble words, nibble k = element k.
+// Per word the nibbles of bytes 0-1 and 2-3 fold into bytes 0 and 2 (x | x
+// >> 4 on the masked nibbles), then one byte permute gathers them; the high
+// nibble is bits 4-7 of the byte, the arithmetic >> 4 of the int8 as a
+// nibble.
 __device__ __forceinline__ void split8(uint32_t a, uint32_t b, uint32_t &hi, uint32_t &lo) {
-    hi = lo = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t byte = ((k < 4 ? a : b) >> (8 * (k & 3))) & 0xffu;
-        hi |= ((byte >> 4) & 0xfu) << (4 * k);  // arithmetic >> 4 of the int8, as a nibble
-        lo |= (byte & 0xfu) << (4 * k);
-    }
+    const uint32_t la = a & 0x0f0f0f0fu, lb = b & 0x0f0f0f0fu;
+    const uint32_t ha = (a >> 4) & 0x0f0f0f0fu, hb = (b >> 4) & 0x0f0f0f0fu;
+    lo = __builtin_amdgcn_perm(lb | (lb >> 4), la | (la >> 4), 0x06040200u);
+    hi = __builtin_amdgcn_perm(hb | (hb >> 4), ha | (ha >> 4), 0x06040200u);
 }
 
 // Even/odd split of 16 int8 values for the HyperVSQ-2 masks: returns the
 // high/low nibble words of elements {0,2,..,14} and {1,3,..,15}.
+// Word q holds elements 4q .. 4q+3: m | (m >> 12) on its masked nibbles
+// puts those of elements 4q, 4q+2 (even) in byte 0 and of 4q+1, 4q+3 (odd)
+// in byte 1; byte permutes then gather bytes 0 and bytes 1 of the four
+// words.
 __device__ __forceinline__ uint4 split16_evenodd(const uint32_t w[4]) {
-    uint32_t he = 0, le = 0, ho = 0, lo = 0;
+    uint32_t t[4], g[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t ev = (w[k >> 1] >> (16 * (k & 1))) & 0xffu;        // element 2k
-        const uint32_t od = (w[k >> 1] >> (16 * (k & 1) + 8)) & 0xffu;    // element 2k+1
-        he |= ((ev >> 4) & 0xfu) << (4 * k);
-        le |= (ev & 0xfu) << (4 * k);
-        ho |= ((od >> 4) & 0xfu) << (4 * k);
-        lo |= (od & 0xfu) << (4 * k);
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t m = w[q] & 0x0f0f0f0fu, h = (w[q] >> 4) & 0x0f0f0f0fu;
+        t[q] = m | (m >> 12);
+        g[q] = h | (h >> 12);
     }
-    return make_uint4(he, le, ho, lo);
+    // [x0.b0, x1.b0, x0.b1, x1.b1] of a pair of words
+    const uint32_t t01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u);
+    const uint32_t t23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u);
+    const uint32_t g01 = __builtin_amdgcn_perm(g[1], g[0], 0x05010400u);
+    const uint32_t g23 = __builtin_amdgcn_perm(g[3], g[2], 0x05010400u);
+    return make_uint4(__builtin_amdgcn_perm(g23, g01, 0x05040100u), __builtin_amdgcn_perm(t23, t01, 0x05040100u),
+                      __builtin_amdgcn_perm(g23, g01, 0x07060302u), __builtin_amdgcn_perm(t23, t01, 0x07060302u));
 }
 
 // Write one 32-activation block (8 dwords of int8, element order) into a

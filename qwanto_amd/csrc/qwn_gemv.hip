@@ -256,17 +256,18 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
     for (uint32_t base = 0; base < nsub; base += blockDim.x) {
         const uint32_t sb = base + tid;
         uint32_t w[E / 4];
-#pragma unroll
-        for (uint32_t i = 0; i < E / 4; ++i) w[i] = 0;
+        uint32_t qb[E];
 #pragma unroll
         for (uint32_t i = 0; i < E; ++i) {
             const uint32_t k = sb * E + i;
+            qb[i] = 0;
             if (sb < nsub && k < K) {
                 const float c = fminf(127.0f, fmaxf(-127.0f, (staged ? vals[k] : value(k)) * inv));
-                w[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(c))))
-                             << (8 * (i & 3));
+                qb[i] = q8_low_byte(c);
             }
         }
+#pragma unroll
+        for (uint32_t i = 0; i < E / 4; ++i) w[i] = pack_low_bytes(qb[4 * i], qb[4 * i + 1], qb[4 * i + 2], qb[4 * i + 3]);
         if (img) put_sub_block<KIND>(img, units, sb, nsub, w);
         if (mimg) {
             if constexpr (KIND == kQ4_0) {
@@ -715,15 +716,11 @@ __global__ __launch_bounds__(kWaveSize * max_waves_for(UPL)) void gemv_kernel(Ge
             if (a.scale_out && blockIdx.x == 0 && threadIdx.x == 0) *a.scale_out = scale;
 #pragma unroll
             for (int r = 0; r < SR; ++r) {
-                uint32_t w[EW];
+                uint32_t w[EW], qb[E];
 #pragma unroll
-                for (int i = 0; i < EW; ++i) w[i] = 0;
+                for (int i = 0; i < E; ++i) qb[i] = q8_low_byte(fminf(127.0f, fmaxf(-127.0f, v[r][i] * inv)));
 #pragma unroll
-                for (int i = 0; i < E; ++i) {
-                    const float c = fminf(127.0f, fmaxf(-127.0f, v[r][i] * inv));
-                    w[i >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(__builtin_rintf(c))))
-                                 << (8 * (i & 3));
-                }
+                for (int i = 0; i < EW; ++i) w[i] = pack_low_bytes(qb[4 * i], qb[4 * i + 1], qb[4 * i + 2], qb[4 * i + 3]);
                 put_sub_block<KIND>(smem, a.units, threadIdx.x + r * blockDim.x, nsub, w);
             }
         }
