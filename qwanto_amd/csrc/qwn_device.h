@@ -110,6 +110,11 @@ __device__ __forceinline__ float wave_max_all(float v) {
 
 // ---- activation images --------------------------------------------------------
 
+// The value of lane ^ 1 / lane ^ 2 within each quad, by DPP quad
+// permutes (a VALU operand, where __shfl_xor goes through the LDS crossbar).
+__device__ __forceinline__ int quad_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xb1, 0xf, 0xf, false); }
+__device__ __forceinline__ int quad_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4e, 0xf, 0xf, false); }
+
 // Nibble-pack 8 int8 values (two dwords, element order) into the high
 // (signed, a >> 4) and low (a & 15) nibble words, nibble k = element k.
 // Per word the nibbles of bytes 0-1 and 2-3 fold into bytes 0 and 2 (x | x
@@ -188,7 +193,7 @@ __device__ __forceinline__ void put_sub_block(uint8_t *img, uint32_t units, uint
         int s = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) s = sdot4(w[i], 0x01010101u, s);
-        s += __shfl_xor(s, 1);
+        s += quad_xor1(s);
         if (sb < nsub) {
             const uint32_t e0 = sb * 16, u = e0 / 256, off = e0 % 256;
             *reinterpret_cast<uint4 *>(img + u * 272 + off) = split16_evenodd(w);
@@ -198,8 +203,8 @@ __device__ __forceinline__ void put_sub_block(uint8_t *img, uint32_t units, uint
         uint32_t hi, lo;
         split8(w[0], w[1], hi, lo);
         int lsum = static_cast<int>(__builtin_amdgcn_udot8(lo, 0x11111111u, 0u, false));
-        lsum += __shfl_xor(lsum, 1);
-        lsum += __shfl_xor(lsum, 2);
+        lsum += quad_xor1(lsum);
+        lsum += quad_xor2(lsum);
         if (sb < nsub) {
             const uint32_t e0 = sb * 8, u = e0 / 128, off = e0 % 128;
             *reinterpret_cast<uint2 *>(img + u * 144 + off) = make_uint2(hi, lo);
