@@ -708,3 +708,31 @@ def test_mfma_int32_block_dots(gpu_ctx, oracle_lib, kind, N, K, M):
             assert bad.size == 0, f"{kind} N={N} K={K} token {t}: block dots differ at {bad[:5]}"
     finally:
         gpu_ctx.release(h)
+
+
+def test_device_quantize_rounds_halves_to_even(gpu_ctx):
+    """Per-token int8 quantization (c/qwanto_kernels.c:354-433, the CPU's
+    rintf) on the device: with max|x| = 127 the scale is exactly 1, so every
+    value x.5 is a tie and must round to the even integer, as numpy's rint
+    does; the kernel rounds by adding 1.5 * 2^23, which this pins for every
+    tie in range and both signs."""
+    import torch
+    halves = np.arange(-126.5, 127.0, 1.0, dtype=np.float32)   # 254 ties
+    K = 512
+    x = np.zeros((2, K), np.float32)
+    x[0, 0], x[1, 0] = 127.0, -127.0
+    x[0, 1:1 + halves.size] = halves
+    x[1, 1:1 + halves.size] = -halves[::-1]
+    x[:, 300:310] = [0.49999997, -0.49999997, 0.5, -0.5, 1.4999999, -1.5000001, 2.5, 3.5, -2.5, -0.0]
+    dev = torch.device("cuda:0")
+    xd = torch.from_numpy(x).to(dev)
+    q8 = torch.full((2, K), 99, dtype=torch.int8, device=dev)
+    sc = torch.zeros(2, dtype=torch.float32, device=dev)
+    gpu_ctx.quantize_device(xd.data_ptr(), 2, K, K, q8.data_ptr(), K, sc.data_ptr(),
+                            stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert sc.cpu().numpy().tolist() == [1.0, 1.0]
+    want = np.clip(np.rint(x), -127, 127).astype(np.int8)
+    got = q8.cpu().numpy()
+    bad = np.nonzero(got != want)
+    assert bad[0].size == 0, f"first mismatches at {list(zip(*bad))[:5]}: got {got[bad][:5]}, want {want[bad][:5]}"
