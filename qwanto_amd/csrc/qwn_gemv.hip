@@ -274,10 +274,10 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
                 // slot (block sb/4, group sb%4): elements {0,2,4,6} then {1,3,5,7}
                 const uint32_t nblk = (K + 31) / 32;
                 if (sb < nblk * 4) {
-                    const uint32_t lo = (w[0] & 0xffu) | ((w[0] >> 8) & 0xff00u) | ((w[1] & 0xffu) << 16) |
-                                        ((w[1] << 8) & 0xff000000u);
-                    const uint32_t hi = ((w[0] >> 8) & 0xffu) | ((w[0] >> 16) & 0xff00u) |
-                                        ((w[1] << 8) & 0xff0000u) | (w[1] & 0xff000000u);
+                    // bytes 0, 2 / 1, 3 of each word (v_perm_b32: bytes 0-3 of
+                    // the second operand, 4-7 of the first)
+                    const uint32_t lo = __builtin_amdgcn_perm(w[1], w[0], 0x06040200u);
+                    const uint32_t hi = __builtin_amdgcn_perm(w[1], w[0], 0x07050301u);
                     *reinterpret_cast<uint2 *>(mimg + (static_cast<size_t>(sb) * 16 + tc) * 8) = make_uint2(lo, hi);
                 }
             } else {
@@ -287,16 +287,23 @@ __global__ __launch_bounds__(NT) void quantize_image_kernel(const float *__restr
                 int s = 0;
 #pragma unroll
                 for (uint32_t i = 0; i < E; ++i) s += static_cast<int8_t>((w[i >> 2] >> (8 * (i & 3))) & 0xffu);
-                s += __shfl_xor(s, 1);
-                s += __shfl_xor(s, 2);
-                s += __shfl_xor(s, 4);
-                s += __shfl_xor(s, 8);
+                // the 16 lanes' sum into the first lane of each 16-lane row
+                // (DPP row shifts toward lane 0; lanes past the row add 0)
+                s += __builtin_amdgcn_update_dpp(0, s, 0x101, 0xf, 0xf, false);
+                s += __builtin_amdgcn_update_dpp(0, s, 0x102, 0xf, 0xf, false);
+                s += __builtin_amdgcn_update_dpp(0, s, 0x104, 0xf, 0xf, false);
+                s += __builtin_amdgcn_update_dpp(0, s, 0x108, 0xf, 0xf, false);
                 if (sb < nsub) {
-                    uint32_t o[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        o[k] = ((w[0] >> (8 * k)) & 0xffu) | (((w[1] >> (8 * k)) & 0xffu) << 8) |
-                               (((w[2] >> (8 * k)) & 0xffu) << 16) | (((w[3] >> (8 * k)) & 0xffu) << 24);
+                    // byte k of w[0..3] -> word k: a 4x4 byte transpose in
+                    // two rounds of byte permutes
+                    const uint32_t p01l = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+                    const uint32_t p01h = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+                    const uint32_t p23l = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+                    const uint32_t p23h = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+                    const uint32_t o[4] = {__builtin_amdgcn_perm(p23l, p01l, 0x05040100u),
+                                           __builtin_amdgcn_perm(p23l, p01l, 0x07060302u),
+                                           __builtin_amdgcn_perm(p23h, p01h, 0x05040100u),
+                                           __builtin_amdgcn_perm(p23h, p01h, 0x07060302u)};
                     const uint32_t slot = (sb & ~15u) | ((sb & 3u) << 2) | ((sb >> 2) & 3u);
                     *reinterpret_cast<uint4 *>(mimg + (static_cast<size_t>(slot) * 16 + tc) * 16) =
                         make_uint4(o[0], o[1], o[2], o[3]);
